@@ -1,0 +1,181 @@
+#!/usr/bin/env python
+"""Benchmark of the fused multihead DIAG chunked scan on one GPU.
+
+Workload: B=8 L=4096 H=16 P=N=64, chunk 128, bf16 x/B/C/y, fp32 dt and
+state, ZOH discretization fused into the load stage (seeded synthetic data).
+A step is one fused scan over the whole batch with inputs resident in HBM.
+Three input/output sets are rotated so that consecutive steps do not hit in
+the 256 MB Infinity Cache.
+
+Prints ONE JSON line on stdout with the metric, the roofline of the scan
+kernel (algorithmic bytes / average kernel time from HIP events on the
+launch stream) and the C restatement timed on the host cores (rank 0, N=1).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "triton-ssm_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "scan elements/sec + achieved HBM GB/s (% of peak), B=8 L=4096 H=16 P=64 N=64"
+PEAK_GBS = 8000.0
+SHAPE = dict(B=8, L=4096, H=16, P=64)
+CHUNK = 128
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, disc, reps):
+    """The C restatement (fp32, OpenMP over (b, head) rows) on the whole
+    workload, inputs already converted to fp32 outside the timed region."""
+    import numpy as np
+    from oracle import cport
+    arrs = [np.ascontiguousarray(w[k].float().numpy()) for k in ("u", "A_log", "B", "C", "dt")]
+    cport.multihead_scan(*arrs, None, disc=disc, prepared=True)   # warm
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        cport.multihead_scan(*arrs, None, disc=disc, prepared=True)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    n = SHAPE["B"] * SHAPE["L"] * SHAPE["H"] * SHAPE["P"]
+    return {"value": n / med, "unit": "elements/s", "cores": cport.threads(), "kind": "port",
+            "sample": f"whole workload (B=8 L=4096 H=16 P=64, {disc}), median of {reps} runs, "
+                      f"{med:.3f} s each"}
+
+
+def traffic_from_profile():
+    p = ROOT / "profiles" / "mh_scan_fused_traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--disc", choices=["zoh", "euler"], default="zoh")
+    ap.add_argument("--a-per-head", action="store_true",
+                    help="pass A_log as [H] (one decay per head) instead of [H, P]")
+    ap.add_argument("--sets", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the scan is data-parallel over (batch, head) "
+              "and this build runs on a single MI355X; run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from tssm import multihead_ssm_forward, workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log("generating inputs ...")
+    w = workloads.multihead(**SHAPE)
+    a_key = "A_log_h" if args.a_per_head else "A_log"
+    base = {k: w[k].to(dev) for k in ("u", "B", "C", "dt")}
+    A_log = w[a_key].to(dev)
+    sets = []
+    for i in range(args.sets):
+        s = {k: torch.roll(v, shifts=i, dims=0).contiguous() for k, v in base.items()}
+        s["y"] = torch.empty_like(s["u"])
+        sets.append(s)
+    del base
+    torch.cuda.synchronize()
+
+    def step(i):
+        s = sets[i % len(sets)]
+        multihead_ssm_forward(s["u"], A_log, s["B"], s["C"], s["dt"], None, disc=args.disc,
+                              chunk=CHUNK, out=s["y"])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step(i)
+        ev[i][1].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    per = [a.elapsed_time(b) for a, b in ev]
+    kern_ms = statistics.mean(per)
+    ms_per_step = total_ms / args.steps
+
+    B, L, H, P = SHAPE["B"], SHAPE["L"], SHAPE["H"], SHAPE["P"]
+    n = B * L * H * P
+    nbytes = workloads.multihead_bytes(B, L, H, P, io_bytes=2) - H * P * 4 + A_log.numel() * 4
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    log(f"kernel avg {kern_ms * 1e3:.1f} us (median {statistics.median(per) * 1e3:.1f}, "
+        f"min {min(per) * 1e3:.1f}), step {ms_per_step * 1e3:.1f} us, {achieved:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        log("timing the CPU baseline ...")
+        cpu = cpu_baseline(w, args.disc, args.cpu_reps)
+
+    out = {
+        "metric": METRIC,
+        "value": n / (ms_per_step * 1e-3),
+        "unit": "elements/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "fused multihead DIAG chunked scan, B=8 L=4096 H=16 P=N=64, chunk 128, "
+                        f"bf16 x/B/C/y, fp32 dt/state, {args.disc.upper()} discretization",
+            "B": B, "L": L, "H": H, "P": P, "N": P, "chunk": CHUNK, "disc": args.disc,
+            "io_dtype": "bf16", "state_dtype": "f32",
+            "a_log": "per head [H]" if args.a_per_head else "per channel [H, P]",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mh_scan_fused_kernel",
+            "achieved": achieved,
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / PEAK_GBS,
+            "traffic": traffic_from_profile(),
+            "algorithmic_bytes_per_launch": nbytes,
+            "kernel_avg_us": kern_ms * 1e3,
+        },
+        "cpu_baseline": cpu,
+        "hbm_gbs": achieved,
+        "pct_of_peak_hbm": 100.0 * achieved / PEAK_GBS,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

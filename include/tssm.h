@@ -1,0 +1,179 @@
+/* tssm -- C ABI of the MI355X (gfx950) selective-SSM library.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, int64 sizes/strides (in elements) and a
+ *     hipStream_t passed as void*; launches asynchronously on that stream;
+ *   - never allocates and never synchronises;
+ *   - returns 0 on success, a negative TSSM_ERR_* code for an invalid
+ *     argument (nothing is launched), or a positive hipError_t.
+ * Innermost (channel) strides are 1, exactly as the reference kernels assume
+ * (they accept innermost strides but never use them).
+ *
+ * Reference citations are file:line into Triton-SSM.  "grid_*" arguments give
+ * the Triton launch grid the caller used: the library computes exactly the
+ * programs of that grid, whatever launch geometry it picks for itself.
+ */
+#ifndef TSSM_H_
+#define TSSM_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define TSSM_OK 0
+#define TSSM_ERR_NULL (-1)        /* a required pointer is NULL */
+#define TSSM_ERR_SHAPE (-2)       /* a size is negative, zero where not allowed, or inconsistent */
+#define TSSM_ERR_STRIDE (-3)      /* a stride is invalid for the access pattern */
+#define TSSM_ERR_DTYPE (-4)       /* unknown or unsupported dtype code */
+#define TSSM_ERR_WORKSPACE (-5)   /* workspace missing or too small */
+#define TSSM_ERR_UNSUPPORTED (-6) /* valid but unsupported configuration */
+#define TSSM_ERR_ALIGN (-7)       /* pointer/stride not aligned for vector access */
+
+/* dtype codes */
+#define TSSM_F32 0
+#define TSSM_BF16 1
+#define TSSM_F16 2
+
+/* input discretization of the fused scans */
+#define TSSM_DISC_EULER 0 /* Bbar = dt * B           (multihead_ssm_kernel.py:73) */
+#define TSSM_DISC_ZOH 1   /* Bbar = expm1(dt a)/a * B (discretize_kernel.py:50-54) */
+
+int tssm_abi_version(void);
+const char* tssm_strerror(int status);
+
+/* Workspaces of the single-pass (decoupled look-back) scans are caller-owned
+ * device buffers, zero-filled ONCE when allocated and then reused by launches
+ * on one stream.  Reads the sticky error word (1 = a bounded look-back wait
+ * expired) with a synchronous copy; tests only. */
+int tssm_workspace_error(const void* workspace, int clear, int* error_out);
+
+/* ------------------------------------------------------------------ ZOH
+ * zoh_discretize_diag_kernel / zoh_discretize_diag_bf16_kernel
+ * (discretize_kernel.py:16-57 / :61-94).  Grid (B, T, ceil(H/BLOCK_H)):
+ * computes (b < grid_b, t < grid_t, h < min(H, h_cover)).
+ * A_log [H] f32, dt [B,T] f32; B, Abar, Bbar in b_dtype / out_dtype. */
+int tssm_zoh_discretize(int b_dtype, int out_dtype, const float* A_log, const void* B,
+                        const float* dt, void* Abar, void* Bbar, int64_t nbatch, int64_t T,
+                        int64_t H, int64_t grid_b, int64_t grid_t, int64_t h_cover,
+                        int64_t sB_b, int64_t sB_t, int64_t sdt_b, int64_t sdt_t, int64_t sa_b,
+                        int64_t sa_t, int64_t sb_b, int64_t sb_t, void* stream);
+
+/* ------------------------------------------------------------------ elementwise scan
+ * ssm_scan.py phase kernels; u, A, B, C, D, h, y, loc_*, carry all in `dtype`,
+ * contiguous [B, L, H] (the reference computes offsets b*L*H + t*H + h).
+ * carry layout [2, B*H, NBLK] (ssm_scan.py:47-50). */
+int tssm_ssm_fwd_local(int dtype, const void* u, const void* A, const void* B, void* loc_a,
+                       void* loc_x, void* carry, int64_t nbatch, int64_t L, int64_t H,
+                       int64_t blk, int64_t nblk, int64_t grid_rows, int64_t grid_blks,
+                       void* stream); /* ssm_fwd_local_kernel, ssm_scan.py:18-50 */
+int tssm_carry_scan(int dtype, void* carry, int64_t nrows, int64_t nblk, int reverse,
+                    int64_t grid_rows, void* stream);
+/* ssm_carry_scan_kernel (ssm_scan.py:54-65), ssm_bwd_carry_scan_kernel (:174-185,
+ * reverse=1), multihead_ssm_carry_scan_kernel (multihead_ssm_kernel.py:106-117) */
+int tssm_ssm_fwd_apply(int dtype, const void* loc_a, const void* loc_x, const void* carry,
+                       void* h_out, int64_t nbatch, int64_t L, int64_t H, int64_t blk,
+                       int64_t nblk, int64_t grid_rows, int64_t grid_blks,
+                       void* stream); /* ssm_fwd_apply_kernel, ssm_scan.py:69-98 */
+int tssm_ssm_output(int dtype, const void* h, const void* C, const void* D, const void* u,
+                    void* y, int64_t nbatch, int64_t L, int64_t H, int64_t blk,
+                    int64_t grid_rows, int64_t grid_blks,
+                    void* stream); /* ssm_output_kernel, ssm_scan.py:102-124 */
+int tssm_ssm_bwd_local(int dtype, const void* A, const void* C, const void* dY, void* loc_a,
+                       void* loc_dh, void* carry, int64_t nbatch, int64_t L, int64_t H,
+                       int64_t blk, int64_t nblk, int64_t grid_rows, int64_t grid_blks,
+                       void* stream); /* ssm_bwd_local_kernel, ssm_scan.py:136-170 */
+int tssm_ssm_bwd_apply(int dtype, const void* loc_a, const void* loc_dh, const void* carry,
+                       const void* u, const void* A, const void* B, const void* h,
+                       const void* dY, void* du, void* dA, void* dB, void* dC, int64_t nbatch,
+                       int64_t L, int64_t H, int64_t blk, int64_t nblk, int64_t grid_rows,
+                       int64_t grid_blks,
+                       void* stream); /* ssm_bwd_apply_kernel, ssm_scan.py:189-231 */
+
+/* ------------------------------------------------------------------ multihead DIAG scan
+ * multihead_ssm_fwd_local_kernel (multihead_ssm_kernel.py:20-102): Euler input
+ * term, loc_a/loc_x f32 [B,L,nh,hd], carry f32 [2, B*nh*hd, NBLK].
+ * u/B in `dtype`; A_log [nh, *] f32 with row stride sal_h; dt f32. */
+int tssm_mh_fwd_local(int dtype, const void* u, const float* A_log, const void* B,
+                      const float* dt, float* loc_a, float* loc_x, float* carry,
+                      int64_t nbatch, int64_t L, int64_t H, int64_t n_heads, int64_t head_dim,
+                      int64_t su_b, int64_t su_l, int64_t sal_h, int64_t sB_b, int64_t sB_l,
+                      int64_t sB_h, int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t blk_l,
+                      int64_t nblk, int64_t grid_rows, int64_t grid_blks, void* stream);
+/* multihead_ssm_output_kernel (multihead_ssm_kernel.py:121-187): y contiguous
+ * [B, L, H] in `dtype`; C/u in `dtype`; D [H] f32. */
+int tssm_mh_output(int dtype, const float* loc_a, const float* loc_x, const float* carry,
+                   const void* C, const float* D, const void* u, void* y, int64_t nbatch,
+                   int64_t L, int64_t H, int64_t n_heads, int64_t head_dim, int64_t su_b,
+                   int64_t su_l, int64_t sC_b, int64_t sC_l, int64_t sC_h, int64_t blk_l,
+                   int64_t nblk, int64_t grid_rows, int64_t grid_blks, void* stream);
+
+/* Fused single-pass DIAG multihead scan (a9 -> a11 in one launch, with the
+ * discretization fused into the load stage and a decoupled look-back across
+ * chunks).  u [B,L,nh*hd], B/C [B,L,nh,hd], y [B,L,nh*hd] in `dtype`;
+ * A_log f32 [nh,hd] (a_per_head=0) or [nh] (a_per_head=1); dt f32 [B,L,nh];
+ * D f32 [nh*hd] or NULL; h0 f32 [B,nh,hd] or NULL; h_last f32 [B,nh,hd] or
+ * NULL.  head_dim must be a multiple of 8 and <= 128; channel rows must be
+ * 16-byte aligned.  `chunk` selects the time tile (64, 128 or 256). */
+int64_t tssm_mh_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t n_heads,
+                                     int64_t head_dim, int64_t chunk);
+int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log, const void* B,
+                       const void* C, const float* dt, const float* D, const float* h0,
+                       void* y, float* h_last, int64_t nbatch, int64_t L, int64_t n_heads,
+                       int64_t head_dim, int a_per_head, int64_t su_b, int64_t su_l,
+                       int64_t sB_b, int64_t sB_l, int64_t sB_h, int64_t sC_b, int64_t sC_l,
+                       int64_t sC_h, int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t sy_b,
+                       int64_t sy_l, int64_t chunk, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/* ------------------------------------------------------------------ interpolation
+ * fused_time_aware_interp_kernel / fused_interp_bf16_kernel /
+ * fused_interp_fp16_kernel (fused_interp_kernel.py:10-100 / :104-181 /
+ * :187-257).  V, Vhat in v_dtype; M and tau in any float dtype.  Grid
+ * (B, T, ceil(F/FTILE)): computes b < grid_b, t < grid_t, tiles < grid_f.
+ * K (search window, <= 64) and FTILE (tile of the "any observed" aggregate)
+ * are semantic: they change results. */
+int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, const void* V, const void* M,
+                           const void* tau, void* Vhat, int64_t nbatch, int64_t T, int64_t F,
+                           int64_t svb, int64_t svt, int64_t smb, int64_t smt, int64_t stb,
+                           int64_t stt, int64_t sob, int64_t sot, int64_t K, int64_t FTILE,
+                           int64_t grid_b, int64_t grid_t, int64_t grid_f, void* stream);
+
+/* fused_interp_ssm_step_kernel (fused_ssm_interp.py:12-101): interpolates
+ * step t_cur into Vhat[:, t_cur] and writes h_out = A_bar*h_in + B_bar*vhat.
+ * A_bar, B_bar [F], h_in, h_out f32.  Grid (B, ceil(F/FTILE)). */
+int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, const void* V, const void* M,
+                         const void* tau, const float* A_bar, const float* B_bar,
+                         const float* h_in, void* Vhat, float* h_out, int64_t nbatch, int64_t T,
+                         int64_t F, int64_t svb, int64_t svt, int64_t smb, int64_t smt,
+                         int64_t stb, int64_t stt, int64_t sob, int64_t sot, int64_t s_hib,
+                         int64_t s_hob, int64_t t_cur, int64_t K, int64_t FTILE, int64_t grid_b,
+                         int64_t grid_f, void* stream);
+
+/* ------------------------------------------------------------------ streaming
+ * streaming_ssm_inplace_kernel / streaming_ssm_inplace_bf16_kernel
+ * (streaming_inference_kernel.py:7-37 / :41-71).  All tensors in `dtype`;
+ * h updated in place; y uses vhat's batch stride svb.  Grid
+ * (B, ceil(H/BLOCK_H)): computes b < grid_b, lanes < min(H, h_cover). */
+int tssm_stream_step(int dtype, const void* vhat, void* h, const void* Abar, const void* Bbar,
+                     const void* C, const void* D, void* y, int64_t nbatch, int64_t H,
+                     int64_t grid_b, int64_t h_cover, int64_t svb, int64_t shb, int64_t scb,
+                     void* stream);
+
+/* streaming_interp_then_ssm_kernel (streaming_inference_kernel.py:75-156),
+ * f32 tensors and int32 ring_head.  One workgroup per stream makes the ring
+ * head update race-free; BLOCK_H stays the tile of the "any observed" test. */
+int tssm_stream_interp_step(float* ring_V, float* ring_M, float* ring_tau, int32_t* ring_head,
+                            const float* v_new, const float* m_new, const float* tau_new,
+                            float* h, const float* Abar, const float* Bbar, const float* C,
+                            const float* D, float* y, int64_t nbatch, int64_t H, int64_t srb,
+                            int64_t srk, int64_t svb, int64_t shb, int64_t scb, int64_t BLOCK_H,
+                            int64_t KRING, int64_t grid_b, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSSM_H_ */

@@ -1,0 +1,228 @@
+"""GPU parity of the reference-named drop-in kernels (discretize, elementwise
+scan, interpolation, fused interp step, streaming) against the float64 oracle.
+Each kernel is launched exactly as a caller of the reference would:
+``kernel[grid](*reference_args)``."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import TOL, assert_close, np64
+from oracle import ssm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------ discretize
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_zoh_discretize(dev, out_dtype):
+    import discretize_kernel as dk
+    g = torch.Generator().manual_seed(3)
+    Bsz, T, H, BLOCK_H = 3, 50, 200, 64
+    A = torch.empty(H).uniform_(np.log(0.5), np.log(5.0), generator=g).to(dev)
+    B = torch.randn(Bsz, T, H, generator=g).to(out_dtype).to(dev)
+    # include tiny dt*a (1e-5..1e-3 range where the accurate expm1 matters) and large ones
+    dt = torch.exp(torch.empty(Bsz, T).uniform_(np.log(1e-6), np.log(3.0), generator=g)).to(dev)
+    Abar = torch.empty(Bsz, T, H, device=dev, dtype=out_dtype)
+    Bbar = torch.empty_like(Abar)
+    kern = dk.zoh_discretize_diag_kernel if out_dtype == torch.float32 else dk.zoh_discretize_diag_bf16_kernel
+    kern[(Bsz, T, (H + BLOCK_H - 1) // BLOCK_H)](
+        A, B, dt, Abar, Bbar, Bsz, T, H, B.stride(0), B.stride(1), B.stride(2),
+        dt.stride(0), dt.stride(1), Abar.stride(0), Abar.stride(1), Abar.stride(2),
+        Bbar.stride(0), Bbar.stride(1), Bbar.stride(2), BLOCK_H=BLOCK_H)
+    torch.cuda.synchronize()
+    Ar, Br = O.zoh_discretize(A, B, dt)
+    tol = TOL[out_dtype]
+    assert_close(Abar, Ar, tol, "Abar")
+    assert_close(Bbar, Br, tol, "Bbar")
+    if out_dtype == torch.float32:  # elementwise relative accuracy of the accurate expm1
+        rel = np.abs(np64(Bbar) - Br) / np.maximum(np.abs(Br), 1e-30)
+        assert rel.max() < 2e-6
+
+
+def test_zoh_discretize_partial_grid(dev):
+    import discretize_kernel as dk
+    Bsz, T, H = 2, 4, 100
+    A = torch.zeros(H, device=dev)
+    B = torch.ones(Bsz, T, H, device=dev)
+    dt = torch.full((Bsz, T), 0.1, device=dev)
+    Abar = torch.full((Bsz, T, H), -7.0, device=dev)
+    Bbar = torch.full_like(Abar, -7.0)
+    dk.zoh_discretize_diag_kernel[(1, 2, 1)](
+        A, B, dt, Abar, Bbar, Bsz, T, H, *B.stride(), *dt.stride(), *Abar.stride(),
+        *Bbar.stride(), BLOCK_H=32)
+    torch.cuda.synchronize()
+    assert torch.all(Abar[0, :2, :32] != -7.0)
+    assert torch.all(Abar[0, :2, 32:] == -7.0) and torch.all(Abar[1] == -7.0)
+    assert torch.all(Abar[0, 2:] == -7.0)
+
+
+# ------------------------------------------------------------------ elementwise scan
+@pytest.mark.parametrize("BLK", [16, 64, 256])
+def test_ssm_forward_backward(dev, BLK):
+    import ssm_scan as ss
+    g = torch.Generator().manual_seed(BLK)
+    Bsz, L, H = 2, 300, 40
+    u, B, C, dY = (torch.randn(Bsz, L, H, generator=g).to(dev) for _ in range(4))
+    A = torch.empty(Bsz, L, H).uniform_(0.5, 1.0, generator=g).to(dev)
+    D = torch.randn(H, generator=g).to(dev)
+    y, h = ss.ssm_forward(u, A, B, C, D, BLK=BLK)
+    du, dA, dB, dC = ss.ssm_backward(u, A, B, C, h, dY, BLK=BLK)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssm_forward(u, A, B, C, D)
+    assert_close(h, h_ref, 1e-5, "h")
+    assert_close(y, y_ref, 1e-5, "y")
+    for got, ref, n in zip((du, dA, dB, dC), O.ssm_backward(u, A, B, C, h_ref, dY), "du dA dB dC".split()):
+        assert_close(got, ref, 1e-5, n)
+
+
+def test_ssm_phase_intermediates(dev):
+    import ssm_scan as ss
+    g = torch.Generator().manual_seed(1)
+    Bsz, L, H, BLK = 2, 100, 8, 32
+    u, B = (torch.randn(Bsz, L, H, generator=g).to(dev) for _ in range(2))
+    A = torch.empty(Bsz, L, H).uniform_(0.5, 1.0, generator=g).to(dev)
+    nblk = ss._nxt_pow2((L + BLK - 1) // BLK)
+    la, lx = torch.empty_like(A), torch.empty_like(A)
+    carry = torch.empty(2 * Bsz * H * nblk, device=dev)
+    ss.ssm_fwd_local_kernel[(Bsz * H, nblk)](u, A, B, la, lx, carry, Bsz, L, H, BLK, nblk)
+    torch.cuda.synchronize()
+    la_r, lx_r, c_r = O.ssm_fwd_local(u, A, B, BLK, nblk)
+    assert_close(la, la_r, 1e-6, "loc_a")
+    assert_close(lx, lx_r, 1e-6, "loc_x")
+    assert_close(carry, c_r, 1e-6, "carry")
+    ss.ssm_carry_scan_kernel[(Bsz * H,)](carry, Bsz * H, nblk)
+    torch.cuda.synchronize()
+    assert_close(carry, O.ssm_carry_scan(c_r, Bsz * H, nblk), 1e-6, "scanned carry")
+
+
+def test_ssm_forward_bf16(dev):
+    import ssm_scan as ss
+    g = torch.Generator().manual_seed(2)
+    Bsz, L, H = 2, 200, 16
+    u, B, C = (torch.randn(Bsz, L, H, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    A = torch.empty(Bsz, L, H).uniform_(0.5, 0.99, generator=g).to(torch.bfloat16).to(dev)
+    D = torch.randn(H, generator=g).to(torch.bfloat16).to(dev)
+    y, h = ss.ssm_forward(u, A, B, C, D, BLK=64)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssm_forward(u, A, B, C, D)
+    assert_close(y, y_ref, 1e-2, "y bf16")
+
+
+# ------------------------------------------------------------------ interpolation
+def _interp_inputs(Bsz, T, F, dtype, seed, p_obs=0.7, dev=None):
+    g = torch.Generator().manual_seed(seed)
+    tau = torch.sort(torch.rand(Bsz, T, generator=g) * 100, dim=1).values
+    M = (torch.rand(Bsz, T, F, generator=g) < p_obs).float()
+    V = (torch.randn(Bsz, T, F, generator=g) * M).to(dtype)
+    return V.to(dev), M.to(dev), tau.to(dev)
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.float32, "fused_time_aware_interp_kernel"),
+                                        (torch.bfloat16, "fused_interp_bf16_kernel"),
+                                        (torch.float16, "fused_interp_fp16_kernel")])
+@pytest.mark.parametrize("K,FTILE,p_obs", [(10, 128, 0.7), (3, 16, 0.02), (5, 7, 0.05)])
+def test_interp(dev, dtype, name, K, FTILE, p_obs):
+    import fused_interp_kernel as fi
+    Bsz, T, F = 3, 150, 100
+    V, M, tau = _interp_inputs(Bsz, T, F, dtype, seed=K * FTILE, p_obs=p_obs, dev=dev)
+    out = torch.full_like(V, float("nan"))
+    getattr(fi, name)[(Bsz, T, (F + FTILE - 1) // FTILE)](
+        V, M, tau, out, Bsz, T, F, *V.stride(), *M.stride(), *tau.stride(), *out.stride(),
+        K=K, FTILE=FTILE)
+    torch.cuda.synchronize()
+    ref = O.time_aware_interp(V, M, tau, K, FTILE)
+    assert_close(out, ref, TOL[dtype] if dtype != torch.float32 else 1e-6, name)
+
+
+def test_interp_full_size(dev):
+    """B=16 T=2048 F=256, K=10, FTILE=128, 30% missing (the measured interp workload)."""
+    import fused_interp_kernel as fi
+    from tssm import workloads
+    w = workloads.interp_mamba1()
+    V, M, tau = (w[k].to(dev) for k in ("V", "M", "tau"))
+    Bsz, T, F = V.shape
+    out = torch.empty_like(V)
+    fi.fused_time_aware_interp_kernel[(Bsz, T, 2)](V, M, tau, out, Bsz, T, F, *V.stride(),
+                                                  *M.stride(), *tau.stride(), *out.stride(), 10, 128)
+    torch.cuda.synchronize()
+    assert_close(out, O.time_aware_interp(V, M, tau, 10, 128), 1e-6, "interp full")
+
+
+def test_interp_ssm_step(dev):
+    import fused_ssm_interp as fs
+    Bsz, T, F, K, FT = 4, 40, 70, 4, 32
+    V, M, tau = _interp_inputs(Bsz, T, F, torch.float32, seed=4, p_obs=0.05, dev=dev)
+    g = torch.Generator().manual_seed(5)
+    Ab = torch.rand(F, generator=g).to(dev)
+    Bb = torch.randn(F, generator=g).to(dev)
+    h_in = torch.randn(Bsz, F, generator=g).to(dev)
+    h_out = torch.empty_like(h_in)
+    Vhat = torch.zeros_like(V)
+    h_ref = np64(h_in)
+    for t in range(T):
+        fs.fused_interp_ssm_step_kernel[(Bsz, (F + FT - 1) // FT)](
+            V, M, tau, Ab, Bb, h_in, Vhat, h_out, Bsz, T, F, *V.stride(), *M.stride(),
+            *tau.stride(), *Vhat.stride(), *h_in.stride(), *h_out.stride(), t, K=K, FTILE=FT)
+        v_ref, h_ref = O.interp_ssm_step(V, M, tau, Ab, Bb, h_ref, t, K, FT)
+        h_in, h_out = h_out, h_in
+    torch.cuda.synchronize()
+    assert_close(h_in, h_ref, 1e-5, "h after T steps")
+    assert_close(Vhat, O.time_aware_interp(V, M, tau, K, FT), 1e-6, "Vhat rows")
+
+
+# ------------------------------------------------------------------ streaming
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_streaming_inplace(dev, dtype):
+    import streaming_inference_kernel as sk
+    g = torch.Generator().manual_seed(6)
+    Bsz, H, BLOCK_H, steps = 5, 300, 128, 20
+    Ab = torch.rand(H, generator=g).to(dtype).to(dev)
+    Bb = torch.randn(H, generator=g).to(dtype).to(dev)
+    D = torch.randn(H, generator=g).to(dtype).to(dev)
+    h = torch.zeros(Bsz, H, device=dev, dtype=dtype)
+    h_chain = np.zeros((Bsz, H))
+    kern = sk.streaming_ssm_inplace_kernel if dtype == torch.float32 else sk.streaming_ssm_inplace_bf16_kernel
+    for _ in range(steps):
+        v = torch.randn(Bsz, H, generator=g).to(dtype).to(dev)
+        C = torch.randn(Bsz, H, generator=g).to(dtype).to(dev)
+        y = torch.empty_like(v)
+        h_before = h.clone()
+        kern[(Bsz, (H + BLOCK_H - 1) // BLOCK_H)](v, h, Ab, Bb, C, D, y, Bsz, H, *v.stride(),
+                                                   *h.stride(), *C.stride(), BLOCK_H=BLOCK_H)
+        h_step, y_ref = O.streaming_step(v, h_before, Ab, Bb, C, D)   # one step from the same state
+        h_chain, _ = O.streaming_step(v, h_chain, Ab, Bb, C, D)       # full-precision chain
+        torch.cuda.synchronize()
+        assert_close(y, y_ref, TOL[dtype], "y")
+        assert_close(h, h_step, TOL[dtype], "h (one step)")
+    assert_close(h, h_chain, TOL[dtype], "h (chained)")
+
+
+def test_streaming_ring_multi_tile(dev):
+    import streaming_inference_kernel as sk
+    g = torch.Generator().manual_seed(7)
+    Bsz, H, BLOCK_H, KR, steps = 3, 100, 32, 5, 12
+    ring_V = torch.zeros(Bsz, KR, H, device=dev)
+    ring_M = torch.zeros_like(ring_V)
+    ring_tau = torch.zeros(Bsz, KR, device=dev)
+    head = torch.zeros(Bsz, dtype=torch.int32, device=dev)
+    h = torch.zeros(Bsz, H, device=dev)
+    Ab, Bb, D = (torch.rand(H, generator=g).to(dev) for _ in range(3))
+    st = [np64(ring_V), np64(ring_M), np64(ring_tau), np.zeros(Bsz, dtype=np.int64), np.zeros((Bsz, H))]
+    for s in range(steps):
+        m = (torch.rand(Bsz, H, generator=g) < (0.0 if s % 3 == 1 else 0.05)).float().to(dev)
+        v = (torch.randn(Bsz, H, generator=g).to(dev)) * m
+        tau = torch.full((Bsz,), float(s), device=dev)
+        C = torch.randn(Bsz, H, generator=g).to(dev)
+        y = torch.empty_like(v)
+        sk.streaming_interp_then_ssm_kernel[(Bsz, (H + BLOCK_H - 1) // BLOCK_H)](
+            ring_V, ring_M, ring_tau, head, v, m, tau, h, Ab, Bb, C, D, y, Bsz, H, KR - 1,
+            *ring_V.stride(), *v.stride(), *h.stride(), *C.stride(), BLOCK_H=BLOCK_H, KRING=KR)
+        rV, rM, rt, hd, h_new, y_ref = O.streaming_interp_step(*st[:4], v, m, tau, st[4], Ab, Bb,
+                                                               C, D, BLOCK_H, KR)
+        st = [rV, rM, rt, hd, h_new]
+        torch.cuda.synchronize()
+        assert_close(y, y_ref, 1e-5, f"y step {s}")
+        assert np.array_equal(head.cpu().numpy(), hd)
+    assert_close(h, st[4], 1e-5, "h")
+    assert_close(ring_V, st[0], 0, "ring_V")
+    assert_close(ring_tau, st[2], 0, "ring_tau")

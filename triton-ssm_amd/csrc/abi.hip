@@ -1,0 +1,36 @@
+// Library-level entry points: version, status text, workspace error word.
+#include "common.h"
+#include "lookback.h"
+
+extern "C" int tssm_abi_version(void) { return 1; }
+
+extern "C" const char* tssm_strerror(int status) {
+  switch (status) {
+    case TSSM_OK: return "ok";
+    case TSSM_ERR_NULL: return "a required pointer is NULL";
+    case TSSM_ERR_SHAPE: return "invalid or inconsistent sizes";
+    case TSSM_ERR_STRIDE: return "invalid stride";
+    case TSSM_ERR_DTYPE: return "unsupported dtype";
+    case TSSM_ERR_WORKSPACE: return "workspace missing or too small";
+    case TSSM_ERR_UNSUPPORTED: return "unsupported configuration";
+    case TSSM_ERR_ALIGN: return "pointer or stride not aligned for vector access";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "unknown tssm status";
+}
+
+extern "C" int tssm_workspace_error(const void* workspace, int clear, int* error_out) {
+  TSSM_CHECK(workspace && error_out, TSSM_ERR_NULL);
+  const auto* hdr = reinterpret_cast<const tssm::WsHeader*>(workspace);
+  uint32_t e = 0;
+  hipError_t st = hipMemcpy(&e, &hdr->error, sizeof(e), hipMemcpyDeviceToHost);
+  if (st != hipSuccess) return (int)st;
+  *error_out = (int)e;
+  if (clear && e) {
+    const uint32_t z = 0;
+    st = hipMemcpy(const_cast<uint32_t*>(&hdr->error), &z, sizeof(z), hipMemcpyHostToDevice);
+    if (st != hipSuccess) return (int)st;
+  }
+  return TSSM_OK;
+}

@@ -1,0 +1,166 @@
+// Shared device/host helpers for the tssm HIP library (gfx950 only).
+//
+// * dtype codes and element conversion (bf16 round-to-nearest-even, fp16 via
+//   the hardware conversion),
+// * 16-byte vector load/store of 8 channels in any of the three dtypes,
+// * fast exp2 and an accurate phi1(x) = expm1(x)/x for the ZOH input term,
+// * status codes and the argument-check macros every C-ABI entry point uses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tssm.h"
+
+namespace tssm {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- dtypes
+enum DType : int { F32 = TSSM_F32, BF16 = TSSM_BF16, F16 = TSSM_F16 };
+
+struct bf16_t { uint16_t bits; };
+using f16_t = _Float16;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __host__ inline float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+// round-to-nearest-even, NaN kept quiet
+__device__ inline uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ inline float ld(const float* p) { return *p; }
+  static __device__ inline void st(float* p, float v) { *p = v; }
+};
+template <> struct Elem<bf16_t> {
+  static __device__ inline float ld(const bf16_t* p) {
+    return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[0]);
+  }
+  static __device__ inline void st(bf16_t* p, float v) {
+    reinterpret_cast<uint16_t*>(p)[0] = (uint16_t)f32_to_bf16_bits(v);
+  }
+};
+template <> struct Elem<f16_t> {
+  static __device__ inline float ld(const f16_t* p) { return (float)*p; }
+  static __device__ inline void st(f16_t* p, float v) { *p = (f16_t)v; }
+};
+
+template <typename T> __device__ inline float ldf(const T* p) { return Elem<T>::ld(p); }
+template <typename T> __device__ inline void stf(T* p, float v) { Elem<T>::st(p, v); }
+
+// Runtime-typed scalar load, for small side inputs (masks, timestamps) whose
+// dtype the caller chooses freely.  The switch is wave-uniform.
+__device__ inline float ld_any(const void* p, int64_t i, int dt) {
+  switch (dt) {
+    case BF16: return ldf(reinterpret_cast<const bf16_t*>(p) + i);
+    case F16: return ldf(reinterpret_cast<const f16_t*>(p) + i);
+    default: return reinterpret_cast<const float*>(p)[i];
+  }
+}
+
+// 8 consecutive channels as one vector load: 16 B for bf16/fp16, 32 B for fp32.
+template <typename T> struct Vec8;
+template <> struct Vec8<bf16_t> {
+  uint4 raw;
+  __device__ inline void load(const bf16_t* p) { raw = *reinterpret_cast<const uint4*>(p); }
+  __device__ inline void zero() { raw = make_uint4(0, 0, 0, 0); }
+  __device__ inline float get(int j) const {
+    uint32_t w = (&raw.x)[j >> 1];
+    return (j & 1) ? __uint_as_float(w & 0xffff0000u) : __uint_as_float(w << 16);
+  }
+};
+template <> struct Vec8<f16_t> {
+  uint4 raw;
+  __device__ inline void load(const f16_t* p) { raw = *reinterpret_cast<const uint4*>(p); }
+  __device__ inline void zero() { raw = make_uint4(0, 0, 0, 0); }
+  __device__ inline float get(int j) const {
+    uint32_t w = (&raw.x)[j >> 1];
+    uint16_t h = (j & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+    return (float)__builtin_bit_cast(f16_t, h);
+  }
+};
+template <> struct Vec8<float> {
+  float4 lo, hi;
+  __device__ inline void load(const float* p) {
+    lo = reinterpret_cast<const float4*>(p)[0];
+    hi = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ inline void zero() { lo = make_float4(0, 0, 0, 0); hi = lo; }
+  __device__ inline float get(int j) const { return j < 4 ? (&lo.x)[j] : (&hi.x)[j - 4]; }
+};
+
+// Store one value broadcast into 8 consecutive channels.
+template <typename T> __device__ inline void store_bcast8(T* p, float v);
+template <> __device__ inline void store_bcast8<bf16_t>(bf16_t* p, float v) {
+  uint32_t b = f32_to_bf16_bits(v);
+  uint32_t w = b | (b << 16);
+  __builtin_nontemporal_store(u32x4{w, w, w, w}, reinterpret_cast<u32x4*>(p));
+}
+template <> __device__ inline void store_bcast8<f16_t>(f16_t* p, float v) {
+  uint32_t b = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)v);
+  uint32_t w = b | (b << 16);
+  __builtin_nontemporal_store(u32x4{w, w, w, w}, reinterpret_cast<u32x4*>(p));
+}
+template <> __device__ inline void store_bcast8<float>(float* p, float v) {
+  f32x4 q = {v, v, v, v};
+  __builtin_nontemporal_store(q, reinterpret_cast<f32x4*>(p));
+  __builtin_nontemporal_store(q, reinterpret_cast<f32x4*>(p) + 1);
+}
+
+// ---------------------------------------------------------------- math
+// exp(x) for x = y*log2(e) given y pre-scaled: one v_exp_f32.  Results below
+// 2^-126 flush to zero (the state simply forgets), which is the intended
+// underflow behaviour for exp(dt*a) with very negative arguments.
+__device__ inline float exp2_fast(float y) { return __builtin_amdgcn_exp2f(y); }
+
+// phi1(x) = expm1(x)/x, phi1(0) = 1, accurate to a few ulp over all x<=0
+// (and moderate x>0).  |x| < 0.5: Taylor series of expm1(x)/x to degree 8
+// (truncation < 1e-9); otherwise (exp(x)-1)/x, where |exp(x)-1| >= 0.39 so
+// the subtraction loses no significant bits.  ``ex`` is exp(x), which every
+// caller has already computed for Abar.
+__device__ inline float phi1_from_exp(float x, float ex) {
+  float p = 1.0f / 362880.0f;
+  p = __builtin_fmaf(p, x, 1.0f / 40320.0f);
+  p = __builtin_fmaf(p, x, 1.0f / 5040.0f);
+  p = __builtin_fmaf(p, x, 1.0f / 720.0f);
+  p = __builtin_fmaf(p, x, 1.0f / 120.0f);
+  p = __builtin_fmaf(p, x, 1.0f / 24.0f);
+  p = __builtin_fmaf(p, x, 1.0f / 6.0f);
+  p = __builtin_fmaf(p, x, 0.5f);
+  p = __builtin_fmaf(p, x, 1.0f);
+  float big = (ex - 1.0f) * __builtin_amdgcn_rcpf(x);
+  return __builtin_fabsf(x) < 0.5f ? p : big;
+}
+__device__ inline float expm1_acc(float x, float ex) {
+  return x * phi1_from_exp(x, ex);
+}
+
+// Accurate exp for the fp32 paths: ocml expf (correctly range-reduced).
+__device__ inline float exp_acc(float x) { return expf(x); }
+
+// ---------------------------------------------------------------- status
+#define TSSM_CHECK(cond, code) \
+  do {                         \
+    if (!(cond)) return (code); \
+  } while (0)
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TSSM_OK : (int)e;
+}
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace tssm

@@ -1,0 +1,248 @@
+// Time-aware interpolation (fused_interp_kernel.py) and the fused
+// interpolation + one SSM step (fused_ssm_interp.py:12-101).
+//
+// Reference semantics kept exactly (they change results):
+//  * "observed" is a per-(b, t, FTILE-wide tile) aggregate: the tile's mask
+//    lanes summed > 0.5 (fused_interp_kernel.py:51-54);
+//  * prev/next = nearest step within K on each side with an observed tile;
+//  * w = clip((tau_t - tau_prev)/(tau_next - tau_prev), 0, 1), 0.5 when the
+//    denominator <= 1e-9 (:80-83);
+//  * vhat = interp / v_prev / v_next when a neighbour exists, else v_cur --
+//    an observed current value is overwritten when any neighbour exists (:94-97).
+//
+// interp_kernel: one workgroup per (b, tile, block of TB steps).  The tile
+// aggregates of the TB + 2K rows the block needs are computed once into LDS
+// (the reference re-reads the mask tile 2K+1 times per output row), the
+// neighbour indices and weights are resolved per step, then every thread
+// streams its feature lanes: V rows are read once plus the neighbour rows.
+#include "common.h"
+
+namespace tssm {
+
+constexpr int kInterpTB = 64;     // time steps per workgroup
+constexpr int kInterpThreads = 256;
+constexpr int kMaxK = 64;         // largest search window supported
+
+// Sum of the tile's mask lanes for one row, by one wave.
+__device__ inline float wave_tile_sum(const void* M, int md, int64_t row_off, int64_t f0,
+                                      int64_t f1, int lane) {
+  float s = 0.0f;
+  for (int64_t f = f0 + lane; f < f1; f += 64) s += ld_any(M, row_off + f, md);
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  return s;
+}
+
+struct InterpArgs {
+  const void* V;
+  const void* M;
+  const void* tau;
+  void* Vhat;
+  int md, td;
+  int64_t T, F, svb, svt, smb, smt, stb, stt, sob, sot;
+  int64_t K, FTILE, grid_t;
+};
+
+template <typename TV>
+__global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
+  __shared__ unsigned char s_obs[kInterpTB + 2 * kMaxK];
+  __shared__ int s_prev[kInterpTB], s_next[kInterpTB];
+  __shared__ float s_w[kInterpTB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * kInterpTB;
+  const int64_t tile = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int64_t f0 = tile * a.FTILE;
+  const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
+  const int K = (int)a.K;
+  const int nrow = kInterpTB + 2 * K;
+  // 1. tile aggregates of rows t0-K .. t0+TB+K-1 (rows outside [0, T) are unobserved)
+  for (int i = wave; i < nrow; i += kInterpThreads / 64) {
+    const int64_t t = t0 - K + i;
+    bool obs = false;
+    if (t >= 0 && t < a.T) obs = wave_tile_sum(a.M, a.md, b * a.smb + t * a.smt, f0, f1, lane) > 0.5f;
+    if (lane == 0) s_obs[i] = obs ? 1 : 0;
+  }
+  __syncthreads();
+  // 2. neighbours and weight per step
+  if (tid < kInterpTB) {
+    const int64_t t = t0 + tid;
+    int prev = -1, next = -1;
+    float w = 0.5f;
+    if (t < a.grid_t) {
+      for (int k = 1; k <= K; ++k)
+        if (prev < 0 && s_obs[tid + K - k]) prev = (int)(t - k);
+      for (int k = 1; k <= K; ++k)
+        if (next < 0 && s_obs[tid + K + k]) next = (int)(t + k);
+      const float tau_t = ld_any(a.tau, b * a.stb + t * a.stt, a.td);
+      const float tp = prev >= 0 ? ld_any(a.tau, b * a.stb + prev * a.stt, a.td) : 0.0f;
+      const float tn = next >= 0 ? ld_any(a.tau, b * a.stb + next * a.stt, a.td) : 0.0f;
+      const float den = tn - tp;
+      w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
+      w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+    }
+    s_prev[tid] = prev;
+    s_next[tid] = next;
+    s_w[tid] = w;
+  }
+  __syncthreads();
+  // 3. feature lanes
+  const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb;
+  TV* O = reinterpret_cast<TV*>(a.Vhat) + b * a.sob;
+  const int tmax = (int)((a.grid_t - t0) < kInterpTB ? (a.grid_t - t0) : kInterpTB);
+  for (int i = 0; i < tmax; ++i) {
+    const int64_t t = t0 + i;
+    const int prev = s_prev[i], next = s_next[i];
+    const float w = s_w[i];
+    for (int64_t f = f0 + tid; f < f1; f += kInterpThreads) {
+      float v;
+      if (prev >= 0 && next >= 0)
+        v = (1.0f - w) * ldf(V + prev * a.svt + f) + w * ldf(V + next * a.svt + f);
+      else if (prev >= 0)
+        v = ldf(V + prev * a.svt + f);
+      else if (next >= 0)
+        v = ldf(V + next * a.svt + f);
+      else
+        v = ldf(V + t * a.svt + f);
+      stf(O + t * a.sot + f, v);
+    }
+  }
+}
+
+// fused_interp_ssm_step_kernel: one workgroup per (b, tile) at step t_cur.
+struct StepArgs {
+  const void* V;
+  const void* M;
+  const void* tau;
+  const float* A_bar;
+  const float* B_bar;
+  const float* h_in;
+  void* Vhat;
+  float* h_out;
+  int md, td;
+  int64_t nb, T, F, svb, svt, smb, smt, stb, stt, sob, sot, s_hib, s_hob;
+  int64_t t_cur, K, FTILE;
+};
+
+template <typename TV>
+__global__ __launch_bounds__(kInterpThreads) void interp_step_kernel(StepArgs a) {
+  __shared__ unsigned char s_obs[2 * kMaxK + 1];
+  __shared__ int s_pn[2];
+  __shared__ float s_w;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t tile = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t f0 = tile * a.FTILE;
+  const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
+  const int K = (int)a.K;
+  for (int i = wave; i < 2 * K + 1; i += kInterpThreads / 64) {
+    const int64_t t = a.t_cur - K + i;
+    bool obs = false;
+    if (t >= 0 && t < a.T) obs = wave_tile_sum(a.M, a.md, b * a.smb + t * a.smt, f0, f1, lane) > 0.5f;
+    if (lane == 0) s_obs[i] = obs ? 1 : 0;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int prev = -1, next = -1;
+    for (int k = 1; k <= K; ++k)
+      if (prev < 0 && s_obs[K - k]) prev = (int)(a.t_cur - k);
+    for (int k = 1; k <= K; ++k)
+      if (next < 0 && s_obs[K + k]) next = (int)(a.t_cur + k);
+    const float tau_t = ld_any(a.tau, b * a.stb + a.t_cur * a.stt, a.td);
+    const float tp = prev >= 0 ? ld_any(a.tau, b * a.stb + prev * a.stt, a.td) : 0.0f;
+    const float tn = next >= 0 ? ld_any(a.tau, b * a.stb + next * a.stt, a.td) : 0.0f;
+    const float den = tn - tp;
+    float w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
+    s_w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+    s_pn[0] = prev;
+    s_pn[1] = next;
+  }
+  __syncthreads();
+  const int prev = s_pn[0], next = s_pn[1];
+  const float w = s_w;
+  const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb;
+  TV* O = reinterpret_cast<TV*>(a.Vhat) + b * a.sob;
+  for (int64_t f = f0 + tid; f < f1; f += kInterpThreads) {
+    float v;
+    if (prev >= 0 && next >= 0)
+      v = (1.0f - w) * ldf(V + prev * a.svt + f) + w * ldf(V + next * a.svt + f);
+    else if (prev >= 0)
+      v = ldf(V + prev * a.svt + f);
+    else if (next >= 0)
+      v = ldf(V + next * a.svt + f);
+    else
+      v = ldf(V + a.t_cur * a.svt + f);
+    stf(O + a.t_cur * a.sot + f, v);
+    // h_in is read as 0 where b*stride_hib + f >= B*F (fused_ssm_interp.py:97-98)
+    const int64_t lin = b * a.s_hib + f;
+    const float hp = lin < a.nb * a.F ? a.h_in[lin] : 0.0f;
+    a.h_out[b * a.s_hob + f] = a.A_bar[f] * hp + a.B_bar[f] * v;
+  }
+}
+
+}  // namespace tssm
+
+using namespace tssm;
+
+static bool float_dtype(int d) { return d == TSSM_F32 || d == TSSM_BF16 || d == TSSM_F16; }
+
+extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, const void* V,
+                                      const void* M, const void* tau, void* Vhat, int64_t nbatch,
+                                      int64_t T, int64_t F, int64_t svb, int64_t svt, int64_t smb,
+                                      int64_t smt, int64_t stb, int64_t stt, int64_t sob,
+                                      int64_t sot, int64_t K, int64_t FTILE, int64_t grid_b,
+                                      int64_t grid_t, int64_t grid_f, void* stream) {
+  TSSM_CHECK(V && M && tau && Vhat, TSSM_ERR_NULL);
+  TSSM_CHECK(float_dtype(v_dtype) && float_dtype(m_dtype) && float_dtype(tau_dtype),
+             TSSM_ERR_DTYPE);
+  TSSM_CHECK(nbatch >= 0 && T >= 0 && F >= 0 && FTILE > 0 && K >= 0, TSSM_ERR_SHAPE);
+  TSSM_CHECK(grid_b >= 0 && grid_t >= 0 && grid_f >= 0 && grid_b <= nbatch && grid_t <= T,
+             TSSM_ERR_SHAPE);
+  TSSM_CHECK(K <= kMaxK, TSSM_ERR_UNSUPPORTED);
+  const int64_t ntile = (F + FTILE - 1) / FTILE;
+  const int64_t gf = grid_f < ntile ? grid_f : ntile;
+  if (grid_b == 0 || grid_t == 0 || gf == 0) return TSSM_OK;
+  TSSM_CHECK(gf <= 65535 && grid_b <= 65535, TSSM_ERR_UNSUPPORTED);
+  InterpArgs a{V, M, tau, Vhat, m_dtype, tau_dtype, T, F, svb, svt, smb, smt, stb, stt, sob, sot,
+               K, FTILE, grid_t};
+  const dim3 grid((unsigned)((grid_t + kInterpTB - 1) / kInterpTB), (unsigned)gf,
+                  (unsigned)grid_b);
+  const hipStream_t s = as_stream(stream);
+  switch (v_dtype) {
+    case TSSM_F32: hipLaunchKernelGGL(interp_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
+    case TSSM_BF16: hipLaunchKernelGGL(interp_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL(interp_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+  }
+  return launch_status();
+}
+
+extern "C" int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, const void* V,
+                                    const void* M, const void* tau, const float* A_bar,
+                                    const float* B_bar, const float* h_in, void* Vhat,
+                                    float* h_out, int64_t nbatch, int64_t T, int64_t F,
+                                    int64_t svb, int64_t svt, int64_t smb, int64_t smt,
+                                    int64_t stb, int64_t stt, int64_t sob, int64_t sot,
+                                    int64_t s_hib, int64_t s_hob, int64_t t_cur, int64_t K,
+                                    int64_t FTILE, int64_t grid_b, int64_t grid_f,
+                                    void* stream) {
+  TSSM_CHECK(V && M && tau && A_bar && B_bar && h_in && Vhat && h_out, TSSM_ERR_NULL);
+  TSSM_CHECK(float_dtype(v_dtype) && float_dtype(m_dtype) && float_dtype(tau_dtype),
+             TSSM_ERR_DTYPE);
+  TSSM_CHECK(nbatch >= 0 && T > 0 && F >= 0 && FTILE > 0 && K >= 0, TSSM_ERR_SHAPE);
+  TSSM_CHECK(t_cur >= 0 && t_cur < T, TSSM_ERR_SHAPE);
+  TSSM_CHECK(grid_b >= 0 && grid_f >= 0 && grid_b <= nbatch, TSSM_ERR_SHAPE);
+  TSSM_CHECK(K <= kMaxK, TSSM_ERR_UNSUPPORTED);
+  const int64_t ntile = (F + FTILE - 1) / FTILE;
+  const int64_t gf = grid_f < ntile ? grid_f : ntile;
+  if (grid_b == 0 || gf == 0) return TSSM_OK;
+  TSSM_CHECK(gf <= 2147483647 && grid_b <= 65535, TSSM_ERR_UNSUPPORTED);
+  StepArgs a{V, M, tau, A_bar, B_bar, h_in, Vhat, h_out, m_dtype, tau_dtype, nbatch, T, F,
+             svb, svt, smb, smt, stb, stt, sob, sot, s_hib, s_hob, t_cur, K, FTILE};
+  const dim3 grid((unsigned)gf, (unsigned)grid_b);
+  const hipStream_t s = as_stream(stream);
+  switch (v_dtype) {
+    case TSSM_F32: hipLaunchKernelGGL(interp_step_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
+    case TSSM_BF16: hipLaunchKernelGGL(interp_step_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL(interp_step_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+  }
+  return launch_status();
+}

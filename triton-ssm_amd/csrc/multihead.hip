@@ -1,0 +1,513 @@
+// Multihead DIAG selective scan (multihead_ssm_kernel.py).
+//
+// mh_scan_fused_kernel -- single pass over HBM:
+//   tile = (batch b, head h, chunk c) of TC time steps x P channels, taken in
+//   ticket order c-major (tile = c * rows + b * n_heads + h), so consecutive
+//   chunks of one row are a whole layer of rows apart in launch order.
+//   Thread layout: a wave covers ROWS = 64/G "runs" of R consecutive steps;
+//   each thread owns 8 consecutive channels (one 16-byte bf16 vector) of one
+//   run, so every load instruction reads ROWS whole 128-byte channel rows.
+//   1. load u, B, C (bf16/fp16/fp32) and dt for the thread's R steps;
+//   2. sweep 1: discretize in registers (Abar = exp(dt a), Euler or ZOH input
+//      term), run-local scan from (1, 0), keep w_t = C_t * a_loc_t and
+//      y1_t = sum C_t x_loc_t + D u_t;
+//   3. run aggregates -> LDS; wave 0 scans the runs per channel, publishes
+//      the tile aggregate, looks back for the carry-in, publishes the
+//      inclusive state and writes each run's entry state to LDS;
+//   4. sweep 2: y_t = y1_t + sum_j w_t[j] S[j], reduced over the G threads of
+//      the run with DPP and stored broadcast over the head's channels.
+//   HBM traffic = inputs once + y once + ~1.5 KB of carry words per tile.
+//
+// mh_fwd_local_kernel / mh_output_kernel -- the reference's phase-exact
+// kernels with its intermediate layouts (loc_a, loc_x, carry).
+#include "common.h"
+#include "lookback.h"
+
+namespace tssm {
+
+// ---------------------------------------------------------------- DPP helpers
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+// Sum over aligned groups of G consecutive lanes (G in 1,2,4,8,16); every lane
+// of the group receives the sum.
+template <int G>
+__device__ inline float group_sum(float v) {
+  if constexpr (G >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
+  if constexpr (G >= 16) v += dpp_mov<0x140>(v); // row_mirror
+  return v;
+}
+
+struct MhArgs {
+  const void* u;
+  const float* A_log;
+  const void* B;
+  const void* C;
+  const float* dt;
+  const float* D;
+  const float* h0;
+  void* y;
+  float* h_last;
+  int64_t L, n_heads, nchunks, nrows;
+  int64_t su_b, su_l, sB_b, sB_l, sB_h, sC_b, sC_l, sC_h, sdt_b, sdt_l, sdt_h, sy_b, sy_l;
+  WsHeader* hdr;
+  uint64_t* words;
+  uint32_t ntiles;
+  uint32_t spin_limit;
+};
+
+constexpr int kMhR = 4;  // consecutive steps per thread
+
+template <typename T, int DISC, bool APH, int G>
+__global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
+  constexpr int P = G * 8;
+  constexpr int ROWS = 64 / G;
+  constexpr int R = kMhR;
+  extern __shared__ float s_mem[];  // [NRUN][P] run aggregates a, then x
+  __shared__ uint32_t s_tk[2];
+
+  const int W = blockDim.x >> 6;
+  const int NRUN = W * ROWS;
+  const int TC = NRUN * R;
+  float* s_a = s_mem;
+  float* s_x = s_mem + NRUN * P;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int g = lane % G;
+  const int run = wave * ROWS + lane / G;
+  const int ch0 = g * 8;
+
+  if (tid == 0) {
+    uint32_t tk, tag;
+    take_ticket(a.hdr, &tk, &tag);
+    s_tk[0] = tk;
+    s_tk[1] = tag;
+  }
+  __syncthreads();
+  if (s_tk[0] >= a.ntiles) {  // counter not reset by a previous launch: touch nothing
+    if (tid == 0) {
+      flag_error(a.hdr);
+      retire(a.hdr, a.ntiles);
+    }
+    return;
+  }
+  const int64_t tile = s_tk[0];
+  const uint32_t tag = s_tk[1];
+  const int64_t c = tile / a.nrows;
+  const int64_t row = tile - c * a.nrows;
+  const int64_t b = row / a.n_heads;
+  const int64_t h = row - b * a.n_heads;
+  const int64_t t0 = c * TC + (int64_t)run * R;
+
+  // ---- loads (all issued before any use)
+  Vec8<T> vu[R], vB[R], vC[R];
+  float dtv[R];
+  {
+    const T* up = reinterpret_cast<const T*>(a.u) + b * a.su_b + h * P + ch0;
+    const T* Bp = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h + ch0;
+    const T* Cp = reinterpret_cast<const T*>(a.C) + b * a.sC_b + h * a.sC_h + ch0;
+    const float* dp = a.dt + b * a.sdt_b + h * a.sdt_h;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t = t0 + r;
+      if (t < a.L) {
+        vu[r].load(up + t * a.su_l);
+        vB[r].load(Bp + t * a.sB_l);
+        vC[r].load(Cp + t * a.sC_l);
+        dtv[r] = dp[t * a.sdt_l];
+      } else {
+        vu[r].zero();
+        vB[r].zero();
+        vC[r].zero();
+        dtv[r] = 0.0f;  // identity step: Abar = 1, input term 0
+      }
+    }
+  }
+  float a2[8];  // a * log2(e) per channel (or per head)
+  if constexpr (APH) {
+    const float v = -expf(a.A_log[h]) * kLog2e;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a2[j] = v;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a2[j] = -expf(a.A_log[h * P + ch0 + j]) * kLog2e;
+  }
+  const bool has_d = a.D != nullptr;
+  float Dv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) Dv[j] = has_d ? a.D[h * P + ch0 + j] : 0.0f;
+
+  // ---- sweep 1: discretize + run-local scan
+  float al[8], xl[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    al[j] = 1.0f;
+    xl[j] = 0.0f;
+  }
+  float w[R][8];
+  float y1[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+    float ab_h = 0.0f, coef_h = 0.0f;
+    if constexpr (APH) {
+      const float arg = dtv[r] * a2[0];
+      ab_h = exp2_fast(arg);
+      coef_h = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab_h) * dtv[r]
+                                       : dtv[r];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float ab, coef;
+      if constexpr (APH) {
+        ab = ab_h;
+        coef = coef_h;
+      } else {
+        const float arg = dtv[r] * a2[j];
+        ab = exp2_fast(arg);
+        coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * dtv[r]
+                                       : dtv[r];
+      }
+      const float uj = vu[r].get(j);
+      const float xin = coef * vB[r].get(j) * uj;
+      xl[j] = __builtin_fmaf(ab, xl[j], xin);
+      al[j] = al[j] * ab;
+      const float cj = vC[r].get(j);
+      w[r][j] = cj * al[j];
+      acc = __builtin_fmaf(cj, xl[j], acc);
+      acc = __builtin_fmaf(Dv[j], uj, acc);
+    }
+    y1[r] = acc;
+  }
+  // run aggregates -> LDS
+  {
+    float4* pa = reinterpret_cast<float4*>(s_a + run * P + ch0);
+    float4* px = reinterpret_cast<float4*>(s_x + run * P + ch0);
+    pa[0] = make_float4(al[0], al[1], al[2], al[3]);
+    pa[1] = make_float4(al[4], al[5], al[6], al[7]);
+    px[0] = make_float4(xl[0], xl[1], xl[2], xl[3]);
+    px[1] = make_float4(xl[4], xl[5], xl[6], xl[7]);
+  }
+  __syncthreads();
+
+  // ---- wave 0: scan runs, look back, publish, per-run entry states
+  if (wave == 0) {
+    CarrySlot slot{a.words + row * a.nchunks * 3 * P, 3 * P, P};
+    for (int ch = lane; ch < P; ch += 64) {
+      float A = 1.0f, X = 0.0f;
+      for (int q = 0; q < NRUN; ++q) {  // exclusive prefix, written in place
+        const float ra = s_a[q * P + ch];
+        const float rx = s_x[q * P + ch];
+        s_a[q * P + ch] = A;
+        s_x[q * P + ch] = X;
+        X = __builtin_fmaf(ra, X, rx);
+        A = A * ra;
+      }
+      if (c > 0) {
+        st_word(slot.agg_a(c, ch), A, tag);
+        st_word(slot.agg_x(c, ch), X, tag);
+      }
+      const float hin = a.h0 ? a.h0[row * P + ch] : 0.0f;
+      const float carry =
+          (c > 0) ? lookback_channel(slot, c, ch, tag, hin, a.spin_limit, a.hdr) : hin;
+      const float incl = __builtin_fmaf(A, carry, X);
+      st_word(slot.inc(c, ch), incl, tag);
+      if (a.h_last && c == a.nchunks - 1) a.h_last[row * P + ch] = incl;
+      for (int q = 0; q < NRUN; ++q)
+        s_x[q * P + ch] = __builtin_fmaf(s_a[q * P + ch], carry, s_x[q * P + ch]);
+    }
+  }
+  __syncthreads();
+  if (tid == 0) retire(a.hdr, a.ntiles);
+
+  // ---- sweep 2: add the carried-in state, reduce over channels, store
+  float S[8];
+  {
+    const float4* px = reinterpret_cast<const float4*>(s_x + run * P + ch0);
+    const float4 s0 = px[0], s1 = px[1];
+    S[0] = s0.x; S[1] = s0.y; S[2] = s0.z; S[3] = s0.w;
+    S[4] = s1.x; S[5] = s1.y; S[6] = s1.z; S[7] = s1.w;
+  }
+  T* yp = reinterpret_cast<T*>(a.y) + b * a.sy_b + h * P + ch0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float v = y1[r];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v = __builtin_fmaf(w[r][j], S[j], v);
+    v = group_sum<G>(v);
+    const int64_t t = t0 + r;
+    if (t < a.L) store_bcast8<T>(yp + t * a.sy_l, v);
+  }
+}
+
+// ---------------------------------------------------------------- phase-exact kernels
+// multihead_ssm_fwd_local_kernel (multihead_ssm_kernel.py:20-102): one
+// workgroup per Triton program (row = b*nh + h, blk); thread per channel p,
+// sequential over the chunk.
+template <typename T>
+__global__ void mh_fwd_local_kernel(const T* __restrict__ u, const float* __restrict__ A_log,
+                                    const T* __restrict__ Bm, const float* __restrict__ dt,
+                                    float* __restrict__ loc_a, float* __restrict__ loc_x,
+                                    float* __restrict__ carry, int64_t nbatch, int64_t L,
+                                    int64_t H, int64_t nh, int64_t hd, int64_t su_b, int64_t su_l,
+                                    int64_t sal_h, int64_t sB_b, int64_t sB_l, int64_t sB_h,
+                                    int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t blk_l,
+                                    int64_t nblk) {
+  const int64_t rowi = blockIdx.y;
+  const int64_t blk = blockIdx.x;
+  const int64_t bi = rowi / nh;
+  const int64_t hi = rowi - bi * nh;
+  const int64_t ts = blk * blk_l;
+  const int64_t te = ts + blk_l > L ? L : ts + blk_l;
+  const int64_t rows_tot = nbatch * nh * hd;
+  for (int64_t p = threadIdx.x; p < hd; p += blockDim.x) {
+    const float a = -expf(A_log[hi * sal_h + p]);
+    const int64_t uo = hi * hd + p;
+    const bool u_ok = uo < H;
+    float ar = 1.0f, xr = 0.0f;
+    for (int64_t t = ts; t < te; ++t) {
+      const float d = dt[bi * sdt_b + t * sdt_l + hi * sdt_h];
+      const float ab = expf(d * a);
+      const float bv = ldf(Bm + bi * sB_b + t * sB_l + hi * sB_h + p);
+      const float uv = u_ok ? ldf(u + bi * su_b + t * su_l + uo) : 0.0f;
+      xr = ab * xr + d * bv * uv;
+      ar = ab * ar;
+      const int64_t off = bi * (L * nh * hd) + t * (nh * hd) + hi * hd + p;
+      loc_a[off] = ar;
+      loc_x[off] = xr;
+    }
+    const int64_t rf = bi * (nh * hd) + hi * hd + p;
+    carry[rf * nblk + blk] = ar;
+    carry[rows_tot * nblk + rf * nblk + blk] = xr;
+  }
+}
+
+// Block-wide sum (blockDim multiple of 64, <= 1024) returned to every thread.
+__device__ inline float block_sum(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int nw = blockDim.x >> 6;
+  if (nw == 1) return v;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.0f;
+  for (int i = 0; i < nw; ++i) s += red[i];
+  return s;
+}
+
+// multihead_ssm_output_kernel (multihead_ssm_kernel.py:121-187).
+template <typename T>
+__global__ void mh_output_kernel(const float* __restrict__ loc_a, const float* __restrict__ loc_x,
+                                 const float* __restrict__ carry, const T* __restrict__ Cm,
+                                 const float* __restrict__ D, const T* __restrict__ u,
+                                 T* __restrict__ y, int64_t nbatch, int64_t L, int64_t H,
+                                 int64_t nh, int64_t hd, int64_t su_b, int64_t su_l, int64_t sC_b,
+                                 int64_t sC_l, int64_t sC_h, int64_t blk_l, int64_t nblk) {
+  __shared__ float red[16];
+  const int64_t rowi = blockIdx.y;
+  const int64_t blk = blockIdx.x;
+  const int64_t bi = rowi / nh;
+  const int64_t hi = rowi - bi * nh;
+  const int64_t ts = blk * blk_l;
+  const int64_t te = ts + blk_l > L ? L : ts + blk_l;
+  const int64_t rows_tot = nbatch * nh * hd;
+  const int64_t p = threadIdx.x;
+  const bool active = p < hd;
+  const int64_t uo = hi * hd + p;
+  const bool u_ok = active && uo < H;
+  float x_pref = 0.0f;
+  if (active && blk > 0) {
+    const int64_t rf = bi * (nh * hd) + hi * hd + p;
+    x_pref = carry[rows_tot * nblk + rf * nblk + blk - 1];
+  }
+  const float dv = u_ok ? D[uo] : 0.0f;
+  for (int64_t t = ts; t < te; ++t) {
+    float contrib = 0.0f;
+    if (active) {
+      const int64_t off = bi * (L * nh * hd) + t * (nh * hd) + hi * hd + p;
+      const float hv = loc_a[off] * x_pref + loc_x[off];
+      contrib = ldf(Cm + bi * sC_b + t * sC_l + hi * sC_h + p) * hv;
+      if (u_ok) contrib += dv * ldf(u + bi * su_b + t * su_l + uo);
+    }
+    const float yv = block_sum(contrib, red);
+    if (u_ok) stf(y + bi * (L * H) + t * H + uo, yv);
+  }
+}
+
+// ---------------------------------------------------------------- host side
+namespace {
+
+struct TileCfg {
+  int G, W, TC;
+};
+
+inline bool mh_tile_cfg(int64_t head_dim, int64_t chunk, TileCfg* cfg) {
+  if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 128) return false;
+  const int G = (int)(head_dim / 8);
+  if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) return false;
+  const int rows = 64 / G;
+  int W = (int)(chunk / (rows * kMhR));
+  if (W < 1) W = 1;
+  if (W > 8) W = 8;
+  cfg->G = G;
+  cfg->W = W;
+  cfg->TC = W * rows * kMhR;
+  return true;
+}
+
+template <typename T, int DISC, bool APH>
+int launch_mh_fused_g(int G, dim3 grid, dim3 block, size_t lds, hipStream_t s, const MhArgs& a) {
+  switch (G) {
+    case 1: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, 1>), grid, block, lds, s, a); break;
+    case 2: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, 2>), grid, block, lds, s, a); break;
+    case 4: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, 4>), grid, block, lds, s, a); break;
+    case 8: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, 8>), grid, block, lds, s, a); break;
+    case 16: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, 16>), grid, block, lds, s, a); break;
+    default: return TSSM_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+template <typename T>
+int launch_mh_fused_t(int disc, bool aph, int G, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                      const MhArgs& a) {
+  if (disc == TSSM_DISC_ZOH)
+    return aph ? launch_mh_fused_g<T, TSSM_DISC_ZOH, true>(G, grid, block, lds, s, a)
+               : launch_mh_fused_g<T, TSSM_DISC_ZOH, false>(G, grid, block, lds, s, a);
+  return aph ? launch_mh_fused_g<T, TSSM_DISC_EULER, true>(G, grid, block, lds, s, a)
+             : launch_mh_fused_g<T, TSSM_DISC_EULER, false>(G, grid, block, lds, s, a);
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+}  // namespace tssm
+
+using namespace tssm;
+
+extern "C" int64_t tssm_mh_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t n_heads,
+                                                int64_t head_dim, int64_t chunk) {
+  TileCfg cfg;
+  if (nbatch <= 0 || L <= 0 || n_heads <= 0 || !mh_tile_cfg(head_dim, chunk, &cfg)) return -1;
+  const int64_t nchunks = cdiv(L, cfg.TC);
+  return (int64_t)sizeof(WsHeader) + nbatch * n_heads * nchunks * 3 * head_dim * 8;
+}
+
+extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log,
+                                  const void* B, const void* C, const float* dt, const float* D,
+                                  const float* h0, void* y, float* h_last, int64_t nbatch,
+                                  int64_t L, int64_t n_heads, int64_t head_dim, int a_per_head,
+                                  int64_t su_b, int64_t su_l, int64_t sB_b, int64_t sB_l,
+                                  int64_t sB_h, int64_t sC_b, int64_t sC_l, int64_t sC_h,
+                                  int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t sy_b,
+                                  int64_t sy_l, int64_t chunk, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(u && A_log && B && C && dt && y, TSSM_ERR_NULL);
+  TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nbatch > 0 && L > 0 && n_heads > 0, TSSM_ERR_SHAPE);
+  TileCfg cfg;
+  TSSM_CHECK(mh_tile_cfg(head_dim, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
+  const int64_t need = tssm_mh_scan_workspace_bytes(nbatch, L, n_heads, head_dim, chunk);
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);
+  // 8-channel vectors must be 16-byte aligned: base pointers and every stride.
+  const int64_t vec = dtype == TSSM_F32 ? 4 : 8;
+  const int64_t strides[] = {su_b, su_l, sB_b, sB_l, sB_h, sC_b, sC_l, sC_h, sy_b, sy_l};
+  for (int64_t s : strides) TSSM_CHECK(s >= 0 && s % vec == 0, TSSM_ERR_ALIGN);
+  TSSM_CHECK(aligned(u, 16) && aligned(B, 16) && aligned(C, 16) && aligned(y, 16),
+             TSSM_ERR_ALIGN);
+  TSSM_CHECK(sdt_b >= 0 && sdt_l >= 0 && sdt_h >= 0, TSSM_ERR_STRIDE);
+
+  MhArgs a;
+  a.u = u; a.A_log = A_log; a.B = B; a.C = C; a.dt = dt; a.D = D; a.h0 = h0; a.y = y;
+  a.h_last = h_last;
+  a.L = L; a.n_heads = n_heads;
+  a.nchunks = cdiv(L, cfg.TC);
+  a.nrows = nbatch * n_heads;
+  a.su_b = su_b; a.su_l = su_l; a.sB_b = sB_b; a.sB_l = sB_l; a.sB_h = sB_h;
+  a.sC_b = sC_b; a.sC_l = sC_l; a.sC_h = sC_h;
+  a.sdt_b = sdt_b; a.sdt_l = sdt_l; a.sdt_h = sdt_h; a.sy_b = sy_b; a.sy_l = sy_l;
+  a.hdr = reinterpret_cast<WsHeader*>(workspace);
+  a.words = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + sizeof(WsHeader));
+  const int64_t ntiles = a.nchunks * a.nrows;
+  TSSM_CHECK(ntiles < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
+  a.ntiles = (uint32_t)ntiles;
+  a.spin_limit = kDefaultSpinLimit;
+
+  const dim3 grid((unsigned)ntiles), block((unsigned)(cfg.W * 64));
+  const size_t lds = (size_t)cfg.W * (64 / cfg.G) * head_dim * 2 * sizeof(float);
+  const hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case TSSM_BF16: return launch_mh_fused_t<bf16_t>(disc, a_per_head != 0, cfg.G, grid, block, lds, s, a);
+    case TSSM_F16: return launch_mh_fused_t<f16_t>(disc, a_per_head != 0, cfg.G, grid, block, lds, s, a);
+    default: return launch_mh_fused_t<float>(disc, a_per_head != 0, cfg.G, grid, block, lds, s, a);
+  }
+}
+
+extern "C" int tssm_mh_fwd_local(int dtype, const void* u, const float* A_log, const void* B,
+                                 const float* dt, float* loc_a, float* loc_x, float* carry,
+                                 int64_t nbatch, int64_t L, int64_t H, int64_t n_heads,
+                                 int64_t head_dim, int64_t su_b, int64_t su_l, int64_t sal_h,
+                                 int64_t sB_b, int64_t sB_l, int64_t sB_h, int64_t sdt_b,
+                                 int64_t sdt_l, int64_t sdt_h, int64_t blk_l, int64_t nblk,
+                                 int64_t grid_rows, int64_t grid_blks, void* stream) {
+  TSSM_CHECK(u && A_log && B && dt && loc_a && loc_x && carry, TSSM_ERR_NULL);
+  TSSM_CHECK(nbatch > 0 && L > 0 && H > 0 && n_heads > 0 && head_dim > 0 && blk_l > 0 &&
+                 nblk > 0 && grid_rows >= 0 && grid_blks >= 0,
+             TSSM_ERR_SHAPE);
+  TSSM_CHECK(grid_rows <= nbatch * n_heads && grid_blks <= nblk, TSSM_ERR_SHAPE);
+  if (grid_rows == 0 || grid_blks == 0) return TSSM_OK;
+  TSSM_CHECK(grid_rows <= 65535, TSSM_ERR_UNSUPPORTED);
+  const dim3 grid((unsigned)grid_blks, (unsigned)grid_rows);
+  const dim3 block(head_dim >= 256 ? 256 : (unsigned)(cdiv(head_dim, 64) * 64));
+  const hipStream_t s = as_stream(stream);
+#define TSSM_MH_LOCAL(T)                                                                        \
+  hipLaunchKernelGGL(mh_fwd_local_kernel<T>, grid, block, 0, s, (const T*)u, A_log,          \
+                     (const T*)B, dt, loc_a, loc_x, carry, nbatch, L, H, n_heads, head_dim,   \
+                     su_b, su_l, sal_h, sB_b, sB_l, sB_h, sdt_b, sdt_l, sdt_h, blk_l, nblk)
+  switch (dtype) {
+    case TSSM_F32: TSSM_MH_LOCAL(float); break;
+    case TSSM_BF16: TSSM_MH_LOCAL(bf16_t); break;
+    case TSSM_F16: TSSM_MH_LOCAL(f16_t); break;
+    default: return TSSM_ERR_DTYPE;
+  }
+#undef TSSM_MH_LOCAL
+  return launch_status();
+}
+
+extern "C" int tssm_mh_output(int dtype, const float* loc_a, const float* loc_x,
+                              const float* carry, const void* C, const float* D, const void* u,
+                              void* y, int64_t nbatch, int64_t L, int64_t H, int64_t n_heads,
+                              int64_t head_dim, int64_t su_b, int64_t su_l, int64_t sC_b,
+                              int64_t sC_l, int64_t sC_h, int64_t blk_l, int64_t nblk,
+                              int64_t grid_rows, int64_t grid_blks, void* stream) {
+  TSSM_CHECK(loc_a && loc_x && carry && C && D && u && y, TSSM_ERR_NULL);
+  TSSM_CHECK(nbatch > 0 && L > 0 && H > 0 && n_heads > 0 && head_dim > 0 && blk_l > 0 &&
+                 nblk > 0 && grid_rows >= 0 && grid_blks >= 0,
+             TSSM_ERR_SHAPE);
+  TSSM_CHECK(grid_rows <= nbatch * n_heads && grid_blks <= nblk, TSSM_ERR_SHAPE);
+  TSSM_CHECK(head_dim <= 1024, TSSM_ERR_UNSUPPORTED);
+  if (grid_rows == 0 || grid_blks == 0) return TSSM_OK;
+  TSSM_CHECK(grid_rows <= 65535, TSSM_ERR_UNSUPPORTED);
+  const dim3 grid((unsigned)grid_blks, (unsigned)grid_rows);
+  const dim3 block((unsigned)(cdiv(head_dim, 64) * 64));
+  const hipStream_t s = as_stream(stream);
+#define TSSM_MH_OUT(T)                                                                         \
+  hipLaunchKernelGGL(mh_output_kernel<T>, grid, block, 0, s, loc_a, loc_x, carry, (const T*)C, \
+                     D, (const T*)u, (T*)y, nbatch, L, H, n_heads, head_dim, su_b, su_l, sC_b, \
+                     sC_l, sC_h, blk_l, nblk)
+  switch (dtype) {
+    case TSSM_F32: TSSM_MH_OUT(float); break;
+    case TSSM_BF16: TSSM_MH_OUT(bf16_t); break;
+    case TSSM_F16: TSSM_MH_OUT(f16_t); break;
+    default: return TSSM_ERR_DTYPE;
+  }
+#undef TSSM_MH_OUT
+  return launch_status();
+}

@@ -1,0 +1,159 @@
+// Streaming single-step updates (streaming_inference_kernel.py).
+//
+// stream_step_kernel: streaming_ssm_inplace_kernel[_bf16] (:7-71) --
+//   h <- Abar*h + Bbar*vhat in place, y = C*h_new + D*vhat, y written with
+//   vhat's batch stride (:37).  The state dtype is the kernel's dtype (the
+//   bf16 variant rounds the state to bf16 on every step, as the reference).
+// stream_interp_step_kernel: streaming_interp_then_ssm_kernel (:75-156) with
+//   one workgroup per stream, so the ring head is read once by every feature
+//   tile and advanced after all of them (the reference reads it in every
+//   tile program but advances it from tile 0 only, :106,115-117).
+#include "common.h"
+
+namespace tssm {
+
+template <typename T>
+__global__ void stream_step_kernel(const T* __restrict__ vhat, T* __restrict__ h,
+                                   const T* __restrict__ Abar, const T* __restrict__ Bbar,
+                                   const T* __restrict__ C, const T* __restrict__ D,
+                                   T* __restrict__ y, int64_t hc, int64_t total, int64_t svb,
+                                   int64_t shb, int64_t scb) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t b = i / hc;
+  const int64_t k = i - b * hc;
+  const float v = ldf(vhat + b * svb + k);
+  const float hn = ldf(Abar + k) * ldf(h + b * shb + k) + ldf(Bbar + k) * v;
+  stf(h + b * shb + k, hn);
+  stf(y + b * svb + k, ldf(C + b * scb + k) * hn + ldf(D + k) * v);
+}
+
+constexpr int kStreamThreads = 256;
+
+struct RingArgs {
+  float* ring_V;
+  float* ring_M;
+  float* ring_tau;
+  int32_t* ring_head;
+  const float* v_new;
+  const float* m_new;
+  const float* tau_new;
+  float* h;
+  const float* Abar;
+  const float* Bbar;
+  const float* C;
+  const float* D;
+  float* y;
+  int64_t H, srb, srk, svb, shb, scb, BLOCK_H, KRING;
+};
+
+__device__ inline float block_reduce_sum(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.0f;
+  for (int i = 0; i < kStreamThreads / 64; ++i) s += red[i];
+  return s;
+}
+
+__global__ __launch_bounds__(kStreamThreads) void stream_interp_step_kernel(RingArgs a) {
+  __shared__ float red[kStreamThreads / 64];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t KR = a.KRING;
+  const int64_t head = a.ring_head[b];
+  const int64_t nh = (head + 1) % KR;                                    // :107
+  float* rV = a.ring_V + b * a.srb;
+  float* rM = a.ring_M + b * a.srb;
+  // insert the new observation (:113-114); m_new uses v's batch stride (:110)
+  for (int64_t k = tid; k < a.H; k += kStreamThreads) {
+    rV[nh * a.srk + k] = a.v_new[b * a.svb + k];
+    rM[nh * a.srk + k] = a.m_new[b * a.svb + k];
+  }
+  __syncthreads();
+  const int64_t ntile = (a.H + a.BLOCK_H - 1) / a.BLOCK_H;
+  for (int64_t tile = 0; tile < ntile; ++tile) {
+    const int64_t f0 = tile * a.BLOCK_H;
+    const int64_t f1 = f0 + a.BLOCK_H < a.H ? f0 + a.BLOCK_H : a.H;
+    // backward search over the previous KRING-1 slots (:124-130): nearest slot
+    // whose tile has any observation
+    int64_t prev_k = -1;
+    for (int64_t k = 1; k < KR; ++k) {
+      const int64_t rk = (nh - k + KR) % KR;
+      float s = 0.0f;
+      for (int64_t f = f0 + tid; f < f1; f += kStreamThreads) s += rM[rk * a.srk + f];
+      s = block_reduce_sum(s, red);
+      if (s > 0.5f) {
+        prev_k = rk;
+        break;
+      }
+    }
+    float sm = 0.0f;
+    for (int64_t f = f0 + tid; f < f1; f += kStreamThreads) sm += a.m_new[b * a.svb + f];
+    sm = block_reduce_sum(sm, red);
+    const bool fill = prev_k >= 0 && sm < 0.5f;                          // :133,143
+    for (int64_t f = f0 + tid; f < f1; f += kStreamThreads) {
+      const float v = fill ? rV[prev_k * a.srk + f] : a.v_new[b * a.svb + f];
+      const float hn = a.Abar[f] * a.h[b * a.shb + f] + a.Bbar[f] * v;  // :152
+      a.h[b * a.shb + f] = hn;
+      a.y[b * a.svb + f] = a.C[b * a.scb + f] * hn + a.D[f] * v;        // :153,156
+    }
+  }
+  if (tid == 0) {
+    a.ring_tau[b * KR + nh] = a.tau_new[b];                              // :116
+    a.ring_head[b] = (int32_t)nh;                                        // :117
+  }
+}
+
+}  // namespace tssm
+
+using namespace tssm;
+
+extern "C" int tssm_stream_step(int dtype, const void* vhat, void* h, const void* Abar,
+                                const void* Bbar, const void* C, const void* D, void* y,
+                                int64_t nbatch, int64_t H, int64_t grid_b, int64_t h_cover,
+                                int64_t svb, int64_t shb, int64_t scb, void* stream) {
+  TSSM_CHECK(vhat && h && Abar && Bbar && C && D && y, TSSM_ERR_NULL);
+  TSSM_CHECK(nbatch >= 0 && H >= 0 && grid_b >= 0 && h_cover >= 0 && grid_b <= nbatch &&
+                 h_cover <= H,
+             TSSM_ERR_SHAPE);
+  const int64_t total = grid_b * h_cover;
+  if (total == 0) return TSSM_OK;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  const hipStream_t s = as_stream(stream);
+#define TSSM_S(T)                                                                              \
+  hipLaunchKernelGGL(stream_step_kernel<T>, grid, dim3(256), 0, s, (const T*)vhat, (T*)h,      \
+                     (const T*)Abar, (const T*)Bbar, (const T*)C, (const T*)D, (T*)y, h_cover, \
+                     total, svb, shb, scb)
+  switch (dtype) {
+    case TSSM_F32: TSSM_S(float); break;
+    case TSSM_BF16: TSSM_S(bf16_t); break;
+    case TSSM_F16: TSSM_S(f16_t); break;
+    default: return TSSM_ERR_DTYPE;
+  }
+#undef TSSM_S
+  return launch_status();
+}
+
+extern "C" int tssm_stream_interp_step(float* ring_V, float* ring_M, float* ring_tau,
+                                       int32_t* ring_head, const float* v_new,
+                                       const float* m_new, const float* tau_new, float* h,
+                                       const float* Abar, const float* Bbar, const float* C,
+                                       const float* D, float* y, int64_t nbatch, int64_t H,
+                                       int64_t srb, int64_t srk, int64_t svb, int64_t shb,
+                                       int64_t scb, int64_t BLOCK_H, int64_t KRING,
+                                       int64_t grid_b, void* stream) {
+  TSSM_CHECK(ring_V && ring_M && ring_tau && ring_head && v_new && m_new && tau_new && h &&
+                 Abar && Bbar && C && D && y,
+             TSSM_ERR_NULL);
+  TSSM_CHECK(nbatch >= 0 && H >= 0 && BLOCK_H > 0 && KRING > 0 && grid_b >= 0 &&
+                 grid_b <= nbatch,
+             TSSM_ERR_SHAPE);
+  if (grid_b == 0 || H == 0) return TSSM_OK;
+  RingArgs a{ring_V, ring_M, ring_tau, ring_head, v_new, m_new, tau_new, h, Abar, Bbar, C, D, y,
+             H, srb, srk, svb, shb, scb, BLOCK_H, KRING};
+  hipLaunchKernelGGL(stream_interp_step_kernel, dim3((unsigned)grid_b), dim3(kStreamThreads), 0,
+                     as_stream(stream), a);
+  return launch_status();
+}

@@ -1,0 +1,14 @@
+"""tssm -- MI355X (gfx950) selective-SSM kernels behind a C ABI.
+
+The reference-named modules next to this package (``discretize_kernel``,
+``ssm_scan``, ``multihead_ssm_kernel``, ``fused_interp_kernel``,
+``fused_ssm_interp``, ``streaming_inference_kernel``) are the drop-in surface;
+this package holds the shared host code: the ctypes binding (``_lib``), the
+Triton-convention launchers (``launch``), look-back workspaces
+(``workspace``), the fused entry points (``fused``) and the seeded synthetic
+workloads (``workloads``).
+"""
+from . import _lib, launch, workspace  # noqa: F401
+from .fused import multihead_ssm_forward  # noqa: F401
+
+__all__ = ["multihead_ssm_forward"]
