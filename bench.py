@@ -70,8 +70,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--disc", choices=["zoh", "euler"], default="zoh")
-    ap.add_argument("--a-per-head", action="store_true",
-                    help="pass A_log as [H] (one decay per head) instead of [H, P]")
+    ap.add_argument("--a-per-channel", action="store_true",
+                    help="pass A_log as [H, P] (the reference kernel's layout, the per-head "
+                         "value repeated) instead of [H] (one decay per head)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run torch copies of a 256 MiB buffer (scales rocprof "
+                         "FETCH_SIZE/WRITE_SIZE to bytes); prints nothing else")
     ap.add_argument("--sets", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -87,9 +91,17 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        src = torch.ones(64 * 2**20, dtype=torch.float32, device=dev)   # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copied 256 MiB x5")
+        return
     log("generating inputs ...")
     w = workloads.multihead(**SHAPE)
-    a_key = "A_log_h" if args.a_per_head else "A_log"
+    a_key = "A_log" if args.a_per_channel else "A_log_h"
     base = {k: w[k].to(dev) for k in ("u", "B", "C", "dt")}
     A_log = w[a_key].to(dev)
     sets = []
@@ -156,7 +168,7 @@ def main():
                         f"bf16 x/B/C/y, fp32 dt/state, {args.disc.upper()} discretization",
             "B": B, "L": L, "H": H, "P": P, "N": P, "chunk": CHUNK, "disc": args.disc,
             "io_dtype": "bf16", "state_dtype": "f32",
-            "a_log": "per head [H]" if args.a_per_head else "per channel [H, P]",
+            "a_log": "per channel [H, P]" if args.a_per_channel else "per head [H]",
             "parallelism": "single GPU",
         },
         "roofline": {

@@ -1,6 +1,20 @@
 // Library-level entry points: version, status text, workspace error word.
+#include <mutex>
+#include <unordered_map>
+
 #include "common.h"
 #include "lookback.h"
+
+namespace tssm {
+uint32_t next_epoch(const void* workspace) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, uint32_t> epochs;
+  std::lock_guard<std::mutex> lock(mu);
+  uint32_t& e = epochs[workspace];
+  if (++e == 0) e = 1;
+  return e;
+}
+}  // namespace tssm
 
 extern "C" int tssm_abi_version(void) { return 1; }
 

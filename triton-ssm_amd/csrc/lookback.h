@@ -1,5 +1,5 @@
-// Single-pass chunked scan support: dynamic tile tickets and a decoupled
-// look-back over per-channel carries.
+// Single-pass chunked scan support: decoupled look-back over per-channel
+// carries between the chunks (tiles) of one sequence row.
 //
 // Every carry value is published as one 64-bit word {float bits, tag}, stored
 // and loaded with relaxed device-scope atomics (global_store/load_dwordx2
@@ -7,14 +7,19 @@
 // sees the current tag also sees the value: no release/acquire fences (and so
 // no L2 write-back or invalidate) are needed between the per-XCD L2 caches.
 //
-// Workspace layout (caller-owned, zero-filled once when allocated):
-//   WsHeader (256 B) | uint64 words ...
-// The header holds the ticket counter, the retire counter, the launch epoch
-// and a sticky error word.  The last workgroup of a launch to retire resets
-// both counters and advances the epoch, so no per-launch clearing is needed
-// and stale words from earlier launches never match the current tag.
-// One workspace serves one stream at a time: launches that overlap on the
-// same workspace race.
+// Tiles are numbered by blockIdx so that a tile only waits on tiles with a
+// smaller index (earlier chunks of its row).  No device-scope atomics are used:
+// one shared counter serialises at ~27 ns per operation, which at thousands
+// of tiles costs more than the scan itself.  Progress relies on each XCD
+// starting its workgroups in increasing index order; every wait is bounded
+// regardless (a timeout sets the sticky error word and the kernel finishes).
+//
+// Workspace layout (caller-owned, zero-filled ONCE when allocated):
+//   WsHeader (256 B: sticky error word) | uint64 carry words ...
+// The tag of a launch is an epoch that the library advances on every launch
+// that uses the workspace (``next_epoch``), so stale words never match and no
+// per-launch clearing is needed.  One workspace serves one stream at a time:
+// launches that overlap on the same workspace race.
 #pragma once
 
 #include "common.h"
@@ -22,19 +27,17 @@
 namespace tssm {
 
 struct WsHeader {
-  uint32_t ticket;
-  uint32_t done;
-  uint32_t epoch;
   uint32_t error;   // sticky: set to 1 when a bounded look-back wait expired
-  uint32_t pad[60];
+  uint32_t pad[63];
 };
 static_assert(sizeof(WsHeader) == 256, "header is 256 bytes");
 
 constexpr uint32_t kDefaultSpinLimit = 1u << 20;  // ~1 s of polling
 
-__device__ inline uint32_t ld_relaxed_u32(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Host: the tag of the next launch on ``workspace`` (never 0; a zero-filled
+// word is "not ready").  Thread-safe; defined in abi.hip.
+uint32_t next_epoch(const void* workspace);
+
 __device__ inline uint64_t ld_word(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -44,24 +47,6 @@ __device__ inline void st_word(uint64_t* p, float v, uint32_t tag) {
 }
 __device__ inline uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 32); }
 __device__ inline float word_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
-
-// Thread 0 of a workgroup: take the next tile ticket and read the epoch.
-__device__ inline void take_ticket(WsHeader* hdr, uint32_t* ticket, uint32_t* tag) {
-  *ticket = __hip_atomic_fetch_add(&hdr->ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  *tag = ld_relaxed_u32(&hdr->epoch) + 1u;   // never 0: a zeroed word is "not ready"
-}
-
-// Thread 0 of a workgroup, after its last use of the ticket/epoch.  The last
-// of ``total`` workgroups resets the counters and advances the epoch.
-__device__ inline void retire(WsHeader* hdr, uint32_t total) {
-  uint32_t d = __hip_atomic_fetch_add(&hdr->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (d == total - 1) {
-    uint32_t e = ld_relaxed_u32(&hdr->epoch);
-    __hip_atomic_store(&hdr->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&hdr->epoch, e + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
 
 __device__ inline void flag_error(WsHeader* hdr) {
   __hip_atomic_store(&hdr->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -80,32 +65,48 @@ struct CarrySlot {
 };
 
 // Resolve the state entering chunk ``c`` for one channel by walking back over
-// predecessors: an inclusive word ends the walk, an aggregate pair is folded
-// in and the walk continues, a missing word is re-polled (bounded).
-// ``h0`` is the state before chunk 0.
+// predecessors, WIN of them per round trip: the words of chunks j, j-1, ...,
+// j-WIN+1 are loaded together, then folded newest first -- an inclusive word
+// ends the walk, an aggregate pair is folded in, a missing word stops the
+// batch and is re-polled (bounded).  ``h0`` is the state before chunk 0.
+template <int WIN>
 __device__ inline float lookback_channel(const CarrySlot& s, int64_t c, int ch, uint32_t tag,
                                          float h0, uint32_t spin_limit, WsHeader* hdr) {
   float A_acc = 1.0f, X_acc = 0.0f;
   int64_t j = c - 1;
   uint32_t spins = 0;
   while (j >= 0) {
-    uint64_t wi = ld_word(s.inc(j, ch));
-    uint64_t wa = ld_word(s.agg_a(j, ch));
-    uint64_t wx = ld_word(s.agg_x(j, ch));
-    if (word_tag(wi) == tag) {
-      return __builtin_fmaf(A_acc, word_val(wi), X_acc);
+    uint64_t wi[WIN], wa[WIN], wx[WIN];
+#pragma unroll
+    for (int k = 0; k < WIN; ++k) {
+      if (j - k >= 0) {
+        wi[k] = ld_word(s.inc(j - k, ch));
+        wa[k] = ld_word(s.agg_a(j - k, ch));
+        wx[k] = ld_word(s.agg_x(j - k, ch));
+      } else {
+        wi[k] = wa[k] = wx[k] = 0;
+      }
     }
-    if (word_tag(wa) == tag && word_tag(wx) == tag) {
-      X_acc = __builtin_fmaf(A_acc, word_val(wx), X_acc);
-      A_acc = A_acc * word_val(wa);
-      --j;
-      continue;
+    bool stalled = false;
+#pragma unroll
+    for (int k = 0; k < WIN; ++k) {
+      if (stalled || j < 0) continue;
+      if (word_tag(wi[k]) == tag) return __builtin_fmaf(A_acc, word_val(wi[k]), X_acc);
+      if (word_tag(wa[k]) == tag && word_tag(wx[k]) == tag) {
+        X_acc = __builtin_fmaf(A_acc, word_val(wx[k]), X_acc);
+        A_acc = A_acc * word_val(wa[k]);
+        --j;
+      } else {
+        stalled = true;
+      }
     }
-    if (++spins > spin_limit) {   // predecessor never published: give up loudly
-      flag_error(hdr);
-      return X_acc;
+    if (stalled) {
+      if (++spins > spin_limit) {   // predecessor never published: give up loudly
+        flag_error(hdr);
+        return X_acc;
+      }
+      __builtin_amdgcn_s_sleep(1);
     }
-    __builtin_amdgcn_s_sleep(1);
   }
   return __builtin_fmaf(A_acc, h0, X_acc);
 }
