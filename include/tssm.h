@@ -172,6 +172,62 @@ int tssm_stream_interp_step(float* ring_V, float* ring_M, float* ring_tau, int32
                             int64_t srk, int64_t svb, int64_t shb, int64_t scb, int64_t BLOCK_H,
                             int64_t KRING, int64_t grid_b, void* stream);
 
+/* ------------------------------------------------------------------ SSD (new fused entry points)
+ * Selective scan with one decay per head and a P x N state per (batch, head):
+ *   h_t[p,n] = exp(dt_t a_h) h_{t-1}[p,n] + Bbar_t x_t[p] B_t[n],
+ *   y_t[p] = sum_n C_t[n] h_t[p,n] + D[h,p] x_t[p]
+ * (the recurrence of ssm_scan.py:5-10 with discretize_kernel.py:44-54's ZOH
+ * or multihead_ssm_kernel.py:73's Euler input term).  No reference kernel
+ * covers this family; the reference's elementwise kernels can express it only
+ * lane by lane.  Single pass with decoupled look-back; workspace rules as for
+ * tssm_mh_scan_fused.  x, B, C, y in `dtype` ([B,L,H,P] / [B,L,H,N]); dt f32
+ * [B,L,H]; A_log f32 [H]; D f32 [H*P] or NULL; h0/h_last f32 [B,H,P,N] or
+ * NULL.  P <= 64, N in {8, 16, 32}; innermost strides 1. */
+int64_t tssm_ssd_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t H, int64_t P,
+                                      int64_t N, int64_t chunk);
+int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt, const float* A_log,
+                  const void* B, const void* C, const float* D, const float* h0, void* y,
+                  float* h_last, int64_t nbatch, int64_t L, int64_t H, int64_t P, int64_t N,
+                  int64_t sx_b, int64_t sx_l, int64_t sx_h, int64_t sdt_b, int64_t sdt_l,
+                  int64_t sdt_h, int64_t sB_b, int64_t sB_l, int64_t sB_h, int64_t sC_b,
+                  int64_t sC_l, int64_t sC_h, int64_t sy_b, int64_t sy_l, int64_t sy_h,
+                  int64_t chunk, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* One streaming SSD step for S independent streams with the state
+ * [S,H,P,N] f32 resident in HBM and updated in place (the per-stream,
+ * per-head generalisation of streaming_ssm_inplace_kernel,
+ * streaming_inference_kernel.py:7-37).  x [S,H,P], B/C [S,H,N] (16-byte
+ * aligned rows), y [S,H,P], dt [S,H] via strides (sdt_h = 0 for one dt per
+ * stream), A_log [H], D [H*P] or NULL; all f32.  N in {16,...,256} (powers of 2). */
+int tssm_ssd_stream_step(int disc, const float* x, const float* dt, const float* A_log,
+                         const float* B, const float* C, const float* D, float* state, float* y,
+                         int64_t S, int64_t H, int64_t P, int64_t N, int64_t sdt_s,
+                         int64_t sdt_h, int64_t sx_s, int64_t sx_h, int64_t sB_s, int64_t sB_h,
+                         int64_t sC_s, int64_t sC_h, int64_t sy_s, int64_t sy_h, void* stream);
+
+/* ------------------------------------------------------------------ Mamba-1 selective scan
+ * Lanes (channel d, state n) of a diagonal selective SSM:
+ *   h_t[d,n] = exp(dt_t a[d,n]) h_{t-1}[d,n] + Bbar_t[d,n] B_t[n] x_t[d],
+ *   y_t[d] = sum_n C_t[n] h_t[d,n] + D[d] x_t[d]
+ * -- what the reference computes with zoh_discretize_diag_kernel over lanes
+ * (d,n) followed by ssm_forward and a sum over n (discretize_kernel.py:16-57,
+ * ssm_scan.py:239-264), fused into one single-pass launch (same kernel as
+ * tssm_mh_scan_fused with the channel input broadcast over the states).
+ * x, B, C, y in `dtype` ([B,L,Dc] / [B,L,N]); A_log f32 [Dc,N]; dt f32 with
+ * strides (b, l, d) -- sdt_d = 0 for one dt per (b,t); with dt_is_tau=1 dt
+ * holds timestamps tau and dt_t = tau_t - tau_{t-1}, dt_0 = tau_0.
+ * D f32 [Dc] or NULL; h0/h_last f32 [B,Dc,N] or NULL.  N a multiple of 8,
+ * <= 128; B/C rows 16-byte aligned. */
+int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc, int64_t N,
+                                            int64_t chunk);
+int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt, int dt_is_tau,
+                        const float* A_log, const void* B, const void* C, const float* D,
+                        const float* h0, void* y, float* h_last, int64_t nbatch, int64_t L,
+                        int64_t Dc, int64_t N, int64_t sx_b, int64_t sx_l, int64_t sdt_b,
+                        int64_t sdt_l, int64_t sdt_d, int64_t sB_b, int64_t sB_l, int64_t sC_b,
+                        int64_t sC_l, int64_t sy_b, int64_t sy_l, int64_t chunk, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

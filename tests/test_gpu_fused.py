@@ -1,0 +1,180 @@
+"""GPU parity of the new fused entry points (SSD scan, streaming SSD step,
+Mamba-1 selective scan, interpolation + scan) against the float64 oracle."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import TOL, assert_close, np64
+from oracle import ssm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _ssd_inputs(dev, Bsz, L, H, P, N, dtype, seed, heavy=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(Bsz, L, H, P, generator=g).to(dtype)
+    Bm = (torch.randn(Bsz, L, H, N, generator=g) / N ** 0.5).to(dtype)
+    Cm = (torch.randn(Bsz, L, H, N, generator=g) / N ** 0.5).to(dtype)
+    if heavy:
+        dt = torch.exp(torch.randn(Bsz, L, H, generator=g) * 1.5 - 3.0)
+    else:
+        dt = torch.nn.functional.softplus(torch.randn(Bsz, L, H, generator=g)) * 0.3
+    A_log = torch.rand(H, generator=g) * np.log(16.0)
+    D = torch.randn(H, P, generator=g)
+    return {k: v.to(dev) for k, v in dict(x=x, B=Bm, C=Cm, dt=dt, A_log=A_log, D=D).items()}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("disc", ["zoh", "euler"])
+@pytest.mark.parametrize("P,N", [(64, 16), (32, 8), (48, 32)])
+def test_ssd_scan(dev, dtype, disc, P, N):
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, 2, 1100, 3, P, N, dtype, seed=P + N, heavy=True)
+    h0 = torch.randn(2, 3, P, N, device=dev)
+    y, hl = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], disc=disc,
+                             h0=h0, chunk=256, return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssd_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], h0=np64(h0), disc=disc)
+    assert_close(y, y_ref, TOL[dtype], f"ssd y {dtype} {disc} P={P} N={N}")
+    assert_close(hl, h_ref, TOL[dtype], "ssd h_last")
+
+
+@pytest.mark.parametrize("chunk", [64, 256, 1024])
+def test_ssd_scan_chunks_and_split(dev, chunk):
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, 1, 3000, 2, 64, 16, torch.float32, seed=chunk)
+    y, h = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], None, chunk=chunk,
+                            return_state=True)
+    y_ref, h_ref = O.ssd_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"], None)
+    torch.cuda.synchronize()
+    assert_close(y, y_ref, 1e-5, f"chunk {chunk}")
+    cut = 1234
+    y1, h1 = ssd_scan_forward(d["x"][:, :cut], d["dt"][:, :cut], d["A_log"], d["B"][:, :cut],
+                              d["C"][:, :cut], None, chunk=chunk, return_state=True)
+    y2 = ssd_scan_forward(d["x"][:, cut:], d["dt"][:, cut:], d["A_log"], d["B"][:, cut:],
+                          d["C"][:, cut:], None, chunk=chunk, h0=h1)
+    torch.cuda.synchronize()
+    assert_close(torch.cat([y1, y2], 1), y_ref, 1e-5, "split/resume")
+
+
+def test_ssd_long_sequence_shape(dev):
+    """B=1 L=262144 H=8 P=64 N=16 bf16, log-normal dt (the long-sequence
+    workload).  Causality: the first 24576 outputs equal the oracle run on
+    that prefix; split/resume of the full run at L/2 reproduces the tail."""
+    from tssm import ssd_scan_forward, workloads, workspace
+    w = workloads.ssd_long()
+    d = {k: w[k].to(dev) for k in ("x", "dt", "A_log", "B", "C")}
+    y, h = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], None, chunk=256,
+                            return_state=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    Lp = 24576
+    y_ref, _ = O.ssd_scan(d["x"][:, :Lp], d["dt"][:, :Lp], d["A_log"], d["B"][:, :Lp], d["C"][:, :Lp])
+    assert_close(y[:, :Lp], y_ref, 1e-2, "prefix")
+    cut = 131072
+    _, h1 = ssd_scan_forward(d["x"][:, :cut], d["dt"][:, :cut], d["A_log"], d["B"][:, :cut],
+                             d["C"][:, :cut], None, chunk=256, return_state=True)
+    y2, h2 = ssd_scan_forward(d["x"][:, cut:], d["dt"][:, cut:], d["A_log"], d["B"][:, cut:],
+                              d["C"][:, cut:], None, chunk=256, h0=h1, return_state=True)
+    torch.cuda.synchronize()
+    assert_close(y2, y[:, cut:], 1e-2, "tail via h0")
+    assert_close(h2, h, 1e-3, "final state via h0")
+    ws = workspace.get(dev, torch.cuda.current_stream(dev).cuda_stream, 0)
+    assert workspace.error_flag(ws) == 0
+
+
+@pytest.mark.parametrize("N", [16, 128])
+@pytest.mark.parametrize("per_stream_dt", [True, False])
+def test_ssd_stream_step(dev, N, per_stream_dt):
+    from tssm import ssd_stream_step
+    g = torch.Generator().manual_seed(N)
+    S, H, P = 37, 4, 64
+    A_log = (torch.rand(H, generator=g) * np.log(16.0)).to(dev)
+    D = torch.randn(H, P, generator=g).to(dev)
+    state = torch.zeros(S, H, P, N, device=dev)
+    st_ref = np.zeros((S, H, P, N))
+    for step in range(12):
+        x = torch.randn(S, H, P, generator=g).to(dev)
+        dt = (torch.empty(S if per_stream_dt else (S, H)).exponential_(10.0, generator=g)).to(dev)
+        Bm = (torch.randn(S, H, N, generator=g) / N ** 0.5).to(dev)
+        Cm = (torch.randn(S, H, N, generator=g) / N ** 0.5).to(dev)
+        y = ssd_stream_step(x, dt, A_log, Bm, Cm, D, state)
+        y_ref = O.ssd_stream_step(x, dt, A_log, Bm, Cm, D, st_ref)
+        torch.cuda.synchronize()
+        assert_close(y, y_ref, 1e-5, f"stream y step {step}")
+    assert_close(state, st_ref, 1e-5, "stream state")
+
+
+def _mamba1_inputs(dev, Bsz, L, Dc, N, dtype, seed, dt_per_channel=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(Bsz, L, Dc, generator=g).to(dtype)
+    shape = (Bsz, L, Dc) if dt_per_channel else (Bsz, L)
+    dt = torch.empty(shape).exponential_(20.0, generator=g).clamp_(1e-3, 1.0)
+    A_log = torch.empty(Dc, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = (torch.randn(Bsz, L, N, generator=g) / N ** 0.5).to(dtype)
+    Cm = (torch.randn(Bsz, L, N, generator=g) / N ** 0.5).to(dtype)
+    D = torch.randn(Dc, generator=g)
+    return {k: v.to(dev) for k, v in dict(x=x, dt=dt, A_log=A_log, B=Bm, C=Cm, D=D).items()}
+
+
+def test_selective_scan_small_config(dev):
+    """B=2 L=256 D=16 N=16 fp32, dt ~ Exp(mean .05) clamped (the small fp32 workload)."""
+    from tssm import selective_scan_forward, workloads
+    w = workloads.mamba1_small()
+    d = {k: w[k].to(dev) for k in w}
+    y, h = selective_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], None,
+                                  return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.selective_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"])
+    assert_close(y, y_ref, 1e-5, "mamba1 y")
+    assert_close(h, h_ref, 1e-5, "mamba1 h")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N", [8, 16, 64])
+@pytest.mark.parametrize("dt_per_channel", [False, True])
+def test_selective_scan(dev, dtype, N, dt_per_channel):
+    from tssm import selective_scan_forward
+    d = _mamba1_inputs(dev, 3, 700, 40, N, dtype, seed=N, dt_per_channel=dt_per_channel)
+    h0 = torch.randn(3, 40, N, device=dev)
+    y, h = selective_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], h0=h0,
+                                  return_state=True, chunk=128)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.selective_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], h0=np64(h0))
+    assert_close(y, y_ref, TOL[dtype], f"mamba1 {dtype} N={N}")
+    assert_close(h, h_ref, TOL[dtype], "mamba1 h_last")
+
+
+@pytest.mark.parametrize("FTILE", [16, 128])
+def test_fused_interp_ssm_small(dev, FTILE):
+    from tssm import fused_interp_ssm_forward
+    g = torch.Generator().manual_seed(FTILE)
+    Bsz, T, F, N = 3, 300, 64, 16
+    tau = torch.sort(torch.rand(Bsz, T, generator=g) * 30, dim=1).values
+    M = (torch.rand(Bsz, T, F, generator=g) < 0.3).float()
+    V = torch.randn(Bsz, T, F, generator=g) * M
+    A_log = torch.empty(F, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = torch.randn(Bsz, T, N, generator=g) / 4
+    Cm = torch.randn(Bsz, T, N, generator=g) / 4
+    d = {k: v.to(dev) for k, v in dict(V=V, M=M, tau=tau, A_log=A_log, B=Bm, C=Cm).items()}
+    vhat, y, h = fused_interp_ssm_forward(d["V"], d["M"], d["tau"], d["A_log"], d["B"], d["C"],
+                                          K=10, FTILE=FTILE, return_state=True)
+    torch.cuda.synchronize()
+    v_ref, y_ref, h_ref = O.fused_interp_ssm(d["V"], d["M"], d["tau"], d["A_log"], d["B"],
+                                             d["C"], K=10, FTILE=FTILE)
+    assert_close(vhat, v_ref, 1e-6, "Vhat")
+    assert_close(y, y_ref, 1e-5, "y")
+    assert_close(h, h_ref, 1e-5, "h_last")
+
+
+def test_fused_interp_ssm_full_shape(dev):
+    """B=16 T=2048 F=D=256 N=16 fp32, 30% missing, K=10 FTILE=128."""
+    from tssm import fused_interp_ssm_forward, workloads
+    w = workloads.interp_mamba1()
+    d = {k: w[k].to(dev) for k in w}
+    vhat, y = fused_interp_ssm_forward(d["V"], d["M"], d["tau"], d["A_log"], d["B"], d["C"])
+    torch.cuda.synchronize()
+    v_ref, y_ref, _ = O.fused_interp_ssm(d["V"], d["M"], d["tau"], d["A_log"], d["B"], d["C"])
+    assert_close(vhat, v_ref, 1e-6, "Vhat")
+    e = assert_close(y, y_ref, 1e-5, "y")
+    print(f"interp+ssm full shape relerr {e:.2e}")

@@ -68,9 +68,15 @@ __device__ inline float ld_any(const void* p, int64_t i, int dt) {
 
 // 8 consecutive channels as one vector load: 16 B for bf16/fp16, 32 B for fp32.
 template <typename T> struct Vec8;
+// load_nt: non-temporal (streamed once, not kept in the caches).
+__device__ inline uint4 ld_nt16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 template <> struct Vec8<bf16_t> {
   uint4 raw;
   __device__ inline void load(const bf16_t* p) { raw = *reinterpret_cast<const uint4*>(p); }
+  __device__ inline void load_nt(const bf16_t* p) { raw = ld_nt16(p); }
   __device__ inline void zero() { raw = make_uint4(0, 0, 0, 0); }
   __device__ inline float get(int j) const {
     uint32_t w = (&raw.x)[j >> 1];
@@ -80,6 +86,7 @@ template <> struct Vec8<bf16_t> {
 template <> struct Vec8<f16_t> {
   uint4 raw;
   __device__ inline void load(const f16_t* p) { raw = *reinterpret_cast<const uint4*>(p); }
+  __device__ inline void load_nt(const f16_t* p) { raw = ld_nt16(p); }
   __device__ inline void zero() { raw = make_uint4(0, 0, 0, 0); }
   __device__ inline float get(int j) const {
     uint32_t w = (&raw.x)[j >> 1];
@@ -92,6 +99,11 @@ template <> struct Vec8<float> {
   __device__ inline void load(const float* p) {
     lo = reinterpret_cast<const float4*>(p)[0];
     hi = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ inline void load_nt(const float* p) {
+    const uint4 a = ld_nt16(p), b = ld_nt16(p + 4);
+    lo = make_float4(__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z), __uint_as_float(a.w));
+    hi = make_float4(__uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), __uint_as_float(b.w));
   }
   __device__ inline void zero() { lo = make_float4(0, 0, 0, 0); hi = lo; }
   __device__ inline float get(int j) const { return j < 4 ? (&lo.x)[j] : (&hi.x)[j - 4]; }

@@ -4,7 +4,7 @@
 //   tile = (batch b, head h, chunk c) of TC time steps x P channels, numbered
 //   row-major (blockIdx = (b*n_heads + h) * nchunks + c): the chunks of one
 //   row are neighbours in launch order, which measured ~20% faster on MI355X
-//   HBM than chunk-major numbering; the look-back reads 4 predecessors per
+//   HBM than chunk-major numbering; the look-back reads 2 predecessors per
 //   round trip to keep the resulting longer walks short.
 //   Thread layout: a wave covers ROWS = 64/G "runs" of R consecutive steps;
 //   each thread owns 8 consecutive channels (one 16-byte bf16 vector) of one
@@ -61,12 +61,23 @@ struct MhArgs {
   uint32_t n_heads, nchunks, nrows;
   uint32_t tag;
   uint32_t spin_limit;
+  uint32_t chunk_major;  // tile order: 0 row-major, 1 chunk-major
+  uint32_t dt_is_tau;    // dt holds timestamps: dt_t = tau_t - tau_{t-1}, dt_0 = tau_0
 };
 
-constexpr int kMhR = 4;    // consecutive steps per thread
-constexpr int kMhWin = 4;  // predecessors read per look-back round trip
+// MODE_DIAG:   reference multihead layout -- u [B,L,nh*hd] per channel, y
+//              broadcast over the head's channels, D per channel.
+// MODE_MAMBA1: selective scan with lanes (channel d, state n): "head" = d,
+//              channels = states; x [B,L,Dc] broadcast over the states, B/C
+//              shared by all channels (head stride 0), y [B,L,Dc] one value per
+//              channel, D per channel (y += D[d] x[d]).
+constexpr int MODE_DIAG = 0;
+constexpr int MODE_MAMBA1 = 1;
 
-template <typename T, int DISC, bool APH, bool HAS_D, int G>
+constexpr int kMhR = 4;    // consecutive steps per thread
+constexpr int kMhWin = 2;  // predecessors read per look-back round trip (measured best)
+
+template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE>
 __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   constexpr int P = G * 8;
   constexpr int ROWS = 64 / G;
@@ -89,32 +100,43 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   const int run = wave * ROWS + lane / G;
   const int ch0 = g * 8;
 
-  // ---- tile = blockIdx, row-major: (row, chunk c) waits only on (row, c-1),
-  // the previous index
+  // ---- tile = blockIdx: row-major (row, chunk c) or chunk-major; either way
+  // (row, c) waits only on (row, c-1), a smaller index
   const uint32_t tag = a.tag;
-  const uint32_t row = blockIdx.x / a.nchunks;
-  const uint32_t c = blockIdx.x - row * a.nchunks;
+  uint32_t row, c;
+  if (a.chunk_major) {
+    c = blockIdx.x / a.nrows;
+    row = blockIdx.x - c * a.nrows;
+  } else {
+    row = blockIdx.x / a.nchunks;
+    c = blockIdx.x - row * a.nchunks;
+  }
   const uint32_t b = row / a.n_heads;
   const uint32_t h = row - b * a.n_heads;
   const int64_t t0 = (int64_t)c * TC + (int64_t)run * R;
 
   // ---- loads (all issued before any use)
   Vec8<T> vu[R], vB[R], vC[R];
+  float us[R];  // MODE_MAMBA1: the channel's input, shared by its 8 state lanes
   float dtv[R];
   {
-    const T* up = reinterpret_cast<const T*>(a.u) + b * a.su_b + h * P + ch0 + t0 * a.su_l;
+    const T* up = reinterpret_cast<const T*>(a.u) + b * a.su_b + t0 * a.su_l +
+                  (MODE == MODE_DIAG ? h * P + ch0 : h);
     const T* Bp = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h + ch0 + t0 * a.sB_l;
     const T* Cp = reinterpret_cast<const T*>(a.C) + b * a.sC_b + h * a.sC_h + ch0 + t0 * a.sC_l;
     const float* dp = a.dt + b * a.sdt_b + h * a.sdt_h + t0 * a.sdt_l;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (t0 + r < a.L) {
-        vu[r].load(up + r * a.su_l);
-        vB[r].load(Bp + r * a.sB_l);
-        vC[r].load(Cp + r * a.sC_l);
+        if constexpr (MODE == MODE_DIAG) vu[r].load_nt(up + r * a.su_l);
+        else us[r] = ldf(up + r * a.su_l);
+        vB[r].load_nt(Bp + r * a.sB_l);
+        vC[r].load_nt(Cp + r * a.sC_l);
         dtv[r] = dp[r * a.sdt_l];
+        if (a.dt_is_tau) dtv[r] -= (t0 + r > 0) ? dp[(r - 1) * a.sdt_l] : 0.0f;
       } else {
-        vu[r].zero();
+        if constexpr (MODE == MODE_DIAG) vu[r].zero();
+        else us[r] = 0.0f;
         vB[r].zero();
         vC[r].zero();
         dtv[r] = 0.0f;  // identity step: Abar = 1, input term 0
@@ -135,7 +157,9 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     for (int j = 0; j < 8; ++j) a2[j] = -expf(a2[j]) * kLog2e;
   }
   float Dv[8];
-  if constexpr (HAS_D) {
+  if constexpr (HAS_D && MODE == MODE_MAMBA1) {
+    Dv[0] = a.D[h];
+  } else if constexpr (HAS_D) {
     const float4* dp4 = reinterpret_cast<const float4*>(a.D + h * P + ch0);
     const float4 d0 = dp4[0], d1 = dp4[1];
     Dv[0] = d0.x; Dv[1] = d0.y; Dv[2] = d0.z; Dv[3] = d0.w;
@@ -173,14 +197,16 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
         coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * dtv[r]
                                        : dtv[r];
       }
-      const float uj = vu[r].get(j);
+      const float uj = (MODE == MODE_DIAG) ? vu[r].get(j) : us[r];
       xl[j] = __builtin_fmaf(ab, xl[j], coef * vB[r].get(j) * uj);
       al[j] = al[j] * ab;
       const float cj = vC[r].get(j);
       w[r][j] = cj * al[j];
       acc = __builtin_fmaf(cj, xl[j], acc);
-      if constexpr (HAS_D) acc = __builtin_fmaf(Dv[j], uj, acc);
+      if constexpr (HAS_D && MODE == MODE_DIAG) acc = __builtin_fmaf(Dv[j], uj, acc);
     }
+    // MODE_MAMBA1: D[d] x[d] once per channel (the group's first thread)
+    if constexpr (HAS_D && MODE == MODE_MAMBA1) acc = g == 0 ? __builtin_fmaf(Dv[0], us[r], acc) : acc;
     y1[r] = acc;
   }
   {
@@ -254,14 +280,18 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     S[4] = __builtin_fmaf(a1.x, c1.x, x1.x); S[5] = __builtin_fmaf(a1.y, c1.y, x1.y);
     S[6] = __builtin_fmaf(a1.z, c1.z, x1.z); S[7] = __builtin_fmaf(a1.w, c1.w, x1.w);
   }
-  T* yp = reinterpret_cast<T*>(a.y) + b * a.sy_b + h * P + ch0 + t0 * a.sy_l;
+  T* yp = reinterpret_cast<T*>(a.y) + b * a.sy_b + t0 * a.sy_l +
+          (MODE == MODE_DIAG ? h * P + ch0 : h);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     float v = y1[r];
 #pragma unroll
     for (int j = 0; j < 8; ++j) v = __builtin_fmaf(w[r][j], S[j], v);
     v = group_sum<G>(v);
-    if (t0 + r < a.L) store_bcast8<T>(yp + r * a.sy_l, v);
+    if (t0 + r < a.L) {
+      if constexpr (MODE == MODE_DIAG) store_bcast8<T>(yp + r * a.sy_l, v);
+      else if (g == 0) stf(yp + r * a.sy_l, v);
+    }
   }
 }
 
@@ -380,14 +410,14 @@ inline bool mh_tile_cfg(int64_t head_dim, int64_t chunk, TileCfg* cfg) {
   return true;
 }
 
-template <typename T, int DISC, bool APH, bool HAS_D>
+template <typename T, int DISC, bool APH, bool HAS_D, int MODE>
 int launch_mh_fused_g(int G, dim3 grid, dim3 block, size_t lds, hipStream_t s, const MhArgs& a) {
   switch (G) {
-    case 1: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 1>), grid, block, lds, s, a); break;
-    case 2: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 2>), grid, block, lds, s, a); break;
-    case 4: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 4>), grid, block, lds, s, a); break;
-    case 8: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 8>), grid, block, lds, s, a); break;
-    case 16: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 16>), grid, block, lds, s, a); break;
+    case 1: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 1, MODE>), grid, block, lds, s, a); break;
+    case 2: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 2, MODE>), grid, block, lds, s, a); break;
+    case 4: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 4, MODE>), grid, block, lds, s, a); break;
+    case 8: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 8, MODE>), grid, block, lds, s, a); break;
+    case 16: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 16, MODE>), grid, block, lds, s, a); break;
     default: return TSSM_ERR_UNSUPPORTED;
   }
   return launch_status();
@@ -397,10 +427,10 @@ template <typename T, int DISC>
 int launch_mh_fused_d(bool aph, bool has_d, int G, dim3 grid, dim3 block, size_t lds,
                       hipStream_t s, const MhArgs& a) {
   if (aph)
-    return has_d ? launch_mh_fused_g<T, DISC, true, true>(G, grid, block, lds, s, a)
-                 : launch_mh_fused_g<T, DISC, true, false>(G, grid, block, lds, s, a);
-  return has_d ? launch_mh_fused_g<T, DISC, false, true>(G, grid, block, lds, s, a)
-               : launch_mh_fused_g<T, DISC, false, false>(G, grid, block, lds, s, a);
+    return has_d ? launch_mh_fused_g<T, DISC, true, true, MODE_DIAG>(G, grid, block, lds, s, a)
+                 : launch_mh_fused_g<T, DISC, true, false, MODE_DIAG>(G, grid, block, lds, s, a);
+  return has_d ? launch_mh_fused_g<T, DISC, false, true, MODE_DIAG>(G, grid, block, lds, s, a)
+               : launch_mh_fused_g<T, DISC, false, false, MODE_DIAG>(G, grid, block, lds, s, a);
 }
 
 template <typename T>
@@ -470,6 +500,8 @@ extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const floa
   a.nrows = (uint32_t)nrows;
   a.tag = next_epoch(workspace);
   a.spin_limit = kDefaultSpinLimit;
+  a.chunk_major = 0;
+  a.dt_is_tau = 0;
 
 
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
@@ -544,4 +576,84 @@ extern "C" int tssm_mh_output(int dtype, const float* loc_a, const float* loc_x,
   }
 #undef TSSM_MH_OUT
   return launch_status();
+}
+
+// ---------------------------------------------------------------- selective scan (Mamba-1 lanes)
+namespace tssm {
+namespace {
+template <typename T, int DISC>
+int launch_sel_d(bool has_d, int G, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                 const MhArgs& a) {
+  return has_d ? launch_mh_fused_g<T, DISC, false, true, MODE_MAMBA1>(G, grid, block, lds, s, a)
+               : launch_mh_fused_g<T, DISC, false, false, MODE_MAMBA1>(G, grid, block, lds, s, a);
+}
+template <typename T>
+int launch_sel_t(int disc, bool has_d, int G, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                 const MhArgs& a) {
+  if (disc == TSSM_DISC_ZOH) return launch_sel_d<T, TSSM_DISC_ZOH>(has_d, G, grid, block, lds, s, a);
+  return launch_sel_d<T, TSSM_DISC_EULER>(has_d, G, grid, block, lds, s, a);
+}
+}  // namespace
+}  // namespace tssm
+
+extern "C" int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc,
+                                                       int64_t N, int64_t chunk) {
+  return tssm_mh_scan_workspace_bytes(nbatch, L, Dc, N, chunk);
+}
+
+extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt,
+                                   int dt_is_tau, const float* A_log, const void* B,
+                                   const void* C, const float* D, const float* h0, void* y,
+                                   float* h_last, int64_t nbatch, int64_t L, int64_t Dc,
+                                   int64_t N, int64_t sx_b, int64_t sx_l, int64_t sdt_b,
+                                   int64_t sdt_l, int64_t sdt_d, int64_t sB_b, int64_t sB_l,
+                                   int64_t sC_b, int64_t sC_l, int64_t sy_b, int64_t sy_l,
+                                   int64_t chunk, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  TSSM_CHECK(x && dt && A_log && B && C && y, TSSM_ERR_NULL);
+  TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nbatch > 0 && L > 0 && Dc > 0, TSSM_ERR_SHAPE);
+  TileCfg cfg;
+  TSSM_CHECK(mh_tile_cfg(N, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
+  const int64_t need = tssm_selective_scan_workspace_bytes(nbatch, L, Dc, N, chunk);
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);
+  const int64_t vec = dtype == TSSM_F32 ? 4 : 8;
+  TSSM_CHECK(sB_b % vec == 0 && sB_l % vec == 0 && sC_b % vec == 0 && sC_l % vec == 0,
+             TSSM_ERR_ALIGN);
+  TSSM_CHECK(aligned(B, 16) && aligned(C, 16) && aligned(A_log, 16), TSSM_ERR_ALIGN);
+  const int64_t strides[] = {sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b, sy_l};
+  for (int64_t s : strides) TSSM_CHECK(s >= 0, TSSM_ERR_STRIDE);
+  const int64_t nchunks = cdiv(L, cfg.TC);
+  const int64_t nrows = nbatch * Dc;
+  TSSM_CHECK(nchunks * nrows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
+  MhArgs a;
+  a.u = x; a.A_log = A_log; a.B = B; a.C = C; a.dt = dt; a.D = D; a.h0 = h0; a.y = y;
+  a.h_last = h_last;
+  a.L = L;
+  a.su_b = sx_b; a.su_l = sx_l;
+  a.sB_b = sB_b; a.sB_l = sB_l; a.sB_h = 0;
+  a.sC_b = sC_b; a.sC_l = sC_l; a.sC_h = 0;
+  a.sdt_b = sdt_b; a.sdt_l = sdt_l; a.sdt_h = sdt_d;
+  a.sy_b = sy_b; a.sy_l = sy_l;
+  a.hdr = reinterpret_cast<WsHeader*>(workspace);
+  a.words = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + sizeof(WsHeader));
+  a.n_heads = (uint32_t)Dc;
+  a.nchunks = (uint32_t)nchunks;
+  a.nrows = (uint32_t)nrows;
+  a.tag = next_epoch(workspace);
+  a.spin_limit = kDefaultSpinLimit;
+  a.chunk_major = 1;  // tiles sharing B/C rows (same batch and chunk) run together
+  a.dt_is_tau = dt_is_tau ? 1u : 0u;
+  const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
+  const int nrun = cfg.W * (64 / cfg.G);
+  const size_t lds = ((size_t)2 * nrun * N + 2 * (nrun / 8) * N + N) * sizeof(float);
+  const hipStream_t s = as_stream(stream);
+  const bool has_d = D != nullptr;
+  switch (dtype) {
+    case TSSM_BF16: return launch_sel_t<bf16_t>(disc, has_d, cfg.G, grid, block, lds, s, a);
+    case TSSM_F16: return launch_sel_t<f16_t>(disc, has_d, cfg.G, grid, block, lds, s, a);
+    default: return launch_sel_t<float>(disc, has_d, cfg.G, grid, block, lds, s, a);
+  }
 }

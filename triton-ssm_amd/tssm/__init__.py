@@ -9,6 +9,8 @@ Triton-convention launchers (``launch``), look-back workspaces
 workloads (``workloads``).
 """
 from . import _lib, launch, workspace  # noqa: F401
-from .fused import multihead_ssm_forward  # noqa: F401
+from .fused import (fused_interp_ssm_forward, multihead_ssm_forward,  # noqa: F401
+                    selective_scan_forward, ssd_scan_forward, ssd_stream_step)
 
-__all__ = ["multihead_ssm_forward"]
+__all__ = ["multihead_ssm_forward", "selective_scan_forward", "ssd_scan_forward",
+           "ssd_stream_step", "fused_interp_ssm_forward"]

@@ -94,3 +94,197 @@ def multihead_ssm_forward(u, A_log, B, C, dt, D=None, *, chunk=128, disc="euler"
               dt.stride(0), dt.stride(1), dt.stride(2), y.stride(0), y.stride(1), int(chunk),
               ws.data_ptr(), ws.numel(), stream)
     return (y, h_last) if return_state else y
+
+
+def _ws(nbytes, t, what):
+    if nbytes < 0:
+        raise ValueError(f"{what}: unsupported shape for the fused kernel")
+    stream = stream_handle(t)
+    return workspace.get(t.device, stream, nbytes), stream
+
+
+def ssd_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=256, disc="zoh", h0=None,
+                     return_state=False, out=None):
+    """SSD selective scan: one decay per head, state [P, N] per (batch, head).
+
+    x      [Bsz, L, H, P]  float32 / bfloat16 / float16 (P <= 64)
+    dt     [Bsz, L, H]     (read as float32)
+    A_log  [H]             log(-a) per head
+    B, C   [Bsz, L, H, N]  dtype of x, N in {8, 16, 32}
+    D      [H, P] / [H*P] or None
+    h0     [Bsz, H, P, N] float32 or None
+
+    h_t[p,n] = exp(dt_t a) h_{t-1}[p,n] + Bbar_t x_t[p] B_t[n];
+    y_t[p] = sum_n C_t[n] h_t[p,n] + D[p] x_t[p].  Returns y (dtype of x)
+    and, with ``return_state``, the final state [Bsz, H, P, N] float32.
+    """
+    for t, w in ((x, "x"), (dt, "dt"), (A_log, "A_log"), (B, "B"), (C, "C")):
+        need_gpu(t, w)
+    if x.dim() != 4 or B.dim() != 4 or C.shape != B.shape or dt.dim() != 3:
+        raise ValueError("expected x [Bsz,L,H,P], B/C [Bsz,L,H,N], dt [Bsz,L,H]")
+    Bsz, L, H, P = x.shape
+    N = B.shape[-1]
+    if B.shape[:3] != (Bsz, L, H) or dt.shape != (Bsz, L, H) or A_log.shape != (H,):
+        raise ValueError("shape mismatch between x, B, C, dt and A_log")
+    if B.dtype != x.dtype or C.dtype != x.dtype:
+        raise TypeError("x, B and C must share one dtype")
+    code = dcode(x, "x")
+    for t, w in ((x, "x"), (B, "B"), (C, "C")):
+        _inner_unit(t, w)
+    A_log = as_f32(A_log, "A_log").contiguous()
+    dt = as_f32(dt, "dt")
+    if D is not None:
+        need_gpu(D, "D")
+        if D.numel() != H * P:
+            raise ValueError("D must have H*P elements")
+        D = as_f32(D, "D").contiguous()
+    if h0 is not None:
+        need_gpu(h0, "h0")
+        if tuple(h0.shape) != (Bsz, H, P, N):
+            raise ValueError("h0 must be [Bsz, H, P, N]")
+        h0 = as_f32(h0, "h0").contiguous()
+    y = torch.empty(Bsz, L, H, P, device=x.device, dtype=x.dtype) if out is None else out
+    need_gpu(y, "out")
+    if y.shape != x.shape or y.dtype != x.dtype:
+        raise ValueError("out must match x in shape and dtype")
+    _inner_unit(y, "out")
+    h_last = torch.empty(Bsz, H, P, N, device=x.device, dtype=torch.float32) if return_state else None
+    L_ = _lib.lib()
+    ws, stream = _ws(L_.tssm_ssd_scan_workspace_bytes(Bsz, L, H, P, N, int(chunk)), x, "ssd_scan")
+    _lib.call("tssm_ssd_scan", code, _disc_code(disc), x.data_ptr(), dt.data_ptr(),
+              A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), ptr(h0), y.data_ptr(),
+              ptr(h_last), Bsz, L, H, P, N, *x.stride()[:3], *dt.stride(), *B.stride()[:3],
+              *C.stride()[:3], *y.stride()[:3], int(chunk), ws.data_ptr(), ws.numel(), stream)
+    return (y, h_last) if return_state else y
+
+
+def ssd_stream_step(x, dt, A_log, B, C, D, state, *, disc="zoh", out=None):
+    """One streaming SSD step, the state updated in place in HBM.
+
+    x [S, H, P], dt [S] (one per stream) or [S, H], A_log [H], B/C [S, H, N],
+    D [H, P] / [H*P] or None, state [S, H, P, N]; all float32.  Returns y [S, H, P].
+    """
+    for t, w in ((x, "x"), (dt, "dt"), (A_log, "A_log"), (B, "B"), (C, "C"), (state, "state")):
+        need_gpu(t, w)
+        if t.dtype != torch.float32:
+            raise TypeError(f"{w} must be float32")
+    S, H, P = x.shape
+    N = B.shape[-1]
+    if B.shape != (S, H, N) or C.shape != (S, H, N) or tuple(state.shape) != (S, H, P, N):
+        raise ValueError("expected B/C [S,H,N] and state [S,H,P,N]")
+    if not state.is_contiguous():
+        raise ValueError("state must be contiguous")
+    if dt.shape == (S,):
+        sdt = (dt.stride(0), 0)
+    elif dt.shape == (S, H):
+        sdt = dt.stride()
+    else:
+        raise ValueError("dt must be [S] or [S, H]")
+    for t, w in ((x, "x"), (B, "B"), (C, "C")):
+        _inner_unit(t, w)
+    A_log = A_log.contiguous()
+    if D is not None:
+        need_gpu(D, "D")
+        D = as_f32(D, "D").contiguous()
+        if D.numel() != H * P:
+            raise ValueError("D must have H*P elements")
+    y = torch.empty(S, H, P, device=x.device, dtype=torch.float32) if out is None else out
+    _inner_unit(y, "out")
+    _lib.call("tssm_ssd_stream_step", _disc_code(disc), x.data_ptr(), dt.data_ptr(),
+              A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), state.data_ptr(),
+              y.data_ptr(), S, H, P, N, *sdt, *x.stride()[:2], *B.stride()[:2],
+              *C.stride()[:2], *y.stride()[:2], stream_handle(x))
+    return y
+
+
+def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh", h0=None,
+                           return_state=False, dt_is_tau=False, out=None):
+    """Mamba-1 selective scan over lanes (channel d, state n).
+
+    x      [Bsz, L, Dc]        float32 / bfloat16 / float16
+    dt     [Bsz, L] (one per step, shared by the channels) or [Bsz, L, Dc];
+           with ``dt_is_tau`` it holds timestamps and dt_t = tau_t - tau_{t-1},
+           dt_0 = tau_0
+    A_log  [Dc, N]             log(-a) per lane
+    B, C   [Bsz, L, N]         dtype of x; N a multiple of 8, <= 128
+    D      [Dc] or None;  h0 [Bsz, Dc, N] float32 or None
+
+    h_t[d,n] = exp(dt_t a[d,n]) h_{t-1}[d,n] + Bbar_t[d,n] B_t[n] x_t[d];
+    y_t[d] = sum_n C_t[n] h_t[d,n] + D[d] x_t[d].
+    """
+    for t, w in ((x, "x"), (dt, "dt"), (A_log, "A_log"), (B, "B"), (C, "C")):
+        need_gpu(t, w)
+    if x.dim() != 3 or B.dim() != 3 or C.shape != B.shape:
+        raise ValueError("expected x [Bsz,L,Dc] and B/C [Bsz,L,N]")
+    Bsz, L, Dc = x.shape
+    N = B.shape[-1]
+    if B.shape[:2] != (Bsz, L) or A_log.shape != (Dc, N):
+        raise ValueError("shape mismatch between x, B, C and A_log")
+    if B.dtype != x.dtype or C.dtype != x.dtype:
+        raise TypeError("x, B and C must share one dtype")
+    code = dcode(x, "x")
+    for t, w in ((B, "B"), (C, "C")):
+        _inner_unit(t, w)
+    dt = as_f32(dt, "dt")
+    if dt.shape == (Bsz, L):
+        sdt = (dt.stride(0), dt.stride(1), 0)
+    elif dt.shape == (Bsz, L, Dc) and not dt_is_tau:
+        sdt = dt.stride()
+    else:
+        raise ValueError("dt must be [Bsz, L] (or [Bsz, L, Dc] without dt_is_tau)")
+    A_log = as_f32(A_log, "A_log").contiguous()
+    if D is not None:
+        need_gpu(D, "D")
+        if D.numel() != Dc:
+            raise ValueError("D must have Dc elements")
+        D = as_f32(D, "D").contiguous()
+    if h0 is not None:
+        need_gpu(h0, "h0")
+        if tuple(h0.shape) != (Bsz, Dc, N):
+            raise ValueError("h0 must be [Bsz, Dc, N]")
+        h0 = as_f32(h0, "h0").contiguous()
+    y = torch.empty(Bsz, L, Dc, device=x.device, dtype=x.dtype) if out is None else out
+    need_gpu(y, "out")
+    if y.shape != x.shape or y.dtype != x.dtype:
+        raise ValueError("out must match x in shape and dtype")
+    h_last = torch.empty(Bsz, Dc, N, device=x.device, dtype=torch.float32) if return_state else None
+    L_ = _lib.lib()
+    ws, stream = _ws(L_.tssm_selective_scan_workspace_bytes(Bsz, L, Dc, N, int(chunk)), x,
+                     "selective_scan")
+    _lib.call("tssm_selective_scan", code, _disc_code(disc), x.data_ptr(), dt.data_ptr(),
+              int(bool(dt_is_tau)), A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D),
+              ptr(h0), y.data_ptr(), ptr(h_last), Bsz, L, Dc, N, x.stride(0), x.stride(1),
+              *sdt, B.stride(0), B.stride(1), C.stride(0), C.stride(1), y.stride(0),
+              y.stride(1), int(chunk), ws.data_ptr(), ws.numel(), stream)
+    return (y, h_last) if return_state else y
+
+
+def fused_interp_ssm_forward(V, M, tau, A_log, B, C, D=None, *, K=10, FTILE=128, disc="zoh",
+                             chunk=128, h0=None, return_state=False):
+    """Interpolation of irregular observations followed by a Mamba-1 scan.
+
+    V, M [Bsz, T, F] (M > 0.5 observed, tested through FTILE-wide tile sums as
+    in fused_interp_kernel.py), tau [Bsz, T] sorted timestamps.  Vhat is the
+    reference's time-aware interpolation (K, FTILE honoured); the scan then
+    runs over channels F with dt_t = tau_t - tau_{t-1} (dt_0 = tau_0) computed
+    in the scan's load stage.  Returns (Vhat, y[, h_last]).
+    """
+    for t, w in ((V, "V"), (M, "M"), (tau, "tau")):
+        need_gpu(t, w)
+    if V.dim() != 3 or M.shape != V.shape or tau.shape != V.shape[:2]:
+        raise ValueError("expected V, M [Bsz,T,F] and tau [Bsz,T]")
+    Bsz, T, F = V.shape
+    _inner_unit(V, "V")
+    _inner_unit(M, "M")
+    Vhat = torch.empty(Bsz, T, F, device=V.device, dtype=V.dtype)
+    tau32 = as_f32(tau, "tau").contiguous()
+    _lib.call("tssm_time_aware_interp", dcode(V, "V"), dcode(M, "M"), dcode(tau32, "tau"),
+              V.data_ptr(), M.data_ptr(), tau32.data_ptr(), Vhat.data_ptr(), Bsz, T, F,
+              V.stride(0), V.stride(1), M.stride(0), M.stride(1), tau32.stride(0),
+              tau32.stride(1), Vhat.stride(0), Vhat.stride(1), int(K), int(FTILE), Bsz, T,
+              -(-F // int(FTILE)), stream_handle(V))
+    res = selective_scan_forward(Vhat, tau32, A_log, B, C, D, chunk=chunk, disc=disc, h0=h0,
+                                 return_state=return_state, dt_is_tau=True)
+    if return_state:
+        return Vhat, res[0], res[1]
+    return Vhat, res
