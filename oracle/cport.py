@@ -21,6 +21,7 @@ _SIGS = {
     "oc_ssd_scan": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L], None),
     "oc_selective_scan": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L], None),
     "oc_ssd_stream_step": ([_I, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L], None),
+    "oc_time_aware_interp": ([_P, _P, _P, _P, _L, _L, _L, _L, _L], None),
 }
 
 
@@ -104,3 +105,11 @@ def ssd_stream_step(x, dt, A_log, B, C, D, state, disc="zoh"):
     lib().oc_ssd_stream_step(int(disc == "zoh"), _p(x), _p(dt), _p(A_log), _p(B), _p(C), _p(D),
                              _p(state), _p(y), S, H, P, N)
     return y
+
+
+def time_aware_interp(V, M, tau, K=10, FTILE=128):
+    V, M, tau = (_f32(v) for v in (V, M, tau))
+    Bsz, T, F = V.shape
+    out = np.empty_like(V)
+    lib().oc_time_aware_interp(_p(V), _p(M), _p(tau), _p(out), Bsz, T, F, K, FTILE)
+    return out

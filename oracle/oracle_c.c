@@ -160,3 +160,48 @@ void oc_ssd_stream_step(int zoh, const float* x, const float* dt, const float* A
     }
   }
 }
+
+/* Time-aware interpolation, fused_interp_kernel.py:29-100 (fp32): for each
+ * (b, t, FTILE-wide tile) the nearest step within K on each side whose tile
+ * has any observed lane (mask tile sum > 0.5); time-weighted linear
+ * interpolation, w = 0.5 when tau_next - tau_prev <= 1e-9.
+ * V, M, Vhat [Bsz,T,F]; tau [Bsz,T]; contiguous fp32. */
+void oc_time_aware_interp(const float* V, const float* M, const float* tau, float* Vhat,
+                          int64_t Bsz, int64_t T, int64_t F, int64_t K, int64_t FTILE) {
+  const int64_t nt = (F + FTILE - 1) / FTILE;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < Bsz; ++b) {
+    for (int64_t tile = 0; tile < nt; ++tile) {
+      const int64_t f0 = tile * FTILE, f1 = f0 + FTILE < F ? f0 + FTILE : F;
+      unsigned char* obs = (unsigned char*)malloc((size_t)T);
+      for (int64_t t = 0; t < T; ++t) {
+        float s = 0.0f;
+        for (int64_t f = f0; f < f1; ++f) s += M[(b * T + t) * F + f];
+        obs[t] = s > 0.5f;
+      }
+      for (int64_t t = 0; t < T; ++t) {
+        int64_t prev = -1, next = -1;
+        for (int64_t k = 1; k <= K && prev < 0; ++k)
+          if (t - k >= 0 && obs[t - k]) prev = t - k;
+        for (int64_t k = 1; k <= K && next < 0; ++k)
+          if (t + k < T && obs[t + k]) next = t + k;
+        const float tp = prev >= 0 ? tau[b * T + prev] : 0.0f;
+        const float tn = next >= 0 ? tau[b * T + next] : 0.0f;
+        const float den = tn - tp;
+        float w = den > 1e-9f ? (tau[b * T + t] - tp) / den : 0.5f;
+        w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+        const float* vr = V + b * T * F;
+        float* o = Vhat + (b * T + t) * F;
+        for (int64_t f = f0; f < f1; ++f) {
+          float v;
+          if (prev >= 0 && next >= 0) v = (1.0f - w) * vr[prev * F + f] + w * vr[next * F + f];
+          else if (prev >= 0) v = vr[prev * F + f];
+          else if (next >= 0) v = vr[next * F + f];
+          else v = vr[t * F + f];
+          o[f] = v;
+        }
+      }
+      free(obs);
+    }
+  }
+}

@@ -52,3 +52,16 @@ def test_ssd_selective_stream():
     y_ref, h_ref = O.selective_scan(xs, dts, Al, Bm, Cm, np.ones(6))
     assert_close(y, y_ref, 1e-5, "mamba1 y")
     assert cport.threads() >= 1
+
+
+def test_interp():
+    r = np.random.default_rng(3)
+    Bsz, T, F = 2, 90, 40
+    # fp32 inputs for both sides: the weight (tau_t - tau_p) / (tau_n - tau_p)
+    # amplifies timestamp rounding
+    tau = np.sort(r.uniform(0, 10, size=(Bsz, T)), axis=1).astype(np.float32)
+    M = (r.random((Bsz, T, F)) < 0.05).astype(np.float32)
+    V = (r.normal(size=(Bsz, T, F)) * M).astype(np.float32)
+    for K, FT in ((10, 128), (3, 8)):
+        out = cport.time_aware_interp(V, M, tau, K, FT)
+        assert_close(out, O.time_aware_interp(V, M, tau, K, FT), 1e-6, f"interp K={K} FTILE={FT}")

@@ -131,12 +131,13 @@ def test_selective_scan_small_config(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("N", [8, 16, 64])
+@pytest.mark.parametrize("N,Dc", [(8, 40), (16, 40), (64, 40), (16, 6), (32, 9), (128, 3)])
 @pytest.mark.parametrize("dt_per_channel", [False, True])
-def test_selective_scan(dev, dtype, N, dt_per_channel):
+def test_selective_scan(dev, dtype, N, Dc, dt_per_channel):
+    """Channel counts that do and do not fill the packed 64-lane rows."""
     from tssm import selective_scan_forward
-    d = _mamba1_inputs(dev, 3, 700, 40, N, dtype, seed=N, dt_per_channel=dt_per_channel)
-    h0 = torch.randn(3, 40, N, device=dev)
+    d = _mamba1_inputs(dev, 3, 700, Dc, N, dtype, seed=N + Dc, dt_per_channel=dt_per_channel)
+    h0 = torch.randn(3, Dc, N, device=dev)
     y, h = selective_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], h0=h0,
                                   return_state=True, chunk=128)
     torch.cuda.synchronize()

@@ -77,8 +77,10 @@ constexpr int MODE_MAMBA1 = 1;
 constexpr int kMhR = 4;    // consecutive steps per thread
 constexpr int kMhWin = 2;  // predecessors read per look-back round trip (measured best)
 
-template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE>
+template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE, int NS>
 __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
+  // NS = threads summed into one output value: the whole row for MODE_DIAG
+  // (NS == G), one channel's N/8 threads for MODE_MAMBA1.
   constexpr int P = G * 8;
   constexpr int ROWS = 64 / G;
   constexpr int R = kMhR;
@@ -114,17 +116,21 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   const uint32_t b = row / a.n_heads;
   const uint32_t h = row - b * a.n_heads;
   const int64_t t0 = (int64_t)c * TC + (int64_t)run * R;
+  // MODE_MAMBA1: a row packs P / (8 NS) channels of N = 8 NS states each
+  const int64_t chan = (MODE == MODE_DIAG) ? (int64_t)h
+                                           : (int64_t)h * (P / (8 * NS)) + g / NS;
 
   // ---- loads (all issued before any use)
   Vec8<T> vu[R], vB[R], vC[R];
   float us[R];  // MODE_MAMBA1: the channel's input, shared by its 8 state lanes
   float dtv[R];
   {
+    const int bc = (MODE == MODE_DIAG) ? ch0 : (g % NS) * 8;  // state offset within B/C rows
     const T* up = reinterpret_cast<const T*>(a.u) + b * a.su_b + t0 * a.su_l +
-                  (MODE == MODE_DIAG ? h * P + ch0 : h);
-    const T* Bp = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h + ch0 + t0 * a.sB_l;
-    const T* Cp = reinterpret_cast<const T*>(a.C) + b * a.sC_b + h * a.sC_h + ch0 + t0 * a.sC_l;
-    const float* dp = a.dt + b * a.sdt_b + h * a.sdt_h + t0 * a.sdt_l;
+                  (MODE == MODE_DIAG ? h * P + ch0 : chan);
+    const T* Bp = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h + bc + t0 * a.sB_l;
+    const T* Cp = reinterpret_cast<const T*>(a.C) + b * a.sC_b + h * a.sC_h + bc + t0 * a.sC_l;
+    const float* dp = a.dt + b * a.sdt_b + chan * a.sdt_h + t0 * a.sdt_l;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (t0 + r < a.L) {
@@ -158,7 +164,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   }
   float Dv[8];
   if constexpr (HAS_D && MODE == MODE_MAMBA1) {
-    Dv[0] = a.D[h];
+    Dv[0] = a.D[chan];
   } else if constexpr (HAS_D) {
     const float4* dp4 = reinterpret_cast<const float4*>(a.D + h * P + ch0);
     const float4 d0 = dp4[0], d1 = dp4[1];
@@ -206,7 +212,8 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       if constexpr (HAS_D && MODE == MODE_DIAG) acc = __builtin_fmaf(Dv[j], uj, acc);
     }
     // MODE_MAMBA1: D[d] x[d] once per channel (the group's first thread)
-    if constexpr (HAS_D && MODE == MODE_MAMBA1) acc = g == 0 ? __builtin_fmaf(Dv[0], us[r], acc) : acc;
+    if constexpr (HAS_D && MODE == MODE_MAMBA1)
+      acc = (g % NS) == 0 ? __builtin_fmaf(Dv[0], us[r], acc) : acc;
     y1[r] = acc;
   }
   {
@@ -281,16 +288,16 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     S[6] = __builtin_fmaf(a1.z, c1.z, x1.z); S[7] = __builtin_fmaf(a1.w, c1.w, x1.w);
   }
   T* yp = reinterpret_cast<T*>(a.y) + b * a.sy_b + t0 * a.sy_l +
-          (MODE == MODE_DIAG ? h * P + ch0 : h);
+          (MODE == MODE_DIAG ? h * P + ch0 : chan);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     float v = y1[r];
 #pragma unroll
     for (int j = 0; j < 8; ++j) v = __builtin_fmaf(w[r][j], S[j], v);
-    v = group_sum<G>(v);
+    v = group_sum<NS>(v);
     if (t0 + r < a.L) {
       if constexpr (MODE == MODE_DIAG) store_bcast8<T>(yp + r * a.sy_l, v);
-      else if (g == 0) stf(yp + r * a.sy_l, v);
+      else if ((g % NS) == 0) stf(yp + r * a.sy_l, v);
     }
   }
 }
@@ -413,14 +420,29 @@ inline bool mh_tile_cfg(int64_t head_dim, int64_t chunk, TileCfg* cfg) {
 template <typename T, int DISC, bool APH, bool HAS_D, int MODE>
 int launch_mh_fused_g(int G, dim3 grid, dim3 block, size_t lds, hipStream_t s, const MhArgs& a) {
   switch (G) {
-    case 1: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 1, MODE>), grid, block, lds, s, a); break;
-    case 2: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 2, MODE>), grid, block, lds, s, a); break;
-    case 4: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 4, MODE>), grid, block, lds, s, a); break;
-    case 8: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 8, MODE>), grid, block, lds, s, a); break;
-    case 16: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 16, MODE>), grid, block, lds, s, a); break;
+    case 1: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 1, MODE, 1>), grid, block, lds, s, a); break;
+    case 2: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 2, MODE, 2>), grid, block, lds, s, a); break;
+    case 4: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 4, MODE, 4>), grid, block, lds, s, a); break;
+    case 8: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 8, MODE, 8>), grid, block, lds, s, a); break;
+    case 16: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 16, MODE, 16>), grid, block, lds, s, a); break;
     default: return TSSM_ERR_UNSUPPORTED;
   }
   return launch_status();
+}
+
+// MODE_MAMBA1 rows of P = 8 G lanes holding channels of N = 8 NS states.
+template <typename T, int DISC, bool HAS_D>
+int launch_sel_gn(int G, int NS, dim3 grid, dim3 block, size_t lds, hipStream_t s, const MhArgs& a) {
+#define TSSM_SEL(GV, NV)                                                                          \
+  if (G == GV && NS == NV) {                                                                    \
+    hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, false, HAS_D, GV, MODE_MAMBA1, NV>), grid, \
+                       block, lds, s, a);                                                       \
+    return launch_status();                                                                     \
+  }
+  TSSM_SEL(8, 1) TSSM_SEL(8, 2) TSSM_SEL(8, 4) TSSM_SEL(8, 8) TSSM_SEL(16, 16)
+  TSSM_SEL(1, 1) TSSM_SEL(2, 1) TSSM_SEL(2, 2) TSSM_SEL(4, 1) TSSM_SEL(4, 2) TSSM_SEL(4, 4)
+#undef TSSM_SEL
+  return TSSM_ERR_UNSUPPORTED;
 }
 
 template <typename T, int DISC>
@@ -582,23 +604,32 @@ extern "C" int tssm_mh_output(int dtype, const float* loc_a, const float* loc_x,
 namespace tssm {
 namespace {
 template <typename T, int DISC>
-int launch_sel_d(bool has_d, int G, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+int launch_sel_d(bool has_d, int G, int NS, dim3 grid, dim3 block, size_t lds, hipStream_t s,
                  const MhArgs& a) {
-  return has_d ? launch_mh_fused_g<T, DISC, false, true, MODE_MAMBA1>(G, grid, block, lds, s, a)
-               : launch_mh_fused_g<T, DISC, false, false, MODE_MAMBA1>(G, grid, block, lds, s, a);
+  return has_d ? launch_sel_gn<T, DISC, true>(G, NS, grid, block, lds, s, a)
+               : launch_sel_gn<T, DISC, false>(G, NS, grid, block, lds, s, a);
 }
 template <typename T>
-int launch_sel_t(int disc, bool has_d, int G, dim3 grid, dim3 block, size_t lds, hipStream_t s,
-                 const MhArgs& a) {
-  if (disc == TSSM_DISC_ZOH) return launch_sel_d<T, TSSM_DISC_ZOH>(has_d, G, grid, block, lds, s, a);
-  return launch_sel_d<T, TSSM_DISC_EULER>(has_d, G, grid, block, lds, s, a);
+int launch_sel_t(int disc, bool has_d, int G, int NS, dim3 grid, dim3 block, size_t lds,
+                 hipStream_t s, const MhArgs& a) {
+  if (disc == TSSM_DISC_ZOH) return launch_sel_d<T, TSSM_DISC_ZOH>(has_d, G, NS, grid, block, lds, s, a);
+  return launch_sel_d<T, TSSM_DISC_EULER>(has_d, G, NS, grid, block, lds, s, a);
+}
+// Channels packed per row: rows of 64 lanes (128 when N = 128), so tiles are
+// as large as the multihead ones; must divide Dc.
+inline int64_t sel_channels_per_row(int64_t Dc, int64_t N) {
+  int64_t cpr = N >= 64 ? 1 : 64 / N;
+  while (cpr > 1 && Dc % cpr != 0) cpr /= 2;
+  return cpr;
 }
 }  // namespace
 }  // namespace tssm
 
 extern "C" int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc,
                                                        int64_t N, int64_t chunk) {
-  return tssm_mh_scan_workspace_bytes(nbatch, L, Dc, N, chunk);
+  if (Dc <= 0 || N <= 0 || N % 8 != 0) return -1;
+  const int64_t cpr = sel_channels_per_row(Dc, N);
+  return tssm_mh_scan_workspace_bytes(nbatch, L, Dc / cpr, cpr * N, chunk);
 }
 
 extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt,
@@ -614,8 +645,11 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
   TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
   TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
   TSSM_CHECK(nbatch > 0 && L > 0 && Dc > 0, TSSM_ERR_SHAPE);
+  TSSM_CHECK(N > 0 && N % 8 == 0 && N <= 128, TSSM_ERR_UNSUPPORTED);
+  const int64_t cpr = sel_channels_per_row(Dc, N);
+  const int64_t P = cpr * N;  // lanes per row
   TileCfg cfg;
-  TSSM_CHECK(mh_tile_cfg(N, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(mh_tile_cfg(P, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
   const int64_t need = tssm_selective_scan_workspace_bytes(nbatch, L, Dc, N, chunk);
   TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
   TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);
@@ -626,7 +660,7 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
   const int64_t strides[] = {sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b, sy_l};
   for (int64_t s : strides) TSSM_CHECK(s >= 0, TSSM_ERR_STRIDE);
   const int64_t nchunks = cdiv(L, cfg.TC);
-  const int64_t nrows = nbatch * Dc;
+  const int64_t nrows = nbatch * (Dc / cpr);
   TSSM_CHECK(nchunks * nrows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
   MhArgs a;
   a.u = x; a.A_log = A_log; a.B = B; a.C = C; a.dt = dt; a.D = D; a.h0 = h0; a.y = y;
@@ -639,21 +673,22 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
   a.sy_b = sy_b; a.sy_l = sy_l;
   a.hdr = reinterpret_cast<WsHeader*>(workspace);
   a.words = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + sizeof(WsHeader));
-  a.n_heads = (uint32_t)Dc;
+  a.n_heads = (uint32_t)(Dc / cpr);
   a.nchunks = (uint32_t)nchunks;
   a.nrows = (uint32_t)nrows;
   a.tag = next_epoch(workspace);
   a.spin_limit = kDefaultSpinLimit;
-  a.chunk_major = 1;  // tiles sharing B/C rows (same batch and chunk) run together
+  a.chunk_major = 0;
   a.dt_is_tau = dt_is_tau ? 1u : 0u;
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
   const int nrun = cfg.W * (64 / cfg.G);
-  const size_t lds = ((size_t)2 * nrun * N + 2 * (nrun / 8) * N + N) * sizeof(float);
+  const size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + P) * sizeof(float);
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr;
+  const int NS = (int)(N / 8);
   switch (dtype) {
-    case TSSM_BF16: return launch_sel_t<bf16_t>(disc, has_d, cfg.G, grid, block, lds, s, a);
-    case TSSM_F16: return launch_sel_t<f16_t>(disc, has_d, cfg.G, grid, block, lds, s, a);
-    default: return launch_sel_t<float>(disc, has_d, cfg.G, grid, block, lds, s, a);
+    case TSSM_BF16: return launch_sel_t<bf16_t>(disc, has_d, cfg.G, NS, grid, block, lds, s, a);
+    case TSSM_F16: return launch_sel_t<f16_t>(disc, has_d, cfg.G, NS, grid, block, lds, s, a);
+    default: return launch_sel_t<float>(disc, has_d, cfg.G, NS, grid, block, lds, s, a);
   }
 }

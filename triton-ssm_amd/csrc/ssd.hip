@@ -6,21 +6,23 @@
 // ssm_scan.py:5-10 with the discretization of discretize_kernel.py:44-54 and
 // one decay per head.
 //
-// ssd_scan_kernel: single pass with decoupled look-back.
-//   tile = (row = b*H + h, chunk c of TC = 4*RUN steps), numbered chunk-major
-//   (blockIdx = c * rows + row): with few rows and many chunks, a tile's
-//   predecessor is a whole layer of rows earlier in launch order.
-//   4 waves = 4 runs of RUN steps; lane = channel p with the N state values of
-//   its row p in registers.  The per-step decay and input coefficient are
-//   computed once per tile into LDS; B_t and C_t are wave-uniform.
-//   sweep 1: each run's local state from zero -> runs combined in LDS ->
-//   the last wave publishes the tile aggregate (one decay word + P*N state
-//   words), looks back for the entry state, publishes the inclusive state ->
-//   sweep 2: each run rescans from its exact entry state and writes y.
+// ssd_scan: three passes (chunk states, state passing, chunk outputs).  With
+// few (batch, head) rows and very long sequences a single pass would keep
+// hundreds of chunks of one row in flight, each look-back hop moving a whole
+// P x N state; the passes instead re-read x, B and dt once.
+//   pass 1 ssd_state_kernel: one wave per (row, chunk of TC steps), lane = p
+//     with its N states in registers; writes the chunk's decay product and
+//     local end state (from zero).
+//   pass 2 ssd_pass_kernel: per state entry, a segmented scan over chunks
+//     gives every chunk's entry state (and the final state).
+//   pass 3 ssd_out_kernel: one wave per chunk rescans from its entry state and
+//     writes y.
+//   Both scans use the rescaled state h_t = P_t g_t (P_t = decay product since
+//   the chunk start), so a step costs one FMA per state for the update; g is
+//   folded back into h whenever P_t would drop below 2^-64.
 // ssd_stream_step_kernel: one streaming step with the state [S,H,P,N] fp32
 //   resident in HBM, updated in place; one workgroup per (stream, head).
 #include "common.h"
-#include "lookback.h"
 
 namespace tssm {
 
@@ -37,210 +39,211 @@ struct SsdArgs {
   int64_t L;
   int64_t sx_b, sx_l, sx_h, sdt_b, sdt_l, sdt_h, sB_b, sB_l, sB_h, sC_b, sC_l, sC_h;
   int64_t sy_b, sy_l, sy_h;
-  WsHeader* hdr;
-  uint64_t* words;
-  uint32_t H, P, rows, nchunks, run, tag, spin_limit;
+  float* chunkA;   // [rows][nchunks] decay product of each chunk
+  float* chunkX;   // [rows][nchunks][P*N] local end state of each chunk (from zero)
+  float* entry;    // [rows][nchunks][P*N] state entering each chunk
+  uint32_t H, P, rows, nchunks, tc;
 };
 
-constexpr int kSsdWaves = 4;
+constexpr float kRescaleFloor = 5.421010862427522e-20f;  // 2^-64
+constexpr int kSsdSub = 16;  // steps staged per sub-block
 
-// B_t[n] / C_t[n] for all n of one step, wave-uniform, converted to fp32.
-template <typename T, int N>
-__device__ inline void load_row(const T* __restrict__ p, float* out) {
+// Per-step decay and input coefficient for steps [t0, t0+64) of one head,
+// computed by lane i for step t0+i and shared through LDS.  Steps at or past
+// L get dt = 0, i.e. decay 1 and coefficient 0, so they leave the state alone.
+template <int DISC>
+__device__ inline void step_scalars(const float* dtp, int64_t sdt_l, int64_t t0, int64_t L,
+                                    float a2, float* s_ab, float* s_cf, int lane) {
+  const int64_t t = t0 + lane;
+  const float d = t < L ? dtp[t * sdt_l] : 0.0f;
+  const float arg = d * a2;
+  const float ab = exp2_fast(arg);
+  s_ab[lane] = ab;
+  s_cf[lane] = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * d : d;
+}
+
+// One step of the rescaled recurrence h = Pt g:  h_t = ab h_{t-1} + xs B_t.
+// When Pt ab would fall below 2^-64 the factor is folded into g (the branch is
+// uniform: Pt and ab are the same on every lane of the wave).
+template <int N>
+__device__ inline void rescaled_step(float* g, float& Pt, float ab, float xs, const float* bv) {
+  // Pt and ab hold the same value on every lane; reading the product through
+  // lane 0 makes the fold decision a scalar branch.
+  const float Pn = __builtin_bit_cast(
+      float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, Pt * ab)));
+  if (Pn < kRescaleFloor) {
 #pragma unroll
-  for (int n = 0; n < N; ++n) out[n] = ldf(p + n);
+    for (int n = 0; n < N; ++n) g[n] = __builtin_fmaf(xs, bv[n], g[n] * Pn);
+    Pt = 1.0f;
+  } else {
+    const float xr = xs * __builtin_amdgcn_rcpf(Pn);
+#pragma unroll
+    for (int n = 0; n < N; ++n) g[n] = __builtin_fmaf(xr, bv[n], g[n]);
+    Pt = Pn;
+  }
+}
+
+// Stage rows [t0, t0+kSsdSub) of an N-wide operand into LDS as fp32
+// (s[i*N + n]); rows at or past L read as zero.
+template <typename T, int N>
+__device__ inline void stage_rows(const T* __restrict__ base, int64_t sl, int64_t t0, int64_t L,
+                                  float* s, int lane) {
+#pragma unroll
+  for (int k = lane; k < kSsdSub * N; k += 64) {
+    const int i = k / N, n = k - (k / N) * N;
+    const int64_t t = t0 + i;
+    s[k] = t < L ? ldf(base + t * sl + n) : 0.0f;
+  }
+}
+
+// Stage x_t[lane] for t in [t0, t0+kSsdSub) into s_x[i*64 + lane].
+template <typename T>
+__device__ inline void stage_x(const T* __restrict__ xp, int64_t sl, int64_t t0, int64_t L,
+                               bool act, float* s_x, int lane) {
+#pragma unroll
+  for (int i = 0; i < kSsdSub; ++i) {
+    const int64_t t = t0 + i;
+    s_x[i * 64 + lane] = (act && t < L) ? ldf(xp + t * sl) : 0.0f;
+  }
+}
+
+template <typename T, int DISC, int N>
+__global__ __launch_bounds__(64) void ssd_state_kernel(SsdArgs a) {
+  __shared__ float s_ab[64], s_cf[64];
+  __shared__ __align__(16) float s_B[kSsdSub * N];
+  __shared__ float s_x[kSsdSub * 64];
+  const int lane = threadIdx.x;
+  const int P = (int)a.P;
+  const bool act = lane < P;
+  const uint32_t row = blockIdx.x / a.nchunks;
+  const uint32_t c = blockIdx.x - row * a.nchunks;
+  const uint32_t b = row / a.H, h = row - (row / a.H) * a.H;
+  const float a2 = -expf(a.A_log[h]) * kLog2e;
+  const int64_t tbeg = (int64_t)c * a.tc;
+  const int64_t tend = tbeg + a.tc < a.L ? tbeg + a.tc : a.L;
+  const float* dtp = a.dt + b * a.sdt_b + h * a.sdt_h;
+  const T* xp = reinterpret_cast<const T*>(a.x) + b * a.sx_b + h * a.sx_h + (act ? lane : 0);
+  const T* Bp = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h;
+  float g[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) g[n] = 0.0f;
+  float Pt = 1.0f, Achunk = 1.0f;
+  for (int64_t t0 = tbeg; t0 < tend; t0 += 64) {
+    step_scalars<DISC>(dtp, a.sdt_l, t0, a.L, a2, s_ab, s_cf, lane);
+    for (int j = 0; j < 64 && t0 + j < tend; j += kSsdSub) {
+      stage_x<T>(xp, a.sx_l, t0 + j, a.L, act, s_x, lane);
+      stage_rows<T, N>(Bp, a.sB_l, t0 + j, a.L, s_B, lane);
+      __syncthreads();
+#pragma unroll 2
+      for (int i = 0; i < kSsdSub; ++i) {
+        const float ab = s_ab[j + i];
+        float bv[N];
+#pragma unroll
+        for (int n = 0; n < N; ++n) bv[n] = s_B[i * N + n];
+        rescaled_step<N>(g, Pt, ab, s_cf[j + i] * s_x[i * 64 + lane], bv);
+        Achunk *= ab;
+      }
+      __syncthreads();
+    }
+  }
+  const int64_t PN = (int64_t)P * N;
+  if (act) {
+    float* out = a.chunkX + ((int64_t)row * a.nchunks + c) * PN + (int64_t)lane * N;
+#pragma unroll
+    for (int n = 0; n < N; ++n) out[n] = Pt * g[n];
+  }
+  if (lane == 0) a.chunkA[(int64_t)row * a.nchunks + c] = Achunk;
+}
+
+// Pass 2: thread (entry e, segment sg) of a 1024-thread workgroup covering 64
+// consecutive state entries of one row and 16 segments of its chunks.
+constexpr int kPassEntries = 64, kPassSegs = 16;
+__global__ __launch_bounds__(1024) void ssd_pass_kernel(SsdArgs a, int64_t PN) {
+  __shared__ float s_a[kPassSegs][kPassEntries], s_x[kPassSegs][kPassEntries];
+  const int el = threadIdx.x % kPassEntries;
+  const int sg = threadIdx.x / kPassEntries;
+  const int64_t nblk = (PN + kPassEntries - 1) / kPassEntries;
+  const int64_t row = blockIdx.x / nblk;
+  const int64_t e = (blockIdx.x - row * nblk) * kPassEntries + el;
+  const bool act = e < PN;
+  const int64_t nc = a.nchunks;
+  const int64_t seg = (nc + kPassSegs - 1) / kPassSegs;
+  const int64_t c0 = sg * seg, c1 = c0 + seg < nc ? c0 + seg : nc;
+  const float* cA = a.chunkA + row * nc;
+  const float* cX = a.chunkX + row * nc * PN + (act ? e : 0);
+  float A = 1.0f, X = 0.0f;
+  for (int64_t c = c0; c < c1; ++c) {
+    const float ac = cA[c];
+    X = __builtin_fmaf(ac, X, cX[c * PN]);
+    A *= ac;
+  }
+  s_a[sg][el] = A;
+  s_x[sg][el] = X;
+  __syncthreads();
+  float S = (act && a.h0) ? a.h0[row * PN + e] : 0.0f;
+  for (int k = 0; k < sg; ++k) S = __builtin_fmaf(s_a[k][el], S, s_x[k][el]);
+  float* en = a.entry + row * nc * PN + (act ? e : 0);
+  for (int64_t c = c0; c < c1; ++c) {
+    if (act) en[c * PN] = S;
+    S = __builtin_fmaf(cA[c], S, cX[c * PN]);
+  }
+  if (act && a.h_last && sg == kPassSegs - 1) a.h_last[row * PN + e] = S;
 }
 
 template <typename T, int DISC, int N, bool HAS_D>
-__global__ __launch_bounds__(256) void ssd_scan_kernel(SsdArgs a) {
-  extern __shared__ float s_mem[];
-  const int RUN = (int)a.run;
-  const int TC = RUN * kSsdWaves;
+__global__ __launch_bounds__(64) void ssd_out_kernel(SsdArgs a) {
+  __shared__ float s_ab[64], s_cf[64];
+  __shared__ __align__(16) float s_B[kSsdSub * N];
+  __shared__ __align__(16) float s_C[kSsdSub * N];
+  __shared__ float s_x[kSsdSub * 64];
+  const int lane = threadIdx.x;
   const int P = (int)a.P;
-  float* s_ab = s_mem;                         // [TC] decay per step
-  float* s_cf = s_ab + TC;                     // [TC] input coefficient per step
-  float* s_ra = s_cf + TC;                     // [4] run decay products
-  float* s_rx = s_ra + kSsdWaves;              // [4][P][N] run local states -> entry prefixes
-  float* s_carry = s_rx + kSsdWaves * P * N;   // [P][N] tile entry state
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int p = tid & 63;
-  const bool act = p < P;
-  const uint32_t c = blockIdx.x / a.rows;
-  const uint32_t row = blockIdx.x - c * a.rows;
-  const uint32_t b = row / a.H;
-  const uint32_t h = row - b * a.H;
-  const int64_t tile_t0 = (int64_t)c * TC;
+  const bool act = lane < P;
+  const uint32_t row = blockIdx.x / a.nchunks;
+  const uint32_t c = blockIdx.x - row * a.nchunks;
+  const uint32_t b = row / a.H, h = row - (row / a.H) * a.H;
   const float a2 = -expf(a.A_log[h]) * kLog2e;
-
-  // ---- per-step decay and input coefficient, once per tile
+  const int64_t tbeg = (int64_t)c * a.tc;
+  const int64_t tend = tbeg + a.tc < a.L ? tbeg + a.tc : a.L;
   const float* dtp = a.dt + b * a.sdt_b + h * a.sdt_h;
-  for (int i = tid; i < TC; i += blockDim.x) {
-    const int64_t t = tile_t0 + i;
-    const float d = t < a.L ? dtp[t * a.sdt_l] : 0.0f;
-    const float arg = d * a2;
-    const float ab = exp2_fast(arg);
-    s_ab[i] = ab;
-    s_cf[i] = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * d : d;
-  }
-  __syncthreads();
-
-  const int64_t t0 = tile_t0 + (int64_t)wave * RUN;
-  int nsteps = RUN;
-  if (t0 >= a.L) nsteps = 0;
-  else if (t0 + RUN > a.L) nsteps = (int)(a.L - t0);
-  const T* xp = reinterpret_cast<const T*>(a.x) + b * a.sx_b + h * a.sx_h + (act ? p : 0);
+  const T* xp = reinterpret_cast<const T*>(a.x) + b * a.sx_b + h * a.sx_h + (act ? lane : 0);
   const T* Bp = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h;
   const T* Cp = reinterpret_cast<const T*>(a.C) + b * a.sC_b + h * a.sC_h;
-  const float* ab_run = s_ab + wave * RUN;
-  const float* cf_run = s_cf + wave * RUN;
-
-  // ---- sweep 1: local state of the run from zero
-  float st[N];
-#pragma unroll
-  for (int n = 0; n < N; ++n) st[n] = 0.0f;
-  float A_run = 1.0f;
-  for (int i = 0; i < nsteps; ++i) {
-    const int64_t t = t0 + i;
-    const float ab = ab_run[i];
-    const float xs = cf_run[i] * ldf(xp + t * a.sx_l);
-    float bv[N];
-    load_row<T, N>(Bp + t * a.sB_l, bv);
-#pragma unroll
-    for (int n = 0; n < N; ++n) st[n] = __builtin_fmaf(ab, st[n], xs * bv[n]);
-    A_run *= ab;
-  }
-  if (act) {
-#pragma unroll
-    for (int n = 0; n < N; ++n) s_rx[(wave * P + p) * N + n] = st[n];
-  }
-  if (p == 0) s_ra[wave] = A_run;
-  __syncthreads();
-
-  // ---- combine runs: entry prefix of each run within the tile; the last
-  //      wave resolves the tile's carry
+  T* yp = reinterpret_cast<T*>(a.y) + b * a.sy_b + h * a.sy_h + (act ? lane : 0);
+  const int64_t PN = (int64_t)P * N;
+  float g[N];
   {
-    float PA = 1.0f;
-    float PX[N];
+    const float* en = a.entry + ((int64_t)row * a.nchunks + c) * PN + (int64_t)(act ? lane : 0) * N;
 #pragma unroll
-    for (int n = 0; n < N; ++n) PX[n] = 0.0f;
-    for (int w = 0; w < wave; ++w) {
-      const float wa = s_ra[w];
-#pragma unroll
-      for (int n = 0; n < N; ++n)
-        PX[n] = __builtin_fmaf(wa, PX[n], act ? s_rx[(w * P + p) * N + n] : 0.0f);
-      PA *= wa;
-    }
-    __syncthreads();  // every wave has read the run states it needs
-    if (act) {
-#pragma unroll
-      for (int n = 0; n < N; ++n) s_rx[(wave * P + p) * N + n] = PX[n];
-    }
-    if (wave == kSsdWaves - 1) {
-      // tile aggregate = (this run) o (prefix of earlier runs)
-      const float TA = A_run * PA;
-      float TX[N];
-#pragma unroll
-      for (int n = 0; n < N; ++n) TX[n] = __builtin_fmaf(A_run, PX[n], st[n]);
-      const int64_t cw = (int64_t)P * N;  // state words per tile
-      uint64_t* tile0 = a.words + (int64_t)row * a.nchunks * (2 * cw + 1);
-      // layout per tile: [agg_a (1)] [agg_x (cw)] [inc (cw)]
-      uint64_t* mine = tile0 + (int64_t)c * (2 * cw + 1);
-      if (c > 0 && act) {
-        if (p == 0) st_word(mine, TA, a.tag);
-#pragma unroll
-        for (int n = 0; n < N; ++n) st_word(mine + 1 + p * N + n, TX[n], a.tag);
-      }
-      float cin[N];
-#pragma unroll
-      for (int n = 0; n < N; ++n) cin[n] = (a.h0 && act) ? a.h0[((int64_t)row * P + p) * N + n] : 0.0f;
-      if (c > 0 && act) {
-        // walk back: all N words of a predecessor must carry the tag
-        float Aacc = 1.0f, Xacc[N];
-#pragma unroll
-        for (int n = 0; n < N; ++n) Xacc[n] = 0.0f;
-        int64_t j = (int64_t)c - 1;
-        uint32_t spins = 0;
-        bool done = false;
-        while (j >= 0 && !done) {
-          const uint64_t* pj = tile0 + j * (2 * cw + 1);
-          uint64_t wi[N], wx[N];
-          const uint64_t wa = ld_word(pj);
-#pragma unroll
-          for (int n = 0; n < N; ++n) {
-            wi[n] = ld_word(pj + 1 + cw + p * N + n);
-            wx[n] = ld_word(pj + 1 + p * N + n);
-          }
-          bool inc_ok = true, agg_ok = word_tag(wa) == a.tag;
-#pragma unroll
-          for (int n = 0; n < N; ++n) {
-            inc_ok = inc_ok && word_tag(wi[n]) == a.tag;
-            agg_ok = agg_ok && word_tag(wx[n]) == a.tag;
-          }
-          if (inc_ok) {
-#pragma unroll
-            for (int n = 0; n < N; ++n) cin[n] = __builtin_fmaf(Aacc, word_val(wi[n]), Xacc[n]);
-            done = true;
-          } else if (agg_ok) {
-            const float ja = word_val(wa);
-#pragma unroll
-            for (int n = 0; n < N; ++n) Xacc[n] = __builtin_fmaf(Aacc, word_val(wx[n]), Xacc[n]);
-            Aacc *= ja;
-            --j;
-          } else {
-            if (++spins > a.spin_limit) {
-              flag_error(a.hdr);
-#pragma unroll
-              for (int n = 0; n < N; ++n) cin[n] = Xacc[n];
-              done = true;
-            } else {
-              __builtin_amdgcn_s_sleep(1);
-            }
-          }
-        }
-        if (!done) {  // reached the row start: fold h0
-#pragma unroll
-          for (int n = 0; n < N; ++n) cin[n] = __builtin_fmaf(Aacc, cin[n], Xacc[n]);
-        }
-      }
-      if (act) {
-#pragma unroll
-        for (int n = 0; n < N; ++n) {
-          const float incl = __builtin_fmaf(TA, cin[n], TX[n]);
-          st_word(mine + 1 + cw + p * N + n, incl, a.tag);
-          s_carry[p * N + n] = cin[n];
-          if (a.h_last && c == a.nchunks - 1) a.h_last[((int64_t)row * P + p) * N + n] = incl;
-        }
-      }
-    }
-    __syncthreads();
-    // entry state of this run = prefix o carry
-    if (act) {
-#pragma unroll
-      for (int n = 0; n < N; ++n)
-        st[n] = __builtin_fmaf(PA, s_carry[p * N + n], s_rx[(wave * P + p) * N + n]);
-    }
+    for (int n = 0; n < N; ++n) g[n] = act ? en[n] : 0.0f;
   }
-
-  // ---- sweep 2: rescan the run from its exact entry state, write y
-  const float dv = (HAS_D && act) ? a.D[h * P + p] : 0.0f;
-  T* yp = reinterpret_cast<T*>(a.y) + b * a.sy_b + h * a.sy_h + p;
-  for (int i = 0; i < nsteps; ++i) {
-    const int64_t t = t0 + i;
-    const float ab = ab_run[i];
-    const float xv = ldf(xp + t * a.sx_l);
-    const float xs = cf_run[i] * xv;
-    float bv[N], cv[N];
-    load_row<T, N>(Bp + t * a.sB_l, bv);
-    load_row<T, N>(Cp + t * a.sC_l, cv);
-    float acc = HAS_D ? dv * xv : 0.0f;
+  const float dv = (HAS_D && act) ? a.D[h * P + lane] : 0.0f;
+  float Pt = 1.0f;
+  for (int64_t t0 = tbeg; t0 < tend; t0 += 64) {
+    step_scalars<DISC>(dtp, a.sdt_l, t0, a.L, a2, s_ab, s_cf, lane);
+    for (int j = 0; j < 64 && t0 + j < tend; j += kSsdSub) {
+      const int64_t ts = t0 + j;
+      stage_x<T>(xp, a.sx_l, ts, a.L, act, s_x, lane);
+      stage_rows<T, N>(Bp, a.sB_l, ts, a.L, s_B, lane);
+      stage_rows<T, N>(Cp, a.sC_l, ts, a.L, s_C, lane);
+      __syncthreads();
+      const int m = a.L - ts < kSsdSub ? (int)(a.L - ts) : kSsdSub;
+#pragma unroll 2
+      for (int i = 0; i < kSsdSub; ++i) {
+        const float xv = s_x[i * 64 + lane];
+        float bv[N];
 #pragma unroll
-    for (int n = 0; n < N; ++n) {
-      st[n] = __builtin_fmaf(ab, st[n], xs * bv[n]);
-      acc = __builtin_fmaf(cv[n], st[n], acc);
+        for (int n = 0; n < N; ++n) bv[n] = s_B[i * N + n];
+        rescaled_step<N>(g, Pt, s_ab[j + i], s_cf[j + i] * xv, bv);
+        float acc = 0.0f;
+#pragma unroll
+        for (int n = 0; n < N; ++n) acc = __builtin_fmaf(s_C[i * N + n], g[n], acc);
+        acc *= Pt;
+        if (HAS_D) acc = __builtin_fmaf(dv, xv, acc);
+        if (act && i < m) stf(yp + (ts + i) * a.sy_l, acc);
+      }
+      __syncthreads();
     }
-    if (act) stf(yp + t * a.sy_l, acc);
   }
 }
 
@@ -304,32 +307,43 @@ __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
 
 inline int64_t cdiv64(int64_t x, int64_t y) { return (x + y - 1) / y; }
 
-template <typename T, int DISC, bool HAS_D>
-int launch_ssd_n(int N, dim3 grid, size_t lds, hipStream_t s, const SsdArgs& a) {
-  switch (N) {
-    case 8: hipLaunchKernelGGL((ssd_scan_kernel<T, DISC, 8, HAS_D>), grid, dim3(256), lds, s, a); break;
-    case 16: hipLaunchKernelGGL((ssd_scan_kernel<T, DISC, 16, HAS_D>), grid, dim3(256), lds, s, a); break;
-    case 32: hipLaunchKernelGGL((ssd_scan_kernel<T, DISC, 32, HAS_D>), grid, dim3(256), lds, s, a); break;
-    default: return TSSM_ERR_UNSUPPORTED;
-  }
+template <typename T, int DISC, int N, bool HAS_D>
+int launch_ssd_passes(int64_t rows, int64_t nchunks, int64_t PN, hipStream_t s, const SsdArgs& a) {
+  const dim3 tiles((unsigned)(rows * nchunks));
+  hipLaunchKernelGGL((ssd_state_kernel<T, DISC, N>), tiles, dim3(64), 0, s, a);
+  const int64_t nblk = (PN + kPassEntries - 1) / kPassEntries;
+  hipLaunchKernelGGL(ssd_pass_kernel, dim3((unsigned)(rows * nblk)), dim3(kPassEntries * kPassSegs),
+                     0, s, a, PN);
+  hipLaunchKernelGGL((ssd_out_kernel<T, DISC, N, HAS_D>), tiles, dim3(64), 0, s, a);
   return launch_status();
 }
 
-template <typename T>
-int launch_ssd_t(int disc, bool has_d, int N, dim3 grid, size_t lds, hipStream_t s,
-                 const SsdArgs& a) {
-  if (disc == TSSM_DISC_ZOH)
-    return has_d ? launch_ssd_n<T, TSSM_DISC_ZOH, true>(N, grid, lds, s, a)
-                 : launch_ssd_n<T, TSSM_DISC_ZOH, false>(N, grid, lds, s, a);
-  return has_d ? launch_ssd_n<T, TSSM_DISC_EULER, true>(N, grid, lds, s, a)
-               : launch_ssd_n<T, TSSM_DISC_EULER, false>(N, grid, lds, s, a);
+template <typename T, int DISC, bool HAS_D>
+int launch_ssd_n(int N, int64_t rows, int64_t nchunks, int64_t PN, hipStream_t s, const SsdArgs& a) {
+  switch (N) {
+    case 8: return launch_ssd_passes<T, DISC, 8, HAS_D>(rows, nchunks, PN, s, a);
+    case 16: return launch_ssd_passes<T, DISC, 16, HAS_D>(rows, nchunks, PN, s, a);
+    case 32: return launch_ssd_passes<T, DISC, 32, HAS_D>(rows, nchunks, PN, s, a);
+    default: return TSSM_ERR_UNSUPPORTED;
+  }
 }
 
-inline int ssd_run(int64_t chunk) {
-  int64_t run = chunk / kSsdWaves;
-  if (run < 16) run = 16;
-  if (run > 256) run = 256;
-  return (int)run;
+template <typename T>
+int launch_ssd_t(int disc, bool has_d, int N, int64_t rows, int64_t nchunks, int64_t PN,
+                 hipStream_t s, const SsdArgs& a) {
+  if (disc == TSSM_DISC_ZOH)
+    return has_d ? launch_ssd_n<T, TSSM_DISC_ZOH, true>(N, rows, nchunks, PN, s, a)
+                 : launch_ssd_n<T, TSSM_DISC_ZOH, false>(N, rows, nchunks, PN, s, a);
+  return has_d ? launch_ssd_n<T, TSSM_DISC_EULER, true>(N, rows, nchunks, PN, s, a)
+               : launch_ssd_n<T, TSSM_DISC_EULER, false>(N, rows, nchunks, PN, s, a);
+}
+
+// Steps per chunk: the `chunk` hint rounded to a multiple of 64 in [64, 1024].
+inline int64_t ssd_tc(int64_t chunk) {
+  int64_t tc = (chunk + 63) / 64 * 64;
+  if (tc < 64) tc = 64;
+  if (tc > 1024) tc = 1024;
+  return tc;
 }
 
 }  // namespace tssm
@@ -339,9 +353,10 @@ using namespace tssm;
 extern "C" int64_t tssm_ssd_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t H, int64_t P,
                                                  int64_t N, int64_t chunk) {
   if (nbatch <= 0 || L <= 0 || H <= 0 || P <= 0 || P > 64 || N <= 0) return -1;
-  const int64_t tc = (int64_t)ssd_run(chunk) * kSsdWaves;
-  const int64_t nchunks = cdiv64(L, tc);
-  return (int64_t)sizeof(WsHeader) + nbatch * H * nchunks * (2 * P * N + 1) * 8;
+  const int64_t nchunks = cdiv64(L, ssd_tc(chunk));
+  const int64_t rows = nbatch * H;
+  // chunk decay products + chunk end states + chunk entry states (fp32)
+  return (rows * nchunks * (1 + 2 * P * N)) * 4 + 256;
 }
 
 extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt,
@@ -364,9 +379,10 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
   const int64_t strides[] = {sx_b, sx_l, sx_h, sdt_b, sdt_l, sdt_h, sB_b, sB_l, sB_h,
                              sC_b, sC_l, sC_h, sy_b, sy_l, sy_h};
   for (int64_t s : strides) TSSM_CHECK(s >= 0, TSSM_ERR_STRIDE);
-  const int run = ssd_run(chunk);
-  const int64_t nchunks = cdiv64(L, (int64_t)run * kSsdWaves);
+  const int64_t tc = ssd_tc(chunk);
+  const int64_t nchunks = cdiv64(L, tc);
   const int64_t rows = nbatch * H;
+  const int64_t PN = P * N;
   TSSM_CHECK(nchunks * rows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
   SsdArgs a;
   a.x = x; a.dt = dt; a.A_log = A_log; a.B = B; a.C = C; a.D = D; a.h0 = h0; a.y = y;
@@ -374,20 +390,20 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
   a.sx_b = sx_b; a.sx_l = sx_l; a.sx_h = sx_h; a.sdt_b = sdt_b; a.sdt_l = sdt_l; a.sdt_h = sdt_h;
   a.sB_b = sB_b; a.sB_l = sB_l; a.sB_h = sB_h; a.sC_b = sC_b; a.sC_l = sC_l; a.sC_h = sC_h;
   a.sy_b = sy_b; a.sy_l = sy_l; a.sy_h = sy_h;
-  a.hdr = reinterpret_cast<WsHeader*>(workspace);
-  a.words = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + sizeof(WsHeader));
+  // The first 256 bytes are the workspace header (sticky error word) shared
+  // with the look-back kernels; the three passes use what follows.
+  float* ws = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + 256);
+  a.chunkX = ws;
+  a.entry = ws + rows * nchunks * PN;
+  a.chunkA = ws + 2 * rows * nchunks * PN;
   a.H = (uint32_t)H; a.P = (uint32_t)P; a.rows = (uint32_t)rows; a.nchunks = (uint32_t)nchunks;
-  a.run = (uint32_t)run; a.tag = next_epoch(workspace); a.spin_limit = kDefaultSpinLimit;
-  const size_t lds = ((size_t)2 * run * kSsdWaves + kSsdWaves + (size_t)(kSsdWaves + 1) * P * N) *
-                     sizeof(float);
-  TSSM_CHECK(lds <= 65536, TSSM_ERR_UNSUPPORTED);
-  const dim3 grid((unsigned)(nchunks * rows));
+  a.tc = (uint32_t)tc;
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr;
   switch (dtype) {
-    case TSSM_BF16: return launch_ssd_t<bf16_t>(disc, has_d, (int)N, grid, lds, s, a);
-    case TSSM_F16: return launch_ssd_t<f16_t>(disc, has_d, (int)N, grid, lds, s, a);
-    default: return launch_ssd_t<float>(disc, has_d, (int)N, grid, lds, s, a);
+    case TSSM_BF16: return launch_ssd_t<bf16_t>(disc, has_d, (int)N, rows, nchunks, PN, s, a);
+    case TSSM_F16: return launch_ssd_t<f16_t>(disc, has_d, (int)N, rows, nchunks, PN, s, a);
+    default: return launch_ssd_t<float>(disc, has_d, (int)N, rows, nchunks, PN, s, a);
   }
 }
 
