@@ -61,6 +61,36 @@ int tssm_zoh_discretize(int b_dtype, int out_dtype, const float* A_log, const vo
                         int64_t sB_b, int64_t sB_t, int64_t sdt_b, int64_t sdt_t, int64_t sa_b,
                         int64_t sa_t, int64_t sb_b, int64_t sb_t, void* stream);
 
+/* zoh_discretize_bwd_kernel (discretize_kernel.py:98-162).  Same grid and
+ * strides as the forward (dB uses B's strides, dAbar Abar's, dBbar Bbar's,
+ * ddt dt's).  dA [H] f32 is ACCUMULATED into (the reference's atomic_add at
+ * :156); ddt [B,T] f32 is overwritten with the sum over the covered lanes (the
+ * intent of the store/atomic pair at :159-162).  Deterministic: partial sums
+ * go through a caller workspace of tssm_zoh_discretize_bwd_workspace_bytes()
+ * bytes (no clearing needed) and are reduced in a fixed order.  B, Abar,
+ * dAbar, dBbar and dB share `dtype`; A_log, dt, dA and ddt are f32. */
+int64_t tssm_zoh_discretize_bwd_workspace_bytes(int64_t grid_b, int64_t grid_t, int64_t h_cover);
+int tssm_zoh_discretize_bwd(int dtype, const float* A_log, const void* B, const float* dt,
+                            const void* Abar, const void* dAbar, const void* dBbar, float* dA,
+                            void* dB, float* ddt, int64_t nbatch, int64_t T, int64_t H,
+                            int64_t grid_b, int64_t grid_t, int64_t h_cover, int64_t sB_b,
+                            int64_t sB_t, int64_t sdt_b, int64_t sdt_t, int64_t sa_b,
+                            int64_t sa_t, int64_t sb_b, int64_t sb_t, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/* dt_project_softplus_kernel (discretize_kernel.py:166-213; the scalar index
+ * of a block tensor at :203 implemented as its evident intent):
+ * dt_out[b,t,h] = clamp(softplus(sum_r dt_raw[b,t,r] W[r,h] + bias[h]),
+ * dt_min, dt_max) for b < grid_b, t < grid_t, h < h_cover.  dt_raw [B,T,rank]
+ * (strides sr_b, sr_t, unit over r), W [rank,H] (row stride sw_r, unit over h),
+ * bias [H], all f32; dt_out in out_dtype with strides so_b, so_t, unit over h. */
+int tssm_dt_project_softplus(int out_dtype, const float* dt_raw, const float* W,
+                             const float* bias, void* dt_out, int64_t nbatch, int64_t T,
+                             int64_t H, int64_t rank, int64_t grid_b, int64_t grid_t,
+                             int64_t h_cover, int64_t sr_b, int64_t sr_t, int64_t sw_r,
+                             int64_t so_b, int64_t so_t, float dt_min, float dt_max,
+                             void* stream);
+
 /* ------------------------------------------------------------------ elementwise scan
  * ssm_scan.py phase kernels; u, A, B, C, D, h, y, loc_*, carry all in `dtype`,
  * contiguous [B, L, H] (the reference computes offsets b*L*H + t*H + h).

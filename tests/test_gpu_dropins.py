@@ -56,6 +56,84 @@ def test_zoh_discretize_partial_grid(dev):
     assert torch.all(Abar[0, 2:] == -7.0)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(3, 50, 200, 64), (2, 70, 300, 128), (1, 3, 5, 4)])
+def test_zoh_discretize_bwd(dev, dtype, shape):
+    """zoh_discretize_bwd_kernel[grid](...) against the float64 oracle (itself
+    pinned by torch.autograd): dA accumulates into its input, ddt is the full
+    lane sum, dB elementwise.  Tiny dt*a exercises the cancellation-free psi."""
+    import discretize_kernel as dk
+    Bsz, T, H, BLOCK_H = shape
+    g = torch.Generator().manual_seed(sum(shape))
+    A = torch.empty(H).uniform_(np.log(0.5), np.log(5.0), generator=g).to(dev)
+    B = torch.randn(Bsz, T, H, generator=g).to(dtype).to(dev)
+    dt = torch.exp(torch.empty(Bsz, T).uniform_(np.log(1e-6), np.log(2.0), generator=g)).to(dev)
+    Abar = torch.exp(dt[..., None] * -torch.exp(A)).to(dtype)
+    dAbar = torch.randn(Bsz, T, H, generator=g).to(dtype).to(dev)
+    dBbar = torch.randn(Bsz, T, H, generator=g).to(dtype).to(dev)
+    dA0 = torch.randn(H, generator=g).to(dev)
+    dA = dA0.clone()
+    dB = torch.empty_like(B)
+    ddt = torch.full((Bsz, T), 123.0, device=dev)
+    dk.zoh_discretize_bwd_kernel[(Bsz, T, (H + BLOCK_H - 1) // BLOCK_H)](
+        A, B, dt, Abar, dAbar, dBbar, dA, dB, ddt, Bsz, T, H, *B.stride(), *dt.stride(),
+        *Abar.stride(), *dBbar.stride(), BLOCK_H=BLOCK_H)
+    torch.cuda.synchronize()
+    dA_r, dB_r, ddt_r = O.zoh_discretize_bwd(A, B, dt, Abar, dAbar, dBbar)
+    tol = 1e-5 if dtype == torch.float32 else TOL[dtype]
+    assert_close(dA - dA0, dA_r, tol, "dA_log (accumulated)")
+    assert_close(dB, dB_r, tol, "dB")
+    assert_close(ddt, ddt_r, tol, "ddt")
+    # deterministic (fixed reduction order, no atomics): a repeat is bitwise equal
+    dA2, ddt2 = dA0.clone(), torch.zeros_like(ddt)
+    dk.zoh_discretize_bwd_kernel[(Bsz, T, (H + BLOCK_H - 1) // BLOCK_H)](
+        A, B, dt, Abar, dAbar, dBbar, dA2, dB, ddt2, Bsz, T, H, *B.stride(), *dt.stride(),
+        *Abar.stride(), *dBbar.stride(), BLOCK_H=BLOCK_H)
+    torch.cuda.synchronize()
+    assert torch.equal(dA2, dA) and torch.equal(ddt2, ddt)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 33, 300, 16, 64, 8), (3, 20, 64, 5, 32, 4),
+                                   (1, 7, 1000, 48, 256, 16)])
+def test_dt_project_softplus(dev, out_dtype, shape):
+    """dt_project_softplus_kernel[grid](...) against the oracle (softplus+clamp
+    pinned to torch in float64); the clamp bounds are hit on purpose."""
+    import discretize_kernel as dk
+    Bsz, T, H, R, BLOCK_H, BLOCK_R = shape
+    g = torch.Generator().manual_seed(H + R)
+    raw = (3.0 * torch.randn(Bsz, T, R, generator=g)).to(dev)
+    W = (torch.randn(R, H, generator=g) / R ** 0.5).to(dev)
+    bias = torch.randn(H, generator=g).to(dev)
+    out = torch.full((Bsz, T, H), -1.0, device=dev, dtype=out_dtype)
+    DT_MIN, DT_MAX = 1e-3, 2.5
+    dk.dt_project_softplus_kernel[(Bsz, T, (H + BLOCK_H - 1) // BLOCK_H)](
+        raw, W, bias, out, Bsz, T, H, R, *raw.stride(), *W.stride(), *out.stride(),
+        DT_MIN=DT_MIN, DT_MAX=DT_MAX, BLOCK_H=BLOCK_H, BLOCK_R=BLOCK_R)
+    torch.cuda.synchronize()
+    ref = O.dt_project_softplus(raw, W, bias, DT_MIN, DT_MAX)
+    assert (ref == DT_MAX).any() and (ref == DT_MIN).any()
+    assert_close(out, ref, TOL[out_dtype], "dt")
+    if out_dtype == torch.float32:
+        rel = np.abs(np64(out) - ref) / ref
+        assert rel.max() < 1e-5
+
+
+def test_dt_project_partial_grid(dev):
+    import discretize_kernel as dk
+    Bsz, T, H, R = 2, 5, 70, 3
+    raw = torch.randn(Bsz, T, R, device=dev)
+    W = torch.randn(R, H, device=dev)
+    bias = torch.zeros(H, device=dev)
+    out = torch.full((Bsz, T, H), -1.0, device=dev)
+    dk.dt_project_softplus_kernel[(1, 3, 1)](
+        raw, W, bias, out, Bsz, T, H, R, *raw.stride(), *W.stride(), *out.stride(),
+        DT_MIN=0.0, DT_MAX=100.0, BLOCK_H=32, BLOCK_R=4)
+    torch.cuda.synchronize()
+    assert torch.all(out[0, :3, :32] >= 0) and torch.all(out[0, :3, 32:] == -1.0)
+    assert torch.all(out[0, 3:] == -1.0) and torch.all(out[1] == -1.0)
+
+
 # ------------------------------------------------------------------ elementwise scan
 @pytest.mark.parametrize("BLK", [16, 64, 256])
 def test_ssm_forward_backward(dev, BLK):

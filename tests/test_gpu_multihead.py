@@ -86,6 +86,27 @@ def test_fused_split_resume_and_repeat(dev):
         assert torch.equal(y_again, y)
 
 
+def test_fused_forgetting_tiles(dev):
+    """Tiles whose decay product underflows to zero publish their state before
+    looking back; rows mixing such tiles with slowly decaying ones (and a
+    nonzero h0) must still match the sequential oracle."""
+    from tssm import multihead_ssm_forward
+    Bsz, L, nh, hd = 2, 1100, 4, 64
+    d = _inputs(dev, Bsz, L, nh, hd, torch.float32, seed=21, per_head=True)
+    chunk_id = torch.arange(L, device=dev) // 128
+    strong = (chunk_id % 3 == 0).view(1, L, 1)
+    d["dt"] = torch.where(strong, torch.full_like(d["dt"], 5.0), torch.full_like(d["dt"], 1e-3))
+    d["A_log"] = torch.tensor([np.log(16.0), np.log(0.01), 0.0, np.log(4.0)],
+                              dtype=torch.float32, device=dev)
+    h0 = torch.randn(Bsz, nh, hd, device=dev)
+    y, hl = multihead_ssm_forward(d["u"], d["A_log"], d["B"], d["C"], d["dt"], d["D"],
+                                  disc="zoh", chunk=128, h0=h0, return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = _oracle(d, "zoh", h0=h0)
+    assert_close(y, y_ref, TOL[torch.float32], "y, mixed forgetting tiles")
+    assert_close(hl, h_ref, TOL[torch.float32], "h_last, mixed forgetting tiles")
+
+
 @pytest.mark.parametrize("disc", ["euler", "zoh"])
 def test_fused_full_headline_shape(dev, disc):
     """B=8 L=4096 H=16 P=N=64 bf16 x/B/C, fp32 dt and state (the measured workload)."""

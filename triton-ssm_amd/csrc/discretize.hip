@@ -73,3 +73,272 @@ extern "C" int tssm_zoh_discretize(int b_dtype, int out_dtype, const float* A_lo
 #undef TSSM_ZOH
   return launch_status();
 }
+
+// ---------------------------------------------------------------- backward
+// zoh_discretize_bwd_kernel (discretize_kernel.py:98-162), deterministic:
+// the reference adds dA_log with atomics over (b, t) and makes ddt a race
+// between a store (hblk 0) and atomics (:156-162).  Here
+//   pass 1: workgroup (lane block of LB lanes, group of RG rows r = b*grid_t+t)
+//           writes dB, a per-lane partial of dA_log over its rows and, per
+//           row, the partial of ddt over its lanes (wave sums + one LDS pass);
+//   pass 2: dA[h] += sum of the row-group partials, ddt[r] = sum of the lane-
+//           block partials, both in a fixed order.
+// The partials live in a caller workspace: [n_rg][hc] then [n_lb][nrows] f32.
+namespace tssm {
+
+constexpr int kBwdLanes = 256;   // lanes per workgroup (threads)
+constexpr int kBwdRows = 64;     // rows per workgroup
+
+// psi(x) = (x e^x - expm1(x)) / x^2 = sum_k x^k (k+1)/(k+2)!, the factor of
+// d/da [expm1(dt a)/a] = dt^2 psi(dt a).  Series below |x| < 0.5 (the direct
+// form cancels there), direct above.
+__device__ inline float psi_from_exp(float x, float ex, float em1) {
+  float p = 10.0f / 39916800.0f;
+  p = __builtin_fmaf(p, x, 9.0f / 3628800.0f);
+  p = __builtin_fmaf(p, x, 8.0f / 362880.0f);
+  p = __builtin_fmaf(p, x, 7.0f / 40320.0f);
+  p = __builtin_fmaf(p, x, 6.0f / 5040.0f);
+  p = __builtin_fmaf(p, x, 5.0f / 720.0f);
+  p = __builtin_fmaf(p, x, 4.0f / 120.0f);
+  p = __builtin_fmaf(p, x, 3.0f / 24.0f);
+  p = __builtin_fmaf(p, x, 2.0f / 6.0f);
+  p = __builtin_fmaf(p, x, 0.5f);
+  const float direct = (x * ex - em1) / (x * x);
+  return __builtin_fabsf(x) < 0.5f ? p : direct;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBwdLanes) void zoh_bwd_pass1_kernel(
+    const float* __restrict__ A_log, const T* __restrict__ B, const float* __restrict__ dt,
+    const T* __restrict__ Abar, const T* __restrict__ dAbar, const T* __restrict__ dBbar,
+    T* __restrict__ dB, float* __restrict__ part_dA, float* __restrict__ part_ddt, int64_t grid_t,
+    int64_t nrows, int64_t hc, int64_t sB_b, int64_t sB_t, int64_t sdt_b, int64_t sdt_t,
+    int64_t sa_b, int64_t sa_t, int64_t sb_b, int64_t sb_t) {
+  __shared__ float red[kBwdRows][kBwdLanes / 64];
+  const int lb = blockIdx.x, rg = blockIdx.y;
+  const int64_t h = (int64_t)lb * blockDim.x + threadIdx.x;
+  const bool act = h < hc;
+  const int nw = blockDim.x >> 6;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float neg_a = 0.0f, a = 0.0f;
+  if (act) {
+    neg_a = exp_acc(A_log[h]);
+    a = -neg_a;
+  }
+  float acc_dA = 0.0f;
+  const int64_t r0 = (int64_t)rg * kBwdRows;
+  for (int k = 0; k < kBwdRows; ++k) {
+    const int64_t r = r0 + k;
+    if (r >= nrows) break;  // uniform over the workgroup
+    const int64_t b = r / grid_t, t = r - b * grid_t;
+    float ddt = 0.0f;
+    if (act) {
+      const float d = dt[b * sdt_b + t * sdt_t];
+      const float bv = ldf(B + b * sB_b + t * sB_t + h);
+      const float ab = ldf(Abar + b * sa_b + t * sa_t + h);
+      const float gA = ldf(dAbar + b * sa_b + t * sa_t + h);
+      const float gB = ldf(dBbar + b * sb_b + t * sb_t + h);
+      const float x = d * a;
+      const float ex = exp_acc(x);
+      const float em1 = expm1_acc(x, ex);
+      ddt = gA * a * ab + gB * ex * bv;                           // :130-140
+      const float aa = a * a;
+      const float num = d * d * psi_from_exp(x, ex, em1) * (aa / (aa + 1e-18f));  // :146
+      const float da = gA * d * ab + gB * num * bv;                // :143-148
+      acc_dA = __builtin_fmaf(da, -neg_a, acc_dA);                 // :151, summed at :156
+      stf(dB + b * sB_b + t * sB_t + h, gB * em1 / (a + 1e-12f));  // :154, :157
+    }
+    for (int o = 32; o > 0; o >>= 1) ddt += __shfl_xor(ddt, o);
+    if (lane == 0) red[k][wave] = ddt;
+  }
+  if (act) part_dA[(int64_t)rg * hc + h] = acc_dA;
+  __syncthreads();
+  if (threadIdx.x < kBwdRows) {
+    const int64_t r = r0 + threadIdx.x;
+    if (r < nrows) {
+      float s = 0.0f;
+      for (int w = 0; w < nw; ++w) s += red[threadIdx.x][w];
+      part_ddt[(int64_t)lb * nrows + r] = s;
+    }
+  }
+}
+
+__global__ void zoh_bwd_pass2_kernel(const float* __restrict__ part_dA,
+                                     const float* __restrict__ part_ddt, float* __restrict__ dA,
+                                     float* __restrict__ ddt, int64_t grid_t, int64_t nrows,
+                                     int64_t hc, int64_t n_rg, int64_t n_lb, int64_t sdt_b,
+                                     int64_t sdt_t) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < hc) {
+    float s = 0.0f;
+    for (int64_t g = 0; g < n_rg; ++g) s += part_dA[g * hc + i];
+    dA[i] += s;
+  } else if (i < hc + nrows) {
+    const int64_t r = i - hc;
+    float s = 0.0f;
+    for (int64_t g = 0; g < n_lb; ++g) s += part_ddt[g * nrows + r];
+    const int64_t b = r / grid_t, t = r - b * grid_t;
+    ddt[b * sdt_b + t * sdt_t] = s;
+  }
+}
+
+inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace tssm
+
+extern "C" int64_t tssm_zoh_discretize_bwd_workspace_bytes(int64_t grid_b, int64_t grid_t,
+                                                           int64_t h_cover) {
+  if (grid_b < 0 || grid_t < 0 || h_cover < 0) return -1;
+  const int64_t nrows = grid_b * grid_t;
+  const int64_t n_rg = cdiv64(nrows, kBwdRows), n_lb = cdiv64(h_cover, kBwdLanes);
+  return (n_rg * h_cover + n_lb * nrows) * (int64_t)sizeof(float);
+}
+
+extern "C" int tssm_zoh_discretize_bwd(int dtype, const float* A_log, const void* B,
+                                       const float* dt, const void* Abar, const void* dAbar,
+                                       const void* dBbar, float* dA, void* dB, float* ddt,
+                                       int64_t nbatch, int64_t T, int64_t H, int64_t grid_b,
+                                       int64_t grid_t, int64_t h_cover, int64_t sB_b,
+                                       int64_t sB_t, int64_t sdt_b, int64_t sdt_t, int64_t sa_b,
+                                       int64_t sa_t, int64_t sb_b, int64_t sb_t, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(A_log && B && dt && Abar && dAbar && dBbar && dA && dB && ddt, TSSM_ERR_NULL);
+  TSSM_CHECK(nbatch >= 0 && T >= 0 && H >= 0 && grid_b >= 0 && grid_t >= 0 && h_cover >= 0,
+             TSSM_ERR_SHAPE);
+  TSSM_CHECK(grid_b <= nbatch && grid_t <= T && h_cover <= H, TSSM_ERR_SHAPE);
+  const int64_t nrows = grid_b * grid_t;
+  if (nrows == 0) return TSSM_OK;
+  const int64_t need = tssm_zoh_discretize_bwd_workspace_bytes(grid_b, grid_t, h_cover);
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  const int64_t n_rg = cdiv64(nrows, kBwdRows);
+  const int64_t n_lb = h_cover == 0 ? 1 : cdiv64(h_cover, kBwdLanes);
+  TSSM_CHECK(n_rg <= 65535, TSSM_ERR_UNSUPPORTED);
+  float* part_dA = reinterpret_cast<float*>(workspace);
+  float* part_ddt = part_dA + n_rg * h_cover;
+  const hipStream_t s = as_stream(stream);
+  if (h_cover == 0) {  // no lanes: ddt is the empty sum
+    const int64_t n = nrows;
+    hipLaunchKernelGGL(zoh_bwd_pass2_kernel, dim3((unsigned)cdiv64(n, 256)), dim3(256), 0, s,
+                       part_dA, part_ddt, dA, ddt, grid_t, nrows, (int64_t)0, n_rg, (int64_t)0,
+                       sdt_b, sdt_t);
+    return launch_status();
+  }
+  const int threads = h_cover >= kBwdLanes ? kBwdLanes : (int)(cdiv64(h_cover, 64) * 64);
+  const dim3 grid1((unsigned)n_lb, (unsigned)n_rg);
+#define TSSM_ZOH_BWD(TT)                                                                       \
+  hipLaunchKernelGGL(zoh_bwd_pass1_kernel<TT>, grid1, dim3(threads), 0, s, A_log,             \
+                     (const TT*)B, dt, (const TT*)Abar, (const TT*)dAbar, (const TT*)dBbar,    \
+                     (TT*)dB, part_dA, part_ddt, grid_t, nrows, h_cover, sB_b, sB_t, sdt_b,    \
+                     sdt_t, sa_b, sa_t, sb_b, sb_t)
+  switch (dtype) {
+    case TSSM_F32: TSSM_ZOH_BWD(float); break;
+    case TSSM_BF16: TSSM_ZOH_BWD(bf16_t); break;
+    case TSSM_F16: TSSM_ZOH_BWD(f16_t); break;
+    default: return TSSM_ERR_DTYPE;
+  }
+#undef TSSM_ZOH_BWD
+  int st = launch_status();
+  if (st != TSSM_OK) return st;
+  const int64_t n2 = h_cover + nrows;
+  hipLaunchKernelGGL(zoh_bwd_pass2_kernel, dim3((unsigned)cdiv64(n2, 256)), dim3(256), 0, s,
+                     part_dA, part_ddt, dA, ddt, grid_t, nrows, h_cover, n_rg, n_lb, sdt_b, sdt_t);
+  return launch_status();
+}
+
+// ---------------------------------------------------------------- dt projection
+// dt_project_softplus_kernel (discretize_kernel.py:166-213, evident intent of
+// :203): dt[b,t,h] = clamp(softplus(sum_r dt_raw[b,t,r] W[r,h] + bias[h]),
+// DT_MIN, DT_MAX).  Workgroup = (lane block of 256 lanes h, group of 16 rows
+// (b,t)); each thread keeps 8 rows of W for its lane in registers while the
+// rows' dt_raw values (uniform over the workgroup) are broadcast, so W is read
+// once per workgroup and dt_raw once per lane block.  Softplus is evaluated as
+// max(x,0) + log1p(exp(-|x|)), equal to log(1+exp(x)) wherever that is finite;
+// the clamp makes the overflow case agree too.
+namespace tssm {
+
+constexpr int kDtRows = 16;
+constexpr int kDtRank = 8;
+
+template <typename TO>
+__global__ __launch_bounds__(256) void dt_project_kernel(
+    const float* __restrict__ raw, const float* __restrict__ W, const float* __restrict__ bias,
+    TO* __restrict__ out, int64_t grid_t, int64_t nrows, int64_t hc, int64_t rank,
+    int64_t sr_b, int64_t sr_t, int64_t sw_r, int64_t so_b, int64_t so_t, float dt_min,
+    float dt_max) {
+  const int64_t h = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool act = h < hc;
+  const int64_t r0 = (int64_t)blockIdx.y * kDtRows;
+  const int nr = (int)((nrows - r0) < kDtRows ? (nrows - r0) : kDtRows);
+  int64_t roff[kDtRows];
+#pragma unroll
+  for (int k = 0; k < kDtRows; ++k) {
+    const int64_t r = r0 + (k < nr ? k : 0);
+    const int64_t b = r / grid_t, t = r - b * grid_t;
+    roff[k] = b * sr_b + t * sr_t;
+  }
+  float acc[kDtRows];
+#pragma unroll
+  for (int k = 0; k < kDtRows; ++k) acc[k] = 0.0f;
+  for (int64_t q0 = 0; q0 < rank; q0 += kDtRank) {
+    float w[kDtRank];
+#pragma unroll
+    for (int i = 0; i < kDtRank; ++i)
+      w[i] = (act && q0 + i < rank) ? W[(q0 + i) * sw_r + h] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kDtRows; ++k) {
+      if (k < nr) {
+#pragma unroll
+        for (int i = 0; i < kDtRank; ++i)
+          if (q0 + i < rank) acc[k] = __builtin_fmaf(raw[roff[k] + q0 + i], w[i], acc[k]);
+      }
+    }
+  }
+  if (!act) return;
+  const float bv = bias[h];
+#pragma unroll
+  for (int k = 0; k < kDtRows; ++k) {
+    if (k < nr) {
+      const float x = acc[k] + bv;
+      float sp = fmaxf(x, 0.0f) + log1pf(expf(-__builtin_fabsf(x)));
+      sp = fminf(fmaxf(sp, dt_min), dt_max);
+      const int64_t r = r0 + k;
+      const int64_t b = r / grid_t, t = r - b * grid_t;
+      stf(out + b * so_b + t * so_t + h, sp);
+    }
+  }
+}
+
+}  // namespace tssm
+
+extern "C" int tssm_dt_project_softplus(int out_dtype, const float* dt_raw, const float* W,
+                                        const float* bias, void* dt_out, int64_t nbatch,
+                                        int64_t T, int64_t H, int64_t rank, int64_t grid_b,
+                                        int64_t grid_t, int64_t h_cover, int64_t sr_b,
+                                        int64_t sr_t, int64_t sw_r, int64_t so_b, int64_t so_t,
+                                        float dt_min, float dt_max, void* stream) {
+  TSSM_CHECK(dt_raw && W && bias && dt_out, TSSM_ERR_NULL);
+  TSSM_CHECK(nbatch >= 0 && T >= 0 && H >= 0 && rank >= 0 && grid_b >= 0 && grid_t >= 0 &&
+                 h_cover >= 0,
+             TSSM_ERR_SHAPE);
+  TSSM_CHECK(grid_b <= nbatch && grid_t <= T && h_cover <= H, TSSM_ERR_SHAPE);
+  TSSM_CHECK(sr_b >= 0 && sr_t >= 0 && sw_r >= 0 && so_b >= 0 && so_t >= 0, TSSM_ERR_STRIDE);
+  const int64_t nrows = grid_b * grid_t;
+  if (nrows == 0 || h_cover == 0) return TSSM_OK;
+  const int64_t n_rg = cdiv64(nrows, kDtRows);
+  TSSM_CHECK(n_rg <= 65535, TSSM_ERR_UNSUPPORTED);
+  const int threads = h_cover >= 256 ? 256 : (int)(cdiv64(h_cover, 64) * 64);
+  const dim3 grid((unsigned)cdiv64(h_cover, threads), (unsigned)n_rg);
+  const hipStream_t s = as_stream(stream);
+#define TSSM_DTP(TT)                                                                            \
+  hipLaunchKernelGGL(dt_project_kernel<TT>, grid, dim3(threads), 0, s, dt_raw, W, bias,         \
+                     (TT*)dt_out, grid_t, nrows, h_cover, rank, sr_b, sr_t, sw_r, so_b, so_t,  \
+                     dt_min, dt_max)
+  switch (out_dtype) {
+    case TSSM_F32: TSSM_DTP(float); break;
+    case TSSM_BF16: TSSM_DTP(bf16_t); break;
+    case TSSM_F16: TSSM_DTP(f16_t); break;
+    default: return TSSM_ERR_DTYPE;
+  }
+#undef TSSM_DTP
+  return launch_status();
+}

@@ -4,8 +4,7 @@
 //   tile = (batch b, head h, chunk c) of TC time steps x P channels, numbered
 //   row-major (blockIdx = (b*n_heads + h) * nchunks + c): the chunks of one
 //   row are neighbours in launch order, which measured ~20% faster on MI355X
-//   HBM than chunk-major numbering; the look-back reads 2 predecessors per
-//   round trip to keep the resulting longer walks short.
+//   HBM than chunk-major numbering.
 //   Thread layout: a wave covers ROWS = 64/G "runs" of R consecutive steps;
 //   each thread owns 8 consecutive channels (one 16-byte bf16 vector) of one
 //   run, so every load instruction reads ROWS whole 128-byte channel rows.
@@ -16,8 +15,11 @@
 //   3. run aggregates -> LDS; a parallel scan over runs (each thread owns one
 //      channel of 8 runs) gives every run's exclusive prefix within the tile;
 //      the threads of the last segment publish the tile aggregate, look back
-//      for the carry-in and publish the inclusive state;
-//   4. sweep 2: y_t = y1_t + sum_j w_t[j] S[j], reduced over the G threads of
+//      for the carry-in and publish the inclusive state (at once, before the
+//      look-back, when the tile's decay product is exactly zero: such a tile
+//      forgets its entry state, so its successors never wait on it);
+//   4. sweep 2: y_t = y1_t + sum_j w_t[j] S[j] (with one decay per head,
+//      w_t[j] = C_t[j] a_loc_t is rebuilt from C), reduced over the G threads of
 //      the run with DPP and stored broadcast over the head's channels.
 //   HBM traffic = inputs once + y once + ~1.5 KB of carry words per tile.
 //
@@ -75,15 +77,15 @@ constexpr int MODE_DIAG = 0;
 constexpr int MODE_MAMBA1 = 1;
 
 constexpr int kMhR = 4;    // consecutive steps per thread
-constexpr int kMhWin = 2;  // predecessors read per look-back round trip (measured best)
+constexpr int kMhWin = 1;  // predecessors read per look-back round trip (measured best)
 
-template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE, int NS>
+template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE, int NS, int R = kMhR,
+          int WIN = kMhWin>
 __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   // NS = threads summed into one output value: the whole row for MODE_DIAG
   // (NS == G), one channel's N/8 threads for MODE_MAMBA1.
   constexpr int P = G * 8;
   constexpr int ROWS = 64 / G;
-  constexpr int R = kMhR;
   extern __shared__ float s_mem[];
   const int W = blockDim.x >> 6;
   const int NRUN = W * ROWS;   // runs of R steps per tile
@@ -173,13 +175,17 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   }
 
   // ---- sweep 1: discretize + run-local scan from (1, 0)
+  // With one decay per head (APH) the run-local decay product is the same for
+  // the thread's 8 channels, so sweep 2 rebuilds w_t = C_t * a_loc_t from the
+  // C vector still held in registers instead of keeping 8 w values per step.
   float al[8], xl[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     al[j] = 1.0f;
     xl[j] = 0.0f;
   }
-  float w[R][8];
+  float w[APH ? 1 : R][8];
+  float alr[R];
   float y1[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -207,10 +213,11 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       xl[j] = __builtin_fmaf(ab, xl[j], coef * vB[r].get(j) * uj);
       al[j] = al[j] * ab;
       const float cj = vC[r].get(j);
-      w[r][j] = cj * al[j];
+      if constexpr (!APH) w[r][j] = cj * al[j];
       acc = __builtin_fmaf(cj, xl[j], acc);
       if constexpr (HAS_D && MODE == MODE_DIAG) acc = __builtin_fmaf(Dv[j], uj, acc);
     }
+    alr[r] = al[0];
     // MODE_MAMBA1: D[d] x[d] once per channel (the group's first thread)
     if constexpr (HAS_D && MODE == MODE_MAMBA1)
       acc = (g % NS) == 0 ? __builtin_fmaf(Dv[0], us[r], acc) : acc;
@@ -264,11 +271,16 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
         st_word(slot.agg_a(c, ch), TA, tag);
         st_word(slot.agg_x(c, ch), TX, tag);
       }
+      // A tile whose decay product underflowed to exactly zero forgets its
+      // entry state: its inclusive state is TX whatever the carry, so it is
+      // published before the look-back and later tiles need not wait on it.
+      const bool forgets = TA == 0.0f;
+      if (forgets) st_word(slot.inc(c, ch), TX, tag);
       const float hin = a.h0 ? a.h0[row * P + ch] : 0.0f;
       const float carry =
-          (c > 0) ? lookback_channel<kMhWin>(slot, c, ch, tag, hin, a.spin_limit, a.hdr) : hin;
+          (c > 0) ? lookback_channel<WIN>(slot, c, ch, tag, hin, a.spin_limit, a.hdr) : hin;
       const float incl = __builtin_fmaf(TA, carry, TX);
-      st_word(slot.inc(c, ch), incl, tag);
+      if (!forgets) st_word(slot.inc(c, ch), incl, tag);
       if (a.h_last && c == a.nchunks - 1) a.h_last[row * P + ch] = incl;
       s_carry[ch] = carry;
     }
@@ -292,8 +304,15 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     float v = y1[r];
+    if constexpr (APH) {
+      float cs = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v = __builtin_fmaf(w[r][j], S[j], v);
+      for (int j = 0; j < 8; ++j) cs = __builtin_fmaf(vC[r].get(j), S[j], cs);
+      v = __builtin_fmaf(alr[r], cs, v);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v = __builtin_fmaf(w[r][j], S[j], v);
+    }
     v = group_sum<NS>(v);
     if (t0 + r < a.L) {
       if constexpr (MODE == MODE_DIAG) store_bcast8<T>(yp + r * a.sy_l, v);

@@ -33,7 +33,7 @@ class TssmError(RuntimeError):
     """A HIP runtime error reported by a tssm entry point."""
 
 
-_CTYPE = {"int": ctypes.c_int, "int64_t": ctypes.c_int64}
+_CTYPE = {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float}
 
 
 def parse_header(text: str) -> dict[str, tuple[str, list[str]]]:
