@@ -39,6 +39,26 @@ def test_ssd_scan(dev, dtype, disc, P, N):
     assert_close(hl, h_ref, TOL[dtype], "ssd h_last")
 
 
+@pytest.mark.parametrize("L", [100, 256, 513, 2600])
+@pytest.mark.parametrize("disc", ["zoh", "euler"])
+@pytest.mark.parametrize("with_d", [False, True])
+def test_ssd_scan_matrix_core_path(dev, L, disc, with_d):
+    """bf16, P=64, N=16, 256-step tiles run on the MFMA passes: ragged and
+    sub-tile lengths, skip term, nonzero h0.  The bar is tighter than the bf16
+    tolerance (the fp32 operands of the products are split hi/lo, so only the
+    bf16 output rounding should remain)."""
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, 2, L, 3, 64, 16, torch.bfloat16, seed=L + with_d, heavy=True)
+    h0 = torch.randn(2, 3, 64, 16, device=dev)
+    D = d["D"] if with_d else None
+    y, hl = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], D, disc=disc,
+                             h0=h0, chunk=256, return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssd_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"], D, h0=np64(h0), disc=disc)
+    assert_close(y, y_ref, 4e-3, f"mfma ssd y L={L} {disc} D={with_d}")
+    assert_close(hl, h_ref, 1e-3, "mfma ssd h_last")
+
+
 @pytest.mark.parametrize("chunk", [64, 256, 1024])
 def test_ssd_scan_chunks_and_split(dev, chunk):
     from tssm import ssd_scan_forward

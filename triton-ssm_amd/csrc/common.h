@@ -27,12 +27,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __host__ inline float bf16_bits_to_f32(uint32_t b) {
   return __uint_as_float(b << 16);
 }
-// round-to-nearest-even, NaN kept quiet
+// round-to-nearest-even (gfx950 converts in hardware: v_cvt_pk_bf16_f32)
+typedef __bf16 hw_bf16x2 __attribute__((ext_vector_type(2)));
 __device__ inline uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+// two floats -> packed bf16 pair (a in the low half), one instruction
+__device__ inline uint32_t pk_bf16(float a, float b) {
+  const hw_bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <typename T> struct Elem;
@@ -112,8 +115,7 @@ template <> struct Vec8<float> {
 // Store one value broadcast into 8 consecutive channels.
 template <typename T> __device__ inline void store_bcast8(T* p, float v);
 template <> __device__ inline void store_bcast8<bf16_t>(bf16_t* p, float v) {
-  uint32_t b = f32_to_bf16_bits(v);
-  uint32_t w = b | (b << 16);
+  const uint32_t w = pk_bf16(v, v);
   __builtin_nontemporal_store(u32x4{w, w, w, w}, reinterpret_cast<u32x4*>(p));
 }
 template <> __device__ inline void store_bcast8<f16_t>(f16_t* p, float v) {
