@@ -307,37 +307,26 @@ __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
 
 // ---------------------------------------------------------------- MFMA passes
 // bf16 inputs, P = 64, N = 16, 256-step tiles (the long-sequence shape): the
-// chunked (dual) form on the matrix cores.  A tile is 8 sub-chunks of 32
-// steps.  With l_t = dt_t a log2(e) and, inside a sub-chunk, the inclusive
-// prefix cum_t and suffix sfx_s = sum_{u>s} l_u:
+// chunked (dual) form on the matrix cores.  A tile is processed as two halves
+// of 128 steps staged in LDS in turn; a half is 4 sub-chunks of 32 steps, one
+// per wave.  With l_t = dt_t a log2(e) and, inside a sub-chunk, the inclusive
+// prefix cum_t and exclusive suffix sfx_s = sum_{u>s} l_u:
 //   M[t][s]  = (C_t . B_s) 2^(cum_t - cum_s) coef_s   (s <= t, same sub-chunk)
 //   y_t      = sum_s M[t][s] x_s + 2^cum_t (H_J C_t) (+ D x_t)
 //   S_J      = sum_{s in J} 2^sfx_s coef_s x_s B_s^T,  H_{J+1} = 2^cumE_J H_J + S_J
-// Pass 1 forms the tile's state directly with suffixes over the whole tile.
-// MFMA operands that are not raw inputs (decay-weighted B, M, H) are fp32
-// values split into bf16 hi + lo parts (two products), which keeps ~16 bits of
-// their mantissa; x, B and C enter exactly.  x is transposed into LDS once
-// per tile ([p][s]) because every product contracts over time steps.
+// Pass 1 forms each half's state with suffixes over the half and combines the
+// halves (state = 2^(half 2 decay) state_1 + state_2).  MFMA operands that are
+// not raw inputs (decay-weighted B, M, H) are fp32 values split into bf16 hi +
+// lo parts (two products), which keeps ~16 bits of their mantissa; x, B and C
+// enter exactly.  x is transposed into LDS ([p][s]) because every product
+// contracts over time steps.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kMq = 256;           // steps per tile
+constexpr int kMq = 256;           // steps per tile (granularity of the state passing)
+constexpr int kMu = 128;           // steps staged in LDS at a time (half a tile)
 constexpr int kMsub = 32;          // steps per sub-chunk
-constexpr int kMnsub = kMq / kMsub;
 constexpr int kMp = 64, kMn = 16;  // head dim, state size
-constexpr int kXs = kMq;           // row stride (elements) of the transposed tiles
-
-// LDS element offsets.  Transposed tiles (xT[p][s], BT[n][s]): the 16-byte
-// column block is XORed with the row's group of 8, so both the transposing
-// writes (8 rows, one column block per lane) and the operand reads (8 rows
-// per lane group) spread over all banks.  Sub-chunk states sH[J][p][n]: the
-// 4-float quad is XORed with (p >> 1) & 3 for the row-per-lane operand reads.
-__device__ inline int tix(int row, int col) {
-  return row * kXs + ((((col >> 3) ^ (row >> 3)) & 31) << 3) + (col & 7);
-}
-__device__ inline int hix(int J, int p, int n) {
-  return (J * 64 + p) * 16 + ((((n >> 2) ^ (p >> 1)) & 3) << 2) + (n & 3);
-}
 
 __device__ inline bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -359,13 +348,32 @@ __device__ inline void split_bf16(const float* v, bf16x8_t& hi, bf16x8_t& lo) {
 __device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// The tile's x and B as raw 16-byte pieces, loaded first (all loads in flight
-// at once) and transposed into LDS afterwards.  Rows at or past L are loaded
-// from row L-1 (in bounds) and zeroed with a select, so no load sits behind a
-// divergent branch.  256 threads: x item = (step quad tq, channel group g of
-// 8), two per thread; B item = (step pair tp, state group ng of 8), one.
+// LDS element offsets.  Transposed half-tiles (xT[p][s], BT[n][s], 128
+// columns): the 16-byte column block is XORed with the row's group of 8, so
+// both the transposing writes (8 rows, one column block per lane) and the
+// operand reads (8 rows per lane group) spread over all banks.  Sub-chunk
+// states sH[J][p][n]: the 4-float quad is XORed with (p >> 1) & 3 for the
+// row-per-lane operand reads.
+__device__ inline int tix(int row, int col) {
+  return row * kMu + ((((col >> 3) ^ (row >> 3)) & (kMu / 8 - 1)) << 3) + (col & 7);
+}
+__device__ inline int hix(int J, int p, int n) {
+  return (J * kMp + p) * kMn + ((((n >> 2) ^ (p >> 1)) & 3) << 2) + (n & 3);
+}
+// Output staging tile [32 t][32 channels] bf16 (2 KB, in place of 32 rows of
+// an sH block): 4-channel units XORed with 2 (t & 3), even, so the 8-channel
+// pairs read back as 16-byte pieces stay intact.
+__device__ inline int yix(int t, int pl) {
+  return t * 32 + ((((pl >> 2) ^ (2 * (t & 3))) & 7) << 2) + (pl & 3);
+}
+
+// x and B of a half-tile as raw 16-byte pieces, loaded first (all loads in
+// flight at once) and transposed into LDS afterwards.  Rows at or past L are
+// loaded from row L-1 (in bounds) and zeroed with a select, so no load sits
+// behind a divergent branch.  x item = (step quad tq, channel group g of 8),
+// one per thread; B item = (step pair tp, state group ng of 8), threads < 128.
 struct XbRegs {
-  u32x4 x[2][4];
+  u32x4 x[4];
   u32x4 b[2];
 };
 
@@ -374,22 +382,20 @@ __device__ inline void mfma_load_xb(const SsdArgs& a, uint32_t b, uint32_t h, in
   const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h;
   const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
   const int64_t last = a.L - 1;
+  const int tq = tid >> 3, g = tid & 7;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int it = tid + 256 * j;
-    const int tq = it >> 3, g = it & 7;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int64_t t = t0 + 4 * tq + k;
-      r.x[j][k] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(xb + (t < last ? t : last) * a.sx_l + 8 * g));
-    }
+  for (int k = 0; k < 4; ++k) {
+    const int64_t t = t0 + 4 * tq + k;
+    r.x[k] = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(xb + (t < last ? t : last) * a.sx_l + 8 * g));
   }
-  const int tp = tid >> 1, ng = tid & 1;
+  if (tid < kMu) {
+    const int tp = tid >> 1, ng = tid & 1;
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int64_t t = t0 + 2 * tp + k;
-    r.b[k] = *reinterpret_cast<const u32x4*>(Bb + (t < last ? t : last) * a.sB_l + 8 * ng);
+    for (int k = 0; k < 2; ++k) {
+      const int64_t t = t0 + 2 * tp + k;
+      r.b[k] = *reinterpret_cast<const u32x4*>(Bb + (t < last ? t : last) * a.sB_l + 8 * ng);
+    }
   }
 }
 
@@ -405,14 +411,12 @@ __device__ inline uint32_t perm_hi(uint32_t w0, uint32_t w1) {
 __device__ inline void mfma_store_xb(const SsdArgs& a, int64_t t0, int tid, const XbRegs& r,
                                      uint16_t* xT, uint16_t* BT) {
   const u32x4 zero = {0, 0, 0, 0};
-  const bool full = t0 + kMq <= a.L;  // uniform: no row of the tile is past L
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int it = tid + 256 * j;
-    const int tq = it >> 3, g = it & 7;
+  const bool full = t0 + kMu <= a.L;  // uniform: no row of the half is past L
+  {
+    const int tq = tid >> 3, g = tid & 7;
     u32x4 w[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) w[k] = (full || t0 + 4 * tq + k < a.L) ? r.x[j][k] : zero;
+    for (int k = 0; k < 4; ++k) w[k] = (full || t0 + 4 * tq + k < a.L) ? r.x[k] : zero;
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
       const int k = e >> 1;
@@ -422,15 +426,17 @@ __device__ inline void mfma_store_xb(const SsdArgs& a, int64_t t0, int tid, cons
           make_uint2(perm_hi(w[0][k], w[1][k]), perm_hi(w[2][k], w[3][k]));
     }
   }
-  const int tp = tid >> 1, ng = tid & 1;
-  u32x4 w[2];
+  if (tid < kMu) {
+    const int tp = tid >> 1, ng = tid & 1;
+    u32x4 w[2];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) w[k] = (full || t0 + 2 * tp + k < a.L) ? r.b[k] : zero;
+    for (int k = 0; k < 2; ++k) w[k] = (full || t0 + 2 * tp + k < a.L) ? r.b[k] : zero;
 #pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    const int k = e >> 1;
-    *reinterpret_cast<uint32_t*>(BT + tix(8 * ng + e, 2 * tp)) = perm_lo(w[0][k], w[1][k]);
-    *reinterpret_cast<uint32_t*>(BT + tix(8 * ng + e + 1, 2 * tp)) = perm_hi(w[0][k], w[1][k]);
+    for (int e = 0; e < 8; e += 2) {
+      const int k = e >> 1;
+      *reinterpret_cast<uint32_t*>(BT + tix(8 * ng + e, 2 * tp)) = perm_lo(w[0][k], w[1][k]);
+      *reinterpret_cast<uint32_t*>(BT + tix(8 * ng + e + 1, 2 * tp)) = perm_hi(w[0][k], w[1][k]);
+    }
   }
 }
 
@@ -453,8 +459,8 @@ __device__ inline void mfma_step_scalars(const SsdArgs& a, uint32_t h, int64_t t
   *coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(x * 0.6931471805599453f, exp2_fast(x)) * d : d;
 }
 
-// Bw operand of a 16x16x32 product: B_s[n] 2^w... for n = lane%16 and the 8
-// steps s0..s0+7 (BT row n), scaled by s_w[s], split hi/lo.
+// Bw operand of a 16x16x32 product: B_s[n] for n = lane%16 and the 8 steps
+// s0..s0+7 (BT row n), scaled by s_w[s], split hi/lo.
 __device__ inline void mfma_bw_operand(const uint16_t* BT, const float* s_w, int n, int s0,
                                        bf16x8_t& hi, bf16x8_t& lo) {
   const u32x4 bv = *reinterpret_cast<const u32x4*>(BT + tix(n, s0));
@@ -484,61 +490,87 @@ struct XcdTiles {
   __device__ uint32_t row_of(uint32_t jj) const { return jj % rows; }
 };
 
+// Unit walk shared by both passes: the halves of a tile in order (a second
+// half that starts at or past L is skipped), then the next tile of the
+// schedule.
+struct UnitWalk {
+  uint32_t jt, c, row;
+  int half;
+  __device__ bool second_half_follows(const SsdArgs& a) const {
+    return half == 0 && (int64_t)c * kMq + kMu < a.L;
+  }
+};
+
 // Pass 1: state of each tile from zero (decay product in chunkA, P x N state
 // [p][n] in chunkX).  Wave w forms the 16 channels 16w..16w+15.  Persistent:
-// a workgroup walks tiles blockIdx.x, +gridDim.x, ... and issues the next
-// tile's global loads before working on the current one.  Tiles are numbered
-// chunk-major, so the heads of one time range (which share the rows of the
-// [B, L, H, *] inputs) are processed together.
+// the next half's global loads are issued before the current half's products.
 template <int DISC>
 __global__ __launch_bounds__(256) void ssd_state_mfma_kernel(SsdArgs a) {
-  __shared__ __align__(16) uint16_t xT[kMp * kXs];
-  __shared__ __align__(16) uint16_t BT[kMn * kXs];
-  __shared__ __align__(16) float s_w[kMq];
-  __shared__ float s_tot[4];
+  __shared__ __align__(16) uint16_t xT[kMp * kMu];
+  __shared__ __align__(16) uint16_t BT[kMn * kMu];
+  __shared__ __align__(16) float s_w[kMu];
+  __shared__ float s_tot[2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const XcdTiles sched(a.rows, a.nchunks);
-  uint32_t jt = sched.j;
-  if (!sched.valid(jt)) return;
-  uint32_t c = sched.chunk_of(jt), row = sched.row_of(jt);
-  float dl = mfma_load_dt(a, row / a.H, row % a.H, (int64_t)c * kMq, tid);
+  if (!sched.valid(sched.j)) return;
+  UnitWalk u{sched.j, sched.chunk_of(sched.j), sched.row_of(sched.j), 0};
+  float dl = 0.0f;
   XbRegs xr;
-  mfma_load_xb(a, row / a.H, row % a.H, (int64_t)c * kMq, tid, xr);
+  auto load_unit = [&](uint32_t cc, uint32_t rr, int hf) {
+    const uint32_t bb = rr / a.H, hd = rr - bb * a.H;
+    const int64_t tt0 = (int64_t)cc * kMq + hf * kMu;
+    if (tid < kMu) dl = mfma_load_dt(a, bb, hd, tt0, tid);
+    mfma_load_xb(a, bb, hd, tt0, tid, xr);
+  };
+  load_unit(u.c, u.row, 0);
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float ltot = 0.0f;  // log2 decay of the tile so far
+  const int n = lane & 15, q = lane >> 4;
+  const int p = 16 * wave + (lane & 15);
   for (;;) {
-    const uint32_t h = row % a.H;
-    const int64_t t0 = (int64_t)c * kMq;
-    float l2, coef;
-    mfma_step_scalars<DISC>(a, h, t0, tid, dl, &l2, &coef);
-    // exclusive suffix sum of l2 over the tile: inclusive suffix within the
-    // wave, shifted down one lane, plus the totals of the later waves
-    float v = l2;
+    const uint32_t h = u.row % a.H;
+    const int64_t t0 = (int64_t)u.c * kMq + u.half * kMu;
+    // exclusive suffix of l2 within the half: inclusive suffix within the
+    // wave, shifted down one lane, plus (wave 0) the other wave's total
+    float ex = 0.0f, coef = 0.0f;
+    if (tid < kMu) {
+      float l2;
+      mfma_step_scalars<DISC>(a, h, t0, tid, dl, &l2, &coef);
+      float v = l2;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float u = __shfl_down(v, o);
-      v += (lane + o < 64) ? u : 0.0f;
+      for (int o = 1; o < 64; o <<= 1) {
+        const float w = __shfl_down(v, o);
+        v += (lane + o < 64) ? w : 0.0f;
+      }
+      if (lane == 0) s_tot[wave] = v;
+      ex = __shfl_down(v, 1);
+      ex = lane < 63 ? ex : 0.0f;
     }
-    if (lane == 0) s_tot[wave] = v;
-    float ex = __shfl_down(v, 1);
-    ex = lane < 63 ? ex : 0.0f;
-    __syncthreads();
-    for (int k = wave + 1; k < 4; ++k) ex += s_tot[k];
-    s_w[tid] = exp2_fast(ex) * coef;
     mfma_store_xb(a, t0, tid, xr, xT, BT);
     __syncthreads();
-    const float atot = s_tot[0] + s_tot[1] + s_tot[2] + s_tot[3];
-    // next tile's loads overlap this tile's products
-    const uint32_t jn = jt + sched.nloc;
-    const bool more = sched.valid(jn);
-    const uint32_t cn = sched.chunk_of(jn), rown = sched.row_of(jn);
-    if (more) {
-      dl = mfma_load_dt(a, rown / a.H, rown % a.H, (int64_t)cn * kMq, tid);
-      mfma_load_xb(a, rown / a.H, rown % a.H, (int64_t)cn * kMq, tid, xr);
+    const float lhalf = s_tot[0] + s_tot[1];
+    if (tid < kMu) s_w[tid] = exp2_fast(wave == 0 ? ex + s_tot[1] : ex) * coef;
+    __syncthreads();
+    // next unit's loads overlap this half's products
+    UnitWalk nx = u;
+    bool more = true;
+    const bool tile_ends = !u.second_half_follows(a);
+    if (!tile_ends) {
+      nx.half = 1;
+    } else {
+      nx.jt = u.jt + sched.nloc;
+      more = sched.valid(nx.jt);
+      nx.c = sched.chunk_of(nx.jt);
+      nx.row = sched.row_of(nx.jt);
+      nx.half = 0;
     }
-    const int n = lane & 15, q = lane >> 4;
-    const int p = 16 * wave + (lane & 15);
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-    for (int kk = 0; kk < kMq / 32; ++kk) {
+    if (more) load_unit(nx.c, nx.row, nx.half);
+    // state <- 2^(this half's decay) state + this half's products
+    const float sc = exp2_fast(lhalf);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] *= sc;
+#pragma unroll
+    for (int kk = 0; kk < kMu / 32; ++kk) {
       const int s0 = 32 * kk + 8 * q;
       const bf16x8_t ax = as_bf16x8(*reinterpret_cast<const u32x4*>(xT + tix(p, s0)));
       bf16x8_t bhi, blo;
@@ -546,141 +578,151 @@ __global__ __launch_bounds__(256) void ssd_state_mfma_kernel(SsdArgs a) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bhi, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, blo, acc, 0, 0, 0);
     }
-    float* out = a.chunkX + ((int64_t)row * a.nchunks + c) * (kMp * kMn);
+    ltot += lhalf;
+    if (tile_ends) {
+      float* out = a.chunkX + ((int64_t)u.row * a.nchunks + u.c) * (kMp * kMn);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out[(16 * wave + 4 * q + r) * kMn + n] = acc[r];
-    if (tid == 0) a.chunkA[(int64_t)row * a.nchunks + c] = exp2_fast(atot);
+      for (int r = 0; r < 4; ++r) out[(16 * wave + 4 * q + r) * kMn + n] = acc[r];
+      if (tid == 0) a.chunkA[(int64_t)u.row * a.nchunks + u.c] = exp2_fast(ltot);
+      acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      ltot = 0.0f;
+    }
     if (!more) break;
-    jt = jn;
-    c = cn;
-    row = rown;
-    __syncthreads();  // LDS is rewritten by the next tile
+    u = nx;
+    __syncthreads();  // LDS is rewritten by the next half
   }
 }
 
-// Pass 3: outputs.  Wave w owns sub-chunks 2w and 2w+1.  Persistent and
-// chunk-major like pass 1: the next tile's global loads are issued before the
-// current tile's sub-chunk states and outputs are formed.
+// Pass 3: outputs.  Wave w owns sub-chunk w of each half.  Persistent like
+// pass 1; the state entering a half is carried in registers (each thread owns
+// 4 of the 1024 entries): the tile's entry state for the first half, the
+// first half's end state for the second.
 template <int DISC, bool HAS_D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void ssd_out_mfma_kernel(SsdArgs a) {
-  __shared__ __align__(16) uint16_t xT[kMp * kXs];
-  __shared__ __align__(16) uint16_t BT[kMn * kXs];
-  __shared__ __align__(16) float sH[kMnsub * kMp * kMn];  // S_J, then H_J, [J][p][n]
-  __shared__ __align__(16) float s_cum[kMq];
-  __shared__ __align__(16) float s_coef[kMq];
-  __shared__ __align__(16) float s_w[kMq];
-  __shared__ float s_AJ[kMnsub];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void ssd_out_mfma_kernel(SsdArgs a) {
+  __shared__ __align__(16) uint16_t xT[kMp * kMu];
+  __shared__ __align__(16) uint16_t BT[kMn * kMu];
+  __shared__ __align__(16) float sH[4 * kMp * kMn];  // S_J, then H_J, [J][p][n]
+  __shared__ __align__(16) float s_cum[kMu];
+  __shared__ __align__(16) float s_coef[kMu];
+  __shared__ __align__(16) float s_w[kMu];
+  __shared__ float s_AJ[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const XcdTiles sched(a.rows, a.nchunks);
-  uint32_t jt = sched.j;
-  if (!sched.valid(jt)) return;
+  if (!sched.valid(sched.j)) return;
+  UnitWalk u{sched.j, sched.chunk_of(sched.j), sched.row_of(sched.j), 0};
 
-  // global loads of one tile: dt of step tid, x and B pieces for the LDS
-  // tiles, B and C rows of the wave's two sub-chunks (Gram and carried-state
+  // global loads of one half: dt of step tid, x and B pieces for the LDS
+  // tiles, B and C rows of the wave's sub-chunk (Gram and carried-state
   // products).  Rows past L are read from row L-1 and zeroed later.
-  float dl;
+  float dl = 0.0f;
   XbRegs xr;
-  u32x4 brow[2], crow[2];
-  auto load_tile = [&](uint32_t cc, uint32_t rr) {
+  u32x4 brow, crow;
+  float hnew[4];
+  auto load_unit = [&](uint32_t cc, uint32_t rr, int hf) {
     const uint32_t bb = rr / a.H, hd = rr - bb * a.H;
-    const int64_t tt0 = (int64_t)cc * kMq;
-    dl = mfma_load_dt(a, bb, hd, tt0, tid);
+    const int64_t tt0 = (int64_t)cc * kMq + hf * kMu;
+    if (tid < kMu) dl = mfma_load_dt(a, bb, hd, tt0, tid);
     const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + bb * a.sB_b + hd * a.sB_h;
     const uint16_t* Cb = reinterpret_cast<const uint16_t*>(a.C) + bb * a.sC_b + hd * a.sC_h;
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int64_t t = tt0 + kMsub * (2 * wave + jj) + l32;
-      const int64_t tc = t < a.L ? t : a.L - 1;
-      brow[jj] = *reinterpret_cast<const u32x4*>(Bb + tc * a.sB_l + 8 * hh);
-      crow[jj] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Cb + tc * a.sC_l + 8 * hh));
-    }
+    const int64_t t = tt0 + kMsub * wave + l32;
+    const int64_t tc = t < a.L ? t : a.L - 1;
+    brow = *reinterpret_cast<const u32x4*>(Bb + tc * a.sB_l + 8 * hh);
+    crow = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Cb + tc * a.sC_l + 8 * hh));
     mfma_load_xb(a, bb, hd, tt0, tid, xr);
+    if (hf == 0) {
+      const float* en = a.entry + ((int64_t)rr * a.nchunks + cc) * (kMp * kMn);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hnew[k] = en[tid + 256 * k];
+    }
   };
-  uint32_t c = sched.chunk_of(jt), row = sched.row_of(jt);
-  load_tile(c, row);
+  load_unit(u.c, u.row, 0);
+  float hc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) hc[k] = hnew[k];
 
   for (;;) {
-    const uint32_t b = row / a.H, h = row - b * a.H;
-    const int64_t t0 = (int64_t)c * kMq;
-    float l2, coef;
-    mfma_step_scalars<DISC>(a, h, t0, tid, dl, &l2, &coef);
-    u32x4 bcur[2], ccur[2];
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const bool live = t0 + kMsub * (2 * wave + jj) + l32 < a.L;
-      bcur[jj] = live ? brow[jj] : u32x4{0, 0, 0, 0};
-      ccur[jj] = live ? crow[jj] : u32x4{0, 0, 0, 0};
-    }
+    const uint32_t b = u.row / a.H, h = u.row - b * a.H;
+    const int64_t t0 = (int64_t)u.c * kMq + u.half * kMu;
     // prefix (inclusive) and suffix (exclusive) sums within 32-step sub-chunks
-    float pre = l2, suf = l2;
+    if (tid < kMu) {
+      float l2, coef;
+      mfma_step_scalars<DISC>(a, h, t0, tid, dl, &l2, &coef);
+      float pre = l2, suf = l2;
 #pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-      const float u = __shfl_up(pre, o), d = __shfl_down(suf, o);
-      pre += (l32 >= o) ? u : 0.0f;
-      suf += (l32 + o < 32) ? d : 0.0f;
+      for (int o = 1; o < 32; o <<= 1) {
+        const float w = __shfl_up(pre, o), d = __shfl_down(suf, o);
+        pre += (l32 >= o) ? w : 0.0f;
+        suf += (l32 + o < 32) ? d : 0.0f;
+      }
+      float sx = __shfl_down(suf, 1);
+      sx = l32 < 31 ? sx : 0.0f;
+      s_cum[tid] = pre;
+      s_coef[tid] = coef;
+      s_w[tid] = exp2_fast(sx) * coef;
+      if (l32 == 31) s_AJ[tid >> 5] = exp2_fast(pre);
     }
-    float sx = __shfl_down(suf, 1);
-    sx = l32 < 31 ? sx : 0.0f;
-    s_cum[tid] = pre;
-    s_coef[tid] = coef;
-    s_w[tid] = exp2_fast(sx) * coef;
-    if (l32 == 31) s_AJ[tid >> 5] = exp2_fast(pre);
+    const bool live = t0 + kMsub * wave + l32 < a.L;
+    const u32x4 bcur = live ? brow : u32x4{0, 0, 0, 0};
+    const u32x4 ccur = live ? crow : u32x4{0, 0, 0, 0};
     mfma_store_xb(a, t0, tid, xr, xT, BT);
     __syncthreads();
 
-    // next tile's loads overlap everything below
-    const uint32_t jn = jt + sched.nloc;
-    const bool more = sched.valid(jn);
-    const uint32_t cn = sched.chunk_of(jn), rown = sched.row_of(jn);
-    if (more) load_tile(cn, rown);
+    // next unit's loads overlap everything below
+    UnitWalk nx = u;
+    bool more = true;
+    if (u.second_half_follows(a)) {
+      nx.half = 1;
+    } else {
+      nx.jt = u.jt + sched.nloc;
+      more = sched.valid(nx.jt);
+      nx.c = sched.chunk_of(nx.jt);
+      nx.row = sched.row_of(nx.jt);
+      nx.half = 0;
+    }
+    if (more) load_unit(nx.c, nx.row, nx.half);
 
-    // local state of each of the wave's sub-chunks (16x16x32, K = the 32 steps)
+    const int J = wave;
+    const int sb = kMsub * J;
+    // local state of the wave's sub-chunk (16x16x32, K = its 32 steps)
     {
       const int n = lane & 15, q = lane >> 4;
+      const int s0 = sb + 8 * q;
+      bf16x8_t bhi, blo;
+      mfma_bw_operand(BT, s_w, n, s0, bhi, blo);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int J = 2 * wave + jj;
-        const int s0 = kMsub * J + 8 * q;
-        bf16x8_t bhi, blo;
-        mfma_bw_operand(BT, s_w, n, s0, bhi, blo);
+      for (int pb = 0; pb < kMp / 16; ++pb) {
+        const bf16x8_t ax = as_bf16x8(*reinterpret_cast<const u32x4*>(xT + tix(16 * pb + n, s0)));
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bhi, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, blo, acc, 0, 0, 0);
 #pragma unroll
-        for (int pb = 0; pb < kMp / 16; ++pb) {
-          const bf16x8_t ax = as_bf16x8(*reinterpret_cast<const u32x4*>(xT + tix(16 * pb + n, s0)));
-          f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bhi, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, blo, acc, 0, 0, 0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sH[hix(J, 16 * pb + 4 * q + r, n)] = acc[r];
-        }
+        for (int r = 0; r < 4; ++r) sH[hix(J, 16 * pb + 4 * q + r, n)] = acc[r];
       }
     }
     __syncthreads();
-    // entry state of every sub-chunk: H_0 = tile entry, H_{J+1} = A_J H_J + S_J
-    {
-      const float* en = a.entry + ((int64_t)row * a.nchunks + c) * (kMp * kMn);
+    // entry state of every sub-chunk: H_0 = state entering the half,
+    // H_{J+1} = A_J H_J + S_J; the end state carries into the next half
 #pragma unroll
-      for (int k = 0; k < (kMp * kMn) / 256; ++k) {
-        const int e = tid + 256 * k;
-        float hv = en[e];
+    for (int k = 0; k < 4; ++k) {
+      const int e = tid + 256 * k;
+      float hv = hc[k];
 #pragma unroll
-        for (int J = 0; J < kMnsub; ++J) {
-          const float sj = sH[hix(J, e >> 4, e & 15)];
-          sH[hix(J, e >> 4, e & 15)] = hv;
-          hv = __builtin_fmaf(s_AJ[J], hv, sj);
-        }
+      for (int JJ = 0; JJ < 4; ++JJ) {
+        const float sj = sH[hix(JJ, e >> 4, e & 15)];
+        sH[hix(JJ, e >> 4, e & 15)] = hv;
+        hv = __builtin_fmaf(s_AJ[JJ], hv, sj);
       }
+      hc[k] = hv;
     }
     __syncthreads();
 
-    uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + b * a.sy_b + h * a.sy_h;
-#pragma unroll 1
-    for (int jj = 0; jj < 2; ++jj) {
-      const int J = 2 * wave + jj;
-      const int sb = kMsub * J;
+    // outputs of the wave's sub-chunk
+    {
+      uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + b * a.sy_b + h * a.sy_h;
       // Gram^T: D[s][t] = B_s . C_t (lane: t = l32, rows s over the registers)
       f32x16_t g = {};
-      g = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(bcur[jj]), as_bf16x8(ccur[jj]), g, 0, 0, 0);
+      g = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(bcur), as_bf16x8(ccur), g, 0, 0, 0);
       const float cum_t = s_cum[sb + l32];
       float m[16];
 #pragma unroll
@@ -689,65 +731,70 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float dec = exp2_fast(cum_t - s_cum[sb + s]) * s_coef[sb + s];
         m[r] = s <= l32 ? g[r] * dec : 0.0f;
       }
-      f32x16_t acc[kMp / 32];
-#pragma unroll
-      for (int pb = 0; pb < kMp / 32; ++pb) acc[pb] = f32x16_t{};
-#pragma unroll
-      for (int kap = 0; kap < 2; ++kap) {
-        bf16x8_t mhi, mlo;
-        split_bf16(m + 8 * kap, mhi, mlo);
-#pragma unroll
-        for (int pb = 0; pb < kMp / 32; ++pb) {
-          const int xr_row = 32 * pb + l32, xr_col = sb + 16 * kap + 4 * hh;
-          const uint2 x0 = *reinterpret_cast<const uint2*>(xT + tix(xr_row, xr_col));
-          const uint2 x1 = *reinterpret_cast<const uint2*>(xT + tix(xr_row, xr_col + 8));
-          const bf16x8_t ax = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
-          acc[pb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, mhi, acc[pb], 0, 0, 0);
-          acc[pb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, mlo, acc[pb], 0, 0, 0);
-        }
-      }
-      // carried state: Z[p][t] = H_J[p] . C_t, scaled by 2^cum_t
+      bf16x8_t mhi[2], mlo[2];
+      split_bf16(m, mhi[0], mlo[0]);
+      split_bf16(m + 8, mhi[1], mlo[1]);
       const float u_t = exp2_fast(cum_t);
-#pragma unroll
+      // one block of 32 channels at a time: carried state Z[p][t] = H_J[p] . C_t
+      // scaled by 2^cum_t, plus the in-sub-chunk products M x, then stage
+#pragma unroll 1
       for (int pb = 0; pb < kMp / 32; ++pb) {
         const float4 h0 = *reinterpret_cast<const float4*>(sH + hix(J, 32 * pb + l32, 8 * hh));
         const float4 h1 = *reinterpret_cast<const float4*>(sH + hix(J, 32 * pb + l32, 8 * hh + 4));
         const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
         bf16x8_t hhi, hlo;
         split_bf16(hv, hhi, hlo);
-        f32x16_t z = {};
-        z = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hhi, as_bf16x8(ccur[jj]), z, 0, 0, 0);
-        z = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hlo, as_bf16x8(ccur[jj]), z, 0, 0, 0);
+        f32x16_t acc = {};
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hhi, as_bf16x8(ccur), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hlo, as_bf16x8(ccur), acc, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[pb][r] = __builtin_fmaf(u_t, z[r], acc[pb][r]);
-      }
-      // skip term and store: lane holds y[t][p] for t = l32 and 4 runs of 4 channels
-      const int64_t t = t0 + sb + l32;
+        for (int r = 0; r < 16; ++r) acc[r] *= u_t;
 #pragma unroll
-      for (int pb = 0; pb < kMp / 32; ++pb) {
+        for (int kap = 0; kap < 2; ++kap) {
+          const int xr_row = 32 * pb + l32, xr_col = sb + 16 * kap + 4 * hh;
+          const uint2 x0 = *reinterpret_cast<const uint2*>(xT + tix(xr_row, xr_col));
+          const uint2 x1 = *reinterpret_cast<const uint2*>(xT + tix(xr_row, xr_col + 8));
+          const bf16x8_t ax = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, mhi[kap], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, mlo[kap], acc, 0, 0, 0);
+        }
+        // skip term; stage y[t][32 pb + pl] (bf16) in the rows of H_J this
+        // block has finished with: lane holds t = l32 and 4 runs of 4 channels
+        uint16_t* ys = reinterpret_cast<uint16_t*>(sH + hix(J, 32 * pb, 0));
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
-          const int p = 32 * pb + 8 * qq + 4 * hh;
+          const int pc = 32 * pb + 8 * qq + 4 * hh;
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            v[r] = acc[pb][4 * qq + r];
+            v[r] = acc[4 * qq + r];
             if constexpr (HAS_D) {
-              const float xv = bf16_bits_to_f32(xT[tix(p + r, sb + l32)]);
-              v[r] = __builtin_fmaf(a.D[h * kMp + p + r], xv, v[r]);
+              const float xv = bf16_bits_to_f32(xT[tix(pc + r, sb + l32)]);
+              v[r] = __builtin_fmaf(a.D[h * kMp + pc + r], xv, v[r]);
             }
           }
-          if (t < a.L)
-            *reinterpret_cast<uint2*>(yb + t * a.sy_l + p) =
-                make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
+          *reinterpret_cast<uint2*>(ys + yix(l32, 8 * qq + 4 * hh)) =
+              make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
         }
+      }
+      // the staged 32 x 64 tile leaves as whole 128-byte rows (8 lanes a row)
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = lane + 64 * k, tr = i >> 3, cg = i & 7;
+        const uint16_t* ys = reinterpret_cast<const uint16_t*>(sH + hix(J, 32 * (cg >> 2), 0));
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ys + yix(tr, 8 * (cg & 3)));
+        const int64_t tt = t0 + sb + tr;
+        if (tt < a.L) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(yb + tt * a.sy_l + 8 * cg));
       }
     }
     if (!more) break;
-    jt = jn;
-    c = cn;
-    row = rown;
-    __syncthreads();  // LDS is rewritten by the next tile
+    if (nx.half == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hc[k] = hnew[k];
+    }
+    u = nx;
+    __syncthreads();  // LDS is rewritten by the next half
   }
 }
 
