@@ -155,9 +155,11 @@ __global__ __launch_bounds__(64) void ssd_state_kernel(SsdArgs a) {
   if (lane == 0) a.chunkA[(int64_t)row * a.nchunks + c] = Achunk;
 }
 
-// Pass 2: thread (entry e, segment sg) of a 1024-thread workgroup covering 64
-// consecutive state entries of one row and 16 segments of its chunks.
-constexpr int kPassEntries = 64, kPassSegs = 16;
+// Pass 2: thread (entry e, segment sg) of a 1024-thread workgroup covering 32
+// consecutive state entries of one row and 32 segments of its chunks.  The
+// chunk loops load 8 chunks at a time (indices clamped into the segment, so
+// every load is in bounds and none waits behind a branch) before folding them.
+constexpr int kPassEntries = 32, kPassSegs = 32, kPassBatch = 8;
 __global__ __launch_bounds__(1024) void ssd_pass_kernel(SsdArgs a, int64_t PN) {
   __shared__ float s_a[kPassSegs][kPassEntries], s_x[kPassSegs][kPassEntries];
   const int el = threadIdx.x % kPassEntries;
@@ -168,14 +170,25 @@ __global__ __launch_bounds__(1024) void ssd_pass_kernel(SsdArgs a, int64_t PN) {
   const bool act = e < PN;
   const int64_t nc = a.nchunks;
   const int64_t seg = (nc + kPassSegs - 1) / kPassSegs;
-  const int64_t c0 = sg * seg, c1 = c0 + seg < nc ? c0 + seg : nc;
+  const int64_t c0 = sg * seg < nc ? sg * seg : nc, c1 = c0 + seg < nc ? c0 + seg : nc;
   const float* cA = a.chunkA + row * nc;
   const float* cX = a.chunkX + row * nc * PN + (act ? e : 0);
   float A = 1.0f, X = 0.0f;
-  for (int64_t c = c0; c < c1; ++c) {
-    const float ac = cA[c];
-    X = __builtin_fmaf(ac, X, cX[c * PN]);
-    A *= ac;
+  for (int64_t c = c0; c < c1; c += kPassBatch) {
+    float xa[kPassBatch], aa[kPassBatch];
+#pragma unroll
+    for (int k = 0; k < kPassBatch; ++k) {
+      const int64_t cc = c + k < c1 ? c + k : c;
+      xa[k] = cX[cc * PN];
+      aa[k] = cA[cc];
+    }
+#pragma unroll
+    for (int k = 0; k < kPassBatch; ++k) {
+      if (c + k < c1) {
+        X = __builtin_fmaf(aa[k], X, xa[k]);
+        A *= aa[k];
+      }
+    }
   }
   s_a[sg][el] = A;
   s_x[sg][el] = X;
@@ -183,9 +196,21 @@ __global__ __launch_bounds__(1024) void ssd_pass_kernel(SsdArgs a, int64_t PN) {
   float S = (act && a.h0) ? a.h0[row * PN + e] : 0.0f;
   for (int k = 0; k < sg; ++k) S = __builtin_fmaf(s_a[k][el], S, s_x[k][el]);
   float* en = a.entry + row * nc * PN + (act ? e : 0);
-  for (int64_t c = c0; c < c1; ++c) {
-    if (act) en[c * PN] = S;
-    S = __builtin_fmaf(cA[c], S, cX[c * PN]);
+  for (int64_t c = c0; c < c1; c += kPassBatch) {
+    float xa[kPassBatch], aa[kPassBatch];
+#pragma unroll
+    for (int k = 0; k < kPassBatch; ++k) {
+      const int64_t cc = c + k < c1 ? c + k : c;
+      xa[k] = cX[cc * PN];
+      aa[k] = cA[cc];
+    }
+#pragma unroll
+    for (int k = 0; k < kPassBatch; ++k) {
+      if (c + k < c1) {
+        if (act) en[(c + k) * PN] = S;
+        S = __builtin_fmaf(aa[k], S, xa[k]);
+      }
+    }
   }
   if (act && a.h_last && sg == kPassSegs - 1) a.h_last[row * PN + e] = S;
 }
