@@ -136,7 +136,7 @@ def wl_interp_mamba1(args, dev):
 
     def step(i):
         fused_interp_ssm_forward(d["V"], d["M"], d["tau"], d["A_log"], d["B"], d["C"],
-                                 K=10, FTILE=128, disc=args.disc)
+                                 K=10, FTILE=128, disc=args.disc, chunk=args.scan_chunk)
 
     def cpu():
         import numpy as np
@@ -263,7 +263,8 @@ def traffic_from_profile(name):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 50; 10000 for ssd_stream, the streaming run length)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="multihead")
     ap.add_argument("--disc", choices=["zoh", "euler"], default="zoh")
@@ -274,11 +275,15 @@ def main():
                     help="only run torch copies of a 256 MiB buffer (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE to bytes); prints nothing else")
     ap.add_argument("--sets", type=int, default=3)
+    ap.add_argument("--scan-chunk", type=int, default=128,
+                    help="interp_mamba1: steps per chunk of the selective scan")
     ap.add_argument("--ssd-chunk", type=int, default=256,
                     help="steps per chunk of the SSD scan passes (multiple of 64, <= 1024)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 10000 if args.workload == "ssd_stream" else 50
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: every workload is data-parallel over rows or "
