@@ -164,12 +164,17 @@ int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log, c
  * :187-257).  V, Vhat in v_dtype; M and tau in any float dtype.  Grid
  * (B, T, ceil(F/FTILE)): computes b < grid_b, t < grid_t, tiles < grid_f.
  * K (search window, <= 64) and FTILE (tile of the "any observed" aggregate)
- * are semantic: they change results. */
+ * are semantic: they change results.  The per-(b, t, tile) "any observed"
+ * flags go through a caller workspace of
+ * tssm_time_aware_interp_workspace_bytes() bytes (no clearing needed). */
+int64_t tssm_time_aware_interp_workspace_bytes(int64_t T, int64_t F, int64_t K, int64_t FTILE,
+                                               int64_t grid_b, int64_t grid_t, int64_t grid_f);
 int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, const void* V, const void* M,
                            const void* tau, void* Vhat, int64_t nbatch, int64_t T, int64_t F,
                            int64_t svb, int64_t svt, int64_t smb, int64_t smt, int64_t stb,
                            int64_t stt, int64_t sob, int64_t sot, int64_t K, int64_t FTILE,
-                           int64_t grid_b, int64_t grid_t, int64_t grid_f, void* stream);
+                           int64_t grid_b, int64_t grid_t, int64_t grid_f, void* workspace,
+                           int64_t workspace_bytes, void* stream);
 
 /* fused_interp_ssm_step_kernel (fused_ssm_interp.py:12-101): interpolates
  * step t_cur into Vhat[:, t_cur] and writes h_out = A_bar*h_in + B_bar*vhat.

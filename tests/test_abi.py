@@ -39,7 +39,7 @@ def test_null_pointers_rejected_before_launch():
     assert L.tssm_mh_scan_workspace_bytes(8, 4096, 16, 12, 128) == -1   # head_dim % 8 != 0
     with pytest.raises(ValueError):
         _lib.call("tssm_time_aware_interp", 0, 0, 0, None, None, None, None, 1, 1, 1,
-                  1, 1, 1, 1, 1, 1, 1, 1, 10, 128, 1, 1, 1, None)
+                  1, 1, 1, 1, 1, 1, 1, 1, 10, 128, 1, 1, 1, None, 0, None)
 
 
 def test_every_reference_symbol_is_exported():

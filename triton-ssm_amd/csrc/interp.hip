@@ -10,11 +10,15 @@
 //  * vhat = interp / v_prev / v_next when a neighbour exists, else v_cur --
 //    an observed current value is overwritten when any neighbour exists (:94-97).
 //
-// interp_kernel: one workgroup per (b, tile, block of TB steps).  The tile
-// aggregates of the TB + 2K rows the block needs are computed once into LDS
-// (the reference re-reads the mask tile 2K+1 times per output row), the
-// neighbour indices and weights are resolved per step, then every thread
-// streams its feature lanes: V rows are read once plus the neighbour rows.
+// Two passes:
+//  interp_obs_kernel: one wave per (b, t) row computes the row's "any lane
+//    observed" flag of every feature tile once (M is read exactly once; the
+//    reference re-reads each mask tile 2K+1 times) into a byte workspace
+//    obs[b][t][tile];
+//  interp_kernel: one workgroup per (b, tile, block of TB steps) resolves
+//    neighbours and weights per step from the flags, then all (step, lane)
+//    pairs of the block are interpolated at once, 16-byte vectors where the
+//    layout allows.
 #include "common.h"
 
 namespace tssm {
@@ -37,30 +41,70 @@ struct InterpArgs {
   const void* M;
   const void* tau;
   void* Vhat;
+  unsigned char* obs;  // [grid_b][rows][ntile] flags
   int md, td;
   int64_t T, F, svb, svt, smb, smt, stb, stt, sob, sot;
-  int64_t K, FTILE, grid_t;
+  int64_t K, FTILE, grid_t, rows, ntile;
 };
 
-template <typename TV>
+__global__ __launch_bounds__(kInterpThreads) void interp_obs_kernel(InterpArgs a, int64_t nrow) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * (kInterpThreads / 64) + (threadIdx.x >> 6);
+  if (r >= nrow) return;  // uniform per wave
+  const int64_t b = r / a.rows, t = r - b * a.rows;
+  for (int64_t tile = 0; tile < a.ntile; ++tile) {
+    const int64_t f0 = tile * a.FTILE;
+    const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
+    const float sum = wave_tile_sum(a.M, a.md, b * a.smb + t * a.smt, f0, f1, lane);
+    if (lane == 0) a.obs[r * a.ntile + tile] = sum > 0.5f ? 1 : 0;
+  }
+}
+
+// E consecutive feature lanes as floats: E = 4 (fp32) or 8 (16-bit) with one
+// 16-byte access, or E = 1.
+template <typename TV, int E> struct Lanes {
+  float v[E];
+  __device__ inline void load(const TV* p) {
+    if constexpr (E == 1) {
+      v[0] = ldf(p);
+    } else if constexpr (sizeof(TV) == 4) {
+      const float4 q = *reinterpret_cast<const float4*>(p);
+      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
+      Vec8<TV> q;
+      q.load(p);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = q.get(j);
+    }
+  }
+  __device__ inline void store(TV* p) const {
+    if constexpr (E == 1) {
+      stf(p, v[0]);
+    } else if constexpr (sizeof(TV) == 4) {
+      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) stf(p + j, v[j]);
+    }
+  }
+};
+
+template <typename TV, int E>
 __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
   __shared__ unsigned char s_obs[kInterpTB + 2 * kMaxK];
   __shared__ int s_prev[kInterpTB], s_next[kInterpTB];
   __shared__ float s_w[kInterpTB];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int64_t t0 = (int64_t)blockIdx.x * kInterpTB;
   const int64_t tile = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int64_t f0 = tile * a.FTILE;
   const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
   const int K = (int)a.K;
-  const int nrow = kInterpTB + 2 * K;
-  // 1. tile aggregates of rows t0-K .. t0+TB+K-1 (rows outside [0, T) are unobserved)
-  for (int i = wave; i < nrow; i += kInterpThreads / 64) {
+  // 1. flags of rows t0-K .. t0+TB+K-1 (rows outside [0, T) are unobserved)
+  for (int i = tid; i < kInterpTB + 2 * K; i += kInterpThreads) {
     const int64_t t = t0 - K + i;
-    bool obs = false;
-    if (t >= 0 && t < a.T) obs = wave_tile_sum(a.M, a.md, b * a.smb + t * a.smt, f0, f1, lane) > 0.5f;
-    if (lane == 0) s_obs[i] = obs ? 1 : 0;
+    s_obs[i] = (t >= 0 && t < a.rows) ? a.obs[(b * a.rows + t) * a.ntile + tile] : 0;
   }
   __syncthreads();
   // 2. neighbours and weight per step
@@ -85,25 +129,47 @@ __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
     s_w[tid] = w;
   }
   __syncthreads();
-  // 3. feature lanes
+  // 3. all (step, lane group) pairs of the block, U per thread per batch with
+  // every load issued before the stores
   const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb;
   TV* O = reinterpret_cast<TV*>(a.Vhat) + b * a.sob;
   const int tmax = (int)((a.grid_t - t0) < kInterpTB ? (a.grid_t - t0) : kInterpTB);
-  for (int i = 0; i < tmax; ++i) {
-    const int64_t t = t0 + i;
-    const int prev = s_prev[i], next = s_next[i];
-    const float w = s_w[i];
-    for (int64_t f = f0 + tid; f < f1; f += kInterpThreads) {
-      float v;
-      if (prev >= 0 && next >= 0)
-        v = (1.0f - w) * ldf(V + prev * a.svt + f) + w * ldf(V + next * a.svt + f);
-      else if (prev >= 0)
-        v = ldf(V + prev * a.svt + f);
-      else if (next >= 0)
-        v = ldf(V + next * a.svt + f);
-      else
-        v = ldf(V + t * a.svt + f);
-      stf(O + t * a.sot + f, v);
+  const int ng = (int)((f1 - f0) / E);  // lane groups per step (E divides the tile)
+  const int total = tmax * ng;
+  constexpr int U = 4;
+  for (int q0 = tid; q0 < total; q0 += U * kInterpThreads) {
+    Lanes<TV, E> vp[U], vn[U];
+    int64_t ot[U], of[U];
+    float wt[U];
+    int mode[U];  // bit 0: prev exists, bit 1: next exists; -1: no pair
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int q = q0 + u * kInterpThreads;
+      mode[u] = -1;
+      if (q < total) {
+        const int i = q / ng;
+        const int64_t f = f0 + (int64_t)(q - i * ng) * E;
+        const int prev = s_prev[i], next = s_next[i];
+        const int64_t t = t0 + i;
+        // row read as "prev" (v_prev, else v_next, else v_cur) and as "next"
+        const int64_t rp = prev >= 0 ? prev : (next >= 0 ? next : t);
+        const int64_t rn = next >= 0 ? next : rp;
+        vp[u].load(V + rp * a.svt + f);
+        vn[u].load(V + rn * a.svt + f);
+        mode[u] = (prev >= 0 ? 1 : 0) | (next >= 0 ? 2 : 0);
+        wt[u] = s_w[i];
+        ot[u] = t;
+        of[u] = f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (mode[u] < 0) continue;
+      Lanes<TV, E> o;
+#pragma unroll
+      for (int j = 0; j < E; ++j)
+        o.v[j] = mode[u] == 3 ? (1.0f - wt[u]) * vp[u].v[j] + wt[u] * vn[u].v[j] : vp[u].v[j];
+      o.store(O + ot[u] * a.sot + of[u]);
     }
   }
 }
@@ -185,12 +251,26 @@ using namespace tssm;
 
 static bool float_dtype(int d) { return d == TSSM_F32 || d == TSSM_BF16 || d == TSSM_F16; }
 
+static int64_t interp_rows(int64_t T, int64_t grid_t, int64_t K) {
+  return grid_t + K < T ? grid_t + K : T;
+}
+
+extern "C" int64_t tssm_time_aware_interp_workspace_bytes(int64_t T, int64_t F, int64_t K,
+                                                          int64_t FTILE, int64_t grid_b,
+                                                          int64_t grid_t, int64_t grid_f) {
+  if (T < 0 || F < 0 || K < 0 || FTILE <= 0 || grid_b < 0 || grid_t < 0 || grid_f < 0) return -1;
+  const int64_t ntile = (F + FTILE - 1) / FTILE;
+  const int64_t gf = grid_f < ntile ? grid_f : ntile;
+  return grid_b * interp_rows(T, grid_t, K) * gf;
+}
+
 extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, const void* V,
                                       const void* M, const void* tau, void* Vhat, int64_t nbatch,
                                       int64_t T, int64_t F, int64_t svb, int64_t svt, int64_t smb,
                                       int64_t smt, int64_t stb, int64_t stt, int64_t sob,
                                       int64_t sot, int64_t K, int64_t FTILE, int64_t grid_b,
-                                      int64_t grid_t, int64_t grid_f, void* stream) {
+                                      int64_t grid_t, int64_t grid_f, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
   TSSM_CHECK(V && M && tau && Vhat, TSSM_ERR_NULL);
   TSSM_CHECK(float_dtype(v_dtype) && float_dtype(m_dtype) && float_dtype(tau_dtype),
              TSSM_ERR_DTYPE);
@@ -202,16 +282,33 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   const int64_t gf = grid_f < ntile ? grid_f : ntile;
   if (grid_b == 0 || grid_t == 0 || gf == 0) return TSSM_OK;
   TSSM_CHECK(gf <= 65535 && grid_b <= 65535, TSSM_ERR_UNSUPPORTED);
-  InterpArgs a{V, M, tau, Vhat, m_dtype, tau_dtype, T, F, svb, svt, smb, smt, stb, stt, sob, sot,
-               K, FTILE, grid_t};
+  const int64_t rows = interp_rows(T, grid_t, K);
+  const int64_t need = grid_b * rows * gf;
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  InterpArgs a{V, M, tau, Vhat, reinterpret_cast<unsigned char*>(workspace), m_dtype, tau_dtype,
+               T, F, svb, svt, smb, smt, stb, stt, sob, sot, K, FTILE, grid_t, rows, gf};
+  const hipStream_t s = as_stream(stream);
+  const int64_t nrow = grid_b * rows;
+  const int64_t wpb = kInterpThreads / 64;
+  TSSM_CHECK((nrow + wpb - 1) / wpb <= 2147483647, TSSM_ERR_UNSUPPORTED);
+  hipLaunchKernelGGL(interp_obs_kernel, dim3((unsigned)((nrow + wpb - 1) / wpb)),
+                     dim3(kInterpThreads), 0, s, a, nrow);
+  const int st = launch_status();
+  if (st != TSSM_OK) return st;
   const dim3 grid((unsigned)((grid_t + kInterpTB - 1) / kInterpTB), (unsigned)gf,
                   (unsigned)grid_b);
-  const hipStream_t s = as_stream(stream);
+  // 16-byte lane groups when every tile, row stride and base pointer allows
+  const int64_t E = v_dtype == TSSM_F32 ? 4 : 8;
+  const bool vec = FTILE % E == 0 && F % E == 0 && svt % E == 0 && sot % E == 0 &&
+                   svb % E == 0 && sob % E == 0 && aligned(V, 16) && aligned(Vhat, 16);
+#define TSSM_INTERP(TT, EE) \
+  hipLaunchKernelGGL((interp_kernel<TT, EE>), grid, dim3(kInterpThreads), 0, s, a)
   switch (v_dtype) {
-    case TSSM_F32: hipLaunchKernelGGL(interp_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
-    case TSSM_BF16: hipLaunchKernelGGL(interp_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL(interp_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+    case TSSM_F32: if (vec) TSSM_INTERP(float, 4); else TSSM_INTERP(float, 1); break;
+    case TSSM_BF16: if (vec) TSSM_INTERP(bf16_t, 8); else TSSM_INTERP(bf16_t, 1); break;
+    default: if (vec) TSSM_INTERP(f16_t, 8); else TSSM_INTERP(f16_t, 1); break;
   }
+#undef TSSM_INTERP
   return launch_status();
 }
 

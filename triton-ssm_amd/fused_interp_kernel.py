@@ -15,6 +15,8 @@ V/Vhat dtype comes from the tensors, M and tau may be any float dtype.
 """
 from __future__ import annotations
 
+import torch
+
 from tssm import _lib
 from tssm.launch import HipKernel, dcode, extent, ival, need_gpu, span, stream_handle
 
@@ -46,11 +48,21 @@ def _launch_interp(grid, a):
     extent(M, span([(gb, g("stride_mb")), (T, g("stride_mt")), (fc, 1)]), "M_ptr")
     extent(tau, span([(gb, g("stride_tb")), (T, g("stride_tt"))]), "tau_ptr")
     extent(O, span([(gb, g("stride_ob")), (gt, g("stride_ot")), (fc, 1)]), "Vhat_ptr")
+    ws = interp_workspace(T, F, K, FT, gb, gt, gf, V.device)
     _lib.call("tssm_time_aware_interp", dcode(V, "V_ptr"), dcode(M, "M_ptr"),
               dcode(tau, "tau_ptr"), V.data_ptr(), M.data_ptr(), tau.data_ptr(), O.data_ptr(),
               nb, T, F, g("stride_vb"), g("stride_vt"), g("stride_mb"), g("stride_mt"),
               g("stride_tb"), g("stride_tt"), g("stride_ob"), g("stride_ot"), K, FT, gb, gt, gf,
-              stream_handle(V))
+              ws.data_ptr(), ws.numel(), stream_handle(V))
+
+
+def interp_workspace(T, F, K, FTILE, gb, gt, gf, device):
+    """Scratch for the per-(b, t, tile) observed flags (freed by torch's
+    caching allocator after the launch is enqueued)."""
+    n = _lib.lib().tssm_time_aware_interp_workspace_bytes(T, F, K, FTILE, gb, gt, gf)
+    if n < 0:
+        raise ValueError("invalid interpolation sizes")
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
 
 
 fused_time_aware_interp_kernel = HipKernel(

@@ -278,11 +278,14 @@ def fused_interp_ssm_forward(V, M, tau, A_log, B, C, D=None, *, K=10, FTILE=128,
     _inner_unit(M, "M")
     Vhat = torch.empty(Bsz, T, F, device=V.device, dtype=V.dtype)
     tau32 = as_f32(tau, "tau").contiguous()
+    nt = -(-F // int(FTILE))
+    nbytes = _lib.lib().tssm_time_aware_interp_workspace_bytes(T, F, int(K), int(FTILE), Bsz, T, nt)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=V.device)
     _lib.call("tssm_time_aware_interp", dcode(V, "V"), dcode(M, "M"), dcode(tau32, "tau"),
               V.data_ptr(), M.data_ptr(), tau32.data_ptr(), Vhat.data_ptr(), Bsz, T, F,
               V.stride(0), V.stride(1), M.stride(0), M.stride(1), tau32.stride(0),
               tau32.stride(1), Vhat.stride(0), Vhat.stride(1), int(K), int(FTILE), Bsz, T,
-              -(-F // int(FTILE)), stream_handle(V))
+              nt, ws.data_ptr(), ws.numel(), stream_handle(V))
     res = selective_scan_forward(Vhat, tau32, A_log, B, C, D, chunk=chunk, disc=disc, h0=h0,
                                  return_state=return_state, dt_is_tau=True)
     if return_state:
