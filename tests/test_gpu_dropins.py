@@ -212,6 +212,25 @@ def test_interp(dev, dtype, name, K, FTILE, p_obs):
     assert_close(out, ref, TOL[dtype] if dtype != torch.float32 else 1e-6, name)
 
 
+@pytest.mark.parametrize("F,FTILE,mdtype,p_obs", [(1000, 300, torch.float32, 0.002),
+                                                   (520, 264, torch.bfloat16, 0.004),
+                                                   (520, 264, torch.float16, 0.004),
+                                                   (96, 8, torch.float32, 0.05)])
+def test_interp_mask_layouts(dev, F, FTILE, mdtype, p_obs):
+    """Observed flags over rows of several 64-vector blocks, tiles spanning blocks,
+    16-bit masks, and sparse masks that leave whole tiles unobserved."""
+    import fused_interp_kernel as fi
+    Bsz, T, K = 2, 90, 6
+    V, M, tau = _interp_inputs(Bsz, T, F, torch.float32, seed=F + FTILE, p_obs=p_obs, dev=dev)
+    Mq = M.to(mdtype)
+    out = torch.full_like(V, float("nan"))
+    fi.fused_time_aware_interp_kernel[(Bsz, T, (F + FTILE - 1) // FTILE)](
+        V, Mq, tau, out, Bsz, T, F, *V.stride(), *Mq.stride(), *tau.stride(), *out.stride(),
+        K=K, FTILE=FTILE)
+    torch.cuda.synchronize()
+    assert_close(out, O.time_aware_interp(V, M, tau, K, FTILE), 1e-6, "interp mask layouts")
+
+
 def test_interp_full_size(dev):
     """B=16 T=2048 F=256, K=10, FTILE=128, 30% missing (the measured interp workload)."""
     import fused_interp_kernel as fi

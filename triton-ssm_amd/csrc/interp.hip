@@ -89,6 +89,74 @@ template <typename TV, int E> struct Lanes {
   }
 };
 
+// Vectorized flags: each wave walks rows of E-lane vectors (16 bytes per
+// lane), all loads of kObsU (row, block) items issued before any reduction.
+// A row's tile sums come from a segmented inclusive scan across the wave
+// keyed by tile index, carried between 64-vector blocks of one row; the lane
+// holding a tile's last vector writes its flag.  Needs FTILE % E == 0 and
+// E-aligned rows.
+constexpr int kObsRowsPerWave = 4;
+constexpr int kObsU = 4;
+
+template <typename TM, int E>
+__global__ __launch_bounds__(kInterpThreads) void interp_obs_vec_kernel(InterpArgs a,
+                                                                       int64_t nrow) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * (kInterpThreads / 64) + (threadIdx.x >> 6);
+  const int64_t r0 = w * kObsRowsPerWave;
+  if (r0 >= nrow) return;  // uniform per wave
+  const int64_t fc = a.F < a.ntile * a.FTILE ? a.F : a.ntile * a.FTILE;
+  const int64_t nvec = fc / E, vpt = a.FTILE / E;
+  const int64_t nblk = (nvec + 63) / 64;
+  const int64_t nr = nrow - r0 < kObsRowsPerWave ? nrow - r0 : kObsRowsPerWave;
+  const int64_t total = nr * nblk;
+  const TM* M = reinterpret_cast<const TM*>(a.M);
+  float carry = 0.0f;
+  int64_t carry_tile = -1;
+  for (int64_t i0 = 0; i0 < total; i0 += kObsU) {
+    float s[kObsU];
+    int64_t vv[kObsU], rr[kObsU];
+#pragma unroll
+    for (int u = 0; u < kObsU; ++u) {
+      const int64_t item = i0 + u;
+      const int64_t rl = (int)item / (int)nblk;  // both below 2^31 (launcher checks)
+      const int64_t r = r0 + rl;
+      const int64_t v = (item - rl * nblk) * 64 + lane;
+      const bool ok = item < total && v < nvec;
+      const int64_t b = r / a.rows, t = r - b * a.rows;
+      // out-of-range lanes read the first vector instead (always in bounds)
+      const int64_t off = ok ? b * a.smb + t * a.smt + v * E : 0;
+      Lanes<TM, E> q;
+      q.load(M + off);
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < E; ++j) sum += q.v[j];
+      s[u] = ok ? sum : 0.0f;
+      vv[u] = ok ? v : -1;
+      rr[u] = r;
+    }
+#pragma unroll
+    for (int u = 0; u < kObsU; ++u) {
+      if (i0 + u >= total) break;  // uniform per wave
+      const int64_t v = vv[u];
+      const int64_t tile = v >= 0 ? (int)v / (int)vpt : -1;
+      if ((int)(i0 + u) % (int)nblk == 0) carry_tile = -1;  // a new row starts
+      float x = s[u];
+      if (lane == 0 && tile == carry_tile) x += carry;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float xo = __shfl_up(x, o);
+        const int64_t to = __shfl_up(tile, o);
+        if (lane >= o && to == tile) x += xo;
+      }
+      const bool last = v >= 0 && ((v + 1) % vpt == 0 || v == nvec - 1);
+      if (last) a.obs[rr[u] * a.ntile + tile] = x > 0.5f ? 1 : 0;
+      carry = __shfl(x, 63);
+      carry_tile = __shfl(tile, 63);
+    }
+  }
+}
+
 template <typename TV, int E>
 __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
   __shared__ unsigned char s_obs[kInterpTB + 2 * kMaxK];
@@ -291,8 +359,25 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   const int64_t nrow = grid_b * rows;
   const int64_t wpb = kInterpThreads / 64;
   TSSM_CHECK((nrow + wpb - 1) / wpb <= 2147483647, TSSM_ERR_UNSUPPORTED);
-  hipLaunchKernelGGL(interp_obs_kernel, dim3((unsigned)((nrow + wpb - 1) / wpb)),
-                     dim3(kInterpThreads), 0, s, a, nrow);
+  // flags: 16-byte mask vectors when tiles and rows are whole vectors
+  const int64_t EM = m_dtype == TSSM_F32 ? 4 : 8;
+  const int64_t fc = F < gf * FTILE ? F : gf * FTILE;
+  if (FTILE % EM == 0 && fc % EM == 0 && smt % EM == 0 && smb % EM == 0 && aligned(M, 16) &&
+      fc / EM < 2147483647 - 64) {
+    const int64_t wv = (nrow + kObsRowsPerWave - 1) / kObsRowsPerWave;
+    const dim3 g((unsigned)((wv + wpb - 1) / wpb));
+    switch (m_dtype) {
+      case TSSM_F32: hipLaunchKernelGGL((interp_obs_vec_kernel<float, 4>), g,
+                                        dim3(kInterpThreads), 0, s, a, nrow); break;
+      case TSSM_BF16: hipLaunchKernelGGL((interp_obs_vec_kernel<bf16_t, 8>), g,
+                                         dim3(kInterpThreads), 0, s, a, nrow); break;
+      default: hipLaunchKernelGGL((interp_obs_vec_kernel<f16_t, 8>), g,
+                                  dim3(kInterpThreads), 0, s, a, nrow); break;
+    }
+  } else {
+    hipLaunchKernelGGL(interp_obs_kernel, dim3((unsigned)((nrow + wpb - 1) / wpb)),
+                       dim3(kInterpThreads), 0, s, a, nrow);
+  }
   const int st = launch_status();
   if (st != TSSM_OK) return st;
   const dim3 grid((unsigned)((grid_t + kInterpTB - 1) / kInterpTB), (unsigned)gf,

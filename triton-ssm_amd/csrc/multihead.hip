@@ -122,6 +122,28 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   const int64_t chan = (MODE == MODE_DIAG) ? (int64_t)h
                                            : (int64_t)h * (P / (8 * NS)) + g / NS;
 
+  // ---- per-channel parameters: raw values loaded first (small, cached), then
+  // the step inputs; transformed after the scheduling barrier below
+  float a2[8];  // a * log2(e) per channel (or per head)
+  float ia[(APH || DISC != TSSM_DISC_ZOH) ? 1 : 8];  // 1 / a per channel (ZOH)
+  if constexpr (APH) {
+    a2[0] = a.A_log[h];
+  } else {
+    const float4* ap = reinterpret_cast<const float4*>(a.A_log + h * P + ch0);
+    const float4 l0 = ap[0], l1 = ap[1];
+    a2[0] = l0.x; a2[1] = l0.y; a2[2] = l0.z; a2[3] = l0.w;
+    a2[4] = l1.x; a2[5] = l1.y; a2[6] = l1.z; a2[7] = l1.w;
+  }
+  float Dv[8];
+  if constexpr (HAS_D && MODE == MODE_MAMBA1) {
+    Dv[0] = a.D[chan];
+  } else if constexpr (HAS_D) {
+    const float4* dp4 = reinterpret_cast<const float4*>(a.D + h * P + ch0);
+    const float4 d0 = dp4[0], d1 = dp4[1];
+    Dv[0] = d0.x; Dv[1] = d0.y; Dv[2] = d0.z; Dv[3] = d0.w;
+    Dv[4] = d1.x; Dv[5] = d1.y; Dv[6] = d1.z; Dv[7] = d1.w;
+  }
+
   // ---- loads (all issued before any use)
   Vec8<T> vu[R], vB[R], vC[R];
   float us[R];  // MODE_MAMBA1: the channel's input, shared by its 8 state lanes
@@ -133,45 +155,44 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     const T* Bp = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h + bc + t0 * a.sB_l;
     const T* Cp = reinterpret_cast<const T*>(a.C) + b * a.sC_b + h * a.sC_h + bc + t0 * a.sC_l;
     const float* dp = a.dt + b * a.sdt_b + chan * a.sdt_h + t0 * a.sdt_l;
+    // Steps past the end read row L-1 instead (no branch around the loads, so
+    // no wait between them) and become identity steps through dt = 0:
+    // Abar = 1 and a zero input term whatever u, B and C hold.
+    const int64_t back = a.L - 1 - t0;  // row L-1 relative to t0
+    const T* up_l = up + back * a.su_l;
+    const T* Bp_l = Bp + back * a.sB_l;
+    const T* Cp_l = Cp + back * a.sC_l;
+    const float* dp_l = dp + back * a.sdt_l;
+    float draw[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (t0 + r < a.L) {
-        if constexpr (MODE == MODE_DIAG) vu[r].load_nt(up + r * a.su_l);
-        else us[r] = ldf(up + r * a.su_l);
-        vB[r].load_nt(Bp + r * a.sB_l);
-        vC[r].load_nt(Cp + r * a.sC_l);
-        dtv[r] = dp[r * a.sdt_l];
-        if (a.dt_is_tau) dtv[r] -= (t0 + r > 0) ? dp[(r - 1) * a.sdt_l] : 0.0f;
-      } else {
-        if constexpr (MODE == MODE_DIAG) vu[r].zero();
-        else us[r] = 0.0f;
-        vB[r].zero();
-        vC[r].zero();
-        dtv[r] = 0.0f;  // identity step: Abar = 1, input term 0
-      }
+      const bool in = t0 + r < a.L;
+      if constexpr (MODE == MODE_DIAG) vu[r].load_nt(in ? up + r * a.su_l : up_l);
+      else us[r] = ldf(in ? up + r * a.su_l : up_l);
+      vB[r].load_nt(in ? Bp + r * a.sB_l : Bp_l);
+      vC[r].load_nt(in ? Cp + r * a.sC_l : Cp_l);
+      draw[r] = *(in ? dp + r * a.sdt_l : dp_l);
+    }
+    // timestamp of step t0 - 1 (read when dt holds timestamps; row 0 for t0 = 0)
+    const float tprev = *(t0 == 0 ? dp : (t0 <= a.L ? dp - a.sdt_l : dp_l));
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float d = draw[r];
+      if (a.dt_is_tau) d -= (t0 + r > 0) ? (r > 0 ? draw[r - 1] : tprev) : 0.0f;
+      dtv[r] = (t0 + r < a.L) ? d : 0.0f;
     }
   }
-  float a2[8];  // a * log2(e) per channel (or per head)
   if constexpr (APH) {
-    const float v = -expf(a.A_log[h]) * kLog2e;
+    const float v = -expf(a2[0]) * kLog2e;
 #pragma unroll
     for (int j = 0; j < 8; ++j) a2[j] = v;
   } else {
-    const float4* ap = reinterpret_cast<const float4*>(a.A_log + h * P + ch0);
-    const float4 l0 = ap[0], l1 = ap[1];
-    a2[0] = l0.x; a2[1] = l0.y; a2[2] = l0.z; a2[3] = l0.w;
-    a2[4] = l1.x; a2[5] = l1.y; a2[6] = l1.z; a2[7] = l1.w;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) a2[j] = -expf(a2[j]) * kLog2e;
-  }
-  float Dv[8];
-  if constexpr (HAS_D && MODE == MODE_MAMBA1) {
-    Dv[0] = a.D[chan];
-  } else if constexpr (HAS_D) {
-    const float4* dp4 = reinterpret_cast<const float4*>(a.D + h * P + ch0);
-    const float4 d0 = dp4[0], d1 = dp4[1];
-    Dv[0] = d0.x; Dv[1] = d0.y; Dv[2] = d0.z; Dv[3] = d0.w;
-    Dv[4] = d1.x; Dv[5] = d1.y; Dv[6] = d1.z; Dv[7] = d1.w;
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (DISC == TSSM_DISC_ZOH) ia[j] = -expf(-a2[j]);
+      a2[j] = -expf(a2[j]) * kLog2e;
+    }
   }
 
   // ---- sweep 1: discretize + run-local scan from (1, 0)
@@ -206,8 +227,8 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       } else {
         const float arg = dtv[r] * a2[j];
         ab = exp2_fast(arg);
-        coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * dtv[r]
-                                       : dtv[r];
+        if constexpr (DISC == TSSM_DISC_ZOH) coef = zoh_coef2(arg, ab, dtv[r], ia[j]);
+        else coef = dtv[r];
       }
       const float uj = (MODE == MODE_DIAG) ? vu[r].get(j) : us[r];
       xl[j] = __builtin_fmaf(ab, xl[j], coef * vB[r].get(j) * uj);
