@@ -275,7 +275,7 @@ def main():
                     help="only run torch copies of a 256 MiB buffer (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE to bytes); prints nothing else")
     ap.add_argument("--sets", type=int, default=3)
-    ap.add_argument("--scan-chunk", type=int, default=128,
+    ap.add_argument("--scan-chunk", type=int, default=256,
                     help="interp_mamba1: steps per chunk of the selective scan")
     ap.add_argument("--ssd-chunk", type=int, default=256,
                     help="steps per chunk of the SSD scan passes (multiple of 64, <= 1024)")

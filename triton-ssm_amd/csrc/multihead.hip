@@ -190,8 +190,9 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       vC[r].load_nt(in ? Cp + r * a.sC_l : Cp_l);
       draw[r] = *(in ? dp + r * a.sdt_l : dp_l);
     }
-    // timestamp of step t0 - 1 (read when dt holds timestamps; row 0 for t0 = 0)
-    const float tprev = *(t0 == 0 ? dp : (t0 <= a.L ? dp - a.sdt_l : dp_l));
+    // timestamp of step t0 - 1 when dt holds timestamps (row 0 for t0 = 0)
+    float tprev = 0.0f;
+    if (a.dt_is_tau) tprev = *(t0 == 0 ? dp : (t0 <= a.L ? dp - a.sdt_l : dp_l));
     __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
 #pragma unroll
     for (int r = 0; r < R; ++r) {

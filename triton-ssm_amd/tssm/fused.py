@@ -260,7 +260,7 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
 
 
 def fused_interp_ssm_forward(V, M, tau, A_log, B, C, D=None, *, K=10, FTILE=128, disc="zoh",
-                             chunk=128, h0=None, return_state=False):
+                             chunk=256, h0=None, return_state=False):
     """Interpolation of irregular observations followed by a Mamba-1 scan.
 
     V, M [Bsz, T, F] (M > 0.5 observed, tested through FTILE-wide tile sums as
