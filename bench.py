@@ -9,6 +9,7 @@ x/B/C/y, fp32 dt and state, ZOH discretization fused into the load stage.
   mamba1_small   Mamba-1 selective scan B=2 L=256 D=16 N=16 fp32
   interp_mamba1  interpolation + Mamba-1 scan B=16 T=2048 F=256 N=16 fp32
   ssd_long       SSD scan B=1 L=262144 H=8 P=64 N=16 bf16, chunk 256
+  ssd_config1    SSD scan on the headline shapes B=8 L=4096 H=16 P=N=64 bf16
   ssd_stream     streaming SSD step, 4096 streams H=32 P=64 N=128 fp32 state
 
 A step is one pass of the path over one batch of seeded synthetic input that
@@ -95,6 +96,50 @@ def wl_multihead(args, dev):
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, kernel="mh_scan_fused_kernel",
                 metric=HEADLINE_METRIC, unit="elements/s", config=cfg,
                 traffic="mh_scan_fused_traffic.json")
+
+
+def wl_ssd_config1(args, dev):
+    """The SSD form (state P x N per head) on the headline shapes: the same seeded
+    x, B, C, dt and per-head A_log as the DIAG workload, x read as [B, L, H, P]."""
+    import torch
+    from tssm import ssd_scan_forward, workloads
+    B, L, H, P = 8, 4096, 16, 64
+    w = workloads.multihead(B=B, L=L, H=H, P=P)
+    base = {"x": w["u"].view(B, L, H, P), "B": w["B"], "C": w["C"], "dt": w["dt"]}
+    base = {k: v.to(dev) for k, v in base.items()}
+    A_log = w["A_log_h"].to(dev)
+    N = base["B"].shape[-1]
+    sets = []
+    for i in range(args.sets):
+        s = {k: torch.roll(v, shifts=i, dims=0).contiguous() for k, v in base.items()}
+        s["y"] = torch.empty_like(s["x"])
+        sets.append(s)
+
+    def step(i):
+        s = sets[i % len(sets)]
+        ssd_scan_forward(s["x"], s["dt"], A_log, s["B"], s["C"], None, chunk=args.ssd_chunk,
+                         disc=args.disc, out=s["y"])
+
+    def cpu():
+        from oracle import cport
+        Bs = 1
+        arrs = [_np32(w["u"][:Bs].view(Bs, L, H, P)), _np32(w["dt"][:Bs]), _np32(w["A_log_h"]),
+                _np32(w["B"][:Bs]), _np32(w["C"][:Bs])]
+        med = _timed_cpu(lambda: cport.ssd_scan(*arrs, None, None, disc=args.disc), args.cpu_reps)
+        return {"value": Bs * L * H * P / med, "unit": "elements/s", "cores": cport.threads(),
+                "kind": "port", "sample": f"batch 0 of {B}, median of {args.cpu_reps} runs, "
+                                          f"{med:.3f} s each"}
+
+    n = B * L * H * P
+    nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
+                kernel="ssd_state_kernel + ssd_pass_kernel + ssd_out_kernel",
+                metric="SSD scan elements/sec on the headline shapes, B=8 L=4096 H=16 P=N=64 bf16",
+                unit="elements/s",
+                config={"workload": "SSD scan (decay per head, P x N state) on the DIAG headline "
+                                    f"shapes, B=8 L=4096 H=16 P=N=64, chunk {args.ssd_chunk}, "
+                                    f"bf16 I/O, fp32 state, {args.disc.upper()}",
+                        "B": B, "L": L, "H": H, "P": P, "N": N, "chunk": args.ssd_chunk})
 
 
 def wl_mamba1_small(args, dev):
@@ -245,6 +290,7 @@ def wl_ssd_stream(args, dev):
 
 WORKLOADS = {"multihead": wl_multihead, "mamba1_small": wl_mamba1_small,
              "interp_mamba1": wl_interp_mamba1, "ssd_long": wl_ssd_long,
+             "ssd_config1": wl_ssd_config1,
              "ssd_stream": wl_ssd_stream}
 
 

@@ -217,7 +217,7 @@ int tssm_stream_interp_step(float* ring_V, float* ring_M, float* ring_tau, int32
  * lane by lane.  Single pass with decoupled look-back; workspace rules as for
  * tssm_mh_scan_fused.  x, B, C, y in `dtype` ([B,L,H,P] / [B,L,H,N]); dt f32
  * [B,L,H]; A_log f32 [H]; D f32 [H*P] or NULL; h0/h_last f32 [B,H,P,N] or
- * NULL.  P <= 64, N in {8, 16, 32}; innermost strides 1. */
+ * NULL.  P <= 64, N in {8, 16, 32, 64}; innermost strides 1. */
 int64_t tssm_ssd_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t H, int64_t P,
                                       int64_t N, int64_t chunk);
 int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt, const float* A_log,
@@ -262,6 +262,60 @@ int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt, int
                         int64_t sdt_l, int64_t sdt_d, int64_t sB_b, int64_t sB_l, int64_t sC_b,
                         int64_t sC_l, int64_t sy_b, int64_t sy_l, int64_t chunk, void* workspace,
                         int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ model layers
+ * The reference's layers around the scan.  Arithmetic fp32; every float
+ * tensor of one call has `dtype` (TSSM_F32/BF16/F16).  Rows are the
+ * (grid_b x grid_l) programs of the reference grid; innermost strides 1. */
+
+/* layernorm_kernel (fused_ssm_interp.py:105-129): out = (x-mu)/sqrt(var+eps)*w
+ * + bias per row of H (x and out share strides).  block_h >= H is the
+ * reference's BLOCK_H: its H..BLOCK_H-1 masked lanes enter var as mu^2. */
+int tssm_layernorm_fwd(int dtype, const void* x, const void* w, const void* bias, void* out,
+                       int64_t nbatch, int64_t L, int64_t H, int64_t stride_b, int64_t stride_l,
+                       float eps, int64_t block_h, int64_t grid_b, int64_t grid_l, void* stream);
+
+/* layernorm_bwd_kernel (fused_ssm_interp.py:134-171): dx per row (dout, x, dx
+ * share strides); dw += sum_rows dout*xhat and db += sum_rows dout, summed in a
+ * fixed order (the reference adds atomically).  Workspace:
+ * tssm_layernorm_bwd_workspace_bytes(grid_b, grid_l, H) bytes, 16-aligned. */
+int64_t tssm_layernorm_bwd_workspace_bytes(int64_t grid_b, int64_t grid_l, int64_t H);
+int tssm_layernorm_bwd(int dtype, const void* dout, const void* x, const void* w, void* dx,
+                       void* dw, void* db, int64_t nbatch, int64_t L, int64_t H, int64_t stride_b,
+                       int64_t stride_l, float eps, int64_t block_h, int64_t grid_b,
+                       int64_t grid_l, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* swiglu_kernel / swiglu_bwd_kernel (fused_ssm_interp.py:174-217): out =
+ * silu(gate)*up; dup = dout*silu(gate), dgate = dout*up*sig*(1+gate*(1-sig)).
+ * All tensors of a call share strides. */
+int tssm_swiglu_fwd(int dtype, const void* gate, const void* up, void* out, int64_t nbatch,
+                    int64_t L, int64_t H, int64_t stride_b, int64_t stride_l, int64_t grid_b,
+                    int64_t grid_l, void* stream);
+int tssm_swiglu_bwd(int dtype, const void* dout, const void* gate, const void* up, void* dgate,
+                    void* dup, int64_t nbatch, int64_t L, int64_t H, int64_t stride_b,
+                    int64_t stride_l, int64_t grid_b, int64_t grid_l, void* stream);
+
+/* residual_add_kernel / dropout_residual_kernel (multihead_ssm_kernel.py:191-222)
+ * over the first n elements (contiguous): out = x + res, or with a uint8 keep
+ * mask out = x*keep/p_keep + res.  keep NULL: plain residual add. */
+int tssm_residual_add(int dtype, const void* x, const void* res, const uint8_t* keep, void* out,
+                      int64_t n, float p_keep, void* stream);
+
+/* mean_pool_logit_kernel (streaming_inference_kernel.py:160-194): out[b] =
+ * sum_{t,h} W[h] h[b,t,h] / (T*H + 1e-9) + bias[0] for b < grid_b; reduced
+ * in a fixed order.  Workspace: tssm_mean_pool_logit_workspace_bytes(grid_b,
+ * T) bytes. */
+int64_t tssm_mean_pool_logit_workspace_bytes(int64_t grid_b, int64_t T);
+int tssm_mean_pool_logit(int dtype, const void* h, const void* W, const void* bias, void* out,
+                         int64_t nbatch, int64_t nt, int64_t H, int64_t stride_b,
+                         int64_t stride_t, int64_t grid_b, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/* masked_fill_zero_kernel (streaming_inference_kernel.py:198-214): out[i] =
+ * mask[i / H] > 0 ? x[i] : 0 over the first n elements (contiguous [B,T,H],
+ * mask [B,T]).  mask_code: 0 f32, 1 bf16, 2 f16, 3 int32, 4 uint8/bool. */
+int tssm_masked_fill_zero(int dtype, int mask_code, const void* x, const void* mask, void* out,
+                          int64_t n, int64_t H, void* stream);
 
 #ifdef __cplusplus
 }

@@ -41,6 +41,12 @@ time_aware_interp     hand-built known-answer cases (boundaries, nearest
 streaming_*           k steps == elementwise scan; ring known-answer cases.
 zoh_discretize_bwd    torch.autograd of a torch float64 ZOH forward.
 dt_project_softplus   torch.nn.functional.softplus + clamp in float64.
+layernorm(_bwd)       torch.nn.functional.layer_norm and its autograd (BLOCK_H =
+                      H); for BLOCK_H > H a torch float64 emulation of the
+                      masked block (rows zero-padded to BLOCK_H) and its autograd.
+swiglu(_bwd)          torch.nn.functional.silu and autograd.
+residual/dropout, mean_pool_logit, masked_fill_zero
+                      torch elementwise / reduction equivalents and known answers.
 """
 from __future__ import annotations
 
@@ -55,6 +61,8 @@ __all__ = [
     "multihead_forward", "selective_scan", "ssd_scan", "ssd_stream_step",
     "time_aware_interp", "interp_ssm_step", "fused_interp_ssm",
     "streaming_step", "streaming_interp_step",
+    "layernorm", "layernorm_bwd", "swiglu", "swiglu_bwd", "residual_add", "dropout_residual",
+    "mean_pool_logit", "masked_fill_zero",
 ]
 
 
@@ -668,3 +676,83 @@ def streaming_interp_step(ring_V, ring_M, ring_tau, ring_head, v_new, m_new, tau
     h_new = Abar * h + Bbar * vhat                                       # :152-153
     y = C * h_new + D * vhat
     return ring_V, ring_M, ring_tau, head, h_new, y
+
+
+# --------------------------------------------------------------------------
+# model layers around the scan (fused_ssm_interp.py, multihead_ssm_kernel.py,
+# streaming_inference_kernel.py)
+# --------------------------------------------------------------------------
+def layernorm(x, w, bias, EPS, BLOCK_H=None):
+    """layernorm_kernel, fused_ssm_interp.py:105-129: per-row normalisation
+    over the last axis (H).  The kernel's masked lanes H..BLOCK_H-1 load 0
+    (:120), so they enter the variance as (0 - mu)^2 (:121-123):
+    var = (sum_h (x_h - mu)^2 + (BLOCK_H - H) mu^2) / H.  BLOCK_H=None: H."""
+    x, w, bias = _f64(x), _f64(w), _f64(bias)
+    H = x.shape[-1]
+    pad = (BLOCK_H or H) - H
+    mu = x.sum(-1, keepdims=True) / H
+    xc = x - mu
+    var = ((xc * xc).sum(-1, keepdims=True) + pad * mu * mu) / H
+    return xc / np.sqrt(var + EPS) * w + bias
+
+
+def layernorm_bwd(dout, x, w, EPS, BLOCK_H=None):
+    """layernorm_bwd_kernel, fused_ssm_interp.py:134-171.  Returns (dx, dw, db)
+    with dw/db the sums over all rows that the kernel adds into its dw/db
+    buffers (:169-170).  The padded lanes of the block enter var and the
+    sum of -2 xc (:154,163) as in ``layernorm``."""
+    dout, x, w = _f64(dout), _f64(x), _f64(w)
+    H = x.shape[-1]
+    pad = (BLOCK_H or H) - H
+    mu = x.sum(-1, keepdims=True) / H                                     # :152
+    xc = x - mu
+    var = ((xc * xc).sum(-1, keepdims=True) + pad * mu * mu) / H          # :154
+    inv = 1.0 / np.sqrt(var + EPS)
+    xhat = xc * inv
+    dxhat = dout * w                                                      # :158
+    dvar = (dxhat * xc).sum(-1, keepdims=True) * -0.5 * (var + EPS) ** -1.5
+    sum_m2xc = (-2.0 * xc).sum(-1, keepdims=True) + 2.0 * pad * mu        # padded xc = -mu
+    dmu = (dxhat * -inv).sum(-1, keepdims=True) + dvar * sum_m2xc / H
+    dx = dxhat * inv + dvar * 2.0 * xc / H + dmu / H                      # :165
+    lead = tuple(range(x.ndim - 1))
+    return dx, (dout * xhat).sum(lead), dout.sum(lead)
+
+
+def swiglu(gate, up):
+    """swiglu_kernel, fused_ssm_interp.py:174-191: silu(gate) * up."""
+    gate, up = _f64(gate), _f64(up)
+    return gate / (1.0 + np.exp(-gate)) * up
+
+
+def swiglu_bwd(dout, gate, up):
+    """swiglu_bwd_kernel, fused_ssm_interp.py:194-217.  Returns (dgate, dup)."""
+    dout, gate, up = _f64(dout), _f64(gate), _f64(up)
+    sig = 1.0 / (1.0 + np.exp(-gate))
+    silu = gate * sig
+    return dout * up * sig * (1.0 + gate * (1.0 - sig)), dout * silu
+
+
+def residual_add(x, res):
+    """residual_add_kernel, multihead_ssm_kernel.py:191-202."""
+    return _f64(x) + _f64(res)
+
+
+def dropout_residual(x, res, mask, p_keep):
+    """dropout_residual_kernel, multihead_ssm_kernel.py:205-222: inverted
+    dropout with a pre-drawn uint8 keep mask, then the residual add."""
+    return _f64(x) * _f64(mask) * (1.0 / p_keep) + _f64(res)
+
+
+def mean_pool_logit(h, W, bias):
+    """mean_pool_logit_kernel, streaming_inference_kernel.py:160-194:
+    logit[b] = sum_{t,h} W[h] h[b,t,h] / (T H + 1e-9) + bias."""
+    h, W = _f64(h), _f64(W)
+    _, T, H = h.shape
+    return (h * W).sum((1, 2)) / (T * H + 1e-9) + float(_f64(bias).reshape(-1)[0])
+
+
+def masked_fill_zero(x, mask):
+    """masked_fill_zero_kernel, streaming_inference_kernel.py:198-214: x where
+    mask[b, t] > 0 (broadcast over H), else 0."""
+    x, mask = _f64(x), _f64(mask)
+    return np.where(mask[..., None] > 0, x, 0.0)

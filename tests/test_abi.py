@@ -8,6 +8,7 @@
 import ctypes
 
 import pytest
+import torch
 
 from tssm import _lib
 from tssm.launch import HipKernel, normalize_grid, span
@@ -104,7 +105,21 @@ def test_launcher_binding():
     assert span([(3, 10), (2, 1)]) == 21 and span([(0, 5)]) == -1
 
 
-def test_not_built_symbols_raise():
+def test_layer_launchers_validate_on_host():
+    """Model-layer drop-ins bind the reference's parameter lists and reject
+    host tensors before any library call."""
     import fused_ssm_interp as fs
-    with pytest.raises(NotImplementedError):
-        fs.layernorm_kernel[(1,)](*range(12))
+    import multihead_ssm_kernel as mk
+    import streaming_inference_kernel as sk
+    x = torch.zeros(2, 3, 8)
+    w = torch.zeros(8)
+    with pytest.raises(ValueError):
+        fs.layernorm_kernel[(2, 3)](x, w, w, x, 2, 3, 8, 24, 8, 1, 1e-5, 8)
+    with pytest.raises(ValueError):
+        fs.swiglu_kernel[(2, 3)](x, x, x, 2, 3, 8, 24, 8, BLOCK_H=8)
+    with pytest.raises(ValueError):
+        mk.residual_add_kernel[(1,)](x, x, x, 48, BLOCK=64)
+    with pytest.raises(ValueError):
+        sk.masked_fill_zero_kernel[(1,)](x, torch.ones(2, 3), x, 2, 3, 8, BLOCK=64)
+    with pytest.raises(TypeError):
+        sk.mean_pool_logit_kernel[(2,)](x, w, w, w)   # missing arguments

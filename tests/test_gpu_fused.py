@@ -26,7 +26,7 @@ def _ssd_inputs(dev, Bsz, L, H, P, N, dtype, seed, heavy=False):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("disc", ["zoh", "euler"])
-@pytest.mark.parametrize("P,N", [(64, 16), (32, 8), (48, 32)])
+@pytest.mark.parametrize("P,N", [(64, 16), (32, 8), (48, 32), (64, 64)])
 def test_ssd_scan(dev, dtype, disc, P, N):
     from tssm import ssd_scan_forward
     d = _ssd_inputs(dev, 2, 1100, 3, P, N, dtype, seed=P + N, heavy=True)

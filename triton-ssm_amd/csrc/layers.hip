@@ -1,0 +1,440 @@
+// Model layers around the scan: LayerNorm forward/backward and SwiGLU
+// forward/backward (fused_ssm_interp.py:105-217), residual add and inverted
+// dropout + residual (multihead_ssm_kernel.py:191-222), the mean-pool logit
+// head and the padding mask (streaming_inference_kernel.py:160-214).
+//
+// All HBM-bound.  Row kernels (LayerNorm) give one wave per row, the row's
+// elements strided over the 64 lanes so every load instruction reads 64
+// consecutive elements; the 2-3 passes over a row re-read it from L1/L2.
+// Elementwise kernels are flat grid-stride loops.  Reductions that the
+// reference does with atomics (LayerNorm's dw/db, :169-170) are done in a
+// fixed order instead, so results are deterministic:
+//   layernorm_bwd_row_kernel   dx per row + the row's (mu, 1/sigma)
+//   ln_param_partial_kernel    column partial sums of dout*xhat, dout over
+//                              blocks of kLnRowBlock rows
+//   ln_param_final_kernel      partials summed in block order, added to dw/db
+// mean_pool_logit reduces each batch's T*H products over blocks of rows, then
+// the block partials in order.
+//
+// Arithmetic is fp32 for every I/O dtype (fp32, bf16, fp16).
+#include "common.h"
+
+namespace tssm {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kLnRowBlock = 128;   // rows per column-partial block
+constexpr int kPoolRows = 64;      // (t) rows per mean-pool block
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Row r of a (grid_b x grid_l) launch -> element offset of its first element.
+struct Rows {
+  int64_t grid_l, sb, sl;
+  __device__ int64_t base(int64_t r) const {
+    const int64_t b = r / grid_l, l = r - b * grid_l;
+    return b * sb + l * sl;
+  }
+};
+
+// mean and 1/sqrt(var + eps) of a row; `pad` = BLOCK_H - H masked lanes of
+// the reference's block, which enter the variance as (0 - mu)^2.
+template <typename T>
+__device__ inline void row_stats(const T* x, int64_t H, int64_t pad, float eps, int lane,
+                                 float* mu_out, float* inv_out) {
+  float s = 0.0f;
+  for (int64_t h = lane; h < H; h += 64) s += ldf(x + h);
+  const float mu = wave_sum(s) / (float)H;
+  float q = 0.0f;
+  for (int64_t h = lane; h < H; h += 64) {
+    const float c = ldf(x + h) - mu;
+    q = __builtin_fmaf(c, c, q);
+  }
+  const float var = (wave_sum(q) + (float)pad * mu * mu) / (float)H;
+  *mu_out = mu;
+  *inv_out = 1.0f / sqrtf(var + eps);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void layernorm_fwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+    T* __restrict__ out, Rows rows, int64_t nrow, int64_t H, int64_t pad, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wpb = kThreads / 64;
+  for (int64_t r = blockIdx.x * wpb + (threadIdx.x >> 6); r < nrow; r += (int64_t)gridDim.x * wpb) {
+    const int64_t o = rows.base(r);
+    float mu, inv;
+    row_stats(x + o, H, pad, eps, lane, &mu, &inv);
+    for (int64_t h = lane; h < H; h += 64)
+      stf(out + o + h, __builtin_fmaf((ldf(x + o + h) - mu) * inv, ldf(w + h), ldf(bias + h)));
+  }
+}
+
+// dx of a row (fused_ssm_interp.py:148-166) and its (mu, inv) for the
+// parameter-gradient pass.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void layernorm_bwd_row_kernel(
+    const T* __restrict__ dout, const T* __restrict__ x, const T* __restrict__ w,
+    T* __restrict__ dx, float* __restrict__ stats, Rows rows, int64_t nrow, int64_t H,
+    int64_t pad, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wpb = kThreads / 64;
+  for (int64_t r = blockIdx.x * wpb + (threadIdx.x >> 6); r < nrow; r += (int64_t)gridDim.x * wpb) {
+    const int64_t o = rows.base(r);
+    float mu, inv;
+    row_stats(x + o, H, pad, eps, lane, &mu, &inv);
+    float s_dxc = 0.0f, s_dx = 0.0f, s_xc = 0.0f;
+    for (int64_t h = lane; h < H; h += 64) {
+      const float xc = ldf(x + o + h) - mu;
+      const float dxh = ldf(dout + o + h) * ldf(w + h);
+      s_dxc = __builtin_fmaf(dxh, xc, s_dxc);
+      s_dx += dxh;
+      s_xc += xc;
+    }
+    s_dxc = wave_sum(s_dxc);
+    s_dx = wave_sum(s_dx);
+    s_xc = wave_sum(s_xc);
+    // (var + eps)^-1.5 = inv^3; the padded lanes hold xc = -mu
+    const float dvar = s_dxc * -0.5f * inv * inv * inv;
+    const float sum_m2xc = -2.0f * s_xc + 2.0f * (float)pad * mu;
+    const float dmu = -inv * s_dx + dvar * sum_m2xc / (float)H;
+    const float k2 = 2.0f * dvar / (float)H, k0 = dmu / (float)H;
+    for (int64_t h = lane; h < H; h += 64) {
+      const float xc = ldf(x + o + h) - mu;
+      const float dxh = ldf(dout + o + h) * ldf(w + h);
+      stf(dx + o + h, __builtin_fmaf(dxh, inv, __builtin_fmaf(k2, xc, k0)));
+    }
+    if (lane == 0) {
+      stats[2 * r] = mu;
+      stats[2 * r + 1] = inv;
+    }
+  }
+}
+
+// Column partials over row block blockIdx.y: part[blk][h] = sum dout*xhat,
+// part[nblk + blk][h] = sum dout (rows in ascending order).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ln_param_partial_kernel(
+    const T* __restrict__ dout, const T* __restrict__ x, const float* __restrict__ stats,
+    float* __restrict__ part, Rows rows, int64_t nrow, int64_t H, int64_t nblk) {
+  const int64_t h = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (h >= H) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kLnRowBlock;
+  const int64_t r1 = r0 + kLnRowBlock < nrow ? r0 + kLnRowBlock : nrow;
+  float sw = 0.0f, sb = 0.0f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const int64_t o = rows.base(r) + h;
+    const float d = ldf(dout + o);
+    sw = __builtin_fmaf(d, (ldf(x + o) - stats[2 * r]) * stats[2 * r + 1], sw);
+    sb += d;
+  }
+  part[blockIdx.y * H + h] = sw;
+  part[(nblk + blockIdx.y) * H + h] = sb;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ln_param_final_kernel(
+    const float* __restrict__ part, T* __restrict__ dw, T* __restrict__ db, int64_t H,
+    int64_t nblk) {
+  const int64_t h = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (h >= H) return;
+  float sw = 0.0f, sb = 0.0f;
+  for (int64_t k = 0; k < nblk; ++k) {
+    sw += part[k * H + h];
+    sb += part[(nblk + k) * H + h];
+  }
+  stf(dw + h, ldf(dw + h) + sw);
+  stf(db + h, ldf(db + h) + sb);
+}
+
+__device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// Elements of (grid_b x grid_l) rows of H, flat: element i -> row i / H.
+struct RowElems {
+  Rows rows;
+  int64_t H;
+  __device__ int64_t off(int64_t i) const {
+    const int64_t r = i / H;
+    return rows.base(r) + (i - r * H);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_kernel(
+    const T* __restrict__ gate, const T* __restrict__ up, T* __restrict__ out, RowElems e,
+    int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const int64_t o = e.off(i);
+    const float g = ldf(gate + o);
+    stf(out + o, g * sigmoid(g) * ldf(up + o));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
+    const T* __restrict__ dout, const T* __restrict__ gate, const T* __restrict__ up,
+    T* __restrict__ dgate, T* __restrict__ dup, RowElems e, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const int64_t o = e.off(i);
+    const float g = ldf(gate + o), u = ldf(up + o), d = ldf(dout + o);
+    const float s = sigmoid(g);
+    stf(dup + o, d * g * s);
+    stf(dgate + o, d * u * s * __builtin_fmaf(g, 1.0f - s, 1.0f));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void residual_kernel(
+    const T* __restrict__ x, const T* __restrict__ res, const uint8_t* __restrict__ keep,
+    T* __restrict__ out, int64_t n, float scale) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads) {
+    const float xv = keep ? ldf(x + i) * (float)keep[i] * scale : ldf(x + i);
+    stf(out + i, xv + ldf(res + i));
+  }
+}
+
+// Partial dot products of W with rows [blockIdx.y * kPoolRows, +kPoolRows) of
+// batch blockIdx.x.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void pool_partial_kernel(
+    const T* __restrict__ h, const T* __restrict__ W, float* __restrict__ part, int64_t T_,
+    int64_t H, int64_t sb, int64_t st, int64_t nblk) {
+  __shared__ float s_w[kThreads / 64];
+  const int64_t b = blockIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.y * kPoolRows;
+  const int64_t t1 = t0 + kPoolRows < T_ ? t0 + kPoolRows : T_;
+  float acc = 0.0f;
+  for (int64_t t = t0; t < t1; ++t) {
+    const T* row = h + b * sb + t * st;
+    for (int64_t k = threadIdx.x; k < H; k += kThreads) acc = __builtin_fmaf(ldf(W + k), ldf(row + k), acc);
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kThreads / 64; ++k) s += s_w[k];
+    part[b * nblk + blockIdx.y] = s;
+  }
+}
+
+template <typename T>
+__global__ void pool_final_kernel(const float* __restrict__ part, const T* __restrict__ bias,
+                                  T* __restrict__ out, int64_t nb, int64_t nblk, float denom) {
+  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nb) return;
+  float s = 0.0f;
+  for (int64_t k = 0; k < nblk; ++k) s += part[b * nblk + k];
+  stf(out + b, s / denom + ldf(bias));
+}
+
+// mask codes: 0 f32, 1 bf16, 2 f16 (the library's), 3 i32, 4 u8 / bool
+__device__ inline bool mask_on(const void* m, int64_t i, int code) {
+  switch (code) {
+    case TSSM_F32: return reinterpret_cast<const float*>(m)[i] > 0.0f;
+    case TSSM_BF16: return ldf(reinterpret_cast<const bf16_t*>(m) + i) > 0.0f;
+    case TSSM_F16: return ldf(reinterpret_cast<const f16_t*>(m) + i) > 0.0f;
+    case 3: return reinterpret_cast<const int32_t*>(m)[i] > 0;
+    default: return reinterpret_cast<const uint8_t*>(m)[i] > 0;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void masked_fill_kernel(
+    const T* __restrict__ x, const void* __restrict__ mask, int mcode, T* __restrict__ out,
+    int64_t n, int64_t H) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    stf(out + i, mask_on(mask, i / H, mcode) ? ldf(x + i) : 0.0f);
+}
+
+// Grid of a flat loop over n items: enough workgroups to fill the chip, at
+// most one item per thread.
+inline unsigned flat_grid(int64_t n) {
+  const int64_t g = (n + kThreads - 1) / kThreads;
+  return (unsigned)(g < 8192 ? (g < 1 ? 1 : g) : 8192);
+}
+inline unsigned row_grid(int64_t nrow) {
+  const int64_t g = (nrow + kThreads / 64 - 1) / (kThreads / 64);
+  return (unsigned)(g < 8192 ? (g < 1 ? 1 : g) : 8192);
+}
+inline bool io_dtype(int d) { return d == TSSM_F32 || d == TSSM_BF16 || d == TSSM_F16; }
+
+#define TSSM_DISPATCH(dtype, LAUNCH)            \
+  switch (dtype) {                              \
+    case TSSM_F32: { using T = float; LAUNCH; } break;   \
+    case TSSM_BF16: { using T = bf16_t; LAUNCH; } break; \
+    default: { using T = f16_t; LAUNCH; } break;         \
+  }
+
+}  // namespace
+}  // namespace tssm
+
+using namespace tssm;
+
+extern "C" int tssm_layernorm_fwd(int dtype, const void* x, const void* w, const void* bias,
+                                  void* out, int64_t nbatch, int64_t L, int64_t H,
+                                  int64_t stride_b, int64_t stride_l, float eps,
+                                  int64_t block_h, int64_t grid_b, int64_t grid_l,
+                                  void* stream) {
+  TSSM_CHECK(x && w && bias && out, TSSM_ERR_NULL);
+  TSSM_CHECK(io_dtype(dtype), TSSM_ERR_DTYPE);
+  TSSM_CHECK(H > 0 && block_h >= H && grid_b >= 0 && grid_l >= 0 && grid_b <= nbatch &&
+                 grid_l <= L, TSSM_ERR_SHAPE);
+  TSSM_CHECK(stride_b >= 0 && stride_l >= 0, TSSM_ERR_STRIDE);
+  const int64_t nrow = grid_b * grid_l;
+  if (nrow == 0) return TSSM_OK;
+  const Rows rows{grid_l, stride_b, stride_l};
+  const hipStream_t s = as_stream(stream);
+  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((layernorm_fwd_kernel<T>), dim3(row_grid(nrow)),
+                                          dim3(kThreads), 0, s, (const T*)x, (const T*)w,
+                                          (const T*)bias, (T*)out, rows, nrow, H, block_h - H,
+                                          eps));
+  return launch_status();
+}
+
+extern "C" int64_t tssm_layernorm_bwd_workspace_bytes(int64_t grid_b, int64_t grid_l, int64_t H) {
+  if (grid_b < 0 || grid_l < 0 || H <= 0) return -1;
+  const int64_t nrow = grid_b * grid_l;
+  const int64_t nblk = (nrow + kLnRowBlock - 1) / kLnRowBlock;
+  return (2 * nrow + 2 * nblk * H) * (int64_t)sizeof(float);
+}
+
+extern "C" int tssm_layernorm_bwd(int dtype, const void* dout, const void* x, const void* w,
+                                  void* dx, void* dw, void* db, int64_t nbatch, int64_t L,
+                                  int64_t H, int64_t stride_b, int64_t stride_l, float eps,
+                                  int64_t block_h, int64_t grid_b, int64_t grid_l,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(dout && x && w && dx && dw && db, TSSM_ERR_NULL);
+  TSSM_CHECK(io_dtype(dtype), TSSM_ERR_DTYPE);
+  TSSM_CHECK(H > 0 && block_h >= H && grid_b >= 0 && grid_l >= 0 && grid_b <= nbatch &&
+                 grid_l <= L, TSSM_ERR_SHAPE);
+  TSSM_CHECK(stride_b >= 0 && stride_l >= 0, TSSM_ERR_STRIDE);
+  const int64_t nrow = grid_b * grid_l;
+  if (nrow == 0) return TSSM_OK;
+  const int64_t need = tssm_layernorm_bwd_workspace_bytes(grid_b, grid_l, H);
+  TSSM_CHECK(workspace && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 16), TSSM_ERR_ALIGN);
+  const int64_t nblk = (nrow + kLnRowBlock - 1) / kLnRowBlock;
+  TSSM_CHECK(nblk <= 65535, TSSM_ERR_UNSUPPORTED);
+  float* stats = reinterpret_cast<float*>(workspace);
+  float* part = stats + 2 * nrow;
+  const Rows rows{grid_l, stride_b, stride_l};
+  const hipStream_t s = as_stream(stream);
+  const dim3 gcol((unsigned)((H + kThreads - 1) / kThreads), (unsigned)nblk);
+  const dim3 gfin((unsigned)((H + kThreads - 1) / kThreads));
+  TSSM_DISPATCH(dtype, {
+    hipLaunchKernelGGL((layernorm_bwd_row_kernel<T>), dim3(row_grid(nrow)), dim3(kThreads), 0, s,
+                       (const T*)dout, (const T*)x, (const T*)w, (T*)dx, stats, rows, nrow, H,
+                       block_h - H, eps);
+    hipLaunchKernelGGL((ln_param_partial_kernel<T>), gcol, dim3(kThreads), 0, s, (const T*)dout,
+                       (const T*)x, stats, part, rows, nrow, H, nblk);
+    hipLaunchKernelGGL((ln_param_final_kernel<T>), gfin, dim3(kThreads), 0, s, part, (T*)dw,
+                       (T*)db, H, nblk);
+  });
+  return launch_status();
+}
+
+extern "C" int tssm_swiglu_fwd(int dtype, const void* gate, const void* up, void* out,
+                               int64_t nbatch, int64_t L, int64_t H, int64_t stride_b,
+                               int64_t stride_l, int64_t grid_b, int64_t grid_l, void* stream) {
+  TSSM_CHECK(gate && up && out, TSSM_ERR_NULL);
+  TSSM_CHECK(io_dtype(dtype), TSSM_ERR_DTYPE);
+  TSSM_CHECK(H >= 0 && grid_b >= 0 && grid_l >= 0 && grid_b <= nbatch && grid_l <= L,
+             TSSM_ERR_SHAPE);
+  TSSM_CHECK(stride_b >= 0 && stride_l >= 0, TSSM_ERR_STRIDE);
+  const int64_t n = grid_b * grid_l * H;
+  if (n == 0) return TSSM_OK;
+  const RowElems e{{grid_l, stride_b, stride_l}, H};
+  const hipStream_t s = as_stream(stream);
+  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((swiglu_fwd_kernel<T>), dim3(flat_grid(n)),
+                                          dim3(kThreads), 0, s, (const T*)gate, (const T*)up,
+                                          (T*)out, e, n));
+  return launch_status();
+}
+
+extern "C" int tssm_swiglu_bwd(int dtype, const void* dout, const void* gate, const void* up,
+                               void* dgate, void* dup, int64_t nbatch, int64_t L, int64_t H,
+                               int64_t stride_b, int64_t stride_l, int64_t grid_b,
+                               int64_t grid_l, void* stream) {
+  TSSM_CHECK(dout && gate && up && dgate && dup, TSSM_ERR_NULL);
+  TSSM_CHECK(io_dtype(dtype), TSSM_ERR_DTYPE);
+  TSSM_CHECK(H >= 0 && grid_b >= 0 && grid_l >= 0 && grid_b <= nbatch && grid_l <= L,
+             TSSM_ERR_SHAPE);
+  TSSM_CHECK(stride_b >= 0 && stride_l >= 0, TSSM_ERR_STRIDE);
+  const int64_t n = grid_b * grid_l * H;
+  if (n == 0) return TSSM_OK;
+  const RowElems e{{grid_l, stride_b, stride_l}, H};
+  const hipStream_t s = as_stream(stream);
+  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((swiglu_bwd_kernel<T>), dim3(flat_grid(n)),
+                                          dim3(kThreads), 0, s, (const T*)dout, (const T*)gate,
+                                          (const T*)up, (T*)dgate, (T*)dup, e, n));
+  return launch_status();
+}
+
+extern "C" int tssm_residual_add(int dtype, const void* x, const void* res, const uint8_t* keep,
+                                 void* out, int64_t n, float p_keep, void* stream) {
+  TSSM_CHECK(x && res && out, TSSM_ERR_NULL);
+  TSSM_CHECK(io_dtype(dtype), TSSM_ERR_DTYPE);
+  TSSM_CHECK(n >= 0, TSSM_ERR_SHAPE);
+  if (n == 0) return TSSM_OK;
+  const hipStream_t s = as_stream(stream);
+  const float scale = 1.0f / p_keep;
+  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((residual_kernel<T>), dim3(flat_grid(n)),
+                                          dim3(kThreads), 0, s, (const T*)x, (const T*)res,
+                                          keep, (T*)out, n, scale));
+  return launch_status();
+}
+
+extern "C" int64_t tssm_mean_pool_logit_workspace_bytes(int64_t grid_b, int64_t T) {
+  if (grid_b < 0 || T < 0) return -1;
+  return grid_b * ((T + kPoolRows - 1) / kPoolRows) * (int64_t)sizeof(float);
+}
+
+extern "C" int tssm_mean_pool_logit(int dtype, const void* h, const void* W, const void* bias,
+                                    void* out, int64_t nbatch, int64_t nt, int64_t H,
+                                    int64_t stride_b, int64_t stride_t, int64_t grid_b,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(h && W && bias && out, TSSM_ERR_NULL);
+  TSSM_CHECK(io_dtype(dtype), TSSM_ERR_DTYPE);
+  TSSM_CHECK(nt > 0 && H > 0 && grid_b >= 0 && grid_b <= nbatch, TSSM_ERR_SHAPE);
+  TSSM_CHECK(stride_b >= 0 && stride_t >= 0, TSSM_ERR_STRIDE);
+  if (grid_b == 0) return TSSM_OK;
+  const int64_t nblk = (nt + kPoolRows - 1) / kPoolRows;
+  TSSM_CHECK(nblk <= 65535 && grid_b <= 2147483647, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(workspace && workspace_bytes >= tssm_mean_pool_logit_workspace_bytes(grid_b, nt),
+             TSSM_ERR_WORKSPACE);
+  float* part = reinterpret_cast<float*>(workspace);
+  // the reference divides in fp32 by (T * H + 1e-9)
+  const float denom = (float)(nt * H) + 1e-9f;
+  const hipStream_t s = as_stream(stream);
+  TSSM_DISPATCH(dtype, {
+    hipLaunchKernelGGL((pool_partial_kernel<T>), dim3((unsigned)grid_b, (unsigned)nblk),
+                       dim3(kThreads), 0, s, (const T*)h, (const T*)W, part, nt, H, stride_b,
+                       stride_t, nblk);
+    hipLaunchKernelGGL((pool_final_kernel<T>), dim3((unsigned)((grid_b + 255) / 256)), dim3(256),
+                       0, s, part, (const T*)bias, (T*)out, grid_b, nblk, denom);
+  });
+  return launch_status();
+}
+
+extern "C" int tssm_masked_fill_zero(int dtype, int mask_code, const void* x, const void* mask,
+                                     void* out, int64_t n, int64_t H, void* stream) {
+  TSSM_CHECK(x && mask && out, TSSM_ERR_NULL);
+  TSSM_CHECK(io_dtype(dtype) && mask_code >= 0 && mask_code <= 4, TSSM_ERR_DTYPE);
+  TSSM_CHECK(n >= 0 && H > 0, TSSM_ERR_SHAPE);
+  if (n == 0) return TSSM_OK;
+  const hipStream_t s = as_stream(stream);
+  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((masked_fill_kernel<T>), dim3(flat_grid(n)),
+                                          dim3(kThreads), 0, s, (const T*)x, mask, mask_code,
+                                          (T*)out, n, H));
+  return launch_status();
+}

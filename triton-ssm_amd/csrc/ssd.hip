@@ -880,6 +880,7 @@ int launch_ssd_n(int N, int64_t rows, int64_t nchunks, int64_t PN, hipStream_t s
     case 8: return launch_ssd_passes<T, DISC, 8, HAS_D>(rows, nchunks, PN, s, a);
     case 16: return launch_ssd_passes<T, DISC, 16, HAS_D>(rows, nchunks, PN, s, a);
     case 32: return launch_ssd_passes<T, DISC, 32, HAS_D>(rows, nchunks, PN, s, a);
+    case 64: return launch_ssd_passes<T, DISC, 64, HAS_D>(rows, nchunks, PN, s, a);
     default: return TSSM_ERR_UNSUPPORTED;
   }
 }
@@ -928,7 +929,7 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
   TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
   TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
   TSSM_CHECK(nbatch > 0 && L > 0 && H > 0 && P > 0, TSSM_ERR_SHAPE);
-  TSSM_CHECK(P <= 64 && (N == 8 || N == 16 || N == 32), TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(P <= 64 && (N == 8 || N == 16 || N == 32 || N == 64), TSSM_ERR_UNSUPPORTED);
   const int64_t need = tssm_ssd_scan_workspace_bytes(nbatch, L, H, P, N, chunk);
   TSSM_CHECK(workspace && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
   TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);

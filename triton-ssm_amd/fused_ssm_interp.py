@@ -7,16 +7,17 @@
       float32.
   _combine_fwd                  :7-8
 
-``layernorm_kernel``, ``layernorm_bwd_kernel``, ``swiglu_kernel`` and
-``swiglu_bwd_kernel`` (:104-217) are transformer/MLP glue outside the
-selective-SSM path and are not provided; launching them raises
-NotImplementedError.
+  layernorm_kernel / layernorm_bwd_kernel   :104-171
+      one wave per (b, l) row; BLOCK_H >= H honoured as the reference's block
+      (its masked lanes enter the variance); dw/db accumulated in a fixed
+      order instead of atomically.
+  swiglu_kernel / swiglu_bwd_kernel         :173-217
 """
 from __future__ import annotations
 
 from tssm import _lib
-from tssm.launch import (HipKernel, as_f32, dcode, extent, ival, need_gpu, not_built, span,
-                         stream_handle)
+from tssm import layers
+from tssm.launch import HipKernel, as_f32, dcode, extent, ival, need_gpu, span, stream_handle
 
 __all__ = ["_combine_fwd", "fused_interp_ssm_step_kernel", "layernorm_kernel",
            "layernorm_bwd_kernel", "swiglu_kernel", "swiglu_bwd_kernel"]
@@ -75,23 +76,21 @@ fused_interp_ssm_step_kernel = HipKernel(
      "stride_hob", "stride_hof", "t_cur", "K", "FTILE"],
     _launch_step, "fused_ssm_interp.py:12-101")
 
-_OUT = "transformer/MLP glue outside the selective-SSM path"
 layernorm_kernel = HipKernel(
     "layernorm_kernel",
     ["x_ptr", "w_ptr", "bias_ptr", "out_ptr", "B", "L", "H", "stride_b", "stride_l", "stride_h",
      "EPS", "BLOCK_H"],
-    not_built("layernorm_kernel", "fused_ssm_interp.py:104-130", _OUT), "fused_ssm_interp.py:104-130")
+    layers.launch_layernorm, "fused_ssm_interp.py:104-130")
 layernorm_bwd_kernel = HipKernel(
     "layernorm_bwd_kernel",
     ["dout_ptr", "x_ptr", "w_ptr", "dx_ptr", "dw_ptr", "db_ptr", "B", "L", "H", "stride_b",
      "stride_l", "EPS", "BLOCK_H"],
-    not_built("layernorm_bwd_kernel", "fused_ssm_interp.py:133-170", _OUT),
-    "fused_ssm_interp.py:133-170")
+    layers.launch_layernorm_bwd, "fused_ssm_interp.py:133-171")
 swiglu_kernel = HipKernel(
     "swiglu_kernel", ["gate_ptr", "up_ptr", "out_ptr", "B", "L", "H", "stride_b", "stride_l", "BLOCK_H"],
-    not_built("swiglu_kernel", "fused_ssm_interp.py:173-190", _OUT), "fused_ssm_interp.py:173-190")
+    layers.launch_swiglu, "fused_ssm_interp.py:173-191")
 swiglu_bwd_kernel = HipKernel(
     "swiglu_bwd_kernel",
     ["dout_ptr", "gate_ptr", "up_ptr", "dgate_ptr", "dup_ptr", "B", "L", "H", "stride_b",
      "stride_l", "BLOCK_H"],
-    not_built("swiglu_bwd_kernel", "fused_ssm_interp.py:193-217", _OUT), "fused_ssm_interp.py:193-217")
+    layers.launch_swiglu_bwd, "fused_ssm_interp.py:193-217")

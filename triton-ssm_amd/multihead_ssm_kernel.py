@@ -15,15 +15,16 @@ per-lane carry store/load.
 ``multihead_ssm_forward`` (new) runs all three phases as ONE single-pass HIP
 kernel with the discretization fused into its load stage.
 
-``residual_add_kernel`` / ``dropout_residual_kernel`` (:190-222) are model-layer
-glue outside the SSM path and are not provided; launching them raises
-NotImplementedError.
+  residual_add_kernel / dropout_residual_kernel  (:190-222)
+      flat over the first min(N, grid*BLOCK) elements; the dropout keep mask
+      is uint8 (or bool).
 """
 from __future__ import annotations
 
 from tssm import _lib
 from tssm.fused import multihead_ssm_forward  # noqa: F401
-from tssm.launch import (HipKernel, as_f32, dcode, extent, ival, need_gpu, not_built, span,
+from tssm import layers
+from tssm.launch import (HipKernel, as_f32, dcode, extent, ival, need_gpu, span,
                          stream_handle)
 
 __all__ = [
@@ -152,12 +153,8 @@ multihead_ssm_output_kernel = HipKernel(
 
 residual_add_kernel = HipKernel(
     "residual_add_kernel", ["x_ptr", "res_ptr", "out_ptr", "N", "BLOCK"],
-    not_built("residual_add_kernel", "multihead_ssm_kernel.py:190-201",
-              "model-layer glue outside the selective-SSM path"),
-    "multihead_ssm_kernel.py:190-201")
+    layers.launch_residual_add, "multihead_ssm_kernel.py:190-201")
 
 dropout_residual_kernel = HipKernel(
     "dropout_residual_kernel", ["x_ptr", "res_ptr", "mask_ptr", "out_ptr", "N", "p_keep", "BLOCK"],
-    not_built("dropout_residual_kernel", "multihead_ssm_kernel.py:204-222",
-              "model-layer glue outside the selective-SSM path"),
-    "multihead_ssm_kernel.py:204-222")
+    layers.launch_dropout_residual, "multihead_ssm_kernel.py:204-222")

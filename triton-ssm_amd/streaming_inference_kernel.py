@@ -10,16 +10,17 @@ the ring head is read once for all feature tiles and advanced once after them
 :106,115-117 -- a race whenever H > BLOCK_H).  BLOCK_H stays the width of the
 "any lane observed" test.  Its grid must cover every tile of H.
 
-``mean_pool_logit_kernel`` / ``masked_fill_zero_kernel`` (:159-214) are a task
-head and a padding utility outside the selective-SSM path and are not
-provided; launching them raises NotImplementedError.
+  mean_pool_logit_kernel             :159-194  (per-batch reduction in a fixed order)
+  masked_fill_zero_kernel            :197-214  (mask [B,T] broadcast over H; float, int32,
+                                                uint8 or bool masks)
 """
 from __future__ import annotations
 
 import torch
 
 from tssm import _lib
-from tssm.launch import HipKernel, dcode, extent, ival, need_gpu, not_built, span, stream_handle
+from tssm import layers
+from tssm.launch import HipKernel, dcode, extent, ival, need_gpu, span, stream_handle
 
 __all__ = ["streaming_ssm_inplace_kernel", "streaming_ssm_inplace_bf16_kernel",
            "streaming_interp_then_ssm_kernel", "mean_pool_logit_kernel",
@@ -104,14 +105,11 @@ streaming_interp_then_ssm_kernel = HipKernel(
      "stride_cb", "stride_ch", "BLOCK_H", "KRING"],
     _launch_ring, "streaming_inference_kernel.py:75-156")
 
-_OUT = "task head / padding utility outside the selective-SSM path"
 mean_pool_logit_kernel = HipKernel(
     "mean_pool_logit_kernel",
     ["h_ptr", "W_ptr", "bias_ptr", "out_ptr", "B", "T", "H", "stride_b", "stride_t", "stride_h",
      "BLOCK_H", "BLOCK_T"],
-    not_built("mean_pool_logit_kernel", "streaming_inference_kernel.py:159-194", _OUT),
-    "streaming_inference_kernel.py:159-194")
+    layers.launch_mean_pool_logit, "streaming_inference_kernel.py:159-194")
 masked_fill_zero_kernel = HipKernel(
     "masked_fill_zero_kernel", ["x_ptr", "mask_ptr", "out_ptr", "B", "T", "H", "BLOCK"],
-    not_built("masked_fill_zero_kernel", "streaming_inference_kernel.py:197-214", _OUT),
-    "streaming_inference_kernel.py:197-214")
+    layers.launch_masked_fill_zero, "streaming_inference_kernel.py:197-214")

@@ -110,7 +110,7 @@ def ssd_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=256, disc="zoh", h0=No
     x      [Bsz, L, H, P]  float32 / bfloat16 / float16 (P <= 64)
     dt     [Bsz, L, H]     (read as float32)
     A_log  [H]             log(-a) per head
-    B, C   [Bsz, L, H, N]  dtype of x, N in {8, 16, 32}
+    B, C   [Bsz, L, H, N]  dtype of x, N in {8, 16, 32, 64}
     D      [H, P] / [H*P] or None
     h0     [Bsz, H, P, N] float32 or None
 

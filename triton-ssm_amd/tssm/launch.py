@@ -71,13 +71,6 @@ def normalize_grid(g) -> tuple[int, int, int]:
     return g + (1,) * (3 - len(g))
 
 
-def not_built(name: str, reference: str, why: str):
-    """A reference symbol that this library does not implement."""
-    def launch(grid, bound):
-        raise NotImplementedError(f"{name} ({reference}) is not provided: {why}")
-    return launch
-
-
 # ------------------------------------------------------------------ tensors
 _DCODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
