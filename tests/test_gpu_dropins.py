@@ -95,7 +95,7 @@ def test_zoh_discretize_bwd(dev, dtype, shape):
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(2, 33, 300, 16, 64, 8), (3, 20, 64, 5, 32, 4),
-                                   (1, 7, 1000, 48, 256, 16)])
+                                   (1, 7, 1000, 48, 256, 16), (2, 9, 301, 7, 128, 4)])
 def test_dt_project_softplus(dev, out_dtype, shape):
     """dt_project_softplus_kernel[grid](...) against the oracle (softplus+clamp
     pinned to torch in float64); the clamp bounds are hit on purpose."""

@@ -256,54 +256,96 @@ extern "C" int tssm_zoh_discretize_bwd(int dtype, const float* A_log, const void
 // the clamp makes the overflow case agree too.
 namespace tssm {
 
-constexpr int kDtRows = 16;
+constexpr int kDtRows = 4;
 constexpr int kDtRank = 8;
 
-template <typename TO>
+// softplus(x) = max(x, 0) + log1p(exp(-|x|)) with hardware exp2/log2:
+// log1p(e) = log(u) e / (u - 1), u = 1 + e rounded, which cancels the
+// rounding of u (Goldberg's identity); e <= 1, so u - 1 is exact.
+__device__ inline float softplus_fast(float x) {
+  const float e = exp2_fast(-__builtin_fabsf(x) * kLog2e);
+  const float u = 1.0f + e;
+  const float lp = u == 1.0f ? e
+                             : __builtin_amdgcn_logf(u) * 0.6931471805599453f * e *
+                                   __builtin_amdgcn_rcpf(u - 1.0f);
+  return fmaxf(x, 0.0f) + lp;
+}
+
+// Workgroup = 256 threads x V consecutive lanes h (V = 4: 16-byte W, bias and
+// output accesses) over kDtRows rows (b, t); dt_raw values are uniform over
+// the workgroup (scalar loads), W rows are read in groups of kDtRank.
+template <typename TO, int V>
 __global__ __launch_bounds__(256) void dt_project_kernel(
     const float* __restrict__ raw, const float* __restrict__ W, const float* __restrict__ bias,
     TO* __restrict__ out, int64_t grid_t, int64_t nrows, int64_t hc, int64_t rank,
     int64_t sr_b, int64_t sr_t, int64_t sw_r, int64_t so_b, int64_t so_t, float dt_min,
     float dt_max) {
-  const int64_t h = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
   const bool act = h < hc;
+  const int64_t hs = act ? h : 0;  // inactive lanes read lane 0 (in bounds), store nothing
   const int64_t r0 = (int64_t)blockIdx.y * kDtRows;
   const int nr = (int)((nrows - r0) < kDtRows ? (nrows - r0) : kDtRows);
-  int64_t roff[kDtRows];
+  const int64_t b0 = r0 / grid_t, t0 = r0 - b0 * grid_t;
+  // row k = (b0, t0) advanced by k steps in t, wrapping into the next batches
+  auto row_off = [&](int k, int64_t sb, int64_t st) {
+    int64_t t = t0 + k, b = b0;
+    while (t >= grid_t) { t -= grid_t; ++b; }
+    return b * sb + t * st;
+  };
+  float acc[kDtRows][V];
 #pragma unroll
-  for (int k = 0; k < kDtRows; ++k) {
-    const int64_t r = r0 + (k < nr ? k : 0);
-    const int64_t b = r / grid_t, t = r - b * grid_t;
-    roff[k] = b * sr_b + t * sr_t;
-  }
-  float acc[kDtRows];
+  for (int k = 0; k < kDtRows; ++k)
 #pragma unroll
-  for (int k = 0; k < kDtRows; ++k) acc[k] = 0.0f;
+    for (int v = 0; v < V; ++v) acc[k][v] = 0.0f;
   for (int64_t q0 = 0; q0 < rank; q0 += kDtRank) {
-    float w[kDtRank];
+    float w[kDtRank][V];
 #pragma unroll
-    for (int i = 0; i < kDtRank; ++i)
-      w[i] = (act && q0 + i < rank) ? W[(q0 + i) * sw_r + h] : 0.0f;
+    for (int i = 0; i < kDtRank; ++i) {
+      const bool ok = q0 + i < rank;
+      const float* wp = W + (ok ? q0 + i : 0) * sw_r + hs;
+      if constexpr (V == 4) {
+        const float4 q = *reinterpret_cast<const float4*>(wp);
+        w[i][0] = ok ? q.x : 0.0f; w[i][1] = ok ? q.y : 0.0f;
+        w[i][2] = ok ? q.z : 0.0f; w[i][3] = ok ? q.w : 0.0f;
+      } else {
+        w[i][0] = ok ? *wp : 0.0f;
+      }
+    }
 #pragma unroll
     for (int k = 0; k < kDtRows; ++k) {
-      if (k < nr) {
+      if (k < nr) {  // uniform
+        const float* rp = raw + row_off(k, sr_b, sr_t) + q0;
 #pragma unroll
-        for (int i = 0; i < kDtRank; ++i)
-          if (q0 + i < rank) acc[k] = __builtin_fmaf(raw[roff[k] + q0 + i], w[i], acc[k]);
+        for (int i = 0; i < kDtRank; ++i) {
+          const float rv = q0 + i < rank ? rp[i] : 0.0f;
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[k][v] = __builtin_fmaf(rv, w[i][v], acc[k][v]);
+        }
       }
     }
   }
   if (!act) return;
-  const float bv = bias[h];
+  float bv[V];
+  if constexpr (V == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(bias + h);
+    bv[0] = q.x; bv[1] = q.y; bv[2] = q.z; bv[3] = q.w;
+  } else {
+    bv[0] = bias[h];
+  }
 #pragma unroll
   for (int k = 0; k < kDtRows; ++k) {
     if (k < nr) {
-      const float x = acc[k] + bv;
-      float sp = fmaxf(x, 0.0f) + log1pf(expf(-__builtin_fabsf(x)));
-      sp = fminf(fmaxf(sp, dt_min), dt_max);
-      const int64_t r = r0 + k;
-      const int64_t b = r / grid_t, t = r - b * grid_t;
-      stf(out + b * so_b + t * so_t + h, sp);
+      float sp[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        sp[v] = fminf(fmaxf(softplus_fast(acc[k][v] + bv[v]), dt_min), dt_max);
+      TO* op = out + row_off(k, so_b, so_t) + h;
+      if constexpr (V == 4 && sizeof(TO) == 4) {
+        *reinterpret_cast<float4*>(op) = make_float4(sp[0], sp[1], sp[2], sp[3]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) stf(op + v, sp[v]);
+      }
     }
   }
 }
@@ -326,17 +368,22 @@ extern "C" int tssm_dt_project_softplus(int out_dtype, const float* dt_raw, cons
   if (nrows == 0 || h_cover == 0) return TSSM_OK;
   const int64_t n_rg = cdiv64(nrows, kDtRows);
   TSSM_CHECK(n_rg <= 65535, TSSM_ERR_UNSUPPORTED);
-  const int threads = h_cover >= 256 ? 256 : (int)(cdiv64(h_cover, 64) * 64);
-  const dim3 grid((unsigned)cdiv64(h_cover, threads), (unsigned)n_rg);
+  // 4 lanes per thread when every W row, bias and output row is 16-byte aligned
+  const bool v4 = h_cover % 4 == 0 && sw_r % 4 == 0 && so_b % 4 == 0 && so_t % 4 == 0 &&
+                  aligned(W, 16) && aligned(bias, 16) &&
+                  aligned(dt_out, out_dtype == TSSM_F32 ? 16 : 8);
+  const int64_t nthr = v4 ? h_cover / 4 : h_cover;
+  const int threads = nthr >= 256 ? 256 : (int)(cdiv64(nthr, 64) * 64);
+  const dim3 grid((unsigned)cdiv64(nthr, threads), (unsigned)n_rg);
   const hipStream_t s = as_stream(stream);
-#define TSSM_DTP(TT)                                                                            \
-  hipLaunchKernelGGL(dt_project_kernel<TT>, grid, dim3(threads), 0, s, dt_raw, W, bias,         \
+#define TSSM_DTP(TT, VV)                                                                        \
+  hipLaunchKernelGGL((dt_project_kernel<TT, VV>), grid, dim3(threads), 0, s, dt_raw, W, bias,   \
                      (TT*)dt_out, grid_t, nrows, h_cover, rank, sr_b, sr_t, sw_r, so_b, so_t,  \
                      dt_min, dt_max)
   switch (out_dtype) {
-    case TSSM_F32: TSSM_DTP(float); break;
-    case TSSM_BF16: TSSM_DTP(bf16_t); break;
-    case TSSM_F16: TSSM_DTP(f16_t); break;
+    case TSSM_F32: if (v4) TSSM_DTP(float, 4); else TSSM_DTP(float, 1); break;
+    case TSSM_BF16: if (v4) TSSM_DTP(bf16_t, 4); else TSSM_DTP(bf16_t, 1); break;
+    case TSSM_F16: if (v4) TSSM_DTP(f16_t, 4); else TSSM_DTP(f16_t, 1); break;
     default: return TSSM_ERR_DTYPE;
   }
 #undef TSSM_DTP
