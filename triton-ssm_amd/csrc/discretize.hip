@@ -280,10 +280,10 @@ __global__ __launch_bounds__(256) void dt_project_kernel(
     TO* __restrict__ out, int64_t grid_t, int64_t nrows, int64_t hc, int64_t rank,
     int64_t sr_b, int64_t sr_t, int64_t sw_r, int64_t so_b, int64_t so_t, float dt_min,
     float dt_max) {
-  const int64_t h = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
+  const int64_t h = ((int64_t)blockIdx.y * blockDim.x + threadIdx.x) * V;
   const bool act = h < hc;
   const int64_t hs = act ? h : 0;  // inactive lanes read lane 0 (in bounds), store nothing
-  const int64_t r0 = (int64_t)blockIdx.y * kDtRows;
+  const int64_t r0 = (int64_t)blockIdx.x * kDtRows;
   const int nr = (int)((nrows - r0) < kDtRows ? (nrows - r0) : kDtRows);
   const int64_t b0 = r0 / grid_t, t0 = r0 - b0 * grid_t;
   // row k = (b0, t0) advanced by k steps in t, wrapping into the next batches
@@ -367,14 +367,15 @@ extern "C" int tssm_dt_project_softplus(int out_dtype, const float* dt_raw, cons
   const int64_t nrows = grid_b * grid_t;
   if (nrows == 0 || h_cover == 0) return TSSM_OK;
   const int64_t n_rg = cdiv64(nrows, kDtRows);
-  TSSM_CHECK(n_rg <= 65535, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(n_rg <= 2147483647, TSSM_ERR_UNSUPPORTED);
   // 4 lanes per thread when every W row, bias and output row is 16-byte aligned
   const bool v4 = h_cover % 4 == 0 && sw_r % 4 == 0 && so_b % 4 == 0 && so_t % 4 == 0 &&
                   aligned(W, 16) && aligned(bias, 16) &&
                   aligned(dt_out, out_dtype == TSSM_F32 ? 16 : 8);
   const int64_t nthr = v4 ? h_cover / 4 : h_cover;
   const int threads = nthr >= 256 ? 256 : (int)(cdiv64(nthr, 64) * 64);
-  const dim3 grid((unsigned)cdiv64(nthr, threads), (unsigned)n_rg);
+  TSSM_CHECK(cdiv64(nthr, threads) <= 65535, TSSM_ERR_UNSUPPORTED);
+  const dim3 grid((unsigned)n_rg, (unsigned)cdiv64(nthr, threads));
   const hipStream_t s = as_stream(stream);
 #define TSSM_DTP(TT, VV)                                                                        \
   hipLaunchKernelGGL((dt_project_kernel<TT, VV>), grid, dim3(threads), 0, s, dt_raw, W, bias,   \
