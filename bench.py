@@ -11,6 +11,7 @@ x/B/C/y, fp32 dt and state, ZOH discretization fused into the load stage.
   ssd_long       SSD scan B=1 L=262144 H=8 P=64 N=16 bf16, chunk 256
   ssd_config1    SSD scan on the headline shapes B=8 L=4096 H=16 P=N=64 bf16
   ssd_stream     streaming SSD step, 4096 streams H=32 P=64 N=128 fp32 state
+  rows           every drop-in kernel at a config-sized shape (one JSON line, "rows" list)
 
 A step is one pass of the path over one batch of seeded synthetic input that
 is already resident in HBM.  Input sets are rotated where memory allows so
@@ -288,6 +289,199 @@ def wl_ssd_stream(args, dev):
                         "S": S, "H": H, "P": P, "N": N})
 
 
+# ------------------------------------------------------------------ per-row sweep
+def rows_sweep(args, dev):
+    """Each drop-in kernel of the path (and its model-layer neighbours) at a
+    config-sized shape: average launch time over back-to-back launches (HIP
+    events on the launch stream), algorithmic bytes (inputs read once, outputs
+    written once, in the dtypes used) and the fraction of 8 TB/s.  Prints one
+    JSON line with a "rows" list; the table goes to stderr."""
+    import math
+    import torch
+    import discretize_kernel as dk
+    import fused_interp_kernel as fi
+    import fused_ssm_interp as fs
+    import multihead_ssm_kernel as mk
+    import ssm_scan as ss
+    import streaming_inference_kernel as sk
+    g = torch.Generator(device=dev).manual_seed(7)
+    rnd = lambda *shape, dtype=torch.float32: torch.randn(*shape, generator=g, device=dev).to(dtype)  # noqa: E731
+    uni = lambda lo, hi, *shape: torch.empty(*shape, device=dev).uniform_(lo, hi, generator=g)  # noqa: E731
+    stream = torch.cuda.current_stream(dev)
+    reps = max(5, min(args.steps, 50))
+    rows = []
+
+    def timeit(name, shape, nbytes, fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(int(1e8))
+        t0.record(stream)
+        for _ in range(reps):
+            fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) / reps * 1e3
+        gbps = nbytes / (us * 1e-6) / 1e9
+        rows.append({"row": name, "shape": shape, "us": round(us, 2), "bytes": int(nbytes),
+                     "gbps": round(gbps, 1), "frac": round(gbps / 8000.0, 4)})
+        log(f"{name:52s} {shape:34s} {us:9.1f} us {gbps:8.0f} GB/s {100 * gbps / 8000:5.1f}%")
+
+    B, T, H = 8, 4096, 1024          # lanes of the headline config
+    n = B * T * H
+    # a1/a2 ZOH discretize, a19 its backward
+    A = uni(math.log(0.5), math.log(5.0), H)
+    dt = torch.exp(uni(-6.0, 0.5, B, T))
+    for dtype, kern, tag in ((torch.float32, dk.zoh_discretize_diag_kernel, "fp32"),
+                             (torch.bfloat16, dk.zoh_discretize_diag_bf16_kernel, "bf16")):
+        Bm = rnd(B, T, H, dtype=dtype)
+        Ab, Bb = torch.empty_like(Bm), torch.empty_like(Bm)
+        es = Bm.element_size()
+        timeit(f"a1/a2 zoh_discretize_diag ({tag})", f"B={B} T={T} H={H}", n * 3 * es + B * T * 4,
+               lambda: kern[(B, T, H // 256)](A, Bm, dt, Ab, Bb, B, T, H, *Bm.stride(),
+                                              *dt.stride(), *Ab.stride(), *Bb.stride(),
+                                              BLOCK_H=256))
+        if dtype == torch.float32:
+            dAb, dBb, dB = rnd(B, T, H), rnd(B, T, H), torch.empty_like(Bm)
+            dA, ddt = torch.zeros(H, device=dev), torch.empty(B, T, device=dev)
+            timeit("a19 zoh_discretize_bwd (fp32)", f"B={B} T={T} H={H}", n * 5 * 4 + B * T * 8,
+                   lambda: dk.zoh_discretize_bwd_kernel[(B, T, H // 256)](
+                       A, Bm, dt, Ab, dAb, dBb, dA, dB, ddt, B, T, H, *Bm.stride(),
+                       *dt.stride(), *Ab.stride(), *dBb.stride(), BLOCK_H=256))
+        del Bm, Ab, Bb
+    # a21 dt projection (Mamba-1 shape: D = 256 channels, rank 16)
+    Bd, Td, Hd, R = 16, 2048, 256, 16
+    raw, W, bias = rnd(Bd, Td, R), rnd(R, Hd) / 4, rnd(Hd)
+    dto = torch.empty(Bd, Td, Hd, device=dev)
+    timeit("a21 dt_project_softplus", f"B={Bd} T={Td} H={Hd} R={R}",
+           4 * (Bd * Td * (R + Hd) + R * Hd + Hd),
+           lambda: dk.dt_project_softplus_kernel[(Bd, Td, 1)](
+               raw, W, bias, dto, Bd, Td, Hd, R, *raw.stride(), *W.stride(), *dto.stride(),
+               DT_MIN=1e-3, DT_MAX=0.1, BLOCK_H=256, BLOCK_R=16))
+    del raw, dto
+    # a4-a8 elementwise scan (ssm_forward), a20 ssm_backward
+    u, Bm, Cm = rnd(B, T, H), rnd(B, T, H), rnd(B, T, H)
+    Am = uni(0.5, 1.0, B, T, H)
+    Dv = rnd(H)
+    out = {}
+    timeit("a4-a8 ssm_forward (4 phase kernels)", f"B={B} L={T} H={H}", n * 6 * 4,
+           lambda: out.update(r=ss.ssm_forward(u, Am, Bm, Cm, Dv, BLK=256)))
+    y_, h_ = out["r"]
+    dY = rnd(B, T, H)
+    timeit("a20 ssm_backward (4 phase kernels)", f"B={B} L={T} H={H}", n * 10 * 4,
+           lambda: ss.ssm_backward(u, Am, Bm, Cm, h_, dY, BLK=256))
+    del u, Bm, Cm, Am, y_, h_, dY, out
+    # a9-a11 multihead phase-exact kernels (reference layouts, fp32)
+    nh, hd, BLK = 16, 64, 128
+    from tssm import workloads
+    w = workloads.multihead(B=B, L=T, H=nh, P=hd, dtype=torch.float32)
+    u, Bm, Cm, dtm = (w[k].to(dev) for k in ("u", "B", "C", "dt"))
+    A_log = w["A_log"].to(dev)
+    Dm = rnd(nh * hd)
+    nblk = 1 << (((T + BLK - 1) // BLK) - 1).bit_length()
+    loc_a = torch.empty(B, T, nh, hd, device=dev)
+    loc_x = torch.empty_like(loc_a)
+    carry = torch.empty(2 * B * nh * hd * nblk, device=dev)
+    y = torch.empty(B, T, nh * hd, device=dev)
+    timeit("a9 multihead_ssm_fwd_local", f"B={B} L={T} nh={nh} hd={hd}", n * 5 * 4 + B * T * nh * 4,
+           lambda: mk.multihead_ssm_fwd_local_kernel[(B * nh, nblk)](
+               u, A_log, Bm, Cm, dtm, loc_a, loc_x, carry, B, T, nh * hd, nh, hd, *u.stride(),
+               *A_log.stride(), *Bm.stride(), *Cm.stride(), *dtm.stride(), BLK_L=BLK, NBLK=nblk,
+               HEAD_DIM=hd))
+    timeit("a10 multihead_ssm_carry_scan", f"{B * nh * hd} lanes x {nblk} chunks",
+           2 * 2 * B * nh * hd * nblk * 4,
+           lambda: mk.multihead_ssm_carry_scan_kernel[(B * nh * hd,)](carry, B * nh * hd, nblk))
+    timeit("a11 multihead_ssm_output", f"B={B} L={T} nh={nh} hd={hd}", n * 5 * 4,
+           lambda: mk.multihead_ssm_output_kernel[(B * nh, nblk)](
+               loc_a, loc_x, carry, Cm, Dm, u, y, B, T, nh * hd, nh, hd, *u.stride(),
+               *Cm.stride(), BLK_L=BLK, NBLK=nblk, HEAD_DIM=hd))
+    del u, Bm, Cm, dtm, loc_a, loc_x, carry, y, w
+    # a12 time-aware interpolation (config 2 shape)
+    wi = workloads.interp_mamba1()
+    V, M, tau = (wi[k].to(dev) for k in ("V", "M", "tau"))
+    Bi, Ti, Fi = V.shape
+    Vh = torch.empty_like(V)
+    timeit("a12 fused_time_aware_interp (fp32)", f"B={Bi} T={Ti} F={Fi} K=10 FTILE=128",
+           Bi * Ti * Fi * 12 + Bi * Ti * 4,
+           lambda: fi.fused_time_aware_interp_kernel[(Bi, Ti, Fi // 128)](
+               V, M, tau, Vh, Bi, Ti, Fi, *V.stride(), *M.stride(), *tau.stride(), *Vh.stride(),
+               K=10, FTILE=128))
+    # a15 interp + SSM step at one t_cur (per-step launch of the reference loop)
+    Ab1, Bb1 = torch.rand(Fi, device=dev), rnd(Fi)
+    h_in, h_out = rnd(Bi, Fi), torch.empty(Bi, Fi, device=dev)
+    timeit("a15 fused_interp_ssm_step (one step)", f"B={Bi} F={Fi} K=10 t=1000",
+           Bi * Fi * 4 * (2 * 21 + 3) + Bi * 21 * 4,
+           lambda: fs.fused_interp_ssm_step_kernel[(Bi, Fi // 128)](
+               V, M, tau, Ab1, Bb1, h_in, Vh, h_out, Bi, Ti, Fi, *V.stride(), *M.stride(),
+               *tau.stride(), *Vh.stride(), *h_in.stride(), *h_out.stride(), 1000, K=10,
+               FTILE=128))
+    del V, M, tau, Vh, wi
+    # a16/a17 streaming in-place step, a18 ring interp + step
+    S, Hs = 4096, 1024
+    for dtype, kern, tag in ((torch.float32, sk.streaming_ssm_inplace_kernel, "fp32"),
+                             (torch.bfloat16, sk.streaming_ssm_inplace_bf16_kernel, "bf16")):
+        v, hs, Cs = rnd(S, Hs, dtype=dtype), rnd(S, Hs, dtype=dtype), rnd(S, Hs, dtype=dtype)
+        Abs, Bbs, Ds = (torch.rand(Hs, device=dev).to(dtype) for _ in range(3))
+        ys = torch.empty_like(v)
+        es = v.element_size()
+        timeit(f"a16/a17 streaming_ssm_inplace ({tag})", f"S={S} H={Hs}", S * Hs * 5 * es,
+               lambda: kern[(S, Hs // 256)](v, hs, Abs, Bbs, Cs, Ds, ys, S, Hs, *v.stride(),
+                                            *hs.stride(), *Cs.stride(), BLOCK_H=256))
+    Sr, Hr, KR = 1024, 256, 11
+    ring_V, ring_M = rnd(Sr, KR, Hr), (torch.rand(Sr, KR, Hr, device=dev) < 0.3).float()
+    ring_tau = torch.arange(KR, device=dev, dtype=torch.float32).repeat(Sr, 1)
+    head = torch.zeros(Sr, dtype=torch.int32, device=dev)
+    vn, mn = rnd(Sr, Hr), (torch.rand(Sr, Hr, device=dev) < 0.3).float()
+    tn = torch.full((Sr,), 20.0, device=dev)
+    hr, Cr, yr = rnd(Sr, Hr), rnd(Sr, Hr), torch.empty(Sr, Hr, device=dev)
+    Abr, Bbr, Dr = (torch.rand(Hr, device=dev) for _ in range(3))
+    timeit("a18 streaming_interp_then_ssm (ring)", f"S={Sr} H={Hr} KRING={KR}", Sr * Hr * 4 * 8,
+           lambda: sk.streaming_interp_then_ssm_kernel[(Sr, Hr // 128)](
+               ring_V, ring_M, ring_tau, head, vn, mn, tn, hr, Abr, Bbr, Cr, Dr, yr, Sr, Hr,
+               KR - 1, *ring_V.stride(), *vn.stride(), *hr.stride(), *Cr.stride(), BLOCK_H=128,
+               KRING=KR))
+    # model layers (fp32, headline lane count)
+    x, dout = rnd(B, T, H), rnd(B, T, H)
+    wv, bv = rnd(H), rnd(H)
+    o1, o2 = torch.empty_like(x), torch.empty_like(x)
+    dw, db = torch.zeros(H, device=dev), torch.zeros(H, device=dev)
+    timeit("layernorm_kernel", f"B={B} L={T} H={H}", n * 8,
+           lambda: fs.layernorm_kernel[(B, T)](x, wv, bv, o1, B, T, H, *x.stride(), EPS=1e-5,
+                                               BLOCK_H=H))
+    timeit("layernorm_bwd_kernel", f"B={B} L={T} H={H}", n * 12,
+           lambda: fs.layernorm_bwd_kernel[(B, T)](dout, x, wv, o1, dw, db, B, T, H,
+                                                   x.stride(0), x.stride(1), EPS=1e-5, BLOCK_H=H))
+    timeit("swiglu_kernel", f"B={B} L={T} H={H}", n * 12,
+           lambda: fs.swiglu_kernel[(B, T)](x, dout, o1, B, T, H, x.stride(0), x.stride(1),
+                                            BLOCK_H=H))
+    o3 = torch.empty_like(x)
+    timeit("swiglu_bwd_kernel", f"B={B} L={T} H={H}", n * 20,
+           lambda: fs.swiglu_bwd_kernel[(B, T)](dout, x, o3, o1, o2, B, T, H, x.stride(0),
+                                                x.stride(1), BLOCK_H=H))
+    del o3
+    keep = (torch.rand(n, device=dev) < 0.9).to(torch.uint8)
+    xf, rf, of = x.view(-1), dout.view(-1), o1.view(-1)
+    timeit("residual_add_kernel", f"N={n}", n * 12,
+           lambda: mk.residual_add_kernel[(n // 1024,)](xf, rf, of, n, BLOCK=1024))
+    timeit("dropout_residual_kernel", f"N={n}", n * 13,
+           lambda: mk.dropout_residual_kernel[(n // 1024,)](xf, rf, keep, of, n, 0.9, BLOCK=1024))
+    mask = (torch.rand(B, T, device=dev) < 0.8).to(torch.uint8)
+    timeit("masked_fill_zero_kernel", f"B={B} T={T} H={H}", n * 8 + B * T,
+           lambda: sk.masked_fill_zero_kernel[(n // 1024,)](x, mask, o1, B, T, H, BLOCK=1024))
+    lo = torch.empty(B, device=dev)
+    b1 = torch.zeros(1, device=dev)
+    timeit("mean_pool_logit_kernel", f"B={B} T={T} H={H}", n * 4,
+           lambda: sk.mean_pool_logit_kernel[(B,)](x, wv, b1, lo, B, T, H, *x.stride(),
+                                                   BLOCK_H=256, BLOCK_T=16))
+    gm = math.exp(sum(math.log(max(r["frac"], 1e-6)) for r in rows) / len(rows))
+    print(json.dumps({"metric": "per-row kernel HBM bandwidth (algorithmic bytes / launch time)",
+                      "value": round(gm, 4), "unit": "geometric-mean fraction of 8 TB/s",
+                      "n_gpus": 1, "steps": reps, "warmup": 3, "higher_is_better": True,
+                      "dtype": "f32", "data": "synthetic", "config": {"workload": "row sweep"},
+                      "rows": rows}))
+
+
 WORKLOADS = {"multihead": wl_multihead, "mamba1_small": wl_mamba1_small,
              "interp_mamba1": wl_interp_mamba1, "ssd_long": wl_ssd_long,
              "ssd_config1": wl_ssd_config1,
@@ -312,7 +506,7 @@ def main():
     ap.add_argument("--steps", type=int, default=None,
                     help="timed steps (default 50; 10000 for ssd_stream, the streaming run length)")
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="multihead")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["rows"], default="multihead")
     ap.add_argument("--disc", choices=["zoh", "euler"], default="zoh")
     ap.add_argument("--a-per-channel", action="store_true",
                     help="multihead: pass A_log as [H, P] (the reference kernel's layout, the "
@@ -349,6 +543,8 @@ def main():
         log("copied 256 MiB x5")
         return
 
+    if args.workload == "rows":
+        return rows_sweep(args, dev)
     log(f"workload {args.workload}: generating inputs ...")
     wl = WORKLOADS[args.workload](args, dev)
     step = wl["step"]

@@ -14,10 +14,11 @@ pytestmark = pytest.mark.gpu
 
 # ------------------------------------------------------------------ discretize
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
-def test_zoh_discretize(dev, out_dtype):
+@pytest.mark.parametrize("H", [200, 203])   # 4-lane and 1-lane accesses
+def test_zoh_discretize(dev, out_dtype, H):
     import discretize_kernel as dk
     g = torch.Generator().manual_seed(3)
-    Bsz, T, H, BLOCK_H = 3, 50, 200, 64
+    Bsz, T, BLOCK_H = 3, 50, 64
     A = torch.empty(H).uniform_(np.log(0.5), np.log(5.0), generator=g).to(dev)
     B = torch.randn(Bsz, T, H, generator=g).to(out_dtype).to(dev)
     # include tiny dt*a (1e-5..1e-3 range where the accurate expm1 matters) and large ones
