@@ -160,9 +160,10 @@ extern "C" int tssm_zoh_discretize(int b_dtype, int out_dtype, const float* A_lo
 // zoh_discretize_bwd_kernel (discretize_kernel.py:98-162), deterministic:
 // the reference adds dA_log with atomics over (b, t) and makes ddt a race
 // between a store (hblk 0) and atomics (:156-162).  Here
-//   pass 1: workgroup (lane block of LB lanes, group of RG rows r = b*grid_t+t)
-//           writes dB, a per-lane partial of dA_log over its rows and, per
-//           row, the partial of ddt over its lanes (wave sums + one LDS pass);
+//   pass 1: workgroup (lane block of up to 256 threads x 4 lanes, group of 64
+//           rows r = b*grid_t+t) writes dB, a per-lane partial of dA_log over
+//           its rows and, per row, the partial of ddt over its lanes (wave
+//           sums + one LDS pass);
 //   pass 2: dA[h] += sum of the row-group partials, ddt[r] = sum of the lane-
 //           block partials, both in a fixed order.
 // The partials live in a caller workspace: [n_rg][hc] then [n_lb][nrows] f32.
@@ -185,11 +186,11 @@ __device__ inline float psi_from_exp(float x, float ex, float em1) {
   p = __builtin_fmaf(p, x, 3.0f / 24.0f);
   p = __builtin_fmaf(p, x, 2.0f / 6.0f);
   p = __builtin_fmaf(p, x, 0.5f);
-  const float direct = (x * ex - em1) / (x * x);
+  const float direct = (x * ex - em1) * __builtin_amdgcn_rcpf(x * x);
   return __builtin_fabsf(x) < 0.5f ? p : direct;
 }
 
-template <typename T>
+template <typename T, int V>
 __global__ __launch_bounds__(kBwdLanes) void zoh_bwd_pass1_kernel(
     const float* __restrict__ A_log, const T* __restrict__ B, const float* __restrict__ dt,
     const T* __restrict__ Abar, const T* __restrict__ dAbar, const T* __restrict__ dBbar,
@@ -197,43 +198,63 @@ __global__ __launch_bounds__(kBwdLanes) void zoh_bwd_pass1_kernel(
     int64_t nrows, int64_t hc, int64_t sB_b, int64_t sB_t, int64_t sdt_b, int64_t sdt_t,
     int64_t sa_b, int64_t sa_t, int64_t sb_b, int64_t sb_t) {
   __shared__ float red[kBwdRows][kBwdLanes / 64];
-  const int lb = blockIdx.x, rg = blockIdx.y;
-  const int64_t h = (int64_t)lb * blockDim.x + threadIdx.x;
+  const int rg = blockIdx.x, lb = blockIdx.y;
+  const int64_t h = ((int64_t)lb * blockDim.x + threadIdx.x) * V;
   const bool act = h < hc;
+  const int64_t hs = act ? h : 0;  // inactive lanes compute on lane 0 and store nothing
   const int nw = blockDim.x >> 6;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  float neg_a = 0.0f, a = 0.0f;
-  if (act) {
-    neg_a = exp_acc(A_log[h]);
-    a = -neg_a;
+  // per-lane constants: a = -exp(A_log), a log2(e), 1/(a + 1e-12), a^2/(a^2 + 1e-18)
+  float a[V], a2[V], ia[V], fac[V], acc_dA[V];
+  {
+    float al[V];
+    ld_lanes<float, V>(A_log + hs, al);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      a[v] = -exp_acc(al[v]);
+      a2[v] = a[v] * kLog2e;
+      ia[v] = 1.0f / (a[v] + 1e-12f);
+      const float aa = a[v] * a[v];
+      fac[v] = aa / (aa + 1e-18f);
+      acc_dA[v] = 0.0f;
+    }
   }
-  float acc_dA = 0.0f;
   const int64_t r0 = (int64_t)rg * kBwdRows;
+  int64_t b = r0 / grid_t, t = r0 - b * grid_t;
   for (int k = 0; k < kBwdRows; ++k) {
-    const int64_t r = r0 + k;
-    if (r >= nrows) break;  // uniform over the workgroup
-    const int64_t b = r / grid_t, t = r - b * grid_t;
+    if (r0 + k >= nrows) break;  // uniform over the workgroup
     float ddt = 0.0f;
     if (act) {
       const float d = dt[b * sdt_b + t * sdt_t];
-      const float bv = ldf(B + b * sB_b + t * sB_t + h);
-      const float ab = ldf(Abar + b * sa_b + t * sa_t + h);
-      const float gA = ldf(dAbar + b * sa_b + t * sa_t + h);
-      const float gB = ldf(dBbar + b * sb_b + t * sb_t + h);
-      const float x = d * a;
-      const float ex = exp_acc(x);
-      const float em1 = expm1_acc(x, ex);
-      ddt = gA * a * ab + gB * ex * bv;                           // :130-140
-      const float aa = a * a;
-      const float num = d * d * psi_from_exp(x, ex, em1) * (aa / (aa + 1e-18f));  // :146
-      const float da = gA * d * ab + gB * num * bv;                // :143-148
-      acc_dA = __builtin_fmaf(da, -neg_a, acc_dA);                 // :151, summed at :156
-      stf(dB + b * sB_b + t * sB_t + h, gB * em1 / (a + 1e-12f));  // :154, :157
+      float bv[V], ab[V], gA[V], gB[V], db[V];
+      ld_lanes<T, V>(B + b * sB_b + t * sB_t + h, bv);
+      ld_lanes<T, V>(Abar + b * sa_b + t * sa_t + h, ab);
+      ld_lanes<T, V>(dAbar + b * sa_b + t * sa_t + h, gA);
+      ld_lanes<T, V>(dBbar + b * sb_b + t * sb_t + h, gB);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float x = d * a[v], y = d * a2[v];
+        const float ex = exp2_fast(y);
+        const float em1 = expm1_base2(x, y, ex);
+        ddt += gA[v] * a[v] * ab[v] + gB[v] * ex * bv[v];                     // :130-140
+        const float num = d * d * psi_from_exp(x, ex, em1) * fac[v];          // :146
+        const float da = gA[v] * d * ab[v] + gB[v] * num * bv[v];             // :143-148
+        acc_dA[v] = __builtin_fmaf(da, a[v], acc_dA[v]);                      // :151, :156
+        db[v] = gB[v] * em1 * ia[v];                                          // :154, :157
+      }
+      st_lanes<T, V>(dB + b * sB_b + t * sB_t + h, db);
     }
     for (int o = 32; o > 0; o >>= 1) ddt += __shfl_xor(ddt, o);
     if (lane == 0) red[k][wave] = ddt;
+    if (++t == grid_t) {
+      t = 0;
+      ++b;
+    }
   }
-  if (act) part_dA[(int64_t)rg * hc + h] = acc_dA;
+  if (act) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) part_dA[(int64_t)rg * hc + h + v] = acc_dA[v];
+  }
   __syncthreads();
   if (threadIdx.x < kBwdRows) {
     const int64_t r = r0 + threadIdx.x;
@@ -245,22 +266,38 @@ __global__ __launch_bounds__(kBwdLanes) void zoh_bwd_pass1_kernel(
   }
 }
 
-__global__ void zoh_bwd_pass2_kernel(const float* __restrict__ part_dA,
-                                     const float* __restrict__ part_ddt, float* __restrict__ dA,
-                                     float* __restrict__ ddt, int64_t grid_t, int64_t nrows,
-                                     int64_t hc, int64_t n_rg, int64_t n_lb, int64_t sdt_b,
-                                     int64_t sdt_t) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < hc) {
+// dA[h] += sum over row groups of part_dA (workgroup = 64 lanes h x 16 waves;
+// wave w sums the row groups g = w mod 16 in order, then the 16 wave sums are
+// added in wave order); ddt[r] = sum over lane blocks of part_ddt.  Both
+// orders are fixed, so results are deterministic.
+constexpr int kRedWaves = 16;
+__global__ __launch_bounds__(64 * kRedWaves) void zoh_bwd_pass2_kernel(
+    const float* __restrict__ part_dA, const float* __restrict__ part_ddt, float* __restrict__ dA,
+    float* __restrict__ ddt, int64_t grid_t, int64_t nrows, int64_t hc, int64_t n_rg,
+    int64_t n_lb, int64_t sdt_b, int64_t sdt_t, int64_t n_hblk) {
+  __shared__ float red[kRedWaves][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if ((int64_t)blockIdx.x < n_hblk) {  // uniform: a dA workgroup
+    const int64_t h = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.0f;
-    for (int64_t g = 0; g < n_rg; ++g) s += part_dA[g * hc + i];
-    dA[i] += s;
-  } else if (i < hc + nrows) {
-    const int64_t r = i - hc;
-    float s = 0.0f;
-    for (int64_t g = 0; g < n_lb; ++g) s += part_ddt[g * nrows + r];
-    const int64_t b = r / grid_t, t = r - b * grid_t;
-    ddt[b * sdt_b + t * sdt_t] = s;
+    if (h < hc)
+      for (int64_t g = wave; g < n_rg; g += kRedWaves) s += part_dA[g * hc + h];
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && h < hc) {
+      float tot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kRedWaves; ++w) tot += red[w][lane];
+      dA[h] += tot;
+    }
+  } else {
+    const int64_t r = ((int64_t)blockIdx.x - n_hblk) * (64 * kRedWaves) + threadIdx.x;
+    if (r < nrows) {
+      float s = 0.0f;
+      for (int64_t g = 0; g < n_lb; ++g) s += part_ddt[g * nrows + r];
+      const int64_t b = r / grid_t, t = r - b * grid_t;
+      ddt[b * sdt_b + t * sdt_t] = s;
+    }
   }
 }
 
@@ -292,38 +329,53 @@ extern "C" int tssm_zoh_discretize_bwd(int dtype, const float* A_log, const void
   if (nrows == 0) return TSSM_OK;
   const int64_t need = tssm_zoh_discretize_bwd_workspace_bytes(grid_b, grid_t, h_cover);
   TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  // 4 lanes per thread when every row and A_log allow 16-byte (fp32) or
+  // 8-byte (16-bit) accesses
+  const int64_t ea = dtype == TSSM_F32 ? 16 : 8;
+  const bool v4 = h_cover % 4 == 0 && sB_b % 4 == 0 && sB_t % 4 == 0 && sa_b % 4 == 0 &&
+                  sa_t % 4 == 0 && sb_b % 4 == 0 && sb_t % 4 == 0 && aligned(A_log, 16) &&
+                  aligned(B, ea) && aligned(Abar, ea) && aligned(dAbar, ea) &&
+                  aligned(dBbar, ea) && aligned(dB, ea);
+  const int V = v4 ? 4 : 1;
+  const int64_t nthr = h_cover / V;
+  const int threads = nthr >= kBwdLanes ? kBwdLanes : (int)(cdiv64(nthr, 64) * 64);
   const int64_t n_rg = cdiv64(nrows, kBwdRows);
-  const int64_t n_lb = h_cover == 0 ? 1 : cdiv64(h_cover, kBwdLanes);
-  TSSM_CHECK(n_rg <= 65535, TSSM_ERR_UNSUPPORTED);
+  // lane blocks of threads * V lanes (never more than the workspace's 256-lane blocks)
+  const int64_t n_lb = h_cover == 0 ? 0 : cdiv64(h_cover, (int64_t)threads * V);
+  TSSM_CHECK(n_rg <= 2147483647 && n_lb <= 65535, TSSM_ERR_UNSUPPORTED);
   float* part_dA = reinterpret_cast<float*>(workspace);
   float* part_ddt = part_dA + n_rg * h_cover;
   const hipStream_t s = as_stream(stream);
-  if (h_cover == 0) {  // no lanes: ddt is the empty sum
-    const int64_t n = nrows;
-    hipLaunchKernelGGL(zoh_bwd_pass2_kernel, dim3((unsigned)cdiv64(n, 256)), dim3(256), 0, s,
-                       part_dA, part_ddt, dA, ddt, grid_t, nrows, (int64_t)0, n_rg, (int64_t)0,
-                       sdt_b, sdt_t);
-    return launch_status();
-  }
-  const int threads = h_cover >= kBwdLanes ? kBwdLanes : (int)(cdiv64(h_cover, 64) * 64);
-  const dim3 grid1((unsigned)n_lb, (unsigned)n_rg);
-#define TSSM_ZOH_BWD(TT)                                                                       \
-  hipLaunchKernelGGL(zoh_bwd_pass1_kernel<TT>, grid1, dim3(threads), 0, s, A_log,             \
-                     (const TT*)B, dt, (const TT*)Abar, (const TT*)dAbar, (const TT*)dBbar,    \
-                     (TT*)dB, part_dA, part_ddt, grid_t, nrows, h_cover, sB_b, sB_t, sdt_b,    \
-                     sdt_t, sa_b, sa_t, sb_b, sb_t)
-  switch (dtype) {
-    case TSSM_F32: TSSM_ZOH_BWD(float); break;
-    case TSSM_BF16: TSSM_ZOH_BWD(bf16_t); break;
-    case TSSM_F16: TSSM_ZOH_BWD(f16_t); break;
-    default: return TSSM_ERR_DTYPE;
-  }
+  if (h_cover > 0) {
+    const dim3 grid1((unsigned)n_rg, (unsigned)n_lb);
+#define TSSM_ZOH_BWD(TT)                                                                        \
+  if (v4)                                                                                        \
+    hipLaunchKernelGGL((zoh_bwd_pass1_kernel<TT, 4>), grid1, dim3(threads), 0, s, A_log,         \
+                       (const TT*)B, dt, (const TT*)Abar, (const TT*)dAbar, (const TT*)dBbar,    \
+                       (TT*)dB, part_dA, part_ddt, grid_t, nrows, h_cover, sB_b, sB_t, sdt_b,    \
+                       sdt_t, sa_b, sa_t, sb_b, sb_t);                                           \
+  else                                                                                           \
+    hipLaunchKernelGGL((zoh_bwd_pass1_kernel<TT, 1>), grid1, dim3(threads), 0, s, A_log,         \
+                       (const TT*)B, dt, (const TT*)Abar, (const TT*)dAbar, (const TT*)dBbar,    \
+                       (TT*)dB, part_dA, part_ddt, grid_t, nrows, h_cover, sB_b, sB_t, sdt_b,    \
+                       sdt_t, sa_b, sa_t, sb_b, sb_t)
+    switch (dtype) {
+      case TSSM_F32: TSSM_ZOH_BWD(float); break;
+      case TSSM_BF16: TSSM_ZOH_BWD(bf16_t); break;
+      case TSSM_F16: TSSM_ZOH_BWD(f16_t); break;
+      default: return TSSM_ERR_DTYPE;
+    }
 #undef TSSM_ZOH_BWD
-  int st = launch_status();
-  if (st != TSSM_OK) return st;
-  const int64_t n2 = h_cover + nrows;
-  hipLaunchKernelGGL(zoh_bwd_pass2_kernel, dim3((unsigned)cdiv64(n2, 256)), dim3(256), 0, s,
-                     part_dA, part_ddt, dA, ddt, grid_t, nrows, h_cover, n_rg, n_lb, sdt_b, sdt_t);
+    const int st = launch_status();
+    if (st != TSSM_OK) return st;
+  }
+  // pass 2: dA workgroups first, then the ddt workgroups (no lanes: ddt = 0)
+  const int64_t n_hblk = cdiv64(h_cover, 64);
+  const int64_t n2 = n_hblk + cdiv64(nrows, 64 * kRedWaves);
+  TSSM_CHECK(n2 <= 2147483647, TSSM_ERR_UNSUPPORTED);
+  hipLaunchKernelGGL(zoh_bwd_pass2_kernel, dim3((unsigned)n2), dim3(64 * kRedWaves), 0, s,
+                     part_dA, part_ddt, dA, ddt, grid_t, nrows, h_cover, n_rg, n_lb, sdt_b, sdt_t,
+                     n_hblk);
   return launch_status();
 }
 
