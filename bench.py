@@ -365,11 +365,11 @@ def rows_sweep(args, dev):
     Am = uni(0.5, 1.0, B, T, H)
     Dv = rnd(H)
     out = {}
-    timeit("a4-a8 ssm_forward (4 phase kernels)", f"B={B} L={T} H={H}", n * 6 * 4,
+    timeit("a4-a8 ssm_forward (single pass)", f"B={B} L={T} H={H}", n * 6 * 4,
            lambda: out.update(r=ss.ssm_forward(u, Am, Bm, Cm, Dv, BLK=256)))
     y_, h_ = out["r"]
     dY = rnd(B, T, H)
-    timeit("a20 ssm_backward (4 phase kernels)", f"B={B} L={T} H={H}", n * 10 * 4,
+    timeit("a20 ssm_backward (single pass)", f"B={B} L={T} H={H}", n * 10 * 4,
            lambda: ss.ssm_backward(u, Am, Bm, Cm, h_, dY, BLK=256))
     del u, Bm, Cm, Am, y_, h_, dY, out
     # a9-a11 multihead phase-exact kernels (reference layouts, fp32)

@@ -263,6 +263,24 @@ int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt, int
                         int64_t sC_l, int64_t sy_b, int64_t sy_l, int64_t chunk, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ elementwise scan, single pass
+ * The host functions ssm_forward / ssm_backward (ssm_scan.py:239-289) as one
+ * launch each over contiguous [B, L, H] tensors of `dtype` (D [H]): every
+ * input read once, every output written once; the state crosses chunks by a
+ * decoupled look-back.  forward: y, h.  backward: du = B dh, dA = h_{t-1} dh,
+ * dB = u dh, dC = dY h with dh_t = A_{t+1} dh_{t+1} + C_t dY_t.  H % 4 == 0;
+ * pointers 16-byte (fp32) / 8-byte (16-bit) aligned.  Workspace: zero-filled
+ * once, 256-aligned, tssm_ssm_scan_fused_workspace_bytes(B, L, H) bytes; one
+ * stream at a time. */
+int64_t tssm_ssm_scan_fused_workspace_bytes(int64_t nbatch, int64_t L, int64_t H);
+int tssm_ssm_forward_fused(int dtype, const void* u, const void* A, const void* B, const void* C,
+                           const void* D, void* y, void* h, int64_t nbatch, int64_t L, int64_t H,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+int tssm_ssm_backward_fused(int dtype, const void* u, const void* A, const void* B,
+                            const void* C, const void* h, const void* dY, void* du, void* dA,
+                            void* dB, void* dC, int64_t nbatch, int64_t L, int64_t H,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ model layers
  * The reference's layers around the scan.  Arithmetic fp32; every float
  * tensor of one call has `dtype` (TSSM_F32/BF16/F16).  Rows are the

@@ -154,6 +154,32 @@ def test_ssm_forward_backward(dev, BLK):
         assert_close(got, ref, 1e-5, n)
 
 
+@pytest.mark.parametrize("Bsz,L,H,zeros", [(2, 5000, 256, False), (3, 129, 68, True),
+                                            (1, 1, 4, False), (2, 300, 42, False),
+                                            (2, 1000, 64, True)])
+def test_ssm_forward_backward_shapes(dev, Bsz, L, H, zeros):
+    """Single-pass path (many chunks, partial lane blocks, one step, tiles whose
+    decay product is exactly zero) and the phase-kernel path (H % 4 != 0)
+    against the oracle."""
+    import ssm_scan as ss
+    g = torch.Generator().manual_seed(L + H)
+    u, B, C, dY = (torch.randn(Bsz, L, H, generator=g).to(dev) for _ in range(4))
+    A = torch.empty(Bsz, L, H).uniform_(0.9, 1.0, generator=g)
+    if zeros:
+        A[:, ::97, ::3] = 0.0
+    A = A.to(dev)
+    D = torch.randn(H, generator=g).to(dev)
+    y, h = ss.ssm_forward(u, A, B, C, D)
+    du, dA, dB, dC = ss.ssm_backward(u, A, B, C, h, dY)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssm_forward(u, A, B, C, D)
+    assert_close(h, h_ref, 1e-5, "h")
+    assert_close(y, y_ref, 1e-5, "y")
+    for got, ref, n in zip((du, dA, dB, dC), O.ssm_backward(u, A, B, C, h_ref, dY),
+                           "du dA dB dC".split()):
+        assert_close(got, ref, 1e-5, n)
+
+
 def test_ssm_phase_intermediates(dev):
     import ssm_scan as ss
     g = torch.Generator().manual_seed(1)

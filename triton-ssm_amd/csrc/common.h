@@ -177,6 +177,36 @@ __device__ inline float expm1_acc(float x, float ex) {
 // Accurate exp for the fp32 paths: ocml expf (correctly range-reduced).
 __device__ inline float exp_acc(float x) { return expf(x); }
 
+// V consecutive elements as floats: V = 4 uses one 16-byte (fp32) or 8-byte
+// (16-bit) access, V = 1 a scalar one.
+template <typename T, int V>
+__device__ inline void ld_lanes(const T* p, float* v) {
+  if constexpr (V == 1) {
+    v[0] = ldf(p);
+  } else if constexpr (sizeof(T) == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else {
+    T tmp[4];
+    *reinterpret_cast<uint2*>(tmp) = *reinterpret_cast<const uint2*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = ldf(tmp + j);
+  }
+}
+template <typename T, int V>
+__device__ inline void st_lanes(T* p, const float* v) {
+  if constexpr (V == 1) {
+    stf(p, v[0]);
+  } else if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    T tmp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) stf(tmp + j, v[j]);
+    *reinterpret_cast<uint2*>(p) = *reinterpret_cast<const uint2*>(tmp);
+  }
+}
+
 // ---------------------------------------------------------------- status
 #define TSSM_CHECK(cond, code) \
   do {                         \

@@ -143,11 +143,39 @@ def _nxt_pow2(n):
     return 1 << (n - 1).bit_length()
 
 
+def _fused_ok(ts, H) -> bool:
+    """One launch replaces the four phase kernels when every operand is a
+    contiguous tensor of one dtype on the GPU, H % 4 == 0 and the base
+    pointers allow 16-byte (fp32) / 8-byte (16-bit) accesses."""
+    d = ts[0].dtype
+    if d not in (torch.float32, torch.bfloat16, torch.float16) or H % 4:
+        return False
+    al = 16 if d == torch.float32 else 8
+    return all(isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == d and t.is_contiguous()
+               and t.data_ptr() % al == 0 for t in ts)
+
+
+def _fused_ws(t, Bsz, L, H):
+    from tssm import workspace
+    n = _lib.lib().tssm_ssm_scan_fused_workspace_bytes(Bsz, L, H)
+    stream = stream_handle(t)
+    return workspace.get(t.device, stream, n), stream
+
+
 def ssm_forward(u, A, B, C, D, BLK=256):
     """u, A, B, C: [batch, seqlen, H] (A, B already discretized); D: [H].
     Returns (y, h), both [batch, seqlen, H] -- h is the full state trajectory
-    (ssm_scan.py:239-264)."""
+    (ssm_scan.py:239-264).  Runs as one single-pass launch where the operands
+    allow (then BLK, which only shapes the phase kernels' intermediates, does
+    not apply), else as the reference's four phase kernels."""
     Bsz, L, H = u.shape
+    if _fused_ok([u, A, B, C, D], H) and D.numel() == H and A.shape == u.shape == B.shape == C.shape:
+        y_out, h_out = torch.empty_like(u), torch.empty_like(u)
+        ws, stream = _fused_ws(u, Bsz, L, H)
+        _lib.call("tssm_ssm_forward_fused", dcode(u, "u"), u.data_ptr(), A.data_ptr(),
+                  B.data_ptr(), C.data_ptr(), D.data_ptr(), y_out.data_ptr(), h_out.data_ptr(),
+                  Bsz, L, H, ws.data_ptr(), ws.numel(), stream)
+        return y_out, h_out
     nrows = Bsz * H
     nblk = _nxt_pow2((L + BLK - 1) // BLK)
     loc_a = torch.empty_like(A)
@@ -164,8 +192,17 @@ def ssm_forward(u, A, B, C, D, BLK=256):
 
 
 def ssm_backward(u, A, B, C, h, dY, BLK=256):
-    """Returns (du, dA, dB, dC) (ssm_scan.py:267-289)."""
+    """Returns (du, dA, dB, dC) (ssm_scan.py:267-289); one single-pass launch
+    where the operands allow, else the reference's four phase kernels."""
     Bsz, L, H = u.shape
+    ts = [u, A, B, C, h, dY]
+    if _fused_ok(ts, H) and all(t.shape == u.shape for t in ts):
+        du, dA, dB, dC = (torch.empty_like(u) for _ in range(4))
+        ws, stream = _fused_ws(u, Bsz, L, H)
+        _lib.call("tssm_ssm_backward_fused", dcode(u, "u"), *(t.data_ptr() for t in ts),
+                  du.data_ptr(), dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), Bsz, L, H,
+                  ws.data_ptr(), ws.numel(), stream)
+        return du, dA, dB, dC
     nrows = Bsz * H
     nblk = _nxt_pow2((L + BLK - 1) // BLK)
     loc_a = torch.empty_like(A)
