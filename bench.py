@@ -428,7 +428,7 @@ def rows_sweep(args, dev):
         timeit(f"a16/a17 streaming_ssm_inplace ({tag})", f"S={S} H={Hs}", S * Hs * 5 * es,
                lambda: kern[(S, Hs // 256)](v, hs, Abs, Bbs, Cs, Ds, ys, S, Hs, *v.stride(),
                                             *hs.stride(), *Cs.stride(), BLOCK_H=256))
-    Sr, Hr, KR = 1024, 256, 11
+    Sr, Hr, KR = 4096, 1024, 11
     ring_V, ring_M = rnd(Sr, KR, Hr), (torch.rand(Sr, KR, Hr, device=dev) < 0.3).float()
     ring_tau = torch.arange(KR, device=dev, dtype=torch.float32).repeat(Sr, 1)
     head = torch.zeros(Sr, dtype=torch.int32, device=dev)

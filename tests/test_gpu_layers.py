@@ -17,7 +17,8 @@ def _r(shape, seed, dtype=torch.float32, scale=1.0, shift=0.0):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("H,BH", [(64, 64), (100, 128), (1024, 1024), (300, 512)])
+@pytest.mark.parametrize("H,BH", [(64, 64), (100, 128), (1024, 1024), (300, 512), (99, 128),
+                                  (2500, 4096)])
 def test_layernorm_forward(dev, dtype, H, BH):
     import fused_ssm_interp as fs
     B, L = 3, 5
@@ -46,7 +47,8 @@ def test_layernorm_partial_grid(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,L,H,BH", [(3, 5, 100, 128), (4, 200, 256, 256), (2, 3, 1000, 1024)])
+@pytest.mark.parametrize("B,L,H,BH", [(3, 5, 100, 128), (4, 200, 256, 256), (2, 3, 1000, 1024),
+                                      (3, 70, 99, 128), (2, 4, 2500, 4096), (8, 1100, 64, 64)])
 def test_layernorm_backward(dev, dtype, B, L, H, BH):
     import fused_ssm_interp as fs
     x = _r((B, L, H), 10 + H, dtype, 1.5, 0.3).to(dev)

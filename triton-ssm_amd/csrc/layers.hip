@@ -17,6 +17,8 @@
 // the block partials in order.
 //
 // Arithmetic is fp32 for every I/O dtype (fp32, bf16, fp16).
+#include <initializer_list>
+
 #include "common.h"
 
 namespace tssm {
@@ -71,6 +73,179 @@ __global__ __launch_bounds__(kThreads) void layernorm_fwd_kernel(
     row_stats(x + o, H, pad, eps, lane, &mu, &inv);
     for (int64_t h = lane; h < H; h += 64)
       stf(out + o + h, __builtin_fmaf((ldf(x + o + h) - mu) * inv, ldf(w + h), ldf(bias + h)));
+  }
+}
+
+// Rows held in registers: NV 4-lane vectors per lane (H <= 256 NV, H % 4 == 0,
+// 16-byte / 8-byte aligned rows), so each row is read from HBM once.  Lane
+// chunk j of a row covers elements 4 (lane + 64 j) .. +3.
+template <typename T, int NV>
+struct RowRegs {
+  float v[NV][4];
+  // chunks past H read chunk 0 (no branch around the loads); every use skips them
+  __device__ inline void load(const T* row, int lane, int64_t H) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e = 4 * (lane + 64 * (int64_t)j);
+      ld_lanes<T, 4>(row + (e < H ? e : 0), v[j]);
+    }
+  }
+};
+
+template <typename T, int NV>
+__device__ inline void row_stats_regs(const RowRegs<T, NV>& x, int lane, int64_t H, int64_t pad,
+                                      float eps, float* mu_out, float* inv_out) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+    if (4 * (lane + 64 * (int64_t)j) < H) s += (x.v[j][0] + x.v[j][1]) + (x.v[j][2] + x.v[j][3]);
+  const float mu = wave_sum(s) / (float)H;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (4 * (lane + 64 * (int64_t)j) >= H) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float c = x.v[j][e] - mu;
+      q = __builtin_fmaf(c, c, q);
+    }
+  }
+  const float var = (wave_sum(q) + (float)pad * mu * mu) / (float)H;
+  *mu_out = mu;
+  *inv_out = 1.0f / sqrtf(var + eps);
+}
+
+template <typename T, int NV>
+__global__ __launch_bounds__(kThreads) void layernorm_fwd_reg_kernel(
+    const T* __restrict__ x, const T* __restrict__ w, const T* __restrict__ bias,
+    T* __restrict__ out, Rows rows, int64_t nrow, int64_t H, int64_t pad, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wpb = kThreads / 64;
+  RowRegs<T, NV> wr, br;
+  wr.load(w, lane, H);
+  br.load(bias, lane, H);
+  for (int64_t r = blockIdx.x * wpb + (threadIdx.x >> 6); r < nrow; r += (int64_t)gridDim.x * wpb) {
+    const int64_t o = rows.base(r);
+    RowRegs<T, NV> xr;
+    xr.load(x + o, lane, H);
+    float mu, inv;
+    row_stats_regs(xr, lane, H, pad, eps, &mu, &inv);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e = 4 * (lane + 64 * (int64_t)j);
+      if (e >= H) continue;
+      float ov[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        ov[k] = __builtin_fmaf((xr.v[j][k] - mu) * inv, wr.v[j][k], br.v[j][k]);
+      st_lanes<T, 4>(out + o + e, ov);
+    }
+  }
+}
+
+// Backward with rows in registers: dx per row, and this wave's partial sums of
+// dout*xhat and dout over its rows (row r = wave, wave + nwaves, ...) kept in
+// registers and written to part[wave][H] / part[nwaves + wave][H].
+template <typename T, int NV>
+__global__ __launch_bounds__(kThreads) void layernorm_bwd_reg_kernel(
+    const T* __restrict__ dout, const T* __restrict__ x, const T* __restrict__ w,
+    T* __restrict__ dx, float* __restrict__ part, Rows rows, int64_t nrow, int64_t H,
+    int64_t pad, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wpb = kThreads / 64;
+  const int64_t wv = blockIdx.x * wpb + (threadIdx.x >> 6);
+  const int64_t nwaves = (int64_t)gridDim.x * wpb;
+  RowRegs<T, NV> wr;
+  wr.load(w, lane, H);
+  float pw[NV][4], pb[NV][4];
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pw[j][k] = pb[j][k] = 0.0f;
+  for (int64_t r = wv; r < nrow; r += nwaves) {
+    const int64_t o = rows.base(r);
+    RowRegs<T, NV> xr, gr;
+    xr.load(x + o, lane, H);
+    gr.load(dout + o, lane, H);
+    float mu, inv;
+    row_stats_regs(xr, lane, H, pad, eps, &mu, &inv);
+    float s_dxc = 0.0f, s_dx = 0.0f, s_xc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      if (4 * (lane + 64 * (int64_t)j) >= H) continue;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float xc = xr.v[j][k] - mu;
+        const float dxh = gr.v[j][k] * wr.v[j][k];
+        s_dxc = __builtin_fmaf(dxh, xc, s_dxc);
+        s_dx += dxh;
+        s_xc += xc;
+        pw[j][k] = __builtin_fmaf(gr.v[j][k], xc * inv, pw[j][k]);
+        pb[j][k] += gr.v[j][k];
+      }
+    }
+    s_dxc = wave_sum(s_dxc);
+    s_dx = wave_sum(s_dx);
+    s_xc = wave_sum(s_xc);
+    const float dvar = s_dxc * -0.5f * inv * inv * inv;
+    const float sum_m2xc = -2.0f * s_xc + 2.0f * (float)pad * mu;
+    const float dmu = -inv * s_dx + dvar * sum_m2xc / (float)H;
+    const float k2 = 2.0f * dvar / (float)H, k0 = dmu / (float)H;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t e = 4 * (lane + 64 * (int64_t)j);
+      if (e >= H) continue;
+      float dv[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float xc = xr.v[j][k] - mu;
+        dv[k] = __builtin_fmaf(gr.v[j][k] * wr.v[j][k], inv, __builtin_fmaf(k2, xc, k0));
+      }
+      st_lanes<T, 4>(dx + o + e, dv);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t e = 4 * (lane + 64 * (int64_t)j);
+    if (e >= H) continue;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      part[wv * H + e + k] = pw[j][k];
+      part[(nwaves + wv) * H + e + k] = pb[j][k];
+    }
+  }
+}
+
+// dw[h] += sum_k part[k][h], db[h] += sum_k part[nblk + k][h]: workgroup = 64
+// lanes h x 16 waves, wave w sums k = w, w + 16, ... in order, then the 16 wave
+// sums are added in wave order (a fixed order: deterministic).
+constexpr int kRedWaves = 16;
+template <typename T>
+__global__ __launch_bounds__(64 * kRedWaves) void ln_param_reduce_kernel(
+    const float* __restrict__ part, T* __restrict__ dw, T* __restrict__ db, int64_t H,
+    int64_t nblk) {
+  __shared__ float red[2][kRedWaves][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t h = (int64_t)blockIdx.x * 64 + lane;
+  float sw = 0.0f, sb = 0.0f;
+  if (h < H) {
+    for (int64_t k = wave; k < nblk; k += kRedWaves) {
+      sw += part[k * H + h];
+      sb += part[(nblk + k) * H + h];
+    }
+  }
+  red[0][wave][lane] = sw;
+  red[1][wave][lane] = sb;
+  __syncthreads();
+  if (wave == 0 && h < H) {
+    float tw = 0.0f, tb = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kRedWaves; ++k) {
+      tw += red[0][k][lane];
+      tb += red[1][k][lane];
+    }
+    stf(dw + h, ldf(dw + h) + tw);
+    stf(db + h, ldf(db + h) + tb);
   }
 }
 
@@ -275,6 +450,18 @@ inline bool io_dtype(int d) { return d == TSSM_F32 || d == TSSM_BF16 || d == TSS
     default: { using T = f16_t; LAUNCH; } break;         \
   }
 
+// 4-lane vectors per lane for rows held in registers (0: rows do not qualify).
+inline int reg_nv(int dtype, int64_t H, int64_t sb, int64_t sl,
+                  std::initializer_list<const void*> ptrs) {
+  if (H % 4 != 0 || H > 2048 || sb % 4 != 0 || sl % 4 != 0) return 0;
+  const uintptr_t al = dtype == TSSM_F32 ? 16 : 8;
+  for (const void* p : ptrs)
+    if (!aligned(p, al)) return 0;
+  const int64_t nv = (H + 255) / 256;
+  return nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
+}
+constexpr int64_t kLnBwdMaxWaves = 2048;   // waves of the register backward (partial rows)
+
 }  // namespace
 }  // namespace tssm
 
@@ -294,10 +481,24 @@ extern "C" int tssm_layernorm_fwd(int dtype, const void* x, const void* w, const
   if (nrow == 0) return TSSM_OK;
   const Rows rows{grid_l, stride_b, stride_l};
   const hipStream_t s = as_stream(stream);
-  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((layernorm_fwd_kernel<T>), dim3(row_grid(nrow)),
-                                          dim3(kThreads), 0, s, (const T*)x, (const T*)w,
-                                          (const T*)bias, (T*)out, rows, nrow, H, block_h - H,
-                                          eps));
+  const int nv = reg_nv(dtype, H, stride_b, stride_l, {x, w, bias, out});
+#define TSSM_LN_REG(NV)                                                                   \
+  hipLaunchKernelGGL((layernorm_fwd_reg_kernel<T, NV>), dim3(row_grid(nrow)), dim3(kThreads), \
+                     0, s, (const T*)x, (const T*)w, (const T*)bias, (T*)out, rows, nrow, H,  \
+                     block_h - H, eps)
+  TSSM_DISPATCH(dtype, {
+    switch (nv) {
+      case 1: TSSM_LN_REG(1); break;
+      case 2: TSSM_LN_REG(2); break;
+      case 4: TSSM_LN_REG(4); break;
+      case 8: TSSM_LN_REG(8); break;
+      default:
+        hipLaunchKernelGGL((layernorm_fwd_kernel<T>), dim3(row_grid(nrow)), dim3(kThreads), 0, s,
+                           (const T*)x, (const T*)w, (const T*)bias, (T*)out, rows, nrow, H,
+                           block_h - H, eps);
+    }
+  });
+#undef TSSM_LN_REG
   return launch_status();
 }
 
@@ -305,7 +506,9 @@ extern "C" int64_t tssm_layernorm_bwd_workspace_bytes(int64_t grid_b, int64_t gr
   if (grid_b < 0 || grid_l < 0 || H <= 0) return -1;
   const int64_t nrow = grid_b * grid_l;
   const int64_t nblk = (nrow + kLnRowBlock - 1) / kLnRowBlock;
-  return (2 * nrow + 2 * nblk * H) * (int64_t)sizeof(float);
+  const int64_t rows_path = 2 * nrow + 2 * nblk * H;            // stats + column partials
+  const int64_t reg_path = 2 * kLnBwdMaxWaves * H;               // per-wave partials
+  return (rows_path > reg_path ? rows_path : reg_path) * (int64_t)sizeof(float);
 }
 
 extern "C" int tssm_layernorm_bwd(int dtype, const void* dout, const void* x, const void* w,
@@ -329,6 +532,30 @@ extern "C" int tssm_layernorm_bwd(int dtype, const void* dout, const void* x, co
   float* part = stats + 2 * nrow;
   const Rows rows{grid_l, stride_b, stride_l};
   const hipStream_t s = as_stream(stream);
+  const int nv = reg_nv(dtype, H, stride_b, stride_l, {dout, x, w, dx});
+  if (nv > 0) {
+    int64_t g = row_grid(nrow);
+    if (g * (kThreads / 64) > kLnBwdMaxWaves) g = kLnBwdMaxWaves / (kThreads / 64);
+    const int64_t nwaves = g * (kThreads / 64);
+    float* wpart = reinterpret_cast<float*>(workspace);
+    const dim3 gred((unsigned)((H + 63) / 64));
+#define TSSM_LNB_REG(NV)                                                                      \
+  hipLaunchKernelGGL((layernorm_bwd_reg_kernel<T, NV>), dim3((unsigned)g), dim3(kThreads), 0, \
+                     s, (const T*)dout, (const T*)x, (const T*)w, (T*)dx, wpart, rows, nrow, H,  \
+                     block_h - H, eps)
+    TSSM_DISPATCH(dtype, {
+      switch (nv) {
+        case 1: TSSM_LNB_REG(1); break;
+        case 2: TSSM_LNB_REG(2); break;
+        case 4: TSSM_LNB_REG(4); break;
+        default: TSSM_LNB_REG(8); break;
+      }
+      hipLaunchKernelGGL((ln_param_reduce_kernel<T>), gred, dim3(64 * kRedWaves), 0, s, wpart,
+                         (T*)dw, (T*)db, H, nwaves);
+    });
+#undef TSSM_LNB_REG
+    return launch_status();
+  }
   const dim3 gcol((unsigned)((H + kThreads - 1) / kThreads), (unsigned)nblk);
   const dim3 gfin((unsigned)((H + kThreads - 1) / kThreads));
   TSSM_DISPATCH(dtype, {

@@ -444,16 +444,36 @@ __global__ void mh_output_kernel(const float* __restrict__ loc_a, const float* _
     x_pref = carry[rows_tot * nblk + rf * nblk + blk - 1];
   }
   const float dv = u_ok ? D[uo] : 0.0f;
-  for (int64_t t = ts; t < te; ++t) {
-    float contrib = 0.0f;
-    if (active) {
-      const int64_t off = bi * (L * nh * hd) + t * (nh * hd) + hi * hd + p;
-      const float hv = loc_a[off] * x_pref + loc_x[off];
-      contrib = ldf(Cm + bi * sC_b + t * sC_l + hi * sC_h + p) * hv;
-      if (u_ok) contrib += dv * ldf(u + bi * su_b + t * su_l + uo);
+  // kU steps at a time: every load of the batch is issued before the first
+  // reduction (steps past the block re-read its last step and store nothing)
+  constexpr int kU = 8;
+  const bool one_wave = blockDim.x == 64;
+  for (int64_t t = ts; t < te; t += kU) {
+    float c[kU];
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      const int64_t tt = t + k < te ? t + k : te - 1;
+      float contrib = 0.0f;
+      if (active) {
+        const int64_t off = bi * (L * nh * hd) + tt * (nh * hd) + hi * hd + p;
+        const float hv = loc_a[off] * x_pref + loc_x[off];
+        contrib = ldf(Cm + bi * sC_b + tt * sC_l + hi * sC_h + p) * hv;
+        if (u_ok) contrib += dv * ldf(u + bi * su_b + tt * su_l + uo);
+      }
+      c[k] = contrib;
     }
-    const float yv = block_sum(contrib, red);
-    if (u_ok) stf(y + bi * (L * H) + t * H + uo, yv);
+    if (one_wave) {  // uniform: the kU wave sums interleaved
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int k = 0; k < kU; ++k) c[k] += __shfl_xor(c[k], o);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kU; ++k) c[k] = block_sum(c[k], red);
+    }
+#pragma unroll
+    for (int k = 0; k < kU; ++k)
+      if (u_ok && t + k < te) stf(y + bi * (L * H) + (t + k) * H + uo, c[k]);
   }
 }
 

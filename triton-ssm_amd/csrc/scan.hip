@@ -61,23 +61,29 @@ __global__ void carry_scan_kernel(T* __restrict__ carry, int64_t nrows, int64_t 
   if (r >= grid_rows) return;
   T* ca = carry + r * nblk;
   T* cx = carry + nrows * nblk + r * nblk;
-  if (!reverse) {
-    float A = ldf(ca), X = ldf(cx);
-    for (int64_t k = 1; k < nblk; ++k) {
-      const float a = ldf(ca + k), x = ldf(cx + k);
-      X = a * X + x;
-      A = a * A;
-      stf(ca + k, A);
-      stf(cx + k, X);
+  // kB carries per batch of loads, all issued before the batch is folded in;
+  // reverse order walks k = nblk-1 .. 0.  The first carry is kept as loaded.
+  constexpr int kB = 8;
+  float A = 1.0f, X = 0.0f;
+  for (int64_t k0 = 0; k0 < nblk; k0 += kB) {
+    float av[kB], xv[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const int64_t i = k0 + j < nblk ? k0 + j : nblk - 1;
+      const int64_t k = reverse ? nblk - 1 - i : i;
+      av[j] = ldf(ca + k);
+      xv[j] = ldf(cx + k);
     }
-  } else {
-    float A = ldf(ca + nblk - 1), X = ldf(cx + nblk - 1);
-    for (int64_t k = nblk - 2; k >= 0; --k) {
-      const float a = ldf(ca + k), x = ldf(cx + k);
-      X = a * X + x;
-      A = a * A;
-      stf(ca + k, A);
-      stf(cx + k, X);
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      if (k0 + j >= nblk) break;
+      const int64_t k = reverse ? nblk - 1 - (k0 + j) : k0 + j;
+      X = __builtin_fmaf(av[j], X, xv[j]);
+      A = av[j] * A;
+      if (k0 + j > 0) {
+        stf(ca + k, A);
+        stf(cx + k, X);
+      }
     }
   }
 }
