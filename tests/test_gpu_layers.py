@@ -75,9 +75,10 @@ def test_layernorm_backward(dev, dtype, B, L, H, BH):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_swiglu_forward_backward(dev, dtype):
+@pytest.mark.parametrize("H", [333, 336])   # 1-lane and 4-lane accesses
+def test_swiglu_forward_backward(dev, dtype, H):
     import fused_ssm_interp as fs
-    B, L, H = 3, 7, 333
+    B, L = 3, 7
     gate = _r((B, L, H), 20, dtype, 3.0).to(dev)
     up = _r((B, L, H), 21, dtype).to(dev)
     dout = _r((B, L, H), 22, dtype).to(dev)
@@ -116,9 +117,10 @@ def test_residual_and_dropout(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_mean_pool_logit(dev, dtype):
+@pytest.mark.parametrize("H", [70, 72])
+def test_mean_pool_logit(dev, dtype, H):
     import streaming_inference_kernel as sk
-    B, T, H = 4, 300, 70
+    B, T = 4, 300
     base = _r((B, T + 2, H), 40, dtype).to(dev)
     h = base[:, 1:T + 1]
     W = _r((H,), 41, dtype).to(dev)
@@ -135,9 +137,10 @@ def test_mean_pool_logit(dev, dtype):
 
 
 @pytest.mark.parametrize("mdtype", [torch.bool, torch.uint8, torch.int32, torch.float32])
-def test_masked_fill_zero(dev, mdtype):
+@pytest.mark.parametrize("H", [37, 40])
+def test_masked_fill_zero(dev, mdtype, H):
     import streaming_inference_kernel as sk
-    B, T, H, BLOCK = 3, 50, 37, 256
+    B, T, BLOCK = 3, 50, 256
     x = _r((B, T, H), 50).to(dev)
     m = (torch.rand(B, T, generator=torch.Generator().manual_seed(51)) < 0.6).to(mdtype).to(dev)
     out = torch.full_like(x, float("nan"))
@@ -145,3 +148,10 @@ def test_masked_fill_zero(dev, mdtype):
     sk.masked_fill_zero_kernel[(-(-n // BLOCK),)](x, m, out, B, T, H, BLOCK=BLOCK)
     torch.cuda.synchronize()
     assert np.array_equal(np64(out), O.masked_fill_zero(x, m))
+    # a grid covering a flat prefix that ends inside a row
+    out2 = torch.full_like(x, float("nan"))
+    sk.masked_fill_zero_kernel[(7,)](x, m, out2, B, T, H, BLOCK=BLOCK)
+    torch.cuda.synchronize()
+    k = 7 * BLOCK
+    assert np.array_equal(np64(out2).reshape(-1)[:k], O.masked_fill_zero(x, m).reshape(-1)[:k])
+    assert torch.isnan(out2.reshape(-1)[k:]).all()

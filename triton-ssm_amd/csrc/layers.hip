@@ -26,7 +26,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kLnRowBlock = 128;   // rows per column-partial block
-constexpr int kPoolRows = 64;      // (t) rows per mean-pool block
+constexpr int kPoolRows = 16;      // (t) rows per mean-pool block
 
 __device__ inline float wave_sum(float v) {
 #pragma unroll
@@ -328,40 +328,57 @@ __global__ __launch_bounds__(kThreads) void ln_param_final_kernel(
 
 __device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
 
-// Elements of (grid_b x grid_l) rows of H, flat: element i -> row i / H.
-struct RowElems {
-  Rows rows;
-  int64_t H;
-  __device__ int64_t off(int64_t i) const {
-    const int64_t r = i / H;
-    return rows.base(r) + (i - r * H);
-  }
-};
-
-template <typename T>
-__global__ __launch_bounds__(kThreads) void swiglu_fwd_kernel(
-    const T* __restrict__ gate, const T* __restrict__ up, T* __restrict__ out, RowElems e,
-    int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kThreads) {
-    const int64_t o = e.off(i);
-    const float g = ldf(gate + o);
-    stf(out + o, g * sigmoid(g) * ldf(up + o));
+// Row-elementwise launch: workgroup = 256 threads x V lanes h (grid y) over
+// kRowsWG consecutive rows (grid x); the row's offset advances without a
+// division per element.
+constexpr int kRowsWG = 4;
+template <int V, typename F>
+__device__ inline void for_rows(const Rows& rows, int64_t nrow, int64_t H, F&& f) {
+  const int64_t h = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * V;
+  if (h >= H) return;
+  const int64_t r0 = (int64_t)blockIdx.x * kRowsWG;
+  int64_t b = r0 / rows.grid_l, l = r0 - b * rows.grid_l;
+  for (int k = 0; k < kRowsWG && r0 + k < nrow; ++k) {
+    f(r0 + k, b * rows.sb + l * rows.sl + h, h);
+    if (++l == rows.grid_l) {
+      l = 0;
+      ++b;
+    }
   }
 }
 
-template <typename T>
+template <typename T, int V>
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_kernel(
+    const T* __restrict__ gate, const T* __restrict__ up, T* __restrict__ out, Rows rows,
+    int64_t nrow, int64_t H) {
+  for_rows<V>(rows, nrow, H, [&](int64_t, int64_t o, int64_t) {
+    float g[V], u[V], y[V];
+    ld_lanes<T, V>(gate + o, g);
+    ld_lanes<T, V>(up + o, u);
+#pragma unroll
+    for (int v = 0; v < V; ++v) y[v] = g[v] * sigmoid(g[v]) * u[v];
+    st_lanes<T, V>(out + o, y);
+  });
+}
+
+template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void swiglu_bwd_kernel(
     const T* __restrict__ dout, const T* __restrict__ gate, const T* __restrict__ up,
-    T* __restrict__ dgate, T* __restrict__ dup, RowElems e, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kThreads) {
-    const int64_t o = e.off(i);
-    const float g = ldf(gate + o), u = ldf(up + o), d = ldf(dout + o);
-    const float s = sigmoid(g);
-    stf(dup + o, d * g * s);
-    stf(dgate + o, d * u * s * __builtin_fmaf(g, 1.0f - s, 1.0f));
-  }
+    T* __restrict__ dgate, T* __restrict__ dup, Rows rows, int64_t nrow, int64_t H) {
+  for_rows<V>(rows, nrow, H, [&](int64_t, int64_t o, int64_t) {
+    float g[V], u[V], d[V], dg[V], du[V];
+    ld_lanes<T, V>(gate + o, g);
+    ld_lanes<T, V>(up + o, u);
+    ld_lanes<T, V>(dout + o, d);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const float sg = sigmoid(g[v]);
+      du[v] = d[v] * g[v] * sg;
+      dg[v] = d[v] * u[v] * sg * __builtin_fmaf(g[v], 1.0f - sg, 1.0f);
+    }
+    st_lanes<T, V>(dup + o, du);
+    st_lanes<T, V>(dgate + o, dg);
+  });
 }
 
 template <typename T>
@@ -377,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(
 
 // Partial dot products of W with rows [blockIdx.y * kPoolRows, +kPoolRows) of
 // batch blockIdx.x.
-template <typename T>
+template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void pool_partial_kernel(
     const T* __restrict__ h, const T* __restrict__ W, float* __restrict__ part, int64_t T_,
     int64_t H, int64_t sb, int64_t st, int64_t nblk) {
@@ -386,9 +403,15 @@ __global__ __launch_bounds__(kThreads) void pool_partial_kernel(
   const int64_t t0 = (int64_t)blockIdx.y * kPoolRows;
   const int64_t t1 = t0 + kPoolRows < T_ ? t0 + kPoolRows : T_;
   float acc = 0.0f;
-  for (int64_t t = t0; t < t1; ++t) {
-    const T* row = h + b * sb + t * st;
-    for (int64_t k = threadIdx.x; k < H; k += kThreads) acc = __builtin_fmaf(ldf(W + k), ldf(row + k), acc);
+  for (int64_t k = (int64_t)threadIdx.x * V; k < H; k += (int64_t)kThreads * V) {
+    float w[V];
+    ld_lanes<T, V>(W + k, w);
+    for (int64_t t = t0; t < t1; ++t) {
+      float x[V];
+      ld_lanes<T, V>(h + b * sb + t * st + k, x);
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc = __builtin_fmaf(w[v], x[v], acc);
+    }
   }
   acc = wave_sum(acc);
   if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = acc;
@@ -422,13 +445,22 @@ __device__ inline bool mask_on(const void* m, int64_t i, int code) {
   }
 }
 
-template <typename T>
+// Rows (b, t) of H contiguous elements; the row's mask value is uniform over
+// the workgroup.  Elements at or past n (a partial last row) are not touched.
+template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void masked_fill_kernel(
     const T* __restrict__ x, const void* __restrict__ mask, int mcode, T* __restrict__ out,
     int64_t n, int64_t H) {
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * kThreads)
-    stf(out + i, mask_on(mask, i / H, mcode) ? ldf(x + i) : 0.0f);
+  const Rows rows{(n + H - 1) / H, 0, H};
+  for_rows<V>(rows, rows.grid_l, H, [&](int64_t r, int64_t o, int64_t) {
+    if (o >= n) return;  // V divides n, so a vector is whole or absent
+    const bool on = mask_on(mask, r, mcode);
+    float v[V];
+    ld_lanes<T, V>(x + o, v);
+#pragma unroll
+    for (int k = 0; k < V; ++k) v[k] = on ? v[k] : 0.0f;
+    st_lanes<T, V>(out + o, v);
+  });
 }
 
 // Grid of a flat loop over n items: enough workgroups to fill the chip, at
@@ -449,6 +481,23 @@ inline bool io_dtype(int d) { return d == TSSM_F32 || d == TSSM_BF16 || d == TSS
     case TSSM_BF16: { using T = bf16_t; LAUNCH; } break; \
     default: { using T = f16_t; LAUNCH; } break;         \
   }
+
+// Rows of H elements allow 4-lane vectors: H and the row strides multiples of
+// 4, base pointers 16-byte (fp32) / 8-byte (16-bit) aligned.
+inline bool vec4_rows(int dtype, int64_t H, int64_t sb, int64_t sl,
+                      std::initializer_list<const void*> ptrs) {
+  if (H % 4 != 0 || sb % 4 != 0 || sl % 4 != 0) return false;
+  const uintptr_t al = dtype == TSSM_F32 ? 16 : 8;
+  for (const void* p : ptrs)
+    if (!aligned(p, al)) return false;
+  return true;
+}
+// Grid of for_rows: row groups on x, lane blocks of 256 V lanes on y.
+inline dim3 rows_grid(int64_t nrow, int64_t H, int V) {
+  const int64_t gy = (H + (int64_t)kThreads * V - 1) / ((int64_t)kThreads * V);
+  const int64_t gx = (nrow + kRowsWG - 1) / kRowsWG;
+  return dim3((unsigned)(gx < 1 ? 1 : gx), (unsigned)(gy < 1 ? 1 : gy));
+}
 
 // 4-lane vectors per lane for rows held in registers (0: rows do not qualify).
 inline int reg_nv(int dtype, int64_t H, int64_t sb, int64_t sl,
@@ -578,13 +627,20 @@ extern "C" int tssm_swiglu_fwd(int dtype, const void* gate, const void* up, void
   TSSM_CHECK(H >= 0 && grid_b >= 0 && grid_l >= 0 && grid_b <= nbatch && grid_l <= L,
              TSSM_ERR_SHAPE);
   TSSM_CHECK(stride_b >= 0 && stride_l >= 0, TSSM_ERR_STRIDE);
-  const int64_t n = grid_b * grid_l * H;
-  if (n == 0) return TSSM_OK;
-  const RowElems e{{grid_l, stride_b, stride_l}, H};
+  const int64_t nrow = grid_b * grid_l;
+  if (nrow == 0 || H == 0) return TSSM_OK;
+  const Rows rows{grid_l, stride_b, stride_l};
+  const int V = vec4_rows(dtype, H, stride_b, stride_l, {gate, up, out}) ? 4 : 1;
+  const dim3 grid = rows_grid(nrow, H, V);
   const hipStream_t s = as_stream(stream);
-  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((swiglu_fwd_kernel<T>), dim3(flat_grid(n)),
-                                          dim3(kThreads), 0, s, (const T*)gate, (const T*)up,
-                                          (T*)out, e, n));
+  TSSM_DISPATCH(dtype, {
+    if (V == 4)
+      hipLaunchKernelGGL((swiglu_fwd_kernel<T, 4>), grid, dim3(kThreads), 0, s, (const T*)gate,
+                         (const T*)up, (T*)out, rows, nrow, H);
+    else
+      hipLaunchKernelGGL((swiglu_fwd_kernel<T, 1>), grid, dim3(kThreads), 0, s, (const T*)gate,
+                         (const T*)up, (T*)out, rows, nrow, H);
+  });
   return launch_status();
 }
 
@@ -597,13 +653,20 @@ extern "C" int tssm_swiglu_bwd(int dtype, const void* dout, const void* gate, co
   TSSM_CHECK(H >= 0 && grid_b >= 0 && grid_l >= 0 && grid_b <= nbatch && grid_l <= L,
              TSSM_ERR_SHAPE);
   TSSM_CHECK(stride_b >= 0 && stride_l >= 0, TSSM_ERR_STRIDE);
-  const int64_t n = grid_b * grid_l * H;
-  if (n == 0) return TSSM_OK;
-  const RowElems e{{grid_l, stride_b, stride_l}, H};
+  const int64_t nrow = grid_b * grid_l;
+  if (nrow == 0 || H == 0) return TSSM_OK;
+  const Rows rows{grid_l, stride_b, stride_l};
+  const int V = vec4_rows(dtype, H, stride_b, stride_l, {dout, gate, up, dgate, dup}) ? 4 : 1;
+  const dim3 grid = rows_grid(nrow, H, V);
   const hipStream_t s = as_stream(stream);
-  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((swiglu_bwd_kernel<T>), dim3(flat_grid(n)),
-                                          dim3(kThreads), 0, s, (const T*)dout, (const T*)gate,
-                                          (const T*)up, (T*)dgate, (T*)dup, e, n));
+  TSSM_DISPATCH(dtype, {
+    if (V == 4)
+      hipLaunchKernelGGL((swiglu_bwd_kernel<T, 4>), grid, dim3(kThreads), 0, s, (const T*)dout,
+                         (const T*)gate, (const T*)up, (T*)dgate, (T*)dup, rows, nrow, H);
+    else
+      hipLaunchKernelGGL((swiglu_bwd_kernel<T, 1>), grid, dim3(kThreads), 0, s, (const T*)dout,
+                         (const T*)gate, (const T*)up, (T*)dgate, (T*)dup, rows, nrow, H);
+  });
   return launch_status();
 }
 
@@ -644,9 +707,14 @@ extern "C" int tssm_mean_pool_logit(int dtype, const void* h, const void* W, con
   const float denom = (float)(nt * H) + 1e-9f;
   const hipStream_t s = as_stream(stream);
   TSSM_DISPATCH(dtype, {
-    hipLaunchKernelGGL((pool_partial_kernel<T>), dim3((unsigned)grid_b, (unsigned)nblk),
-                       dim3(kThreads), 0, s, (const T*)h, (const T*)W, part, nt, H, stride_b,
-                       stride_t, nblk);
+    if (vec4_rows(dtype, H, stride_b, stride_t, {h, W}))
+      hipLaunchKernelGGL((pool_partial_kernel<T, 4>), dim3((unsigned)grid_b, (unsigned)nblk),
+                         dim3(kThreads), 0, s, (const T*)h, (const T*)W, part, nt, H, stride_b,
+                         stride_t, nblk);
+    else
+      hipLaunchKernelGGL((pool_partial_kernel<T, 1>), dim3((unsigned)grid_b, (unsigned)nblk),
+                         dim3(kThreads), 0, s, (const T*)h, (const T*)W, part, nt, H, stride_b,
+                         stride_t, nblk);
     hipLaunchKernelGGL((pool_final_kernel<T>), dim3((unsigned)((grid_b + 255) / 256)), dim3(256),
                        0, s, part, (const T*)bias, (T*)out, grid_b, nblk, denom);
   });
@@ -660,8 +728,15 @@ extern "C" int tssm_masked_fill_zero(int dtype, int mask_code, const void* x, co
   TSSM_CHECK(n >= 0 && H > 0, TSSM_ERR_SHAPE);
   if (n == 0) return TSSM_OK;
   const hipStream_t s = as_stream(stream);
-  TSSM_DISPATCH(dtype, hipLaunchKernelGGL((masked_fill_kernel<T>), dim3(flat_grid(n)),
-                                          dim3(kThreads), 0, s, (const T*)x, mask, mask_code,
-                                          (T*)out, n, H));
+  const int V = (n % 4 == 0 && vec4_rows(dtype, H, 0, 0, {x, out})) ? 4 : 1;
+  const dim3 grid = rows_grid((n + H - 1) / H, H, V);
+  TSSM_DISPATCH(dtype, {
+    if (V == 4)
+      hipLaunchKernelGGL((masked_fill_kernel<T, 4>), grid, dim3(kThreads), 0, s, (const T*)x,
+                         mask, mask_code, (T*)out, n, H);
+    else
+      hipLaunchKernelGGL((masked_fill_kernel<T, 1>), grid, dim3(kThreads), 0, s, (const T*)x,
+                         mask, mask_code, (T*)out, n, H);
+  });
   return launch_status();
 }
