@@ -216,20 +216,24 @@ __global__ __launch_bounds__(kThreads) void layernorm_bwd_reg_kernel(
   }
 }
 
-// dw[h] += sum_k part[k][h], db[h] += sum_k part[nblk + k][h]: workgroup = 64
-// lanes h x 16 waves, wave w sums k = w, w + 16, ... in order, then the 16 wave
-// sums are added in wave order (a fixed order: deterministic).
+// dw[h] += sum_k part[k][h], db[h] += sum_k part[nblk + k][h] in two fixed-
+// order levels (deterministic).  Level 1: workgroup (64 lanes h, split y) =
+// 16 waves over the partials of split y, wave w taking k = k0 + w, k0 + w + 16,
+// ...; the 16 wave sums are added in wave order into part2[y][h] (and
+// part2[kSplits + y][h] for db).  Level 2: the kSplits sums in split order.
 constexpr int kRedWaves = 16;
-template <typename T>
+constexpr int kSplits = 16;
 __global__ __launch_bounds__(64 * kRedWaves) void ln_param_reduce_kernel(
-    const float* __restrict__ part, T* __restrict__ dw, T* __restrict__ db, int64_t H,
-    int64_t nblk) {
+    const float* __restrict__ part, float* __restrict__ part2, int64_t H, int64_t nblk) {
   __shared__ float red[2][kRedWaves][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t h = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t per = (nblk + kSplits - 1) / kSplits;
+  const int64_t k0 = (int64_t)blockIdx.y * per;
+  const int64_t k1 = k0 + per < nblk ? k0 + per : nblk;
   float sw = 0.0f, sb = 0.0f;
   if (h < H) {
-    for (int64_t k = wave; k < nblk; k += kRedWaves) {
+    for (int64_t k = k0 + wave; k < k1; k += kRedWaves) {
       sw += part[k * H + h];
       sb += part[(nblk + k) * H + h];
     }
@@ -244,9 +248,25 @@ __global__ __launch_bounds__(64 * kRedWaves) void ln_param_reduce_kernel(
       tw += red[0][k][lane];
       tb += red[1][k][lane];
     }
-    stf(dw + h, ldf(dw + h) + tw);
-    stf(db + h, ldf(db + h) + tb);
+    part2[blockIdx.y * H + h] = tw;
+    part2[(kSplits + blockIdx.y) * H + h] = tb;
   }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ln_param_add_kernel(const float* __restrict__ part2,
+                                                                T* __restrict__ dw,
+                                                                T* __restrict__ db, int64_t H) {
+  const int64_t h = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (h >= H) return;
+  float tw = 0.0f, tb = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kSplits; ++k) {
+    tw += part2[k * H + h];
+    tb += part2[(kSplits + k) * H + h];
+  }
+  stf(dw + h, ldf(dw + h) + tw);
+  stf(db + h, ldf(db + h) + tb);
 }
 
 // dx of a row (fused_ssm_interp.py:148-166) and its (mu, inv) for the
@@ -424,14 +444,19 @@ __global__ __launch_bounds__(kThreads) void pool_partial_kernel(
   }
 }
 
+// One wave per batch: lane j sums partials j, j + 64, ... in order, then the
+// fixed-order wave reduction (deterministic).
 template <typename T>
-__global__ void pool_final_kernel(const float* __restrict__ part, const T* __restrict__ bias,
-                                  T* __restrict__ out, int64_t nb, int64_t nblk, float denom) {
-  const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= nb) return;
+__global__ __launch_bounds__(64) void pool_final_kernel(const float* __restrict__ part,
+                                                        const T* __restrict__ bias,
+                                                        T* __restrict__ out, int64_t nb,
+                                                        int64_t nblk, float denom) {
+  const int64_t b = blockIdx.x;
+  const int lane = threadIdx.x;
   float s = 0.0f;
-  for (int64_t k = 0; k < nblk; ++k) s += part[b * nblk + k];
-  stf(out + b, s / denom + ldf(bias));
+  for (int64_t k = lane; k < nblk; k += 64) s += part[b * nblk + k];
+  s = wave_sum(s);
+  if (lane == 0) stf(out + b, s / denom + ldf(bias));
 }
 
 // mask codes: 0 f32, 1 bf16, 2 f16 (the library's), 3 i32, 4 u8 / bool
@@ -556,7 +581,7 @@ extern "C" int64_t tssm_layernorm_bwd_workspace_bytes(int64_t grid_b, int64_t gr
   const int64_t nrow = grid_b * grid_l;
   const int64_t nblk = (nrow + kLnRowBlock - 1) / kLnRowBlock;
   const int64_t rows_path = 2 * nrow + 2 * nblk * H;            // stats + column partials
-  const int64_t reg_path = 2 * kLnBwdMaxWaves * H;               // per-wave partials
+  const int64_t reg_path = 2 * (kLnBwdMaxWaves + kSplits) * H;  // per-wave + split partials
   return (rows_path > reg_path ? rows_path : reg_path) * (int64_t)sizeof(float);
 }
 
@@ -587,7 +612,9 @@ extern "C" int tssm_layernorm_bwd(int dtype, const void* dout, const void* x, co
     if (g * (kThreads / 64) > kLnBwdMaxWaves) g = kLnBwdMaxWaves / (kThreads / 64);
     const int64_t nwaves = g * (kThreads / 64);
     float* wpart = reinterpret_cast<float*>(workspace);
-    const dim3 gred((unsigned)((H + 63) / 64));
+    float* part2 = wpart + 2 * nwaves * H;
+    const dim3 gred((unsigned)((H + 63) / 64), (unsigned)kSplits);
+    const dim3 gadd((unsigned)((H + kThreads - 1) / kThreads));
 #define TSSM_LNB_REG(NV)                                                                      \
   hipLaunchKernelGGL((layernorm_bwd_reg_kernel<T, NV>), dim3((unsigned)g), dim3(kThreads), 0, \
                      s, (const T*)dout, (const T*)x, (const T*)w, (T*)dx, wpart, rows, nrow, H,  \
@@ -599,8 +626,10 @@ extern "C" int tssm_layernorm_bwd(int dtype, const void* dout, const void* x, co
         case 4: TSSM_LNB_REG(4); break;
         default: TSSM_LNB_REG(8); break;
       }
-      hipLaunchKernelGGL((ln_param_reduce_kernel<T>), gred, dim3(64 * kRedWaves), 0, s, wpart,
-                         (T*)dw, (T*)db, H, nwaves);
+      hipLaunchKernelGGL(ln_param_reduce_kernel, gred, dim3(64 * kRedWaves), 0, s, wpart, part2,
+                         H, nwaves);
+      hipLaunchKernelGGL((ln_param_add_kernel<T>), gadd, dim3(kThreads), 0, s, part2, (T*)dw,
+                         (T*)db, H);
     });
 #undef TSSM_LNB_REG
     return launch_status();
@@ -715,8 +744,8 @@ extern "C" int tssm_mean_pool_logit(int dtype, const void* h, const void* W, con
       hipLaunchKernelGGL((pool_partial_kernel<T, 1>), dim3((unsigned)grid_b, (unsigned)nblk),
                          dim3(kThreads), 0, s, (const T*)h, (const T*)W, part, nt, H, stride_b,
                          stride_t, nblk);
-    hipLaunchKernelGGL((pool_final_kernel<T>), dim3((unsigned)((grid_b + 255) / 256)), dim3(256),
-                       0, s, part, (const T*)bias, (T*)out, grid_b, nblk, denom);
+    hipLaunchKernelGGL((pool_final_kernel<T>), dim3((unsigned)grid_b), dim3(64), 0, s, part,
+                       (const T*)bias, (T*)out, grid_b, nblk, denom);
   });
   return launch_status();
 }
