@@ -296,10 +296,11 @@ def test_interp_ssm_step(dev):
 
 # ------------------------------------------------------------------ streaming
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_streaming_inplace(dev, dtype):
+@pytest.mark.parametrize("H", [300, 301])   # 4-lane and 1-lane accesses
+def test_streaming_inplace(dev, dtype, H):
     import streaming_inference_kernel as sk
     g = torch.Generator().manual_seed(6)
-    Bsz, H, BLOCK_H, steps = 5, 300, 128, 20
+    Bsz, BLOCK_H, steps = 5, 128, 20
     Ab = torch.rand(H, generator=g).to(dtype).to(dev)
     Bb = torch.randn(H, generator=g).to(dtype).to(dev)
     D = torch.randn(H, generator=g).to(dtype).to(dev)
@@ -321,10 +322,11 @@ def test_streaming_inplace(dev, dtype):
     assert_close(h, h_chain, TOL[dtype], "h (chained)")
 
 
-def test_streaming_ring_multi_tile(dev):
+@pytest.mark.parametrize("H,BLOCK_H", [(100, 32), (1000, 64)])   # tiles <= / > waves
+def test_streaming_ring_multi_tile(dev, H, BLOCK_H):
     import streaming_inference_kernel as sk
     g = torch.Generator().manual_seed(7)
-    Bsz, H, BLOCK_H, KR, steps = 3, 100, 32, 5, 12
+    Bsz, KR, steps = 3, 5, 12
     ring_V = torch.zeros(Bsz, KR, H, device=dev)
     ring_M = torch.zeros_like(ring_V)
     ring_tau = torch.zeros(Bsz, KR, device=dev)

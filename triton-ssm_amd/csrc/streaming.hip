@@ -12,20 +12,36 @@
 
 namespace tssm {
 
-template <typename T>
-__global__ void stream_step_kernel(const T* __restrict__ vhat, T* __restrict__ h,
-                                   const T* __restrict__ Abar, const T* __restrict__ Bbar,
-                                   const T* __restrict__ C, const T* __restrict__ D,
-                                   T* __restrict__ y, int64_t hc, int64_t total, int64_t svb,
-                                   int64_t shb, int64_t scb) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int64_t b = i / hc;
-  const int64_t k = i - b * hc;
-  const float v = ldf(vhat + b * svb + k);
-  const float hn = ldf(Abar + k) * ldf(h + b * shb + k) + ldf(Bbar + k) * v;
-  stf(h + b * shb + k, hn);
-  stf(y + b * svb + k, ldf(C + b * scb + k) * hn + ldf(D + k) * v);
+// Workgroup = 256 threads x V lanes (grid y) of kStepRows streams (grid x):
+// no per-element division, 16-byte (fp32) / 8-byte (16-bit) accesses when
+// aligned (V = 4).
+constexpr int kStepRows = 4;
+template <typename T, int V>
+__global__ __launch_bounds__(256) void stream_step_kernel(
+    const T* __restrict__ vhat, T* __restrict__ h, const T* __restrict__ Abar,
+    const T* __restrict__ Bbar, const T* __restrict__ C, const T* __restrict__ D,
+    T* __restrict__ y, int64_t hc, int64_t nb, int64_t svb, int64_t shb, int64_t scb) {
+  const int64_t k = ((int64_t)blockIdx.y * 256 + threadIdx.x) * V;
+  if (k >= hc) return;
+  float ab[V], bb[V], dv[V];
+  ld_lanes<T, V>(Abar + k, ab);
+  ld_lanes<T, V>(Bbar + k, bb);
+  ld_lanes<T, V>(D + k, dv);
+  const int64_t b0 = (int64_t)blockIdx.x * kStepRows;
+  for (int r = 0; r < kStepRows && b0 + r < nb; ++r) {
+    const int64_t b = b0 + r;
+    float v[V], hv[V], cv[V], yv[V];
+    ld_lanes<T, V>(vhat + b * svb + k, v);
+    ld_lanes<T, V>(h + b * shb + k, hv);
+    ld_lanes<T, V>(C + b * scb + k, cv);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      hv[j] = ab[j] * hv[j] + bb[j] * v[j];
+      yv[j] = cv[j] * hv[j] + dv[j] * v[j];
+    }
+    st_lanes<T, V>(h + b * shb + k, hv);
+    st_lanes<T, V>(y + b * svb + k, yv);
+  }
 }
 
 constexpr int kStreamThreads = 256;
@@ -47,20 +63,20 @@ struct RingArgs {
   int64_t H, srb, srk, svb, shb, scb, BLOCK_H, KRING;
 };
 
-__device__ inline float block_reduce_sum(float v, float* red) {
+__device__ inline float wave_sum(float v) {
+#pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float s = 0.0f;
-  for (int i = 0; i < kStreamThreads / 64; ++i) s += red[i];
-  return s;
+  return v;
 }
 
+// One workgroup per stream; feature tiles are spread over its waves, each tile
+// searched and updated by one wave with wave-level sums.  The search never
+// reads the slot being written (it starts one slot behind it), so the insert
+// needs no barrier; one barrier before the head advances.
 __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_kernel(RingArgs a) {
-  __shared__ float red[kStreamThreads / 64];
   const int64_t b = blockIdx.x;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  constexpr int nwaves = kStreamThreads / 64;
   const int64_t KR = a.KRING;
   const int64_t head = a.ring_head[b];
   const int64_t nh = (head + 1) % KR;                                    // :107
@@ -71,9 +87,8 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_kernel(Ring
     rV[nh * a.srk + k] = a.v_new[b * a.svb + k];
     rM[nh * a.srk + k] = a.m_new[b * a.svb + k];
   }
-  __syncthreads();
   const int64_t ntile = (a.H + a.BLOCK_H - 1) / a.BLOCK_H;
-  for (int64_t tile = 0; tile < ntile; ++tile) {
+  for (int64_t tile = wave; tile < ntile; tile += nwaves) {
     const int64_t f0 = tile * a.BLOCK_H;
     const int64_t f1 = f0 + a.BLOCK_H < a.H ? f0 + a.BLOCK_H : a.H;
     // backward search over the previous KRING-1 slots (:124-130): nearest slot
@@ -82,24 +97,23 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_kernel(Ring
     for (int64_t k = 1; k < KR; ++k) {
       const int64_t rk = (nh - k + KR) % KR;
       float s = 0.0f;
-      for (int64_t f = f0 + tid; f < f1; f += kStreamThreads) s += rM[rk * a.srk + f];
-      s = block_reduce_sum(s, red);
-      if (s > 0.5f) {
+      for (int64_t f = f0 + lane; f < f1; f += 64) s += rM[rk * a.srk + f];
+      if (wave_sum(s) > 0.5f) {  // uniform over the wave
         prev_k = rk;
         break;
       }
     }
     float sm = 0.0f;
-    for (int64_t f = f0 + tid; f < f1; f += kStreamThreads) sm += a.m_new[b * a.svb + f];
-    sm = block_reduce_sum(sm, red);
-    const bool fill = prev_k >= 0 && sm < 0.5f;                          // :133,143
-    for (int64_t f = f0 + tid; f < f1; f += kStreamThreads) {
+    for (int64_t f = f0 + lane; f < f1; f += 64) sm += a.m_new[b * a.svb + f];
+    const bool fill = prev_k >= 0 && wave_sum(sm) < 0.5f;                // :133,143
+    for (int64_t f = f0 + lane; f < f1; f += 64) {
       const float v = fill ? rV[prev_k * a.srk + f] : a.v_new[b * a.svb + f];
       const float hn = a.Abar[f] * a.h[b * a.shb + f] + a.Bbar[f] * v;  // :152
       a.h[b * a.shb + f] = hn;
       a.y[b * a.svb + f] = a.C[b * a.scb + f] * hn + a.D[f] * v;        // :153,156
     }
   }
+  __syncthreads();  // every wave has read the head before it advances
   if (tid == 0) {
     a.ring_tau[b * KR + nh] = a.tau_new[b];                              // :116
     a.ring_head[b] = (int32_t)nh;                                        // :117
@@ -118,14 +132,26 @@ extern "C" int tssm_stream_step(int dtype, const void* vhat, void* h, const void
   TSSM_CHECK(nbatch >= 0 && H >= 0 && grid_b >= 0 && h_cover >= 0 && grid_b <= nbatch &&
                  h_cover <= H,
              TSSM_ERR_SHAPE);
-  const int64_t total = grid_b * h_cover;
-  if (total == 0) return TSSM_OK;
-  const dim3 grid((unsigned)((total + 255) / 256));
+  if (grid_b == 0 || h_cover == 0) return TSSM_OK;
+  const uintptr_t al = dtype == TSSM_F32 ? 16 : 8;
+  const bool v4 = h_cover % 4 == 0 && svb % 4 == 0 && shb % 4 == 0 && scb % 4 == 0 &&
+                  aligned(vhat, al) && aligned(h, al) && aligned(Abar, al) && aligned(Bbar, al) &&
+                  aligned(C, al) && aligned(D, al) && aligned(y, al);
+  const int64_t V = v4 ? 4 : 1;
+  const int64_t gy = (h_cover + 256 * V - 1) / (256 * V);
+  const int64_t gx = (grid_b + kStepRows - 1) / kStepRows;
+  TSSM_CHECK(gy <= 65535 && gx <= 2147483647, TSSM_ERR_UNSUPPORTED);
+  const dim3 grid((unsigned)gx, (unsigned)gy);
   const hipStream_t s = as_stream(stream);
-#define TSSM_S(T)                                                                              \
-  hipLaunchKernelGGL(stream_step_kernel<T>, grid, dim3(256), 0, s, (const T*)vhat, (T*)h,      \
-                     (const T*)Abar, (const T*)Bbar, (const T*)C, (const T*)D, (T*)y, h_cover, \
-                     total, svb, shb, scb)
+#define TSSM_S(T)                                                                               \
+  if (v4)                                                                                       \
+    hipLaunchKernelGGL((stream_step_kernel<T, 4>), grid, dim3(256), 0, s, (const T*)vhat, (T*)h, \
+                       (const T*)Abar, (const T*)Bbar, (const T*)C, (const T*)D, (T*)y,          \
+                       h_cover, grid_b, svb, shb, scb);                                          \
+  else                                                                                          \
+    hipLaunchKernelGGL((stream_step_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)vhat, (T*)h, \
+                       (const T*)Abar, (const T*)Bbar, (const T*)C, (const T*)D, (T*)y,          \
+                       h_cover, grid_b, svb, shb, scb)
   switch (dtype) {
     case TSSM_F32: TSSM_S(float); break;
     case TSSM_BF16: TSSM_S(bf16_t); break;
