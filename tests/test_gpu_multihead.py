@@ -61,6 +61,36 @@ def test_fused_head_dims_and_chunks(dev, hd, chunk):
     assert_close(y, y_ref, TOL[torch.float32], f"hd={hd} chunk={chunk}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hd,nh", [(32, 8), (32, 6), (16, 8), (8, 16), (8, 12)])
+@pytest.mark.parametrize("per_head", [False, True])
+@pytest.mark.parametrize("bc", ["strided", "shared"])
+def test_fused_packed_heads(dev, dtype, hd, nh, per_head, bc):
+    """Heads narrower than 64 channels share a 128-lane tile row (128/hd heads)
+    when nh allows (else one per row): per-head decay, D, B/C head strides
+    (padded, or 0 = one B/C for all heads), h0 and the final state must land
+    on the right head."""
+    from tssm import multihead_ssm_forward
+    Bsz, L = 2, 611
+    d = _inputs(dev, Bsz, L, nh, hd, dtype, seed=40 + nh, per_head=per_head)
+    for k in ("B", "C"):
+        if bc == "strided":
+            wide = torch.zeros(Bsz, L, nh, 40, dtype=dtype, device=dev)
+            wide[..., :hd] = d[k]
+            d[k] = wide[..., :hd]                  # head stride 40 channels
+        else:
+            d[k] = d[k][:, :, :1].expand(Bsz, L, nh, hd)  # head stride 0
+    h0 = torch.randn(Bsz, nh, hd, device=dev)
+    y, hl = multihead_ssm_forward(d["u"], d["A_log"], d["B"], d["C"], d["dt"], d["D"],
+                                  disc="zoh", chunk=128, h0=h0, return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = _oracle(d, "zoh", h0=h0)
+    assert_close(y, y_ref, TOL[dtype], f"y packed hd={hd} nh={nh} {dtype}")
+    assert_close(hl, h_ref, TOL[dtype], f"h_last packed hd={hd} nh={nh} {dtype}")
+    yh = y.float().view(Bsz, L, nh, hd)
+    assert torch.equal(yh, yh[..., :1].expand_as(yh))
+
+
 def test_fused_split_resume_and_repeat(dev):
     """scan(x1 || x2) == scan(x2, h0 = h_last(x1)); repeated launches reuse the
     workspace (epoch advance) and give identical results."""

@@ -32,6 +32,7 @@ constexpr int kRowsW = 64 / kG;        // runs per wave
 constexpr int kRuns = kW * kRowsW;     // runs per tile (32)
 constexpr int kTC = kRuns * kR;        // steps per tile (128)
 constexpr int kLanes = kG * kV;        // lanes per tile (64)
+static_assert(kLanes == 64, "the look-back walks one whole wave per tile");
 constexpr int kSeg = 4;                // runs per run-scan segment
 constexpr int kSegs = kRuns / kSeg;    // 8: kSegs * kLanes == threads
 static_assert(kSegs * kLanes == kW * 64, "run scan covers the workgroup");
@@ -52,6 +53,7 @@ struct EwArgs {
   uint32_t nchunks;
   WsHeader* hdr;
   uint64_t* words;
+  uint64_t* status;  // TileStatus of every row: [rows][nchunks][2]
   uint32_t tag, spin_limit;
 };
 
@@ -108,17 +110,22 @@ __device__ inline void tile_scan(const EwArgs& a, const EwTile& t, float (*s_a)[
     const float TA = A * SA, TX = __builtin_fmaf(A, SX, X);
     // every lane publishes; lanes past H (their runs read lane 0) are never stored
     CarrySlot slot{a.words + (int64_t)t.row * a.nchunks * 3 * kLanes, 3 * kLanes, kLanes};
+    const TileStatus tst{a.status + (int64_t)t.row * a.nchunks * 2};
     if (t.c > 0) {
       st_word(slot.agg_a(t.c, ch), TA, a.tag);
       st_word(slot.agg_x(t.c, ch), TX, a.tag);
+      if (ch == 0) st_word(tst.agg(t.c), 0.0f, a.tag);
     }
     // a tile whose decay product is exactly zero forgets its entry state:
     // its inclusive state is published before the look-back
     const bool forgets = TA == 0.0f;
     if (forgets) st_word(slot.inc(t.c, ch), TX, a.tag);
-    const float carry =
-        t.c > 0 ? lookback_channel<1>(slot, t.c, ch, a.tag, 0.0f, a.spin_limit, a.hdr) : 0.0f;
+    // one whole wave (kLanes == 64) walks back by the status words
+    const float carry = t.c > 0 ? lookback_wave<16, 4>(slot, tst, t.c, ch, a.tag, 0.0f,
+                                                       a.spin_limit, a.hdr)
+                                : 0.0f;
     if (!forgets) st_word(slot.inc(t.c, ch), __builtin_fmaf(TA, carry, TX), a.tag);
+    if (ch == 0) st_word(tst.inc(t.c), 0.0f, a.tag);
     s_carry[ch] = carry;
   }
   __syncthreads();
@@ -308,6 +315,7 @@ int ew_setup(EwArgs& a, int64_t nbatch, int64_t L, int64_t H, void* workspace,
   a.nchunks = (uint32_t)nch;
   a.hdr = reinterpret_cast<WsHeader*>(workspace);
   a.words = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + sizeof(WsHeader));
+  a.status = a.words + ntiles * 3 * kLanes;
   a.tag = next_epoch(workspace);
   a.spin_limit = kDefaultSpinLimit;
   *grid = dim3((unsigned)ntiles);
@@ -321,8 +329,9 @@ using namespace tssm;
 
 extern "C" int64_t tssm_ssm_scan_fused_workspace_bytes(int64_t nbatch, int64_t L, int64_t H) {
   if (nbatch <= 0 || L <= 0 || H <= 0) return -1;
+  // header | carry words [tiles][3][kLanes] | status words [tiles][2]
   return (int64_t)sizeof(WsHeader) +
-         nbatch * cdiv(H, kLanes) * cdiv(L, kTC) * 3 * kLanes * (int64_t)sizeof(uint64_t);
+         nbatch * cdiv(H, kLanes) * cdiv(L, kTC) * (3 * kLanes + 2) * (int64_t)sizeof(uint64_t);
 }
 
 extern "C" int tssm_ssm_forward_fused(int dtype, const void* u, const void* A, const void* B,

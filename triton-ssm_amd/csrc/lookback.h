@@ -111,4 +111,107 @@ __device__ inline float lookback_channel(const CarrySlot& s, int64_t c, int ch, 
   return __builtin_fmaf(A_acc, h0, X_acc);
 }
 
+// Per-tile status of one row: a word pair per chunk {aggregate out, inclusive
+// out} carrying only the tag, stored by the lane of channel 0 after its own
+// carry words.  A status word says that the tile's carry words are (about to
+// be) visible; every carry word is still checked by its own tag.  Polling the
+// status instead of the carry words costs one 128-byte line per round trip
+// per tile instead of 3 words x channels: under a full HBM stream, polling
+// traffic competes with the data.
+struct TileStatus {
+  uint64_t* base;  // status of chunk 0 of this row
+  __device__ inline uint64_t* agg(int64_t c) const { return base + 2 * c; }
+  __device__ inline uint64_t* inc(int64_t c) const { return base + 2 * c + 1; }
+};
+
+// Bounded wait for one carry word whose status was already seen.
+__device__ inline uint64_t settle_word(const uint64_t* p, uint64_t w, uint32_t tag,
+                                       uint32_t& spins, uint32_t spin_limit, WsHeader* hdr) {
+  while (word_tag(w) != tag && spins <= spin_limit) {
+    if (++spins > spin_limit) {
+      flag_error(hdr);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    w = ld_word(p);
+  }
+  return w;
+}
+
+// Look-back of whole waves (all 64 lanes active, lane = channel ch): the walk
+// is decided per wave from the status of SW predecessors read at once (lane k
+// reads chunk j-k), then exactly the carry words it needs are loaded, FB
+// predecessors per round trip.  Resolves like lookback_channel: fold
+// aggregates newest first until an inclusive state (or the row start, h0).
+template <int SW, int FB>
+__device__ inline float lookback_wave(const CarrySlot& s, const TileStatus& st, int64_t c, int ch,
+                                      uint32_t tag, float h0, uint32_t spin_limit,
+                                      WsHeader* hdr) {
+  static_assert(SW >= 1 && SW <= 64 && FB >= 1, "status window within a wave");
+  const int lane = threadIdx.x & 63;
+  float A = 1.0f, X = 0.0f;
+  int64_t j = c - 1;  // newest predecessor not folded yet
+  uint32_t spins = 0;
+  while (true) {
+    // lanes k < SW: predecessor j-k; before chunk 0 stands the row's initial
+    // state, an inclusive value
+    bool inc_k = false, rdy_k = false;
+    if (lane < SW) {
+      if (j - lane < 0) {
+        inc_k = rdy_k = true;
+      } else {
+        const uint64_t wi = ld_word(st.inc(j - lane));
+        const uint64_t wa = ld_word(st.agg(j - lane));
+        inc_k = word_tag(wi) == tag;
+        rdy_k = inc_k || word_tag(wa) == tag;
+      }
+    }
+    const uint64_t m_inc = __ballot(inc_k);
+    const uint64_t m_rdy = __ballot(rdy_k);
+    const int k_inc = m_inc ? __builtin_ctzll(m_inc) : 64;   // nearest inclusive
+    const int k_gap = ~m_rdy ? __builtin_ctzll(~m_rdy) : 64;  // nearest with nothing out
+    const bool resolve = k_inc < k_gap;
+    const int n = resolve ? k_inc : k_gap;  // aggregates to fold this round
+    // inclusive word in flight together with the aggregates
+    const int64_t ji = j - k_inc;
+    uint64_t wi = 0;
+    if (resolve && ji >= 0) wi = ld_word(s.inc(ji, ch));
+    for (int k0 = 0; k0 < n; k0 += FB) {
+      uint64_t wa[FB], wx[FB];
+#pragma unroll
+      for (int k = 0; k < FB; ++k) {
+        if (k0 + k < n) {
+          wa[k] = ld_word(s.agg_a(j - k0 - k, ch));
+          wx[k] = ld_word(s.agg_x(j - k0 - k, ch));
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < FB; ++k) {
+        if (k0 + k < n) {
+          wa[k] = settle_word(s.agg_a(j - k0 - k, ch), wa[k], tag, spins, spin_limit, hdr);
+          wx[k] = settle_word(s.agg_x(j - k0 - k, ch), wx[k], tag, spins, spin_limit, hdr);
+          X = __builtin_fmaf(A, word_val(wx[k]), X);
+          A = A * word_val(wa[k]);
+        }
+      }
+    }
+    if (resolve) {
+      if (ji < 0) return __builtin_fmaf(A, h0, X);
+      wi = settle_word(s.inc(ji, ch), wi, tag, spins, spin_limit, hdr);
+      return __builtin_fmaf(A, word_val(wi), X);
+    }
+    j -= n;
+    // every channel's decay product is exactly zero: earlier tiles cannot matter
+    if (__ballot(A != 0.0f) == 0) return X;
+    if (n == 0) {
+      if (++spins > spin_limit) {  // predecessor never published: give up loudly
+        flag_error(hdr);
+        return X;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (spins > spin_limit) return X;
+  }
+}
+
 }  // namespace tssm

@@ -1,10 +1,13 @@
 // Multihead DIAG selective scan (multihead_ssm_kernel.py).
 //
 // mh_scan_fused_kernel -- single pass over HBM:
-//   tile = (batch b, head h, chunk c) of TC time steps x P channels, numbered
-//   row-major (blockIdx = (b*n_heads + h) * nchunks + c): the chunks of one
-//   row are neighbours in launch order, which measured ~20% faster on MI355X
-//   HBM than chunk-major numbering.
+//   tile = (batch b, row h, chunk c) of TC time steps x P channels, numbered
+//   row-major (blockIdx = (b*rows_per_batch + h) * nchunks + c): the chunks of
+//   one row are neighbours in launch order, which measured ~20% faster on
+//   MI355X HBM than chunk-major numbering.  A row is one head, or 2 (4) heads
+//   of 64 (32) channels when the head count allows: then a load instruction
+//   reads 256 contiguous bytes per bf16 step instead of 128, which copies at
+//   75% of HBM peak in this tile shape against 71-72% for one head.
 //   Thread layout: a wave covers ROWS = 64/G "runs" of R consecutive steps;
 //   each thread owns 8 consecutive channels (one 16-byte bf16 vector) of one
 //   run, so every load instruction reads ROWS whole 128-byte channel rows.
@@ -69,12 +72,13 @@ struct MhArgs {
   uint32_t n_heads, nchunks, nrows;
   uint32_t tag;
   uint32_t spin_limit;
-  uint32_t chunk_major;  // tile order: 0 row-major, 1 chunk-major
   uint32_t dt_is_tau;    // dt holds timestamps: dt_t = tau_t - tau_{t-1}, dt_0 = tau_0
 };
 
 // MODE_DIAG:   reference multihead layout -- u [B,L,nh*hd] per channel, y
-//              broadcast over the head's channels, D per channel.
+//              broadcast over the head's channels, D per channel.  A row holds
+//              G / NS consecutive heads of 8 NS channels (1 for head_dim >= 128;
+//              several when they fit, so a load covers more contiguous bytes).
 // MODE_MAMBA1: selective scan with lanes (channel d, state n): "head" = d,
 //              channels = states; x [B,L,Dc] broadcast over the states, B/C
 //              shared by all channels (head stride 0), y [B,L,Dc] one value per
@@ -88,8 +92,8 @@ constexpr int kMhWin = 1;  // predecessors read per look-back round trip (measur
 template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE, int NS, int R = kMhR,
           int WIN = kMhWin>
 __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
-  // NS = threads summed into one output value: the whole row for MODE_DIAG
-  // (NS == G), one channel's N/8 threads for MODE_MAMBA1.
+  // NS = threads summed into one output value: one head's head_dim/8 threads
+  // for MODE_DIAG, one channel's N/8 threads for MODE_MAMBA1.
   constexpr int P = G * 8;
   constexpr int ROWS = 64 / G;
   extern __shared__ float s_mem[];
@@ -110,17 +114,13 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   const int run = wave * ROWS + lane / G;
   const int ch0 = g * 8;
 
-  // ---- tile = blockIdx: row-major (row, chunk c) or chunk-major; either way
-  // (row, c) waits only on (row, c-1), a smaller index
+  // ---- tile = blockIdx, row-major (row, chunk c): (row, c) waits only on
+  // (row, c-1), a smaller index.  Numbering the chunks of all rows in groups
+  // (chunk-major, or groups of 4-16 chunks) measured 7-25% slower: the
+  // resident tiles then cover a scattered address range.
   const uint32_t tag = a.tag;
-  uint32_t row, c;
-  if (a.chunk_major) {
-    c = blockIdx.x / a.nrows;
-    row = blockIdx.x - c * a.nrows;
-  } else {
-    row = blockIdx.x / a.nchunks;
-    c = blockIdx.x - row * a.nchunks;
-  }
+  const uint32_t row = blockIdx.x / a.nchunks;
+  const uint32_t c = blockIdx.x - row * a.nchunks;
   const uint32_t b = row / a.n_heads;
   const uint32_t h = row - b * a.n_heads;
   // step t0 = tw + tr: tw uniform over the workgroup, tr a small per-lane
@@ -129,9 +129,10 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   const int64_t tw = (int64_t)c * TC;
   const uint32_t tr = (uint32_t)(run * R);
   const int64_t t0 = tw + tr;
-  // MODE_MAMBA1: a row packs P / (8 NS) channels of N = 8 NS states each
-  constexpr int CPR = (MODE == MODE_DIAG) ? 1 : P / (8 * NS);
-  const uint32_t cl = (MODE == MODE_DIAG) ? 0u : (uint32_t)(g / NS);  // channel within the row
+  // A row packs CPR = G / NS groups of NS threads: heads of 8 NS channels
+  // (MODE_DIAG) or channels of N = 8 NS states (MODE_MAMBA1).
+  constexpr int CPR = G / NS;
+  const uint32_t cl = CPR == 1 ? 0u : (uint32_t)(g / NS);  // head / channel within the row
   const int64_t chan = (int64_t)h * CPR + cl;
 
   // ---- per-channel parameters: raw values loaded first (small, cached), then
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   float a2[8];  // a * log2(e) per channel (or per head)
   float ia[(APH || DISC != TSSM_DISC_ZOH) ? 1 : 8];  // 1 / a per channel (ZOH)
   if constexpr (APH) {
-    a2[0] = a.A_log[h];
+    a2[0] = a.A_log[chan];
   } else {
     const float4* ap = reinterpret_cast<const float4*>(a.A_log + h * P + ch0);
     const float4 l0 = ap[0], l1 = ap[1];
@@ -161,12 +162,15 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   float us[R];  // MODE_MAMBA1: the channel's input, shared by its 8 state lanes
   float dtv[R];
   {
-    const int bc = (MODE == MODE_DIAG) ? ch0 : (g % NS) * 8;  // state offset within B/C rows
-    // bases at step 0 (uniform part + lane column)
+    const int bc = (g % NS) * 8;  // offset within the group's B/C row
+    // bases at step 0 (uniform part + lane column); B/C head stride is 0 in
+    // MODE_MAMBA1 (shared by all channels)
     const T* ub = reinterpret_cast<const T*>(a.u) + b * a.su_b +
                   (MODE == MODE_DIAG ? (int64_t)h * P + ch0 : (int64_t)h * CPR + cl);
-    const T* Bb = reinterpret_cast<const T*>(a.B) + b * a.sB_b + h * a.sB_h + bc;
-    const T* Cb = reinterpret_cast<const T*>(a.C) + b * a.sC_b + h * a.sC_h + bc;
+    const T* Bb = reinterpret_cast<const T*>(a.B) + b * a.sB_b + (int64_t)h * CPR * a.sB_h +
+                  lane_mul(cl, a.sB_h) + bc;
+    const T* Cb = reinterpret_cast<const T*>(a.C) + b * a.sC_b + (int64_t)h * CPR * a.sC_h +
+                  lane_mul(cl, a.sC_h) + bc;
     const float* db = a.dt + b * a.sdt_b + (int64_t)h * CPR * a.sdt_h + lane_mul(cl, a.sdt_h);
     const T* up = ub + tw * a.su_l + lane_mul(tr, a.su_l);
     const T* Bp = Bb + tw * a.sB_l + lane_mul(tr, a.sB_l);
@@ -319,6 +323,8 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       const bool forgets = TA == 0.0f;
       if (forgets) st_word(slot.inc(c, ch), TX, tag);
       const float hin = a.h0 ? a.h0[row * P + ch] : 0.0f;
+      // per-channel walk: measured faster here than the status-word walk
+      // (lookback_wave), which costs a second round trip per step
       const float carry =
           (c > 0) ? lookback_channel<WIN>(slot, c, ch, tag, hin, a.spin_limit, a.hdr) : hin;
       const float incl = __builtin_fmaf(TA, carry, TX);
@@ -481,7 +487,8 @@ __global__ void mh_output_kernel(const float* __restrict__ loc_a, const float* _
 namespace {
 
 struct TileCfg {
-  int G, W, TC;
+  int G, NS, W, TC;
+  int64_t hpr;  // heads per row (MODE_DIAG)
 };
 
 inline bool mh_tile_cfg(int64_t head_dim, int64_t chunk, TileCfg* cfg) {
@@ -493,22 +500,48 @@ inline bool mh_tile_cfg(int64_t head_dim, int64_t chunk, TileCfg* cfg) {
   if (W < 1) W = 1;
   if (W > 8) W = 8;
   cfg->G = G;
+  cfg->NS = G;
   cfg->W = W;
   cfg->TC = W * rows * kMhR;
+  cfg->hpr = 1;
   return true;
 }
 
-template <typename T, int DISC, bool APH, bool HAS_D, int MODE>
-int launch_mh_fused_g(int G, dim3 grid, dim3 block, size_t lds, hipStream_t s, const MhArgs& a) {
-  switch (G) {
-    case 1: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 1, MODE, 1>), grid, block, lds, s, a); break;
-    case 2: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 2, MODE, 2>), grid, block, lds, s, a); break;
-    case 4: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 4, MODE, 4>), grid, block, lds, s, a); break;
-    case 8: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 8, MODE, 8>), grid, block, lds, s, a); break;
-    case 16: hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, 16, MODE, 16>), grid, block, lds, s, a); break;
-    default: return TSSM_ERR_UNSUPPORTED;
+// MODE_DIAG rows: heads narrower than 64 channels (64-, 32- or 16-byte bf16
+// rows, 8-32 rows per wave instruction) are packed 128 / head_dim to a
+// 128-lane row when n_heads allows, with tiles of the same chunk of steps.
+// 64-channel heads stay one per row: packed in pairs they measured slower.
+inline bool mh_diag_cfg(int64_t head_dim, int64_t n_heads, int64_t chunk, TileCfg* cfg) {
+  if (!mh_tile_cfg(head_dim, chunk, cfg)) return false;
+  if (head_dim < 64) {
+    const int64_t hpr = 128 / head_dim;
+    TileCfg p;
+    if (n_heads % hpr == 0 && mh_tile_cfg(128, chunk, &p)) {
+      p.NS = (int)(head_dim / 8);
+      p.hpr = hpr;
+      *cfg = p;
+    }
   }
-  return launch_status();
+  return true;
+}
+
+inline int64_t mh_ws_bytes(int64_t nrows, int64_t L, int64_t P, int TC) {
+  return (int64_t)sizeof(WsHeader) + nrows * ((L + TC - 1) / TC) * 3 * P * 8;
+}
+
+template <typename T, int DISC, bool APH, bool HAS_D, int MODE>
+int launch_mh_fused_g(int G, int NS, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                      const MhArgs& a) {
+#define TSSM_MH(GV, NV)                                                                         \
+  if (G == GV && NS == NV) {                                                                   \
+    hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, APH, HAS_D, GV, MODE, NV>), grid, block, \
+                       lds, s, a);                                                             \
+    return launch_status();                                                                    \
+  }
+  TSSM_MH(1, 1) TSSM_MH(2, 2) TSSM_MH(4, 4) TSSM_MH(8, 8) TSSM_MH(16, 16)
+  TSSM_MH(16, 4) TSSM_MH(16, 2) TSSM_MH(16, 1)
+#undef TSSM_MH
+  return TSSM_ERR_UNSUPPORTED;
 }
 
 // MODE_MAMBA1 rows of P = 8 G lanes holding channels of N = 8 NS states.
@@ -527,21 +560,21 @@ int launch_sel_gn(int G, int NS, dim3 grid, dim3 block, size_t lds, hipStream_t 
 }
 
 template <typename T, int DISC>
-int launch_mh_fused_d(bool aph, bool has_d, int G, dim3 grid, dim3 block, size_t lds,
+int launch_mh_fused_d(bool aph, bool has_d, int G, int NS, dim3 grid, dim3 block, size_t lds,
                       hipStream_t s, const MhArgs& a) {
   if (aph)
-    return has_d ? launch_mh_fused_g<T, DISC, true, true, MODE_DIAG>(G, grid, block, lds, s, a)
-                 : launch_mh_fused_g<T, DISC, true, false, MODE_DIAG>(G, grid, block, lds, s, a);
-  return has_d ? launch_mh_fused_g<T, DISC, false, true, MODE_DIAG>(G, grid, block, lds, s, a)
-               : launch_mh_fused_g<T, DISC, false, false, MODE_DIAG>(G, grid, block, lds, s, a);
+    return has_d ? launch_mh_fused_g<T, DISC, true, true, MODE_DIAG>(G, NS, grid, block, lds, s, a)
+                 : launch_mh_fused_g<T, DISC, true, false, MODE_DIAG>(G, NS, grid, block, lds, s, a);
+  return has_d ? launch_mh_fused_g<T, DISC, false, true, MODE_DIAG>(G, NS, grid, block, lds, s, a)
+               : launch_mh_fused_g<T, DISC, false, false, MODE_DIAG>(G, NS, grid, block, lds, s, a);
 }
 
 template <typename T>
-int launch_mh_fused_t(int disc, bool aph, bool has_d, int G, dim3 grid, dim3 block, size_t lds,
-                      hipStream_t s, const MhArgs& a) {
+int launch_mh_fused_t(int disc, bool aph, bool has_d, int G, int NS, dim3 grid, dim3 block,
+                      size_t lds, hipStream_t s, const MhArgs& a) {
   if (disc == TSSM_DISC_ZOH)
-    return launch_mh_fused_d<T, TSSM_DISC_ZOH>(aph, has_d, G, grid, block, lds, s, a);
-  return launch_mh_fused_d<T, TSSM_DISC_EULER>(aph, has_d, G, grid, block, lds, s, a);
+    return launch_mh_fused_d<T, TSSM_DISC_ZOH>(aph, has_d, G, NS, grid, block, lds, s, a);
+  return launch_mh_fused_d<T, TSSM_DISC_EULER>(aph, has_d, G, NS, grid, block, lds, s, a);
 }
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -554,9 +587,9 @@ using namespace tssm;
 extern "C" int64_t tssm_mh_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t n_heads,
                                                 int64_t head_dim, int64_t chunk) {
   TileCfg cfg;
-  if (nbatch <= 0 || L <= 0 || n_heads <= 0 || !mh_tile_cfg(head_dim, chunk, &cfg)) return -1;
-  const int64_t nchunks = cdiv(L, cfg.TC);
-  return (int64_t)sizeof(WsHeader) + nbatch * n_heads * nchunks * 3 * head_dim * 8;
+  if (nbatch <= 0 || L <= 0 || n_heads <= 0 || !mh_diag_cfg(head_dim, n_heads, chunk, &cfg))
+    return -1;
+  return mh_ws_bytes(nbatch * n_heads / cfg.hpr, L, head_dim * cfg.hpr, cfg.TC);
 }
 
 extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log,
@@ -573,7 +606,7 @@ extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const floa
   TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
   TSSM_CHECK(nbatch > 0 && L > 0 && n_heads > 0, TSSM_ERR_SHAPE);
   TileCfg cfg;
-  TSSM_CHECK(mh_tile_cfg(head_dim, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(mh_diag_cfg(head_dim, n_heads, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
   const int64_t need = tssm_mh_scan_workspace_bytes(nbatch, L, n_heads, head_dim, chunk);
   TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
   TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);
@@ -587,7 +620,8 @@ extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const floa
   TSSM_CHECK(sdt_b >= 0 && sdt_l >= 0 && sdt_h >= 0, TSSM_ERR_STRIDE);
 
   const int64_t nchunks = cdiv(L, cfg.TC);
-  const int64_t nrows = nbatch * n_heads;
+  const int64_t nrows = nbatch * (n_heads / cfg.hpr);
+  const int64_t P = head_dim * cfg.hpr;  // lanes per row
   TSSM_CHECK(nchunks * nrows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
   MhArgs a;
   a.u = u; a.A_log = A_log; a.B = B; a.C = C; a.dt = dt; a.D = D; a.h0 = h0; a.y = y;
@@ -598,24 +632,23 @@ extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const floa
   a.sdt_b = sdt_b; a.sdt_l = sdt_l; a.sdt_h = sdt_h; a.sy_b = sy_b; a.sy_l = sy_l;
   a.hdr = reinterpret_cast<WsHeader*>(workspace);
   a.words = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + sizeof(WsHeader));
-  a.n_heads = (uint32_t)n_heads;
+  a.n_heads = (uint32_t)(n_heads / cfg.hpr);  // rows per batch
   a.nchunks = (uint32_t)nchunks;
   a.nrows = (uint32_t)nrows;
   a.tag = next_epoch(workspace);
   a.spin_limit = kDefaultSpinLimit;
-  a.chunk_major = 0;
   a.dt_is_tau = 0;
-
 
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
   const int nrun = cfg.W * (64 / cfg.G);
-  const size_t lds = ((size_t)2 * nrun * head_dim + 2 * (nrun / 8) * head_dim + head_dim) * sizeof(float);
+  const size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + P) * sizeof(float);
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr;
+  const bool aph = a_per_head != 0;
   switch (dtype) {
-    case TSSM_BF16: return launch_mh_fused_t<bf16_t>(disc, a_per_head != 0, has_d, cfg.G, grid, block, lds, s, a);
-    case TSSM_F16: return launch_mh_fused_t<f16_t>(disc, a_per_head != 0, has_d, cfg.G, grid, block, lds, s, a);
-    default: return launch_mh_fused_t<float>(disc, a_per_head != 0, has_d, cfg.G, grid, block, lds, s, a);
+    case TSSM_BF16: return launch_mh_fused_t<bf16_t>(disc, aph, has_d, cfg.G, cfg.NS, grid, block, lds, s, a);
+    case TSSM_F16: return launch_mh_fused_t<f16_t>(disc, aph, has_d, cfg.G, cfg.NS, grid, block, lds, s, a);
+    default: return launch_mh_fused_t<float>(disc, aph, has_d, cfg.G, cfg.NS, grid, block, lds, s, a);
   }
 }
 
@@ -710,7 +743,9 @@ extern "C" int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L
                                                        int64_t N, int64_t chunk) {
   if (Dc <= 0 || N <= 0 || N % 8 != 0) return -1;
   const int64_t cpr = sel_channels_per_row(Dc, N);
-  return tssm_mh_scan_workspace_bytes(nbatch, L, Dc / cpr, cpr * N, chunk);
+  TileCfg cfg;
+  if (nbatch <= 0 || L <= 0 || !mh_tile_cfg(cpr * N, chunk, &cfg)) return -1;
+  return mh_ws_bytes(nbatch * (Dc / cpr), L, cpr * N, cfg.TC);
 }
 
 extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt,
@@ -759,7 +794,6 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
   a.nrows = (uint32_t)nrows;
   a.tag = next_epoch(workspace);
   a.spin_limit = kDefaultSpinLimit;
-  a.chunk_major = 0;
   a.dt_is_tau = dt_is_tau ? 1u : 0u;
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
   const int nrun = cfg.W * (64 / cfg.G);
