@@ -96,7 +96,11 @@ def test_zoh_discretize_bwd(dev, dtype, shape):
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(2, 33, 300, 16, 64, 8), (3, 20, 64, 5, 32, 4),
-                                   (1, 7, 1000, 48, 256, 16), (2, 9, 301, 7, 128, 4)])
+                                   (1, 7, 1000, 48, 256, 16), (2, 9, 301, 7, 128, 4),
+                                   # matrix-core path: rank 4..20 with partial rank
+                                   # blocks, ragged T and H tiles
+                                   (2, 200, 256, 12, 256, 16), (2, 70, 100, 4, 128, 4),
+                                   (3, 130, 68, 20, 64, 32), (16, 2048, 256, 16, 256, 16)])
 def test_dt_project_softplus(dev, out_dtype, shape):
     """dt_project_softplus_kernel[grid](...) against the oracle (softplus+clamp
     pinned to torch in float64); the clamp bounds are hit on purpose."""
@@ -118,6 +122,26 @@ def test_dt_project_softplus(dev, out_dtype, shape):
     if out_dtype == torch.float32:
         rel = np.abs(np64(out) - ref) / ref
         assert rel.max() < 1e-5
+
+
+def test_dt_project_partial_grid_matrix_cores(dev):
+    """4-aligned operands take the matrix-core kernel: a partial grid still
+    writes exactly rows (0, :3) and lanes :64."""
+    import discretize_kernel as dk
+    Bsz, T, H, R = 2, 100, 128, 16
+    g = torch.Generator().manual_seed(3)
+    raw = torch.randn(Bsz, T, R, generator=g).to(dev)
+    W = torch.randn(R, H, generator=g).to(dev)
+    bias = torch.randn(H, generator=g).to(dev)
+    out = torch.full((Bsz, T, H), -1.0, device=dev)
+    dk.dt_project_softplus_kernel[(1, 3, 1)](
+        raw, W, bias, out, Bsz, T, H, R, *raw.stride(), *W.stride(), *out.stride(),
+        DT_MIN=0.0, DT_MAX=100.0, BLOCK_H=64, BLOCK_R=16)
+    torch.cuda.synchronize()
+    ref = O.dt_project_softplus(raw[:1, :3], W[:, :64], bias[:64], 0.0, 100.0)
+    assert_close(out[:1, :3, :64], ref, 1e-5, "partial dt")
+    assert torch.all(out[0, :3, 64:] == -1.0) and torch.all(out[0, 3:] == -1.0)
+    assert torch.all(out[1] == -1.0)
 
 
 def test_dt_project_partial_grid(dev):

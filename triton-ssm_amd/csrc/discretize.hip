@@ -360,48 +360,73 @@ extern "C" int tssm_zoh_discretize_bwd(int dtype, const float* A_log, const void
 // the clamp makes the overflow case agree too.
 namespace tssm {
 
-constexpr int kDtRows = 4;
+constexpr int kDtRows = 8;
 constexpr int kDtRank = 8;
 
-// softplus(x) = max(x, 0) + log1p(exp(-|x|)) with hardware exp2/log2:
-// log1p(e) = log(u) e / (u - 1), u = 1 + e rounded, which cancels the
-// rounding of u (Goldberg's identity); e <= 1, so u - 1 is exact.
+// softplus(x) = max(x, 0) + log1p(exp(-|x|)) with hardware exp2/log2.  With
+// e = exp(-|x|) <= 1 and u = 1 + e rounded, c = (u - 1) - e is the rounding
+// error exactly (u - 1 and the difference are exact by Sterbenz), and
+// log1p(e) = log(u) - c / u + O(c^2).  1/u is replaced by 1 - e + e^2: its
+// error e^3 / (1 + e) multiplies c <= 2^-23, negligible at every e (for
+// e < 2^-24, u = 1, c = -e and the result is e (1 - e + e^2)).  11 operations,
+// two of them transcendental, and no division.
 __device__ inline float softplus_fast(float x) {
   const float e = exp2_fast(-__builtin_fabsf(x) * kLog2e);
   const float u = 1.0f + e;
-  const float lp = u == 1.0f ? e
-                             : __builtin_amdgcn_logf(u) * 0.6931471805599453f * e *
-                                   __builtin_amdgcn_rcpf(u - 1.0f);
+  const float c = (u - 1.0f) - e;
+  const float r = __builtin_fmaf(e, e - 1.0f, 1.0f);
+  const float lp = __builtin_fmaf(__builtin_amdgcn_logf(u), 0.6931471805599453f, -c * r);
   return fmaxf(x, 0.0f) + lp;
 }
 
-// Workgroup = 256 threads x V consecutive lanes h (V = 4: 16-byte W, bias and
-// output accesses) over kDtRows rows (b, t); dt_raw values are uniform over
-// the workgroup (scalar loads), W rows are read in groups of kDtRank.
-template <typename TO, int V>
+// clamp to [lo, hi] (lo <= hi) in one v_med3_f32
+__device__ inline float clamp_med3(float x, float lo, float hi) {
+  return __builtin_amdgcn_fmed3f(x, lo, hi);
+}
+
+// Workgroup = 256 threads in 256 / LPR row groups of LPR threads (whole
+// waves); a thread covers V consecutive lanes h (V = 4: 16-byte W, bias and
+// output accesses) of kDtRows rows (b, t).  dt_raw values are uniform over a
+// row group's waves (scalar loads); W rows are read in groups of kDtRank.
+// Several row groups per workgroup keep short rows (H / V <= 128) from
+// launching one-wave workgroups.
+template <typename TO, int V, int LPR>
 __global__ __launch_bounds__(256) void dt_project_kernel(
     const float* __restrict__ raw, const float* __restrict__ W, const float* __restrict__ bias,
     TO* __restrict__ out, int64_t grid_t, int64_t nrows, int64_t hc, int64_t rank,
     int64_t sr_b, int64_t sr_t, int64_t sw_r, int64_t so_b, int64_t so_t, float dt_min,
     float dt_max) {
-  const int64_t h = ((int64_t)blockIdx.y * blockDim.x + threadIdx.x) * V;
+  static_assert(LPR % 64 == 0 && 256 % LPR == 0, "row groups of whole waves");
+  constexpr int NRG = 256 / LPR;
+  const int rg = __builtin_amdgcn_readfirstlane((int)threadIdx.x / LPR);
+  const int64_t h = ((int64_t)blockIdx.y * LPR + (int)threadIdx.x % LPR) * V;
   const bool act = h < hc;
   const int64_t hs = act ? h : 0;  // inactive lanes read lane 0 (in bounds), store nothing
-  const int64_t r0 = (int64_t)blockIdx.x * kDtRows;
+  const int64_t r0 = ((int64_t)blockIdx.x * NRG + rg) * kDtRows;
+  if (r0 >= nrows) return;  // whole waves; no barrier in this kernel
   const int nr = (int)((nrows - r0) < kDtRows ? (nrows - r0) : kDtRows);
-  const int64_t b0 = r0 / grid_t, t0 = r0 - b0 * grid_t;
-  // row k = (b0, t0) advanced by k steps in t, wrapping into the next batches
-  auto row_off = [&](int k, int64_t sb, int64_t st) {
-    int64_t t = t0 + k, b = b0;
-    while (t >= grid_t) { t -= grid_t; ++b; }
-    return b * sb + t * st;
-  };
+  // offsets of rows r0 .. r0+kDtRows-1 = (b, t) walking t, wrapping into the
+  // next batch (uniform: scalar registers)
+  int64_t ro_in[kDtRows], ro_out[kDtRows];
+  {
+    int64_t bb = r0 / grid_t, tt = r0 - bb * grid_t;
+#pragma unroll
+    for (int k = 0; k < kDtRows; ++k) {
+      ro_in[k] = bb * sr_b + tt * sr_t;
+      ro_out[k] = bb * so_b + tt * so_t;
+      if (++tt == grid_t) {
+        tt = 0;
+        ++bb;
+      }
+    }
+  }
   float acc[kDtRows][V];
 #pragma unroll
   for (int k = 0; k < kDtRows; ++k)
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[k][v] = 0.0f;
   for (int64_t q0 = 0; q0 < rank; q0 += kDtRank) {
+    const bool full = q0 + kDtRank <= rank;  // uniform: unguarded raw loads
     float w[kDtRank][V];
 #pragma unroll
     for (int i = 0; i < kDtRank; ++i) {
@@ -415,18 +440,35 @@ __global__ __launch_bounds__(256) void dt_project_kernel(
         w[i][0] = ok ? *wp : 0.0f;
       }
     }
+    // every row's values of this rank group are loaded before any is used:
+    // unconditional loads (rows past the end repeat the last row, columns past
+    // rank repeat the last column and are zeroed), so they go out together
+    float rv[kDtRows][kDtRank];
+    if (full) {
 #pragma unroll
-    for (int k = 0; k < kDtRows; ++k) {
-      if (k < nr) {  // uniform
-        const float* rp = raw + row_off(k, sr_b, sr_t) + q0;
+      for (int k = 0; k < kDtRows; ++k) {
+        const float* rp = raw + ro_in[k < nr ? k : nr - 1] + q0;
+#pragma unroll
+        for (int i = 0; i < kDtRank; ++i) rv[k][i] = rp[i];
+      }
+    } else {
+      const int64_t lim = rank - 1 - q0;  // last column of this group, >= 0
+#pragma unroll
+      for (int k = 0; k < kDtRows; ++k) {
+        const float* rp = raw + ro_in[k < nr ? k : nr - 1] + q0;
 #pragma unroll
         for (int i = 0; i < kDtRank; ++i) {
-          const float rv = q0 + i < rank ? rp[i] : 0.0f;
-#pragma unroll
-          for (int v = 0; v < V; ++v) acc[k][v] = __builtin_fmaf(rv, w[i][v], acc[k][v]);
+          const float x = rp[i < lim ? i : lim];
+          rv[k][i] = i <= lim ? x : 0.0f;
         }
       }
     }
+#pragma unroll
+    for (int k = 0; k < kDtRows; ++k)
+#pragma unroll
+      for (int i = 0; i < kDtRank; ++i)
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[k][v] = __builtin_fmaf(rv[k][i], w[i][v], acc[k][v]);
   }
   if (!act) return;
   float bv[V];
@@ -442,14 +484,105 @@ __global__ __launch_bounds__(256) void dt_project_kernel(
       float sp[V];
 #pragma unroll
       for (int v = 0; v < V; ++v)
-        sp[v] = fminf(fmaxf(softplus_fast(acc[k][v] + bv[v]), dt_min), dt_max);
-      TO* op = out + row_off(k, so_b, so_t) + h;
+        sp[v] = clamp_med3(softplus_fast(acc[k][v] + bv[v]), dt_min, dt_max);
+      TO* op = out + ro_out[k] + h;
       if constexpr (V == 4 && sizeof(TO) == 4) {
         *reinterpret_cast<float4*>(op) = make_float4(sp[0], sp[1], sp[2], sp[3]);
       } else {
 #pragma unroll
         for (int v = 0; v < V; ++v) stf(op + v, sp[v]);
       }
+    }
+  }
+}
+
+// Matrix-core form for 4-aligned operands: per 16 x 16 tile, out^T = W^T raw^T
+// on v_mfma_f32_16x16x4_f32 (fp32 products and sums, like the FMA form).  A
+// wave owns (batch b, 32 steps, 32 lanes h): 2 x 2 tiles, 4 MFMAs per tile
+// and 16 rank columns.  Lane l = (li = l % 16, lj = l / 16): operand A is
+// W^T[h0 + li][q], operand B raw^T[q][t0 + li], and at k-step s the MFMA
+// index k = lj stands for rank column q = 4 lj + s, so lane l's raw values for
+// one rank block are one 16-byte load.  The accumulator, seeded with the bias,
+// gives lane l out[t0 + li][h0 + 4 lj + v], v = 0..3: softplus and clamp on
+// the VALU and one 16-byte store.  Every load is clamped in bounds; tiles past grid_t
+// or h_cover are computed and not stored.
+constexpr int kDpTiles = 2;  // 16-row tiles and 16-lane tiles per wave (2 x 2 measured faster than 4 x 4)
+
+template <typename TO>
+__global__ __launch_bounds__(256) void dt_project_mfma_kernel(
+    const float* __restrict__ raw, const float* __restrict__ W, const float* __restrict__ bias,
+    TO* __restrict__ out, int64_t grid_b, int64_t grid_t, int64_t ntsb, int64_t hc,
+    int64_t rank, int64_t sr_b, int64_t sr_t, int64_t sw_r, int64_t so_b, int64_t so_t,
+    float dt_min, float dt_max) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wv = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (wv >= grid_b * ntsb) return;  // whole waves; no barrier in this kernel
+  const int64_t b = wv / ntsb;
+  const int64_t t0 = (wv - b * ntsb) * (16 * kDpTiles);
+  const int64_t h0 = (int64_t)blockIdx.y * (16 * kDpTiles);
+  const int li = lane & 15, lj = lane >> 4;
+  const float* rb = raw + b * sr_b;
+
+  // the accumulators start from the bias of the lane's 4 h (h_cover % 4 == 0:
+  // all 4 in range or none)
+  f32x4 acc[kDpTiles][kDpTiles];
+#pragma unroll
+  for (int ct = 0; ct < kDpTiles; ++ct) {
+    const int64_t h = h0 + 16 * ct + 4 * lj;
+    const float4 bq = *reinterpret_cast<const float4*>(bias + (h < hc ? h : 0));
+#pragma unroll
+    for (int rt = 0; rt < kDpTiles; ++rt) acc[rt][ct] = f32x4{bq.x, bq.y, bq.z, bq.w};
+  }
+
+  for (int64_t q0 = 0; q0 < rank; q0 += 16) {
+    // rank % 4 == 0: lane group lj's 4 columns are all in range or all out
+    const bool qok = q0 + 4 * lj < rank;
+    const int64_t qa = qok ? q0 + 4 * lj : 0;
+    float wa[kDpTiles][4];
+#pragma unroll
+    for (int ct = 0; ct < kDpTiles; ++ct) {
+      const int64_t h = h0 + 16 * ct + li;
+      const float* wp = W + (h < hc ? h : hc - 1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float v = wp[(qa + s) * sw_r];
+        wa[ct][s] = qok ? v : 0.0f;
+      }
+    }
+    f32x4 rv[kDpTiles];
+#pragma unroll
+    for (int rt = 0; rt < kDpTiles; ++rt) {
+      const int64_t t = t0 + 16 * rt + li;
+      const f32x4 v =
+          *reinterpret_cast<const f32x4*>(rb + (t < grid_t ? t : grid_t - 1) * sr_t + qa);
+      rv[rt] = qok ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int rt = 0; rt < kDpTiles; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < kDpTiles; ++ct)
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[ct][s], rv[rt][s], acc[rt][ct],
+                                                              0, 0, 0);
+  }
+
+  // row by row, so the 64-byte pieces of one output line leave in consecutive
+  // store instructions
+  TO* ob = out + b * so_b + h0 + 4 * lj;
+#pragma unroll
+  for (int rt = 0; rt < kDpTiles; ++rt) {
+    const int64_t t = t0 + 16 * rt + li;
+    if (t >= grid_t) continue;
+    TO* orow = ob + t * so_t;
+#pragma unroll
+    for (int ct = 0; ct < kDpTiles; ++ct) {
+      if (h0 + 16 * ct + 4 * lj >= hc) continue;
+      float sp[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sp[v] = clamp_med3(softplus_fast(acc[rt][ct][v]), dt_min, dt_max);
+      st_lanes<TO, 4>(orow + 16 * ct, sp);
     }
   }
 }
@@ -471,26 +604,52 @@ extern "C" int tssm_dt_project_softplus(int out_dtype, const float* dt_raw, cons
   const int64_t nrows = grid_b * grid_t;
   if (nrows == 0 || h_cover == 0) return TSSM_OK;
   const int64_t n_rg = cdiv64(nrows, kDtRows);
-  TSSM_CHECK(n_rg <= 2147483647, TSSM_ERR_UNSUPPORTED);
   // 4 lanes per thread when every W row, bias and output row is 16-byte aligned
   const bool v4 = h_cover % 4 == 0 && sw_r % 4 == 0 && so_b % 4 == 0 && so_t % 4 == 0 &&
                   aligned(W, 16) && aligned(bias, 16) &&
                   aligned(dt_out, out_dtype == TSSM_F32 ? 16 : 8);
+  // matrix cores when raw rows are 16-byte vectors of a rank that is a
+  // multiple of 4 (and the 4-lane output conditions above hold)
+  if (v4 && rank % 4 == 0 && rank > 0 && sr_b % 4 == 0 && sr_t % 4 == 0 && aligned(dt_raw, 16)) {
+    const int64_t ntsb = cdiv64(grid_t, 16 * kDpTiles);
+    const int64_t gx = cdiv64(grid_b * ntsb, 4), gy = cdiv64(h_cover, 16 * kDpTiles);
+    TSSM_CHECK(gx <= 2147483647 && gy <= 65535, TSSM_ERR_UNSUPPORTED);
+    const dim3 grid((unsigned)gx, (unsigned)gy);
+    const hipStream_t s = as_stream(stream);
+#define TSSM_DTM(TT)                                                                           \
+  hipLaunchKernelGGL(dt_project_mfma_kernel<TT>, grid, dim3(256), 0, s, dt_raw, W, bias,       \
+                     (TT*)dt_out, grid_b, grid_t, ntsb, h_cover, rank, sr_b, sr_t, sw_r, so_b, \
+                     so_t, dt_min, dt_max)
+    switch (out_dtype) {
+      case TSSM_F32: TSSM_DTM(float); break;
+      case TSSM_BF16: TSSM_DTM(bf16_t); break;
+      case TSSM_F16: TSSM_DTM(f16_t); break;
+      default: return TSSM_ERR_DTYPE;
+    }
+#undef TSSM_DTM
+    return launch_status();
+  }
   const int64_t nthr = v4 ? h_cover / 4 : h_cover;
-  const int threads = nthr >= 256 ? 256 : (int)(cdiv64(nthr, 64) * 64);
-  TSSM_CHECK(cdiv64(nthr, threads) <= 65535, TSSM_ERR_UNSUPPORTED);
-  const dim3 grid((unsigned)n_rg, (unsigned)cdiv64(nthr, threads));
+  const int lpr = nthr > 128 ? 256 : (nthr > 64 ? 128 : 64);  // threads per row group
+  const int64_t gx = cdiv64(n_rg, 256 / lpr);
+  TSSM_CHECK(gx <= 2147483647 && cdiv64(nthr, lpr) <= 65535, TSSM_ERR_UNSUPPORTED);
+  const dim3 grid((unsigned)gx, (unsigned)cdiv64(nthr, lpr));
   const hipStream_t s = as_stream(stream);
-#define TSSM_DTP(TT, VV)                                                                        \
-  hipLaunchKernelGGL((dt_project_kernel<TT, VV>), grid, dim3(threads), 0, s, dt_raw, W, bias,   \
-                     (TT*)dt_out, grid_t, nrows, h_cover, rank, sr_b, sr_t, sw_r, so_b, so_t,  \
+#define TSSM_DTP(TT, VV, LP)                                                                   \
+  hipLaunchKernelGGL((dt_project_kernel<TT, VV, LP>), grid, dim3(256), 0, s, dt_raw, W, bias,  \
+                     (TT*)dt_out, grid_t, nrows, h_cover, rank, sr_b, sr_t, sw_r, so_b, so_t, \
                      dt_min, dt_max)
+#define TSSM_DTP_L(TT, VV)                     \
+  if (lpr == 64) TSSM_DTP(TT, VV, 64);         \
+  else if (lpr == 128) TSSM_DTP(TT, VV, 128);  \
+  else TSSM_DTP(TT, VV, 256)
   switch (out_dtype) {
-    case TSSM_F32: if (v4) TSSM_DTP(float, 4); else TSSM_DTP(float, 1); break;
-    case TSSM_BF16: if (v4) TSSM_DTP(bf16_t, 4); else TSSM_DTP(bf16_t, 1); break;
-    case TSSM_F16: if (v4) TSSM_DTP(f16_t, 4); else TSSM_DTP(f16_t, 1); break;
+    case TSSM_F32: if (v4) { TSSM_DTP_L(float, 4); } else { TSSM_DTP_L(float, 1); } break;
+    case TSSM_BF16: if (v4) { TSSM_DTP_L(bf16_t, 4); } else { TSSM_DTP_L(bf16_t, 1); } break;
+    case TSSM_F16: if (v4) { TSSM_DTP_L(f16_t, 4); } else { TSSM_DTP_L(f16_t, 1); } break;
     default: return TSSM_ERR_DTYPE;
   }
+#undef TSSM_DTP_L
 #undef TSSM_DTP
   return launch_status();
 }
