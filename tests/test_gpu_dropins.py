@@ -296,10 +296,15 @@ def test_interp_full_size(dev):
     assert_close(out, O.time_aware_interp(V, M, tau, 10, 128), 1e-6, "interp full")
 
 
-def test_interp_ssm_step(dev):
+@pytest.mark.parametrize("Bsz,T,F,K,FT,p_obs,dtype,mdtype", [
+    (4, 40, 70, 4, 32, 0.05, torch.float32, torch.float32),
+    (3, 60, 300, 10, 128, 0.02, torch.bfloat16, torch.bfloat16),   # config-2 tile, K
+    (2, 90, 256, 64, 256, 0.01, torch.float32, torch.float16),     # K = 64: 129 rows x 256
+    (2, 50, 600, 20, 512, 0.03, torch.float32, torch.float32)])    # tiles over 256 features
+def test_interp_ssm_step(dev, Bsz, T, F, K, FT, p_obs, dtype, mdtype):
     import fused_ssm_interp as fs
-    Bsz, T, F, K, FT = 4, 40, 70, 4, 32
-    V, M, tau = _interp_inputs(Bsz, T, F, torch.float32, seed=4, p_obs=0.05, dev=dev)
+    V, M, tau = _interp_inputs(Bsz, T, F, dtype, seed=4 + K, p_obs=p_obs, dev=dev)
+    M = M.to(mdtype)
     g = torch.Generator().manual_seed(5)
     Ab = torch.rand(F, generator=g).to(dev)
     Bb = torch.randn(F, generator=g).to(dev)
@@ -315,7 +320,8 @@ def test_interp_ssm_step(dev):
         h_in, h_out = h_out, h_in
     torch.cuda.synchronize()
     assert_close(h_in, h_ref, 1e-5, "h after T steps")
-    assert_close(Vhat, O.time_aware_interp(V, M, tau, K, FT), 1e-6, "Vhat rows")
+    vtol = 1e-6 if dtype == torch.float32 else TOL[dtype]
+    assert_close(Vhat, O.time_aware_interp(V, M, tau, K, FT), vtol, "Vhat rows")
 
 
 # ------------------------------------------------------------------ streaming

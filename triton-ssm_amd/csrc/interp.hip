@@ -313,6 +313,105 @@ __global__ __launch_bounds__(kInterpThreads) void interp_step_kernel(StepArgs a)
   }
 }
 
+// Tiles of at most 256 features: one thread per feature, and every load that
+// does not depend on the neighbour search goes out in the first round trip --
+// the mask values of all 2K+1 candidate rows (spread flat over the
+// workgroup, kStepBatch per thread at a time), tau of every candidate row,
+// and h_in, A_bar, B_bar of the thread's feature.  Threads that see an
+// observed lane store 1 into the row's flag (the same value: no atomics);
+// every thread then searches the flags in LDS, and only the two V rows of
+// the chosen neighbours are loaded after that.  Same selection and weights
+// as interp_step_kernel (fused_ssm_interp.py:41-101).
+constexpr int kStepBatch = 16;
+
+template <typename TM>
+__device__ inline void step_mask_batch(const TM* M, int64_t row0, int64_t smt, int64_t f0,
+                                       int64_t t_lo, int64_t T, int nf, int total, int base,
+                                       int tid, float* mv, int* mi) {
+#pragma unroll
+  for (int j = 0; j < kStepBatch; ++j) {
+    const int idx = base + tid + j * kInterpThreads;
+    const int ix = idx < total ? idx : 0;
+    const int i = ix / nf, f = ix - i * nf;
+    int64_t t = t_lo + i;
+    t = t < 0 ? 0 : (t < T ? t : T - 1);  // rows outside [0, T) are never observed
+    mv[j] = ldf(M + row0 + t * smt + f0 + f);
+    mi[j] = idx < total && t_lo + i >= 0 && t_lo + i < T ? i : -1;
+  }
+}
+
+template <typename TV>
+__global__ __launch_bounds__(kInterpThreads) void interp_step_fast_kernel(StepArgs a) {
+  __shared__ unsigned char s_obs[2 * kMaxK + 1];
+  __shared__ float s_tau[2 * kMaxK + 1];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const int64_t f0 = (int64_t)blockIdx.x * a.FTILE;
+  const int nf = (int)((f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F) - f0);
+  const int K = (int)a.K, nrow = 2 * K + 1;
+  const int64_t t_lo = a.t_cur - K;
+  const int total = nrow * nf;
+  const int64_t mrow = b * a.smb;
+
+  float mv[kStepBatch];
+  int mi[kStepBatch];
+  switch (a.md) {  // uniform
+    case TSSM_BF16: step_mask_batch(reinterpret_cast<const bf16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, 0, tid, mv, mi); break;
+    case TSSM_F16: step_mask_batch(reinterpret_cast<const f16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, 0, tid, mv, mi); break;
+    default: step_mask_batch(reinterpret_cast<const float*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, 0, tid, mv, mi); break;
+  }
+  // feature side inputs
+  const bool fact = tid < nf;
+  const int64_t f = f0 + (fact ? tid : 0);
+  const int64_t lin = b * a.s_hib + f;  // h_in reads 0 where b*stride_hib + f >= B*F (:97-98)
+  const float hp = lin < a.nb * a.F ? a.h_in[lin] : 0.0f;
+  const float abar = a.A_bar[f], bbar = a.B_bar[f];
+  for (int i = tid; i < nrow; i += kInterpThreads) {
+    const int64_t t = t_lo + i;
+    s_obs[i] = 0;
+    s_tau[i] = (t >= 0 && t < a.T) ? ld_any(a.tau, b * a.stb + t * a.stt, a.td) : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kStepBatch; ++j)
+    if (mi[j] >= 0 && mv[j] > 0.5f) s_obs[mi[j]] = 1;
+  for (int base = kStepBatch * kInterpThreads; base < total; base += kStepBatch * kInterpThreads) {
+    switch (a.md) {
+      case TSSM_BF16: step_mask_batch(reinterpret_cast<const bf16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, base, tid, mv, mi); break;
+      case TSSM_F16: step_mask_batch(reinterpret_cast<const f16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, base, tid, mv, mi); break;
+      default: step_mask_batch(reinterpret_cast<const float*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, base, tid, mv, mi); break;
+    }
+#pragma unroll
+    for (int j = 0; j < kStepBatch; ++j)
+      if (mi[j] >= 0 && mv[j] > 0.5f) s_obs[mi[j]] = 1;
+  }
+  __syncthreads();
+  // nearest observed row within K on each side (the tile's "any observed")
+  int kp = 0, kn = 0;
+  for (int k = 1; k <= K; ++k)
+    if (kp == 0 && s_obs[K - k]) kp = k;
+  for (int k = 1; k <= K; ++k)
+    if (kn == 0 && s_obs[K + k]) kn = k;
+  if (!fact) return;  // after the last barrier
+  const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb + f;
+  float v;
+  if (kp > 0 && kn > 0) {
+    const float tp = s_tau[K - kp], tn = s_tau[K + kn], den = tn - tp;
+    float w = den > 1e-9f ? (s_tau[K] - tp) / den : 0.5f;
+    w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+    const float vp = ldf(V + (a.t_cur - kp) * a.svt), vn = ldf(V + (a.t_cur + kn) * a.svt);
+    v = (1.0f - w) * vp + w * vn;
+  } else if (kp > 0) {
+    v = ldf(V + (a.t_cur - kp) * a.svt);
+  } else if (kn > 0) {
+    v = ldf(V + (a.t_cur + kn) * a.svt);
+  } else {
+    v = ldf(V + a.t_cur * a.svt);
+  }
+  stf(reinterpret_cast<TV*>(a.Vhat) + b * a.sob + a.t_cur * a.sot + f, v);
+  a.h_out[b * a.s_hob + f] = abar * hp + bbar * v;
+}
+
 }  // namespace tssm
 
 using namespace tssm;
@@ -421,6 +520,14 @@ extern "C" int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, con
              svb, svt, smb, smt, stb, stt, sob, sot, s_hib, s_hob, t_cur, K, FTILE};
   const dim3 grid((unsigned)gf, (unsigned)grid_b);
   const hipStream_t s = as_stream(stream);
+  if (FTILE <= kInterpThreads) {  // one thread per feature: every load up front
+    switch (v_dtype) {
+      case TSSM_F32: hipLaunchKernelGGL(interp_step_fast_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
+      case TSSM_BF16: hipLaunchKernelGGL(interp_step_fast_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+      default: hipLaunchKernelGGL(interp_step_fast_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+    }
+    return launch_status();
+  }
   switch (v_dtype) {
     case TSSM_F32: hipLaunchKernelGGL(interp_step_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
     case TSSM_BF16: hipLaunchKernelGGL(interp_step_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
