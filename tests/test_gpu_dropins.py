@@ -224,6 +224,30 @@ def test_ssm_phase_intermediates(dev):
     assert_close(carry, O.ssm_carry_scan(c_r, Bsz * H, nblk), 1e-6, "scanned carry")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("nblk", [1, 2, 32, 64, 128, 256])
+def test_carry_scans(dev, dtype, nblk):
+    """ssm_carry_scan_kernel and ssm_bwd_carry_scan_kernel over 37 rows with a
+    grid of 30: scanned rows match the oracle, rows past the grid are untouched
+    (nblk > 64 chains 64-carry segments)."""
+    import ssm_scan as ss
+    rows, grid_rows = 37, 30
+    g = torch.Generator().manual_seed(nblk)
+    a = torch.empty(rows * nblk).uniform_(0.5, 1.0, generator=g)
+    x = torch.randn(rows * nblk, generator=g)
+    base = torch.cat([a, x]).to(dtype)
+    tol = 1e-5 if dtype == torch.float32 else TOL[dtype]
+    for kern, ref in ((ss.ssm_carry_scan_kernel, O.ssm_carry_scan),
+                      (ss.ssm_bwd_carry_scan_kernel, O.ssm_bwd_carry_scan)):
+        carry = base.clone().to(dev)
+        kern[(grid_rows,)](carry, rows, nblk)
+        torch.cuda.synchronize()
+        exp = ref(base, rows, nblk).reshape(2, rows, nblk)
+        got = carry.view(2, rows, nblk)
+        assert_close(got[:, :grid_rows], exp[:, :grid_rows], tol, f"{kern.fn_name} nblk={nblk}")
+        assert torch.equal(got[:, grid_rows:].cpu(), base.view(2, rows, nblk)[:, grid_rows:])
+
+
 def test_ssm_forward_bf16(dev):
     import ssm_scan as ss
     g = torch.Generator().manual_seed(2)

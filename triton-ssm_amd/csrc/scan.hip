@@ -53,37 +53,51 @@ __global__ void ssm_fwd_local_kernel(const T* __restrict__ u, const T* __restric
 
 // ssm_carry_scan_kernel (ssm_scan.py:54-65) and the reverse variant
 // ssm_bwd_carry_scan_kernel (:174-185): inclusive scan of NBLK carries per
-// row, sequential per thread in fp32, rounded to the carry dtype on store.
-template <typename T>
-__global__ void carry_scan_kernel(T* __restrict__ carry, int64_t nrows, int64_t nblk,
-                                  int reverse, int64_t grid_rows) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= grid_rows) return;
-  T* ca = carry + r * nblk;
-  T* cx = carry + nrows * nblk + r * nblk;
-  // kB carries per batch of loads, all issued before the batch is folded in;
-  // reverse order walks k = nblk-1 .. 0.  The first carry is kept as loaded.
-  constexpr int kB = 8;
-  float A = 1.0f, X = 0.0f;
-  for (int64_t k0 = 0; k0 < nblk; k0 += kB) {
-    float av[kB], xv[kB];
+// row in fp32, rounded to the carry dtype on store.  A wave holds 64 / S rows of S = min(64, pow2 >= nblk)
+// carries, lane = (row, carry k); one load round trip, then a segmented
+// inclusive scan across the row's lanes (Hillis-Steele, log2 S shuffles,
+// earlier carries on the left as in _combine), and one store.  Rows longer
+// than 64 carries go in 64-carry segments, each started from the previous
+// segment's last state.  reverse walks k = nblk-1 .. 0.  The first carry is
+// kept as loaded, as in the sequential form; sums are reassociated like the
+// reference's tree-shaped tl.associative_scan.
+template <typename T, int S>
+__global__ __launch_bounds__(256) void carry_scan_lanes_kernel(T* __restrict__ carry,
+                                                               int64_t nrows, int64_t nblk,
+                                                               int reverse, int64_t grid_rows) {
+  constexpr int RPW = 64 / S;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / S;
+  const int j = lane % S;
+  const bool row_ok = r < grid_rows;
+  T* ca = carry + (row_ok ? r : 0) * nblk;
+  T* cx = carry + nrows * nblk + (row_ok ? r : 0) * nblk;
+  float Ain = 1.0f, Xin = 0.0f;  // state entering the segment
+  for (int64_t i0 = 0; i0 < nblk; i0 += S) {
+    const int64_t i = i0 + j;
+    const bool ok = row_ok && i < nblk;
+    const int64_t k = reverse ? nblk - 1 - (ok ? i : 0) : (ok ? i : 0);
+    float A = ok ? ldf(ca + k) : 1.0f;
+    float X = ok ? ldf(cx + k) : 0.0f;
 #pragma unroll
-    for (int j = 0; j < kB; ++j) {
-      const int64_t i = k0 + j < nblk ? k0 + j : nblk - 1;
-      const int64_t k = reverse ? nblk - 1 - i : i;
-      av[j] = ldf(ca + k);
-      xv[j] = ldf(cx + k);
-    }
-#pragma unroll
-    for (int j = 0; j < kB; ++j) {
-      if (k0 + j >= nblk) break;
-      const int64_t k = reverse ? nblk - 1 - (k0 + j) : k0 + j;
-      X = __builtin_fmaf(av[j], X, xv[j]);
-      A = av[j] * A;
-      if (k0 + j > 0) {
-        stf(ca + k, A);
-        stf(cx + k, X);
+    for (int d = 1; d < S; d <<= 1) {
+      const float Al = __shfl_up(A, d, S), Xl = __shfl_up(X, d, S);
+      if (j >= d) {
+        X = __builtin_fmaf(A, Xl, X);
+        A = A * Al;
       }
+    }
+    if (i0 > 0) {  // fold in the previous segments
+      X = __builtin_fmaf(A, Xin, X);
+      A = A * Ain;
+    }
+    if (ok && i > 0) {
+      stf(ca + k, A);
+      stf(cx + k, X);
+    }
+    if (i0 + S < nblk) {  // S == 64 here: the segment's last lane carries on
+      Ain = __shfl(A, 63);
+      Xin = __shfl(X, 63);
     }
   }
 }
@@ -227,11 +241,29 @@ extern "C" int tssm_carry_scan(int dtype, void* carry, int64_t nrows, int64_t nb
   TSSM_CHECK(nrows > 0 && nblk > 0 && grid_rows >= 0 && grid_rows <= nrows, TSSM_ERR_SHAPE);
   if (grid_rows == 0) return TSSM_OK;
   const hipStream_t s = as_stream(stream);
-#define TSSM_C(T)                                                                              \
-  hipLaunchKernelGGL(carry_scan_kernel<T>, dim3(blocks_for(grid_rows, 64)), dim3(64), 0, s,    \
-                     (T*)carry, nrows, nblk, reverse, grid_rows)
+  // lanes over carries: rows of S lanes, 4 waves per workgroup
+  int S = 1;
+  while (S < 64 && S < nblk) S <<= 1;
+  const int64_t rows_per_wg = 4 * (64 / S);
+  const int64_t nwg = (grid_rows + rows_per_wg - 1) / rows_per_wg;
+  TSSM_CHECK(nwg <= 2147483647, TSSM_ERR_UNSUPPORTED);
+  const dim3 grid((unsigned)nwg);
+#define TSSM_CS(T, SV)                                                                         \
+  hipLaunchKernelGGL((carry_scan_lanes_kernel<T, SV>), grid, dim3(256), 0, s, (T*)carry,       \
+                     nrows, nblk, reverse, grid_rows)
+#define TSSM_C(T)                      \
+  switch (S) {                         \
+    case 1: TSSM_CS(T, 1); break;      \
+    case 2: TSSM_CS(T, 2); break;      \
+    case 4: TSSM_CS(T, 4); break;      \
+    case 8: TSSM_CS(T, 8); break;      \
+    case 16: TSSM_CS(T, 16); break;    \
+    case 32: TSSM_CS(T, 32); break;    \
+    default: TSSM_CS(T, 64); break;    \
+  }
   TSSM_DISPATCH_T(dtype, TSSM_C)
 #undef TSSM_C
+#undef TSSM_CS
   return launch_status();
 }
 
