@@ -153,25 +153,31 @@ def test_fused_full_headline_shape(dev, disc):
     assert workspace.error_flag(ws) == 0
 
 
-def test_phase_exact_dropins(dev):
+@pytest.mark.parametrize("hd,dtype,BLK,L", [(16, torch.float32, 16, 70),
+                                          (64, torch.float32, 128, 300),
+                                          (32, torch.bfloat16, 64, 200),
+                                          (128, torch.float32, 32, 90),
+                                          (24, torch.float32, 16, 50)])   # scalar output path
+def test_phase_exact_dropins(dev, hd, dtype, BLK, L):
     """multihead_ssm_fwd_local/carry_scan/output launched exactly as a caller of
-    the reference would, intermediates and y checked against the oracle."""
+    the reference would, intermediates and y checked against the oracle; a
+    partial output grid writes exactly its rows and blocks."""
     import multihead_ssm_kernel as mk
-    Bsz, L, nh, hd, BLK = 2, 70, 3, 16, 16
-    d = _inputs(dev, Bsz, L, nh, hd, torch.float32, seed=9)
+    Bsz, nh = 2, 3
+    d = _inputs(dev, Bsz, L, nh, hd, dtype, seed=9 + hd)
     u, A_log, B, C, dt, D = (d[k] for k in ("u", "A_log", "B", "C", "dt", "D"))
     H = nh * hd
     nblk = 1 << (((L + BLK - 1) // BLK) - 1).bit_length()
     loc_a = torch.empty(Bsz, L, nh, hd, device=dev)
     loc_x = torch.empty_like(loc_a)
     carry = torch.empty(2 * Bsz * nh * hd * nblk, device=dev)
-    y = torch.zeros(Bsz, L, H, device=dev)
+    y = torch.zeros(Bsz, L, H, device=dev, dtype=dtype)
     mk.multihead_ssm_fwd_local_kernel[(Bsz * nh, nblk)](
         u, A_log, B, C, dt, loc_a, loc_x, carry, Bsz, L, H, nh, hd,
         u.stride(0), u.stride(1), u.stride(2), A_log.stride(0), A_log.stride(1),
         B.stride(0), B.stride(1), B.stride(2), B.stride(3),
         C.stride(0), C.stride(1), C.stride(2), C.stride(3),
-        dt.stride(0), dt.stride(1), dt.stride(2), BLK_L=BLK, NBLK=nblk, HEAD_DIM=16)
+        dt.stride(0), dt.stride(1), dt.stride(2), BLK_L=BLK, NBLK=nblk, HEAD_DIM=hd)
     la_ref, lx_ref, c_ref = O.multihead_fwd_local(u, A_log, B, C, dt, nh, hd, BLK, nblk)
     torch.cuda.synchronize()
     assert_close(loc_a, la_ref, 1e-5, "loc_a")
@@ -184,10 +190,28 @@ def test_phase_exact_dropins(dev):
     mk.multihead_ssm_output_kernel[(Bsz * nh, nblk)](
         loc_a, loc_x, carry, C, D, u, y, Bsz, L, H, nh, hd,
         u.stride(0), u.stride(1), u.stride(2), C.stride(0), C.stride(1), C.stride(2),
-        C.stride(3), BLK_L=BLK, NBLK=nblk, HEAD_DIM=16, num_warps=4)
+        C.stride(3), BLK_L=BLK, NBLK=nblk, HEAD_DIM=hd, num_warps=4)
     torch.cuda.synchronize()
     y_ref, _ = O.multihead_forward(u, A_log, B, C, dt, D, disc="euler")
-    assert_close(y, y_ref, 1e-5, "y (phases)")
+    tol = 1e-5 if dtype == torch.float32 else TOL[dtype]
+    assert_close(y, y_ref, tol, "y (phases)")
+    # partial grid: rows (b, h) < Bsz*nh - 1, blocks < nblk - 1 (when there are 2)
+    gr, gb = Bsz * nh - 1, max(nblk - 1, 1)
+    y2 = torch.zeros_like(y)
+    mk.multihead_ssm_output_kernel[(gr, gb)](
+        loc_a, loc_x, carry, C, D, u, y2, Bsz, L, H, nh, hd,
+        u.stride(0), u.stride(1), u.stride(2), C.stride(0), C.stride(1), C.stride(2),
+        C.stride(3), BLK_L=BLK, NBLK=nblk, HEAD_DIM=hd, num_warps=4)
+    torch.cuda.synchronize()
+    t_end = min(gb * BLK, L)
+    yv, y2v = y.view(Bsz, L, nh, hd), y2.view(Bsz, L, nh, hd)
+    for r in range(Bsz * nh):
+        b_, h_ = divmod(r, nh)
+        if r < gr:
+            assert torch.equal(y2v[b_, :t_end, h_], yv[b_, :t_end, h_])
+            assert torch.all(y2v[b_, t_end:, h_] == 0)
+        else:
+            assert torch.all(y2v[b_, :, h_] == 0)
 
 
 def test_launcher_rejects_out_of_bounds(dev):

@@ -389,21 +389,39 @@ __global__ void mh_fwd_local_kernel(const T* __restrict__ u, const float* __rest
   const int64_t ts = blk * blk_l;
   const int64_t te = ts + blk_l > L ? L : ts + blk_l;
   const int64_t rows_tot = nbatch * nh * hd;
+  // kB steps' loads are issued before any is used (clamped to the block's
+  // last step, whose duplicates are never stored): one load round trip per
+  // kB steps instead of one per step.  exp(d a) as hardware exp2 of d a log2e.
+  constexpr int kB = 8;
   for (int64_t p = threadIdx.x; p < hd; p += blockDim.x) {
-    const float a = -expf(A_log[hi * sal_h + p]);
+    const float a2 = -expf(A_log[hi * sal_h + p]) * kLog2e;
     const int64_t uo = hi * hd + p;
     const bool u_ok = uo < H;
+    const float* dtp = dt + bi * sdt_b + hi * sdt_h;
+    const T* bp = Bm + bi * sB_b + hi * sB_h + p;
+    const T* up = u + bi * su_b + (u_ok ? uo : 0);
+    float* lap = loc_a + bi * (L * nh * hd) + hi * hd + p;
+    float* lxp = loc_x + bi * (L * nh * hd) + hi * hd + p;
     float ar = 1.0f, xr = 0.0f;
-    for (int64_t t = ts; t < te; ++t) {
-      const float d = dt[bi * sdt_b + t * sdt_l + hi * sdt_h];
-      const float ab = expf(d * a);
-      const float bv = ldf(Bm + bi * sB_b + t * sB_l + hi * sB_h + p);
-      const float uv = u_ok ? ldf(u + bi * su_b + t * su_l + uo) : 0.0f;
-      xr = ab * xr + d * bv * uv;
-      ar = ab * ar;
-      const int64_t off = bi * (L * nh * hd) + t * (nh * hd) + hi * hd + p;
-      loc_a[off] = ar;
-      loc_x[off] = xr;
+    for (int64_t t0 = ts; t0 < te; t0 += kB) {
+      float dv[kB], bv[kB], uv[kB];
+#pragma unroll
+      for (int k = 0; k < kB; ++k) {
+        const int64_t t = t0 + k < te ? t0 + k : te - 1;
+        dv[k] = dtp[t * sdt_l];
+        bv[k] = ldf(bp + t * sB_l);
+        uv[k] = ldf(up + t * su_l);
+      }
+#pragma unroll
+      for (int k = 0; k < kB; ++k) {
+        if (t0 + k >= te) break;  // uniform
+        const float ab = exp2_fast(dv[k] * a2);
+        xr = ab * xr + dv[k] * bv[k] * (u_ok ? uv[k] : 0.0f);
+        ar = ab * ar;
+        const int64_t off = (t0 + k) * (nh * hd);
+        lap[off] = ar;
+        lxp[off] = xr;
+      }
     }
     const int64_t rf = bi * (nh * hd) + hi * hd + p;
     carry[rf * nblk + blk] = ar;
@@ -480,6 +498,94 @@ __global__ void mh_output_kernel(const float* __restrict__ loc_a, const float* _
 #pragma unroll
     for (int k = 0; k < kU; ++k)
       if (u_ok && t + k < te) stf(y + bi * (L * H) + (t + k) * H + uo, c[k]);
+  }
+}
+
+// Vector form for 4-aligned operands (head_dim = 4 LPS, LPS in 4..32): a
+// thread owns 4 channels (16-byte fp32 / 8-byte 16-bit accesses), LPS lanes
+// cover one step, so one wave instruction covers 64 / LPS steps.  Per step:
+// the 4-channel partial sum, then an LPS-lane sum (DPP up to 16 lanes), the
+// head value stored broadcast over the thread's 4 channels.  kOutR steps per
+// thread are loaded before any is reduced.  Same grid and results as
+// mh_output_kernel (the sums reassociate).
+constexpr int kOutR = 4;
+
+template <int LPS>
+__device__ inline float lanes_sum(float v) {
+  if constexpr (LPS <= 16) {
+    return group_sum<LPS>(v);
+  } else {
+#pragma unroll
+    for (int o = LPS / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+  }
+}
+
+template <typename T, int LPS>
+__global__ __launch_bounds__(256) void mh_output_vec_kernel(
+    const float* __restrict__ loc_a, const float* __restrict__ loc_x,
+    const float* __restrict__ carry, const T* __restrict__ Cm, const float* __restrict__ D,
+    const T* __restrict__ u, T* __restrict__ y, int64_t nbatch, int64_t L, int64_t H, int64_t nh,
+    int64_t hd, int64_t su_b, int64_t su_l, int64_t sC_b, int64_t sC_l, int64_t sC_h,
+    int64_t blk_l, int64_t nblk) {
+  constexpr int SPW = 64 / LPS;  // steps per wave instruction
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane % LPS, sl = lane / LPS;
+  const int64_t rowi = blockIdx.y, blk = blockIdx.x;
+  const int64_t bi = rowi / nh, hi = rowi - bi * nh;
+  const int64_t ts = blk * blk_l;
+  const int64_t te = ts + blk_l > L ? L : ts + blk_l;
+  const int64_t p = 4 * q;
+  const int64_t uo = hi * hd + p;
+  const bool u_ok = uo < H;  // H % 4 == 0: all 4 channels or none
+  float xp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (blk > 0) {
+    const int64_t rows_tot = nbatch * nh * hd;
+    const int64_t rf = bi * (nh * hd) + hi * hd + p;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xp[j] = carry[rows_tot * nblk + (rf + j) * nblk + blk - 1];
+  }
+  float dv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (u_ok) ld_lanes<float, 4>(D + uo, dv);
+  const float* la = loc_a + bi * (L * nh * hd) + hi * hd + p;
+  const float* lx = loc_x + bi * (L * nh * hd) + hi * hd + p;
+  const T* cb = Cm + bi * sC_b + hi * sC_h + p;
+  const T* ub = u + bi * su_b + (u_ok ? uo : 0);
+  T* yb = y + bi * (L * H) + uo;
+  const int64_t row = nh * hd;  // loc_a / loc_x step stride
+  constexpr int PASS = 4 * SPW * kOutR;  // steps per workgroup pass (4 waves)
+  for (int64_t t0 = ts; t0 < te; t0 += PASS) {
+    float a4[kOutR][4], x4[kOutR][4], c4[kOutR][4], u4[kOutR][4];
+#pragma unroll
+    for (int k = 0; k < kOutR; ++k) {
+      const int64_t t = t0 + (k * 4 + wave) * SPW + sl;
+      const int64_t tt = t < te ? t : te - 1;  // steps past the block re-read its last step
+      ld_lanes<float, 4>(la + tt * row, a4[k]);
+      ld_lanes<float, 4>(lx + tt * row, x4[k]);
+      ld_lanes<T, 4>(cb + tt * sC_l, c4[k]);
+      ld_lanes<T, 4>(ub + tt * su_l, u4[k]);
+    }
+    float c[kOutR];
+#pragma unroll
+    for (int k = 0; k < kOutR; ++k) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc = __builtin_fmaf(c4[k][j], __builtin_fmaf(a4[k][j], xp[j], x4[k][j]), acc);
+        if (u_ok) acc = __builtin_fmaf(dv[j], u4[k][j], acc);
+      }
+      c[k] = acc;
+    }
+#pragma unroll
+    for (int k = 0; k < kOutR; ++k) c[k] = lanes_sum<LPS>(c[k]);
+#pragma unroll
+    for (int k = 0; k < kOutR; ++k) {
+      const int64_t t = t0 + (k * 4 + wave) * SPW + sl;
+      if (u_ok && t < te) {
+        const float v[4] = {c[k], c[k], c[k], c[k]};
+        st_lanes<T, 4>(yb + t * H, v);
+      }
+    }
   }
 }
 
@@ -698,8 +804,39 @@ extern "C" int tssm_mh_output(int dtype, const float* loc_a, const float* loc_x,
   if (grid_rows == 0 || grid_blks == 0) return TSSM_OK;
   TSSM_CHECK(grid_rows <= 65535, TSSM_ERR_UNSUPPORTED);
   const dim3 grid((unsigned)grid_blks, (unsigned)grid_rows);
-  const dim3 block((unsigned)(cdiv(head_dim, 64) * 64));
   const hipStream_t s = as_stream(stream);
+  {
+    // 4 channels per thread when every row start is a 4-element vector
+    const int64_t ve = dtype == TSSM_F32 ? 16 : 8;  // bytes of 4 elements
+    const int lps = (int)(head_dim / 4);
+    const bool vec = head_dim % 4 == 0 && (lps == 4 || lps == 8 || lps == 16 || lps == 32) &&
+                     H % 4 == 0 && su_b % 4 == 0 && su_l % 4 == 0 && sC_b % 4 == 0 &&
+                     sC_l % 4 == 0 && sC_h % 4 == 0 && aligned(loc_a, 16) && aligned(loc_x, 16) &&
+                     aligned(D, 16) && aligned(C, ve) && aligned(u, ve) && aligned(y, ve);
+    if (vec) {
+#define TSSM_MH_OV(T, LP)                                                                      \
+  hipLaunchKernelGGL((mh_output_vec_kernel<T, LP>), grid, dim3(256), 0, s, loc_a, loc_x, carry, \
+                     (const T*)C, D, (const T*)u, (T*)y, nbatch, L, H, n_heads, head_dim, su_b, \
+                     su_l, sC_b, sC_l, sC_h, blk_l, nblk)
+#define TSSM_MH_OVL(T)                       \
+  switch (lps) {                             \
+    case 4: TSSM_MH_OV(T, 4); break;         \
+    case 8: TSSM_MH_OV(T, 8); break;         \
+    case 16: TSSM_MH_OV(T, 16); break;       \
+    default: TSSM_MH_OV(T, 32); break;       \
+  }
+      switch (dtype) {
+        case TSSM_F32: TSSM_MH_OVL(float); break;
+        case TSSM_BF16: TSSM_MH_OVL(bf16_t); break;
+        case TSSM_F16: TSSM_MH_OVL(f16_t); break;
+        default: return TSSM_ERR_DTYPE;
+      }
+#undef TSSM_MH_OVL
+#undef TSSM_MH_OV
+      return launch_status();
+    }
+  }
+  const dim3 block((unsigned)(cdiv(head_dim, 64) * 64));
 #define TSSM_MH_OUT(T)                                                                         \
   hipLaunchKernelGGL(mh_output_kernel<T>, grid, block, 0, s, loc_a, loc_x, carry, (const T*)C, \
                      D, (const T*)u, (T*)y, nbatch, L, H, n_heads, head_dim, su_b, su_l, sC_b, \
