@@ -273,7 +273,8 @@ def _interp_inputs(Bsz, T, F, dtype, seed, p_obs=0.7, dev=None):
 @pytest.mark.parametrize("dtype,name", [(torch.float32, "fused_time_aware_interp_kernel"),
                                         (torch.bfloat16, "fused_interp_bf16_kernel"),
                                         (torch.float16, "fused_interp_fp16_kernel")])
-@pytest.mark.parametrize("K,FTILE,p_obs", [(10, 128, 0.7), (3, 16, 0.02), (5, 7, 0.05)])
+@pytest.mark.parametrize("K,FTILE,p_obs", [(10, 128, 0.7), (3, 16, 0.02), (5, 7, 0.05),
+                                         (4, 48, 0.1), (2, 512, 0.3)])
 def test_interp(dev, dtype, name, K, FTILE, p_obs):
     import fused_interp_kernel as fi
     Bsz, T, F = 3, 150, 100
@@ -287,16 +288,21 @@ def test_interp(dev, dtype, name, K, FTILE, p_obs):
     assert_close(out, ref, TOL[dtype] if dtype != torch.float32 else 1e-6, name)
 
 
-@pytest.mark.parametrize("F,FTILE,mdtype,p_obs", [(1000, 300, torch.float32, 0.002),
-                                                   (520, 264, torch.bfloat16, 0.004),
-                                                   (520, 264, torch.float16, 0.004),
-                                                   (96, 8, torch.float32, 0.05)])
-def test_interp_mask_layouts(dev, F, FTILE, mdtype, p_obs):
+@pytest.mark.parametrize("F,FTILE,mdtype,p_obs,mscale", [(1000, 300, torch.float32, 0.002, 1.0),
+                                                          (520, 264, torch.bfloat16, 0.004, 1.0),
+                                                          (520, 264, torch.float16, 0.004, 1.0),
+                                                          (96, 8, torch.float32, 0.05, 1.0),
+                                                          (1000, 64, torch.bfloat16, 0.003, 1.0),
+                                                          (520, 128, torch.float16, 0.004, 1.0),
+                                                          (256, 128, torch.float32, 0.02, 0.3)])
+def test_interp_mask_layouts(dev, F, FTILE, mdtype, p_obs, mscale):
     """Observed flags over rows of several 64-vector blocks, tiles spanning blocks,
-    16-bit masks, and sparse masks that leave whole tiles unobserved."""
+    16-bit masks, sparse masks that leave whole tiles unobserved, and fractional
+    masks (a tile counts as observed when its mask sum exceeds 0.5)."""
     import fused_interp_kernel as fi
     Bsz, T, K = 2, 90, 6
     V, M, tau = _interp_inputs(Bsz, T, F, torch.float32, seed=F + FTILE, p_obs=p_obs, dev=dev)
+    M = M * mscale
     Mq = M.to(mdtype)
     out = torch.full_like(V, float("nan"))
     fi.fused_time_aware_interp_kernel[(Bsz, T, (F + FTILE - 1) // FTILE)](

@@ -157,6 +157,67 @@ __global__ __launch_bounds__(kInterpThreads) void interp_obs_vec_kernel(InterpAr
   }
 }
 
+// Tiles of vpt = 2^lvpt 16-byte vectors (vpt <= 64) line up with aligned
+// vpt-lane groups of a 64-vector block, so a tile's sum is the lanes' vector
+// sums reduced over their group (xor shuffles) and the group's first lane
+// writes the flag.  A wave takes kObsP2Rows (row, block) items per batch, all
+// loads issued first; the row's (b, t) advance as wave-uniform counters.
+constexpr int kObsP2Rows = 8;
+
+template <typename TM, int E>
+__global__ __launch_bounds__(kInterpThreads) void interp_obs_pow2_kernel(InterpArgs a,
+                                                                        int64_t nrow, int lvpt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * (kInterpThreads / 64) +
+                    __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int64_t r0 = w * kObsP2Rows;
+  if (r0 >= nrow) return;  // uniform per wave
+  const int64_t fc = a.F < a.ntile * a.FTILE ? a.F : a.ntile * a.FTILE;
+  const int64_t nvec = fc / E;
+  const int nblk = (int)((nvec + 63) / 64);
+  const int nr = (int)(nrow - r0 < kObsP2Rows ? nrow - r0 : kObsP2Rows);
+  const int total = nr * nblk;
+  const int vpt = 1 << lvpt;
+  const TM* M = reinterpret_cast<const TM*>(a.M);
+  int64_t b = r0 / a.rows, t = r0 - b * a.rows;  // (b, t) of the next item's row
+  int64_t r = r0;
+  int blk = 0;
+  for (int i0 = 0; i0 < total; i0 += kObsP2Rows) {
+    float s[kObsP2Rows];
+    int64_t vv[kObsP2Rows], rr[kObsP2Rows];
+#pragma unroll
+    for (int u = 0; u < kObsP2Rows; ++u) {
+      const int64_t v = (int64_t)blk * 64 + lane;
+      const bool ok = i0 + u < total && v < nvec;
+      // lanes past the row or the batch read the first vector (in bounds)
+      const int64_t off = ok ? b * a.smb + t * a.smt + v * E : 0;
+      Lanes<TM, E> q;
+      q.load(M + off);
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < E; ++j) sum += q.v[j];
+      s[u] = ok ? sum : 0.0f;
+      vv[u] = ok ? v : -1;
+      rr[u] = r;
+      if (++blk == nblk) {  // uniform: next row
+        blk = 0;
+        ++r;
+        if (++t == a.rows) {
+          t = 0;
+          ++b;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kObsP2Rows; ++u) {
+      float x = s[u];
+      for (int o = 1; o < vpt; o <<= 1) x += __shfl_xor(x, o);
+      if (vv[u] >= 0 && (lane & (vpt - 1)) == 0)
+        a.obs[rr[u] * a.ntile + (vv[u] >> lvpt)] = x > 0.5f ? 1 : 0;
+    }
+  }
+}
+
 template <typename TV, int E>
 __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
   __shared__ unsigned char s_obs[kInterpTB + 2 * kMaxK];
@@ -463,6 +524,21 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   const int64_t fc = F < gf * FTILE ? F : gf * FTILE;
   if (FTILE % EM == 0 && fc % EM == 0 && smt % EM == 0 && smb % EM == 0 && aligned(M, 16) &&
       fc / EM < 2147483647 - 64) {
+    const int64_t vpt = FTILE / EM;
+    int lvpt = 0;
+    while ((int64_t(1) << lvpt) < vpt) ++lvpt;
+    if ((int64_t(1) << lvpt) == vpt && vpt <= 64) {  // tiles = aligned lane groups
+      const int64_t wv = (nrow + kObsP2Rows - 1) / kObsP2Rows;
+      const dim3 g((unsigned)((wv + wpb - 1) / wpb));
+      switch (m_dtype) {
+        case TSSM_F32: hipLaunchKernelGGL((interp_obs_pow2_kernel<float, 4>), g,
+                                          dim3(kInterpThreads), 0, s, a, nrow, lvpt); break;
+        case TSSM_BF16: hipLaunchKernelGGL((interp_obs_pow2_kernel<bf16_t, 8>), g,
+                                           dim3(kInterpThreads), 0, s, a, nrow, lvpt); break;
+        default: hipLaunchKernelGGL((interp_obs_pow2_kernel<f16_t, 8>), g,
+                                    dim3(kInterpThreads), 0, s, a, nrow, lvpt); break;
+      }
+    } else {
     const int64_t wv = (nrow + kObsRowsPerWave - 1) / kObsRowsPerWave;
     const dim3 g((unsigned)((wv + wpb - 1) / wpb));
     switch (m_dtype) {
@@ -472,6 +548,7 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
                                          dim3(kInterpThreads), 0, s, a, nrow); break;
       default: hipLaunchKernelGGL((interp_obs_vec_kernel<f16_t, 8>), g,
                                   dim3(kInterpThreads), 0, s, a, nrow); break;
+    }
     }
   } else {
     hipLaunchKernelGGL(interp_obs_kernel, dim3((unsigned)((nrow + wpb - 1) / wpb)),
