@@ -155,20 +155,18 @@ __device__ inline float phi1_from_exp(float x, float ex) {
 }
 // ZOH input coefficient expm1(dt a) / a for dt >= 0, a < 0, from the base-2
 // exponent y = dt a log2(e), e = exp2(y) (already computed for Abar) and
-// ia = 1/a.  |dt a| < 0.25: dt phi1(dt a), phi1's Taylor series to degree 6
-// written in y (coefficients ln2^k / (k+1)!; truncation < 2e-9 relative);
-// otherwise (e - 1) / a as one fma, where |e - 1| >= 0.22 keeps the
-// subtraction within ~3e-7 relative.  No reciprocal per call.
+// ia = 1/a.  |dt a| < 0.125: dt phi1(dt a), phi1's Taylor series to degree 4
+// written in y (coefficients ln2^k / (k+1)!; truncation < 4.3e-8 relative);
+// otherwise (e - 1) / a as one fma, where |e - 1| >= 0.1175 keeps the
+// subtraction within ~5e-7 relative.  No reciprocal per call.
 __device__ inline float zoh_coef2(float y, float e, float dt, float ia) {
-  float p = 2.2005043419116583e-05f;
-  p = __builtin_fmaf(p, y, 2.222259691071407e-04f);
-  p = __builtin_fmaf(p, y, 1.9236258215256953e-03f);
+  float p = 1.9236258215256953e-03f;
   p = __builtin_fmaf(p, y, 1.3876027166205394e-02f);
   p = __builtin_fmaf(p, y, 8.007550231970023e-02f);
   p = __builtin_fmaf(p, y, 0.34657359027997264f);
   p = __builtin_fmaf(p, y, 1.0f);
   const float big = __builtin_fmaf(e, ia, -ia);
-  return __builtin_fabsf(y) < 0.36067376022224085f ? p * dt : big;
+  return __builtin_fabsf(y) < 0.18033688011112042f ? p * dt : big;
 }
 __device__ inline float expm1_acc(float x, float ex) {
   return x * phi1_from_exp(x, ex);
