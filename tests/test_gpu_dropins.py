@@ -382,11 +382,16 @@ def test_streaming_inplace(dev, dtype, H):
     assert_close(h, h_chain, TOL[dtype], "h (chained)")
 
 
-@pytest.mark.parametrize("H,BLOCK_H", [(100, 32), (1000, 64)])   # tiles <= / > waves
-def test_streaming_ring_multi_tile(dev, H, BLOCK_H):
+@pytest.mark.parametrize("H,BLOCK_H,KR", [(100, 32, 5), (1000, 64, 5), (1000, 64, 17),
+                                         (300, 128, 5), (200, 64, 24), (301, 64, 5),
+                                         (96, 16, 9), (1000, 256, 11), (301, 128, 5)])
+def test_streaming_ring_multi_tile(dev, H, BLOCK_H, KR):
+    """Ring insert + backward search + step: 16-byte lanes for BLOCK_H 16..256
+    and H % 4 == 0 with the search slots in registers for KRING <= 17; other
+    shapes take the per-feature kernel."""
     import streaming_inference_kernel as sk
     g = torch.Generator().manual_seed(7)
-    Bsz, KR, steps = 3, 5, 12
+    Bsz, steps = 3, max(12, KR + 6)
     ring_V = torch.zeros(Bsz, KR, H, device=dev)
     ring_M = torch.zeros_like(ring_V)
     ring_tau = torch.zeros(Bsz, KR, device=dev)

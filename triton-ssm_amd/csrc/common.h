@@ -153,6 +153,25 @@ __device__ inline float phi1_from_exp(float x, float ex) {
   float big = (ex - 1.0f) * __builtin_amdgcn_rcpf(x);
   return __builtin_fabsf(x) < 0.5f ? p : big;
 }
+// ---------------------------------------------------------------- DPP helpers
+template <int CTRL>
+__device__ inline float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+// Sum over aligned groups of G consecutive lanes (G a power of two <= 64; DPP
+// within rows of 16, lane shuffles beyond); every lane of the group receives
+// the sum.
+template <int G>
+__device__ inline float group_sum(float v) {
+  if constexpr (G >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
+  if constexpr (G >= 16) v += dpp_mov<0x140>(v); // row_mirror
+  if constexpr (G >= 32) v += __shfl_xor(v, 16);
+  if constexpr (G >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
 // ZOH input coefficient expm1(dt a) / a for dt >= 0, a < 0, from the base-2
 // exponent y = dt a log2(e), e = exp2(y) (already computed for Abar) and
 // ia = 1/a.  |dt a| < 0.125: dt phi1(dt a), phi1's Taylor series to degree 4

@@ -33,21 +33,6 @@
 
 namespace tssm {
 
-// ---------------------------------------------------------------- DPP helpers
-template <int CTRL>
-__device__ inline float dpp_mov(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
-}
-// Sum over aligned groups of G consecutive lanes (G in 1,2,4,8,16); every lane
-// of the group receives the sum.
-template <int G>
-__device__ inline float group_sum(float v) {
-  if constexpr (G >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
-  if constexpr (G >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
-  if constexpr (G >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
-  if constexpr (G >= 16) v += dpp_mov<0x140>(v); // row_mirror
-  return v;
-}
 
 // k * s for a small non-negative per-lane k and a (uniform) 64-bit stride:
 // one 32 x 64-bit product (two's complement, so negative strides work too).

@@ -45,6 +45,7 @@ __global__ __launch_bounds__(256) void stream_step_kernel(
 }
 
 constexpr int kStreamThreads = 256;
+constexpr int kRingFast = 16;  // search slots held in registers (KRING <= 17)
 
 struct RingArgs {
   float* ring_V;
@@ -88,6 +89,46 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_kernel(Ring
     rM[nh * a.srk + k] = a.m_new[b * a.svb + k];
   }
   const int64_t ntile = (a.H + a.BLOCK_H - 1) / a.BLOCK_H;
+  if (a.BLOCK_H <= 64 && KR - 1 <= kRingFast) {
+    // one feature per lane.  The search result is used only when the new
+    // observation leaves the tile empty (fill, :133,143), so the tile's new
+    // mask is summed first and the ring is searched only then, every slot's
+    // mask value loaded before the first wave sum.
+    for (int64_t tile = wave; tile < ntile; tile += nwaves) {
+      const int64_t f = tile * a.BLOCK_H + lane;
+      const bool act = lane < a.BLOCK_H && f < a.H;
+      const int64_t fs = act ? f : tile * a.BLOCK_H;  // in bounds for idle lanes
+      const float vn = a.v_new[b * a.svb + fs];
+      const float mn = act ? a.m_new[b * a.svb + fs] : 0.0f;
+      const float hv = a.h[b * a.shb + fs], ab = a.Abar[fs], bb = a.Bbar[fs];
+      const float cv = a.C[b * a.scb + fs], dv = a.D[fs];
+      float v = vn;
+      if (wave_sum(mn) < 0.5f) {  // uniform
+        float ms[kRingFast];
+#pragma unroll
+        for (int k = 1; k <= kRingFast; ++k) {
+          const int64_t kk = k < KR ? k : KR - 1;  // clamped, zeroed below
+          const int64_t rk = (nh - kk + KR) % KR;
+          const float m = rM[rk * a.srk + fs];
+          ms[k - 1] = (act && k < KR) ? m : 0.0f;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+          for (int k = 0; k < kRingFast; ++k) ms[k] += __shfl_xor(ms[k], o);
+        int prev_k = -1;  // nearest earlier slot whose tile has any observation (:124-130)
+#pragma unroll
+        for (int k = kRingFast; k >= 1; --k)
+          if (k < KR && ms[k - 1] > 0.5f) prev_k = (int)((nh - k + KR) % KR);
+        if (prev_k >= 0) v = rV[prev_k * a.srk + fs];
+      }
+      if (act) {
+        const float hn = ab * hv + bb * v;                           // :152
+        a.h[b * a.shb + f] = hn;
+        a.y[b * a.svb + f] = cv * hn + dv * v;                       // :153,156
+      }
+    }
+  } else {
   for (int64_t tile = wave; tile < ntile; tile += nwaves) {
     const int64_t f0 = tile * a.BLOCK_H;
     const int64_t f1 = f0 + a.BLOCK_H < a.H ? f0 + a.BLOCK_H : a.H;
@@ -111,6 +152,83 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_kernel(Ring
       const float hn = a.Abar[f] * a.h[b * a.shb + f] + a.Bbar[f] * v;  // :152
       a.h[b * a.shb + f] = hn;
       a.y[b * a.svb + f] = a.C[b * a.scb + f] * hn + a.D[f] * v;        // :153,156
+    }
+  }
+  }
+  __syncthreads();  // every wave has read the head before it advances
+  if (tid == 0) {
+    a.ring_tau[b * KR + nh] = a.tau_new[b];                              // :116
+    a.ring_head[b] = (int32_t)nh;                                        // :117
+  }
+}
+
+// 16-byte form (BLOCK_H = 4 LPT with LPT in 4 .. 64; H % 4 == 0; aligned
+// rows): a lane owns 4 adjacent features, LPT lanes one tile, so a wave
+// instruction covers 64 / LPT tiles.  Same steps as stream_interp_step_kernel:
+// insert, then per tile the new mask sum (an LPT-lane group sum), the ring
+// searched (all slots at once) only when some tile of the wave has no new
+// observation, and the in-place step.
+template <int LPT>
+__global__ __launch_bounds__(kStreamThreads) void stream_interp_step_vec_kernel(RingArgs a) {
+  constexpr int TPW = 64 / LPT;  // tiles per wave instruction
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  constexpr int nwaves = kStreamThreads / 64;
+  const int64_t KR = a.KRING;
+  const int64_t head = a.ring_head[b];
+  const int64_t nh = (head + 1) % KR;                                    // :107
+  float* rV = a.ring_V + b * a.srb;
+  float* rM = a.ring_M + b * a.srb;
+  for (int64_t k = 4 * (int64_t)tid; k < a.H; k += 4 * kStreamThreads) {  // :110-114
+    *reinterpret_cast<float4*>(rV + nh * a.srk + k) =
+        *reinterpret_cast<const float4*>(a.v_new + b * a.svb + k);
+    *reinterpret_cast<float4*>(rM + nh * a.srk + k) =
+        *reinterpret_cast<const float4*>(a.m_new + b * a.svb + k);
+  }
+  const int64_t ntile = (a.H + a.BLOCK_H - 1) / a.BLOCK_H;
+  for (int64_t tg = (int64_t)wave * TPW; tg < ntile; tg += nwaves * TPW) {
+    const int64_t tile = tg + lane / LPT;
+    const int64_t f = tile * a.BLOCK_H + 4 * (lane % LPT);
+    const bool act = tile < ntile && f < a.H;  // H % 4 == 0: all 4 features or none
+    const int64_t fs = act ? f : 0;
+    float vn[4], mn[4], hv[4], cv[4], ab[4], bb[4], dv[4];
+    ld_lanes<float, 4>(a.v_new + b * a.svb + fs, vn);
+    ld_lanes<float, 4>(a.m_new + b * a.svb + fs, mn);
+    ld_lanes<float, 4>(a.h + b * a.shb + fs, hv);
+    ld_lanes<float, 4>(a.C + b * a.scb + fs, cv);
+    ld_lanes<float, 4>(a.Abar + fs, ab);
+    ld_lanes<float, 4>(a.Bbar + fs, bb);
+    ld_lanes<float, 4>(a.D + fs, dv);
+    const float sm = group_sum<LPT>(act ? (mn[0] + mn[1]) + (mn[2] + mn[3]) : 0.0f);
+    const bool need = act && sm < 0.5f;  // same on every lane of the tile
+    float v[4] = {vn[0], vn[1], vn[2], vn[3]};
+    if (__ballot(need) != 0) {  // uniform
+      float ms[kRingFast];
+#pragma unroll
+      for (int k = 1; k <= kRingFast; ++k) {
+        const int64_t kk = k < KR ? k : KR - 1;  // clamped, zeroed below
+        const int64_t rk = (nh - kk + KR) % KR;
+        float m[4];
+        ld_lanes<float, 4>(rM + rk * a.srk + fs, m);
+        ms[k - 1] = (act && k < KR) ? (m[0] + m[1]) + (m[2] + m[3]) : 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < kRingFast; ++k) ms[k] = group_sum<LPT>(ms[k]);
+      int prev_k = -1;  // nearest earlier slot whose tile has any observation (:124-130)
+#pragma unroll
+      for (int k = kRingFast; k >= 1; --k)
+        if (k < KR && ms[k - 1] > 0.5f) prev_k = (int)((nh - k + KR) % KR);
+      if (need && prev_k >= 0) ld_lanes<float, 4>(rV + prev_k * a.srk + fs, v);  // :133,143
+    }
+    if (act) {
+      float hn[4], yo[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hn[j] = ab[j] * hv[j] + bb[j] * v[j];                            // :152
+        yo[j] = cv[j] * hn[j] + dv[j] * v[j];                            // :153,156
+      }
+      st_lanes<float, 4>(a.h + b * a.shb + f, hn);
+      st_lanes<float, 4>(a.y + b * a.svb + f, yo);
     }
   }
   __syncthreads();  // every wave has read the head before it advances
@@ -179,7 +297,25 @@ extern "C" int tssm_stream_interp_step(float* ring_V, float* ring_M, float* ring
   if (grid_b == 0 || H == 0) return TSSM_OK;
   RingArgs a{ring_V, ring_M, ring_tau, ring_head, v_new, m_new, tau_new, h, Abar, Bbar, C, D, y,
              H, srb, srk, svb, shb, scb, BLOCK_H, KRING};
-  hipLaunchKernelGGL(stream_interp_step_kernel, dim3((unsigned)grid_b), dim3(kStreamThreads), 0,
-                     as_stream(stream), a);
+  const bool vec = (BLOCK_H == 16 || BLOCK_H == 32 || BLOCK_H == 64 || BLOCK_H == 128 ||
+                    BLOCK_H == 256) && KRING - 1 <= kRingFast &&
+                   H % 4 == 0 && srb % 4 == 0 && srk % 4 == 0 && svb % 4 == 0 && shb % 4 == 0 &&
+                   scb % 4 == 0 && aligned(ring_V, 16) && aligned(ring_M, 16) &&
+                   aligned(v_new, 16) && aligned(m_new, 16) && aligned(h, 16) &&
+                   aligned(Abar, 16) && aligned(Bbar, 16) && aligned(C, 16) && aligned(D, 16) &&
+                   aligned(y, 16);
+  const dim3 grid((unsigned)grid_b), block(kStreamThreads);
+  const hipStream_t s = as_stream(stream);
+  if (vec) {
+    switch (BLOCK_H) {
+      case 16: hipLaunchKernelGGL(stream_interp_step_vec_kernel<4>, grid, block, 0, s, a); break;
+      case 32: hipLaunchKernelGGL(stream_interp_step_vec_kernel<8>, grid, block, 0, s, a); break;
+      case 64: hipLaunchKernelGGL(stream_interp_step_vec_kernel<16>, grid, block, 0, s, a); break;
+      case 128: hipLaunchKernelGGL(stream_interp_step_vec_kernel<32>, grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL(stream_interp_step_vec_kernel<64>, grid, block, 0, s, a); break;
+    }
+  } else {
+    hipLaunchKernelGGL(stream_interp_step_kernel, grid, block, 0, s, a);
+  }
   return launch_status();
 }
