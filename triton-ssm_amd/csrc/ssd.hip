@@ -374,13 +374,16 @@ __device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // LDS element offsets.  Transposed half-tiles (xT[p][s], BT[n][s], 128
-// columns): the 16-byte column block is XORed with the row's group of 8, so
-// both the transposing writes (8 rows, one column block per lane) and the
-// operand reads (8 rows per lane group) spread over all banks.  Sub-chunk
-// states sH[J][p][n]: the 4-float quad is XORed with (p >> 1) & 3 for the
-// row-per-lane operand reads.
+// columns = 16 blocks of 16 bytes per row): the column block is XORed with
+// (row ^ row >> 3) mod 16, which takes 16 distinct values over any 16
+// consecutive rows and over the 8-row groups of the transposing writes, so
+// the operand reads (16 or 32 consecutive rows, one block per lane), the
+// output reads and the transposing writes each touch every bank about
+// equally.  (XOR with row >> 3 alone left 32-row reads on 4 blocks.)
+// Sub-chunk states sH[J][p][n]: the 4-float quad is XORed with (p >> 1) & 3
+// for the row-per-lane operand reads.
 __device__ inline int tix(int row, int col) {
-  return row * kMu + ((((col >> 3) ^ (row >> 3)) & (kMu / 8 - 1)) << 3) + (col & 7);
+  return row * kMu + ((((col >> 3) ^ row ^ (row >> 3)) & (kMu / 8 - 1)) << 3) + (col & 7);
 }
 __device__ inline int hix(int J, int p, int n) {
   return (J * kMp + p) * kMn + ((((n >> 2) ^ (p >> 1)) & 3) << 2) + (n & 3);
