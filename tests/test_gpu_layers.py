@@ -95,25 +95,28 @@ def test_swiglu_forward_backward(dev, dtype, H):
     assert_close(du, rdu, tol, "swiglu dup")
 
 
-def test_residual_and_dropout(dev):
+@pytest.mark.parametrize("N,dtype", [(10_000, torch.float32), (10_001, torch.float32),
+                                     (10_000, torch.bfloat16)])   # 4-element and scalar paths
+def test_residual_and_dropout(dev, N, dtype):
     import multihead_ssm_kernel as mk
-    N, BLOCK = 10_000, 1024
-    x, res = _r((N,), 30).to(dev), _r((N,), 31).to(dev)
+    BLOCK = 1024
+    x, res = _r((N,), 30, dtype).to(dev), _r((N,), 31, dtype).to(dev)
     keep = (torch.rand(N, generator=torch.Generator().manual_seed(32)) < 0.8).to(torch.uint8).to(dev)
+    tol = 1e-6 if dtype == torch.float32 else TOL[dtype]
     out = torch.full_like(x, float("nan"))
     mk.residual_add_kernel[(-(-N // BLOCK),)](x, res, out, N, BLOCK=BLOCK)
     torch.cuda.synchronize()
-    assert_close(out, O.residual_add(x, res), 1e-6, "residual")
+    assert_close(out, O.residual_add(x, res), tol, "residual")
     out2 = torch.full_like(x, float("nan"))
     mk.dropout_residual_kernel[(4,)](x, res, keep, out2, N, 0.8, BLOCK=BLOCK)   # first 4096 only
     torch.cuda.synchronize()
-    assert_close(out2[:4096], O.dropout_residual(x[:4096], res[:4096], keep[:4096], 0.8), 1e-6,
+    assert_close(out2[:4096], O.dropout_residual(x[:4096], res[:4096], keep[:4096], 0.8), tol,
                  "dropout")
     assert torch.isnan(out2[4096:]).all()
     out3 = torch.empty_like(x)
     mk.dropout_residual_kernel[(10,)](x, res, keep.bool(), out3, N, 0.8, BLOCK=BLOCK)
     torch.cuda.synchronize()
-    assert_close(out3, O.dropout_residual(x, res, keep, 0.8), 1e-6, "dropout bool mask")
+    assert_close(out3, O.dropout_residual(x, res, keep, 0.8), tol, "dropout bool mask")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -412,6 +412,29 @@ __global__ __launch_bounds__(kThreads) void residual_kernel(
   }
 }
 
+// Dropout + residual with 4 elements per thread (16-byte fp32 / 8-byte 16-bit
+// accesses, one 4-byte keep load): n % 4 == 0 and aligned pointers.  Same
+// values as residual_kernel.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void residual_vec_kernel(
+    const T* __restrict__ x, const T* __restrict__ res, const uint8_t* __restrict__ keep,
+    T* __restrict__ out, int64_t n4, float scale) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4;
+       i += (int64_t)gridDim.x * kThreads) {
+    float xv[4], rv[4], o[4];
+    ld_lanes<T, 4>(x + 4 * i, xv);
+    ld_lanes<T, 4>(res + 4 * i, rv);
+    if (keep) {
+      const uint32_t k = reinterpret_cast<const uint32_t*>(keep)[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[j] = xv[j] * (float)((k >> (8 * j)) & 0xffu) * scale;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = xv[j] + rv[j];
+    st_lanes<T, 4>(out + 4 * i, o);
+  }
+}
+
 // Partial dot products of W with rows [blockIdx.y * kPoolRows, +kPoolRows) of
 // batch blockIdx.x.
 template <typename T, int V>
@@ -707,6 +730,17 @@ extern "C" int tssm_residual_add(int dtype, const void* x, const void* res, cons
   if (n == 0) return TSSM_OK;
   const hipStream_t s = as_stream(stream);
   const float scale = 1.0f / p_keep;
+  // dropout: 4 elements per thread (one 4-byte keep load) measured 97 -> 81 us
+  // at 33.5 M fp32 elements; the plain add stays one element per thread (the
+  // 4-element form measured 3 us slower there)
+  const uintptr_t ve = dtype == TSSM_F32 ? 16 : 8;  // bytes of 4 elements
+  if (keep && n % 4 == 0 && aligned(x, ve) && aligned(res, ve) && aligned(out, ve) &&
+      aligned(keep, 4)) {
+    TSSM_DISPATCH(dtype, hipLaunchKernelGGL((residual_vec_kernel<T>), dim3(flat_grid(n / 4)),
+                                            dim3(kThreads), 0, s, (const T*)x, (const T*)res,
+                                            keep, (T*)out, n / 4, scale));
+    return launch_status();
+  }
   TSSM_DISPATCH(dtype, hipLaunchKernelGGL((residual_kernel<T>), dim3(flat_grid(n)),
                                           dim3(kThreads), 0, s, (const T*)x, (const T*)res,
                                           keep, (T*)out, n, scale));
