@@ -407,6 +407,10 @@ def rows_sweep(args, dev):
            lambda: fi.fused_time_aware_interp_kernel[(Bi, Ti, Fi // 128)](
                V, M, tau, Vh, Bi, Ti, Fi, *V.stride(), *M.stride(), *tau.stride(), *Vh.stride(),
                K=10, FTILE=128))
+    # opt-in corrected interpolation (per-feature neighbours), same shape
+    from tssm import time_aware_interp_corrected
+    timeit("f4 interp corrected (fp32)", f"B={Bi} T={Ti} F={Fi} K=10", Bi * Ti * Fi * 12 + Bi * Ti * 4,
+           lambda: time_aware_interp_corrected(V, M, tau, K=10, out=Vh))
     # a15 interp + SSM step at one t_cur (per-step launch of the reference loop)
     Ab1, Bb1 = torch.rand(Fi, device=dev), rnd(Fi)
     h_in, h_out = rnd(Bi, Fi), torch.empty(Bi, Fi, device=dev)
@@ -441,6 +445,11 @@ def rows_sweep(args, dev):
                ring_V, ring_M, ring_tau, head, vn, mn, tn, hr, Abr, Bbr, Cr, Dr, yr, Sr, Hr,
                KR - 1, *ring_V.stride(), *vn.stride(), *hr.stride(), *Cr.stride(), BLOCK_H=128,
                KRING=KR))
+    # opt-in corrected interpolation (per-feature neighbours), same shapes
+    from tssm import streaming_interp_step_corrected
+    timeit("f4 streaming corrected (ring)", f"S={Sr} H={Hr} KRING={KR}", Sr * Hr * 4 * 8,
+           lambda: streaming_interp_step_corrected(ring_V, ring_M, ring_tau, head, vn, mn, tn, hr,
+                                                   Abr, Bbr, Cr, Dr, yr))
     # model layers (fp32, headline lane count)
     x, dout = rnd(B, T, H), rnd(B, T, H)
     wv, bv = rnd(H), rnd(H)

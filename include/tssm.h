@@ -176,6 +176,18 @@ int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, const void* 
                            int64_t grid_b, int64_t grid_t, int64_t grid_f, void* workspace,
                            int64_t workspace_bytes, void* stream);
 
+/* Opt-in "corrected" interpolation (no reference counterpart: the intent
+ * stated at fused_interp_kernel.py:49-50, not the reference's behaviour, which
+ * tssm_time_aware_interp keeps).  Per (b, t, f): an observed value (M > 0.5)
+ * is kept; otherwise the nearest steps within K on each side where that
+ * feature is observed give the value with the reference's weights, clipping
+ * and one-sided fills.  Whole tensors, no workspace. */
+int tssm_time_aware_interp_corrected(int v_dtype, int m_dtype, int tau_dtype, const void* V,
+                                     const void* M, const void* tau, void* Vhat, int64_t nbatch,
+                                     int64_t T, int64_t F, int64_t svb, int64_t svt, int64_t smb,
+                                     int64_t smt, int64_t stb, int64_t stt, int64_t sob,
+                                     int64_t sot, int64_t K, void* stream);
+
 /* fused_interp_ssm_step_kernel (fused_ssm_interp.py:12-101): interpolates
  * step t_cur into Vhat[:, t_cur] and writes h_out = A_bar*h_in + B_bar*vhat.
  * A_bar, B_bar [F], h_in, h_out f32.  Grid (B, ceil(F/FTILE)). */
@@ -206,6 +218,18 @@ int tssm_stream_interp_step(float* ring_V, float* ring_M, float* ring_tau, int32
                             const float* D, float* y, int64_t nbatch, int64_t H, int64_t srb,
                             int64_t srk, int64_t svb, int64_t shb, int64_t scb, int64_t BLOCK_H,
                             int64_t KRING, int64_t grid_b, void* stream);
+
+/* Opt-in corrected streaming step (no reference counterpart): the insert and
+ * race-free head update of tssm_stream_interp_step, then per feature an
+ * observed new value is kept and an unobserved one is forward-filled from the
+ * most recent of the previous KRING-1 slots where that feature was observed. */
+int tssm_stream_interp_step_corrected(float* ring_V, float* ring_M, float* ring_tau,
+                                      int32_t* ring_head, const float* v_new, const float* m_new,
+                                      const float* tau_new, float* h, const float* Abar,
+                                      const float* Bbar, const float* C, const float* D, float* y,
+                                      int64_t nbatch, int64_t H, int64_t srb, int64_t srk,
+                                      int64_t svb, int64_t shb, int64_t scb, int64_t KRING,
+                                      void* stream);
 
 /* ------------------------------------------------------------------ SSD (new fused entry points)
  * Selective scan with one decay per head and a P x N state per (batch, head):

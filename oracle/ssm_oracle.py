@@ -679,6 +679,77 @@ def streaming_interp_step(ring_V, ring_M, ring_tau, ring_head, v_new, m_new, tau
 
 
 # --------------------------------------------------------------------------
+# opt-in "corrected" interpolation (the intent stated at
+# fused_interp_kernel.py:49-50; not the reference's behaviour, which stays the
+# default everywhere)
+# --------------------------------------------------------------------------
+def time_aware_interp_corrected(V, M, tau, K=10):
+    """Per-feature neighbours: for each (b, t, f) an observed value
+    (M > 0.5) is kept; otherwise prev/next are the nearest steps within K on
+    each side where that feature is observed, and the weights, clipping and
+    one-sided fills follow fused_interp_kernel.py:71-97 (w = (tau_t - tau_p) /
+    (tau_n - tau_p) clipped to [0, 1], 0.5 when the gap is <= 1e-9; only one
+    neighbour: its value; none: V[t] as stored)."""
+    V, M, tau = _f64(V), _f64(M), _f64(tau)
+    Bsz, T, F = V.shape
+    obs = M > 0.5
+    out = V.copy()
+    bidx = np.arange(Bsz)[:, None]
+    fidx = np.arange(F)[None, :]
+    for t in range(T):
+        prev = np.full((Bsz, F), -1, dtype=np.int64)
+        nxt = np.full((Bsz, F), -1, dtype=np.int64)
+        for k in range(K, 0, -1):            # nearest wins
+            if t - k >= 0:
+                prev = np.where(obs[:, t - k], t - k, prev)
+            if t + k < T:
+                nxt = np.where(obs[:, t + k], t + k, nxt)
+        tp = np.where(prev >= 0, tau[bidx, np.maximum(prev, 0)], 0.0)
+        tn = np.where(nxt >= 0, tau[bidx, np.maximum(nxt, 0)], 0.0)
+        den = tn - tp
+        with np.errstate(divide="ignore", invalid="ignore"):
+            w = np.where(den > 1e-9, (tau[:, t][:, None] - tp) / den, 0.5)
+        w = np.clip(w, 0.0, 1.0)
+        vp = V[bidx, np.maximum(prev, 0), fidx]
+        vn = V[bidx, np.maximum(nxt, 0), fidx]
+        v = np.where((prev >= 0) & (nxt >= 0), (1.0 - w) * vp + w * vn,
+                     np.where(prev >= 0, vp, np.where(nxt >= 0, vn, V[:, t])))
+        out[:, t] = np.where(obs[:, t], V[:, t], v)
+    return out
+
+
+def streaming_interp_step_corrected(ring_V, ring_M, ring_tau, ring_head, v_new, m_new,
+                                    tau_new, h, Abar, Bbar, C, D, KRING):
+    """Streaming counterpart of time_aware_interp_corrected: the ring insert
+    and head update of streaming_interp_step, then per feature an observed
+    new value is kept and an unobserved one is forward-filled from the most
+    recent of the previous KRING-1 slots where that feature was observed (a
+    causal step has no later neighbour to weight against); none: v_new as
+    given.  Returns new copies (ring_V, ring_M, ring_tau, ring_head, h_new, y)."""
+    ring_V, ring_M, ring_tau = _f64(ring_V).copy(), _f64(ring_M).copy(), _f64(ring_tau).copy()
+    head = np.asarray(ring_head).astype(np.int64).copy()
+    v_new, m_new, tau_new = _f64(v_new), _f64(m_new), _f64(tau_new)
+    h, Abar, Bbar, C, D = map(_f64, (h, Abar, Bbar, C, D))
+    Bsz, H = v_new.shape
+    vhat = v_new.copy()
+    for b in range(Bsz):
+        nh = (head[b] + 1) % KRING
+        ring_V[b, nh] = v_new[b]
+        ring_M[b, nh] = m_new[b]
+        ring_tau[b, nh] = tau_new[b]
+        need = ~(m_new[b] > 0.5)
+        for k in range(1, KRING):            # nearest first
+            rk = (nh - k + KRING) % KRING
+            hit = need & (ring_M[b, rk] > 0.5)
+            vhat[b] = np.where(hit, ring_V[b, rk], vhat[b])
+            need &= ~hit
+        head[b] = nh
+    h_new = Abar * h + Bbar * vhat
+    y = C * h_new + D * vhat
+    return ring_V, ring_M, ring_tau, head, h_new, y
+
+
+# --------------------------------------------------------------------------
 # model layers around the scan (fused_ssm_interp.py, multihead_ssm_kernel.py,
 # streaming_inference_kernel.py)
 # --------------------------------------------------------------------------

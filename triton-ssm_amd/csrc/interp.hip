@@ -473,6 +473,66 @@ __global__ __launch_bounds__(kInterpThreads) void interp_step_fast_kernel(StepAr
   a.h_out[b * a.s_hob + f] = abar * hp + bbar * v;
 }
 
+// Opt-in corrected interpolation (per-feature neighbours, observed values
+// kept; the reference behaviour above stays the default).  Workgroup = (b,
+// 64 steps, 64 features): the observed flags (M > 0.5) and tau of rows
+// t0-K .. t0+63+K are staged in LDS, lane = feature, wave w takes steps
+// t0 + w + 4 i; the nearest observed step within K on each side is found in
+// LDS and V is read only at the step itself or at the chosen neighbours.
+constexpr int kCorrTB = 64;
+
+template <typename TV>
+__global__ __launch_bounds__(kInterpThreads) void interp_corrected_kernel(InterpArgs a) {
+  __shared__ unsigned char s_obs[kCorrTB + 2 * kMaxK][64];
+  __shared__ float s_tau[kCorrTB + 2 * kMaxK];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * kCorrTB;
+  const int64_t f = (int64_t)blockIdx.y * 64 + lane;
+  const int64_t b = blockIdx.z;
+  const int K = (int)a.K;
+  const int nrow = kCorrTB + 2 * K;
+  const bool fok = f < a.F;
+  const int64_t fs = fok ? f : 0;
+  for (int i = wave; i < nrow; i += kInterpThreads / 64) {
+    const int64_t t = t0 - K + i;
+    const bool in = t >= 0 && t < a.T;
+    s_obs[i][lane] = (in && fok && ld_any(a.M, b * a.smb + t * a.smt + fs, a.md) > 0.5f) ? 1 : 0;
+    if (lane == 0) s_tau[i] = in ? ld_any(a.tau, b * a.stb + t * a.stt, a.td) : 0.0f;
+  }
+  __syncthreads();
+  if (!fok) return;  // after the only barrier
+  const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb + f;
+  TV* O = reinterpret_cast<TV*>(a.Vhat) + b * a.sob + f;
+  for (int j = wave; j < kCorrTB; j += kInterpThreads / 64) {
+    const int64_t t = t0 + j;
+    if (t >= a.grid_t) break;
+    const int i = K + j;  // row of step t in the staged window
+    float v;
+    if (s_obs[i][lane]) {
+      v = ldf(V + t * a.svt);
+    } else {
+      int kp = 0, kn = 0;
+      for (int k = 1; k <= K && kp == 0; ++k)
+        if (s_obs[i - k][lane]) kp = k;
+      for (int k = 1; k <= K && kn == 0; ++k)
+        if (s_obs[i + k][lane]) kn = k;
+      if (kp > 0 && kn > 0) {
+        const float tp = s_tau[i - kp], tn = s_tau[i + kn], den = tn - tp;
+        float w = den > 1e-9f ? (s_tau[i] - tp) / den : 0.5f;
+        w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+        v = (1.0f - w) * ldf(V + (t - kp) * a.svt) + w * ldf(V + (t + kn) * a.svt);
+      } else if (kp > 0) {
+        v = ldf(V + (t - kp) * a.svt);
+      } else if (kn > 0) {
+        v = ldf(V + (t + kn) * a.svt);
+      } else {
+        v = ldf(V + t * a.svt);
+      }
+    }
+    stf(O + t * a.sot, v);
+  }
+}
+
 }  // namespace tssm
 
 using namespace tssm;
@@ -609,6 +669,32 @@ extern "C" int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, con
     case TSSM_F32: hipLaunchKernelGGL(interp_step_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
     case TSSM_BF16: hipLaunchKernelGGL(interp_step_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
     default: hipLaunchKernelGGL(interp_step_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+  }
+  return launch_status();
+}
+
+extern "C" int tssm_time_aware_interp_corrected(int v_dtype, int m_dtype, int tau_dtype,
+                                                const void* V, const void* M, const void* tau,
+                                                void* Vhat, int64_t nbatch, int64_t T, int64_t F,
+                                                int64_t svb, int64_t svt, int64_t smb, int64_t smt,
+                                                int64_t stb, int64_t stt, int64_t sob, int64_t sot,
+                                                int64_t K, void* stream) {
+  TSSM_CHECK(V && M && tau && Vhat, TSSM_ERR_NULL);
+  TSSM_CHECK(float_dtype(v_dtype) && float_dtype(m_dtype) && float_dtype(tau_dtype),
+             TSSM_ERR_DTYPE);
+  TSSM_CHECK(nbatch >= 0 && T >= 0 && F >= 0 && K >= 0, TSSM_ERR_SHAPE);
+  TSSM_CHECK(K <= kMaxK, TSSM_ERR_UNSUPPORTED);
+  if (nbatch == 0 || T == 0 || F == 0) return TSSM_OK;
+  const int64_t gx = (T + kCorrTB - 1) / kCorrTB, gy = (F + 63) / 64;
+  TSSM_CHECK(gx <= 2147483647 && gy <= 65535 && nbatch <= 65535, TSSM_ERR_UNSUPPORTED);
+  InterpArgs a{V, M, tau, Vhat, nullptr, m_dtype, tau_dtype, T, F, svb, svt, smb, smt, stb, stt,
+               sob, sot, K, 1, T, T, 0};
+  const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)nbatch);
+  const hipStream_t s = as_stream(stream);
+  switch (v_dtype) {
+    case TSSM_F32: hipLaunchKernelGGL(interp_corrected_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
+    case TSSM_BF16: hipLaunchKernelGGL(interp_corrected_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL(interp_corrected_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
   }
   return launch_status();
 }

@@ -238,6 +238,56 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_vec_kernel(
   }
 }
 
+// Opt-in corrected streaming interpolation: the same insert and head update
+// as stream_interp_step_kernel, then per feature an observed new value is
+// kept and an unobserved one is forward-filled from the most recent of the
+// previous KRING-1 slots where that feature was observed (a causal step has
+// no later neighbour to weight against); none: v_new as given.
+__global__ __launch_bounds__(kStreamThreads) void stream_interp_step_corrected_kernel(RingArgs a) {
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t KR = a.KRING;
+  const int64_t head = a.ring_head[b];
+  const int64_t nh = (head + 1) % KR;
+  float* rV = a.ring_V + b * a.srb;
+  float* rM = a.ring_M + b * a.srb;
+  for (int64_t f = tid; f < a.H; f += kStreamThreads) {
+    const float vn = a.v_new[b * a.svb + f];
+    const float mn = a.m_new[b * a.svb + f];
+    rV[nh * a.srk + f] = vn;  // this thread's own feature: no other thread reads it
+    rM[nh * a.srk + f] = mn;
+    float v = vn;
+    if (!(mn > 0.5f)) {
+      int64_t hit = -1;
+      if (KR - 1 <= kRingFast) {  // every slot's mask at once, nearest hit kept
+        float ms[kRingFast];
+#pragma unroll
+        for (int k = 1; k <= kRingFast; ++k) {
+          const int64_t kk = k < KR ? k : KR - 1;  // clamped, ignored below
+          ms[k - 1] = rM[((nh - kk + KR) % KR) * a.srk + f];
+        }
+#pragma unroll
+        for (int k = kRingFast; k >= 1; --k)
+          if (k < KR && ms[k - 1] > 0.5f) hit = (nh - k + KR) % KR;
+      } else {
+        for (int64_t k = 1; k < KR && hit < 0; ++k) {  // nearest first
+          const int64_t rk = (nh - k + KR) % KR;
+          if (rM[rk * a.srk + f] > 0.5f) hit = rk;
+        }
+      }
+      if (hit >= 0) v = rV[hit * a.srk + f];
+    }
+    const float hn = a.Abar[f] * a.h[b * a.shb + f] + a.Bbar[f] * v;
+    a.h[b * a.shb + f] = hn;
+    a.y[b * a.svb + f] = a.C[b * a.scb + f] * hn + a.D[f] * v;
+  }
+  __syncthreads();  // every thread has read the head before it advances
+  if (tid == 0) {
+    a.ring_tau[b * KR + nh] = a.tau_new[b];
+    a.ring_head[b] = (int32_t)nh;
+  }
+}
+
 }  // namespace tssm
 
 using namespace tssm;
@@ -317,5 +367,23 @@ extern "C" int tssm_stream_interp_step(float* ring_V, float* ring_M, float* ring
   } else {
     hipLaunchKernelGGL(stream_interp_step_kernel, grid, block, 0, s, a);
   }
+  return launch_status();
+}
+
+extern "C" int tssm_stream_interp_step_corrected(
+    float* ring_V, float* ring_M, float* ring_tau, int32_t* ring_head, const float* v_new,
+    const float* m_new, const float* tau_new, float* h, const float* Abar, const float* Bbar,
+    const float* C, const float* D, float* y, int64_t nbatch, int64_t H, int64_t srb,
+    int64_t srk, int64_t svb, int64_t shb, int64_t scb, int64_t KRING, void* stream) {
+  TSSM_CHECK(ring_V && ring_M && ring_tau && ring_head && v_new && m_new && tau_new && h &&
+                 Abar && Bbar && C && D && y,
+             TSSM_ERR_NULL);
+  TSSM_CHECK(nbatch >= 0 && H >= 0 && KRING > 0, TSSM_ERR_SHAPE);
+  if (nbatch == 0 || H == 0) return TSSM_OK;
+  TSSM_CHECK(nbatch <= 2147483647, TSSM_ERR_UNSUPPORTED);
+  RingArgs a{ring_V, ring_M, ring_tau, ring_head, v_new, m_new, tau_new, h, Abar, Bbar, C, D, y,
+             H, srb, srk, svb, shb, scb, 1, KRING};
+  hipLaunchKernelGGL(stream_interp_step_corrected_kernel, dim3((unsigned)nbatch),
+                     dim3(kStreamThreads), 0, as_stream(stream), a);
   return launch_status();
 }
