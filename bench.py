@@ -134,7 +134,7 @@ def wl_ssd_config1(args, dev):
     n = B * L * H * P
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
-                kernel="ssd_state_kernel + ssd_pass_kernel + ssd_out_kernel",
+                kernel="ssd_seq_kernel",
                 metric="SSD scan elements/sec on the headline shapes, B=8 L=4096 H=16 P=N=64 bf16",
                 unit="elements/s",
                 config={"workload": "SSD scan (decay per head, P x N state) on the DIAG headline "
@@ -241,7 +241,7 @@ def wl_ssd_long(args, dev):
     n = B * L * H * P
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
-                kernel="ssd_state_kernel + ssd_pass_kernel + ssd_out_kernel",
+                kernel="ssd_state_mfma_kernel + ssd_pass_kernel + ssd_out_mfma_kernel",
                 metric="SSD long-sequence scan elements/sec, B=1 L=262144 H=8 P=64 N=16 bf16",
                 unit="elements/s",
                 config={"workload": "SSD scan (decay per head, P x N state), B=1 L=262144 H=8 "

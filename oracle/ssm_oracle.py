@@ -39,6 +39,11 @@ ssd_stream_step       k streaming steps == ssd_scan over the same k inputs.
 time_aware_interp     hand-built known-answer cases (boundaries, nearest
                       neighbour, tile aggregate, affine invariance, w=0.5).
 streaming_*           k steps == elementwise scan; ring known-answer cases.
+*_corrected           closed forms (all observed -> V; linear values and times
+                      reproduced exactly between neighbours), agreement with
+                      time_aware_interp / streaming_interp_step where every
+                      FTILE tile is uniformly observed, brute-force per-feature
+                      nearest-neighbour search on small inputs.
 zoh_discretize_bwd    torch.autograd of a torch float64 ZOH forward.
 dt_project_softplus   torch.nn.functional.softplus + clamp in float64.
 layernorm(_bwd)       torch.nn.functional.layer_norm and its autograd (BLOCK_H =

@@ -59,6 +59,50 @@ def test_ssd_scan_matrix_core_path(dev, L, disc, with_d):
     assert_close(hl, h_ref, 1e-3, "mfma ssd h_last")
 
 
+@pytest.mark.parametrize("Bsz,L,H,P", [(2, 300, 3, 64), (2, 200, 4, 32), (1, 130, 8, 48),
+                                        (1, 64, 8, 16), (1, 1, 2, 64), (3, 1000, 8, 64)])
+@pytest.mark.parametrize("disc", ["zoh", "euler"])
+@pytest.mark.parametrize("with_d", [False, True])
+def test_ssd_scan_n64_matrix_core_path(dev, Bsz, L, H, P, disc, with_d):
+    """bf16 with N = 64 runs one matrix-core pass per (row, 16-channel block):
+    ragged blocks of 64 steps, 1-4 channel blocks per row, row counts that are
+    and are not multiples of 8 (the two block mappings), skip term, nonzero h0
+    and the final state.  Same bar as the other matrix-core path."""
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, Bsz, L, H, P, 64, torch.bfloat16, seed=L + P + with_d, heavy=True)
+    h0 = torch.randn(Bsz, H, P, 64, device=dev)
+    D = d["D"] if with_d else None
+    y, hl = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], D, disc=disc,
+                             h0=h0, chunk=256, return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssd_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"], D, h0=np64(h0), disc=disc)
+    assert_close(y, y_ref, 4e-3, f"n64 ssd y L={L} P={P} {disc} D={with_d}")
+    assert_close(hl, h_ref, 1e-3, f"n64 ssd h_last L={L} P={P} {disc}")
+
+
+def test_ssd_scan_n64_headline_shape(dev):
+    """B=8 L=4096 H=16 P=N=64 bf16 (the headline shapes read as SSD), the
+    seeded workload of the benchmark: batch 0 and 7, heads 0 and 15 against
+    the oracle on those slices; zero initial state."""
+    from tssm import ssd_scan_forward, workloads
+    Bsz, L, H, P = 8, 4096, 16, 64
+    w = workloads.multihead(B=Bsz, L=L, H=H, P=P)
+    x = w["u"].view(Bsz, L, H, P)
+    d = {k: v.to(dev) for k, v in dict(x=x, B=w["B"], C=w["C"], dt=w["dt"]).items()}
+    A_log = w["A_log_h"].to(dev)
+    y, hl = ssd_scan_forward(d["x"], d["dt"], A_log, d["B"], d["C"], None, chunk=128,
+                             return_state=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    for b in (0, 7):
+        for hh in (0, 15):
+            sl = (slice(b, b + 1), slice(None), slice(hh, hh + 1))
+            y_ref, h_ref = O.ssd_scan(x[sl], w["dt"][sl], w["A_log_h"][hh:hh + 1], w["B"][sl],
+                                      w["C"][sl])
+            assert_close(y[sl], y_ref, 4e-3, f"headline-shape ssd y b={b} h={hh}")
+            assert_close(hl[b:b + 1, hh:hh + 1], h_ref, 1e-3, f"headline-shape ssd h b={b} h={hh}")
+
+
 @pytest.mark.parametrize("chunk", [64, 256, 1024])
 def test_ssd_scan_chunks_and_split(dev, chunk):
     from tssm import ssd_scan_forward

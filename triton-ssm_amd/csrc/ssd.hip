@@ -864,6 +864,255 @@ int launch_ssd_mfma(bool has_d, int64_t rows, int64_t nchunks, int64_t PN, hipSt
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// SSD with N = 64 and bf16 I/O on the matrix cores, in one pass.  With N = 64
+// a chunk state is P x 64 fp32 (16 KB per head), so state passing between
+// workgroups would move as many bytes as the inputs.  Instead one workgroup
+// owns (row, block of 16 channels) and walks the whole sequence in blocks of
+// 64 steps, carrying its 16 x 64 slice of the state in LDS: the recurrence of
+// channel p involves only state row p, so the channel blocks of a row are
+// independent (they share the B, C and dt reads, which the XCD-aware mapping
+// keeps in one L2).  Per block, with cum_t the inclusive sum of
+// log2(decay) over the block and coef_s the input coefficient:
+//   y_t[p]   = sum_{s<=t} 2^(cum_t-cum_s) coef_s (C_t.B_s) x_s[p]
+//              + 2^cum_t (C_t . H[p,:])                     (+ D[p] x_t[p])
+//   H'[p, n] = 2^cum_63 H[p, n] + sum_s 2^(cum_63-cum_s) coef_s x_s[p] B_s[n]
+// Wave w produces the outputs of steps 16w..16w+15 and state columns
+// 16w..16w+15.  Every decay factor is <= 1, so nothing needs rescaling.
+// Products whose operand is not a raw input (the decay-weighted Gram matrix,
+// the weighted x and the state) split it into bf16 hi + lo parts.
+constexpr int kSqQ = 64;  // steps per block
+constexpr int kSqN = 64;  // state size
+constexpr int kSqP = 16;  // channels per workgroup
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// LDS element offsets: 16-byte column blocks XORed with the row so that the
+// 16 rows read by one operand fetch spread over the banks.
+__device__ inline int sq_tix(int row, int col) {  // [row][64] bf16, col = step or state index
+  return row * 64 + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
+}
+__device__ inline int sq_hix(int p, int n) {  // [16][64] fp32 state slice
+  return p * 64 + ((((n >> 2) ^ p) & 15) << 2) + (n & 3);
+}
+
+__device__ inline void split_bf16x4(const float* v, s16x4_t& hi, s16x4_t& lo) {
+  const uint32_t h0 = pk_bf16(v[0], v[1]), h1 = pk_bf16(v[2], v[3]);
+  const uint32_t l0 = pk_bf16(v[0] - bf16_lo(h0), v[1] - bf16_hi(h0));
+  const uint32_t l1 = pk_bf16(v[2] - bf16_lo(h1), v[3] - bf16_hi(h1));
+  hi = __builtin_bit_cast(s16x4_t, make_uint2(h0, h1));
+  lo = __builtin_bit_cast(s16x4_t, make_uint2(l0, l1));
+}
+
+template <int DISC, bool HAS_D>
+__global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
+  __shared__ __align__(16) uint16_t xT[kSqP * kSqQ];   // x^T [p][s]
+  __shared__ __align__(16) uint16_t Bn[kSqQ * kSqN];   // B [s][n]
+  __shared__ __align__(16) uint16_t BT[kSqN * kSqQ];   // B^T [n][s]
+  __shared__ __align__(16) float sH[2][kSqP * kSqN];   // state slice, ping-pong
+  __shared__ __align__(16) float s_cum[kSqQ], s_coef[kSqQ], s_w[kSqQ];
+  __shared__ float s_dec;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, c16 = lane & 15;
+  uint32_t row, pb;
+  if (a.rows % 8 == 0) {  // the channel blocks of a row on one XCD, dispatched together
+    const uint32_t j = blockIdx.x >> 3;
+    pb = j % npb;
+    row = (j / npb) * 8 + (blockIdx.x & 7);
+  } else {
+    row = blockIdx.x / npb;
+    pb = blockIdx.x - row * npb;
+  }
+  const uint32_t b = row / a.H, h = row - b * a.H;
+  const int p0 = (int)pb * kSqP;
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h + p0;
+  const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
+  const uint16_t* Cb = reinterpret_cast<const uint16_t*>(a.C) + b * a.sC_b + h * a.sC_h;
+  const float* dtb = a.dt + b * a.sdt_b + h * a.sdt_h;
+  uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + b * a.sy_b + h * a.sy_h + p0;
+  const int64_t PN = (int64_t)a.P * kSqN;
+  for (int k = tid; k < kSqP * kSqN; k += 256) {
+    const int p = k >> 6, n = k & 63;
+    sH[0][sq_hix(p, n)] = a.h0 ? a.h0[row * PN + (int64_t)(p0 + p) * kSqN + n] : 0.0f;
+  }
+  // global loads of one block (rows at or past L read row L-1; their
+  // coefficient is 0 and their outputs are not stored)
+  const int64_t last = a.L - 1;
+  uint2 xr;
+  u32x4 br0, br1, cr0, cr1;
+  float dl = 0.0f;
+  auto load = [&](int64_t t0) {
+    {
+      int64_t t = t0 + (tid >> 2);
+      t = t < last ? t : last;
+      xr = *reinterpret_cast<const uint2*>(xb + t * a.sx_l + 4 * (tid & 3));
+    }
+    {
+      int64_t t = t0 + 2 * (tid >> 3);
+      const int64_t t1 = t + 1 < last ? t + 1 : last;
+      t = t < last ? t : last;
+      br0 = *reinterpret_cast<const u32x4*>(Bb + t * a.sB_l + 8 * (tid & 7));
+      br1 = *reinterpret_cast<const u32x4*>(Bb + t1 * a.sB_l + 8 * (tid & 7));
+    }
+    {
+      int64_t t = t0 + 16 * w + c16;
+      t = t < last ? t : last;
+      cr0 = *reinterpret_cast<const u32x4*>(Cb + t * a.sC_l + 8 * q);
+      cr1 = *reinterpret_cast<const u32x4*>(Cb + t * a.sC_l + 8 * q + 32);
+    }
+    if (w == 0) {
+      const int64_t t = t0 + lane;
+      dl = dtb[(t < last ? t : last) * a.sdt_l];
+    }
+  };
+  const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
+  load(0);
+  int cur = 0;
+  const int tl = 16 * w + c16;  // this lane's step within the block (outputs)
+  for (int64_t blk = 0; blk < nblk; ++blk) {
+    const int64_t t0 = blk * kSqQ;
+    __syncthreads();  // the previous block's LDS reads are done
+    {
+      const int s = tid >> 2, pq = tid & 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wd = j < 2 ? xr.x : xr.y;
+        xT[sq_tix(4 * pq + j, s)] = (uint16_t)((j & 1) ? wd >> 16 : wd & 0xffffu);
+      }
+    }
+    {
+      const int s = 2 * (tid >> 3), ng = tid & 7;
+      *reinterpret_cast<u32x4*>(Bn + sq_tix(s, 8 * ng)) = br0;
+      *reinterpret_cast<u32x4*>(Bn + sq_tix(s + 1, 8 * ng)) = br1;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const int k = e >> 1;
+        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e, s)) = perm_lo(br0[k], br1[k]);
+        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e + 1, s)) = perm_hi(br0[k], br1[k]);
+      }
+    }
+    const u32x4 c0 = cr0, c1 = cr1;
+    if (w == 0) {
+      float l2, coef;
+      mfma_step_scalars<DISC>(a, h, t0, lane, dl, &l2, &coef);
+      float cum = l2;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(cum, o);
+        cum += lane >= o ? u : 0.0f;
+      }
+      const float tot = __shfl(cum, 63);
+      s_cum[lane] = cum;
+      s_coef[lane] = coef;
+      s_w[lane] = exp2_fast(tot - cum) * coef;
+      if (lane == 0) s_dec = exp2_fast(tot);
+    }
+    if (blk + 1 < nblk) load(t0 + kSqQ);
+    __syncthreads();
+
+    const float* Hc = sH[cur];
+    float* Hn = sH[cur ^ 1];
+    const float cum_t = s_cum[tl];
+    // decay-weighted Gram block by block (s-blocks up to the wave's own) and
+    // its product with x: acc1[p][t]
+    f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sb = 0; sb <= w; ++sb) {
+      const int sr = 16 * sb + c16;
+      const bf16x8_t g0 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_tix(sr, 8 * q)));
+      const bf16x8_t g1 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_tix(sr, 8 * q + 32)));
+      f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
+      g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g0, as_bf16x8(c0), g, 0, 0, 0);
+      g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g1, as_bf16x8(c1), g, 0, 0, 0);
+      const float4 cs = *reinterpret_cast<const float4*>(s_cum + 16 * sb + 4 * q);
+      const float4 cf = *reinterpret_cast<const float4*>(s_coef + 16 * sb + 4 * q);
+      const float csv[4] = {cs.x, cs.y, cs.z, cs.w}, cfv[4] = {cf.x, cf.y, cf.z, cf.w};
+      float m[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int s = 16 * sb + 4 * q + v;
+        m[v] = s <= tl ? g[v] * exp2_fast(cum_t - csv[v]) * cfv[v] : 0.0f;
+      }
+      s16x4_t mh, ml;
+      split_bf16x4(m, mh, ml);
+      const s16x4_t ax =
+          __builtin_bit_cast(s16x4_t, *reinterpret_cast<const uint2*>(xT + sq_tix(c16, 16 * sb + 4 * q)));
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, mh, acc1, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, ml, acc1, 0, 0, 0);
+    }
+    // carried state: acc2[p][t] = H[p,:] . C_t
+    f32x4 acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const float4 h0v = *reinterpret_cast<const float4*>(Hc + sq_hix(c16, 8 * q + 32 * ks));
+      const float4 h1v = *reinterpret_cast<const float4*>(Hc + sq_hix(c16, 8 * q + 32 * ks + 4));
+      const float hv[8] = {h0v.x, h0v.y, h0v.z, h0v.w, h1v.x, h1v.y, h1v.z, h1v.w};
+      bf16x8_t hh, hl;
+      split_bf16(hv, hh, hl);
+      const bf16x8_t cb = as_bf16x8(ks == 0 ? c0 : c1);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hh, cb, acc2, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hl, cb, acc2, 0, 0, 0);
+    }
+    // outputs y[t0 + tl][p0 + 4q .. 4q+3]
+    {
+      const float u_t = exp2_fast(cum_t);
+      float yv[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        yv[v] = __builtin_fmaf(u_t, acc2[v], acc1[v]);
+        if constexpr (HAS_D) {
+          const float xv = bf16_bits_to_f32(xT[sq_tix(4 * q + v, tl)]);
+          yv[v] = __builtin_fmaf(a.D[h * a.P + p0 + 4 * q + v], xv, yv[v]);
+        }
+      }
+      const int64_t t = t0 + tl;
+      if (t < a.L)
+        *reinterpret_cast<uint2*>(yb + t * a.sy_l + 4 * q) =
+            make_uint2(pk_bf16(yv[0], yv[1]), pk_bf16(yv[2], yv[3]));
+    }
+    // state columns 16w..16w+15: H' = 2^cum_63 H + (x w)^T B
+    {
+      const float dec = s_dec;
+      const int n = 16 * w + c16;
+      f32x4 st;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) st[v] = dec * Hc[sq_hix(4 * q + v, n)];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int s0 = 8 * q + 32 * ks;
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + sq_tix(c16, s0));
+        const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
+        const float4 w1 = *reinterpret_cast<const float4*>(s_w + s0 + 4);
+        const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
+                            bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
+                            bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
+        bf16x8_t fh, fl;
+        split_bf16(f, fh, fl);
+        const bf16x8_t bt = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + sq_tix(n, s0)));
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt, st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt, st, 0, 0, 0);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) Hn[sq_hix(4 * q + v, n)] = st[v];
+    }
+    cur ^= 1;
+  }
+  if (a.h_last) {
+    __syncthreads();
+    for (int k = tid; k < kSqP * kSqN; k += 256) {
+      const int p = k >> 6, n = k & 63;
+      a.h_last[row * PN + (int64_t)(p0 + p) * kSqN + n] = sH[cur][sq_hix(p, n)];
+    }
+  }
+}
+
+template <int DISC>
+int launch_ssd_seq(bool has_d, int64_t rows, int64_t P, hipStream_t s, const SsdArgs& a) {
+  const uint32_t npb = (uint32_t)(P / kSqP);
+  const dim3 grid((unsigned)(rows * npb));
+  if (has_d) hipLaunchKernelGGL((ssd_seq_kernel<DISC, true>), grid, dim3(256), 0, s, a, npb);
+  else hipLaunchKernelGGL((ssd_seq_kernel<DISC, false>), grid, dim3(256), 0, s, a, npb);
+  return launch_status();
+}
+
 inline int64_t cdiv64(int64_t x, int64_t y) { return (x + y - 1) / y; }
 
 template <typename T, int DISC, int N, bool HAS_D>
@@ -970,6 +1219,14 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
     return disc == TSSM_DISC_ZOH ? launch_ssd_mfma<TSSM_DISC_ZOH>(has_d, rows, nchunks, PN, s, a)
                                  : launch_ssd_mfma<TSSM_DISC_EULER>(has_d, rows, nchunks, PN, s, a);
   }
+  // bf16 at N = 64 with 16-channel blocks: one matrix-core pass per channel block
+  if (dtype == TSSM_BF16 && N == kSqN && P % kSqP == 0 && aligned(x, 8) && aligned(B, 16) &&
+      aligned(C, 16) && aligned(y, 8) && sx_l % 4 == 0 && sx_h % 4 == 0 && sx_b % 4 == 0 &&
+      sB_l % 8 == 0 && sB_h % 8 == 0 && sB_b % 8 == 0 && sC_l % 8 == 0 && sC_h % 8 == 0 &&
+      sC_b % 8 == 0 && sy_l % 4 == 0 && sy_h % 4 == 0 && sy_b % 4 == 0 &&
+      rows * (P / kSqP) < (int64_t)INT32_MAX)
+    return disc == TSSM_DISC_ZOH ? launch_ssd_seq<TSSM_DISC_ZOH>(has_d, rows, P, s, a)
+                                 : launch_ssd_seq<TSSM_DISC_EULER>(has_d, rows, P, s, a);
   switch (dtype) {
     case TSSM_BF16: return launch_ssd_t<bf16_t>(disc, has_d, (int)N, rows, nchunks, PN, s, a);
     case TSSM_F16: return launch_ssd_t<f16_t>(disc, has_d, (int)N, rows, nchunks, PN, s, a);
