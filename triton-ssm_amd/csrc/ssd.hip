@@ -869,28 +869,34 @@ int launch_ssd_mfma(bool has_d, int64_t rows, int64_t nchunks, int64_t PN, hipSt
 // a chunk state is P x 64 fp32 (16 KB per head), so state passing between
 // workgroups would move as many bytes as the inputs.  Instead one workgroup
 // owns (row, block of 16 channels) and walks the whole sequence in blocks of
-// 64 steps, carrying its 16 x 64 slice of the state in LDS: the recurrence of
+// steps, carrying its 16 x 64 slice of the state in LDS: the recurrence of
 // channel p involves only state row p, so the channel blocks of a row are
 // independent (they share the B, C and dt reads, which the XCD-aware mapping
 // keeps in one L2).  Per block, with cum_t the inclusive sum of
 // log2(decay) over the block and coef_s the input coefficient:
 //   y_t[p]   = sum_{s<=t} 2^(cum_t-cum_s) coef_s (C_t.B_s) x_s[p]
 //              + 2^cum_t (C_t . H[p,:])                     (+ D[p] x_t[p])
-//   H'[p, n] = 2^cum_63 H[p, n] + sum_s 2^(cum_63-cum_s) coef_s x_s[p] B_s[n]
-// Wave w produces the outputs of steps 16w..16w+15 and state columns
-// 16w..16w+15.  Every decay factor is <= 1, so nothing needs rescaling.
-// Products whose operand is not a raw input (the decay-weighted Gram matrix,
-// the weighted x and the state) split it into bf16 hi + lo parts.
-constexpr int kSqQ = 64;  // steps per block
-constexpr int kSqN = 64;  // state size
-constexpr int kSqP = 16;  // channels per workgroup
+//   H'[p, n] = 2^cum_e H[p, n] + sum_s 2^(cum_e-cum_s) coef_s x_s[p] B_s[n]
+// (cum_e: the sum over the whole block).
+// Blocks of 128 steps: wave w produces the outputs of the 16-step groups w and
+// 7 - w (9 Gram blocks of the lower triangle each, two independent product
+// chains) and state columns 16w..16w+15.  Every decay factor is <= 1, so
+// nothing needs rescaling.  Products whose operand is not a raw input (the
+// decay-weighted Gram matrix, the weighted x and the state) split it into
+// bf16 hi + lo parts.
+constexpr int kSqQ = 128;  // steps per block
+constexpr int kSqN = 64;   // state size
+constexpr int kSqP = 16;   // channels per workgroup
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 // LDS element offsets: 16-byte column blocks XORed with the row so that the
 // 16 rows read by one operand fetch spread over the banks.
-__device__ inline int sq_tix(int row, int col) {  // [row][64] bf16, col = step or state index
-  return row * 64 + ((((col >> 3) ^ row) & 7) << 3) + (col & 7);
+__device__ inline int sq_tix(int row, int col) {  // [row][128] bf16, col = step
+  return row * 128 + ((((col >> 3) ^ row ^ (row >> 3)) & 15) << 3) + (col & 7);
+}
+__device__ inline int sq_bix(int s, int n) {  // [s][64] bf16
+  return s * 64 + ((((n >> 3) ^ s) & 7) << 3) + (n & 7);
 }
 __device__ inline int sq_hix(int p, int n) {  // [16][64] fp32 state slice
   return p * 64 + ((((n >> 2) ^ p) & 15) << 2) + (n & 3);
@@ -904,15 +910,97 @@ __device__ inline void split_bf16x4(const float* v, s16x4_t& hi, s16x4_t& lo) {
   lo = __builtin_bit_cast(s16x4_t, make_uint2(l0, l1));
 }
 
+// One Gram block (steps 16sb.. of B against the lane's output step t of group
+// tb), masked and decay-weighted, then its product with x into acc[p][t].
+// Factored form (FAC): the weight of step s is v_s = 2^(ref - cum_s) coef_s and
+// the caller scales the sum by u_t = 2^(cum_t - ref); exact form: each
+// element takes 2^(cum_t - cum_s) coef_s.  DIAG: the block holds the diagonal
+// (mask s <= t).
+template <bool FAC, bool DIAG>
+__device__ inline void sq_gram_mx(const uint16_t* Bn, const uint16_t* xT, const float* s_cum,
+                                  const float* s_coef, const float* s_v, int sb, int t,
+                                  float cum_t, u32x4 c0, u32x4 c1, int q, int c16, f32x4& acc) {
+  const int sr = 16 * sb + c16;
+  const bf16x8_t g0 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_bix(sr, 8 * q)));
+  const bf16x8_t g1 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_bix(sr, 8 * q + 32)));
+  f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
+  g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g0, as_bf16x8(c0), g, 0, 0, 0);
+  g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g1, as_bf16x8(c1), g, 0, 0, 0);
+  float m[4];
+  if constexpr (FAC) {
+    const float4 vv = *reinterpret_cast<const float4*>(s_v + 16 * sb + 4 * q);
+    const float vs[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) m[v] = g[v] * vs[v];
+  } else {
+    const float4 cs = *reinterpret_cast<const float4*>(s_cum + 16 * sb + 4 * q);
+    const float4 cf = *reinterpret_cast<const float4*>(s_coef + 16 * sb + 4 * q);
+    const float csv[4] = {cs.x, cs.y, cs.z, cs.w}, cfv[4] = {cf.x, cf.y, cf.z, cf.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) m[v] = g[v] * exp2_fast(cum_t - csv[v]) * cfv[v];
+  }
+  if constexpr (DIAG) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) m[v] = 16 * sb + 4 * q + v <= t ? m[v] : 0.0f;
+  }
+  s16x4_t mh, ml;
+  split_bf16x4(m, mh, ml);
+  const s16x4_t ax =
+      __builtin_bit_cast(s16x4_t, *reinterpret_cast<const uint2*>(xT + sq_tix(c16, 16 * sb + 4 * q)));
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, mh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, ml, acc, 0, 0, 0);
+}
+
+// Both output groups of a wave: Gram blocks 0..tA (group A) and 0..tB.
+template <bool FAC>
+__device__ inline void sq_groups(const uint16_t* Bn, const uint16_t* xT, const float* s_cum,
+                                 const float* s_coef, const float* s_v, int tA, int tB, int sA,
+                                 int sB, float cum_a, float cum_b, u32x4 a0, u32x4 a1, u32x4 b0,
+                                 u32x4 b1, int q, int c16, f32x4& accA, f32x4& accB) {
+  for (int sb = 0; sb < tA; ++sb) {
+    sq_gram_mx<FAC, false>(Bn, xT, s_cum, s_coef, s_v, sb, sA, cum_a, a0, a1, q, c16, accA);
+    sq_gram_mx<FAC, false>(Bn, xT, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, accB);
+  }
+  sq_gram_mx<FAC, true>(Bn, xT, s_cum, s_coef, s_v, tA, sA, cum_a, a0, a1, q, c16, accA);
+  for (int sb = tA; sb < tB; ++sb)
+    sq_gram_mx<FAC, false>(Bn, xT, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, accB);
+  sq_gram_mx<FAC, true>(Bn, xT, s_cum, s_coef, s_v, tB, sB, cum_b, b0, b1, q, c16, accB);
+}
+
+// Carried state H[p,:] . C_t into acc[p][t]; the state slice is kept in LDS
+// as bf16 hi and lo parts ([p][n], like B) next to its fp32 values.
+__device__ inline void sq_state_c(const uint16_t* Hh, const uint16_t* Hl, u32x4 c0, u32x4 c1,
+                                  int q, int c16, f32x4& acc) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const bf16x8_t hh = as_bf16x8(*reinterpret_cast<const u32x4*>(Hh + sq_bix(c16, 8 * q + 32 * ks)));
+    const bf16x8_t hl = as_bf16x8(*reinterpret_cast<const u32x4*>(Hl + sq_bix(c16, 8 * q + 32 * ks)));
+    const bf16x8_t cb = as_bf16x8(ks == 0 ? c0 : c1);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hh, cb, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hl, cb, acc, 0, 0, 0);
+  }
+}
+
+// Store one state value: fp32, bf16 hi and bf16 lo.
+__device__ inline void sq_put_state(float* Hf, uint16_t* Hh, uint16_t* Hl, int p, int n, float v) {
+  const uint32_t hi = pk_bf16(v, 0.0f);
+  Hf[sq_hix(p, n)] = v;
+  Hh[sq_bix(p, n)] = (uint16_t)hi;
+  Hl[sq_bix(p, n)] = (uint16_t)pk_bf16(v - bf16_lo(hi), 0.0f);
+}
+
 template <int DISC, bool HAS_D>
-__global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
   __shared__ __align__(16) uint16_t xT[kSqP * kSqQ];   // x^T [p][s]
   __shared__ __align__(16) uint16_t Bn[kSqQ * kSqN];   // B [s][n]
   __shared__ __align__(16) uint16_t BT[kSqN * kSqQ];   // B^T [n][s]
   __shared__ __align__(16) float sH[2][kSqP * kSqN];   // state slice, ping-pong
-  __shared__ __align__(16) float s_cum[kSqQ], s_coef[kSqQ], s_w[kSqQ];
-  __shared__ float s_dec;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, q = lane >> 4, c16 = lane & 15;
+  __shared__ __align__(16) uint16_t sHh[2][kSqP * kSqN], sHl[2][kSqP * kSqN];  // its bf16 parts
+  __shared__ __align__(16) float s_cum[kSqQ], s_coef[kSqQ], s_w[kSqQ], s_u[kSqQ], s_v[kSqQ];
+  __shared__ float s_dec, s_eref;
+  __shared__ int s_fac;
+  const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, c16 = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint32_t row, pb;
   if (a.rows % 8 == 0) {  // the channel blocks of a row on one XCD, dispatched together
     const uint32_t j = blockIdx.x >> 3;
@@ -932,143 +1020,138 @@ __global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
   const int64_t PN = (int64_t)a.P * kSqN;
   for (int k = tid; k < kSqP * kSqN; k += 256) {
     const int p = k >> 6, n = k & 63;
-    sH[0][sq_hix(p, n)] = a.h0 ? a.h0[row * PN + (int64_t)(p0 + p) * kSqN + n] : 0.0f;
+    sq_put_state(sH[0], sHh[0], sHl[0], p, n,
+                 a.h0 ? a.h0[row * PN + (int64_t)(p0 + p) * kSqN + n] : 0.0f);
   }
+  // output groups of this wave and their steps
+  const int tA = w, tB = 7 - w;
+  const int sA = 16 * tA + c16, sB = 16 * tB + c16;
   // global loads of one block (rows at or past L read row L-1; their
   // coefficient is 0 and their outputs are not stored)
   const int64_t last = a.L - 1;
-  uint2 xr;
-  u32x4 br0, br1, cr0, cr1;
-  float dl = 0.0f;
+  auto clampt = [&](int64_t t) { return t < last ? t : last; };
+  uint2 xr[2];
+  u32x4 br[4], cA0, cA1, cB0, cB1;
+  float dl0 = 0.0f, dl1 = 0.0f;
   auto load = [&](int64_t t0) {
-    {
-      int64_t t = t0 + (tid >> 2);
-      t = t < last ? t : last;
-      xr = *reinterpret_cast<const uint2*>(xb + t * a.sx_l + 4 * (tid & 3));
+#pragma unroll
+    for (int k = 0; k < 2; ++k)  // steps 2 (tid >> 2) + k, channels 4 (tid & 3) ..
+      xr[k] = *reinterpret_cast<const uint2*>(xb + clampt(t0 + 2 * (tid >> 2) + k) * a.sx_l +
+                                              4 * (tid & 3));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // steps 2 (tid >> 3) + {0, 1} + 64 (k >> 1)
+      const int64_t t = t0 + 64 * (k >> 1) + 2 * (tid >> 3) + (k & 1);
+      br[k] = *reinterpret_cast<const u32x4*>(Bb + clampt(t) * a.sB_l + 8 * (tid & 7));
     }
-    {
-      int64_t t = t0 + 2 * (tid >> 3);
-      const int64_t t1 = t + 1 < last ? t + 1 : last;
-      t = t < last ? t : last;
-      br0 = *reinterpret_cast<const u32x4*>(Bb + t * a.sB_l + 8 * (tid & 7));
-      br1 = *reinterpret_cast<const u32x4*>(Bb + t1 * a.sB_l + 8 * (tid & 7));
-    }
-    {
-      int64_t t = t0 + 16 * w + c16;
-      t = t < last ? t : last;
-      cr0 = *reinterpret_cast<const u32x4*>(Cb + t * a.sC_l + 8 * q);
-      cr1 = *reinterpret_cast<const u32x4*>(Cb + t * a.sC_l + 8 * q + 32);
-    }
+    const int64_t ta = clampt(t0 + sA), tb = clampt(t0 + sB);
+    cA0 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q);
+    cA1 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q + 32);
+    cB0 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q);
+    cB1 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q + 32);
     if (w == 0) {
-      const int64_t t = t0 + lane;
-      dl = dtb[(t < last ? t : last) * a.sdt_l];
+      dl0 = dtb[clampt(t0 + 2 * lane) * a.sdt_l];
+      dl1 = dtb[clampt(t0 + 2 * lane + 1) * a.sdt_l];
     }
   };
   const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
   load(0);
   int cur = 0;
-  const int tl = 16 * w + c16;  // this lane's step within the block (outputs)
   for (int64_t blk = 0; blk < nblk; ++blk) {
     const int64_t t0 = blk * kSqQ;
     __syncthreads();  // the previous block's LDS reads are done
     {
-      const int s = tid >> 2, pq = tid & 3;
+      const int s = 2 * (tid >> 2), pq = tid & 3;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t wd = j < 2 ? xr.x : xr.y;
-        xT[sq_tix(4 * pq + j, s)] = (uint16_t)((j & 1) ? wd >> 16 : wd & 0xffffu);
+      for (int j = 0; j < 4; j += 2) {
+        const uint32_t w0 = j == 0 ? xr[0].x : xr[0].y, w1 = j == 0 ? xr[1].x : xr[1].y;
+        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * pq + j, s)) = perm_lo(w0, w1);
+        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * pq + j + 1, s)) = perm_hi(w0, w1);
       }
     }
-    {
-      const int s = 2 * (tid >> 3), ng = tid & 7;
-      *reinterpret_cast<u32x4*>(Bn + sq_tix(s, 8 * ng)) = br0;
-      *reinterpret_cast<u32x4*>(Bn + sq_tix(s + 1, 8 * ng)) = br1;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int s = 64 * hf + 2 * (tid >> 3), ng = tid & 7;
+      const u32x4 b0 = br[2 * hf], b1 = br[2 * hf + 1];
+      *reinterpret_cast<u32x4*>(Bn + sq_bix(s, 8 * ng)) = b0;
+      *reinterpret_cast<u32x4*>(Bn + sq_bix(s + 1, 8 * ng)) = b1;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         const int k = e >> 1;
-        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e, s)) = perm_lo(br0[k], br1[k]);
-        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e + 1, s)) = perm_hi(br0[k], br1[k]);
+        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e, s)) = perm_lo(b0[k], b1[k]);
+        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e + 1, s)) = perm_hi(b0[k], b1[k]);
       }
     }
-    const u32x4 c0 = cr0, c1 = cr1;
-    if (w == 0) {
-      float l2, coef;
-      mfma_step_scalars<DISC>(a, h, t0, lane, dl, &l2, &coef);
-      float cum = l2;
+    const u32x4 a0 = cA0, a1 = cA1, b0 = cB0, b1 = cB1;
+    if (w == 0) {  // lane: steps 2 lane, 2 lane + 1
+      float l2a, ca, l2b, cb;
+      mfma_step_scalars<DISC>(a, h, t0, 2 * lane, dl0, &l2a, &ca);
+      mfma_step_scalars<DISC>(a, h, t0, 2 * lane + 1, dl1, &l2b, &cb);
+      float cum = l2a + l2b;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const float u = __shfl_up(cum, o);
         cum += lane >= o ? u : 0.0f;
       }
       const float tot = __shfl(cum, 63);
-      s_cum[lane] = cum;
-      s_coef[lane] = coef;
-      s_w[lane] = exp2_fast(tot - cum) * coef;
-      if (lane == 0) s_dec = exp2_fast(tot);
+      const float cum_a = cum - l2b;
+      // factored decay about the block's mid-value: every factor stays within
+      // 2^+-120 while the block decays by at most 2^-240
+      const float ref = 0.5f * tot;
+      *reinterpret_cast<float2*>(s_cum + 2 * lane) = make_float2(cum_a, cum);
+      *reinterpret_cast<float2*>(s_coef + 2 * lane) = make_float2(ca, cb);
+      *reinterpret_cast<float2*>(s_w + 2 * lane) =
+          make_float2(exp2_fast(tot - cum_a) * ca, exp2_fast(tot - cum) * cb);
+      *reinterpret_cast<float2*>(s_u + 2 * lane) =
+          make_float2(exp2_fast(cum_a - ref), exp2_fast(cum - ref));
+      *reinterpret_cast<float2*>(s_v + 2 * lane) =
+          make_float2(exp2_fast(ref - cum_a) * ca, exp2_fast(ref - cum) * cb);
+      if (lane == 0) {
+        s_dec = exp2_fast(tot);
+        s_eref = exp2_fast(ref);
+        s_fac = tot >= -240.0f;
+      }
     }
     if (blk + 1 < nblk) load(t0 + kSqQ);
     __syncthreads();
 
     const float* Hc = sH[cur];
-    float* Hn = sH[cur ^ 1];
-    const float cum_t = s_cum[tl];
-    // decay-weighted Gram block by block (s-blocks up to the wave's own) and
-    // its product with x: acc1[p][t]
-    f32x4 acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int sb = 0; sb <= w; ++sb) {
-      const int sr = 16 * sb + c16;
-      const bf16x8_t g0 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_tix(sr, 8 * q)));
-      const bf16x8_t g1 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_tix(sr, 8 * q + 32)));
-      f32x4 g = {0.0f, 0.0f, 0.0f, 0.0f};
-      g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g0, as_bf16x8(c0), g, 0, 0, 0);
-      g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g1, as_bf16x8(c1), g, 0, 0, 0);
-      const float4 cs = *reinterpret_cast<const float4*>(s_cum + 16 * sb + 4 * q);
-      const float4 cf = *reinterpret_cast<const float4*>(s_coef + 16 * sb + 4 * q);
-      const float csv[4] = {cs.x, cs.y, cs.z, cs.w}, cfv[4] = {cf.x, cf.y, cf.z, cf.w};
-      float m[4];
+    const float cum_a = s_cum[sA], cum_b = s_cum[sB];
+    const bool fac = __builtin_amdgcn_readfirstlane(s_fac) != 0;
+    // decay-weighted Gram blocks and their products with x, both groups
+    f32x4 accA = {0.0f, 0.0f, 0.0f, 0.0f}, accB = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (fac)
+      sq_groups<true>(Bn, xT, s_cum, s_coef, s_v, tA, tB, sA, sB, cum_a, cum_b, a0, a1, b0, b1,
+                      q, c16, accA, accB);
+    else
+      sq_groups<false>(Bn, xT, s_cum, s_coef, s_v, tA, tB, sA, sB, cum_a, cum_b, a0, a1, b0, b1,
+                       q, c16, accA, accB);
+    f32x4 zA = {0.0f, 0.0f, 0.0f, 0.0f}, zB = {0.0f, 0.0f, 0.0f, 0.0f};
+    sq_state_c(sHh[cur], sHl[cur], a0, a1, q, c16, zA);
+    sq_state_c(sHh[cur], sHl[cur], b0, b1, q, c16, zB);
+    // outputs y[t0 + s][p0 + 4q .. 4q+3] of both groups:
+    //   factored: y = u_t (acc + 2^ref z);  exact: y = acc + 2^cum_t z
+    const float eref = s_eref;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int s = 16 * sb + 4 * q + v;
-        m[v] = s <= tl ? g[v] * exp2_fast(cum_t - csv[v]) * cfv[v] : 0.0f;
-      }
-      s16x4_t mh, ml;
-      split_bf16x4(m, mh, ml);
-      const s16x4_t ax =
-          __builtin_bit_cast(s16x4_t, *reinterpret_cast<const uint2*>(xT + sq_tix(c16, 16 * sb + 4 * q)));
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, mh, acc1, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, ml, acc1, 0, 0, 0);
-    }
-    // carried state: acc2[p][t] = H[p,:] . C_t
-    f32x4 acc2 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const float4 h0v = *reinterpret_cast<const float4*>(Hc + sq_hix(c16, 8 * q + 32 * ks));
-      const float4 h1v = *reinterpret_cast<const float4*>(Hc + sq_hix(c16, 8 * q + 32 * ks + 4));
-      const float hv[8] = {h0v.x, h0v.y, h0v.z, h0v.w, h1v.x, h1v.y, h1v.z, h1v.w};
-      bf16x8_t hh, hl;
-      split_bf16(hv, hh, hl);
-      const bf16x8_t cb = as_bf16x8(ks == 0 ? c0 : c1);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hh, cb, acc2, 0, 0, 0);
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hl, cb, acc2, 0, 0, 0);
-    }
-    // outputs y[t0 + tl][p0 + 4q .. 4q+3]
-    {
-      const float u_t = exp2_fast(cum_t);
+    for (int g = 0; g < 2; ++g) {
+      const int s = g == 0 ? sA : sB;
+      const float u_t = fac ? s_u[s] : 1.0f;
+      const float zs = fac ? eref : exp2_fast(g == 0 ? cum_a : cum_b);
+      const f32x4 acc = g == 0 ? accA : accB, z = g == 0 ? zA : zB;
       float yv[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        yv[v] = __builtin_fmaf(u_t, acc2[v], acc1[v]);
+        yv[v] = u_t * __builtin_fmaf(zs, z[v], acc[v]);
         if constexpr (HAS_D) {
-          const float xv = bf16_bits_to_f32(xT[sq_tix(4 * q + v, tl)]);
+          const float xv = bf16_bits_to_f32(xT[sq_tix(4 * q + v, s)]);
           yv[v] = __builtin_fmaf(a.D[h * a.P + p0 + 4 * q + v], xv, yv[v]);
         }
       }
-      const int64_t t = t0 + tl;
+      const int64_t t = t0 + s;
       if (t < a.L)
         *reinterpret_cast<uint2*>(yb + t * a.sy_l + 4 * q) =
             make_uint2(pk_bf16(yv[0], yv[1]), pk_bf16(yv[2], yv[3]));
     }
-    // state columns 16w..16w+15: H' = 2^cum_63 H + (x w)^T B
+    // state columns 16w..16w+15: H' = 2^cum_e H + (x w)^T B
     {
       const float dec = s_dec;
       const int n = 16 * w + c16;
@@ -1076,7 +1159,7 @@ __global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) st[v] = dec * Hc[sq_hix(4 * q + v, n)];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < kSqQ / 32; ++ks) {
         const int s0 = 8 * q + 32 * ks;
         const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + sq_tix(c16, s0));
         const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
@@ -1091,7 +1174,7 @@ __global__ __launch_bounds__(256) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
         st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt, st, 0, 0, 0);
       }
 #pragma unroll
-      for (int v = 0; v < 4; ++v) Hn[sq_hix(4 * q + v, n)] = st[v];
+      for (int v = 0; v < 4; ++v) sq_put_state(sH[cur ^ 1], sHh[cur ^ 1], sHl[cur ^ 1], 4 * q + v, n, st[v]);
     }
     cur ^= 1;
   }
@@ -1220,8 +1303,8 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
                                  : launch_ssd_mfma<TSSM_DISC_EULER>(has_d, rows, nchunks, PN, s, a);
   }
   // bf16 at N = 64 with 16-channel blocks: one matrix-core pass per channel block
-  if (dtype == TSSM_BF16 && N == kSqN && P % kSqP == 0 && aligned(x, 8) && aligned(B, 16) &&
-      aligned(C, 16) && aligned(y, 8) && sx_l % 4 == 0 && sx_h % 4 == 0 && sx_b % 4 == 0 &&
+  if (dtype == TSSM_BF16 && N == kSqN && P % kSqP == 0 && aligned(x, 16) && aligned(B, 16) &&
+      aligned(C, 16) && aligned(y, 8) && sx_l % 8 == 0 && sx_h % 8 == 0 && sx_b % 8 == 0 &&
       sB_l % 8 == 0 && sB_h % 8 == 0 && sB_b % 8 == 0 && sC_l % 8 == 0 && sC_h % 8 == 0 &&
       sC_b % 8 == 0 && sy_l % 4 == 0 && sy_h % 4 == 0 && sy_b % 4 == 0 &&
       rows * (P / kSqP) < (int64_t)INT32_MAX)
