@@ -910,16 +910,16 @@ __device__ inline void split_bf16x4(const float* v, s16x4_t& hi, s16x4_t& lo) {
   lo = __builtin_bit_cast(s16x4_t, make_uint2(l0, l1));
 }
 
-// One Gram block (steps 16sb.. of B against the lane's output step t of group
-// tb), masked and decay-weighted, then its product with x into acc[p][t].
-// Factored form (FAC): the weight of step s is v_s = 2^(ref - cum_s) coef_s and
-// the caller scales the sum by u_t = 2^(cum_t - ref); exact form: each
-// element takes 2^(cum_t - cum_s) coef_s.  DIAG: the block holds the diagonal
-// (mask s <= t).
+// One Gram block: steps 16sb.. of B against the lane's output step t,
+// masked (DIAG: the block holds the diagonal, s <= t) and decay-weighted, as
+// the bf16 hi/lo parts of the B operand of the product with x.  Factored form
+// (FAC): the weight of step s is v_s = 2^(ref - cum_s) coef_s and the caller
+// scales the sum by u_t = 2^(cum_t - ref); exact form: each element takes
+// 2^(cum_t - cum_s) coef_s.
 template <bool FAC, bool DIAG>
-__device__ inline void sq_gram_mx(const uint16_t* Bn, const uint16_t* xT, const float* s_cum,
-                                  const float* s_coef, const float* s_v, int sb, int t,
-                                  float cum_t, u32x4 c0, u32x4 c1, int q, int c16, f32x4& acc) {
+__device__ inline void sq_gram_m(const uint16_t* Bn, const float* s_cum, const float* s_coef,
+                                 const float* s_v, int sb, int t, float cum_t, u32x4 c0, u32x4 c1,
+                                 int q, int c16, s16x4_t& mh, s16x4_t& ml) {
   const int sr = 16 * sb + c16;
   const bf16x8_t g0 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_bix(sr, 8 * q)));
   const bf16x8_t g1 = as_bf16x8(*reinterpret_cast<const u32x4*>(Bn + sq_bix(sr, 8 * q + 32)));
@@ -943,38 +943,53 @@ __device__ inline void sq_gram_mx(const uint16_t* Bn, const uint16_t* xT, const 
 #pragma unroll
     for (int v = 0; v < 4; ++v) m[v] = 16 * sb + 4 * q + v <= t ? m[v] : 0.0f;
   }
-  s16x4_t mh, ml;
   split_bf16x4(m, mh, ml);
-  const s16x4_t ax =
-      __builtin_bit_cast(s16x4_t, *reinterpret_cast<const uint2*>(xT + sq_tix(c16, 16 * sb + 4 * q)));
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, mh, acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, ml, acc, 0, 0, 0);
+}
+
+// acc[k][p][t] += x^T[16k + p][16sb..] . (weighted block), channel blocks k < PB.
+template <int PB>
+__device__ inline void sq_mx(const uint16_t* xT, int sb, int q, int c16, s16x4_t mh, s16x4_t ml,
+                             f32x4* acc) {
+#pragma unroll
+  for (int k = 0; k < PB; ++k) {
+    const s16x4_t ax = __builtin_bit_cast(
+        s16x4_t, *reinterpret_cast<const uint2*>(xT + sq_tix(16 * k + c16, 16 * sb + 4 * q)));
+    acc[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, mh, acc[k], 0, 0, 0);
+    acc[k] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ax, ml, acc[k], 0, 0, 0);
+  }
 }
 
 // Both output groups of a wave: Gram blocks 0..tA (group A) and 0..tB.
-template <bool FAC>
+template <bool FAC, int PB>
 __device__ inline void sq_groups(const uint16_t* Bn, const uint16_t* xT, const float* s_cum,
                                  const float* s_coef, const float* s_v, int tA, int tB, int sA,
                                  int sB, float cum_a, float cum_b, u32x4 a0, u32x4 a1, u32x4 b0,
-                                 u32x4 b1, int q, int c16, f32x4& accA, f32x4& accB) {
+                                 u32x4 b1, int q, int c16, f32x4* accA, f32x4* accB) {
+  s16x4_t mh, ml;
   for (int sb = 0; sb < tA; ++sb) {
-    sq_gram_mx<FAC, false>(Bn, xT, s_cum, s_coef, s_v, sb, sA, cum_a, a0, a1, q, c16, accA);
-    sq_gram_mx<FAC, false>(Bn, xT, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, accB);
+    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, sA, cum_a, a0, a1, q, c16, mh, ml);
+    sq_mx<PB>(xT, sb, q, c16, mh, ml, accA);
+    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, mh, ml);
+    sq_mx<PB>(xT, sb, q, c16, mh, ml, accB);
   }
-  sq_gram_mx<FAC, true>(Bn, xT, s_cum, s_coef, s_v, tA, sA, cum_a, a0, a1, q, c16, accA);
-  for (int sb = tA; sb < tB; ++sb)
-    sq_gram_mx<FAC, false>(Bn, xT, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, accB);
-  sq_gram_mx<FAC, true>(Bn, xT, s_cum, s_coef, s_v, tB, sB, cum_b, b0, b1, q, c16, accB);
+  sq_gram_m<FAC, true>(Bn, s_cum, s_coef, s_v, tA, sA, cum_a, a0, a1, q, c16, mh, ml);
+  sq_mx<PB>(xT, tA, q, c16, mh, ml, accA);
+  for (int sb = tA; sb < tB; ++sb) {
+    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, mh, ml);
+    sq_mx<PB>(xT, sb, q, c16, mh, ml, accB);
+  }
+  sq_gram_m<FAC, true>(Bn, s_cum, s_coef, s_v, tB, sB, cum_b, b0, b1, q, c16, mh, ml);
+  sq_mx<PB>(xT, tB, q, c16, mh, ml, accB);
 }
 
 // Carried state H[p,:] . C_t into acc[p][t]; the state slice is kept in LDS
 // as bf16 hi and lo parts ([p][n], like B) next to its fp32 values.
-__device__ inline void sq_state_c(const uint16_t* Hh, const uint16_t* Hl, u32x4 c0, u32x4 c1,
-                                  int q, int c16, f32x4& acc) {
+__device__ inline void sq_state_c(const uint16_t* Hh, const uint16_t* Hl, int p, u32x4 c0,
+                                  u32x4 c1, int q, f32x4& acc) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const bf16x8_t hh = as_bf16x8(*reinterpret_cast<const u32x4*>(Hh + sq_bix(c16, 8 * q + 32 * ks)));
-    const bf16x8_t hl = as_bf16x8(*reinterpret_cast<const u32x4*>(Hl + sq_bix(c16, 8 * q + 32 * ks)));
+    const bf16x8_t hh = as_bf16x8(*reinterpret_cast<const u32x4*>(Hh + sq_bix(p, 8 * q + 32 * ks)));
+    const bf16x8_t hl = as_bf16x8(*reinterpret_cast<const u32x4*>(Hl + sq_bix(p, 8 * q + 32 * ks)));
     const bf16x8_t cb = as_bf16x8(ks == 0 ? c0 : c1);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hh, cb, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hl, cb, acc, 0, 0, 0);
@@ -989,18 +1004,25 @@ __device__ inline void sq_put_state(float* Hf, uint16_t* Hh, uint16_t* Hl, int p
   Hl[sq_bix(p, n)] = (uint16_t)pk_bf16(v - bf16_lo(hi), 0.0f);
 }
 
-template <int DISC, bool HAS_D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
-  __shared__ __align__(16) uint16_t xT[kSqP * kSqQ];   // x^T [p][s]
+// 8 waves: waves 0-3 form the weighted Gram blocks of their output groups
+// once and apply them to every channel block of the workgroup (PB blocks of
+// 16), then the carried-state term and the outputs; waves 4-7 update state
+// columns 16(w-4).. for every channel block.  Both read the state entering the
+// block; the updated state goes to the other buffer.
+template <int DISC, bool HAS_D, int PB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
+  constexpr int CP = kSqP * PB;  // channels per workgroup
+  __shared__ __align__(16) uint16_t xT[CP * kSqQ];     // x^T [p][s]
   __shared__ __align__(16) uint16_t Bn[kSqQ * kSqN];   // B [s][n]
   __shared__ __align__(16) uint16_t BT[kSqN * kSqQ];   // B^T [n][s]
-  __shared__ __align__(16) float sH[2][kSqP * kSqN];   // state slice, ping-pong
-  __shared__ __align__(16) uint16_t sHh[2][kSqP * kSqN], sHl[2][kSqP * kSqN];  // its bf16 parts
+  __shared__ __align__(16) float sH[2][CP * kSqN];     // state slice, ping-pong
+  __shared__ __align__(16) uint16_t sHh[2][CP * kSqN], sHl[2][CP * kSqN];  // its bf16 parts
   __shared__ __align__(16) float s_cum[kSqQ], s_coef[kSqQ], s_w[kSqQ], s_u[kSqQ], s_v[kSqQ];
   __shared__ float s_dec, s_eref;
   __shared__ int s_fac;
   const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, c16 = lane & 15;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wv & 3;
   uint32_t row, pb;
   if (a.rows % 8 == 0) {  // the channel blocks of a row on one XCD, dispatched together
     const uint32_t j = blockIdx.x >> 3;
@@ -1011,44 +1033,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     pb = blockIdx.x - row * npb;
   }
   const uint32_t b = row / a.H, h = row - b * a.H;
-  const int p0 = (int)pb * kSqP;
+  const int p0 = (int)pb * CP;
   const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h + p0;
   const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
   const uint16_t* Cb = reinterpret_cast<const uint16_t*>(a.C) + b * a.sC_b + h * a.sC_h;
   const float* dtb = a.dt + b * a.sdt_b + h * a.sdt_h;
   uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + b * a.sy_b + h * a.sy_h + p0;
   const int64_t PN = (int64_t)a.P * kSqN;
-  for (int k = tid; k < kSqP * kSqN; k += 256) {
+  for (int k = tid; k < CP * kSqN; k += 512) {
     const int p = k >> 6, n = k & 63;
     sq_put_state(sH[0], sHh[0], sHl[0], p, n,
                  a.h0 ? a.h0[row * PN + (int64_t)(p0 + p) * kSqN + n] : 0.0f);
   }
-  // output groups of this wave and their steps
+  // output groups of an output wave and their steps
   const int tA = w, tB = 7 - w;
   const int sA = 16 * tA + c16, sB = 16 * tB + c16;
   // global loads of one block (rows at or past L read row L-1; their
   // coefficient is 0 and their outputs are not stored)
   const int64_t last = a.L - 1;
   auto clampt = [&](int64_t t) { return t < last ? t : last; };
-  uint2 xr[2];
-  u32x4 br[4], cA0, cA1, cB0, cB1;
+  constexpr int kXq = CP / 4;             // channel quads
+  const bool x_item = tid < 64 * kXq;     // (step pair, channel quad) items
+  const int x_sp = tid / kXq, x_pq = tid % kXq;
+  uint2 xr[2] = {};
+  u32x4 br[2], cA0 = {}, cA1 = {}, cB0 = {}, cB1 = {};
   float dl0 = 0.0f, dl1 = 0.0f;
   auto load = [&](int64_t t0) {
+    if (x_item) {
 #pragma unroll
-    for (int k = 0; k < 2; ++k)  // steps 2 (tid >> 2) + k, channels 4 (tid & 3) ..
-      xr[k] = *reinterpret_cast<const uint2*>(xb + clampt(t0 + 2 * (tid >> 2) + k) * a.sx_l +
-                                              4 * (tid & 3));
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {  // steps 2 (tid >> 3) + {0, 1} + 64 (k >> 1)
-      const int64_t t = t0 + 64 * (k >> 1) + 2 * (tid >> 3) + (k & 1);
-      br[k] = *reinterpret_cast<const u32x4*>(Bb + clampt(t) * a.sB_l + 8 * (tid & 7));
+      for (int k = 0; k < 2; ++k)
+        xr[k] = *reinterpret_cast<const uint2*>(xb + clampt(t0 + 2 * x_sp + k) * a.sx_l + 4 * x_pq);
     }
-    const int64_t ta = clampt(t0 + sA), tb = clampt(t0 + sB);
-    cA0 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q);
-    cA1 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q + 32);
-    cB0 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q);
-    cB1 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q + 32);
-    if (w == 0) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)  // steps 2 (tid >> 3) + k, state columns 8 (tid & 7) ..
+      br[k] = *reinterpret_cast<const u32x4*>(Bb + clampt(t0 + 2 * (tid >> 3) + k) * a.sB_l +
+                                              8 * (tid & 7));
+    if (wv < 4) {
+      const int64_t ta = clampt(t0 + sA), tb = clampt(t0 + sB);
+      cA0 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q);
+      cA1 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q + 32);
+      cB0 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q);
+      cB1 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q + 32);
+    } else if (wv == 4) {
       dl0 = dtb[clampt(t0 + 2 * lane) * a.sdt_l];
       dl1 = dtb[clampt(t0 + 2 * lane + 1) * a.sdt_l];
     }
@@ -1059,19 +1085,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
   for (int64_t blk = 0; blk < nblk; ++blk) {
     const int64_t t0 = blk * kSqQ;
     __syncthreads();  // the previous block's LDS reads are done
-    {
-      const int s = 2 * (tid >> 2), pq = tid & 3;
+    if (x_item) {
+      const int s = 2 * x_sp;
 #pragma unroll
       for (int j = 0; j < 4; j += 2) {
         const uint32_t w0 = j == 0 ? xr[0].x : xr[0].y, w1 = j == 0 ? xr[1].x : xr[1].y;
-        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * pq + j, s)) = perm_lo(w0, w1);
-        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * pq + j + 1, s)) = perm_hi(w0, w1);
+        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * x_pq + j, s)) = perm_lo(w0, w1);
+        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * x_pq + j + 1, s)) = perm_hi(w0, w1);
       }
     }
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int s = 64 * hf + 2 * (tid >> 3), ng = tid & 7;
-      const u32x4 b0 = br[2 * hf], b1 = br[2 * hf + 1];
+    {
+      const int s = 2 * (tid >> 3), ng = tid & 7;
+      const u32x4 b0 = br[0], b1 = br[1];
       *reinterpret_cast<u32x4*>(Bn + sq_bix(s, 8 * ng)) = b0;
       *reinterpret_cast<u32x4*>(Bn + sq_bix(s + 1, 8 * ng)) = b1;
 #pragma unroll
@@ -1082,7 +1107,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
       }
     }
     const u32x4 a0 = cA0, a1 = cA1, b0 = cB0, b1 = cB1;
-    if (w == 0) {  // lane: steps 2 lane, 2 lane + 1
+    if (wv == 4) {  // lane: steps 2 lane, 2 lane + 1
       float l2a, ca, l2b, cb;
       mfma_step_scalars<DISC>(a, h, t0, 2 * lane, dl0, &l2a, &ca);
       mfma_step_scalars<DISC>(a, h, t0, 2 * lane + 1, dl1, &l2b, &cb);
@@ -1114,86 +1139,113 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void s
     if (blk + 1 < nblk) load(t0 + kSqQ);
     __syncthreads();
 
-    const float* Hc = sH[cur];
-    const float cum_a = s_cum[sA], cum_b = s_cum[sB];
-    const bool fac = __builtin_amdgcn_readfirstlane(s_fac) != 0;
-    // decay-weighted Gram blocks and their products with x, both groups
-    f32x4 accA = {0.0f, 0.0f, 0.0f, 0.0f}, accB = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (fac)
-      sq_groups<true>(Bn, xT, s_cum, s_coef, s_v, tA, tB, sA, sB, cum_a, cum_b, a0, a1, b0, b1,
-                      q, c16, accA, accB);
-    else
-      sq_groups<false>(Bn, xT, s_cum, s_coef, s_v, tA, tB, sA, sB, cum_a, cum_b, a0, a1, b0, b1,
-                       q, c16, accA, accB);
-    f32x4 zA = {0.0f, 0.0f, 0.0f, 0.0f}, zB = {0.0f, 0.0f, 0.0f, 0.0f};
-    sq_state_c(sHh[cur], sHl[cur], a0, a1, q, c16, zA);
-    sq_state_c(sHh[cur], sHl[cur], b0, b1, q, c16, zB);
-    // outputs y[t0 + s][p0 + 4q .. 4q+3] of both groups:
-    //   factored: y = u_t (acc + 2^ref z);  exact: y = acc + 2^cum_t z
-    const float eref = s_eref;
+    if (wv < 4) {
+      const float cum_a = s_cum[sA], cum_b = s_cum[sB];
+      const bool fac = __builtin_amdgcn_readfirstlane(s_fac) != 0;
+      // decay-weighted Gram blocks and their products with x, both groups
+      f32x4 accA[PB], accB[PB], zA[PB], zB[PB];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int s = g == 0 ? sA : sB;
-      const float u_t = fac ? s_u[s] : 1.0f;
-      const float zs = fac ? eref : exp2_fast(g == 0 ? cum_a : cum_b);
-      const f32x4 acc = g == 0 ? accA : accB, z = g == 0 ? zA : zB;
-      float yv[4];
+      for (int k = 0; k < PB; ++k) accA[k] = accB[k] = zA[k] = zB[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (fac)
+        sq_groups<true, PB>(Bn, xT, s_cum, s_coef, s_v, tA, tB, sA, sB, cum_a, cum_b, a0, a1, b0,
+                            b1, q, c16, accA, accB);
+      else
+        sq_groups<false, PB>(Bn, xT, s_cum, s_coef, s_v, tA, tB, sA, sB, cum_a, cum_b, a0, a1, b0,
+                             b1, q, c16, accA, accB);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        yv[v] = u_t * __builtin_fmaf(zs, z[v], acc[v]);
-        if constexpr (HAS_D) {
-          const float xv = bf16_bits_to_f32(xT[sq_tix(4 * q + v, s)]);
-          yv[v] = __builtin_fmaf(a.D[h * a.P + p0 + 4 * q + v], xv, yv[v]);
+      for (int k = 0; k < PB; ++k) {
+        sq_state_c(sHh[cur], sHl[cur], 16 * k + c16, a0, a1, q, zA[k]);
+        sq_state_c(sHh[cur], sHl[cur], 16 * k + c16, b0, b1, q, zB[k]);
+      }
+      // outputs y[t0 + s][p0 + 16k + 4q .. +3]:
+      //   factored: y = u_t (acc + 2^ref z);  exact: y = acc + 2^cum_t z
+      const float eref = s_eref;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int s = g == 0 ? sA : sB;
+        const float u_t = fac ? s_u[s] : 1.0f;
+        const float zs = fac ? eref : exp2_fast(g == 0 ? cum_a : cum_b);
+        const int64_t t = t0 + s;
+#pragma unroll
+        for (int k = 0; k < PB; ++k) {
+          const f32x4 acc = g == 0 ? accA[k] : accB[k], z = g == 0 ? zA[k] : zB[k];
+          float yv[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            yv[v] = u_t * __builtin_fmaf(zs, z[v], acc[v]);
+            if constexpr (HAS_D) {
+              const float xv = bf16_bits_to_f32(xT[sq_tix(16 * k + 4 * q + v, s)]);
+              yv[v] = __builtin_fmaf(a.D[h * a.P + p0 + 16 * k + 4 * q + v], xv, yv[v]);
+            }
+          }
+          if (t < a.L)
+            *reinterpret_cast<uint2*>(yb + t * a.sy_l + 16 * k + 4 * q) =
+                make_uint2(pk_bf16(yv[0], yv[1]), pk_bf16(yv[2], yv[3]));
         }
       }
-      const int64_t t = t0 + s;
-      if (t < a.L)
-        *reinterpret_cast<uint2*>(yb + t * a.sy_l + 4 * q) =
-            make_uint2(pk_bf16(yv[0], yv[1]), pk_bf16(yv[2], yv[3]));
-    }
-    // state columns 16w..16w+15: H' = 2^cum_e H + (x w)^T B
-    {
+    } else {
+      // state columns 16w..16w+15 of every channel block: H' = 2^cum_e H + (x w)^T B
       const float dec = s_dec;
       const int n = 16 * w + c16;
-      f32x4 st;
+      const float* Hc = sH[cur];
+      f32x4 st[PB];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) st[v] = dec * Hc[sq_hix(4 * q + v, n)];
+      for (int k = 0; k < PB; ++k)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) st[k][v] = dec * Hc[sq_hix(16 * k + 4 * q + v, n)];
 #pragma unroll
       for (int ks = 0; ks < kSqQ / 32; ++ks) {
         const int s0 = 8 * q + 32 * ks;
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + sq_tix(c16, s0));
+        const bf16x8_t bt = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + sq_tix(n, s0)));
         const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
         const float4 w1 = *reinterpret_cast<const float4*>(s_w + s0 + 4);
-        const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
-                            bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
-                            bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
-        bf16x8_t fh, fl;
-        split_bf16(f, fh, fl);
-        const bf16x8_t bt = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + sq_tix(n, s0)));
-        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt, st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt, st, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < PB; ++k) {
+          const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + sq_tix(16 * k + c16, s0));
+          const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
+                              bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
+                              bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
+          bf16x8_t fh, fl;
+          split_bf16(f, fh, fl);
+          st[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt, st[k], 0, 0, 0);
+          st[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt, st[k], 0, 0, 0);
+        }
       }
 #pragma unroll
-      for (int v = 0; v < 4; ++v) sq_put_state(sH[cur ^ 1], sHh[cur ^ 1], sHl[cur ^ 1], 4 * q + v, n, st[v]);
+      for (int k = 0; k < PB; ++k)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          sq_put_state(sH[cur ^ 1], sHh[cur ^ 1], sHl[cur ^ 1], 16 * k + 4 * q + v, n, st[k][v]);
     }
     cur ^= 1;
   }
   if (a.h_last) {
     __syncthreads();
-    for (int k = tid; k < kSqP * kSqN; k += 256) {
+    for (int k = tid; k < CP * kSqN; k += 512) {
       const int p = k >> 6, n = k & 63;
       a.h_last[row * PN + (int64_t)(p0 + p) * kSqN + n] = sH[cur][sq_hix(p, n)];
     }
   }
 }
 
+template <int DISC, bool HAS_D>
+int launch_ssd_seq_d(int64_t rows, int64_t P, hipStream_t s, const SsdArgs& a) {
+  if (P % 32 == 0) {
+    const uint32_t npb = (uint32_t)(P / 32);
+    hipLaunchKernelGGL((ssd_seq_kernel<DISC, HAS_D, 2>), dim3((unsigned)(rows * npb)), dim3(512), 0,
+                       s, a, npb);
+  } else {
+    const uint32_t npb = (uint32_t)(P / 16);
+    hipLaunchKernelGGL((ssd_seq_kernel<DISC, HAS_D, 1>), dim3((unsigned)(rows * npb)), dim3(512), 0,
+                       s, a, npb);
+  }
+  return launch_status();
+}
+
 template <int DISC>
 int launch_ssd_seq(bool has_d, int64_t rows, int64_t P, hipStream_t s, const SsdArgs& a) {
-  const uint32_t npb = (uint32_t)(P / kSqP);
-  const dim3 grid((unsigned)(rows * npb));
-  if (has_d) hipLaunchKernelGGL((ssd_seq_kernel<DISC, true>), grid, dim3(256), 0, s, a, npb);
-  else hipLaunchKernelGGL((ssd_seq_kernel<DISC, false>), grid, dim3(256), 0, s, a, npb);
-  return launch_status();
+  return has_d ? launch_ssd_seq_d<DISC, true>(rows, P, s, a)
+               : launch_ssd_seq_d<DISC, false>(rows, P, s, a);
 }
 
 inline int64_t cdiv64(int64_t x, int64_t y) { return (x + y - 1) / y; }
