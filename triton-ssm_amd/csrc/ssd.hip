@@ -959,27 +959,57 @@ __device__ inline void sq_mx(const uint16_t* xT, int sb, int q, int c16, s16x4_t
   }
 }
 
+// Two weighted blocks (steps 16sb.. and 16sb+16..) in one K = 32 product:
+// the contraction order is free, so lane l's 8 k-values are its 4 steps of
+// each block, and the x operand is read in the same order.
+template <int PB>
+__device__ inline void sq_mx2(const uint16_t* xT, int sb, int q, int c16, s16x4_t mh, s16x4_t ml,
+                              s16x4_t mh2, s16x4_t ml2, f32x4* acc) {
+  const bf16x8_t bh = __builtin_bit_cast(
+      bf16x8_t, u32x4{__builtin_bit_cast(uint2, mh).x, __builtin_bit_cast(uint2, mh).y,
+                      __builtin_bit_cast(uint2, mh2).x, __builtin_bit_cast(uint2, mh2).y});
+  const bf16x8_t bl = __builtin_bit_cast(
+      bf16x8_t, u32x4{__builtin_bit_cast(uint2, ml).x, __builtin_bit_cast(uint2, ml).y,
+                      __builtin_bit_cast(uint2, ml2).x, __builtin_bit_cast(uint2, ml2).y});
+#pragma unroll
+  for (int k = 0; k < PB; ++k) {
+    const uint2 x0 = *reinterpret_cast<const uint2*>(xT + sq_tix(16 * k + c16, 16 * sb + 4 * q));
+    const uint2 x1 = *reinterpret_cast<const uint2*>(xT + sq_tix(16 * k + c16, 16 * sb + 16 + 4 * q));
+    const bf16x8_t ax = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
+    acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bh, acc[k], 0, 0, 0);
+    acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bl, acc[k], 0, 0, 0);
+  }
+}
+
+// The Gram blocks 0..tg of one output group: off-diagonal blocks two at a
+// time (one K = 32 product per pair), then the diagonal block.
+template <bool FAC, int PB>
+__device__ inline void sq_group(const uint16_t* Bn, const uint16_t* xT, const float* s_cum,
+                                const float* s_coef, const float* s_v, int tg, int st, float cum_t,
+                                u32x4 c0, u32x4 c1, int q, int c16, f32x4* acc) {
+  s16x4_t mh, ml, mh2, ml2;
+  int sb = 0;
+  for (; sb + 1 < tg; sb += 2) {
+    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, st, cum_t, c0, c1, q, c16, mh, ml);
+    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb + 1, st, cum_t, c0, c1, q, c16, mh2, ml2);
+    sq_mx2<PB>(xT, sb, q, c16, mh, ml, mh2, ml2, acc);
+  }
+  if (sb < tg) {
+    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, st, cum_t, c0, c1, q, c16, mh, ml);
+    sq_mx<PB>(xT, sb, q, c16, mh, ml, acc);
+  }
+  sq_gram_m<FAC, true>(Bn, s_cum, s_coef, s_v, tg, st, cum_t, c0, c1, q, c16, mh, ml);
+  sq_mx<PB>(xT, tg, q, c16, mh, ml, acc);
+}
+
 // Both output groups of a wave: Gram blocks 0..tA (group A) and 0..tB.
 template <bool FAC, int PB>
 __device__ inline void sq_groups(const uint16_t* Bn, const uint16_t* xT, const float* s_cum,
                                  const float* s_coef, const float* s_v, int tA, int tB, int sA,
                                  int sB, float cum_a, float cum_b, u32x4 a0, u32x4 a1, u32x4 b0,
                                  u32x4 b1, int q, int c16, f32x4* accA, f32x4* accB) {
-  s16x4_t mh, ml;
-  for (int sb = 0; sb < tA; ++sb) {
-    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, sA, cum_a, a0, a1, q, c16, mh, ml);
-    sq_mx<PB>(xT, sb, q, c16, mh, ml, accA);
-    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, mh, ml);
-    sq_mx<PB>(xT, sb, q, c16, mh, ml, accB);
-  }
-  sq_gram_m<FAC, true>(Bn, s_cum, s_coef, s_v, tA, sA, cum_a, a0, a1, q, c16, mh, ml);
-  sq_mx<PB>(xT, tA, q, c16, mh, ml, accA);
-  for (int sb = tA; sb < tB; ++sb) {
-    sq_gram_m<FAC, false>(Bn, s_cum, s_coef, s_v, sb, sB, cum_b, b0, b1, q, c16, mh, ml);
-    sq_mx<PB>(xT, sb, q, c16, mh, ml, accB);
-  }
-  sq_gram_m<FAC, true>(Bn, s_cum, s_coef, s_v, tB, sB, cum_b, b0, b1, q, c16, mh, ml);
-  sq_mx<PB>(xT, tB, q, c16, mh, ml, accB);
+  sq_group<FAC, PB>(Bn, xT, s_cum, s_coef, s_v, tA, sA, cum_a, a0, a1, q, c16, accA);
+  sq_group<FAC, PB>(Bn, xT, s_cum, s_coef, s_v, tB, sB, cum_b, b0, b1, q, c16, accB);
 }
 
 // Carried state H[p,:] . C_t into acc[p][t]; the state slice is kept in LDS
