@@ -316,17 +316,31 @@ def rows_sweep(args, dev):
             fn()
         torch.cuda.synchronize()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(int(1e8))
-        t0.record(stream)
-        for _ in range(reps):
-            fn()
-        t1.record(stream)
-        torch.cuda.synchronize()
-        us = t0.elapsed_time(t1) / reps * 1e3
+        # best of three trials: a host stall (the launches are enqueued behind a
+        # ~40 ms GPU sleep, which hides host time only up to that long) spoils
+        # one trial, not all three
+        best = None
+        for _ in range(3):
+            torch.cuda._sleep(int(1e8))
+            t0.record(stream)
+            h0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            host_ms = (time.perf_counter() - h0) * 1e3
+            t1.record(stream)
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) / reps * 1e3
+            if best is None or us < best[0]:
+                best = (us, host_ms)
+        us, host_ms = best
+        host_us = host_ms / reps * 1e3
         gbps = nbytes / (us * 1e-6) / 1e9
         rows.append({"row": name, "shape": shape, "us": round(us, 2), "bytes": int(nbytes),
-                     "gbps": round(gbps, 1), "frac": round(gbps / 8000.0, 4)})
-        log(f"{name:52s} {shape:34s} {us:9.1f} us {gbps:8.0f} GB/s {100 * gbps / 8000:5.1f}%")
+                     "gbps": round(gbps, 1), "frac": round(gbps / 8000.0, 4),
+                     "host_us": round(host_us, 1)})
+        flag = "  (host-bound)" if host_ms > 30.0 else ""
+        log(f"{name:52s} {shape:34s} {us:9.1f} us {gbps:8.0f} GB/s {100 * gbps / 8000:5.1f}%"
+            f"  host {host_us:7.1f} us{flag}")
 
     B, T, H = 8, 4096, 1024          # lanes of the headline config
     n = B * T * H
