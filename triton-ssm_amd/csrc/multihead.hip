@@ -349,7 +349,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     v = group_sum<NS>(v);
     if (t0 + r < a.L) {
       if constexpr (MODE == MODE_DIAG) store_bcast8<T>(yp + r * a.sy_l, v);
-      else if ((g % NS) == 0) stf(yp + r * a.sy_l, v);
+      else if ((g % NS) == 0) stf_cached(yp + r * a.sy_l, v);  // sparse: combined in L2
     }
   }
 }
@@ -493,7 +493,7 @@ __global__ void mh_output_kernel(const float* __restrict__ loc_a, const float* _
 // head value stored broadcast over the thread's 4 channels.  kOutR steps per
 // thread are loaded before any is reduced.  Same grid and results as
 // mh_output_kernel (the sums reassociate).
-constexpr int kOutR = 4;
+constexpr int kOutR = 8;
 
 template <int LPS>
 __device__ inline float lanes_sum(float v) {
@@ -545,8 +545,14 @@ __global__ __launch_bounds__(256) void mh_output_vec_kernel(
     for (int k = 0; k < kOutR; ++k) {
       const int64_t t = t0 + (k * 4 + wave) * SPW + sl;
       const int64_t tt = t < te ? t : te - 1;  // steps past the block re-read its last step
-      ld_lanes<float, 4>(la + tt * row, a4[k]);
-      ld_lanes<float, 4>(lx + tt * row, x4[k]);
+      // loc_a / loc_x are read exactly once: streaming (nontemporal) loads
+      const f32x4 va = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(la + tt * row));
+      const f32x4 vx = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(lx + tt * row));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a4[k][j] = va[j];
+        x4[k][j] = vx[j];
+      }
       ld_lanes<T, 4>(cb + tt * sC_l, c4[k]);
       ld_lanes<T, 4>(ub + tt * su_l, u4[k]);
     }
