@@ -22,7 +22,6 @@ enum DType : int { F32 = TSSM_F32, BF16 = TSSM_BF16, F16 = TSSM_F16 };
 struct bf16_t { uint16_t bits; };
 using f16_t = _Float16;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __host__ inline float bf16_bits_to_f32(uint32_t b) {
@@ -39,17 +38,10 @@ __device__ inline uint32_t pk_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Stores.  Outputs that the kernel's caller does not read back soon leave as
-// streaming (nontemporal) stores: ordinary stores allocate their lines in the
-// L2 and evict the streaming inputs of the same kernel (measured 16-24% on the
-// elementwise rows).  Outputs read back soon -- state updated in place,
-// per-chunk carries and intermediates of the phase kernels, parameter-gradient
-// accumulators -- use the _cached forms.
 template <typename T> struct Elem;
 template <> struct Elem<float> {
   static __device__ inline float ld(const float* p) { return *p; }
   static __device__ inline void st(float* p, float v) { *p = v; }
-  static __device__ inline void st_nt(float* p, float v) { __builtin_nontemporal_store(v, p); }
 };
 template <> struct Elem<bf16_t> {
   static __device__ inline float ld(const bf16_t* p) {
@@ -58,21 +50,14 @@ template <> struct Elem<bf16_t> {
   static __device__ inline void st(bf16_t* p, float v) {
     reinterpret_cast<uint16_t*>(p)[0] = (uint16_t)f32_to_bf16_bits(v);
   }
-  static __device__ inline void st_nt(bf16_t* p, float v) {
-    __builtin_nontemporal_store((uint16_t)f32_to_bf16_bits(v), reinterpret_cast<uint16_t*>(p));
-  }
 };
 template <> struct Elem<f16_t> {
   static __device__ inline float ld(const f16_t* p) { return (float)*p; }
   static __device__ inline void st(f16_t* p, float v) { *p = (f16_t)v; }
-  static __device__ inline void st_nt(f16_t* p, float v) {
-    __builtin_nontemporal_store(__builtin_bit_cast(uint16_t, (f16_t)v), reinterpret_cast<uint16_t*>(p));
-  }
 };
 
 template <typename T> __device__ inline float ldf(const T* p) { return Elem<T>::ld(p); }
-template <typename T> __device__ inline void stf(T* p, float v) { Elem<T>::st_nt(p, v); }
-template <typename T> __device__ inline void stf_cached(T* p, float v) { Elem<T>::st(p, v); }
+template <typename T> __device__ inline void stf(T* p, float v) { Elem<T>::st(p, v); }
 
 // Runtime-typed scalar load, for small side inputs (masks, timestamps) whose
 // dtype the caller chooses freely.  The switch is wave-uniform.
@@ -226,29 +211,15 @@ __device__ inline void ld_lanes(const T* p, float* v) {
   }
 }
 template <typename T, int V>
-__device__ inline void st_lanes(T* p, const float* v) {  // streaming store
+__device__ inline void st_lanes(T* p, const float* v) {
   if constexpr (V == 1) {
     stf(p, v[0]);
-  } else if constexpr (sizeof(T) == 4) {
-    __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4*>(p));
-  } else {
-    T tmp[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) stf_cached(tmp + j, v[j]);
-    const uint2 w = *reinterpret_cast<const uint2*>(tmp);
-    __builtin_nontemporal_store(u32x2{w.x, w.y}, reinterpret_cast<u32x2*>(p));
-  }
-}
-template <typename T, int V>
-__device__ inline void st_lanes_cached(T* p, const float* v) {
-  if constexpr (V == 1) {
-    stf_cached(p, v[0]);
   } else if constexpr (sizeof(T) == 4) {
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
   } else {
     T tmp[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) stf_cached(tmp + j, v[j]);
+    for (int j = 0; j < 4; ++j) stf(tmp + j, v[j]);
     *reinterpret_cast<uint2*>(p) = *reinterpret_cast<const uint2*>(tmp);
   }
 }

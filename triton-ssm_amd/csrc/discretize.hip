@@ -487,7 +487,7 @@ __global__ __launch_bounds__(256) void dt_project_kernel(
         sp[v] = clamp_med3(softplus_fast(acc[k][v] + bv[v]), dt_min, dt_max);
       TO* op = out + ro_out[k] + h;
       if constexpr (V == 4 && sizeof(TO) == 4) {
-        __builtin_nontemporal_store(f32x4{sp[0], sp[1], sp[2], sp[3]}, reinterpret_cast<f32x4*>(op));
+        *reinterpret_cast<float4*>(op) = make_float4(sp[0], sp[1], sp[2], sp[3]);
       } else {
 #pragma unroll
         for (int v = 0; v < V; ++v) stf(op + v, sp[v]);

@@ -77,16 +77,14 @@ template <typename TV, int E> struct Lanes {
       for (int j = 0; j < 8; ++j) v[j] = q.get(j);
     }
   }
-  // Vhat goes through the caches (not a streaming store): the scan that
-  // follows in the interpolation + scan pipeline reads it back right away.
   __device__ inline void store(TV* p) const {
     if constexpr (E == 1) {
-      stf_cached(p, v[0]);
+      stf(p, v[0]);
     } else if constexpr (sizeof(TV) == 4) {
       *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) stf_cached(p + j, v[j]);
+      for (int j = 0; j < 8; ++j) stf(p + j, v[j]);
     }
   }
 };
@@ -368,7 +366,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_step_kernel(StepArgs a)
       v = ldf(V + next * a.svt + f);
     else
       v = ldf(V + a.t_cur * a.svt + f);
-    stf_cached(O + a.t_cur * a.sot + f, v);
+    stf(O + a.t_cur * a.sot + f, v);
     // h_in is read as 0 where b*stride_hib + f >= B*F (fused_ssm_interp.py:97-98)
     const int64_t lin = b * a.s_hib + f;
     const float hp = lin < a.nb * a.F ? a.h_in[lin] : 0.0f;
@@ -471,7 +469,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_step_fast_kernel(StepAr
   } else {
     v = ldf(V + a.t_cur * a.svt);
   }
-  stf_cached(reinterpret_cast<TV*>(a.Vhat) + b * a.sob + a.t_cur * a.sot + f, v);
+  stf(reinterpret_cast<TV*>(a.Vhat) + b * a.sob + a.t_cur * a.sot + f, v);
   a.h_out[b * a.s_hob + f] = abar * hp + bbar * v;
 }
 
@@ -531,7 +529,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_corrected_kernel(Interp
         v = ldf(V + t * a.svt);
       }
     }
-    stf_cached(O + t * a.sot, v);
+    stf(O + t * a.sot, v);
   }
 }
 

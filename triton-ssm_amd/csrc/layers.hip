@@ -265,8 +265,8 @@ __global__ __launch_bounds__(kThreads) void ln_param_add_kernel(const float* __r
     tw += part2[k * H + h];
     tb += part2[(kSplits + k) * H + h];
   }
-  stf_cached(dw + h, ldf(dw + h) + tw);
-  stf_cached(db + h, ldf(db + h) + tb);
+  stf(dw + h, ldf(dw + h) + tw);
+  stf(db + h, ldf(db + h) + tb);
 }
 
 // dx of a row (fused_ssm_interp.py:148-166) and its (mu, inv) for the
@@ -342,8 +342,8 @@ __global__ __launch_bounds__(kThreads) void ln_param_final_kernel(
     sw += part[k * H + h];
     sb += part[(nblk + k) * H + h];
   }
-  stf_cached(dw + h, ldf(dw + h) + sw);
-  stf_cached(db + h, ldf(db + h) + sb);
+  stf(dw + h, ldf(dw + h) + sw);
+  stf(db + h, ldf(db + h) + sb);
 }
 
 __device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }

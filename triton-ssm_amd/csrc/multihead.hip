@@ -349,7 +349,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     v = group_sum<NS>(v);
     if (t0 + r < a.L) {
       if constexpr (MODE == MODE_DIAG) store_bcast8<T>(yp + r * a.sy_l, v);
-      else if ((g % NS) == 0) stf_cached(yp + r * a.sy_l, v);  // sparse: combined in L2
+      else if ((g % NS) == 0) stf(yp + r * a.sy_l, v);
     }
   }
 }

@@ -43,12 +43,12 @@ __global__ void ssm_fwd_local_kernel(const T* __restrict__ u, const T* __restric
     const float a = ldf(A + off);
     xr = a * xr + ldf(Bm + off) * ldf(u + off);
     ar = a * ar;
-    stf_cached(loc_a + off, ar);
-    stf_cached(loc_x + off, xr);
+    stf(loc_a + off, ar);
+    stf(loc_x + off, xr);
   }
   const int64_t nrows = nb * H;
-  stf_cached(carry + m.rid * nblk + m.blk, ar);
-  stf_cached(carry + nrows * nblk + m.rid * nblk + m.blk, xr);
+  stf(carry + m.rid * nblk + m.blk, ar);
+  stf(carry + nrows * nblk + m.rid * nblk + m.blk, xr);
 }
 
 // ssm_carry_scan_kernel (ssm_scan.py:54-65) and the reverse variant
@@ -92,8 +92,8 @@ __global__ __launch_bounds__(256) void carry_scan_lanes_kernel(T* __restrict__ c
       A = A * Ain;
     }
     if (ok && i > 0) {
-      stf_cached(ca + k, A);
-      stf_cached(cx + k, X);
+      stf(ca + k, A);
+      stf(cx + k, X);
     }
     if (i0 + S < nblk) {  // S == 64 here: the segment's last lane carries on
       Ain = __shfl(A, 63);
@@ -157,12 +157,12 @@ __global__ void ssm_bwd_local_kernel(const T* __restrict__ A, const T* __restric
     const float a1 = (p + 1 < L) ? ldf(A + off + H) : 0.0f;
     xr = a1 * xr + ldf(C + off) * ldf(dY + off);
     ar = a1 * ar;
-    stf_cached(loc_a + off, ar);
-    stf_cached(loc_dh + off, xr);
+    stf(loc_a + off, ar);
+    stf(loc_dh + off, xr);
   }
   const int64_t nrows = nb * H;
-  stf_cached(carry + m.rid * nblk + m.blk, ar);
-  stf_cached(carry + nrows * nblk + m.rid * nblk + m.blk, xr);
+  stf(carry + m.rid * nblk + m.blk, ar);
+  stf(carry + nrows * nblk + m.rid * nblk + m.blk, xr);
 }
 
 // ssm_bwd_apply_kernel, ssm_scan.py:189-231

@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void stream_step_kernel(
       hv[j] = ab[j] * hv[j] + bb[j] * v[j];
       yv[j] = cv[j] * hv[j] + dv[j] * v[j];
     }
-    st_lanes_cached<T, V>(h + b * shb + k, hv);
+    st_lanes<T, V>(h + b * shb + k, hv);
     st_lanes<T, V>(y + b * svb + k, yv);
   }
 }
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_vec_kernel(
         hn[j] = ab[j] * hv[j] + bb[j] * v[j];                            // :152
         yo[j] = cv[j] * hn[j] + dv[j] * v[j];                            // :153,156
       }
-      st_lanes_cached<float, 4>(a.h + b * a.shb + f, hn);
+      st_lanes<float, 4>(a.h + b * a.shb + f, hn);
       st_lanes<float, 4>(a.y + b * a.svb + f, yo);
     }
   }
