@@ -449,11 +449,20 @@ __global__ __launch_bounds__(kThreads) void pool_partial_kernel(
   for (int64_t k = (int64_t)threadIdx.x * V; k < H; k += (int64_t)kThreads * V) {
     float w[V];
     ld_lanes<T, V>(W + k, w);
-    for (int64_t t = t0; t < t1; ++t) {
-      float x[V];
-      ld_lanes<T, V>(h + b * sb + t * st + k, x);
+    // all rows' loads in flight before the (in-order) accumulation; rows past
+    // the block re-read its last row and are not accumulated
+    float x[kPoolRows][V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc = __builtin_fmaf(w[v], x[v], acc);
+    for (int r = 0; r < kPoolRows; ++r) {
+      const int64_t t = t0 + r < t1 ? t0 + r : t1 - 1;
+      ld_lanes<T, V>(h + b * sb + t * st + k, x[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < kPoolRows; ++r) {
+      if (t0 + r < t1) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc = __builtin_fmaf(w[v], x[r][v], acc);
+      }
     }
   }
   acc = wave_sum(acc);
