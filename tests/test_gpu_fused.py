@@ -80,6 +80,22 @@ def test_ssd_scan_n64_matrix_core_path(dev, Bsz, L, H, P, disc, with_d):
     assert_close(hl, h_ref, 1e-3, f"n64 ssd h_last L={L} P={P} {disc}")
 
 
+@pytest.mark.parametrize("cut", [128, 200, 1])
+def test_ssd_scan_n64_split_resume(dev, cut):
+    """bf16 N = 64 on the one-pass matrix-core kernel: a run split at `cut`
+    (the second half starting at an offset view of the same tensors) and
+    resumed from the first half's final state reproduces the whole run."""
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, 2, 700, 4, 64, 64, torch.bfloat16, seed=cut, heavy=True)
+    args = lambda s: (d["x"][:, s], d["dt"][:, s], d["A_log"], d["B"][:, s], d["C"][:, s])  # noqa: E731
+    y, h = ssd_scan_forward(*args(slice(None)), d["D"], return_state=True)
+    _, h1 = ssd_scan_forward(*args(slice(0, cut)), d["D"], return_state=True)
+    y2, h2 = ssd_scan_forward(*args(slice(cut, None)), d["D"], h0=h1, return_state=True)
+    torch.cuda.synchronize()
+    assert_close(y2, y[:, cut:], 4e-3, f"n64 tail via h0, cut {cut}")
+    assert_close(h2, h, 1e-3, f"n64 final state via h0, cut {cut}")
+
+
 def test_ssd_scan_n64_headline_shape(dev):
     """B=8 L=4096 H=16 P=N=64 bf16 (the headline shapes read as SSD), the
     seeded workload of the benchmark: batch 0 and 7, heads 0 and 15 against
