@@ -868,25 +868,26 @@ int launch_ssd_mfma(bool has_d, int64_t rows, int64_t nchunks, int64_t PN, hipSt
 // SSD with N = 64 and bf16 I/O on the matrix cores, in one pass.  With N = 64
 // a chunk state is P x 64 fp32 (16 KB per head), so state passing between
 // workgroups would move as many bytes as the inputs.  Instead one workgroup
-// owns (row, block of 16 channels) and walks the whole sequence in blocks of
-// steps, carrying its 16 x 64 slice of the state in LDS: the recurrence of
-// channel p involves only state row p, so the channel blocks of a row are
-// independent (they share the B, C and dt reads, which the XCD-aware mapping
-// keeps in one L2).  Per block, with cum_t the inclusive sum of
+// owns (row, block of 32 channels -- 16 when P is not a multiple of 32) and
+// walks the whole sequence in blocks of steps, carrying its slice of the
+// state (channels x 64) in LDS: the recurrence of channel p involves only
+// state row p, so the channel blocks of a row are independent (they share the
+// B, C and dt reads, which the XCD-aware mapping keeps in one L2).  Per block,
+// with cum_t the inclusive sum of
 // log2(decay) over the block and coef_s the input coefficient:
 //   y_t[p]   = sum_{s<=t} 2^(cum_t-cum_s) coef_s (C_t.B_s) x_s[p]
 //              + 2^cum_t (C_t . H[p,:])                     (+ D[p] x_t[p])
 //   H'[p, n] = 2^cum_e H[p, n] + sum_s 2^(cum_e-cum_s) coef_s x_s[p] B_s[n]
 // (cum_e: the sum over the whole block).
-// Blocks of 128 steps: wave w produces the outputs of the 16-step groups w and
-// 7 - w (9 Gram blocks of the lower triangle each, two independent product
-// chains) and state columns 16w..16w+15.  Every decay factor is <= 1, so
-// nothing needs rescaling.  Products whose operand is not a raw input (the
+// Blocks of 128 steps: output wave w (0-3) produces the outputs of the 16-step
+// groups w and 7 - w (9 Gram blocks of the lower triangle each) and state wave
+// 4 + w the state columns 16w..16w+15 (the kernel below).  Every decay factor
+// is <= 1, so nothing needs rescaling.  Products whose operand is not a raw input (the
 // decay-weighted Gram matrix, the weighted x and the state) split it into
 // bf16 hi + lo parts.
 constexpr int kSqQ = 128;  // steps per block
 constexpr int kSqN = 64;   // state size
-constexpr int kSqP = 16;   // channels per workgroup
+constexpr int kSqP = 16;   // channels per product tile (a workgroup takes 1 or 2)
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
