@@ -134,7 +134,7 @@ def wl_ssd_config1(args, dev):
     n = B * L * H * P
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
-                kernel="ssd_seq_kernel",
+                kernel="ssd_seq_kernel", traffic="ssd_seq_traffic.json",
                 metric="SSD scan elements/sec on the headline shapes, B=8 L=4096 H=16 P=N=64 bf16",
                 unit="elements/s",
                 config={"workload": "SSD scan (decay per head, P x N state) on the DIAG headline "
