@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_obs_vec_kernel(InterpAr
 // sums reduced over their group (xor shuffles) and the group's first lane
 // writes the flag.  A wave takes kObsP2Rows (row, block) items per batch, all
 // loads issued first; the row's (b, t) advance as wave-uniform counters.
-constexpr int kObsP2Rows = 8;
+constexpr int kObsP2Rows = 4;
 
 template <typename TM, int E>
 __global__ __launch_bounds__(kInterpThreads) void interp_obs_pow2_kernel(InterpArgs a,
