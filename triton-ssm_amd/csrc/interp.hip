@@ -265,7 +265,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
   const int tmax = (int)((a.grid_t - t0) < kInterpTB ? (a.grid_t - t0) : kInterpTB);
   const int ng = (int)((f1 - f0) / E);  // lane groups per step (E divides the tile)
   const int total = tmax * ng;
-  constexpr int U = 4;
+  constexpr int U = 2;  // 27.0 us at the a12 shape cold (U = 4: 27.7, U = 8: 27.0)
   for (int q0 = tid; q0 < total; q0 += U * kInterpThreads) {
     Lanes<TV, E> vp[U], vn[U];
     int64_t ot[U], of[U];
