@@ -141,6 +141,8 @@ namespace tssm {
 
 constexpr int kBwdLanes = 256;   // lanes per workgroup (threads)
 constexpr int kBwdRows = 64;     // rows per workgroup
+static_assert(kBwdRows <= 64, "the final ddt sum takes one thread per row, and a narrow H "
+                              "launches workgroups of only 64 threads");
 
 // psi(x) = (x e^x - expm1(x)) / x^2 = sum_k x^k (k+1)/(k+2)!, the factor of
 // d/da [expm1(dt a)/a] = dt^2 psi(dt a).  Series below |x| < 0.5 (the direct

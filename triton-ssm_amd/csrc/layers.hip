@@ -351,7 +351,7 @@ __device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
 // Row-elementwise launch: workgroup = 256 threads x V lanes h (grid y) over
 // kRowsWG consecutive rows (grid x); the row's offset advances without a
 // division per element.
-constexpr int kRowsWG = 4;
+constexpr int kRowsWG = 2;  // swiglu 69.0 -> 65.4 us cold against 4 rows
 template <int V, typename F>
 __device__ inline void for_rows(const Rows& rows, int64_t nrow, int64_t H, F&& f) {
   const int64_t h = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * V;
