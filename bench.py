@@ -95,7 +95,7 @@ def wl_multihead(args, dev):
            "io_dtype": "bf16", "state_dtype": "f32",
            "a_log": "per channel [H, P]" if args.a_per_channel else "per head [H]"}
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, kernel="mh_scan_fused_kernel",
-                metric=HEADLINE_METRIC, unit="elements/s", config=cfg,
+                dtype="bf16", metric=HEADLINE_METRIC, unit="elements/s", config=cfg,
                 traffic="mh_scan_fused_traffic.json")
 
 
@@ -134,7 +134,7 @@ def wl_ssd_config1(args, dev):
     n = B * L * H * P
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
-                kernel="ssd_seq_kernel", traffic="ssd_seq_traffic.json",
+                kernel="ssd_seq_kernel", traffic="ssd_seq_traffic.json", dtype="bf16",
                 metric="SSD scan elements/sec on the headline shapes, B=8 L=4096 H=16 P=N=64 bf16",
                 unit="elements/s",
                 config={"workload": "SSD scan (decay per head, P x N state) on the DIAG headline "
@@ -251,6 +251,7 @@ def wl_ssd_long(args, dev):
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
                 kernel="ssd_state_mfma_kernel + ssd_pass_kernel + ssd_out_mfma_kernel",
+                dtype="bf16",
                 metric="SSD long-sequence scan elements/sec, B=1 L=262144 H=8 P=64 N=16 bf16",
                 unit="elements/s",
                 config={"workload": "SSD scan (decay per head, P x N state), B=1 L=262144 H=8 "
@@ -628,9 +629,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        # I/O dtype of x/B/C/y; arithmetic and the state are fp32 in every workload
+        "dtype": wl.get("dtype", "f32"),
         "data": "synthetic",
-        "config": dict(wl["config"], parallelism="single GPU"),
+        "config": dict(wl["config"], parallelism="single GPU", arithmetic="f32", state="f32"),
         "roofline": {
             "bound": "hbm",
             "kernel": wl["kernel"],

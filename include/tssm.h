@@ -46,8 +46,12 @@ const char* tssm_strerror(int status);
 
 /* Workspaces of the single-pass (decoupled look-back) scans are caller-owned
  * device buffers, zero-filled ONCE when allocated and then reused by launches
- * on one stream.  Reads the sticky error word (1 = a bounded look-back wait
- * expired) with a synchronous copy; tests only. */
+ * on one stream; nothing else may be written into them (tssm_ssd_scan's
+ * workspace in particular is a separate buffer).  A bounded look-back wait
+ * that expires (~1 s) sets the workspace's sticky error word and the launch
+ * completes with that tile's carry incomplete.  This reads the word
+ * (1 = expired) with a synchronous copy -- call it after the stream has
+ * finished; with clear=1 a set word is reset to 0. */
 int tssm_workspace_error(const void* workspace, int clear, int* error_out);
 
 /* ------------------------------------------------------------------ ZOH
@@ -238,8 +242,9 @@ int tssm_stream_interp_step_corrected(float* ring_V, float* ring_M, float* ring_
  * (the recurrence of ssm_scan.py:5-10 with discretize_kernel.py:44-54's ZOH
  * or multihead_ssm_kernel.py:73's Euler input term).  No reference kernel
  * covers this family; the reference's elementwise kernels can express it only
- * lane by lane.  Single pass with decoupled look-back; workspace rules as for
- * tssm_mh_scan_fused.  x, B, C, y in `dtype` ([B,L,H,P] / [B,L,H,N]); dt f32
+ * lane by lane.  Chunk states pass through the workspace (raw fp32, no
+ * clearing needed); it must NOT be a workspace of the look-back scans, whose
+ * tagged words it would overwrite.  x, B, C, y in `dtype` ([B,L,H,P] / [B,L,H,N]); dt f32
  * [B,L,H]; A_log f32 [H]; D f32 [H*P] or NULL; h0/h_last f32 [B,H,P,N] or
  * NULL.  P <= 64, N in {8, 16, 32, 64}; innermost strides 1. */
 int64_t tssm_ssd_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t H, int64_t P,

@@ -35,9 +35,12 @@ def _oracle(d, disc, h0=None):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("disc", ["euler", "zoh"])
 @pytest.mark.parametrize("per_head", [False, True])
-def test_fused_small(dev, dtype, disc, per_head):
+@pytest.mark.parametrize("with_d", [True, False])
+def test_fused_small(dev, dtype, disc, per_head, with_d):
+    """Every (dtype, discretization, decay layout, skip term) instance of the
+    fused kernel at head_dim 64, ragged length."""
     from tssm import multihead_ssm_forward
-    d = _inputs(dev, 2, 300, 3, 64, dtype, seed=1, per_head=per_head)
+    d = _inputs(dev, 2, 300, 3, 64, dtype, seed=1, per_head=per_head, with_d=with_d)
     y, hl = multihead_ssm_forward(d["u"], d["A_log"], d["B"], d["C"], d["dt"], d["D"],
                                   disc=disc, return_state=True)
     torch.cuda.synchronize()
@@ -137,20 +140,28 @@ def test_fused_forgetting_tiles(dev):
     assert_close(hl, h_ref, TOL[torch.float32], "h_last, mixed forgetting tiles")
 
 
-@pytest.mark.parametrize("disc", ["euler", "zoh"])
-def test_fused_full_headline_shape(dev, disc):
-    """B=8 L=4096 H=16 P=N=64 bf16 x/B/C, fp32 dt and state (the measured workload)."""
-    from tssm import multihead_ssm_forward, workloads, workspace
+@pytest.mark.parametrize("disc", ["zoh", "euler"])
+@pytest.mark.parametrize("a_layout", ["per_head", "per_channel"])
+@pytest.mark.parametrize("with_d", [False, True])
+def test_fused_full_headline_shape(dev, disc, a_layout, with_d):
+    """B=8 L=4096 H=16 P=N=64 bf16 x/B/C, fp32 dt and state.  The instance the
+    benchmark times is a_layout="per_head" (A_log [H]: one decay per head),
+    with_d=False, ZOH; the others are the per-channel A_log [H, P] layout of
+    the reference kernel and the skip term.  Every y of the launch is
+    compared against the float64 oracle."""
+    import tssm
+    from tssm import multihead_ssm_forward, workloads
     w = workloads.multihead()
-    d = {k: w[k].to(dev) for k in ("u", "B", "C", "dt", "A_log")}
-    y = multihead_ssm_forward(d["u"], d["A_log"], d["B"], d["C"], d["dt"], None,
-                              disc=disc, chunk=128)
+    d = {k: w[k].to(dev) for k in ("u", "B", "C", "dt")}
+    A_log = w["A_log_h" if a_layout == "per_head" else "A_log"].to(dev)
+    H, P = w["B"].shape[2], w["B"].shape[3]
+    D = torch.randn(H * P, generator=torch.Generator().manual_seed(5)).to(dev) if with_d else None
+    y = multihead_ssm_forward(d["u"], A_log, d["B"], d["C"], d["dt"], D, disc=disc, chunk=128)
     torch.cuda.synchronize()
-    y_ref, _ = O.multihead_forward(d["u"], d["A_log"], d["B"], d["C"], d["dt"], None, disc=disc)
-    e = assert_close(y, y_ref, 1e-2, f"headline {disc}")
-    print(f"headline {disc} normwise relerr {e:.3e}")
-    ws = workspace.get(dev, torch.cuda.current_stream(dev).cuda_stream, 0)
-    assert workspace.error_flag(ws) == 0
+    tssm.check(dev)
+    y_ref, _ = O.multihead_forward(d["u"], w["A_log"], d["B"], d["C"], d["dt"], D, disc=disc)
+    e = assert_close(y, y_ref, 1e-2, f"headline {disc} {a_layout} D={with_d}")
+    print(f"headline {disc} {a_layout} D={with_d} normwise relerr {e:.3e}")
 
 
 @pytest.mark.parametrize("hd,dtype,BLK,L", [(16, torch.float32, 16, 70),

@@ -10,10 +10,12 @@ interpolation (``corrected``) and the seeded synthetic workloads
 (``workloads``).
 """
 from . import _lib, launch, workspace  # noqa: F401
+from ._lib import TssmError  # noqa: F401
 from .corrected import streaming_interp_step_corrected, time_aware_interp_corrected  # noqa: F401
 from .fused import (fused_interp_ssm_forward, multihead_ssm_forward,  # noqa: F401
                     selective_scan_forward, ssd_scan_forward, ssd_stream_step)
+from .workspace import check  # noqa: F401
 
 __all__ = ["multihead_ssm_forward", "selective_scan_forward", "ssd_scan_forward",
            "ssd_stream_step", "fused_interp_ssm_forward", "time_aware_interp_corrected",
-           "streaming_interp_step_corrected"]
+           "streaming_interp_step_corrected", "check", "TssmError"]

@@ -96,11 +96,11 @@ def multihead_ssm_forward(u, A_log, B, C, dt, D=None, *, chunk=128, disc="euler"
     return (y, h_last) if return_state else y
 
 
-def _ws(nbytes, t, what):
+def _ws(nbytes, t, what, kind=workspace.LOOKBACK):
     if nbytes < 0:
         raise ValueError(f"{what}: unsupported shape for the fused kernel")
     stream = stream_handle(t)
-    return workspace.get(t.device, stream, nbytes), stream
+    return workspace.get(t.device, stream, nbytes, kind), stream
 
 
 def ssd_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=256, disc="zoh", h0=None,
@@ -150,7 +150,8 @@ def ssd_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=256, disc="zoh", h0=No
     _inner_unit(y, "out")
     h_last = torch.empty(Bsz, H, P, N, device=x.device, dtype=torch.float32) if return_state else None
     L_ = _lib.lib()
-    ws, stream = _ws(L_.tssm_ssd_scan_workspace_bytes(Bsz, L, H, P, N, int(chunk)), x, "ssd_scan")
+    ws, stream = _ws(L_.tssm_ssd_scan_workspace_bytes(Bsz, L, H, P, N, int(chunk)), x, "ssd_scan",
+                     workspace.SSD)
     _lib.call("tssm_ssd_scan", code, _disc_code(disc), x.data_ptr(), dt.data_ptr(),
               A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), ptr(h0), y.data_ptr(),
               ptr(h_last), Bsz, L, H, P, N, *x.stride()[:3], *dt.stride(), *B.stride()[:3],
@@ -162,16 +163,34 @@ def ssd_stream_step(x, dt, A_log, B, C, D, state, *, disc="zoh", out=None):
     """One streaming SSD step, the state updated in place in HBM.
 
     x [S, H, P], dt [S] (one per stream) or [S, H], A_log [H], B/C [S, H, N],
-    D [H, P] / [H*P] or None, state [S, H, P, N]; all float32.  Returns y [S, H, P].
+    D [H, P] / [H*P] or None, state [S, H, P, N], out [S, H, P] or None; all
+    float32.  Returns y [S, H, P].  Shapes and dtypes are checked before the
+    devices, and everything before the launch.
     """
-    for t, w in ((x, "x"), (dt, "dt"), (A_log, "A_log"), (B, "B"), (C, "C"), (state, "state")):
-        need_gpu(t, w)
+    named = [(x, "x"), (dt, "dt"), (A_log, "A_log"), (B, "B"), (C, "C"), (state, "state")]
+    if D is not None:
+        named.append((D, "D"))
+    if out is not None:
+        named.append((out, "out"))
+    for t, w in named:
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{w}: expected a torch.Tensor, got {type(t).__name__}")
         if t.dtype != torch.float32:
             raise TypeError(f"{w} must be float32")
+    if x.dim() != 3:
+        raise ValueError("x must be [S, H, P]")
     S, H, P = x.shape
+    if B.dim() != 3:
+        raise ValueError("B must be [S, H, N]")
     N = B.shape[-1]
     if B.shape != (S, H, N) or C.shape != (S, H, N) or tuple(state.shape) != (S, H, P, N):
         raise ValueError("expected B/C [S,H,N] and state [S,H,P,N]")
+    if A_log.shape != (H,):
+        raise ValueError(f"A_log must be [H] = [{H}], got {tuple(A_log.shape)}")
+    if D is not None and tuple(D.shape) not in ((H, P), (H * P,)):
+        raise ValueError(f"D must be [H, P] or [H*P], got {tuple(D.shape)}")
+    if out is not None and tuple(out.shape) != (S, H, P):
+        raise ValueError(f"out must be [S, H, P] = {(S, H, P)}, got {tuple(out.shape)}")
     if not state.is_contiguous():
         raise ValueError("state must be contiguous")
     if dt.shape == (S,):
@@ -180,16 +199,14 @@ def ssd_stream_step(x, dt, A_log, B, C, D, state, *, disc="zoh", out=None):
         sdt = dt.stride()
     else:
         raise ValueError("dt must be [S] or [S, H]")
-    for t, w in ((x, "x"), (B, "B"), (C, "C")):
+    for t, w in ((x, "x"), (B, "B"), (C, "C")) + (((out, "out"),) if out is not None else ()):
         _inner_unit(t, w)
+    for t, w in named:
+        need_gpu(t, w)
     A_log = A_log.contiguous()
     if D is not None:
-        need_gpu(D, "D")
-        D = as_f32(D, "D").contiguous()
-        if D.numel() != H * P:
-            raise ValueError("D must have H*P elements")
+        D = D.contiguous()
     y = torch.empty(S, H, P, device=x.device, dtype=torch.float32) if out is None else out
-    _inner_unit(y, "out")
     _lib.call("tssm_ssd_stream_step", _disc_code(disc), x.data_ptr(), dt.data_ptr(),
               A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), state.data_ptr(),
               y.data_ptr(), S, H, P, N, *sdt, *x.stride()[:2], *B.stride()[:2],
@@ -223,7 +240,7 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
     if B.dtype != x.dtype or C.dtype != x.dtype:
         raise TypeError("x, B and C must share one dtype")
     code = dcode(x, "x")
-    for t, w in ((B, "B"), (C, "C")):
+    for t, w in ((x, "x"), (B, "B"), (C, "C")):
         _inner_unit(t, w)
     dt = as_f32(dt, "dt")
     if dt.shape == (Bsz, L):
@@ -247,6 +264,7 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
     need_gpu(y, "out")
     if y.shape != x.shape or y.dtype != x.dtype:
         raise ValueError("out must match x in shape and dtype")
+    _inner_unit(y, "out")
     h_last = torch.empty(Bsz, Dc, N, device=x.device, dtype=torch.float32) if return_state else None
     L_ = _lib.lib()
     ws, stream = _ws(L_.tssm_selective_scan_workspace_bytes(Bsz, L, Dc, N, int(chunk)), x,

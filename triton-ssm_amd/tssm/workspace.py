@@ -1,25 +1,51 @@
-"""Look-back workspaces for the single-pass scans.
+"""Device workspaces of the fused scans, and the look-back error check.
 
 A workspace is a zero-filled device buffer that one stream reuses across
-launches (its header resets itself at the end of every launch and carries an
-epoch that invalidates stale carry words).  One buffer is kept per
-(device, stream) and grown when a launch needs more; launches on different
-streams therefore never share one.
+launches.  Two kinds never share a buffer:
+
+``lookback``  the single-pass scans (multihead, selective, elementwise):
+              tagged carry words {value, epoch} after a 256-byte header whose
+              first word is a sticky error flag.  The epoch advances on every
+              launch, so stale words never match and no per-launch clearing
+              is needed -- provided nothing but tagged words is ever written
+              there.
+``ssd``       the SSD passes: raw fp32 chunk states and decays.  Kept apart
+              because an arbitrary fp32 pair read as a carry word could carry
+              a current epoch in its upper half.
+
+One buffer is kept per (device, stream, kind) and grown when a launch needs
+more; launches on different streams therefore never share one.
+
+A bounded look-back wait that expires (a predecessor tile that never
+published, ~1 s of polling) sets the sticky flag and the kernel finishes with
+that tile's carry incomplete.  ``check()`` synchronises, reads every lookback
+workspace's flag and raises ``TssmError`` if one is set.
 """
 from __future__ import annotations
 
+import ctypes
 import threading
 
 import torch
 
 from . import _lib
 
+LOOKBACK = "lookback"
+SSD = "ssd"
+KINDS = (LOOKBACK, SSD)
+
 _lock = threading.Lock()
-_cache: dict[tuple[int, int], torch.Tensor] = {}
+_cache: dict[tuple[int, int, str], torch.Tensor] = {}
 
 
-def get(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+def _dev_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def get(device: torch.device, stream: int, nbytes: int, kind: str = LOOKBACK) -> torch.Tensor:
+    if kind not in KINDS:
+        raise ValueError(f"unknown workspace kind {kind!r}")
+    key = (_dev_index(device), stream, kind)
     with _lock:
         buf = _cache.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -30,11 +56,35 @@ def get(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
 
 
 def error_flag(buf: torch.Tensor, clear: bool = True) -> int:
-    """Sticky look-back timeout flag of a workspace (synchronous; tests only)."""
-    import ctypes
+    """Sticky look-back timeout flag of one workspace (a synchronous read)."""
     out = ctypes.c_int(0)
     _lib.call("tssm_workspace_error", buf.data_ptr(), int(clear), ctypes.byref(out))
     return out.value
+
+
+def check(device: torch.device | int | None = None, clear: bool = True) -> None:
+    """Synchronise and raise ``TssmError`` if a look-back wait expired.
+
+    Reads the sticky flag of every lookback workspace (of ``device``, or of
+    every device when None).  A set flag means that some launch on that
+    workspace since the last check produced outputs without its full carry;
+    the flag is cleared (with ``clear``) before raising, so later launches can
+    be checked afresh.
+    """
+    want = None if device is None else (device if isinstance(device, int) else
+                                        _dev_index(torch.device(device)))
+    with _lock:
+        items = [(k, b) for k, b in _cache.items() if k[2] == LOOKBACK and
+                 (want is None or k[0] == want)]
+    bad = []
+    for (dev_idx, stream, _), buf in items:
+        torch.cuda.synchronize(dev_idx)
+        if error_flag(buf, clear):
+            bad.append(f"device {dev_idx} stream {stream:#x}")
+    if bad:
+        raise _lib.TssmError(
+            "a bounded look-back wait expired (a predecessor tile never published its carry); "
+            "outputs of fused scans since the last check are invalid: " + ", ".join(bad))
 
 
 def clear() -> None:
