@@ -31,6 +31,7 @@ extern "C" {
 #define TSSM_ERR_WORKSPACE (-5)   /* workspace missing or too small */
 #define TSSM_ERR_UNSUPPORTED (-6) /* valid but unsupported configuration */
 #define TSSM_ERR_ALIGN (-7)       /* pointer/stride not aligned for vector access */
+#define TSSM_ERR_SCRATCH (-8)     /* too large for the no-allocation entry point's scratch */
 
 /* dtype codes */
 #define TSSM_F32 0
@@ -51,7 +52,8 @@ const char* tssm_strerror(int status);
  * that expires (~1 s) sets the workspace's sticky error word and the launch
  * completes with that tile's carry incomplete.  This reads the word
  * (1 = expired) with a synchronous copy -- call it after the stream has
- * finished; with clear=1 a set word is reset to 0. */
+ * finished; with clear=1 a set word is reset to 0.  workspace == NULL reads
+ * the word of the current device's tssm_mh_scan_fused_noalloc scratch. */
 int tssm_workspace_error(const void* workspace, int clear, int* error_out);
 
 /* ------------------------------------------------------------------ ZOH
@@ -161,6 +163,27 @@ int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log, c
                        int64_t sC_h, int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t sy_b,
                        int64_t sy_l, int64_t chunk, void* workspace, int64_t workspace_bytes,
                        void* stream);
+
+/* No-allocation variant of tssm_mh_scan_fused.  No reference counterpart: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernel and results as tssm_mh_scan_fused, without the workspace:
+ * the look-back words live in a fixed device array of
+ * TSSM_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends), whose
+ * address is resolved on the first call on each device.  Problems needing
+ * more than that (tssm_mh_scan_workspace_bytes() > the maximum) return
+ * TSSM_ERR_SCRATCH; `stream` must belong to the current device.  Calls that
+ * overlap on one GPU race on the shared array.  Its sticky look-back error
+ * word is read with tssm_workspace_error(NULL, ...). */
+#define TSSM_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int tssm_mh_scan_fused_noalloc(int dtype, int disc, const void* u, const float* A_log,
+                               const void* B, const void* C, const float* dt, const float* D,
+                               const float* h0, void* y, float* h_last, int64_t nbatch,
+                               int64_t L, int64_t n_heads, int64_t head_dim, int a_per_head,
+                               int64_t su_b, int64_t su_l, int64_t sB_b, int64_t sB_l,
+                               int64_t sB_h, int64_t sC_b, int64_t sC_l, int64_t sC_h,
+                               int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t sy_b,
+                               int64_t sy_l, int64_t chunk, void* stream);
 
 /* ------------------------------------------------------------------ interpolation
  * fused_time_aware_interp_kernel / fused_interp_bf16_kernel /

@@ -28,6 +28,9 @@ extern "C" const char* tssm_strerror(int status) {
     case TSSM_ERR_WORKSPACE: return "workspace missing or too small";
     case TSSM_ERR_UNSUPPORTED: return "unsupported configuration";
     case TSSM_ERR_ALIGN: return "pointer or stride not aligned for vector access";
+    case TSSM_ERR_SCRATCH:
+      return "problem needs more look-back words than the fixed scratch of the "
+             "no-allocation entry point holds (TSSM_NOALLOC_SCRATCH_BYTES)";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
@@ -35,7 +38,8 @@ extern "C" const char* tssm_strerror(int status) {
 }
 
 extern "C" int tssm_workspace_error(const void* workspace, int clear, int* error_out) {
-  TSSM_CHECK(workspace && error_out, TSSM_ERR_NULL);
+  TSSM_CHECK(error_out, TSSM_ERR_NULL);
+  if (workspace == nullptr) return tssm::noalloc_scratch_error(clear, error_out);
   const auto* hdr = reinterpret_cast<const tssm::WsHeader*>(workspace);
   uint32_t e = 0;
   hipError_t st = hipMemcpy(&e, &hdr->error, sizeof(e), hipMemcpyDeviceToHost);

@@ -38,6 +38,10 @@ constexpr uint32_t kDefaultSpinLimit = 1u << 20;  // ~1 s of polling
 // word is "not ready").  Thread-safe; defined in abi.hip.
 uint32_t next_epoch(const void* workspace);
 
+// Host: the sticky error word of the current device's no-allocation scratch
+// (0 when no no-allocation launch ran there yet); defined in multihead.hip.
+int noalloc_scratch_error(int clear, int* error_out);
+
 __device__ inline uint64_t ld_word(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

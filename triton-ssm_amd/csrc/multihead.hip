@@ -28,6 +28,8 @@
 //
 // mh_fwd_local_kernel / mh_output_kernel -- the reference's phase-exact
 // kernels with its intermediate layouts (loc_a, loc_x, carry).
+#include <mutex>
+
 #include "common.h"
 #include "lookback.h"
 
@@ -689,24 +691,51 @@ extern "C" int64_t tssm_mh_scan_workspace_bytes(int64_t nbatch, int64_t L, int64
   return mh_ws_bytes(nbatch * n_heads / cfg.hpr, L, head_dim * cfg.hpr, cfg.TC);
 }
 
-extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log,
-                                  const void* B, const void* C, const float* dt, const float* D,
-                                  const float* h0, void* y, float* h_last, int64_t nbatch,
-                                  int64_t L, int64_t n_heads, int64_t head_dim, int a_per_head,
-                                  int64_t su_b, int64_t su_l, int64_t sB_b, int64_t sB_l,
-                                  int64_t sB_h, int64_t sC_b, int64_t sC_l, int64_t sC_h,
-                                  int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t sy_b,
-                                  int64_t sy_l, int64_t chunk, void* workspace,
-                                  int64_t workspace_bytes, void* stream) {
-  TSSM_CHECK(u && A_log && B && C && dt && y, TSSM_ERR_NULL);
-  TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
-  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
-  TSSM_CHECK(nbatch > 0 && L > 0 && n_heads > 0, TSSM_ERR_SHAPE);
-  TileCfg cfg;
-  TSSM_CHECK(mh_diag_cfg(head_dim, n_heads, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
-  const int64_t need = tssm_mh_scan_workspace_bytes(nbatch, L, n_heads, head_dim, chunk);
-  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
-  TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);
+namespace tssm {
+namespace {
+
+// Scratch of the no-allocation entry point (tssm_mh_scan_fused_noalloc): the
+// look-back workspace as one fixed array per device, zero when the module is
+// loaded.  Host code never passes `scratch` itself to a kernel (on the host
+// the name is a stand-in, not a device address): each device's address is
+// resolved once with hipGetSymbolAddress, with that device current, and kept
+// in g_scratch.  The epoch scheme needs no clearing between calls; calls that
+// overlap on one device race on the array.
+constexpr int64_t kScratchBytes = TSSM_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];
+uint32_t g_scratch_epoch[kMaxDevices];
+
+// Device address of the current device's scratch and the tag of its next
+// launch.  `device` is the current device.
+int scratch_for(int device, void** ptr, uint32_t* tag) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[device] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    g_scratch[device] = p;
+  }
+  *ptr = g_scratch[device];
+  uint32_t& e = g_scratch_epoch[device];
+  if (++e == 0) e = 1;
+  *tag = e;
+  return TSSM_OK;
+}
+
+// Argument checks and launch shared by tssm_mh_scan_fused and its
+// no-allocation variant; `tag` is the epoch of this launch on `workspace`.
+int mh_scan_fused_launch(int dtype, int disc, const void* u, const float* A_log, const void* B,
+                         const void* C, const float* dt, const float* D, const float* h0,
+                         void* y, float* h_last, int64_t nbatch, int64_t L, int64_t n_heads,
+                         int64_t head_dim, int a_per_head, int64_t su_b, int64_t su_l,
+                         int64_t sB_b, int64_t sB_l, int64_t sB_h, int64_t sC_b, int64_t sC_l,
+                         int64_t sC_h, int64_t sdt_b, int64_t sdt_l, int64_t sdt_h,
+                         int64_t sy_b, int64_t sy_l, const TileCfg& cfg, void* workspace,
+                         uint32_t tag, void* stream) {
   // 8-channel vectors must be 16-byte aligned: base pointers and every stride.
   const int64_t vec = dtype == TSSM_F32 ? 4 : 8;
   const int64_t strides[] = {su_b, su_l, sB_b, sB_l, sB_h, sC_b, sC_l, sC_h, sy_b, sy_l};
@@ -732,7 +761,7 @@ extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const floa
   a.n_heads = (uint32_t)(n_heads / cfg.hpr);  // rows per batch
   a.nchunks = (uint32_t)nchunks;
   a.nrows = (uint32_t)nrows;
-  a.tag = next_epoch(workspace);
+  a.tag = tag;
   a.spin_limit = kDefaultSpinLimit;
   a.dt_is_tau = 0;
 
@@ -747,6 +776,94 @@ extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const floa
     case TSSM_F16: return launch_mh_fused_t<f16_t>(disc, aph, has_d, cfg.G, cfg.NS, grid, block, lds, s, a);
     default: return launch_mh_fused_t<float>(disc, aph, has_d, cfg.G, cfg.NS, grid, block, lds, s, a);
   }
+}
+
+}  // namespace
+
+int noalloc_scratch_error(int clear, int* error_out) {
+  int device = 0;
+  hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) return (int)st;
+  TSSM_CHECK(device >= 0 && device < kMaxDevices, TSSM_ERR_UNSUPPORTED);
+  void* p = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[device];
+  }
+  *error_out = 0;
+  if (p == nullptr) return TSSM_OK;  // no no-allocation launch on this device yet
+  const auto* hdr = reinterpret_cast<const WsHeader*>(p);
+  uint32_t e = 0;
+  st = hipMemcpy(&e, &hdr->error, sizeof(e), hipMemcpyDeviceToHost);
+  if (st != hipSuccess) return (int)st;
+  *error_out = (int)e;
+  if (clear && e) {
+    const uint32_t z = 0;
+    st = hipMemcpy(const_cast<uint32_t*>(&hdr->error), &z, sizeof(z), hipMemcpyHostToDevice);
+    if (st != hipSuccess) return (int)st;
+  }
+  return TSSM_OK;
+}
+
+}  // namespace tssm
+
+extern "C" int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log,
+                                  const void* B, const void* C, const float* dt, const float* D,
+                                  const float* h0, void* y, float* h_last, int64_t nbatch,
+                                  int64_t L, int64_t n_heads, int64_t head_dim, int a_per_head,
+                                  int64_t su_b, int64_t su_l, int64_t sB_b, int64_t sB_l,
+                                  int64_t sB_h, int64_t sC_b, int64_t sC_l, int64_t sC_h,
+                                  int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t sy_b,
+                                  int64_t sy_l, int64_t chunk, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(u && A_log && B && C && dt && y, TSSM_ERR_NULL);
+  TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nbatch > 0 && L > 0 && n_heads > 0, TSSM_ERR_SHAPE);
+  TileCfg cfg;
+  TSSM_CHECK(mh_diag_cfg(head_dim, n_heads, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
+  const int64_t need = tssm_mh_scan_workspace_bytes(nbatch, L, n_heads, head_dim, chunk);
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);
+  return mh_scan_fused_launch(dtype, disc, u, A_log, B, C, dt, D, h0, y, h_last, nbatch, L,
+                              n_heads, head_dim, a_per_head, su_b, su_l, sB_b, sB_l, sB_h, sC_b,
+                              sC_l, sC_h, sdt_b, sdt_l, sdt_h, sy_b, sy_l, cfg, workspace,
+                              next_epoch(workspace), stream);
+}
+
+extern "C" int tssm_mh_scan_fused_noalloc(int dtype, int disc, const void* u, const float* A_log,
+                                          const void* B, const void* C, const float* dt,
+                                          const float* D, const float* h0, void* y,
+                                          float* h_last, int64_t nbatch, int64_t L,
+                                          int64_t n_heads, int64_t head_dim, int a_per_head,
+                                          int64_t su_b, int64_t su_l, int64_t sB_b, int64_t sB_l,
+                                          int64_t sB_h, int64_t sC_b, int64_t sC_l, int64_t sC_h,
+                                          int64_t sdt_b, int64_t sdt_l, int64_t sdt_h,
+                                          int64_t sy_b, int64_t sy_l, int64_t chunk,
+                                          void* stream) {
+  TSSM_CHECK(u && A_log && B && C && dt && y, TSSM_ERR_NULL);
+  TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nbatch > 0 && L > 0 && n_heads > 0, TSSM_ERR_SHAPE);
+  TileCfg cfg;
+  TSSM_CHECK(mh_diag_cfg(head_dim, n_heads, chunk, &cfg), TSSM_ERR_UNSUPPORTED);
+  const int64_t need = tssm_mh_scan_workspace_bytes(nbatch, L, n_heads, head_dim, chunk);
+  TSSM_CHECK(need > 0 && need <= kScratchBytes, TSSM_ERR_SCRATCH);
+  // the scratch is resolved for the current device: the stream must be on it
+  int device = 0, stream_device = 0;
+  hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) return (int)st;
+  st = hipStreamGetDevice(as_stream(stream), &stream_device);
+  if (st != hipSuccess) return (int)st;
+  TSSM_CHECK(device == stream_device && device >= 0 && device < kMaxDevices,
+             TSSM_ERR_UNSUPPORTED);
+  void* ws = nullptr;
+  uint32_t tag = 0;
+  const int rc = scratch_for(device, &ws, &tag);
+  if (rc != TSSM_OK) return rc;
+  return mh_scan_fused_launch(dtype, disc, u, A_log, B, C, dt, D, h0, y, h_last, nbatch, L,
+                              n_heads, head_dim, a_per_head, su_b, su_l, sB_b, sB_l, sB_h, sC_b,
+                              sC_l, sC_h, sdt_b, sdt_l, sdt_h, sy_b, sy_l, cfg, ws, tag, stream);
 }
 
 extern "C" int tssm_mh_fwd_local(int dtype, const void* u, const float* A_log, const void* B,

@@ -26,6 +26,7 @@ DISC_EULER, DISC_ZOH = 0, 1
 ERR_NAMES = {
     -1: "TSSM_ERR_NULL", -2: "TSSM_ERR_SHAPE", -3: "TSSM_ERR_STRIDE", -4: "TSSM_ERR_DTYPE",
     -5: "TSSM_ERR_WORKSPACE", -6: "TSSM_ERR_UNSUPPORTED", -7: "TSSM_ERR_ALIGN",
+    -8: "TSSM_ERR_SCRATCH",
 }
 
 
