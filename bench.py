@@ -11,6 +11,9 @@ x/B/C/y, fp32 dt and state, ZOH discretization fused into the load stage.
   ssd_long       SSD scan B=1 L=262144 H=8 P=64 N=16 bf16, chunk 256
   ssd_config1    SSD scan on the headline shapes B=8 L=4096 H=16 P=N=64 bf16
   ssd_stream     streaming SSD step, 4096 streams H=32 P=64 N=128 fp32 state
+  dtproj         Mamba-1 scan B=16 L=2048 D=256 N=16 fp32 with dt = clamp(softplus(
+                 dt_raw W + bias)) computed in the scan's load stage (rank 16)
+  dtproj_two_launch  the same as dt_project_softplus_kernel + the scan
   rows           every drop-in kernel at a config-sized shape (one JSON line, "rows" list)
 
 A step is one pass of the path over one batch of seeded synthetic input that
@@ -216,6 +219,80 @@ def wl_interp_mamba1(args, dev):
                 config={"workload": "time-aware interpolation (K=10, FTILE=128, 30% missing) + "
                                     f"Mamba-1 scan, B=16 T=2048 F=256 N=16 fp32, {args.disc.upper()}",
                         "B": B, "T": T, "F": F, "N": N, "K": 10, "FTILE": 128})
+
+
+def _wl_dtproj(args, dev, fused):
+    """Mamba-1 scan with dt from the rank-16 projection, B=16 L=2048 D=256 N=16
+    fp32: fused into the scan's load stage, or as two launches
+    (dt_project_softplus_kernel writing dt [B,L,D], then the scan reading it)."""
+    import torch
+    import discretize_kernel as dk
+    from tssm import selective_scan_forward, workloads
+    w = workloads.dtproj_mamba1()
+    base = {k: v.to(dev) for k, v in w.items() if isinstance(v, torch.Tensor)}
+    B, L, Dc = base["x"].shape
+    N = base["A_log"].shape[1]
+    R = base["dt_raw"].shape[2]
+    sets = []
+    for i in range(max(args.sets, 3)):
+        st = {k: (v if k in ("W", "bias", "A_log") else torch.roll(v, shifts=i, dims=0).contiguous())
+              for k, v in base.items()}
+        st["y"] = torch.empty_like(st["x"])
+        st["dt"] = torch.empty(B, L, Dc, device=dev)
+        sets.append(st)
+    lo, hi = w["DT_MIN"], w["DT_MAX"]
+
+    def step(i):
+        d = sets[i % len(sets)]
+        if fused:
+            selective_scan_forward(d["x"], d["dt_raw"], d["A_log"], d["B"], d["C"], None,
+                                   chunk=args.scan_chunk, disc=args.disc, out=d["y"],
+                                   dt_proj=(d["W"], d["bias"], lo, hi))
+        else:
+            dk.dt_project_softplus_kernel[(B, L, Dc // 256)](
+                d["dt_raw"], d["W"], d["bias"], d["dt"], B, L, Dc, R, *d["dt_raw"].stride(),
+                *d["W"].stride(), *d["dt"].stride(), DT_MIN=lo, DT_MAX=hi, BLOCK_H=256,
+                BLOCK_R=16)
+            selective_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], None,
+                                   chunk=args.scan_chunk, disc=args.disc, out=d["y"])
+
+    def cpu():
+        import numpy as np
+        from oracle import cport
+        raw, W, bias = (_np32(w[k]) for k in ("dt_raw", "W", "bias"))
+        rest = [_np32(w[k]) for k in ("A_log", "B", "C")]
+        x = _np32(w["x"])
+
+        def run():
+            dt = np.clip(np.logaddexp(0.0, raw @ W + bias), lo, hi).astype(np.float32)
+            cport.selective_scan(x, dt, *rest, None, disc=args.disc)
+        med = _timed_cpu(run, args.cpu_reps)
+        return {"value": B * L * Dc / med, "unit": "elements/s", "cores": cport.threads(),
+                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                                          f"{med:.3f} s each (projection in numpy)"}
+
+    n = B * L * Dc
+    nbytes = 4 * (2 * n + B * L * R + R * Dc + Dc + Dc * N + 2 * B * L * N)
+    if not fused:
+        nbytes += 2 * 4 * n      # dt written by the projection and read by the scan
+    how = "fused into the scan's load stage" if fused else "two launches through dt [B,L,D]"
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, kernel="mh_scan_fused_kernel" if fused
+                else "dt_project_mfma_kernel + mh_scan_fused_kernel",
+                metric=f"Mamba-1 scan with dt projection ({how}) elements/sec, B=16 L=2048 "
+                       "D=256 N=16 rank 16 fp32",
+                unit="elements/s",
+                config={"workload": f"dt = clamp(softplus(dt_raw W + bias)) {how} + Mamba-1 "
+                                    f"scan, B=16 L=2048 D=256 N=16 rank 16 fp32, "
+                                    f"{args.disc.upper()}",
+                        "B": B, "L": L, "D": Dc, "N": N, "rank": R})
+
+
+def wl_dtproj(args, dev):
+    return _wl_dtproj(args, dev, True)
+
+
+def wl_dtproj_two_launch(args, dev):
+    return _wl_dtproj(args, dev, False)
 
 
 def wl_ssd_long(args, dev):
@@ -513,7 +590,8 @@ def rows_sweep(args, dev):
 WORKLOADS = {"multihead": wl_multihead, "mamba1_small": wl_mamba1_small,
              "interp_mamba1": wl_interp_mamba1, "ssd_long": wl_ssd_long,
              "ssd_config1": wl_ssd_config1,
-             "ssd_stream": wl_ssd_stream}
+             "ssd_stream": wl_ssd_stream, "dtproj": wl_dtproj,
+             "dtproj_two_launch": wl_dtproj_two_launch}
 
 
 def traffic_from_profile(name):

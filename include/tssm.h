@@ -315,6 +315,24 @@ int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt, int
                         int64_t sC_l, int64_t sy_b, int64_t sy_l, int64_t chunk, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* tssm_selective_scan with the dt producer fused into the load stage: per
+ * (b, t, d), dt = clamp(softplus(sum_k dt_raw[b,t,k] W[k,d] + bias[d]),
+ * dt_min, dt_max) -- dt_project_softplus_kernel (discretize_kernel.py:166-213,
+ * the scalar block index at :203 taken as its evident intent) feeding the
+ * scan, without the [B,L,Dc] dt tensor in between.  dt_raw f32 [B,L,rank]
+ * (strides sr_b, sr_l, unit over k), W f32 [rank, Dc] (row stride sw_r, unit
+ * over d), bias f32 [Dc]; rank <= 64.  Everything else as tssm_selective_scan
+ * (same workspace size). */
+int tssm_selective_scan_dtproj(int dtype, int disc, const void* x, const float* dt_raw,
+                               const float* W, const float* bias, float dt_min, float dt_max,
+                               const float* A_log, const void* B, const void* C, const float* D,
+                               const float* h0, void* y, float* h_last, int64_t nbatch,
+                               int64_t L, int64_t Dc, int64_t N, int64_t rank, int64_t sx_b,
+                               int64_t sx_l, int64_t sr_b, int64_t sr_l, int64_t sw_r,
+                               int64_t sB_b, int64_t sB_l, int64_t sC_b, int64_t sC_l,
+                               int64_t sy_b, int64_t sy_l, int64_t chunk, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ elementwise scan, single pass
  * The host functions ssm_forward / ssm_backward (ssm_scan.py:239-289) as one
  * launch each over contiguous [B, L, H] tensors of `dtype` (D [H]): every

@@ -298,6 +298,66 @@ def test_selective_scan(dev, dtype, N, Dc, dt_per_channel):
     assert_close(h, h_ref, TOL[dtype], "mamba1 h_last")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,Dc,rank,L", [(16, 40, 16, 700), (8, 24, 1, 333), (64, 6, 33, 520),
+                                         (16, 256, 64, 300), (32, 9, 4, 129), (128, 3, 7, 200)])
+def test_selective_scan_dtproj(dev, dtype, N, Dc, rank, L):
+    """dt produced in the scan's load stage (dt_project_softplus fused into the
+    Mamba-1 scan) against the oracle's projection followed by its selective
+    scan; the projection spans both clamps; nonzero h0, skip term, ragged L."""
+    from tssm import selective_scan_forward
+    g = torch.Generator().manual_seed(N * 1000 + Dc + rank)
+    x = torch.randn(3, L, Dc, generator=g).to(dtype)
+    raw = torch.randn(3, L, rank, generator=g)
+    W = torch.randn(rank, Dc, generator=g) * (3.0 / rank ** 0.5)
+    bias = torch.empty(Dc).uniform_(-4.0, 0.0, generator=g)
+    A_log = torch.empty(Dc, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = (torch.randn(3, L, N, generator=g) / N ** 0.5).to(dtype)
+    Cm = (torch.randn(3, L, N, generator=g) / N ** 0.5).to(dtype)
+    D = torch.randn(Dc, generator=g)
+    h0 = torch.randn(3, Dc, N, generator=g)
+    DT_MIN, DT_MAX = 2e-3, 0.4
+    dt_ref = O.dt_project_softplus(raw, W, bias, DT_MIN, DT_MAX)
+    assert (dt_ref == DT_MIN).any() and (dt_ref == DT_MAX).any()   # both clamps hit
+    d = {k: v.to(dev) for k, v in dict(x=x, raw=raw, W=W, bias=bias, A_log=A_log, B=Bm, C=Cm,
+                                        D=D, h0=h0).items()}
+    y, h = selective_scan_forward(d["x"], d["raw"], d["A_log"], d["B"], d["C"], d["D"],
+                                  h0=d["h0"], return_state=True,
+                                  dt_proj=(d["W"], d["bias"], DT_MIN, DT_MAX))
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.selective_scan(x, dt_ref, A_log, Bm, Cm, D, h0=np64(h0))
+    assert_close(y, y_ref, TOL[dtype], f"dtproj y {dtype} N={N} Dc={Dc} rank={rank}")
+    assert_close(h, h_ref, TOL[dtype], "dtproj h_last")
+
+
+def test_selective_scan_dtproj_config_shape(dev):
+    """B=16 L=2048 D=256 N=16 fp32, rank 16 (the interpolation workload's scan
+    shape): the fused projection against the oracle, and against the two-launch
+    path (dt_project_softplus_kernel, then the scan over the [B,L,D] dt)."""
+    import discretize_kernel as dk
+    from tssm import selective_scan_forward, workloads
+    w = workloads.dtproj_mamba1()
+    d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in w.items()}
+    proj = (d["W"], d["bias"], w["DT_MIN"], w["DT_MAX"])
+    y = selective_scan_forward(d["x"], d["dt_raw"], d["A_log"], d["B"], d["C"], None,
+                               chunk=256, dt_proj=proj)
+    Bsz, L, R = w["dt_raw"].shape
+    Dc = w["W"].shape[1]
+    dt = torch.empty(Bsz, L, Dc, device=dev)
+    dk.dt_project_softplus_kernel[(Bsz, L, Dc // 256)](
+        d["dt_raw"], d["W"], d["bias"], dt, Bsz, L, Dc, R, *d["dt_raw"].stride()[:2],
+        d["dt_raw"].stride(2), d["W"].stride(0), d["W"].stride(1), *dt.stride(),
+        DT_MIN=w["DT_MIN"], DT_MAX=w["DT_MAX"], BLOCK_H=256, BLOCK_R=16)
+    y2 = selective_scan_forward(d["x"], dt, d["A_log"], d["B"], d["C"], None, chunk=256)
+    torch.cuda.synchronize()
+    dt_ref = O.dt_project_softplus(w["dt_raw"], w["W"], w["bias"], w["DT_MIN"], w["DT_MAX"])
+    y_ref, _ = O.selective_scan(w["x"], dt_ref, w["A_log"], w["B"], w["C"])
+    e = assert_close(y, y_ref, 1e-5, "fused projection y")
+    assert_close(y2, y_ref, 1e-5, "two-launch y")
+    assert_close(y, y2, 1e-5, "fused vs two-launch")
+    print(f"dtproj config shape relerr {e:.2e}")
+
+
 @pytest.mark.parametrize("FTILE", [16, 128])
 def test_fused_interp_ssm_small(dev, FTILE):
     from tssm import fused_interp_ssm_forward

@@ -172,6 +172,27 @@ __device__ inline float group_sum(float v) {
   return v;
 }
 
+// softplus(x) = max(x, 0) + log1p(exp(-|x|)) with hardware exp2/log2.  With
+// e = exp(-|x|) <= 1 and u = 1 + e rounded, c = (u - 1) - e is the rounding
+// error exactly (u - 1 and the difference are exact by Sterbenz), and
+// log1p(e) = log(u) - c / u + O(c^2).  1/u is replaced by 1 - e + e^2: its
+// error e^3 / (1 + e) multiplies c <= 2^-23, negligible at every e (for
+// e < 2^-24, u = 1, c = -e and the result is e (1 - e + e^2)).  11 operations,
+// two of them transcendental, and no division.
+__device__ inline float softplus_fast(float x) {
+  const float e = exp2_fast(-__builtin_fabsf(x) * kLog2e);
+  const float u = 1.0f + e;
+  const float c = (u - 1.0f) - e;
+  const float r = __builtin_fmaf(e, e - 1.0f, 1.0f);
+  const float lp = __builtin_fmaf(__builtin_amdgcn_logf(u), 0.6931471805599453f, -c * r);
+  return fmaxf(x, 0.0f) + lp;
+}
+
+// clamp to [lo, hi] (lo <= hi) in one v_med3_f32
+__device__ inline float clamp_med3(float x, float lo, float hi) {
+  return __builtin_amdgcn_fmed3f(x, lo, hi);
+}
+
 // ZOH input coefficient expm1(dt a) / a for dt >= 0, a < 0, from the base-2
 // exponent y = dt a log2(e), e = exp2(y) (already computed for Abar) and
 // ia = 1/a.  |dt a| < 0.125: dt phi1(dt a), phi1's Taylor series to degree 4

@@ -60,6 +60,14 @@ struct MhArgs {
   uint32_t tag;
   uint32_t spin_limit;
   uint32_t dt_is_tau;    // dt holds timestamps: dt_t = tau_t - tau_{t-1}, dt_0 = tau_0
+  // MODE_MAMBA1 only: dt projected in the load stage,
+  // dt[b,t,d] = clamp(softplus(sum_k dt[b,t,k] W[k,d] + bias[d]), dt_min, dt_max)
+  // with `dt` then holding the raw rows [B, L, dt_rank] (strides sdt_b, sdt_l, 1).
+  const float* dtW = nullptr;     // [dt_rank, channels], row stride sw_r; NULL: dt given
+  const float* dtbias = nullptr;  // [channels]
+  int64_t sw_r = 0;
+  uint32_t dt_rank = 0;
+  float dt_min = 0.0f, dt_max = 0.0f;
 };
 
 // MODE_DIAG:   reference multihead layout -- u [B,L,nh*hd] per channel, y
@@ -76,8 +84,11 @@ constexpr int MODE_MAMBA1 = 1;
 constexpr int kMhR = 4;    // consecutive steps per thread
 constexpr int kMhWin = 1;  // predecessors read per look-back round trip (measured best)
 
-template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE, int NS, int R = kMhR,
-          int WIN = kMhWin>
+// DTP (MODE_MAMBA1 only): dt produced in the load stage by the projection
+// (MhArgs::dtW); a template flag so that the other instances carry none of
+// its code and registers.
+template <typename T, int DISC, bool APH, bool HAS_D, int G, int MODE, int NS, bool DTP = false,
+          int R = kMhR, int WIN = kMhWin>
 __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   // NS = threads summed into one output value: one head's head_dim/8 threads
   // for MODE_DIAG, one channel's N/8 threads for MODE_MAMBA1.
@@ -93,6 +104,9 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   float* s_sa = s_x + NRUN * P;        // [NSEG][P] segment totals
   float* s_sx = s_sa + NSEG * P;
   float* s_carry = s_sx + NSEG * P;    // [P] state entering the tile
+  // dt projection (MODE_MAMBA1): [TC][CPR] dt values, [TC][rank] raw rows,
+  // [rank][CPR] weights of the row's channels
+  float* s_dt = s_carry + P;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -144,6 +158,9 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     Dv[4] = d1.x; Dv[5] = d1.y; Dv[6] = d1.z; Dv[7] = d1.w;
   }
 
+  // dt from the projection (computed below, once per (step, channel) of the tile)
+  constexpr bool dtp = MODE == MODE_MAMBA1 && DTP;
+
   // ---- loads (all issued before any use)
   Vec8<T> vu[R], vB[R], vC[R];
   float us[R];  // MODE_MAMBA1: the channel's input, shared by its 8 state lanes
@@ -181,7 +198,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     float dlane = 0.0f, tprev_lane = 0.0f;
     if constexpr (DT_SHFL) {
       const int64_t tk = tw + (int64_t)wave * WSTEPS + lane;  // this lane's step
-      if (lane < WSTEPS) {
+      if (lane < WSTEPS && !dtp) {
         dlane = *(tk < a.L ? db + tk * a.sdt_l : dp_l);
         // timestamp of step tk - 1 (0 before the first step)
         if (a.dt_is_tau && tk > 0) tprev_lane = *(tk <= a.L ? db + (tk - 1) * a.sdt_l : dp_l);
@@ -194,7 +211,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       else us[r] = ldf(in ? up + r * a.su_l : up_l);
       vB[r].load_nt(in ? Bp + r * a.sB_l : Bp_l);
       vC[r].load_nt(in ? Cp + r * a.sC_l : Cp_l);
-      if constexpr (!DT_SHFL) draw[r] = *(in ? dp + r * a.sdt_l : dp_l);
+      if constexpr (!DT_SHFL) draw[r] = dtp ? 0.0f : *(in ? dp + r * a.sdt_l : dp_l);
     }
     if constexpr (DT_SHFL) {
       __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
@@ -214,6 +231,66 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
         float d = draw[r];
         if (a.dt_is_tau) d -= (t0 + r > 0) ? (r > 0 ? draw[r - 1] : tprev) : 0.0f;
         dtv[r] = (t0 + r < a.L) ? d : 0.0f;
+      }
+    }
+  }
+  if constexpr (dtp) {
+    {
+      // stage the tile's raw rows [TC][RS] and the row's weights, transposed
+      // to [CPR][RP] (a channel's column contiguous), in LDS; then one thread
+      // per (step, channel) pair: rank FMAs from 16-byte LDS reads, softplus,
+      // clamp -> s_dt.  Rows are padded to whole float4s (RP) and spaced RS =
+      // RP + 4 floats apart, so the 16-byte reads of different steps fall in
+      // different bank groups.
+      const int rank = (int)a.dt_rank;
+      const int RP = (rank + 3) & ~3;
+      const int RS = RP + 4;
+      float* s_raw = s_dt + TC * CPR;
+      float* s_w = s_raw + TC * RS;
+      const float* rawb = a.dt + b * a.sdt_b;
+      for (int i = tid; i < TC * RP; i += blockDim.x) {
+        const int st = i / RP, k = i - st * RP;
+        const int64_t t = tw + st;
+        s_raw[st * RS + k] = (t < a.L && k < rank) ? rawb[t * a.sdt_l + k] : 0.0f;
+      }
+      for (int i = tid; i < CPR * RP; i += blockDim.x) {
+        const int cw = i / RP, k = i - cw * RP;
+        s_w[i] = k < rank ? a.dtW[k * a.sw_r + (int64_t)h * CPR + cw] : 0.0f;
+      }
+      __syncthreads();
+      const int cl_t = tid % CPR;  // the same channel for every pair of this thread
+      const float bias = a.dtbias[(int64_t)h * CPR + cl_t];
+      const float4* wv = reinterpret_cast<const float4*>(s_w + cl_t * RP);
+      for (int pr = tid; pr < TC * CPR; pr += blockDim.x) {
+        const int st = pr / CPR;
+        const float4* rv = reinterpret_cast<const float4*>(s_raw + st * RS);
+        float acc0 = bias, acc1 = 0.0f;
+#pragma unroll 4
+        for (int k = 0; k < RP / 4; ++k) {
+          const float4 r4 = rv[k], w4 = wv[k];
+          acc0 = __builtin_fmaf(r4.x, w4.x, acc0);
+          acc1 = __builtin_fmaf(r4.y, w4.y, acc1);
+          acc0 = __builtin_fmaf(r4.z, w4.z, acc0);
+          acc1 = __builtin_fmaf(r4.w, w4.w, acc1);
+        }
+        // steps past the end are identity steps (dt = 0)
+        s_dt[pr] = tw + st < a.L ? clamp_med3(softplus_fast(acc0 + acc1), a.dt_min, a.dt_max)
+                                 : 0.0f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < R; ++r) dtv[r] = s_dt[(tr + r) * CPR + cl];
+    }
+  }
+  // ZOH with a decay per lane updates h' = ab h + (ab - 1) B u / a, which must
+  // stay h at the identity steps past the end: their input is zeroed.
+  if constexpr (!APH && DISC == TSSM_DISC_ZOH) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if constexpr (MODE == MODE_MAMBA1) {
+        us[r] = t0 + r < a.L ? us[r] : 0.0f;
+      } else {
+        if (!(t0 + r < a.L)) vB[r].zero();
       }
     }
   }
@@ -262,13 +339,21 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
         ab = ab_h;
         coef = coef_h;
       } else {
-        const float arg = dtv[r] * a2[j];
-        ab = exp2_fast(arg);
-        if constexpr (DISC == TSSM_DISC_ZOH) coef = zoh_coef2(arg, ab, dtv[r], ia[j]);
-        else coef = dtv[r];
+        ab = exp2_fast(dtv[r] * a2[j]);
+        coef = dtv[r];  // Euler input term
       }
       const float uj = (MODE == MODE_DIAG) ? vu[r].get(j) : us[r];
-      xl[j] = __builtin_fmaf(ab, xl[j], coef * vB[r].get(j) * uj);
+      if constexpr (!APH && DISC == TSSM_DISC_ZOH) {
+        // ZOH with a decay per lane: the input term expm1(dt a) / a B u equals
+        // (ab - 1) ibx with ibx = B u / a, so h' = ab h + (ab - 1) ibx =
+        // fma(ab, h + ibx, -ibx): two operations instead of a coefficient
+        // series, a select and two products.  Exact in real arithmetic; the
+        // rounding of h + ibx adds one half-ulp of max(|h|, |ibx|) per step.
+        const float ibx = ia[j] * (vB[r].get(j) * uj);
+        xl[j] = __builtin_fmaf(ab, xl[j] + ibx, -ibx);
+      } else {
+        xl[j] = __builtin_fmaf(ab, xl[j], coef * vB[r].get(j) * uj);
+      }
       al[j] = al[j] * ab;
       const float cj = vC[r].get(j);
       if constexpr (!APH) w[r][j] = cj * al[j];
@@ -671,10 +756,15 @@ int launch_mh_fused_g(int G, int NS, dim3 grid, dim3 block, size_t lds, hipStrea
 // MODE_MAMBA1 rows of P = 8 G lanes holding channels of N = 8 NS states.
 template <typename T, int DISC, bool HAS_D>
 int launch_sel_gn(int G, int NS, dim3 grid, dim3 block, size_t lds, hipStream_t s, const MhArgs& a) {
+  const bool dtp = a.dtW != nullptr;
 #define TSSM_SEL(GV, NV)                                                                          \
   if (G == GV && NS == NV) {                                                                    \
-    hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, false, HAS_D, GV, MODE_MAMBA1, NV>), grid, \
-                       block, lds, s, a);                                                       \
+    if (dtp)                                                                                    \
+      hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, false, HAS_D, GV, MODE_MAMBA1, NV, true>), \
+                         grid, block, lds, s, a);                                               \
+    else                                                                                        \
+      hipLaunchKernelGGL((mh_scan_fused_kernel<T, DISC, false, HAS_D, GV, MODE_MAMBA1, NV>), grid, \
+                         block, lds, s, a);                                                     \
     return launch_status();                                                                     \
   }
   TSSM_SEL(8, 1) TSSM_SEL(8, 2) TSSM_SEL(8, 4) TSSM_SEL(8, 8) TSSM_SEL(16, 16)
@@ -1018,15 +1108,28 @@ extern "C" int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L
   return mh_ws_bytes(nbatch * (Dc / cpr), L, cpr * N, cfg.TC);
 }
 
-extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt,
-                                   int dt_is_tau, const float* A_log, const void* B,
-                                   const void* C, const float* D, const float* h0, void* y,
-                                   float* h_last, int64_t nbatch, int64_t L, int64_t Dc,
-                                   int64_t N, int64_t sx_b, int64_t sx_l, int64_t sdt_b,
-                                   int64_t sdt_l, int64_t sdt_d, int64_t sB_b, int64_t sB_l,
-                                   int64_t sC_b, int64_t sC_l, int64_t sy_b, int64_t sy_l,
-                                   int64_t chunk, void* workspace, int64_t workspace_bytes,
-                                   void* stream) {
+namespace tssm {
+namespace {
+
+// Largest rank of the fused dt projection: raw rows, weights and dt values of
+// a tile are staged in LDS.
+constexpr int64_t kMaxDtRank = 64;
+
+struct DtProj {
+  const float* W = nullptr;
+  const float* bias = nullptr;
+  int64_t sw_r = 0, rank = 0;
+  float dt_min = 0.0f, dt_max = 0.0f;
+};
+
+int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, int dt_is_tau,
+                          const DtProj& proj, const float* A_log, const void* B, const void* C,
+                          const float* D, const float* h0, void* y, float* h_last,
+                          int64_t nbatch, int64_t L, int64_t Dc, int64_t N, int64_t sx_b,
+                          int64_t sx_l, int64_t sdt_b, int64_t sdt_l, int64_t sdt_d,
+                          int64_t sB_b, int64_t sB_l, int64_t sC_b, int64_t sC_l, int64_t sy_b,
+                          int64_t sy_l, int64_t chunk, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
   TSSM_CHECK(x && dt && A_log && B && C && y, TSSM_ERR_NULL);
   TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16 || dtype == TSSM_F16, TSSM_ERR_DTYPE);
   TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
@@ -1048,6 +1151,17 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
   const int64_t nchunks = cdiv(L, cfg.TC);
   const int64_t nrows = nbatch * (Dc / cpr);
   TSSM_CHECK(nchunks * nrows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
+  const int nrun = cfg.W * (64 / cfg.G);
+  size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + P) * sizeof(float);
+  if (proj.W) {
+    TSSM_CHECK(proj.bias, TSSM_ERR_NULL);
+    TSSM_CHECK(!dt_is_tau, TSSM_ERR_UNSUPPORTED);
+    TSSM_CHECK(proj.rank > 0 && proj.rank <= kMaxDtRank, TSSM_ERR_UNSUPPORTED);
+    TSSM_CHECK(proj.sw_r >= 0 && proj.dt_min <= proj.dt_max, TSSM_ERR_SHAPE);
+    const int64_t rp = (proj.rank + 3) & ~3ll;  // rank padded to whole float4s
+    lds += (size_t)(cfg.TC * cpr + cfg.TC * (rp + 4) + rp * cpr) * sizeof(float);
+    TSSM_CHECK(lds <= 64 * 1024, TSSM_ERR_UNSUPPORTED);
+  }
   MhArgs a;
   a.u = x; a.A_log = A_log; a.B = B; a.C = C; a.dt = dt; a.D = D; a.h0 = h0; a.y = y;
   a.h_last = h_last;
@@ -1055,7 +1169,7 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
   a.su_b = sx_b; a.su_l = sx_l;
   a.sB_b = sB_b; a.sB_l = sB_l; a.sB_h = 0;
   a.sC_b = sC_b; a.sC_l = sC_l; a.sC_h = 0;
-  a.sdt_b = sdt_b; a.sdt_l = sdt_l; a.sdt_h = sdt_d;
+  a.sdt_b = sdt_b; a.sdt_l = sdt_l; a.sdt_h = proj.W ? 0 : sdt_d;
   a.sy_b = sy_b; a.sy_l = sy_l;
   a.hdr = reinterpret_cast<WsHeader*>(workspace);
   a.words = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(workspace) + sizeof(WsHeader));
@@ -1065,9 +1179,9 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
   a.tag = next_epoch(workspace);
   a.spin_limit = kDefaultSpinLimit;
   a.dt_is_tau = dt_is_tau ? 1u : 0u;
+  a.dtW = proj.W; a.dtbias = proj.bias; a.sw_r = proj.sw_r; a.dt_rank = (uint32_t)proj.rank;
+  a.dt_min = proj.dt_min; a.dt_max = proj.dt_max;
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
-  const int nrun = cfg.W * (64 / cfg.G);
-  const size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + P) * sizeof(float);
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr;
   const int NS = (int)(N / 8);
@@ -1076,4 +1190,42 @@ extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const flo
     case TSSM_F16: return launch_sel_t<f16_t>(disc, has_d, cfg.G, NS, grid, block, lds, s, a);
     default: return launch_sel_t<float>(disc, has_d, cfg.G, NS, grid, block, lds, s, a);
   }
+}
+
+}  // namespace
+}  // namespace tssm
+
+extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt,
+                                   int dt_is_tau, const float* A_log, const void* B,
+                                   const void* C, const float* D, const float* h0, void* y,
+                                   float* h_last, int64_t nbatch, int64_t L, int64_t Dc,
+                                   int64_t N, int64_t sx_b, int64_t sx_l, int64_t sdt_b,
+                                   int64_t sdt_l, int64_t sdt_d, int64_t sB_b, int64_t sB_l,
+                                   int64_t sC_b, int64_t sC_l, int64_t sy_b, int64_t sy_l,
+                                   int64_t chunk, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  return selective_scan_launch(dtype, disc, x, dt, dt_is_tau, DtProj{}, A_log, B, C, D, h0, y,
+                               h_last, nbatch, L, Dc, N, sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b,
+                               sB_l, sC_b, sC_l, sy_b, sy_l, chunk, workspace, workspace_bytes,
+                               stream);
+}
+
+extern "C" int tssm_selective_scan_dtproj(int dtype, int disc, const void* x,
+                                          const float* dt_raw, const float* W, const float* bias,
+                                          float dt_min, float dt_max, const float* A_log,
+                                          const void* B, const void* C, const float* D,
+                                          const float* h0, void* y, float* h_last,
+                                          int64_t nbatch, int64_t L, int64_t Dc, int64_t N,
+                                          int64_t rank, int64_t sx_b, int64_t sx_l, int64_t sr_b,
+                                          int64_t sr_l, int64_t sw_r, int64_t sB_b, int64_t sB_l,
+                                          int64_t sC_b, int64_t sC_l, int64_t sy_b, int64_t sy_l,
+                                          int64_t chunk, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(W && bias, TSSM_ERR_NULL);
+  DtProj proj;
+  proj.W = W; proj.bias = bias; proj.sw_r = sw_r; proj.rank = rank;
+  proj.dt_min = dt_min; proj.dt_max = dt_max;
+  return selective_scan_launch(dtype, disc, x, dt_raw, 0, proj, A_log, B, C, D, h0, y, h_last,
+                               nbatch, L, Dc, N, sx_b, sx_l, sr_b, sr_l, 0, sB_b, sB_l, sC_b,
+                               sC_l, sy_b, sy_l, chunk, workspace, workspace_bytes, stream);
 }

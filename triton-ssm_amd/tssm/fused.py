@@ -215,16 +215,20 @@ def ssd_stream_step(x, dt, A_log, B, C, D, state, *, disc="zoh", out=None):
 
 
 def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh", h0=None,
-                           return_state=False, dt_is_tau=False, out=None):
+                           return_state=False, dt_is_tau=False, out=None, dt_proj=None):
     """Mamba-1 selective scan over lanes (channel d, state n).
 
     x      [Bsz, L, Dc]        float32 / bfloat16 / float16
     dt     [Bsz, L] (one per step, shared by the channels) or [Bsz, L, Dc];
            with ``dt_is_tau`` it holds timestamps and dt_t = tau_t - tau_{t-1},
-           dt_0 = tau_0
+           dt_0 = tau_0; with ``dt_proj`` it holds dt_raw [Bsz, L, rank]
     A_log  [Dc, N]             log(-a) per lane
     B, C   [Bsz, L, N]         dtype of x; N a multiple of 8, <= 128
     D      [Dc] or None;  h0 [Bsz, Dc, N] float32 or None
+    dt_proj  (W [rank, Dc], bias [Dc], DT_MIN, DT_MAX) or None: dt is produced
+           in the scan's load stage as clamp(softplus(dt_raw @ W + bias),
+           DT_MIN, DT_MAX) -- dt_project_softplus_kernel
+           (discretize_kernel.py:166-213) fused into the scan; rank <= 64
 
     h_t[d,n] = exp(dt_t a[d,n]) h_{t-1}[d,n] + Bbar_t[d,n] B_t[n] x_t[d];
     y_t[d] = sum_n C_t[n] h_t[d,n] + D[d] x_t[d].
@@ -243,7 +247,27 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
     for t, w in ((x, "x"), (B, "B"), (C, "C")):
         _inner_unit(t, w)
     dt = as_f32(dt, "dt")
-    if dt.shape == (Bsz, L):
+    proj = None
+    if dt_proj is not None:
+        if dt_is_tau:
+            raise ValueError("dt_proj and dt_is_tau are exclusive")
+        W, bias, dt_min, dt_max = dt_proj
+        need_gpu(W, "W")
+        need_gpu(bias, "bias")
+        if dt.dim() != 3 or dt.shape[:2] != (Bsz, L):
+            raise ValueError("with dt_proj, dt holds dt_raw [Bsz, L, rank]")
+        rank = dt.shape[2]
+        if W.shape != (rank, Dc) or bias.shape != (Dc,):
+            raise ValueError(f"dt_proj: W must be [rank, Dc] = {(rank, Dc)} and bias [Dc]")
+        if not 1 <= rank <= 64:
+            raise ValueError("dt_proj: rank must be in 1..64")
+        if not float(dt_min) <= float(dt_max):
+            raise ValueError("dt_proj: DT_MIN must not exceed DT_MAX")
+        _inner_unit(dt, "dt_raw")
+        W = as_f32(W, "W")
+        _inner_unit(W, "W")
+        proj = (W, as_f32(bias, "bias").contiguous(), float(dt_min), float(dt_max), rank)
+    elif dt.shape == (Bsz, L):
         sdt = (dt.stride(0), dt.stride(1), 0)
     elif dt.shape == (Bsz, L, Dc) and not dt_is_tau:
         sdt = dt.stride()
@@ -269,11 +293,21 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
     L_ = _lib.lib()
     ws, stream = _ws(L_.tssm_selective_scan_workspace_bytes(Bsz, L, Dc, N, int(chunk)), x,
                      "selective_scan")
-    _lib.call("tssm_selective_scan", code, _disc_code(disc), x.data_ptr(), dt.data_ptr(),
-              int(bool(dt_is_tau)), A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D),
-              ptr(h0), y.data_ptr(), ptr(h_last), Bsz, L, Dc, N, x.stride(0), x.stride(1),
-              *sdt, B.stride(0), B.stride(1), C.stride(0), C.stride(1), y.stride(0),
-              y.stride(1), int(chunk), ws.data_ptr(), ws.numel(), stream)
+    if proj is not None:
+        W, bias, dt_min, dt_max, rank = proj
+        _lib.call("tssm_selective_scan_dtproj", code, _disc_code(disc), x.data_ptr(),
+                  dt.data_ptr(), W.data_ptr(), bias.data_ptr(), dt_min, dt_max,
+                  A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), ptr(h0), y.data_ptr(),
+                  ptr(h_last), Bsz, L, Dc, N, rank, x.stride(0), x.stride(1), dt.stride(0),
+                  dt.stride(1), W.stride(0), B.stride(0), B.stride(1), C.stride(0),
+                  C.stride(1), y.stride(0), y.stride(1), int(chunk), ws.data_ptr(), ws.numel(),
+                  stream)
+    else:
+        _lib.call("tssm_selective_scan", code, _disc_code(disc), x.data_ptr(), dt.data_ptr(),
+                  int(bool(dt_is_tau)), A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D),
+                  ptr(h0), y.data_ptr(), ptr(h_last), Bsz, L, Dc, N, x.stride(0), x.stride(1),
+                  *sdt, B.stride(0), B.stride(1), C.stride(0), C.stride(1), y.stride(0),
+                  y.stride(1), int(chunk), ws.data_ptr(), ws.numel(), stream)
     return (y, h_last) if return_state else y
 
 

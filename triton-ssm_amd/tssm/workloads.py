@@ -20,6 +20,8 @@ distributions.
                  LogNormal(-3, 1.5) per (t,h); A_log as multihead
   ssd_stream     S=4096 H=32 P=64 N=128 fp32 state; per step x ~ N(0,1),
                  dt ~ Exp(mean 0.1) per stream, B, C ~ N(0, 1/N)
+  dtproj_mamba1  the interpolation workload's scan shape with dt produced by a
+                 rank-16 projection (dt_raw, W, bias)
 """
 from __future__ import annotations
 
@@ -97,6 +99,24 @@ def ssd_stream(seed=1004, S=4096, H=32, P=64, N=128, pool=16):
             "C": torch.randn(S, H, N, generator=g) / math.sqrt(N),
         })
     return {"A_log": A_log, "steps": steps, "S": S, "H": H, "P": P, "N": N}
+
+
+def dtproj_mamba1(seed=1005, B=16, L=2048, D=256, N=16, R=16):
+    """Mamba-1 scan with dt produced by the rank-R projection, at the
+    interpolation workload's scan shape (B=16 L=2048 D=256 N=16 fp32):
+    dt_raw ~ N(0,1) [B,L,R], W ~ N(0, 0.25/R) [R,D], bias [D] =
+    softplus^-1(0.05) + U(-0.5, 0.5), DT_MIN=1e-3, DT_MAX=1; x, A_log, B, C as
+    mamba1_small."""
+    g = _gen(seed)
+    x = torch.randn(B, L, D, generator=g)
+    dt_raw = torch.randn(B, L, R, generator=g)
+    W = torch.randn(R, D, generator=g) * (0.5 / math.sqrt(R))
+    bias = math.log(math.expm1(0.05)) + _unif(g, (D,), -0.5, 0.5)
+    A_log = _unif(g, (D, N), math.log(0.5), math.log(5.0))
+    Bm = torch.randn(B, L, N, generator=g) / math.sqrt(N)
+    Cm = torch.randn(B, L, N, generator=g) / math.sqrt(N)
+    return {"x": x, "dt_raw": dt_raw, "W": W, "bias": bias, "A_log": A_log, "B": Bm, "C": Cm,
+            "DT_MIN": 1e-3, "DT_MAX": 1.0}
 
 
 # ------------------------------------------------------------------ bytes
