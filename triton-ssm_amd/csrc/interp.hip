@@ -25,7 +25,12 @@ namespace tssm {
 
 constexpr int kInterpTB = 64;     // time steps per workgroup
 constexpr int kInterpThreads = 256;
-constexpr int kMaxK = 64;         // largest search window supported
+// The search window K sizes each kernel's LDS (flags and timestamps of the
+// candidate rows), allocated at launch; a launch needing more than this per
+// workgroup is refused (K up to ~6500 in every kernel, ~32000 in the offline one).
+constexpr int64_t kMaxLds = 64 * 1024;
+// Batches launch in slices of at most this many (a grid y/z dimension).
+constexpr int64_t kMaxGridYZ = 65535;
 
 // Sum of the tile's mask lanes for one row, by one wave.
 __device__ inline float wave_tile_sum(const void* M, int md, int64_t row_off, int64_t f0,
@@ -45,6 +50,7 @@ struct InterpArgs {
   int md, td;
   int64_t T, F, svb, svt, smb, smt, stb, stt, sob, sot;
   int64_t K, FTILE, grid_t, rows, ntile;
+  int64_t b0;  // first batch of this launch (batches launch in slices)
 };
 
 __global__ __launch_bounds__(kInterpThreads) void interp_obs_kernel(InterpArgs a, int64_t nrow) {
@@ -220,13 +226,13 @@ __global__ __launch_bounds__(kInterpThreads) void interp_obs_pow2_kernel(InterpA
 
 template <typename TV, int E>
 __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
-  __shared__ unsigned char s_obs[kInterpTB + 2 * kMaxK];
+  extern __shared__ unsigned char s_obs[];  // [kInterpTB + 2K]
   __shared__ int s_prev[kInterpTB], s_next[kInterpTB];
   __shared__ float s_w[kInterpTB];
   const int tid = threadIdx.x;
   const int64_t t0 = (int64_t)blockIdx.x * kInterpTB;
   const int64_t tile = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  const int64_t b = a.b0 + blockIdx.z;
   const int64_t f0 = tile * a.FTILE;
   const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
   const int K = (int)a.K;
@@ -316,16 +322,17 @@ struct StepArgs {
   int md, td;
   int64_t nb, T, F, svb, svt, smb, smt, stb, stt, sob, sot, s_hib, s_hob;
   int64_t t_cur, K, FTILE;
+  int64_t b0;  // first batch of this launch (batches launch in slices)
 };
 
 template <typename TV>
 __global__ __launch_bounds__(kInterpThreads) void interp_step_kernel(StepArgs a) {
-  __shared__ unsigned char s_obs[2 * kMaxK + 1];
+  extern __shared__ unsigned char s_obs[];  // [2K + 1]
   __shared__ int s_pn[2];
   __shared__ float s_w;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t tile = blockIdx.x;
-  const int64_t b = blockIdx.y;
+  const int64_t b = a.b0 + blockIdx.y;
   const int64_t f0 = tile * a.FTILE;
   const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
   const int K = (int)a.K;
@@ -403,10 +410,10 @@ __device__ inline void step_mask_batch(const TM* M, int64_t row0, int64_t smt, i
 
 template <typename TV>
 __global__ __launch_bounds__(kInterpThreads) void interp_step_fast_kernel(StepArgs a) {
-  __shared__ unsigned char s_obs[2 * kMaxK + 1];
-  __shared__ float s_tau[2 * kMaxK + 1];
+  extern __shared__ float s_tau[];  // [2K + 1], then the flags
+  unsigned char* s_obs = reinterpret_cast<unsigned char*>(s_tau + 2 * a.K + 1);  // [2K + 1]
   const int tid = threadIdx.x;
-  const int64_t b = blockIdx.y;
+  const int64_t b = a.b0 + blockIdx.y;
   const int64_t f0 = (int64_t)blockIdx.x * a.FTILE;
   const int nf = (int)((f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F) - f0);
   const int K = (int)a.K, nrow = 2 * K + 1;
@@ -483,12 +490,12 @@ constexpr int kCorrTB = 64;
 
 template <typename TV>
 __global__ __launch_bounds__(kInterpThreads) void interp_corrected_kernel(InterpArgs a) {
-  __shared__ unsigned char s_obs[kCorrTB + 2 * kMaxK][64];
-  __shared__ float s_tau[kCorrTB + 2 * kMaxK];
+  extern __shared__ float s_tau[];  // [kCorrTB + 2K], then the flags [kCorrTB + 2K][64]
+  auto s_obs = reinterpret_cast<unsigned char (*)[64]>(s_tau + kCorrTB + 2 * a.K);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * kCorrTB;
   const int64_t f = (int64_t)blockIdx.y * 64 + lane;
-  const int64_t b = blockIdx.z;
+  const int64_t b = a.b0 + blockIdx.z;
   const int K = (int)a.K;
   const int nrow = kCorrTB + 2 * K;
   const bool fok = f < a.F;
@@ -565,16 +572,19 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   TSSM_CHECK(nbatch >= 0 && T >= 0 && F >= 0 && FTILE > 0 && K >= 0, TSSM_ERR_SHAPE);
   TSSM_CHECK(grid_b >= 0 && grid_t >= 0 && grid_f >= 0 && grid_b <= nbatch && grid_t <= T,
              TSSM_ERR_SHAPE);
-  TSSM_CHECK(K <= kMaxK, TSSM_ERR_UNSUPPORTED);
+  // interp_kernel's LDS: flags of kInterpTB + 2K rows after its fixed arrays
+  const size_t lds_interp = (size_t)(kInterpTB + 2 * K);
+  TSSM_CHECK(K <= kMaxLds && (int64_t)lds_interp + 3 * kInterpTB * 4 <= kMaxLds,
+             TSSM_ERR_UNSUPPORTED);
   const int64_t ntile = (F + FTILE - 1) / FTILE;
   const int64_t gf = grid_f < ntile ? grid_f : ntile;
   if (grid_b == 0 || grid_t == 0 || gf == 0) return TSSM_OK;
-  TSSM_CHECK(gf <= 65535 && grid_b <= 65535, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(gf <= kMaxGridYZ, TSSM_ERR_UNSUPPORTED);
   const int64_t rows = interp_rows(T, grid_t, K);
   const int64_t need = grid_b * rows * gf;
   TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
   InterpArgs a{V, M, tau, Vhat, reinterpret_cast<unsigned char*>(workspace), m_dtype, tau_dtype,
-               T, F, svb, svt, smb, smt, stb, stt, sob, sot, K, FTILE, grid_t, rows, gf};
+               T, F, svb, svt, smb, smt, stb, stt, sob, sot, K, FTILE, grid_t, rows, gf, 0};
   const hipStream_t s = as_stream(stream);
   const int64_t nrow = grid_b * rows;
   const int64_t wpb = kInterpThreads / 64;
@@ -616,21 +626,27 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   }
   const int st = launch_status();
   if (st != TSSM_OK) return st;
-  const dim3 grid((unsigned)((grid_t + kInterpTB - 1) / kInterpTB), (unsigned)gf,
-                  (unsigned)grid_b);
   // 16-byte lane groups when every tile, row stride and base pointer allows
   const int64_t E = v_dtype == TSSM_F32 ? 4 : 8;
   const bool vec = FTILE % E == 0 && F % E == 0 && svt % E == 0 && sot % E == 0 &&
                    svb % E == 0 && sob % E == 0 && aligned(V, 16) && aligned(Vhat, 16);
+  for (int64_t b0 = 0; b0 < grid_b; b0 += kMaxGridYZ) {  // batches in grid-z slices
+    a.b0 = b0;
+    const int64_t nb = grid_b - b0 < kMaxGridYZ ? grid_b - b0 : kMaxGridYZ;
+    const dim3 grid((unsigned)((grid_t + kInterpTB - 1) / kInterpTB), (unsigned)gf,
+                    (unsigned)nb);
 #define TSSM_INTERP(TT, EE) \
-  hipLaunchKernelGGL((interp_kernel<TT, EE>), grid, dim3(kInterpThreads), 0, s, a)
-  switch (v_dtype) {
-    case TSSM_F32: if (vec) TSSM_INTERP(float, 4); else TSSM_INTERP(float, 1); break;
-    case TSSM_BF16: if (vec) TSSM_INTERP(bf16_t, 8); else TSSM_INTERP(bf16_t, 1); break;
-    default: if (vec) TSSM_INTERP(f16_t, 8); else TSSM_INTERP(f16_t, 1); break;
-  }
+  hipLaunchKernelGGL((interp_kernel<TT, EE>), grid, dim3(kInterpThreads), lds_interp, s, a)
+    switch (v_dtype) {
+      case TSSM_F32: if (vec) TSSM_INTERP(float, 4); else TSSM_INTERP(float, 1); break;
+      case TSSM_BF16: if (vec) TSSM_INTERP(bf16_t, 8); else TSSM_INTERP(bf16_t, 1); break;
+      default: if (vec) TSSM_INTERP(f16_t, 8); else TSSM_INTERP(f16_t, 1); break;
+    }
 #undef TSSM_INTERP
-  return launch_status();
+    const int st2 = launch_status();
+    if (st2 != TSSM_OK) return st2;
+  }
+  return TSSM_OK;
 }
 
 extern "C" int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, const void* V,
@@ -648,29 +664,38 @@ extern "C" int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, con
   TSSM_CHECK(nbatch >= 0 && T > 0 && F >= 0 && FTILE > 0 && K >= 0, TSSM_ERR_SHAPE);
   TSSM_CHECK(t_cur >= 0 && t_cur < T, TSSM_ERR_SHAPE);
   TSSM_CHECK(grid_b >= 0 && grid_f >= 0 && grid_b <= nbatch, TSSM_ERR_SHAPE);
-  TSSM_CHECK(K <= kMaxK, TSSM_ERR_UNSUPPORTED);
+  // LDS: the 2K+1 candidate rows' timestamps (fast kernel) and flags
+  const bool fast = FTILE <= kInterpThreads;  // one thread per feature: every load up front
+  const size_t lds = fast ? (size_t)(2 * K + 1) * 5 : (size_t)(2 * K + 1);
+  TSSM_CHECK(K <= kMaxLds && (int64_t)lds + 64 <= kMaxLds, TSSM_ERR_UNSUPPORTED);
   const int64_t ntile = (F + FTILE - 1) / FTILE;
   const int64_t gf = grid_f < ntile ? grid_f : ntile;
   if (grid_b == 0 || gf == 0) return TSSM_OK;
-  TSSM_CHECK(gf <= 2147483647 && grid_b <= 65535, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(gf <= 2147483647, TSSM_ERR_UNSUPPORTED);
   StepArgs a{V, M, tau, A_bar, B_bar, h_in, Vhat, h_out, m_dtype, tau_dtype, nbatch, T, F,
-             svb, svt, smb, smt, stb, stt, sob, sot, s_hib, s_hob, t_cur, K, FTILE};
-  const dim3 grid((unsigned)gf, (unsigned)grid_b);
+             svb, svt, smb, smt, stb, stt, sob, sot, s_hib, s_hob, t_cur, K, FTILE, 0};
   const hipStream_t s = as_stream(stream);
-  if (FTILE <= kInterpThreads) {  // one thread per feature: every load up front
-    switch (v_dtype) {
-      case TSSM_F32: hipLaunchKernelGGL(interp_step_fast_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
-      case TSSM_BF16: hipLaunchKernelGGL(interp_step_fast_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
-      default: hipLaunchKernelGGL(interp_step_fast_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+  for (int64_t b0 = 0; b0 < grid_b; b0 += kMaxGridYZ) {  // batches in grid-y slices
+    a.b0 = b0;
+    const int64_t nb = grid_b - b0 < kMaxGridYZ ? grid_b - b0 : kMaxGridYZ;
+    const dim3 grid((unsigned)gf, (unsigned)nb);
+    if (fast) {
+      switch (v_dtype) {
+        case TSSM_F32: hipLaunchKernelGGL(interp_step_fast_kernel<float>, grid, dim3(kInterpThreads), lds, s, a); break;
+        case TSSM_BF16: hipLaunchKernelGGL(interp_step_fast_kernel<bf16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+        default: hipLaunchKernelGGL(interp_step_fast_kernel<f16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+      }
+    } else {
+      switch (v_dtype) {
+        case TSSM_F32: hipLaunchKernelGGL(interp_step_kernel<float>, grid, dim3(kInterpThreads), lds, s, a); break;
+        case TSSM_BF16: hipLaunchKernelGGL(interp_step_kernel<bf16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+        default: hipLaunchKernelGGL(interp_step_kernel<f16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+      }
     }
-    return launch_status();
+    const int st = launch_status();
+    if (st != TSSM_OK) return st;
   }
-  switch (v_dtype) {
-    case TSSM_F32: hipLaunchKernelGGL(interp_step_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
-    case TSSM_BF16: hipLaunchKernelGGL(interp_step_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL(interp_step_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
-  }
-  return launch_status();
+  return TSSM_OK;
 }
 
 extern "C" int tssm_time_aware_interp_corrected(int v_dtype, int m_dtype, int tau_dtype,
@@ -683,18 +708,26 @@ extern "C" int tssm_time_aware_interp_corrected(int v_dtype, int m_dtype, int ta
   TSSM_CHECK(float_dtype(v_dtype) && float_dtype(m_dtype) && float_dtype(tau_dtype),
              TSSM_ERR_DTYPE);
   TSSM_CHECK(nbatch >= 0 && T >= 0 && F >= 0 && K >= 0, TSSM_ERR_SHAPE);
-  TSSM_CHECK(K <= kMaxK, TSSM_ERR_UNSUPPORTED);
+  // LDS: timestamps and per-feature flags of kCorrTB + 2K rows (K up to 449)
+  const size_t lds = (size_t)(kCorrTB + 2 * K) * (4 + 64);
+  TSSM_CHECK(K <= kMaxLds && (int64_t)lds <= kMaxLds, TSSM_ERR_UNSUPPORTED);
   if (nbatch == 0 || T == 0 || F == 0) return TSSM_OK;
   const int64_t gx = (T + kCorrTB - 1) / kCorrTB, gy = (F + 63) / 64;
-  TSSM_CHECK(gx <= 2147483647 && gy <= 65535 && nbatch <= 65535, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(gx <= 2147483647 && gy <= kMaxGridYZ, TSSM_ERR_UNSUPPORTED);
   InterpArgs a{V, M, tau, Vhat, nullptr, m_dtype, tau_dtype, T, F, svb, svt, smb, smt, stb, stt,
-               sob, sot, K, 1, T, T, 0};
-  const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)nbatch);
+               sob, sot, K, 1, T, T, 0, 0};
   const hipStream_t s = as_stream(stream);
-  switch (v_dtype) {
-    case TSSM_F32: hipLaunchKernelGGL(interp_corrected_kernel<float>, grid, dim3(kInterpThreads), 0, s, a); break;
-    case TSSM_BF16: hipLaunchKernelGGL(interp_corrected_kernel<bf16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL(interp_corrected_kernel<f16_t>, grid, dim3(kInterpThreads), 0, s, a); break;
+  for (int64_t b0 = 0; b0 < nbatch; b0 += kMaxGridYZ) {  // batches in grid-z slices
+    a.b0 = b0;
+    const int64_t nb = nbatch - b0 < kMaxGridYZ ? nbatch - b0 : kMaxGridYZ;
+    const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)nb);
+    switch (v_dtype) {
+      case TSSM_F32: hipLaunchKernelGGL(interp_corrected_kernel<float>, grid, dim3(kInterpThreads), lds, s, a); break;
+      case TSSM_BF16: hipLaunchKernelGGL(interp_corrected_kernel<bf16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+      default: hipLaunchKernelGGL(interp_corrected_kernel<f16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+    }
+    const int st = launch_status();
+    if (st != TSSM_OK) return st;
   }
-  return launch_status();
+  return TSSM_OK;
 }

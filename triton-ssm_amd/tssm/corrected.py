@@ -34,8 +34,8 @@ def time_aware_interp_corrected(V: torch.Tensor, M: torch.Tensor, tau: torch.Ten
     if V.dim() != 3 or M.shape != V.shape or tau.dim() != 2 or tuple(tau.shape) != V.shape[:2]:
         raise ValueError("expected V, M [B,T,F] and tau [B,T]")
     K = int(K)
-    if not 0 <= K <= 64:
-        raise ValueError("K must be in [0, 64]")
+    if not 0 <= K <= 449:   # the workgroup's LDS holds flags of 64 + 2K rows
+        raise ValueError("K must be in [0, 449]")
     Bsz, T, F = V.shape
     if V.stride(2) != 1 or M.stride(2) != 1:
         raise ValueError("V and M need a unit feature stride")
