@@ -681,6 +681,8 @@ def main():
 
     total_ms, _ = timed(False)        # the measured K steps, back to back
     _, per = timed(True)              # per-step events: p50 latency only
+    import tssm
+    tssm.check()   # raises if a bounded look-back wait expired in any run above
     ms_per_step = total_ms / args.steps
     # Roofline: the kernels of a step run back to back on the launch stream,
     # so the timed region's average is their average launch duration (an

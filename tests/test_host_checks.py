@@ -4,6 +4,8 @@ No GPU compute: every bad argument must raise before any library call, and
 ``tssm.check`` must turn a set sticky flag into ``TssmError`` (the flag is
 faked through the library call it reads it with).
 """
+import contextlib
+
 import pytest
 import torch
 
@@ -69,6 +71,7 @@ def test_check_raises_on_a_set_flag(monkeypatch):
     sd = torch.zeros(256, dtype=torch.uint8)
     monkeypatch.setattr(_lib, "call", fake_call)
     monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    monkeypatch.setattr(torch.cuda, "device", lambda d: contextlib.nullcontext())
     monkeypatch.setattr(workspace, "_cache", {(0, 7, workspace.LOOKBACK): lb,
                                               (0, 7, workspace.SSD): sd})
     workspace.check()                      # nothing set
@@ -84,6 +87,10 @@ def test_check_raises_on_a_set_flag(monkeypatch):
         workspace.check(device=0, clear=False)
     with pytest.raises(_lib.TssmError):    # still set: clear=False kept it
         tssm.check()
+    flags[None] = 1                        # the no-allocation scratch (workspace NULL)
+    with pytest.raises(_lib.TssmError, match="no-allocation scratch"):
+        workspace.check()
+    workspace.check()
 
 
 def test_workspace_kinds_are_distinct():

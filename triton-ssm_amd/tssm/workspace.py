@@ -19,7 +19,8 @@ more; launches on different streams therefore never share one.
 A bounded look-back wait that expires (a predecessor tile that never
 published, ~1 s of polling) sets the sticky flag and the kernel finishes with
 that tile's carry incomplete.  ``check()`` synchronises, reads every lookback
-workspace's flag and raises ``TssmError`` if one is set.
+workspace's flag (and the no-allocation scratch's) and raises ``TssmError``
+if one is set.
 """
 from __future__ import annotations
 
@@ -66,10 +67,11 @@ def check(device: torch.device | int | None = None, clear: bool = True) -> None:
     """Synchronise and raise ``TssmError`` if a look-back wait expired.
 
     Reads the sticky flag of every lookback workspace (of ``device``, or of
-    every device when None).  A set flag means that some launch on that
-    workspace since the last check produced outputs without its full carry;
-    the flag is cleared (with ``clear``) before raising, so later launches can
-    be checked afresh.
+    every device when None) and of the no-allocation entry point's scratch on
+    those devices and the current one.  A set flag means that some launch on
+    that workspace since the last check produced outputs without its full
+    carry; the flag is cleared (with ``clear``) before raising, so later
+    launches can be checked afresh.
     """
     want = None if device is None else (device if isinstance(device, int) else
                                         _dev_index(torch.device(device)))
@@ -81,6 +83,18 @@ def check(device: torch.device | int | None = None, clear: bool = True) -> None:
         torch.cuda.synchronize(dev_idx)
         if error_flag(buf, clear):
             bad.append(f"device {dev_idx} stream {stream:#x}")
+    devs = {k[0] for k, _ in items}
+    if want is not None:
+        devs.add(want)
+    elif torch.cuda.is_initialized():
+        devs.add(torch.cuda.current_device())
+    for dev_idx in sorted(devs):
+        with torch.cuda.device(dev_idx):
+            torch.cuda.synchronize(dev_idx)
+            out = ctypes.c_int(0)
+            _lib.call("tssm_workspace_error", None, int(clear), ctypes.byref(out))
+            if out.value:
+                bad.append(f"device {dev_idx} no-allocation scratch")
     if bad:
         raise _lib.TssmError(
             "a bounded look-back wait expired (a predecessor tile never published its carry); "
