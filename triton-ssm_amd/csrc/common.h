@@ -70,6 +70,34 @@ __device__ inline float ld_any(const void* p, int64_t i, int dt) {
 }
 
 // 8 consecutive channels as one vector load: 16 B for bf16/fp16, 32 B for fp32.
+// Raw buffer loads: a descriptor for a uniform base (scalar registers), a
+// per-lane byte offset (VGPR) and a uniform byte offset (SGPR), so per-step
+// offsets of a tile cost no vector instructions.  The range covers 2^31 bytes
+// from the base; callers keep every offset below that.
+__device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+constexpr int kBufNt = 2;  // cache policy bit: non-temporal
+__device__ inline uint4 buf_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, int32_t soff) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, soff, kBufNt);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <typename T> __device__ inline float buf_ldf(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                      int32_t soff);
+template <> __device__ inline float buf_ldf<float>(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                   int32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, soff, 0));
+}
+template <> __device__ inline float buf_ldf<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                    int32_t soff) {
+  return bf16_bits_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, soff, 0));
+}
+template <> __device__ inline float buf_ldf<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                   int32_t soff) {
+  return (float)__builtin_bit_cast(f16_t, __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, soff, 0));
+}
+
 template <typename T> struct Vec8;
 // load_nt: non-temporal (streamed once, not kept in the caches).
 __device__ inline uint4 ld_nt16(const void* p) {
@@ -80,6 +108,9 @@ template <> struct Vec8<bf16_t> {
   uint4 raw;
   __device__ inline void load(const bf16_t* p) { raw = *reinterpret_cast<const uint4*>(p); }
   __device__ inline void load_nt(const bf16_t* p) { raw = ld_nt16(p); }
+  __device__ inline void load_nt(__amdgpu_buffer_rsrc_t r, uint32_t vo, int32_t so) {
+    raw = buf_ld16_nt(r, vo, so);
+  }
   __device__ inline void zero() { raw = make_uint4(0, 0, 0, 0); }
   __device__ inline float get(int j) const {
     uint32_t w = (&raw.x)[j >> 1];
@@ -90,6 +121,9 @@ template <> struct Vec8<f16_t> {
   uint4 raw;
   __device__ inline void load(const f16_t* p) { raw = *reinterpret_cast<const uint4*>(p); }
   __device__ inline void load_nt(const f16_t* p) { raw = ld_nt16(p); }
+  __device__ inline void load_nt(__amdgpu_buffer_rsrc_t r, uint32_t vo, int32_t so) {
+    raw = buf_ld16_nt(r, vo, so);
+  }
   __device__ inline void zero() { raw = make_uint4(0, 0, 0, 0); }
   __device__ inline float get(int j) const {
     uint32_t w = (&raw.x)[j >> 1];
@@ -105,6 +139,11 @@ template <> struct Vec8<float> {
   }
   __device__ inline void load_nt(const float* p) {
     const uint4 a = ld_nt16(p), b = ld_nt16(p + 4);
+    lo = make_float4(__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z), __uint_as_float(a.w));
+    hi = make_float4(__uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), __uint_as_float(b.w));
+  }
+  __device__ inline void load_nt(__amdgpu_buffer_rsrc_t r, uint32_t vo, int32_t so) {
+    const uint4 a = buf_ld16_nt(r, vo, so), b = buf_ld16_nt(r, vo + 16, so);
     lo = make_float4(__uint_as_float(a.x), __uint_as_float(a.y), __uint_as_float(a.z), __uint_as_float(a.w));
     hi = make_float4(__uint_as_float(b.x), __uint_as_float(b.y), __uint_as_float(b.z), __uint_as_float(b.w));
   }

@@ -60,6 +60,9 @@ struct MhArgs {
   uint32_t tag;
   uint32_t spin_limit;
   uint32_t dt_is_tau;    // dt holds timestamps: dt_t = tau_t - tau_{t-1}, dt_0 = tau_0
+  // Every operand's per-lane offset within a tile (steps x row stride +
+  // column, in bytes) fits in 31 bits: full tiles take the scalar-base loads.
+  uint32_t off32 = 0;
   // MODE_MAMBA1 only: dt projected in the load stage,
   // dt[b,t,d] = clamp(softplus(sum_k dt[b,t,k] W[k,d] + bias[d]), dt_min, dt_max)
   // with `dt` then holding the raw rows [B, L, dt_rank] (strides sdt_b, sdt_l, 1).
@@ -165,67 +168,105 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   Vec8<T> vu[R], vB[R], vC[R];
   float us[R];  // MODE_MAMBA1: the channel's input, shared by its 8 state lanes
   float dtv[R];
+  // A full tile (every tile of a row but the last) with 32-bit lane offsets:
+  // each load is a uniform per-step base plus one per-lane byte offset
+  // (global_load with a scalar base), so addresses take no per-step vector
+  // arithmetic and no clamps.  Otherwise steps past the end read row L-1
+  // instead (no branch around the loads, so no wait between them) and become
+  // identity steps through dt = 0: Abar = 1 and a zero input term whatever u,
+  // B and C hold.
+  const bool fast = a.off32 && tw + TC <= a.L;
+  // With one dt row per tile row (CPR == 1) and the wave's steps fitting in
+  // its lanes, lane k loads the dt of the wave's k-th step and the threads
+  // take theirs by lane shuffles: one load instruction per wave instead of
+  // R (measured +2% of HBM peak on this tile's traffic).
+  constexpr int WSTEPS = ROWS * R;  // steps covered by one wave
+  constexpr bool DT_SHFL = CPR == 1 && WSTEPS <= 64;
   {
     const int bc = (g % NS) * 8;  // offset within the group's B/C row
-    // bases at step 0 (uniform part + lane column); B/C head stride is 0 in
-    // MODE_MAMBA1 (shared by all channels)
-    const T* ub = reinterpret_cast<const T*>(a.u) + b * a.su_b +
-                  (MODE == MODE_DIAG ? (int64_t)h * P + ch0 : (int64_t)h * CPR + cl);
-    const T* Bb = reinterpret_cast<const T*>(a.B) + b * a.sB_b + (int64_t)h * CPR * a.sB_h +
-                  lane_mul(cl, a.sB_h) + bc;
-    const T* Cb = reinterpret_cast<const T*>(a.C) + b * a.sC_b + (int64_t)h * CPR * a.sC_h +
-                  lane_mul(cl, a.sC_h) + bc;
-    const float* db = a.dt + b * a.sdt_b + (int64_t)h * CPR * a.sdt_h + lane_mul(cl, a.sdt_h);
-    const T* up = ub + tw * a.su_l + lane_mul(tr, a.su_l);
-    const T* Bp = Bb + tw * a.sB_l + lane_mul(tr, a.sB_l);
-    const T* Cp = Cb + tw * a.sC_l + lane_mul(tr, a.sC_l);
-    const float* dp = db + tw * a.sdt_l + lane_mul(tr, a.sdt_l);
-    // Steps past the end read row L-1 instead (no branch around the loads, so
-    // no wait between them) and become identity steps through dt = 0:
-    // Abar = 1 and a zero input term whatever u, B and C hold.
-    const int64_t tl = a.L - 1;
-    const T* up_l = ub + tl * a.su_l;
-    const T* Bp_l = Bb + tl * a.sB_l;
-    const T* Cp_l = Cb + tl * a.sC_l;
-    const float* dp_l = db + tl * a.sdt_l;
-    // With one dt row per tile row (CPR == 1) and the wave's steps fitting in
-    // its lanes, lane k loads the dt of the wave's k-th step and the threads
-    // take theirs by lane shuffles: one load instruction per wave instead of
-    // R (measured +2% of HBM peak on this tile's traffic).
-    constexpr int WSTEPS = ROWS * R;  // steps covered by one wave
-    constexpr bool DT_SHFL = CPR == 1 && WSTEPS <= 64;
+    // uniform row bases (B/C head stride is 0 in MODE_MAMBA1: shared by all
+    // channels) and the lane's column within the row
+    const T* ur = reinterpret_cast<const T*>(a.u) + b * a.su_b +
+                  (MODE == MODE_DIAG ? (int64_t)h * P : (int64_t)h * CPR);
+    const T* Br = reinterpret_cast<const T*>(a.B) + b * a.sB_b + (int64_t)h * CPR * a.sB_h;
+    const T* Cr = reinterpret_cast<const T*>(a.C) + b * a.sC_b + (int64_t)h * CPR * a.sC_h;
+    const float* dr = a.dt + b * a.sdt_b + (int64_t)h * CPR * a.sdt_h;
+    const int64_t ucol = MODE == MODE_DIAG ? ch0 : cl;
+    const int64_t Bcol = lane_mul(cl, a.sB_h) + bc;
+    const int64_t Ccol = lane_mul(cl, a.sC_h) + bc;
+    const int64_t dcol = lane_mul(cl, a.sdt_h);
     float draw[DT_SHFL ? 1 : R];
-    float dlane = 0.0f, tprev_lane = 0.0f;
-    if constexpr (DT_SHFL) {
-      const int64_t tk = tw + (int64_t)wave * WSTEPS + lane;  // this lane's step
-      if (lane < WSTEPS && !dtp) {
-        dlane = *(tk < a.L ? db + tk * a.sdt_l : dp_l);
-        // timestamp of step tk - 1 (0 before the first step)
-        if (a.dt_is_tau && tk > 0) tprev_lane = *(tk <= a.L ? db + (tk - 1) * a.sdt_l : dp_l);
+    float dlane = 0.0f, tprev_lane = 0.0f, tprev = 0.0f;
+    const int64_t tk = tw + (int64_t)wave * WSTEPS + lane;  // DT_SHFL: this lane's step
+    if (fast) {
+      // one descriptor per operand at the tile's first step, the lane's byte
+      // offset in a VGPR, each step's in a scalar register
+      const __amdgpu_buffer_rsrc_t ru = buf_rsrc(ur + tw * a.su_l);
+      const __amdgpu_buffer_rsrc_t rB = buf_rsrc(Br + tw * a.sB_l);
+      const __amdgpu_buffer_rsrc_t rC = buf_rsrc(Cr + tw * a.sC_l);
+      const __amdgpu_buffer_rsrc_t rd = buf_rsrc(dr + tw * a.sdt_l);
+      const uint32_t uo = (uint32_t)((lane_mul(tr, a.su_l) + ucol) * (int64_t)sizeof(T));
+      const uint32_t Bo = (uint32_t)((lane_mul(tr, a.sB_l) + Bcol) * (int64_t)sizeof(T));
+      const uint32_t Co = (uint32_t)((lane_mul(tr, a.sC_l) + Ccol) * (int64_t)sizeof(T));
+      if constexpr (DT_SHFL) {
+        if (lane < WSTEPS && !dtp) {
+          const uint32_t ko = (uint32_t)(lane_mul((uint32_t)(wave * WSTEPS + lane), a.sdt_l) * 4);
+          dlane = buf_ldf<float>(rd, ko, 0);
+          // timestamp of step tk - 1 (0 before the first step)
+          if (a.dt_is_tau && tk > 0) tprev_lane = buf_ldf<float>(rd, ko - (uint32_t)(a.sdt_l * 4), 0);
+        }
       }
-    }
+      const uint32_t dof = (uint32_t)((lane_mul(tr, a.sdt_l) + dcol) * 4);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const bool in = t0 + r < a.L;
-      if constexpr (MODE == MODE_DIAG) vu[r].load_nt(in ? up + r * a.su_l : up_l);
-      else us[r] = ldf(in ? up + r * a.su_l : up_l);
-      vB[r].load_nt(in ? Bp + r * a.sB_l : Bp_l);
-      vC[r].load_nt(in ? Cp + r * a.sC_l : Cp_l);
-      if constexpr (!DT_SHFL) draw[r] = dtp ? 0.0f : *(in ? dp + r * a.sdt_l : dp_l);
+      for (int r = 0; r < R; ++r) {
+        const int32_t su = (int32_t)(r * a.su_l * (int64_t)sizeof(T));
+        const int32_t sb = (int32_t)(r * a.sB_l * (int64_t)sizeof(T));
+        const int32_t sc = (int32_t)(r * a.sC_l * (int64_t)sizeof(T));
+        if constexpr (MODE == MODE_DIAG) vu[r].load_nt(ru, uo, su);
+        else us[r] = buf_ldf<T>(ru, uo, su);
+        vB[r].load_nt(rB, Bo, sb);
+        vC[r].load_nt(rC, Co, sc);
+        if constexpr (!DT_SHFL)
+          draw[r] = dtp ? 0.0f : buf_ldf<float>(rd, dof, (int32_t)(r * a.sdt_l * 4));
+      }
+      // timestamp of step t0 - 1 when dt holds timestamps (row 0 for t0 = 0)
+      if (!DT_SHFL && a.dt_is_tau) tprev = *(dr + dcol + (t0 > 0 ? t0 - 1 : 0) * a.sdt_l);
+    } else {
+      const T* up = ur + ucol + tw * a.su_l + lane_mul(tr, a.su_l);
+      const T* Bp = Br + Bcol + tw * a.sB_l + lane_mul(tr, a.sB_l);
+      const T* Cp = Cr + Ccol + tw * a.sC_l + lane_mul(tr, a.sC_l);
+      const float* db = dr + dcol;
+      const float* dp = db + tw * a.sdt_l + lane_mul(tr, a.sdt_l);
+      const int64_t tl = a.L - 1;
+      const T* up_l = ur + ucol + tl * a.su_l;
+      const T* Bp_l = Br + Bcol + tl * a.sB_l;
+      const T* Cp_l = Cr + Ccol + tl * a.sC_l;
+      const float* dp_l = db + tl * a.sdt_l;
+      if constexpr (DT_SHFL) {
+        if (lane < WSTEPS && !dtp) {
+          dlane = *(tk < a.L ? db + tk * a.sdt_l : dp_l);
+          if (a.dt_is_tau && tk > 0) tprev_lane = *(tk <= a.L ? db + (tk - 1) * a.sdt_l : dp_l);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const bool in = t0 + r < a.L;
+        if constexpr (MODE == MODE_DIAG) vu[r].load_nt(in ? up + r * a.su_l : up_l);
+        else us[r] = ldf(in ? up + r * a.su_l : up_l);
+        vB[r].load_nt(in ? Bp + r * a.sB_l : Bp_l);
+        vC[r].load_nt(in ? Cp + r * a.sC_l : Cp_l);
+        if constexpr (!DT_SHFL) draw[r] = dtp ? 0.0f : *(in ? dp + r * a.sdt_l : dp_l);
+      }
+      if (!DT_SHFL && a.dt_is_tau) tprev = *(t0 == 0 ? dp : (t0 <= a.L ? dp - a.sdt_l : dp_l));
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
     if constexpr (DT_SHFL) {
-      __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
-      const int64_t tk = tw + (int64_t)wave * WSTEPS + lane;
       float d = a.dt_is_tau ? dlane - tprev_lane : dlane;
       d = tk < a.L ? d : 0.0f;  // steps past the end are identity steps
       const int src0 = (lane / G) * R;  // lane of the thread's first step
 #pragma unroll
       for (int r = 0; r < R; ++r) dtv[r] = __shfl(d, src0 + r);
     } else {
-      // timestamp of step t0 - 1 when dt holds timestamps (row 0 for t0 = 0)
-      float tprev = 0.0f;
-      if (a.dt_is_tau) tprev = *(t0 == 0 ? dp : (t0 <= a.L ? dp - a.sdt_l : dp_l));
-      __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float d = draw[r];
@@ -284,7 +325,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   }
   // ZOH with a decay per lane updates h' = ab h + (ab - 1) B u / a, which must
   // stay h at the identity steps past the end: their input is zeroed.
-  if constexpr (!APH && DISC == TSSM_DISC_ZOH) {
+  if (!APH && DISC == TSSM_DISC_ZOH && !fast) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if constexpr (MODE == MODE_MAMBA1) {
@@ -734,6 +775,22 @@ inline bool mh_diag_cfg(int64_t head_dim, int64_t n_heads, int64_t chunk, TileCf
   return true;
 }
 
+// True when every per-lane byte offset of a tile -- up to TC steps of the
+// largest row stride plus the row's columns, for the I/O operands (element
+// size esize) and for dt (fp32) -- stays below 2^31: full tiles then load
+// through a uniform base plus a 32-bit lane offset.  Strides are >= 0.
+inline bool tile_offsets_fit(int64_t TC, int64_t cpr, int64_t cols, int64_t esize, int64_t su_l,
+                             int64_t sB_l, int64_t sC_l, int64_t sB_h, int64_t sC_h,
+                             int64_t sdt_l, int64_t sdt_h) {
+  const int64_t lim = int64_t(1) << 31;
+  const int64_t sl = su_l > sB_l ? (su_l > sC_l ? su_l : sC_l) : (sB_l > sC_l ? sB_l : sC_l);
+  const int64_t sh = sB_h > sC_h ? sB_h : sC_h;
+  if (sl >= lim || sh >= lim || sdt_l >= lim || sdt_h >= lim) return false;
+  const int64_t io = (TC * sl + cpr * sh + cols + 8) * esize;
+  const int64_t dt = (TC * sdt_l + cpr * sdt_h) * 4;
+  return io < lim && dt < lim;
+}
+
 inline int64_t mh_ws_bytes(int64_t nrows, int64_t L, int64_t P, int TC) {
   return (int64_t)sizeof(WsHeader) + nrows * ((L + TC - 1) / TC) * 3 * P * 8;
 }
@@ -879,6 +936,8 @@ int mh_scan_fused_launch(int dtype, int disc, const void* u, const float* A_log,
   a.tag = tag;
   a.spin_limit = kDefaultSpinLimit;
   a.dt_is_tau = 0;
+  a.off32 = tile_offsets_fit(cfg.TC, cfg.hpr, P, dtype == TSSM_F32 ? 4 : 2, su_l, sB_l, sC_l,
+                             sB_h, sC_h, sdt_l, sdt_h) ? 1u : 0u;
 
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
   const int nrun = cfg.W * (64 / cfg.G);
@@ -1179,6 +1238,8 @@ int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, i
   a.tag = next_epoch(workspace);
   a.spin_limit = kDefaultSpinLimit;
   a.dt_is_tau = dt_is_tau ? 1u : 0u;
+  a.off32 = tile_offsets_fit(cfg.TC, cpr, P, dtype == TSSM_F32 ? 4 : 2, sx_l, sB_l, sC_l, 0, 0,
+                             sdt_l, proj.W ? 0 : sdt_d) ? 1u : 0u;
   a.dtW = proj.W; a.dtbias = proj.bias; a.sw_r = proj.sw_r; a.dt_rank = (uint32_t)proj.rank;
   a.dt_min = proj.dt_min; a.dt_max = proj.dt_max;
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
