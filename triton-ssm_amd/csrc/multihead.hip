@@ -107,9 +107,10 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   float* s_sa = s_x + NRUN * P;        // [NSEG][P] segment totals
   float* s_sx = s_sa + NSEG * P;
   float* s_carry = s_sx + NSEG * P;    // [P] state entering the tile
+  float* s_par = s_carry + P;          // [2][P] per-lane a log2(e) and 1/a (decay per lane)
   // dt projection (MODE_MAMBA1): [TC][CPR] dt values, [TC][rank] raw rows,
   // [rank][CPR] weights of the row's channels
-  float* s_dt = s_carry + P;
+  float* s_dt = s_par + 2 * P;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -143,8 +144,18 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   // the step inputs; transformed after the scheduling barrier below
   float a2[8];  // a * log2(e) per channel (or per head)
   float ia[(APH || DISC != TSSM_DISC_ZOH) ? 1 : 8];  // 1 / a per channel (ZOH)
+  // MODE_DIAG with a decay per channel: the row's P lanes share their
+  // parameters over the workgroup's runs, so thread tid < P forms lane tid's
+  // a log2(e) (and 1/a) once, into LDS, read back after the step loads are
+  // issued (measured 4% faster at the headline shape).  MODE_MAMBA1 keeps
+  // them per thread: there the extra barrier costs what the exp2s save.
+  constexpr bool PAR_LDS = !APH && MODE == MODE_DIAG;
+  float alog = 0.0f;
   if constexpr (APH) {
     a2[0] = a.A_log[chan];
+  } else if constexpr (PAR_LDS) {
+    if (tid < P) alog = a.A_log[h * P + tid];
+    __builtin_amdgcn_sched_barrier(0);  // issued before the step loads
   } else {
     const float4* ap = reinterpret_cast<const float4*>(a.A_log + h * P + ch0);
     const float4 l0 = ap[0], l1 = ap[1];
@@ -260,6 +271,31 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       if (!DT_SHFL && a.dt_is_tau) tprev = *(t0 == 0 ? dp : (t0 <= a.L ? dp - a.sdt_l : dp_l));
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
+    if constexpr (PAR_LDS) {
+      // lane parameters while the step loads are in flight: every wave
+      // reaches this barrier right after issuing its loads.  Hardware exp2 of
+      // the base-2 argument: within ~4e-7 relative of -exp(A_log), at 4
+      // operations per lane instead of a library expf.
+      if (tid < P) {
+        const float x = alog * kLog2e;
+        s_par[tid] = -exp2_fast(x) * kLog2e;
+        if constexpr (DISC == TSSM_DISC_ZOH) s_par[P + tid] = -exp2_fast(-x);
+      }
+      // nothing that waits on the step loads may move above the barrier
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      const float4* pa = reinterpret_cast<const float4*>(s_par + ch0);
+      const float4 a0 = pa[0], a1 = pa[1];
+      a2[0] = a0.x; a2[1] = a0.y; a2[2] = a0.z; a2[3] = a0.w;
+      a2[4] = a1.x; a2[5] = a1.y; a2[6] = a1.z; a2[7] = a1.w;
+      if constexpr (DISC == TSSM_DISC_ZOH) {
+        const float4* pi = reinterpret_cast<const float4*>(s_par + P + ch0);
+        const float4 i0 = pi[0], i1 = pi[1];
+        ia[0] = i0.x; ia[1] = i0.y; ia[2] = i0.z; ia[3] = i0.w;
+        ia[4] = i1.x; ia[5] = i1.y; ia[6] = i1.z; ia[7] = i1.w;
+      }
+    }
     if constexpr (DT_SHFL) {
       float d = a.dt_is_tau ? dlane - tprev_lane : dlane;
       d = tk < a.L ? d : 0.0f;  // steps past the end are identity steps
@@ -339,7 +375,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     const float v = -expf(a2[0]) * kLog2e;
 #pragma unroll
     for (int j = 0; j < 8; ++j) a2[j] = v;
-  } else {
+  } else if constexpr (!PAR_LDS) {
     // hardware exp2 of the base-2 argument: within ~4e-7 relative of
     // -exp(A_log), at 4 operations per channel instead of a library expf
 #pragma unroll
@@ -436,11 +472,24 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     s_sa[sg * P + ch] = A;
     s_sx[sg * P + ch] = X;
     __syncthreads();
-    float SA = 1.0f, SX = 0.0f;  // segments 0 .. sg-1 combined
-    for (int k = 0; k < sg; ++k) {
-      const float ka = s_sa[k * P + ch];
-      SX = __builtin_fmaf(ka, SX, s_sx[k * P + ch]);
-      SA = SA * ka;
+    // segments 0 .. sg-1 combined (sg is uniform per wave): their totals are
+    // read 4 at a time, all reads of a batch issued before the first is used
+    float SA = 1.0f, SX = 0.0f;
+    for (int k0 = 0; k0 < sg; k0 += 4) {
+      float ka[4], kx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int k = k0 + i < sg ? k0 + i : sg - 1;
+        ka[i] = s_sa[k * P + ch];
+        kx[i] = s_sx[k * P + ch];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (k0 + i < sg) {
+          SX = __builtin_fmaf(ka[i], SX, kx[i]);
+          SA = SA * ka[i];
+        }
+      }
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) {  // exclusive prefix of run q0+q within the tile
@@ -941,7 +990,7 @@ int mh_scan_fused_launch(int dtype, int disc, const void* u, const float* A_log,
 
   const dim3 grid((unsigned)(nchunks * nrows)), block((unsigned)(cfg.W * 64));
   const int nrun = cfg.W * (64 / cfg.G);
-  const size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + P) * sizeof(float);
+  const size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + 3 * P) * sizeof(float);
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr;
   const bool aph = a_per_head != 0;
@@ -1211,7 +1260,7 @@ int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, i
   const int64_t nrows = nbatch * (Dc / cpr);
   TSSM_CHECK(nchunks * nrows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
   const int nrun = cfg.W * (64 / cfg.G);
-  size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + P) * sizeof(float);
+  size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + 3 * P) * sizeof(float);
   if (proj.W) {
     TSSM_CHECK(proj.bias, TSSM_ERR_NULL);
     TSSM_CHECK(!dt_is_tau, TSSM_ERR_UNSUPPORTED);
