@@ -23,7 +23,10 @@ def _inputs(Bsz, T, F, dtype, mdtype, p, seed, dev):
     (2, 150, 100, 10, 0.3, torch.float32, torch.float32),
     (3, 64, 64, 5, 0.05, torch.bfloat16, torch.bfloat16),
     (1, 300, 130, 64, 0.02, torch.float32, torch.float16),     # K = 64, ragged tiles
-    (2, 70, 7, 0, 0.5, torch.float16, torch.float32)])          # K = 0: identity
+    (2, 70, 7, 0, 0.5, torch.float16, torch.float32),           # K = 0: identity
+    (2, 200, 256, 10, 0.3, torch.float32, torch.float32),       # 16-byte staging path
+    (1, 333, 128, 64, 0.05, torch.float32, torch.float32),      # 16-byte staging, K = 64
+    (1, 150, 128, 80, 0.02, torch.float32, torch.float32)])     # window past LDS staging
 def test_interp_corrected(dev, Bsz, T, F, K, p, dtype, mdtype):
     from tssm import time_aware_interp_corrected
     V, M, tau = _inputs(Bsz, T, F, dtype, mdtype, p, 10 + K, dev)

@@ -540,6 +540,152 @@ __global__ __launch_bounds__(kInterpThreads) void interp_corrected_kernel(Interp
   }
 }
 
+// Staged form for windows whose V rows fit in LDS beside the flags (324 bytes
+// per window row, K up to 69): the flags, tau and V of rows t0-K .. t0+63+K are
+// loaded as coalesced rows, kCorrBatch rows per wave in flight, and every step
+// is then resolved from LDS.  The direct form above reads V behind each step's
+// data-dependent branch, one step at a time per wave.  VEC (fp32 V and M,
+// 16-byte rows, whole 64-feature tiles): 16 lanes stage a row with 16-byte
+// loads, so one wave instruction covers 4 rows.
+constexpr int kCorrBatch = 8;
+
+__host__ __device__ constexpr int64_t corr_staged_lds(int64_t K) {
+  return ((kCorrTB + 2 * K + 3) / 4 * 4) * 4 + (kCorrTB + 2 * K) * (64 * 4 + 64);
+}
+
+template <typename TV, bool VEC>
+__global__ __launch_bounds__(kInterpThreads) void interp_corrected_staged_kernel(InterpArgs a) {
+  extern __shared__ float s_tau[];  // [nrow (padded)], then V [nrow][64], then flags [nrow][64]
+  const int K = (int)a.K;
+  const int nrow = kCorrTB + 2 * K;
+  const int npad = (nrow + 3) / 4 * 4;
+  float (*s_v)[64] = reinterpret_cast<float (*)[64]>(s_tau + npad);
+  auto s_obs = reinterpret_cast<unsigned char (*)[64]>(s_tau + npad + nrow * 64);
+  constexpr int NW = kInterpThreads / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * kCorrTB;
+  const int64_t f = (int64_t)blockIdx.y * 64 + lane;
+  const int64_t b = a.b0 + blockIdx.z;
+  const bool fok = f < a.F;
+  const int64_t fs = fok ? f : 0;
+  const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb + fs;
+  if constexpr (VEC) {
+    // lane = (row of 4 within the wave instruction, 4 features): rows
+    // 4 (wave + NW q) + lane / 16 of the window
+    const int rl = lane >> 4, c4 = (lane & 15) * 4;
+    const int64_t f0 = (int64_t)blockIdx.y * 64 + c4;
+    const float* Vq = reinterpret_cast<const float*>(a.V) + b * a.svb + f0;
+    const float* Mq = reinterpret_cast<const float*>(a.M) + b * a.smb + f0;
+    for (int q0 = 0; q0 * 4 * NW < nrow; q0 += kCorrBatch) {
+      float4 mv[kCorrBatch], vv[kCorrBatch];
+#pragma unroll
+      for (int q = 0; q < kCorrBatch; ++q) {  // rows out of range read row 0, discarded below
+        const int i = 4 * (wave + NW * (q0 + q)) + rl;
+        const int64_t t = t0 - K + i;
+        const int64_t tc = (t >= 0 && t < a.T) ? t : 0;
+        mv[q] = *reinterpret_cast<const float4*>(Mq + tc * a.smt);
+        vv[q] = *reinterpret_cast<const float4*>(Vq + tc * a.svt);
+      }
+#pragma unroll
+      for (int q = 0; q < kCorrBatch; ++q) {
+        const int i = 4 * (wave + NW * (q0 + q)) + rl;
+        if (i < nrow) {
+          const int64_t t = t0 - K + i;
+          const bool in = t >= 0 && t < a.T;
+          const uint32_t fl = in ? ((mv[q].x > 0.5f ? 1u : 0u) | (mv[q].y > 0.5f ? 0x100u : 0u) |
+                                    (mv[q].z > 0.5f ? 0x10000u : 0u) | (mv[q].w > 0.5f ? 0x1000000u : 0u))
+                                 : 0u;
+          *reinterpret_cast<uint32_t*>(&s_obs[i][c4]) = fl;
+          *reinterpret_cast<float4*>(&s_v[i][c4]) = vv[q];
+        }
+      }
+    }
+    for (int i = tid; i < nrow; i += kInterpThreads) {
+      const int64_t t = t0 - K + i;
+      s_tau[i] = (t >= 0 && t < a.T) ? ld_any(a.tau, b * a.stb + t * a.stt, a.td) : 0.0f;
+    }
+  } else {
+  for (int i0 = wave; i0 < nrow; i0 += NW * kCorrBatch) {
+    float mv[kCorrBatch], vv[kCorrBatch], tv[kCorrBatch];
+#pragma unroll
+    for (int q = 0; q < kCorrBatch; ++q) {  // rows out of range read row 0, discarded below
+      const int64_t t = t0 - K + i0 + NW * q;
+      const int64_t tc = (t >= 0 && t < a.T) ? t : 0;
+      mv[q] = ld_any(a.M, b * a.smb + tc * a.smt + fs, a.md);
+      vv[q] = ldf(V + tc * a.svt);
+      tv[q] = lane == 0 ? ld_any(a.tau, b * a.stb + tc * a.stt, a.td) : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < kCorrBatch; ++q) {
+      const int i = i0 + NW * q;
+      if (i < nrow) {
+        const int64_t t = t0 - K + i;
+        const bool in = t >= 0 && t < a.T;
+        s_obs[i][lane] = (in && fok && mv[q] > 0.5f) ? 1 : 0;
+        s_v[i][lane] = vv[q];
+        if (lane == 0) s_tau[i] = in ? tv[q] : 0.0f;
+      }
+    }
+  }
+  }
+  __syncthreads();
+  if (!fok) return;  // after the only barrier
+  TV* O = reinterpret_cast<TV*>(a.Vhat) + b * a.sob + f;
+  // value of step t (row i of the window) from the nearest observed rows kp
+  // before and kn after it (0: none within K).  The weight's division is a
+  // hardware reciprocal (about 1 ulp) times the numerator.
+  auto resolve = [&](int i, int kp, int kn) {
+    if (kp > 0 && kn > 0) {
+      const float tp = s_tau[i - kp], tn = s_tau[i + kn], den = tn - tp;
+      float w = den > 1e-9f ? (s_tau[i] - tp) * __builtin_amdgcn_rcpf(den) : 0.5f;
+      w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+      return (1.0f - w) * s_v[i - kp][lane] + w * s_v[i + kn][lane];
+    }
+    return kp > 0 ? s_v[i - kp][lane] : (kn > 0 ? s_v[i + kn][lane] : s_v[i][lane]);
+  };
+  constexpr int JW = kCorrTB / NW;  // consecutive steps per wave
+  const int jw = wave * JW;
+  if (JW + 2 * K <= 64) {
+    // the wave's rows jw .. jw + JW + 2K - 1 as one observed-bit mask per lane:
+    // the nearest observed row on each side is a leading/trailing-zero count
+    uint64_t mask = 0;
+    for (int r = 0; r < JW + 2 * K; ++r) mask |= (uint64_t)s_obs[jw + r][lane] << r;
+    const uint64_t lowK = (uint64_t(1) << K) - 1;
+    for (int jj = 0; jj < JW; ++jj) {
+      const int64_t t = t0 + jw + jj;
+      if (t >= a.grid_t) break;
+      const int r = K + jj;  // bit of step t; its row in the window is jw + r
+      float v;
+      if ((mask >> r) & 1) {
+        v = s_v[jw + r][lane];
+      } else {
+        const uint64_t below = (mask >> (r - K)) & lowK;  // bit p: row r - K + p
+        const uint64_t above = (mask >> (r + 1)) & lowK;  // bit p: row r + 1 + p
+        const int kp = below ? K - (63 - __builtin_clzll(below)) : 0;
+        const int kn = above ? __builtin_ctzll(above) + 1 : 0;
+        v = resolve(jw + r, kp, kn);
+      }
+      stf(O + t * a.sot, v);
+    }
+  } else {
+    for (int j = wave; j < kCorrTB; j += NW) {
+      const int64_t t = t0 + j;
+      if (t >= a.grid_t) break;
+      const int i = K + j;  // row of step t in the staged window
+      float v = s_v[i][lane];
+      if (!s_obs[i][lane]) {
+        int kp = 0, kn = 0;
+        for (int k = 1; k <= K && kp == 0; ++k)
+          if (s_obs[i - k][lane]) kp = k;
+        for (int k = 1; k <= K && kn == 0; ++k)
+          if (s_obs[i + k][lane]) kn = k;
+        v = resolve(i, kp, kn);
+      }
+      stf(O + t * a.sot, v);
+    }
+  }
+}
+
 }  // namespace tssm
 
 using namespace tssm;
@@ -717,14 +863,30 @@ extern "C" int tssm_time_aware_interp_corrected(int v_dtype, int m_dtype, int ta
   InterpArgs a{V, M, tau, Vhat, nullptr, m_dtype, tau_dtype, T, F, svb, svt, smb, smt, stb, stt,
                sob, sot, K, 1, T, T, 0, 0};
   const hipStream_t s = as_stream(stream);
+  // V staged in LDS with the flags when the window fits (K up to 69)
+  const int64_t lds_st = corr_staged_lds(K);
+  const bool staged = lds_st <= kMaxLds;
+  // 16-byte staging: fp32 V and M, rows and bases 16-byte aligned, whole tiles
+  const bool vec = v_dtype == TSSM_F32 && m_dtype == TSSM_F32 && F % 64 == 0 && svt % 4 == 0 &&
+                   svb % 4 == 0 && smt % 4 == 0 && smb % 4 == 0 && aligned(V, 16) && aligned(M, 16);
   for (int64_t b0 = 0; b0 < nbatch; b0 += kMaxGridYZ) {  // batches in grid-z slices
     a.b0 = b0;
     const int64_t nb = nbatch - b0 < kMaxGridYZ ? nbatch - b0 : kMaxGridYZ;
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)nb);
-    switch (v_dtype) {
-      case TSSM_F32: hipLaunchKernelGGL(interp_corrected_kernel<float>, grid, dim3(kInterpThreads), lds, s, a); break;
-      case TSSM_BF16: hipLaunchKernelGGL(interp_corrected_kernel<bf16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
-      default: hipLaunchKernelGGL(interp_corrected_kernel<f16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+    if (staged && vec) {
+      hipLaunchKernelGGL((interp_corrected_staged_kernel<float, true>), grid, dim3(kInterpThreads), lds_st, s, a);
+    } else if (staged) {
+      switch (v_dtype) {
+        case TSSM_F32: hipLaunchKernelGGL((interp_corrected_staged_kernel<float, false>), grid, dim3(kInterpThreads), lds_st, s, a); break;
+        case TSSM_BF16: hipLaunchKernelGGL((interp_corrected_staged_kernel<bf16_t, false>), grid, dim3(kInterpThreads), lds_st, s, a); break;
+        default: hipLaunchKernelGGL((interp_corrected_staged_kernel<f16_t, false>), grid, dim3(kInterpThreads), lds_st, s, a); break;
+      }
+    } else {
+      switch (v_dtype) {
+        case TSSM_F32: hipLaunchKernelGGL(interp_corrected_kernel<float>, grid, dim3(kInterpThreads), lds, s, a); break;
+        case TSSM_BF16: hipLaunchKernelGGL(interp_corrected_kernel<bf16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+        default: hipLaunchKernelGGL(interp_corrected_kernel<f16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+      }
     }
     const int st = launch_status();
     if (st != TSSM_OK) return st;
