@@ -53,7 +53,9 @@ def test_interp_corrected_strided_and_out(dev):
         time_aware_interp_corrected(V, M, tau, K=450)
 
 
-@pytest.mark.parametrize("S,H,KR", [(3, 100, 5), (4, 1000, 11), (2, 64, 24)])   # 24: slot walk
+@pytest.mark.parametrize("S,H,KR", [(3, 100, 5), (4, 1000, 11),   # 16-byte rows
+                                    (3, 130, 17),                 # H % 4 != 0: scalar rows
+                                    (2, 64, 24)])                 # 24: slot walk
 def test_streaming_corrected(dev, S, H, KR):
     from tssm import streaming_interp_step_corrected
     g = torch.Generator().manual_seed(S + H)

@@ -288,6 +288,67 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_corrected_k
   }
 }
 
+// Vector form for 16-byte-aligned rows (H % 4 == 0, KRING <= 17): a thread
+// owns 4 consecutive features and issues every load that does not depend on
+// the search -- v_new, m_new, h, the parameters and the masks of all previous
+// slots -- at once; only V of the chosen slots follows.  Same results as the
+// kernel above.
+__device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ inline void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ inline float comp(const float4& v, int e) {
+  return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+}
+
+__global__ __launch_bounds__(kStreamThreads) void stream_interp_step_corrected_vec_kernel(RingArgs a) {
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t KR = a.KRING;
+  const int64_t nh = (a.ring_head[b] + 1) % KR;
+  float* rV = a.ring_V + b * a.srb;
+  float* rM = a.ring_M + b * a.srb;
+  for (int64_t f = 4 * tid; f < a.H; f += 4 * kStreamThreads) {
+    const float4 vn = ld4(a.v_new + b * a.svb + f);
+    const float4 mn = ld4(a.m_new + b * a.svb + f);
+    const float4 hp = ld4(a.h + b * a.shb + f);
+    const float4 ab = ld4(a.Abar + f), bb = ld4(a.Bbar + f), dd = ld4(a.D + f);
+    const float4 cc = ld4(a.C + b * a.scb + f);
+    float4 ms[kRingFast];
+#pragma unroll
+    for (int k = 1; k <= kRingFast; ++k) {
+      const int64_t kk = k < KR ? k : KR - 1;  // clamped, ignored below
+      ms[k - 1] = ld4(rM + ((nh - kk + KR) % KR) * a.srk + f);
+    }
+    st4(rV + nh * a.srk + f, vn);  // the new slot: not among the slots searched
+    st4(rM + nh * a.srk + f, mn);
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      int64_t hit = -1;
+#pragma unroll
+      for (int k = kRingFast; k >= 1; --k)  // nearest observed slot kept
+        if (k < KR && comp(ms[k - 1], e) > 0.5f) hit = (nh - k + KR) % KR;
+      v[e] = comp(vn, e);
+      if (!(comp(mn, e) > 0.5f) && hit >= 0) v[e] = rV[hit * a.srk + f + e];
+    }
+    float4 hn, yo;
+    hn.x = ab.x * hp.x + bb.x * v[0];
+    hn.y = ab.y * hp.y + bb.y * v[1];
+    hn.z = ab.z * hp.z + bb.z * v[2];
+    hn.w = ab.w * hp.w + bb.w * v[3];
+    yo.x = cc.x * hn.x + dd.x * v[0];
+    yo.y = cc.y * hn.y + dd.y * v[1];
+    yo.z = cc.z * hn.z + dd.z * v[2];
+    yo.w = cc.w * hn.w + dd.w * v[3];
+    st4(a.h + b * a.shb + f, hn);
+    st4(a.y + b * a.svb + f, yo);
+  }
+  __syncthreads();  // every thread has read the head before it advances
+  if (tid == 0) {
+    a.ring_tau[b * KR + nh] = a.tau_new[b];
+    a.ring_head[b] = (int32_t)nh;
+  }
+}
+
 }  // namespace tssm
 
 using namespace tssm;
@@ -383,7 +444,16 @@ extern "C" int tssm_stream_interp_step_corrected(
   TSSM_CHECK(nbatch <= 2147483647, TSSM_ERR_UNSUPPORTED);
   RingArgs a{ring_V, ring_M, ring_tau, ring_head, v_new, m_new, tau_new, h, Abar, Bbar, C, D, y,
              H, srb, srk, svb, shb, scb, 1, KRING};
-  hipLaunchKernelGGL(stream_interp_step_corrected_kernel, dim3((unsigned)nbatch),
-                     dim3(kStreamThreads), 0, as_stream(stream), a);
+  const bool vec = KRING - 1 <= kRingFast && H % 4 == 0 && srb % 4 == 0 && srk % 4 == 0 &&
+                   svb % 4 == 0 && shb % 4 == 0 && scb % 4 == 0 && aligned(ring_V, 16) &&
+                   aligned(ring_M, 16) && aligned(v_new, 16) && aligned(m_new, 16) &&
+                   aligned(h, 16) && aligned(Abar, 16) && aligned(Bbar, 16) && aligned(C, 16) &&
+                   aligned(D, 16) && aligned(y, 16);
+  if (vec)
+    hipLaunchKernelGGL(stream_interp_step_corrected_vec_kernel, dim3((unsigned)nbatch),
+                       dim3(kStreamThreads), 0, as_stream(stream), a);
+  else
+    hipLaunchKernelGGL(stream_interp_step_corrected_kernel, dim3((unsigned)nbatch),
+                       dim3(kStreamThreads), 0, as_stream(stream), a);
   return launch_status();
 }
