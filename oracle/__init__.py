@@ -1,6 +1,6 @@
 """CPU oracle for the selective-SSM path -- TEST INFRASTRUCTURE ONLY.
 
-This package is the checker, never the product.  Only ``tests/``,
+This package is test infrastructure, never the product.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  Nothing under ``triton-ssm_amd/`` imports it, and the product path
 has no CPU fallback: when the HIP library is missing it raises.

@@ -333,7 +333,7 @@ def _mh_coeffs(u, A_log, B, dt, n_heads, head_dim, disc):
 
     Abar = exp(dt[b,t,h] * a[h,p]) with a = -exp(A_log) (:64-69).
     euler (reference, :73-82): x = dt * B * u.
-    zoh   (north-star):        x = expm1(dt*a)/a * B * u  (= phi1(dt a) dt B u).
+    zoh   (discretize_kernel.py:44-54): x = expm1(dt*a)/a * B * u  (= phi1(dt a) dt B u).
     u lanes beyond the channel count read 0 (:77-80).
     """
     u, A_log, B, dt = _f64(u), _f64(A_log), _f64(B), _f64(dt)
