@@ -141,6 +141,25 @@ def test_fused_forgetting_tiles(dev):
 
 
 @pytest.mark.parametrize("disc", ["zoh", "euler"])
+def test_fused_headline_scaling_is_exact(dev, disc):
+    """Every output of the benchmarked instance at its full size: the scan is
+    linear in u with dt, A, B, C fixed, and doubling is exact in bf16 and in
+    every fp32 operation, so y(2u) = 2 y(u) and h_last(2u) = 2 h_last(u) bit
+    for bit -- a check of all 33.5 M outputs that needs no reference."""
+    import tssm
+    from tssm import multihead_ssm_forward, workloads
+    w = workloads.multihead()
+    d = {k: w[k].to(dev) for k in ("u", "B", "C", "dt", "A_log_h")}
+    y1, h1 = multihead_ssm_forward(d["u"], d["A_log_h"], d["B"], d["C"], d["dt"], None,
+                                   disc=disc, chunk=128, return_state=True)
+    y2, h2 = multihead_ssm_forward(d["u"] * 2, d["A_log_h"], d["B"], d["C"], d["dt"], None,
+                                   disc=disc, chunk=128, return_state=True)
+    tssm.check(dev)
+    assert torch.equal(y2, y1 * 2), "y(2u) != 2 y(u)"
+    assert torch.equal(h2, h1 * 2), "h_last(2u) != 2 h_last(u)"
+
+
+@pytest.mark.parametrize("disc", ["zoh", "euler"])
 @pytest.mark.parametrize("a_layout", ["per_head", "per_channel"])
 @pytest.mark.parametrize("with_d", [False, True])
 def test_fused_full_headline_shape(dev, disc, a_layout, with_d):
