@@ -298,8 +298,12 @@ int tssm_ssd_stream_step(int disc, const float* x, const float* dt, const float*
  *   y_t[d] = sum_n C_t[n] h_t[d,n] + D[d] x_t[d]
  * -- what the reference computes with zoh_discretize_diag_kernel over lanes
  * (d,n) followed by ssm_forward and a sum over n (discretize_kernel.py:16-57,
- * ssm_scan.py:239-264), fused into one single-pass launch (same kernel as
- * tssm_mh_scan_fused with the channel input broadcast over the states).
+ * ssm_scan.py:239-264), fused: one single-pass launch (same kernel as
+ * tssm_mh_scan_fused with the channel input broadcast over the states), or,
+ * for N = 8 or 16 with f32/bf16 I/O and at least 512 blocks of 64 channels x
+ * 32 steps, three launches on `stream` (chunk end states, a carry scan over
+ * the chunks, the outputs) with lanes = channels; `chunk` then does not
+ * apply.  The workspace size covers either.
  * x, B, C, y in `dtype` ([B,L,Dc] / [B,L,N]); A_log f32 [Dc,N]; dt f32 with
  * strides (b, l, d) -- sdt_d = 0 for one dt per (b,t); with dt_is_tau=1 dt
  * holds timestamps tau and dt_t = tau_t - tau_{t-1}, dt_0 = tau_0.

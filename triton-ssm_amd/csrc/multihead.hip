@@ -32,6 +32,7 @@
 
 #include "common.h"
 #include "lookback.h"
+#include "selective.h"
 
 namespace tssm {
 
@@ -147,15 +148,23 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   // MODE_DIAG with a decay per channel: the row's P lanes share their
   // parameters over the workgroup's runs, so thread tid < P forms lane tid's
   // a log2(e) (and 1/a) once, into LDS, read back after the step loads are
-  // issued (measured 4% faster at the headline shape).  MODE_MAMBA1 keeps
-  // them per thread: there the extra barrier costs what the exp2s save.
+  // issued (measured 4% faster at the headline shape).  For MODE_MAMBA1 the
+  // extra barrier measured as costly as the exp2s it saves.
   constexpr bool PAR_LDS = !APH && MODE == MODE_DIAG;
+  // MODE_MAMBA1 with at least 8 runs per wave: the wave's runs share the
+  // parameters of each lane group g, so lane (run k, g) forms those of state
+  // k % 8 only and the group's 8 values are gathered by ds_bpermute (no
+  // barrier, 2 exp2 per thread instead of 16; measured ~1% faster at
+  // B=16 L=2048 Dc=256 N=16).
+  constexpr bool PAR_SHFL = !APH && MODE == MODE_MAMBA1 && ROWS >= 8;
   float alog = 0.0f;
   if constexpr (APH) {
     a2[0] = a.A_log[chan];
   } else if constexpr (PAR_LDS) {
     if (tid < P) alog = a.A_log[h * P + tid];
     __builtin_amdgcn_sched_barrier(0);  // issued before the step loads
+  } else if constexpr (PAR_SHFL) {
+    alog = a.A_log[h * P + ch0 + (lane / G) % 8];
   } else {
     const float4* ap = reinterpret_cast<const float4*>(a.A_log + h * P + ch0);
     const float4 l0 = ap[0], l1 = ap[1];
@@ -375,6 +384,17 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
     const float v = -expf(a2[0]) * kLog2e;
 #pragma unroll
     for (int j = 0; j < 8; ++j) a2[j] = v;
+  } else if constexpr (PAR_SHFL) {
+    const float x = alog * kLog2e;
+    const float pa = -exp2_fast(x) * kLog2e;
+    const float pi = DISC == TSSM_DISC_ZOH ? -exp2_fast(-x) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // state j of group g: lane (run j, g)
+      const int src = (j * G + g) << 2;
+      a2[j] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(pa)));
+      if constexpr (DISC == TSSM_DISC_ZOH)
+        ia[j] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(pi)));
+    }
   } else if constexpr (!PAR_LDS) {
     // hardware exp2 of the base-2 argument: within ~4e-7 relative of
     // -exp(A_log), at 4 operations per channel instead of a library expf
@@ -1207,13 +1227,28 @@ inline int64_t sel_channels_per_row(int64_t Dc, int64_t N) {
 }  // namespace
 }  // namespace tssm
 
-extern "C" int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc,
-                                                       int64_t N, int64_t chunk) {
+namespace tssm {
+namespace {
+// Look-back words of the single-pass scan (tagged, epoch-checked), then the
+// three-pass scan's chunk states in a separate region, so neither ever reads
+// the other's data as its own.
+int64_t sel_lookback_bytes(int64_t nbatch, int64_t L, int64_t Dc, int64_t N, int64_t chunk) {
   if (Dc <= 0 || N <= 0 || N % 8 != 0) return -1;
   const int64_t cpr = sel_channels_per_row(Dc, N);
   TileCfg cfg;
   if (nbatch <= 0 || L <= 0 || !mh_tile_cfg(cpr * N, chunk, &cfg)) return -1;
   return mh_ws_bytes(nbatch * (Dc / cpr), L, cpr * N, cfg.TC);
+}
+int64_t sel_chunked_offset(int64_t lookback_bytes) { return (lookback_bytes + 255) / 256 * 256; }
+}  // namespace
+}  // namespace tssm
+
+extern "C" int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc,
+                                                       int64_t N, int64_t chunk) {
+  const int64_t lb = sel_lookback_bytes(nbatch, L, Dc, N, chunk);
+  if (lb < 0) return -1;
+  const int64_t cb = sel_chunked_bytes(nbatch, L, Dc, N);
+  return cb > 0 ? sel_chunked_offset(lb) + cb : lb;
 }
 
 namespace tssm {
@@ -1256,6 +1291,27 @@ int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, i
   TSSM_CHECK(aligned(B, 16) && aligned(C, 16) && aligned(A_log, 16), TSSM_ERR_ALIGN);
   const int64_t strides[] = {sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b, sy_l};
   for (int64_t s : strides) TSSM_CHECK(s >= 0, TSSM_ERR_STRIDE);
+  // Large problems with 8 or 16 states take the three-pass scan (lanes =
+  // channels, B/C through scalar loads): fp32 or bf16 I/O, dt given (not
+  // projected), timestamps only when shared by the channels.
+  {
+    const int64_t rs = sel_chunk_steps(nbatch, L, Dc);
+    const int64_t cb = sel_chunked_bytes(nbatch, L, Dc, N);
+    const bool dt_shared = sdt_d == 0;
+    if (!proj.W && cb > 0 && (dtype == TSSM_F32 || dtype == TSSM_BF16) &&
+        (dt_shared || !dt_is_tau) && nbatch <= 65535 &&
+        nbatch * ((Dc + 63) / 64) * ((L + rs - 1) / rs) >= kSelMinWaves) {
+      SelPtrs p;
+      p.x = x; p.dt = dt; p.A_log = A_log; p.B = B; p.C = C; p.D = D; p.h0 = h0; p.y = y;
+      p.h_last = h_last;
+      const int64_t off = sel_chunked_offset(sel_lookback_bytes(nbatch, L, Dc, N, chunk));
+      p.S = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
+      p.T = p.S + nbatch * ((L + rs - 1) / rs) * Dc * N;
+      return sel_chunked_launch(dtype, disc, dt_shared, dt_is_tau != 0, p, nbatch, L, Dc, N,
+                                sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b,
+                                sy_l, as_stream(stream));
+    }
+  }
   const int64_t nchunks = cdiv(L, cfg.TC);
   const int64_t nrows = nbatch * (Dc / cpr);
   TSSM_CHECK(nchunks * nrows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);

@@ -1,0 +1,403 @@
+// Mamba-1 selective scan in three passes over lanes = channels (N = 8 or 16
+// states per lane, fp32 or bf16 I/O), the path tssm_selective_scan takes for
+// large problems.  The recurrence is the one of discretize_kernel.py:16-57
+// followed by ssm_scan.py:239-264 and a sum over n (y[b,t,d] = sum_n
+// C[b,t,n] h[b,t,d,n] + D[d] x[b,t,d]), as in the single-pass kernel of
+// multihead.hip; only the blocking differs.
+//
+//   pass 1 (sel_chunk_state_kernel): every wave takes 64 channels of one
+//     batch over one chunk of Rs steps and runs the recurrence from a zero
+//     state, keeping the N states of its channel in registers; it writes the
+//     chunk's end state X[b,c,d,:] and the chunk's dt sum.
+//   pass 2 (sel_carry_kernel): one thread per (b, d, n) walks the chunks:
+//     S_0 = h0, S_{c+1} = exp2(a log2e sum_c dt) S_c + X_c, overwriting X_c
+//     with the entry state S_c and writing h_last = S_nch.
+//   pass 3 (sel_output_kernel): the recurrence again from S_c, now with the
+//     readout C . h + D x per step.
+//
+// A workgroup is 256 consecutive channels of one batch over one chunk.  B and
+// C rows are the same for every channel of a batch, so the workgroup stages
+// the chunk's rows (and a dt shared by the channels) in LDS once and every
+// wave reads a step's row with broadcast LDS reads; x (and a per-channel dt)
+// is fetched four steps ahead into registers.  No pass has a look-back, and
+// passes 1 and 3 one barrier each.  Per lane update pass 1 issues 6 vector
+// instructions (mul, exp2, add, mul, fma, fma; ~98.5 per step of 16 states)
+// and pass 3 7 (~115.5 with the readout and store), against ~19 for the
+// single-pass kernel with its run scan and second sweep.
+#include <stdint.h>
+
+#include "common.h"
+#include "selective.h"
+
+namespace tssm {
+
+constexpr int kSelWaves = 4;                  // waves per workgroup
+constexpr int kSelThreads = 64 * kSelWaves;   // consecutive channels per workgroup
+constexpr int kSelCarryThreads = 256;
+constexpr int kSelCarryBatch = 32;            // chunks loaded ahead by pass 2
+constexpr int kSelPf = 4;                     // steps of x and dt fetched ahead
+
+struct SelDims {
+  int64_t L, Dc, Rs, nch;
+  int64_t sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b, sy_l;
+  int64_t nbatch;
+};
+
+// ab = exp2(dt a log2e) for each state; ZOH input term (ab - 1) B x / a
+// (h' = ab h + (ab - 1) B x / a); Euler B dt x.
+template <int DISC, int NST>
+__device__ inline void sel_update(float (&h)[NST], const float (&a2)[NST], const float (&nia)[NST],
+                                  const float (&Bv)[NST], float u, float dtv) {
+  if constexpr (DISC == TSSM_DISC_ZOH) {
+#pragma unroll
+    for (int k = 0; k < NST; ++k) {
+      // h' = ab (h + B x / a) - B x / a = h + (ab - 1)(h + B x / a): the
+      // accumulating form adds onto h itself (no register copy per state),
+      // and ab - 1 is exact for ab in [0.5, 1] (Sterbenz)
+      const float abm1 = __builtin_amdgcn_exp2f(dtv * a2[k]) - 1.0f;
+      const float hb = __builtin_fmaf(-nia[k], Bv[k] * u, h[k]);
+      h[k] = __builtin_fmaf(abm1, hb, h[k]);
+    }
+  } else {
+    const float du = dtv * u;
+#pragma unroll
+    for (int k = 0; k < NST; ++k) {
+      const float ab = __builtin_amdgcn_exp2f(dtv * a2[k]);
+      h[k] = __builtin_fmaf(ab, h[k], Bv[k] * du);
+    }
+  }
+}
+
+// Lane parameters: a log2(e) and -1/a with a = -exp(A_log[d, k]).
+template <int NST>
+__device__ inline void sel_params(const float* __restrict__ A_log, int64_t d, float (&a2)[NST],
+                                  float (&nia)[NST]) {
+  const float4* ap = reinterpret_cast<const float4*>(A_log + d * NST);
+#pragma unroll
+  for (int q = 0; q < NST / 4; ++q) {
+    const float4 v = ap[q];
+    const float l[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = l[i] * kLog2e;
+      a2[4 * q + i] = -__builtin_amdgcn_exp2f(x) * kLog2e;
+      nia[4 * q + i] = __builtin_amdgcn_exp2f(-x);
+    }
+  }
+}
+
+// The chunk's rows [n4][NST] of B (or C) of this batch, staged once per
+// workgroup in LDS as fp32 (4 elements per thread and pass); rows n .. n4-1
+// (the padding to whole groups of kSelPf steps) repeat row n-1.  Every wave
+// then reads a step's row with broadcast LDS reads.
+template <typename T, int NST>
+__device__ inline void stage_rows(float* s, const T* __restrict__ base, int64_t sl, int n,
+                                  int n4) {
+  for (int i = (int)threadIdx.x * 4; i < n4 * NST; i += kSelThreads * 4) {
+    const int row = i / NST, col = i - row * NST;
+    const T* p = base + (int64_t)(row < n ? row : n - 1) * sl + col;
+    float4 v;
+    if constexpr (sizeof(T) == 4) {
+      v = *reinterpret_cast<const float4*>(p);
+    } else {
+      const uint2 w = *reinterpret_cast<const uint2*>(p);
+      v = make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                      __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+    }
+    *reinterpret_cast<float4*>(s + i) = v;
+  }
+}
+
+// dt shared by the channels: the chunk's values [n4] in LDS, formed once per
+// workgroup (with timestamps the differences, dt_0 = tau_0); padded steps 0.
+template <bool TAU>
+__device__ inline void stage_dt(float* s, const float* __restrict__ row, int64_t sl, int64_t t0,
+                                int n, int n4) {
+  for (int i = (int)threadIdx.x; i < n4; i += kSelThreads) {
+    float v = 0.0f;
+    if (i < n) {
+      v = row[(t0 + i) * sl];
+      if constexpr (TAU) v -= (t0 + i > 0) ? row[(t0 + i - 1) * sl] : 0.0f;
+    }
+    s[i] = v;
+  }
+}
+
+template <int NST>
+__device__ inline void lds_row(const float* s, float (&v)[NST]) {
+  const float4* q = reinterpret_cast<const float4*>(s);
+#pragma unroll
+  for (int i = 0; i < NST / 4; ++i) {
+    const float4 w = q[i];
+    v[4 * i] = w.x; v[4 * i + 1] = w.y; v[4 * i + 2] = w.z; v[4 * i + 3] = w.w;
+  }
+}
+
+// One chunk of the recurrence for a lane (channel dc of batch b), in groups
+// of kSelPf steps: x (and a per-channel dt) of step r + kSelPf is fetched
+// right after step r, into the register step r just freed, so no value is
+// copied and each fetch has kSelPf - 1 steps to arrive.
+// Only the prologue's fetches pass through opaque copies (one wait before the
+// loop); otherwise the compiler merges them with the loop's fetches into a
+// load at the top of the group, waited on at once.  Padded steps (r >= n)
+// have dt = 0 -- an identity step -- and repeat step n-1's x and B/C rows,
+// so they reproduce step n-1's output.  `step(r, u, dtv)` gets every step.
+template <typename T, bool DTS, typename F>
+__device__ inline void chunk_steps(const T* __restrict__ xp, int64_t sx_l,
+                                   const float* __restrict__ dtp, int64_t sdt_l,
+                                   const float* s_dt, int64_t t0, int n, int n4, F&& step) {
+  float u[kSelPf], dr[kSelPf];
+#pragma unroll
+  for (int j = 0; j < kSelPf; ++j) {
+    const int64_t tt = t0 + (j < n ? j : n - 1);
+    u[j] = ldf(xp + tt * sx_l);
+    dr[j] = DTS ? 0.0f : dtp[tt * sdt_l];
+    asm volatile("" : "+v"(u[j]), "+v"(dr[j]));
+  }
+  __syncthreads();  // rows (and shared dt) staged by the caller
+  for (int r = 0; r < n4; r += kSelPf) {
+#pragma unroll
+    for (int j = 0; j < kSelPf; ++j) {
+      const int rr = r + j;
+      step(rr, u[j], DTS ? s_dt[rr] : (rr < n ? dr[j] : 0.0f));
+      // refill the registers step rr just used (no copies across the loop)
+      __builtin_amdgcn_sched_barrier(0);
+      const int64_t tn = t0 + min(rr + kSelPf, n - 1);
+      u[j] = ldf(xp + tn * sx_l);
+      if constexpr (!DTS) dr[j] = dtp[tn * sdt_l];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+template <typename T, int DISC, int NST, bool DTS, bool TAU>
+__global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
+    const T* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
+    const T* __restrict__ Bm, float* __restrict__ S, float* __restrict__ Tsum, SelDims m) {
+  static_assert(!TAU || DTS, "timestamps only when shared by the channels");
+  const int64_t c = blockIdx.x, b = blockIdx.z;
+  const int64_t d = (int64_t)blockIdx.y * kSelThreads + threadIdx.x;
+  const bool ok = d < m.Dc;
+  const int64_t dc = ok ? d : m.Dc - 1;  // lanes past Dc compute channel Dc-1, store nothing
+  const int64_t t0 = c * m.Rs;
+  const int n = (int)(m.L - t0 < m.Rs ? m.L - t0 : m.Rs);
+  const int n4 = (n + kSelPf - 1) / kSelPf * kSelPf;
+
+  __shared__ float sB[kSelChunkSteps * NST];
+  __shared__ float sD[DTS ? kSelChunkSteps : 1];
+  stage_rows<T, NST>(sB, Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
+  if constexpr (DTS) stage_dt<TAU>(sD, dt + b * m.sdt_b, m.sdt_l, t0, n, n4);
+
+  float a2[NST], nia[NST], h[NST];
+  sel_params<NST>(A_log, dc, a2, nia);
+#pragma unroll
+  for (int k = 0; k < NST; ++k) {
+    h[k] = 0.0f;
+    asm volatile("" : "+v"(a2[k]), "+v"(nia[k]));  // complete before the loop (as in pass 3)
+  }
+
+  float sdt = 0.0f;
+  chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d),
+                      m.sdt_l, sD, t0, n, n4, [&](int rr, float u, float dtv) {
+                        float Bv[NST];
+                        lds_row<NST>(sB + rr * NST, Bv);
+                        sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
+                        sdt += dtv;
+                      });
+  if (ok) {
+    float4* sp = reinterpret_cast<float4*>(S + ((b * m.nch + c) * m.Dc + d) * NST);
+#pragma unroll
+    for (int q = 0; q < NST / 4; ++q)
+      sp[q] = make_float4(h[4 * q], h[4 * q + 1], h[4 * q + 2], h[4 * q + 3]);
+    if constexpr (DTS) {
+      if (d == 0) Tsum[b * m.nch + c] = sdt;
+    } else {
+      Tsum[(b * m.nch + c) * m.Dc + d] = sdt;
+    }
+  }
+}
+
+template <int NST, bool DTS>
+__global__ __launch_bounds__(kSelCarryThreads) void sel_carry_kernel(
+    const float* __restrict__ A_log, const float* __restrict__ h0, float* __restrict__ S,
+    const float* __restrict__ Tsum, float* __restrict__ h_last, SelDims m) {
+  // blockIdx.y = batch (uniform: the shared dt sums are scalar loads)
+  const int64_t b = blockIdx.y;
+  const int64_t per_b = m.Dc * NST;
+  const int64_t rem = (int64_t)blockIdx.x * kSelCarryThreads + threadIdx.x;
+  if (rem >= per_b) return;  // no barrier in this kernel
+  const int64_t d = rem / NST;
+  const float a2 = -__builtin_amdgcn_exp2f(A_log[rem] * kLog2e) * kLog2e;
+  const int64_t idx = b * per_b + rem;
+  float st = h0 ? h0[idx] : 0.0f;
+  float* sp = S + b * m.nch * per_b + rem;
+  const float* tp = Tsum + b * m.nch * (DTS ? 1 : m.Dc) + (DTS ? 0 : d);
+  const int64_t ts = DTS ? 1 : m.Dc;
+  // all loads of a batch of chunks are issued before the first use
+  int64_t c0 = 0;
+  for (; c0 + kSelCarryBatch <= m.nch; c0 += kSelCarryBatch) {
+    float X[kSelCarryBatch], Tv[kSelCarryBatch];
+#pragma unroll
+    for (int i = 0; i < kSelCarryBatch; ++i) {
+      X[i] = sp[(c0 + i) * per_b];
+      Tv[i] = tp[(c0 + i) * ts];
+    }
+#pragma unroll
+    for (int i = 0; i < kSelCarryBatch; ++i) {
+      sp[(c0 + i) * per_b] = st;  // entry state of chunk c0 + i
+      st = __builtin_fmaf(__builtin_amdgcn_exp2f(a2 * Tv[i]), st, X[i]);
+    }
+  }
+  for (; c0 < m.nch; ++c0) {
+    const float X = sp[c0 * per_b], Tv = tp[c0 * ts];
+    sp[c0 * per_b] = st;
+    st = __builtin_fmaf(__builtin_amdgcn_exp2f(a2 * Tv), st, X);
+  }
+  if (h_last) h_last[idx] = st;
+}
+
+template <typename T, int DISC, int NST, bool DTS, bool TAU, bool HAS_D>
+__global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
+    const T* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ D,
+    const float* __restrict__ S, T* __restrict__ y, SelDims m) {
+  static_assert(!TAU || DTS, "timestamps only when shared by the channels");
+  const int64_t c = blockIdx.x, b = blockIdx.z;
+  const int64_t d = (int64_t)blockIdx.y * kSelThreads + threadIdx.x;
+  const int64_t dc = d < m.Dc ? d : m.Dc - 1;
+  const int64_t t0 = c * m.Rs;
+  const int n = (int)(m.L - t0 < m.Rs ? m.L - t0 : m.Rs);
+  const int n4 = (n + kSelPf - 1) / kSelPf * kSelPf;
+
+  __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
+  __shared__ float sD[DTS ? kSelChunkSteps : 1];
+  stage_rows<T, NST>(sB, Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
+  stage_rows<T, NST>(sC, Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
+  if constexpr (DTS) stage_dt<TAU>(sD, dt + b * m.sdt_b, m.sdt_l, t0, n, n4);
+
+  float a2[NST], nia[NST], h[NST];
+  sel_params<NST>(A_log, dc, a2, nia);
+  {
+    const float4* sp = reinterpret_cast<const float4*>(S + ((b * m.nch + c) * m.Dc + dc) * NST);
+#pragma unroll
+    for (int q = 0; q < NST / 4; ++q) {
+      const float4 v = sp[q];
+      h[4 * q] = v.x; h[4 * q + 1] = v.y; h[4 * q + 2] = v.z; h[4 * q + 3] = v.w;
+    }
+  }
+  float Dd = HAS_D ? D[dc] : 0.0f;
+  // the lane's state, parameters and skip weight complete before the loop,
+  // so its waits count only the loop's own fetches and stores
+#pragma unroll
+  for (int k = 0; k < NST; ++k) asm volatile("" : "+v"(h[k]), "+v"(a2[k]), "+v"(nia[k]));
+  asm volatile("" : "+v"(Dd));
+  T* yp = y + b * m.sy_b + dc;
+
+  chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d),
+                      m.sdt_l, sD, t0, n, n4, [&](int rr, float u, float dtv) {
+                        float Bv[NST], Cv[NST];
+                        lds_row<NST>(sB + rr * NST, Bv);
+                        lds_row<NST>(sC + rr * NST, Cv);
+                        sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
+                        // readout in two interleaved partial sums
+                        float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < NST; k += 2) {
+                          acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
+                          acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
+                        }
+                        // Unconditional store: lanes past Dc computed channel
+                        // Dc-1 and padded steps step n-1, identical values to
+                        // what those write there, so no branch holds up the
+                        // waits for later fetches.
+                        const int64_t tw = t0 + (rr < n ? rr : n - 1);
+                        stf(yp + tw * m.sy_l, acc0 + acc1);
+                      });
+}
+
+// ---------------------------------------------------------------- host
+namespace {
+
+template <typename T, int DISC, int NST, bool DTS, bool TAU>
+int sel_chunked_t(bool has_d, const SelPtrs& p, const SelDims& m, hipStream_t s) {
+  const dim3 grid((unsigned)m.nch, (unsigned)((m.Dc + kSelThreads - 1) / kSelThreads),
+                  (unsigned)m.nbatch);
+  const T* x = static_cast<const T*>(p.x);
+  hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU>), grid, dim3(kSelThreads), 0,
+                     s, x, p.dt, p.A_log, static_cast<const T*>(p.B), p.S, p.T, m);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const int64_t lanes = m.Dc * NST;  // per batch
+  hipLaunchKernelGGL((sel_carry_kernel<NST, DTS>),
+                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
+                          (unsigned)m.nbatch),
+                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  if (has_d)
+    hipLaunchKernelGGL((sel_output_kernel<T, DISC, NST, DTS, TAU, true>), grid, dim3(kSelThreads),
+                       0, s, x, p.dt, p.A_log, static_cast<const T*>(p.B),
+                       static_cast<const T*>(p.C), p.D, p.S, static_cast<T*>(p.y), m);
+  else
+    hipLaunchKernelGGL((sel_output_kernel<T, DISC, NST, DTS, TAU, false>), grid,
+                       dim3(kSelThreads), 0, s, x, p.dt, p.A_log, static_cast<const T*>(p.B),
+                       static_cast<const T*>(p.C), p.D, p.S, static_cast<T*>(p.y), m);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int DISC, int NST>
+int sel_chunked_dt(bool has_d, bool dts, bool tau, const SelPtrs& p, const SelDims& m,
+                   hipStream_t s) {
+  if (dts) {
+    return tau ? sel_chunked_t<T, DISC, NST, true, true>(has_d, p, m, s)
+               : sel_chunked_t<T, DISC, NST, true, false>(has_d, p, m, s);
+  }
+  return sel_chunked_t<T, DISC, NST, false, false>(has_d, p, m, s);  // per-channel dt, no tau
+}
+
+template <typename T, int DISC>
+int sel_chunked_n(int64_t N, bool has_d, bool dts, bool tau, const SelPtrs& p, const SelDims& m,
+                  hipStream_t s) {
+  return N == 16 ? sel_chunked_dt<T, DISC, 16>(has_d, dts, tau, p, m, s)
+                 : sel_chunked_dt<T, DISC, 8>(has_d, dts, tau, p, m, s);
+}
+
+}  // namespace
+
+int64_t sel_chunk_steps(int64_t nbatch, int64_t L, int64_t Dc) {
+  (void)nbatch;
+  (void)Dc;
+  return L >= 64 ? kSelChunkSteps : 0;
+}
+
+int64_t sel_chunked_bytes(int64_t nbatch, int64_t L, int64_t Dc, int64_t N) {
+  if (!(N == 8 || N == 16) || nbatch <= 0 || L <= 0 || Dc <= 0) return 0;
+  const int64_t rs = sel_chunk_steps(nbatch, L, Dc);
+  if (rs == 0) return 0;
+  const int64_t nch = (L + rs - 1) / rs;
+  return (nbatch * nch * Dc * N + nbatch * nch * Dc) * (int64_t)sizeof(float);
+}
+
+int sel_chunked_launch(int dtype, int disc, bool dt_shared, bool tau, const SelPtrs& p,
+                       int64_t nbatch, int64_t L, int64_t Dc, int64_t N, int64_t sx_b,
+                       int64_t sx_l, int64_t sdt_b, int64_t sdt_l, int64_t sdt_d, int64_t sB_b,
+                       int64_t sB_l, int64_t sC_b, int64_t sC_l, int64_t sy_b, int64_t sy_l,
+                       hipStream_t s) {
+  SelDims m;
+  m.L = L; m.Dc = Dc; m.nbatch = nbatch;
+  m.Rs = sel_chunk_steps(nbatch, L, Dc);
+  m.nch = (L + m.Rs - 1) / m.Rs;
+  m.sx_b = sx_b; m.sx_l = sx_l; m.sdt_b = sdt_b; m.sdt_l = sdt_l; m.sdt_d = sdt_d;
+  m.sB_b = sB_b; m.sB_l = sB_l; m.sC_b = sC_b; m.sC_l = sC_l; m.sy_b = sy_b; m.sy_l = sy_l;
+  const bool has_d = p.D != nullptr;
+  if (dtype == TSSM_BF16) {
+    return disc == TSSM_DISC_ZOH
+               ? sel_chunked_n<bf16_t, TSSM_DISC_ZOH>(N, has_d, dt_shared, tau, p, m, s)
+               : sel_chunked_n<bf16_t, TSSM_DISC_EULER>(N, has_d, dt_shared, tau, p, m, s);
+  }
+  return disc == TSSM_DISC_ZOH
+             ? sel_chunked_n<float, TSSM_DISC_ZOH>(N, has_d, dt_shared, tau, p, m, s)
+             : sel_chunked_n<float, TSSM_DISC_EULER>(N, has_d, dt_shared, tau, p, m, s);
+}
+
+}  // namespace tssm
