@@ -5,25 +5,26 @@
 // C[b,t,n] h[b,t,d,n] + D[d] x[b,t,d]), as in the single-pass kernel of
 // multihead.hip; only the blocking differs.
 //
-//   pass 1 (sel_chunk_state_kernel): every wave takes 64 channels of one
-//     batch over one chunk of Rs steps and runs the recurrence from a zero
-//     state, keeping the N states of its channel in registers; it writes the
+//   pass 1 (sel_chunk_state_kernel): a workgroup takes 256 consecutive
+//     channels of one batch over one chunk of Rs steps and runs the
+//     recurrence from a zero state, each lane keeping the N states of its
+//     channel in registers.  It stores y for that zero entry state, the
 //     chunk's end state X[b,c,d,:] and the chunk's dt sum.
 //   pass 2 (sel_carry_kernel): one thread per (b, d, n) walks the chunks:
 //     S_0 = h0, S_{c+1} = exp2(a log2e sum_c dt) S_c + X_c, overwriting X_c
 //     with the entry state S_c and writing h_last = S_nch.
-//   pass 3 (sel_output_kernel): the recurrence again from S_c, now with the
-//     readout C . h + D x per step.
+//   pass 3 (sel_output_kernel): adds the entry state's share of the output,
+//     y[t] += sum_n C_t[n] exp2(a[n] log2e cum_t) S_c[n].
 //
-// A workgroup is 256 consecutive channels of one batch over one chunk.  B and
-// C rows are the same for every channel of a batch, so the workgroup stages
-// the chunk's rows (and a dt shared by the channels) in LDS once and every
-// wave reads a step's row with broadcast LDS reads; x (and a per-channel dt)
-// is fetched four steps ahead into registers.  No pass has a look-back, and
-// passes 1 and 3 one barrier each.  Per lane update pass 1 issues 6 vector
-// instructions (mul, exp2, add, mul, fma, fma; ~98.5 per step of 16 states)
-// and pass 3 7 (~115.5 with the readout and store), against ~19 for the
-// single-pass kernel with its run scan and second sweep.
+// B and C rows are the same for every channel of a batch, so a workgroup
+// stages the chunk's rows (and a dt shared by the channels) in LDS once and
+// every wave reads a step's row with broadcast LDS reads; x (y in pass 3,
+// and a per-channel dt) is fetched four steps ahead into registers.  No pass
+// has a look-back; passes 1 and 3 have one barrier each.  Vector
+// instructions per step of 16 states: ~116.5 in pass 1 (6 per state update
+// -- mul, exp2, add, mul, fma, fma -- and 1 per state of readout) and ~68.5
+// in pass 3 (mul, exp2, mul, fma per state), against ~300 (19 per lane
+// update) for the single-pass kernel with its run scan and second sweep.
 #include <stdint.h>
 
 #include "common.h"
@@ -170,39 +171,59 @@ __device__ inline void chunk_steps(const T* __restrict__ xp, int64_t sx_l,
   }
 }
 
-template <typename T, int DISC, int NST, bool DTS, bool TAU>
+template <typename T, int DISC, int NST, bool DTS, bool TAU, bool HAS_D>
 __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
     const T* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
-    const T* __restrict__ Bm, float* __restrict__ S, float* __restrict__ Tsum, SelDims m) {
+    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ D,
+    T* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum, SelDims m) {
   static_assert(!TAU || DTS, "timestamps only when shared by the channels");
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int64_t d = (int64_t)blockIdx.y * kSelThreads + threadIdx.x;
   const bool ok = d < m.Dc;
-  const int64_t dc = ok ? d : m.Dc - 1;  // lanes past Dc compute channel Dc-1, store nothing
+  const int64_t dc = ok ? d : m.Dc - 1;  // lanes past Dc compute channel Dc-1
   const int64_t t0 = c * m.Rs;
   const int n = (int)(m.L - t0 < m.Rs ? m.L - t0 : m.Rs);
   const int n4 = (n + kSelPf - 1) / kSelPf * kSelPf;
 
-  __shared__ float sB[kSelChunkSteps * NST];
+  __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
   __shared__ float sD[DTS ? kSelChunkSteps : 1];
   stage_rows<T, NST>(sB, Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
+  stage_rows<T, NST>(sC, Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
   if constexpr (DTS) stage_dt<TAU>(sD, dt + b * m.sdt_b, m.sdt_l, t0, n, n4);
 
   float a2[NST], nia[NST], h[NST];
   sel_params<NST>(A_log, dc, a2, nia);
+  float Dd = HAS_D ? D[dc] : 0.0f;
 #pragma unroll
   for (int k = 0; k < NST; ++k) {
     h[k] = 0.0f;
-    asm volatile("" : "+v"(a2[k]), "+v"(nia[k]));  // complete before the loop (as in pass 3)
+    asm volatile("" : "+v"(a2[k]), "+v"(nia[k]));  // complete before the loop
   }
+  asm volatile("" : "+v"(Dd));
+  T* yp = y + b * m.sy_b + dc;
 
   float sdt = 0.0f;
   chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d),
                       m.sdt_l, sD, t0, n, n4, [&](int rr, float u, float dtv) {
-                        float Bv[NST];
+                        float Bv[NST], Cv[NST];
                         lds_row<NST>(sB + rr * NST, Bv);
+                        lds_row<NST>(sC + rr * NST, Cv);
                         sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
                         sdt += dtv;
+                        // output for a zero entry state, in two interleaved
+                        // partial sums; pass 3 adds the entry state's part
+                        float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
+#pragma unroll
+                        for (int k = 0; k < NST; k += 2) {
+                          acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
+                          acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
+                        }
+                        // Unconditional store: lanes past Dc computed channel
+                        // Dc-1 and padded steps step n-1, identical values to
+                        // what those write there, so no branch holds up the
+                        // waits for later fetches.
+                        const int64_t tw = t0 + (rr < n ? rr : n - 1);
+                        stf(yp + tw * m.sy_l, acc0 + acc1);
                       });
   if (ok) {
     float4* sp = reinterpret_cast<float4*>(S + ((b * m.nch + c) * m.Dc + d) * NST);
@@ -256,11 +277,16 @@ __global__ __launch_bounds__(kSelCarryThreads) void sel_carry_kernel(
   if (h_last) h_last[idx] = st;
 }
 
-template <typename T, int DISC, int NST, bool DTS, bool TAU, bool HAS_D>
+// Pass 3: y[t] += sum_n C_t[n] 2^(a[n] log2e cum_t) S_c[n], the part of the
+// output carried in by the chunk's entry state (cum_t: dt summed over the
+// chunk up to and including t); pass 1 stored the rest.  The decay factor is
+// the product of the per-step factors of the recurrence written as one
+// exponential; it does not depend on the discretization.  y is read (four
+// steps ahead) and written in place, so it is not declared restrict.
+template <typename T, int NST, bool DTS, bool TAU>
 __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
-    const T* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
-    const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ D,
-    const float* __restrict__ S, T* __restrict__ y, SelDims m) {
+    const float* __restrict__ dt, const float* __restrict__ A_log, const T* __restrict__ Cm,
+    const float* __restrict__ S, T* y, SelDims m) {
   static_assert(!TAU || DTS, "timestamps only when shared by the channels");
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int64_t d = (int64_t)blockIdx.y * kSelThreads + threadIdx.x;
@@ -269,9 +295,8 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
   const int n = (int)(m.L - t0 < m.Rs ? m.L - t0 : m.Rs);
   const int n4 = (n + kSelPf - 1) / kSelPf * kSelPf;
 
-  __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
+  __shared__ float sC[kSelChunkSteps * NST];
   __shared__ float sD[DTS ? kSelChunkSteps : 1];
-  stage_rows<T, NST>(sB, Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
   stage_rows<T, NST>(sC, Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
   if constexpr (DTS) stage_dt<TAU>(sD, dt + b * m.sdt_b, m.sdt_l, t0, n, n4);
 
@@ -285,31 +310,25 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
       h[4 * q] = v.x; h[4 * q + 1] = v.y; h[4 * q + 2] = v.z; h[4 * q + 3] = v.w;
     }
   }
-  float Dd = HAS_D ? D[dc] : 0.0f;
-  // the lane's state, parameters and skip weight complete before the loop,
-  // so its waits count only the loop's own fetches and stores
 #pragma unroll
-  for (int k = 0; k < NST; ++k) asm volatile("" : "+v"(h[k]), "+v"(a2[k]), "+v"(nia[k]));
-  asm volatile("" : "+v"(Dd));
+  for (int k = 0; k < NST; ++k) asm volatile("" : "+v"(h[k]), "+v"(a2[k]));  // before the loop
   T* yp = y + b * m.sy_b + dc;
 
-  chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d),
-                      m.sdt_l, sD, t0, n, n4, [&](int rr, float u, float dtv) {
-                        float Bv[NST], Cv[NST];
-                        lds_row<NST>(sB + rr * NST, Bv);
+  float cum = 0.0f;
+  chunk_steps<T, DTS>(yp, m.sy_l, dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d), m.sdt_l, sD, t0,
+                      n, n4, [&](int rr, float y1, float dtv) {
+                        float Cv[NST];
                         lds_row<NST>(sC + rr * NST, Cv);
-                        sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
-                        // readout in two interleaved partial sums
-                        float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
+                        cum += dtv;
+                        float acc0 = y1, acc1 = 0.0f;
 #pragma unroll
                         for (int k = 0; k < NST; k += 2) {
-                          acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
-                          acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
+                          acc0 = __builtin_fmaf(Cv[k] * h[k],
+                                                __builtin_amdgcn_exp2f(a2[k] * cum), acc0);
+                          acc1 = __builtin_fmaf(Cv[k + 1] * h[k + 1],
+                                                __builtin_amdgcn_exp2f(a2[k + 1] * cum), acc1);
                         }
-                        // Unconditional store: lanes past Dc computed channel
-                        // Dc-1 and padded steps step n-1, identical values to
-                        // what those write there, so no branch holds up the
-                        // waits for later fetches.
+                        // Unconditional (identical values as in pass 1).
                         const int64_t tw = t0 + (rr < n ? rr : n - 1);
                         stf(yp + tw * m.sy_l, acc0 + acc1);
                       });
@@ -323,8 +342,15 @@ int sel_chunked_t(bool has_d, const SelPtrs& p, const SelDims& m, hipStream_t s)
   const dim3 grid((unsigned)m.nch, (unsigned)((m.Dc + kSelThreads - 1) / kSelThreads),
                   (unsigned)m.nbatch);
   const T* x = static_cast<const T*>(p.x);
-  hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU>), grid, dim3(kSelThreads), 0,
-                     s, x, p.dt, p.A_log, static_cast<const T*>(p.B), p.S, p.T, m);
+  const T* Bm = static_cast<const T*>(p.B);
+  const T* Cm = static_cast<const T*>(p.C);
+  T* y = static_cast<T*>(p.y);
+  if (has_d)
+    hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU, true>), grid,
+                       dim3(kSelThreads), 0, s, x, p.dt, p.A_log, Bm, Cm, p.D, y, p.S, p.T, m);
+  else
+    hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU, false>), grid,
+                       dim3(kSelThreads), 0, s, x, p.dt, p.A_log, Bm, Cm, p.D, y, p.S, p.T, m);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   const int64_t lanes = m.Dc * NST;  // per batch
@@ -334,14 +360,8 @@ int sel_chunked_t(bool has_d, const SelPtrs& p, const SelDims& m, hipStream_t s)
                      dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
   e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  if (has_d)
-    hipLaunchKernelGGL((sel_output_kernel<T, DISC, NST, DTS, TAU, true>), grid, dim3(kSelThreads),
-                       0, s, x, p.dt, p.A_log, static_cast<const T*>(p.B),
-                       static_cast<const T*>(p.C), p.D, p.S, static_cast<T*>(p.y), m);
-  else
-    hipLaunchKernelGGL((sel_output_kernel<T, DISC, NST, DTS, TAU, false>), grid,
-                       dim3(kSelThreads), 0, s, x, p.dt, p.A_log, static_cast<const T*>(p.B),
-                       static_cast<const T*>(p.C), p.D, p.S, static_cast<T*>(p.y), m);
+  hipLaunchKernelGGL((sel_output_kernel<T, NST, DTS, TAU>), grid, dim3(kSelThreads), 0, s, p.dt,
+                     p.A_log, Cm, p.S, y, m);
   return (int)hipGetLastError();
 }
 
