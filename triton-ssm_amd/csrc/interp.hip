@@ -309,6 +309,124 @@ __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
   }
 }
 
+// interp_obs_pow2_kernel and interp_kernel in one launch: a workgroup forms
+// the flags of its tile's rows t0-K .. t0+TB+K-1 itself from M (same per-lane
+// vector sums and xor reduction over the tile's aligned lane group as the
+// flags kernel, so the same flags), keeps them in LDS and interpolates as
+// interp_kernel.  M is read (TB + 2K) / TB times instead of once, but the
+// flags' round trip through memory and a launch are gone.  Needs the
+// conditions of both vector paths: tiles of vpt = FTILE / EM mask vectors
+// with vpt a power of two <= 64, E-aligned V/Vhat rows.
+constexpr int kFusedU = 4;  // mask vectors per lane in flight
+
+template <typename TV, int E, typename TM, int EM>
+__global__ __launch_bounds__(kInterpThreads) void interp_fused_kernel(InterpArgs a, int lvpt) {
+  extern __shared__ unsigned char s_obs[];  // [kInterpTB + 2K]
+  __shared__ int s_prev[kInterpTB], s_next[kInterpTB];
+  __shared__ float s_w[kInterpTB];
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.x * kInterpTB;
+  const int64_t tile = blockIdx.y;
+  const int64_t b = a.b0 + blockIdx.z;
+  const int64_t f0 = tile * a.FTILE;
+  const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
+  const int K = (int)a.K;
+  const int NR = kInterpTB + 2 * K;
+  // 1. flags: item q = (row q >> lvpt, vector q & (vpt - 1)) of the tile
+  {
+    const int vpt = 1 << lvpt;
+    const int nitem = NR << lvpt;
+    const TM* M = reinterpret_cast<const TM*>(a.M) + b * a.smb + f0;
+    for (int q0 = tid; q0 < nitem; q0 += kFusedU * kInterpThreads) {
+      float sv[kFusedU];
+#pragma unroll
+      for (int u = 0; u < kFusedU; ++u) {
+        const int q = q0 + u * kInterpThreads;
+        const int i = q >> lvpt, j = q & (vpt - 1);
+        const int64_t t = t0 - K + i;
+        const bool ok = q < nitem && t >= 0 && t < a.rows && f0 + (int64_t)j * EM < f1;
+        Lanes<TM, EM> v;
+        v.load(M + (ok ? t * a.smt + (int64_t)j * EM : 0));  // invalid items read vector 0
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < EM; ++k) sum += v.v[k];
+        sv[u] = ok ? sum : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kFusedU; ++u) {
+        const int q = q0 + u * kInterpThreads;  // uniform per wave in whether q < nitem
+        float x = sv[u];
+        for (int o = 1; o < vpt; o <<= 1) x += __shfl_xor(x, o);
+        if (q < nitem && (q & (vpt - 1)) == 0) s_obs[q >> lvpt] = x > 0.5f ? 1 : 0;
+      }
+    }
+  }
+  __syncthreads();
+  // 2. neighbours and weight per step (as interp_kernel)
+  if (tid < kInterpTB) {
+    const int64_t t = t0 + tid;
+    int prev = -1, next = -1;
+    float w = 0.5f;
+    if (t < a.grid_t) {
+      for (int k = 1; k <= K; ++k)
+        if (prev < 0 && s_obs[tid + K - k]) prev = (int)(t - k);
+      for (int k = 1; k <= K; ++k)
+        if (next < 0 && s_obs[tid + K + k]) next = (int)(t + k);
+      const float tau_t = ld_any(a.tau, b * a.stb + t * a.stt, a.td);
+      const float tp = prev >= 0 ? ld_any(a.tau, b * a.stb + prev * a.stt, a.td) : 0.0f;
+      const float tn = next >= 0 ? ld_any(a.tau, b * a.stb + next * a.stt, a.td) : 0.0f;
+      const float den = tn - tp;
+      w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
+      w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+    }
+    s_prev[tid] = prev;
+    s_next[tid] = next;
+    s_w[tid] = w;
+  }
+  __syncthreads();
+  // 3. interpolation (as interp_kernel)
+  const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb;
+  TV* O = reinterpret_cast<TV*>(a.Vhat) + b * a.sob;
+  const int tmax = (int)((a.grid_t - t0) < kInterpTB ? (a.grid_t - t0) : kInterpTB);
+  const int ng = (int)((f1 - f0) / E);
+  const int total = tmax * ng;
+  constexpr int U = 2;
+  for (int q0 = tid; q0 < total; q0 += U * kInterpThreads) {
+    Lanes<TV, E> vp[U], vn[U];
+    int64_t ot[U], of[U];
+    float wt[U];
+    int mode[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int q = q0 + u * kInterpThreads;
+      mode[u] = -1;
+      if (q < total) {
+        const int i = q / ng;
+        const int64_t f = f0 + (int64_t)(q - i * ng) * E;
+        const int prev = s_prev[i], next = s_next[i];
+        const int64_t t = t0 + i;
+        const int64_t rp = prev >= 0 ? prev : (next >= 0 ? next : t);
+        const int64_t rn = next >= 0 ? next : rp;
+        vp[u].load(V + rp * a.svt + f);
+        vn[u].load(V + rn * a.svt + f);
+        mode[u] = (prev >= 0 ? 1 : 0) | (next >= 0 ? 2 : 0);
+        wt[u] = s_w[i];
+        ot[u] = t;
+        of[u] = f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (mode[u] < 0) continue;
+      Lanes<TV, E> o;
+#pragma unroll
+      for (int j = 0; j < E; ++j)
+        o.v[j] = mode[u] == 3 ? (1.0f - wt[u]) * vp[u].v[j] + wt[u] * vn[u].v[j] : vp[u].v[j];
+      o.store(O + ot[u] * a.sot + of[u]);
+    }
+  }
+}
+
 // fused_interp_ssm_step_kernel: one workgroup per (b, tile) at step t_cur.
 struct StepArgs {
   const void* V;
@@ -738,11 +856,43 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   // flags: 16-byte mask vectors when tiles and rows are whole vectors
   const int64_t EM = m_dtype == TSSM_F32 ? 4 : 8;
   const int64_t fc = F < gf * FTILE ? F : gf * FTILE;
-  if (FTILE % EM == 0 && fc % EM == 0 && smt % EM == 0 && smb % EM == 0 && aligned(M, 16) &&
-      fc / EM < 2147483647 - 64) {
+  const int64_t E = v_dtype == TSSM_F32 ? 4 : 8;
+  const bool vec = FTILE % E == 0 && F % E == 0 && svt % E == 0 && sot % E == 0 &&
+                   svb % E == 0 && sob % E == 0 && aligned(V, 16) && aligned(Vhat, 16);
+  int lvpt = 0;
+  while ((int64_t(1) << lvpt) < FTILE / EM) ++lvpt;
+  const bool mvec = FTILE % EM == 0 && fc % EM == 0 && smt % EM == 0 && smb % EM == 0 &&
+                    aligned(M, 16) && fc / EM < 2147483647 - 64;
+  // Both vector paths apply: one launch forms its flags and interpolates.
+  if (vec && mvec && (int64_t(1) << lvpt) == FTILE / EM && FTILE / EM <= 64) {
+    for (int64_t b0 = 0; b0 < grid_b; b0 += kMaxGridYZ) {  // batches in grid-z slices
+      a.b0 = b0;
+      const int64_t nb = grid_b - b0 < kMaxGridYZ ? grid_b - b0 : kMaxGridYZ;
+      const dim3 grid((unsigned)((grid_t + kInterpTB - 1) / kInterpTB), (unsigned)gf,
+                      (unsigned)nb);
+#define TSSM_FUSED(TT, EE, MT, ME)                                                         \
+  hipLaunchKernelGGL((interp_fused_kernel<TT, EE, MT, ME>), grid, dim3(kInterpThreads), \
+                     lds_interp, s, a, lvpt)
+#define TSSM_FUSED_M(TT, EE)                                      \
+  switch (m_dtype) {                                              \
+    case TSSM_F32: TSSM_FUSED(TT, EE, float, 4); break;            \
+    case TSSM_BF16: TSSM_FUSED(TT, EE, bf16_t, 8); break;          \
+    default: TSSM_FUSED(TT, EE, f16_t, 8); break;                  \
+  }
+      switch (v_dtype) {
+        case TSSM_F32: TSSM_FUSED_M(float, 4); break;
+        case TSSM_BF16: TSSM_FUSED_M(bf16_t, 8); break;
+        default: TSSM_FUSED_M(f16_t, 8); break;
+      }
+#undef TSSM_FUSED_M
+#undef TSSM_FUSED
+      const int st2 = launch_status();
+      if (st2 != TSSM_OK) return st2;
+    }
+    return TSSM_OK;
+  }
+  if (mvec) {
     const int64_t vpt = FTILE / EM;
-    int lvpt = 0;
-    while ((int64_t(1) << lvpt) < vpt) ++lvpt;
     if ((int64_t(1) << lvpt) == vpt && vpt <= 64) {  // tiles = aligned lane groups
       const int64_t wv = (nrow + kObsP2Rows - 1) / kObsP2Rows;
       const dim3 g((unsigned)((wv + wpb - 1) / wpb));
@@ -772,10 +922,7 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   }
   const int st = launch_status();
   if (st != TSSM_OK) return st;
-  // 16-byte lane groups when every tile, row stride and base pointer allows
-  const int64_t E = v_dtype == TSSM_F32 ? 4 : 8;
-  const bool vec = FTILE % E == 0 && F % E == 0 && svt % E == 0 && sot % E == 0 &&
-                   svb % E == 0 && sob % E == 0 && aligned(V, 16) && aligned(Vhat, 16);
+  // 16-byte lane groups when every tile, row stride and base pointer allows (vec)
   for (int64_t b0 = 0; b0 < grid_b; b0 += kMaxGridYZ) {  // batches in grid-z slices
     a.b0 = b0;
     const int64_t nb = grid_b - b0 < kMaxGridYZ ? grid_b - b0 : kMaxGridYZ;
