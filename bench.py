@@ -213,7 +213,9 @@ def wl_interp_mamba1(args, dev):
 
     n = B * T * F
     nbytes = 4 * (4 * n + B * T + F * N + 2 * B * T * N)   # V, M in; Vhat, y out
-    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, kernel="mh_scan_fused_kernel",
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
+                kernel="whole step: interp_fused_kernel, sel_chunk_state_kernel, "
+                       "sel_carry_kernel, sel_output_kernel",
                 metric="interp + Mamba-1 scan elements/sec, B=16 T=2048 F=256 N=16 fp32",
                 unit="elements/s",
                 config={"workload": "time-aware interpolation (K=10, FTILE=128, 30% missing) + "
@@ -277,7 +279,8 @@ def _wl_dtproj(args, dev, fused):
         nbytes += 2 * 4 * n      # dt written by the projection and read by the scan
     how = "fused into the scan's load stage" if fused else "two launches through dt [B,L,D]"
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, kernel="mh_scan_fused_kernel" if fused
-                else "dt_project_mfma_kernel + mh_scan_fused_kernel",
+                else "dt_project_mfma_kernel + sel_chunk_state_kernel + sel_carry_kernel + "
+                     "sel_output_kernel",
                 metric=f"Mamba-1 scan with dt projection ({how}) elements/sec, B=16 L=2048 "
                        "D=256 N=16 rank 16 fp32",
                 unit="elements/s",
