@@ -59,6 +59,20 @@ def test_ssd_scan_matrix_core_path(dev, L, disc, with_d):
     assert_close(hl, h_ref, 1e-3, "mfma ssd h_last")
 
 
+def test_ssd_scan_time_broadcast_b(dev):
+    """bf16 P=64 N=16 with B broadcast over time (row stride 0): the matrix-core
+    tile passes need every row stride to cover a row, so this layout runs the
+    generic passes, against the same oracle."""
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, 2, 700, 3, 64, 16, torch.bfloat16, seed=77, heavy=True)
+    Bb = d["B"][:, :1].expand(-1, 700, -1, -1)
+    assert Bb.stride(1) == 0
+    y = ssd_scan_forward(d["x"], d["dt"], d["A_log"], Bb, d["C"], d["D"], chunk=256)
+    torch.cuda.synchronize()
+    y_ref, _ = O.ssd_scan(d["x"], d["dt"], d["A_log"], Bb.contiguous(), d["C"], d["D"])
+    assert_close(y, y_ref, TOL[torch.bfloat16], "ssd y, B broadcast over time")
+
+
 @pytest.mark.parametrize("Bsz,L,H,P", [(2, 300, 3, 64), (2, 200, 4, 32), (1, 130, 8, 48),
                                         (1, 64, 8, 16), (1, 1, 2, 64), (3, 1000, 8, 64)])
 @pytest.mark.parametrize("disc", ["zoh", "euler"])

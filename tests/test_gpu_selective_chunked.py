@@ -55,6 +55,26 @@ def test_three_pass_selective_scan(dev, dtype, disc, N, dt_mode):
     assert_close(h, h_ref, TOL[dtype], "three-pass h_last")
 
 
+def test_three_pass_many_chunks(dev):
+    """1 x 9000 steps: 282 chunks per sequence, so the carry pass walks eight
+    full register batches of 32 chunks and a remainder of 26."""
+    from tssm import selective_scan_forward
+    g = torch.Generator().manual_seed(11)
+    Lm, Dm, N = 9000, 128, 16
+    x = torch.randn(1, Lm, Dm, generator=g)
+    dt = torch.empty(1, Lm).exponential_(20.0, generator=g).clamp_(1e-3, 1.0)
+    A_log = torch.empty(Dm, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = torch.randn(1, Lm, N, generator=g) / N ** 0.5
+    Cm = torch.randn(1, Lm, N, generator=g) / N ** 0.5
+    h0 = torch.randn(1, Dm, N, generator=g)
+    y, h = selective_scan_forward(*(t.to(dev) for t in (x, dt, A_log, Bm, Cm)), None,
+                                  h0=h0.to(dev), return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.selective_scan(x, dt, A_log, Bm, Cm, h0=np64(h0))
+    assert_close(y, y_ref, 1e-5, "three-pass y, 282 chunks")
+    assert_close(h, h_ref, 1e-5, "three-pass h_last, 282 chunks")
+
+
 def test_three_pass_without_skip_or_state_and_reuse(dev):
     """No D, no h0, no h_last; then a second, smaller call on the same stream
     (the workspace is reused) whose result must not depend on the first."""

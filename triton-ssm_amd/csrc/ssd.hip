@@ -331,27 +331,11 @@ __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
 }
 
 // ---------------------------------------------------------------- MFMA passes
-// bf16 inputs, P = 64, N = 16, 256-step tiles (the long-sequence shape): the
-// chunked (dual) form on the matrix cores.  A tile is processed as two halves
-// of 128 steps staged in LDS in turn; a half is 4 sub-chunks of 32 steps, one
-// per wave.  With l_t = dt_t a log2(e) and, inside a sub-chunk, the inclusive
-// prefix cum_t and exclusive suffix sfx_s = sum_{u>s} l_u:
-//   M[t][s]  = (C_t . B_s) 2^(cum_t - cum_s) coef_s   (s <= t, same sub-chunk)
-//   y_t      = sum_s M[t][s] x_s + 2^cum_t (H_J C_t) (+ D x_t)
-//   S_J      = sum_{s in J} 2^sfx_s coef_s x_s B_s^T,  H_{J+1} = 2^cumE_J H_J + S_J
-// Pass 1 forms each half's state with suffixes over the half and combines the
-// halves (state = 2^(half 2 decay) state_1 + state_2).  MFMA operands that are
-// not raw inputs (decay-weighted B, M, H) are fp32 values split into bf16 hi +
-// lo parts (two products), which keeps ~16 bits of their mantissa; x, B and C
-// enter exactly.  x is transposed into LDS ([p][s]) because every product
-// contracts over time steps.
+// bf16 inputs on the matrix cores: shared types, sizes and conversions.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kMq = 256;           // steps per tile (granularity of the state passing)
-constexpr int kMu = 128;           // steps staged in LDS at a time (half a tile)
-constexpr int kMsub = 32;          // steps per sub-chunk
-constexpr int kMp = 64, kMn = 16;  // head dim, state size
+constexpr int kMp = 64, kMn = 16;  // head dim, state size of the tile passes
 
 __device__ inline bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -373,60 +357,6 @@ __device__ inline void split_bf16(const float* v, bf16x8_t& hi, bf16x8_t& lo) {
 __device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// LDS element offsets.  Transposed half-tiles (xT[p][s], BT[n][s], 128
-// columns = 16 blocks of 16 bytes per row): the column block is XORed with
-// (row ^ row >> 3) mod 16, which takes 16 distinct values over any 16
-// consecutive rows and over the 8-row groups of the transposing writes, so
-// the operand reads (16 or 32 consecutive rows, one block per lane), the
-// output reads and the transposing writes each touch every bank about
-// equally.  (XOR with row >> 3 alone left 32-row reads on 4 blocks.)
-// Sub-chunk states sH[J][p][n]: the 4-float quad is XORed with (p >> 1) & 3
-// for the row-per-lane operand reads.
-__device__ inline int tix(int row, int col) {
-  return row * kMu + ((((col >> 3) ^ row ^ (row >> 3)) & (kMu / 8 - 1)) << 3) + (col & 7);
-}
-__device__ inline int hix(int J, int p, int n) {
-  return (J * kMp + p) * kMn + ((((n >> 2) ^ (p >> 1)) & 3) << 2) + (n & 3);
-}
-// Output staging tile [32 t][32 channels] bf16 (2 KB, in place of 32 rows of
-// an sH block): 4-channel units XORed with 2 (t & 3), even, so the 8-channel
-// pairs read back as 16-byte pieces stay intact.
-__device__ inline int yix(int t, int pl) {
-  return t * 32 + ((((pl >> 2) ^ (2 * (t & 3))) & 7) << 2) + (pl & 3);
-}
-
-// x and B of a half-tile as raw 16-byte pieces, loaded first (all loads in
-// flight at once) and transposed into LDS afterwards.  Rows at or past L are
-// loaded from row L-1 (in bounds) and zeroed with a select, so no load sits
-// behind a divergent branch.  x item = (step quad tq, channel group g of 8),
-// one per thread; B item = (step pair tp, state group ng of 8), threads < 128.
-struct XbRegs {
-  u32x4 x[4];
-  u32x4 b[2];
-};
-
-__device__ inline void mfma_load_xb(const SsdArgs& a, uint32_t b, uint32_t h, int64_t t0,
-                                    int tid, XbRegs& r) {
-  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h;
-  const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
-  const int64_t last = a.L - 1;
-  const int tq = tid >> 3, g = tid & 7;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int64_t t = t0 + 4 * tq + k;
-    r.x[k] = __builtin_nontemporal_load(
-        reinterpret_cast<const u32x4*>(xb + (t < last ? t : last) * a.sx_l + 8 * g));
-  }
-  if (tid < kMu) {
-    const int tp = tid >> 1, ng = tid & 1;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int64_t t = t0 + 2 * tp + k;
-      r.b[k] = *reinterpret_cast<const u32x4*>(Bb + (t < last ? t : last) * a.sB_l + 8 * ng);
-    }
-  }
-}
-
 // Low (sel 0x05040100) or high (0x07060302) 16-bit halves of two words,
 // packed (first word's half in the low half): one v_perm_b32.
 __device__ inline uint32_t perm_lo(uint32_t w0, uint32_t w1) {
@@ -434,45 +364,6 @@ __device__ inline uint32_t perm_lo(uint32_t w0, uint32_t w1) {
 }
 __device__ inline uint32_t perm_hi(uint32_t w0, uint32_t w1) {
   return __builtin_amdgcn_perm(w1, w0, 0x07060302u);
-}
-
-__device__ inline void mfma_store_xb(const SsdArgs& a, int64_t t0, int tid, const XbRegs& r,
-                                     uint16_t* xT, uint16_t* BT) {
-  const u32x4 zero = {0, 0, 0, 0};
-  const bool full = t0 + kMu <= a.L;  // uniform: no row of the half is past L
-  {
-    const int tq = tid >> 3, g = tid & 7;
-    u32x4 w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) w[k] = (full || t0 + 4 * tq + k < a.L) ? r.x[k] : zero;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const int k = e >> 1;
-      *reinterpret_cast<uint2*>(xT + tix(8 * g + e, 4 * tq)) =
-          make_uint2(perm_lo(w[0][k], w[1][k]), perm_lo(w[2][k], w[3][k]));
-      *reinterpret_cast<uint2*>(xT + tix(8 * g + e + 1, 4 * tq)) =
-          make_uint2(perm_hi(w[0][k], w[1][k]), perm_hi(w[2][k], w[3][k]));
-    }
-  }
-  if (tid < kMu) {
-    const int tp = tid >> 1, ng = tid & 1;
-    u32x4 w[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) w[k] = (full || t0 + 2 * tp + k < a.L) ? r.b[k] : zero;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const int k = e >> 1;
-      *reinterpret_cast<uint32_t*>(BT + tix(8 * ng + e, 2 * tp)) = perm_lo(w[0][k], w[1][k]);
-      *reinterpret_cast<uint32_t*>(BT + tix(8 * ng + e + 1, 2 * tp)) = perm_hi(w[0][k], w[1][k]);
-    }
-  }
-}
-
-// dt of step t0+tid (row clamped into [0, L); zeroed by mfma_step_scalars).
-__device__ inline float mfma_load_dt(const SsdArgs& a, uint32_t b, uint32_t h, int64_t t0,
-                                     int tid) {
-  const int64_t t = t0 + tid;
-  return a.dt[b * a.sdt_b + (t < a.L ? t : a.L - 1) * a.sdt_l + h * a.sdt_h];
 }
 
 // Per-step decay exponent (log2 units) and input coefficient of step t0+tid;
@@ -487,380 +378,408 @@ __device__ inline void mfma_step_scalars(const SsdArgs& a, uint32_t h, int64_t t
   *coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(x * 0.6931471805599453f, exp2_fast(x)) * d : d;
 }
 
-// Bw operand of a 16x16x32 product: B_s[n] for n = lane%16 and the 8 steps
-// s0..s0+7 (BT row n), scaled by s_w[s], split hi/lo.
-__device__ inline void mfma_bw_operand(const uint16_t* BT, const float* s_w, int n, int s0,
-                                       bf16x8_t& hi, bf16x8_t& lo) {
-  const u32x4 bv = *reinterpret_cast<const u32x4*>(BT + tix(n, s0));
-  const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
-  const float4 w1 = *reinterpret_cast<const float4*>(s_w + s0 + 4);
-  float v[8] = {bf16_lo(bv[0]) * w0.x, bf16_hi(bv[0]) * w0.y, bf16_lo(bv[1]) * w0.z,
-                bf16_hi(bv[1]) * w0.w, bf16_lo(bv[2]) * w1.x, bf16_hi(bv[2]) * w1.y,
-                bf16_lo(bv[3]) * w1.z, bf16_hi(bv[3]) * w1.w};
-  split_bf16(v, hi, lo);
+// Tile passes on the matrix cores, one wave per tile: wave w of a workgroup
+// takes one (row, chunk) tile and walks its 32-step sub-chunks in order, the
+// P x N state held in registers (16 per lane).  The waves of a workgroup (4
+// rows of one chunk, sharing the 128-byte lines of B, C and dt) never wait
+// for each other.  Every product is a 16x16x16 bf16 MFMA.  Its result layout
+// (lane: column l%16, rows 4(l/16)+r) is its B operand layout (column l%16,
+// k = 4(l/16)+j), and its A operand layout (row l%16, k = 4(l/16)+j) is that
+// of the state as the state update leaves it, so Gram block, x product,
+// carried-state product and state update chain without moving data between
+// lanes.  With cum the inclusive prefix of log2 decay over a sub-chunk and
+// cumE its total:
+//   G[s][t]    = B_s . C_t                                (A = B rows, B = C rows)
+//   M[s][t]    = G[s][t] 2^(cum_t - cum_s) coef_s,  s <= t
+//   Y^T[p][t]  = 2^cum_t sum_n H[p][n] C_t[n] + sum_s x_s[p] M[s][t]
+//   H^T[n][p] <- 2^cumE H^T[n][p] + sum_s w_s B_s[n] x_s[p],  w_s = 2^(cumE - cum_s) coef_s
+// Pass 1 (ssd_state_wave_kernel) runs the state update from zero and writes
+// each tile's end state and decay product; pass 3 (ssd_out_wave_kernel)
+// starts from the tile's entry state and forms the outputs.  x, B and C
+// enter the products exactly; operands formed in fp32 (weighted Gram blocks,
+// weighted B, the state) enter as bf16 hi + lo parts (two products, ~16
+// mantissa bits), and every product and the state accumulate in fp32.
+constexpr int kWsub = 32;      // steps per sub-chunk
+constexpr int kWaveRows = 4;   // tiles (one per wave) per workgroup
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Wave-private LDS tiles, rows padded so that every access of a lane is one
+// base register plus a constant offset and the 16-row operand reads spread
+// over the banks (units of 8 bytes: bank pair 9 p + unit for x^T, 17 t + unit
+// for y, 10-dword rows for B):
+//   x^T [p][s]  64 rows x 32 steps bf16, 72-byte rows
+//   y   [t][p]  32 rows x 64 channels bf16, 136-byte rows (in the x^T space)
+//   B   [s][n]  32 rows x 16 states bf16, 40-byte rows
+constexpr int kWxRow = 36;   // bf16 elements per x^T row
+constexpr int kWyRow = 68;   // per y row
+constexpr int kWbRow = 20;   // per B row
+constexpr int kWxElems = kMp * kWxRow;  // 2304 (>= 32 * kWyRow = 2176)
+
+__device__ inline s16x4_t pk_s16x4(f32x4 v) {
+  return __builtin_bit_cast(s16x4_t, make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])));
+}
+__device__ inline f32x4 unpk_s16x4(s16x4_t v) {
+  const uint2 w = __builtin_bit_cast(uint2, v);
+  return f32x4{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+}
+__device__ inline f32x4 mfma16(s16x4_t a, s16x4_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
-// Persistent, XCD-aware tile schedule.  Workgroups are dispatched round-robin
-// over the 8 XCDs (blockIdx.x % 8), each with its own L2.  The heads of one
-// (batch, time range) share the 128-byte lines of the [B, L, H, *] inputs
-// (a head owns 128 B of x but only 32 B of B/C and 4 B of dt per step), so
-// XCD x takes the chunks c = x (mod 8) and its workgroups walk that list
-// chunk by chunk, all rows of a chunk at once: every line is fetched into one
-// L2 once.  The mapping affects only locality; every tile is visited exactly
-// once for any grid size that is a multiple of 8.
-struct XcdTiles {
-  uint32_t xcd, j, nloc, rows, nchunks;
-  __device__ XcdTiles(uint32_t rows_, uint32_t nchunks_)
-      : xcd(blockIdx.x & 7u), j(blockIdx.x >> 3), nloc(gridDim.x >> 3), rows(rows_),
-        nchunks(nchunks_) {}
-  __device__ uint32_t chunk_of(uint32_t jj) const { return xcd + 8u * (jj / rows); }
-  __device__ bool valid(uint32_t jj) const { return chunk_of(jj) < nchunks; }
-  __device__ uint32_t row_of(uint32_t jj) const { return jj % rows; }
-};
+// Buffer descriptor over [base, base + bytes): loads past the end read zero,
+// stores past it are dropped.
+__device__ inline __amdgpu_buffer_rsrc_t wave_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           0x00020000);
+}
 
-// Unit walk shared by both passes: the halves of a tile in order (a second
-// half that starts at or past L is skipped), then the next tile of the
-// schedule.
-struct UnitWalk {
-  uint32_t jt, c, row;
-  int half;
-  __device__ bool second_half_follows(const SsdArgs& a) const {
-    return half == 0 && (int64_t)c * kMq + kMu < a.L;
+// One wave's tile.  blockIdx -> (chunk, group of rows): XCD x (blockIdx % 8)
+// takes the chunks c = x (mod 8), all row groups of a chunk in consecutive
+// slots, so every line shared by the heads of a step is fetched into one L2.
+// Global memory goes through buffer descriptors based at the tile's first row
+// and ending at the sequence's last row, so rows past L read as zero and
+// their stores are dropped (every row stride covers a row, which the host
+// checks); lane offsets are 32-bit registers, sub-chunk offsets scalars.
+// x is read as (step quad sq, channel group g8) 16-byte pieces, B and C as
+// (step 16 sg + c16, states 4q..4q+3) 8-byte pieces, dt at step lane % 32.
+struct WaveTile {
+  uint32_t row, c, b, h;
+  int64_t tbeg;
+  int nsub;
+  __amdgpu_buffer_rsrc_t rx, rB, rd;
+  int32_t bx, bB, bd;
+  uint32_t ox, oB, od;
+  // wave index as a scalar: every base below is uniform per wave
+  __device__ bool init(const SsdArgs& a, uint32_t ngroups, int wv, int lane) {
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    c = xcd + 8u * (slot / ngroups);
+    row = (slot % ngroups) * kWaveRows + (uint32_t)wv;
+    if (c >= a.nchunks || row >= a.rows) return false;
+    b = row / a.H;
+    h = row - b * a.H;
+    tbeg = (int64_t)c * kMq;
+    const int64_t nrow = (tbeg + kMq < a.L ? tbeg + kMq : a.L) - tbeg;
+    nsub = (int)((nrow + kWsub - 1) / kWsub);
+    const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h;
+    const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
+    const float* dtb = a.dt + b * a.sdt_b + h * a.sdt_h;
+    rx = wave_rsrc(xb + tbeg * a.sx_l, ((nrow - 1) * a.sx_l + kMp) * 2);
+    rB = wave_rsrc(Bb + tbeg * a.sB_l, ((nrow - 1) * a.sB_l + kMn) * 2);
+    rd = wave_rsrc(dtb + tbeg * a.sdt_l, ((nrow - 1) * a.sdt_l + 1) * 4);
+    bx = (int32_t)(a.sx_l * 2);
+    bB = (int32_t)(a.sB_l * 2);
+    bd = (int32_t)(a.sdt_l * 4);
+    const int c16 = lane & 15, q = lane >> 4, g8 = lane & 7, sq = lane >> 3;
+    ox = (uint32_t)(4 * sq * bx + 16 * g8);
+    oB = (uint32_t)(c16 * bB + 8 * q);
+    od = (uint32_t)((lane & 31) * bd);
+    return true;
+  }
+  __device__ void load(int r0, u32x4* xr, u32x2* bq, float& dtv) const {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      xr[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)ox, (r0 + k) * bx, kBufNt);
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg)
+      bq[sg] = __builtin_amdgcn_raw_buffer_load_b64(rB, (int)oB, (r0 + 16 * sg) * bB, 0);
+    dtv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, (int)od, r0 * bd, 0));
   }
 };
 
-// Pass 1: state of each tile from zero (decay product in chunkA, P x N state
-// [p][n] in chunkX).  Wave w forms the 16 channels 16w..16w+15.  Persistent:
-// the next half's global loads are issued before the current half's products.
+// x^T of a sub-chunk into LDS: the lane holds rows 4sq..4sq+3, channels
+// 8g8..8g8+7, and writes 4 steps of each of its 8 channels.
+__device__ inline void wave_put_xt(uint16_t* xt, const u32x4* w, int g8, int sq) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const int m = e >> 1;
+    *reinterpret_cast<uint2*>(xt + (8 * g8 + e) * kWxRow + 4 * sq) =
+        make_uint2(perm_lo(w[0][m], w[1][m]), perm_lo(w[2][m], w[3][m]));
+    *reinterpret_cast<uint2*>(xt + (8 * g8 + e + 1) * kWxRow + 4 * sq) =
+        make_uint2(perm_hi(w[0][m], w[1][m]), perm_hi(w[2][m], w[3][m]));
+  }
+}
+
+// Per-step scalars of a sub-chunk (lanes i and i + 32: step i): inclusive
+// prefix of the log2 decay, input coefficient and the sub-chunk total.
+// Steps at or past L get dt = 0 (decay 1, coefficient 0).
 template <int DISC>
-__global__ __launch_bounds__(256) void ssd_state_mfma_kernel(SsdArgs a) {
-  __shared__ __align__(16) uint16_t xT[kMp * kMu];
-  __shared__ __align__(16) uint16_t BT[kMn * kMu];
-  __shared__ __align__(16) float s_w[kMu];
-  __shared__ float s_tot[2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const XcdTiles sched(a.rows, a.nchunks);
-  if (!sched.valid(sched.j)) return;
-  UnitWalk u{sched.j, sched.chunk_of(sched.j), sched.row_of(sched.j), 0};
-  float dl = 0.0f;
-  XbRegs xr;
-  auto load_unit = [&](uint32_t cc, uint32_t rr, int hf) {
-    const uint32_t bb = rr / a.H, hd = rr - bb * a.H;
-    const int64_t tt0 = (int64_t)cc * kMq + hf * kMu;
-    if (tid < kMu) dl = mfma_load_dt(a, bb, hd, tt0, tid);
-    mfma_load_xb(a, bb, hd, tt0, tid, xr);
-  };
-  load_unit(u.c, u.row, 0);
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  float ltot = 0.0f;  // log2 decay of the tile so far
-  const int n = lane & 15, q = lane >> 4;
-  const int p = 16 * wave + (lane & 15);
-  for (;;) {
-    const uint32_t h = u.row % a.H;
-    const int64_t t0 = (int64_t)u.c * kMq + u.half * kMu;
-    // exclusive suffix of l2 within the half: inclusive suffix within the
-    // wave, shifted down one lane, plus (wave 0) the other wave's total
-    float ex = 0.0f, coef = 0.0f;
-    if (tid < kMu) {
-      float l2;
-      mfma_step_scalars<DISC>(a, h, t0, tid, dl, &l2, &coef);
-      float v = l2;
+__device__ inline void wave_scalars(float dtv, bool live, float a2, int lane, float& pre,
+                                    float& cf, float& cumE) {
+  const int s = lane & 31;
+  const float d = live ? dtv : 0.0f;
+  const float l2 = d * a2;
+  cf = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(l2 * 0.6931471805599453f, exp2_fast(l2)) * d : d;
+  pre = l2;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float w = __shfl_down(v, o);
-        v += (lane + o < 64) ? w : 0.0f;
-      }
-      if (lane == 0) s_tot[wave] = v;
-      ex = __shfl_down(v, 1);
-      ex = lane < 63 ? ex : 0.0f;
-    }
-    mfma_store_xb(a, t0, tid, xr, xT, BT);
-    __syncthreads();
-    const float lhalf = s_tot[0] + s_tot[1];
-    if (tid < kMu) s_w[tid] = exp2_fast(wave == 0 ? ex + s_tot[1] : ex) * coef;
-    __syncthreads();
-    // next unit's loads overlap this half's products
-    UnitWalk nx = u;
-    bool more = true;
-    const bool tile_ends = !u.second_half_follows(a);
-    if (!tile_ends) {
-      nx.half = 1;
-    } else {
-      nx.jt = u.jt + sched.nloc;
-      more = sched.valid(nx.jt);
-      nx.c = sched.chunk_of(nx.jt);
-      nx.row = sched.row_of(nx.jt);
-      nx.half = 0;
-    }
-    if (more) load_unit(nx.c, nx.row, nx.half);
-    // state <- 2^(this half's decay) state + this half's products
-    const float sc = exp2_fast(lhalf);
+  for (int o = 1; o < 32; o <<= 1) {
+    const float v = __shfl_up(pre, o);
+    pre += (s >= o) ? v : 0.0f;
+  }
+  cumE = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pre), 31));
+}
+
+// x^T pieces: x_s[p] for p = 16 pi + c16, s = 16 sg + 4q .. +3.
+__device__ inline void wave_get_xa(const uint16_t* xt, int c16, int q, s16x4_t (*xa)[2]) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] *= sc;
+  for (int pi = 0; pi < 4; ++pi)
 #pragma unroll
-    for (int kk = 0; kk < kMu / 32; ++kk) {
-      const int s0 = 32 * kk + 8 * q;
-      const bf16x8_t ax = as_bf16x8(*reinterpret_cast<const u32x4*>(xT + tix(p, s0)));
-      bf16x8_t bhi, blo;
-      mfma_bw_operand(BT, s_w, n, s0, bhi, blo);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bhi, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, blo, acc, 0, 0, 0);
-    }
-    ltot += lhalf;
-    if (tile_ends) {
-      float* out = a.chunkX + ((int64_t)u.row * a.nchunks + u.c) * (kMp * kMn);
+    for (int sg = 0; sg < 2; ++sg)
+      xa[pi][sg] = __builtin_bit_cast(
+          s16x4_t, *reinterpret_cast<const uint2*>(xt + (16 * pi + c16) * kWxRow + 16 * sg + 4 * q));
+}
+
+// State update to the end of a sub-chunk: H^T <- At H^T + (w B)^T x, with the
+// A operand (w B)^T (row n = c16, k = steps 16 sg + 4q .. +3) read transposed
+// from the B rows in LDS and split hi/lo.
+__device__ inline void wave_state_update(f32x4* st, const s16x4_t (*xa)[2], const uint16_t* bs,
+                                         const float* sw, int c16, int q, float At) {
+  s16x4_t wb[2], wl[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) out[(16 * wave + 4 * q + r) * kMn + n] = acc[r];
-      if (tid == 0) a.chunkA[(int64_t)u.row * a.nchunks + u.c] = exp2_fast(ltot);
-      acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      ltot = 0.0f;
-    }
-    if (!more) break;
-    u = nx;
-    __syncthreads();  // LDS is rewritten by the next half
+  for (int sg = 0; sg < 2; ++sg) {
+    const f32x4 ws = *reinterpret_cast<const f32x4*>(sw + 16 * sg + 4 * q);
+    f32x4 v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = bf16_bits_to_f32(bs[(16 * sg + 4 * q + j) * kWbRow + c16]) * ws[j];
+    wb[sg] = pk_s16x4(v);
+    wl[sg] = pk_s16x4(v - unpk_s16x4(wb[sg]));
+  }
+#pragma unroll
+  for (int pi = 0; pi < 4; ++pi) {
+    f32x4 v = st[pi];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] *= At;
+    v = mfma16(wb[0], xa[pi][0], v);
+    v = mfma16(wl[0], xa[pi][0], v);
+    v = mfma16(wb[1], xa[pi][1], v);
+    v = mfma16(wl[1], xa[pi][1], v);
+    st[pi] = v;
   }
 }
 
-// Pass 3: outputs.  Wave w owns sub-chunk w of each half.  Persistent like
-// pass 1; the state entering a half is carried in registers (each thread owns
-// 4 of the 1024 entries): the tile's entry state for the first half, the
-// first half's end state for the second.
-template <int DISC, bool HAS_D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void ssd_out_mfma_kernel(SsdArgs a) {
-  __shared__ __align__(16) uint16_t xT[kMp * kMu];
-  __shared__ __align__(16) uint16_t BT[kMn * kMu];
-  __shared__ __align__(16) float sH[4 * kMp * kMn];  // S_J, then H_J, [J][p][n]
-  __shared__ __align__(16) float s_cum[kMu];
-  __shared__ __align__(16) float s_coef[kMu];
-  __shared__ __align__(16) float s_w[kMu];
-  __shared__ float s_AJ[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hh = lane >> 5;
-  const XcdTiles sched(a.rows, a.nchunks);
-  if (!sched.valid(sched.j)) return;
-  UnitWalk u{sched.j, sched.chunk_of(sched.j), sched.row_of(sched.j), 0};
-
-  // global loads of one half: dt of step tid, x and B pieces for the LDS
-  // tiles, B and C rows of the wave's sub-chunk (Gram and carried-state
-  // products).  Rows past L are read from row L-1 and zeroed later.
-  float dl = 0.0f;
-  XbRegs xr;
-  u32x4 brow, crow;
-  float hnew[4];
-  auto load_unit = [&](uint32_t cc, uint32_t rr, int hf) {
-    const uint32_t bb = rr / a.H, hd = rr - bb * a.H;
-    const int64_t tt0 = (int64_t)cc * kMq + hf * kMu;
-    if (tid < kMu) dl = mfma_load_dt(a, bb, hd, tt0, tid);
-    const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + bb * a.sB_b + hd * a.sB_h;
-    const uint16_t* Cb = reinterpret_cast<const uint16_t*>(a.C) + bb * a.sC_b + hd * a.sC_h;
-    const int64_t t = tt0 + kMsub * wave + l32;
-    const int64_t tc = t < a.L ? t : a.L - 1;
-    brow = *reinterpret_cast<const u32x4*>(Bb + tc * a.sB_l + 8 * hh);
-    crow = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(Cb + tc * a.sC_l + 8 * hh));
-    mfma_load_xb(a, bb, hd, tt0, tid, xr);
-    if (hf == 0) {
-      const float* en = a.entry + ((int64_t)rr * a.nchunks + cc) * (kMp * kMn);
+// Pass 1: end state of each tile from zero ([p][n] in chunkX) and its decay
+// product (chunkA).
+template <int DISC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_state_wave_kernel(SsdArgs a, uint32_t ngroups) {
+  __shared__ __align__(16) uint16_t s_xt[kWaveRows][kMp * kWxRow];
+  __shared__ __align__(16) uint16_t s_b[kWaveRows][kWsub * kWbRow];
+  __shared__ __align__(16) float s_w[kWaveRows][kWsub];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, q = lane >> 4, g8 = lane & 7, sq = lane >> 3;
+  WaveTile wt;
+  if (!wt.init(a, ngroups, wv, lane)) return;  // whole waves; no barriers below
+  uint16_t* xt = s_xt[wv];
+  uint16_t* bs = s_b[wv];
+  float* sw = s_w[wv];
+  const float a2 = -expf(a.A_log[wt.h]) * kLog2e;
+  u32x4 xr[4];
+  u32x2 bq[2];
+  float dtv;
+  wt.load(0, xr, bq, dtv);
+  f32x4 st[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) hnew[k] = en[tid + 256 * k];
-    }
-  };
-  load_unit(u.c, u.row, 0);
-  float hc[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) hc[k] = hnew[k];
-
-  for (;;) {
-    const uint32_t b = u.row / a.H, h = u.row - b * a.H;
-    const int64_t t0 = (int64_t)u.c * kMq + u.half * kMu;
-    // prefix (inclusive) and suffix (exclusive) sums within 32-step sub-chunks
-    if (tid < kMu) {
-      float l2, coef;
-      mfma_step_scalars<DISC>(a, h, t0, tid, dl, &l2, &coef);
-      float pre = l2, suf = l2;
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) {
-        const float w = __shfl_up(pre, o), d = __shfl_down(suf, o);
-        pre += (l32 >= o) ? w : 0.0f;
-        suf += (l32 + o < 32) ? d : 0.0f;
-      }
-      float sx = __shfl_down(suf, 1);
-      sx = l32 < 31 ? sx : 0.0f;
-      s_cum[tid] = pre;
-      s_coef[tid] = coef;
-      s_w[tid] = exp2_fast(sx) * coef;
-      if (l32 == 31) s_AJ[tid >> 5] = exp2_fast(pre);
-    }
-    const bool live = t0 + kMsub * wave + l32 < a.L;
-    const u32x4 bcur = live ? brow : u32x4{0, 0, 0, 0};
-    const u32x4 ccur = live ? crow : u32x4{0, 0, 0, 0};
-    mfma_store_xb(a, t0, tid, xr, xT, BT);
-    __syncthreads();
-
-    // next unit's loads overlap everything below
-    UnitWalk nx = u;
-    bool more = true;
-    if (u.second_half_follows(a)) {
-      nx.half = 1;
-    } else {
-      nx.jt = u.jt + sched.nloc;
-      more = sched.valid(nx.jt);
-      nx.c = sched.chunk_of(nx.jt);
-      nx.row = sched.row_of(nx.jt);
-      nx.half = 0;
-    }
-    if (more) load_unit(nx.c, nx.row, nx.half);
-
-    const int J = wave;
-    const int sb = kMsub * J;
-    // local state of the wave's sub-chunk (16x16x32, K = its 32 steps)
-    {
-      const int n = lane & 15, q = lane >> 4;
-      const int s0 = sb + 8 * q;
-      bf16x8_t bhi, blo;
-      mfma_bw_operand(BT, s_w, n, s0, bhi, blo);
-#pragma unroll
-      for (int pb = 0; pb < kMp / 16; ++pb) {
-        const bf16x8_t ax = as_bf16x8(*reinterpret_cast<const u32x4*>(xT + tix(16 * pb + n, s0)));
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bhi, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, blo, acc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sH[hix(J, 16 * pb + 4 * q + r, n)] = acc[r];
-      }
-    }
-    __syncthreads();
-    // entry state of every sub-chunk: H_0 = state entering the half,
-    // H_{J+1} = A_J H_J + S_J; the end state carries into the next half
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int e = tid + 256 * k;
-      float hv = hc[k];
-#pragma unroll
-      for (int JJ = 0; JJ < 4; ++JJ) {
-        const float sj = sH[hix(JJ, e >> 4, e & 15)];
-        sH[hix(JJ, e >> 4, e & 15)] = hv;
-        hv = __builtin_fmaf(s_AJ[JJ], hv, sj);
-      }
-      hc[k] = hv;
-    }
-    __syncthreads();
-
-    // outputs of the wave's sub-chunk
-    {
-      uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + b * a.sy_b + h * a.sy_h;
-      // Gram^T: D[s][t] = B_s . C_t (lane: t = l32, rows s over the registers)
-      f32x16_t g = {};
-      g = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(bcur), as_bf16x8(ccur), g, 0, 0, 0);
-      const float cum_t = s_cum[sb + l32];
-      float m[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int s = (r >> 2) * 8 + 4 * hh + (r & 3);
-        const float dec = exp2_fast(cum_t - s_cum[sb + s]) * s_coef[sb + s];
-        m[r] = s <= l32 ? g[r] * dec : 0.0f;
-      }
-      bf16x8_t mhi[2], mlo[2];
-      split_bf16(m, mhi[0], mlo[0]);
-      split_bf16(m + 8, mhi[1], mlo[1]);
-      const float u_t = exp2_fast(cum_t);
-      // one block of 32 channels at a time: carried state Z[p][t] = H_J[p] . C_t
-      // scaled by 2^cum_t, plus the in-sub-chunk products M x, then stage
+  for (int pi = 0; pi < 4; ++pi) st[pi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float ltot = 0.0f;
 #pragma unroll 1
-      for (int pb = 0; pb < kMp / 32; ++pb) {
-        const float4 h0 = *reinterpret_cast<const float4*>(sH + hix(J, 32 * pb + l32, 8 * hh));
-        const float4 h1 = *reinterpret_cast<const float4*>(sH + hix(J, 32 * pb + l32, 8 * hh + 4));
-        const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-        bf16x8_t hhi, hlo;
-        split_bf16(hv, hhi, hlo);
-        f32x16_t acc = {};
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hhi, as_bf16x8(ccur), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hlo, as_bf16x8(ccur), acc, 0, 0, 0);
+  for (int k = 0; k < wt.nsub; ++k) {
+    const int r0 = k * kWsub;
+    wave_put_xt(xt, xr, g8, sq);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] *= u_t;
+    for (int sg = 0; sg < 2; ++sg)
+      *reinterpret_cast<u32x2*>(bs + (16 * sg + c16) * kWbRow + 4 * q) = bq[sg];
+    float pre, cf, cumE;
+    wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, lane, pre, cf, cumE);
+    if (lane < 32) sw[lane] = exp2_fast(cumE - pre) * cf;
+    ltot += cumE;
+    // the next sub-chunk's loads overlap everything below
+    if (k + 1 < wt.nsub) wt.load(r0 + kWsub, xr, bq, dtv);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    s16x4_t xa[4][2];
+    wave_get_xa(xt, c16, q, xa);
+    wave_state_update(st, xa, bs, sw, c16, q, exp2_fast(cumE));
+  }
+  float* out = a.chunkX + ((int64_t)wt.row * a.nchunks + wt.c) * (kMp * kMn);
 #pragma unroll
-        for (int kap = 0; kap < 2; ++kap) {
-          const int xr_row = 32 * pb + l32, xr_col = sb + 16 * kap + 4 * hh;
-          const uint2 x0 = *reinterpret_cast<const uint2*>(xT + tix(xr_row, xr_col));
-          const uint2 x1 = *reinterpret_cast<const uint2*>(xT + tix(xr_row, xr_col + 8));
-          const bf16x8_t ax = as_bf16x8(u32x4{x0.x, x0.y, x1.x, x1.y});
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, mhi[kap], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, mlo[kap], acc, 0, 0, 0);
+  for (int pi = 0; pi < 4; ++pi)
+    *reinterpret_cast<f32x4*>(out + (16 * pi + c16) * kMn + 4 * q) = st[pi];
+  if (lane == 0) a.chunkA[(int64_t)wt.row * a.nchunks + wt.c] = exp2_fast(ltot);
+}
+
+// Pass 3: outputs of each tile from its entry state.
+template <int DISC, bool HAS_D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_out_wave_kernel(SsdArgs a, uint32_t ngroups) {
+  __shared__ __align__(16) uint16_t s_xt[kWaveRows][kWxElems];
+  __shared__ __align__(16) uint16_t s_b[kWaveRows][kWsub * kWbRow];
+  __shared__ __align__(16) float s_sc[kWaveRows][3][kWsub];  // cum, coef, w
+  __shared__ __align__(16) uint16_t s_xr[HAS_D ? kWaveRows : 1][HAS_D ? kWsub * kMp : 4];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, q = lane >> 4, g8 = lane & 7, sq = lane >> 3;
+  WaveTile wt;
+  if (!wt.init(a, ngroups, wv, lane)) return;  // whole waves; no barriers below
+  uint16_t* xt = s_xt[wv];
+  uint16_t* bs = s_b[wv];
+  float* scum = s_sc[wv][0];
+  float* scoef = s_sc[wv][1];
+  float* sw = s_sc[wv][2];
+  uint16_t* xrow = s_xr[HAS_D ? wv : 0];
+  const float a2 = -expf(a.A_log[wt.h]) * kLog2e;
+  const int64_t nrow = (wt.tbeg + kMq < a.L ? wt.tbeg + kMq : a.L) - wt.tbeg;
+  const uint16_t* Cb =
+      reinterpret_cast<const uint16_t*>(a.C) + wt.b * a.sC_b + wt.h * a.sC_h + wt.tbeg * a.sC_l;
+  uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + wt.b * a.sy_b + wt.h * a.sy_h + wt.tbeg * a.sy_l;
+  const __amdgpu_buffer_rsrc_t rC = wave_rsrc(Cb, ((nrow - 1) * a.sC_l + kMn) * 2);
+  const __amdgpu_buffer_rsrc_t ry = wave_rsrc(yb, ((nrow - 1) * a.sy_l + kMp) * 2);
+  const int32_t bC = (int32_t)(a.sC_l * 2), by = (int32_t)(a.sy_l * 2);
+  const uint32_t oC = (uint32_t)(c16 * bC + 8 * q);
+  const uint32_t oy = (uint32_t)(q * by + 8 * c16);
+  u32x4 xr[4];
+  u32x2 bq[2], cq[2];
+  float dtv;
+  auto load_sub = [&](int r0) {  // r0: first row of the sub-chunk, from the tile start
+    wt.load(r0, xr, bq, dtv);
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg)
+      cq[sg] = __builtin_amdgcn_raw_buffer_load_b64(rC, (int)oC, (r0 + 16 * sg) * bC, kBufNt);
+  };
+  load_sub(0);
+
+  // state entering the tile: lane holds H[16 pi + c16][4q..4q+3]
+  f32x4 st[4];
+  {
+    const float* en = a.entry + ((int64_t)wt.row * a.nchunks + wt.c) * (kMp * kMn);
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi)
+      st[pi] = *reinterpret_cast<const f32x4*>(en + (16 * pi + c16) * kMn + 4 * q);
+  }
+  float dsk[4][4];
+  if constexpr (HAS_D) {
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dsk[pi][r] = a.D[wt.h * kMp + 16 * pi + 4 * q + r];
+  }
+
+#pragma unroll 1
+  for (int k = 0; k < wt.nsub; ++k) {
+    const int r0 = k * kWsub;
+    // x^T, B rows (and the row-major x for the skip term) into LDS
+    const u32x2 bz[2] = {bq[0], bq[1]}, cz[2] = {cq[0], cq[1]};
+    wave_put_xt(xt, xr, g8, sq);
+    if constexpr (HAS_D) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        *reinterpret_cast<u32x4*>(xrow + (4 * sq + kk) * kMp + 8 * g8) = xr[kk];
+    }
+#pragma unroll
+    for (int sg = 0; sg < 2; ++sg)
+      *reinterpret_cast<u32x2*>(bs + (16 * sg + c16) * kWbRow + 4 * q) = bz[sg];
+    float pre, cf, cumE;
+    wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, lane, pre, cf, cumE);
+    if (lane < 32) {
+      scum[lane] = pre;
+      scoef[lane] = cf;
+      sw[lane] = exp2_fast(cumE - pre) * cf;
+    }
+    // the next sub-chunk's loads overlap everything below
+    if (k + 1 < wt.nsub) load_sub(r0 + kWsub);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+
+    // decay-weighted Gram blocks (s-block sg <= t-block tb) as the B operands
+    // of the x products, split hi/lo
+    s16x4_t mb[3], ml[3];  // (tb, sg) = (0, 0), (1, 0), (1, 1)
+    {
+      const f32x4 cs[2] = {*reinterpret_cast<const f32x4*>(scum + 4 * q),
+                           *reinterpret_cast<const f32x4*>(scum + 16 + 4 * q)};
+      const f32x4 cfv[2] = {*reinterpret_cast<const f32x4*>(scoef + 4 * q),
+                            *reinterpret_cast<const f32x4*>(scoef + 16 + 4 * q)};
+      const float cumt[2] = {scum[c16], scum[16 + c16]};
+#pragma unroll
+      for (int blk = 0; blk < 3; ++blk) {
+        const int tb = blk == 0 ? 0 : 1, sg = blk == 2 ? 1 : 0;
+        const f32x4 g = mfma16(__builtin_bit_cast(s16x4_t, bz[sg]),
+                               __builtin_bit_cast(s16x4_t, cz[tb]), f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        f32x4 m;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          m[r] = g[r] * exp2_fast(cumt[tb] - cs[sg][r]) * cfv[sg][r];
+          if (sg == tb) m[r] = 4 * q + r <= c16 ? m[r] : 0.0f;
         }
-        // skip term; stage y[t][32 pb + pl] (bf16) in the rows of H_J this
-        // block has finished with: lane holds t = l32 and 4 runs of 4 channels
-        uint16_t* ys = reinterpret_cast<uint16_t*>(sH + hix(J, 32 * pb, 0));
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int pc = 32 * pb + 8 * qq + 4 * hh;
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            v[r] = acc[4 * qq + r];
-            if constexpr (HAS_D) {
-              const float xv = bf16_bits_to_f32(xT[tix(pc + r, sb + l32)]);
-              v[r] = __builtin_fmaf(a.D[h * kMp + pc + r], xv, v[r]);
-            }
-          }
-          *reinterpret_cast<uint2*>(ys + yix(l32, 8 * qq + 4 * hh)) =
-              make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3]));
-        }
-      }
-      // the staged 32 x 64 tile leaves as whole 128-byte rows (8 lanes a row)
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = lane + 64 * k, tr = i >> 3, cg = i & 7;
-        const uint16_t* ys = reinterpret_cast<const uint16_t*>(sH + hix(J, 32 * (cg >> 2), 0));
-        const u32x4 v = *reinterpret_cast<const u32x4*>(ys + yix(tr, 8 * (cg & 3)));
-        const int64_t tt = t0 + sb + tr;
-        if (tt < a.L) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(yb + tt * a.sy_l + 8 * cg));
+        mb[blk] = pk_s16x4(m);
+        ml[blk] = pk_s16x4(m - unpk_s16x4(mb[blk]));
       }
     }
-    if (!more) break;
-    if (nx.half == 0) {
+    s16x4_t xa[4][2];
+    wave_get_xa(xt, c16, q, xa);
+
+    // outputs, 16 steps t at a time; the staged rows replace x^T (all of
+    // whose reads are above)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) hc[k] = hnew[k];
+    for (int tb = 0; tb < 2; ++tb) {
+      const s16x4_t cb = __builtin_bit_cast(s16x4_t, cz[tb]);
+      const int t = 16 * tb + c16;
+      const float ut = exp2_fast(scum[t]);
+#pragma unroll
+      for (int pi = 0; pi < 4; ++pi) {
+        const s16x4_t sh = pk_s16x4(st[pi]);
+        f32x4 acc = mfma16(sh, cb, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        acc = mfma16(pk_s16x4(st[pi] - unpk_s16x4(sh)), cb, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] *= ut;
+        acc = mfma16(xa[pi][0], mb[tb], acc);
+        acc = mfma16(xa[pi][0], ml[tb], acc);
+        if (tb == 1) {
+          acc = mfma16(xa[pi][1], mb[2], acc);
+          acc = mfma16(xa[pi][1], ml[2], acc);
+        }
+        if constexpr (HAS_D) {
+          const uint2 xv = *reinterpret_cast<const uint2*>(xrow + t * kMp + 16 * pi + 4 * q);
+          acc[0] = __builtin_fmaf(dsk[pi][0], bf16_lo(xv.x), acc[0]);
+          acc[1] = __builtin_fmaf(dsk[pi][1], bf16_hi(xv.x), acc[1]);
+          acc[2] = __builtin_fmaf(dsk[pi][2], bf16_lo(xv.y), acc[2]);
+          acc[3] = __builtin_fmaf(dsk[pi][3], bf16_hi(xv.y), acc[3]);
+        }
+        *reinterpret_cast<uint2*>(xt + t * kWyRow + 16 * pi + 4 * q) =
+            make_uint2(pk_bf16(acc[0], acc[1]), pk_bf16(acc[2], acc[3]));
+      }
     }
-    u = nx;
-    __syncthreads();  // LDS is rewritten by the next half
+    wave_state_update(st, xa, bs, sw, c16, q, exp2_fast(cumE));
+
+    // the staged 32 x 64 outputs leave as whole 128-byte rows (16 lanes a row)
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int tr = q + 4 * i;
+      const u32x2 v = *reinterpret_cast<const u32x2*>(xt + tr * kWyRow + 4 * c16);
+      __builtin_amdgcn_raw_buffer_store_b64(v, ry, (int)oy, (r0 + 4 * i) * by, kBufNt);
+    }
   }
 }
 
-// Workgroups of a persistent kernel: as many as can be resident at once,
-// rounded to a multiple of the 8 XCDs (at least 8), and no more than needed
-// to give every workgroup a tile.
-inline unsigned persistent_grid(const void* kernel, int threads, int64_t ntiles) {
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-      cus <= 0 || per_cu <= 0) {
-    (void)hipGetLastError();
-    cus = 1;
-    per_cu = 1;
-  }
-  int64_t g = (int64_t)cus * per_cu;
-  const int64_t cap = (ntiles + 7) / 8 * 8;
-  if (g > cap) g = cap;
-  g = g / 8 * 8;
-  return (unsigned)(g < 8 ? 8 : g);
+// The tile passes read rows past L as zero through the buffer range check:
+// every row stride must cover one row of the operand, and a tile's 256 rows
+// of every operand must span less than 2^31 bytes.
+inline bool ssd_wave_ok(const SsdArgs& a) {
+  const int64_t lim = (int64_t)1 << 31;
+  return a.sx_l >= kMp && a.sB_l >= kMn && a.sC_l >= kMn && a.sy_l >= kMp && a.sdt_l >= 1 &&
+         (kMq * a.sx_l + kMp) * 2 < lim && (kMq * a.sB_l + kMn) * 2 < lim &&
+         (kMq * a.sC_l + kMn) * 2 < lim && (kMq * a.sy_l + kMp) * 2 < lim &&
+         (kMq * a.sdt_l + 1) * 4 < lim;
 }
 
 template <int DISC>
 int launch_ssd_mfma(bool has_d, int64_t rows, int64_t nchunks, int64_t PN, hipStream_t s,
                     const SsdArgs& a) {
-  const int64_t ntiles = rows * nchunks;
-  const void* k1 = reinterpret_cast<const void*>(&ssd_state_mfma_kernel<DISC>);
-  const void* k3 = has_d ? reinterpret_cast<const void*>(&ssd_out_mfma_kernel<DISC, true>)
-                         : reinterpret_cast<const void*>(&ssd_out_mfma_kernel<DISC, false>);
-  hipLaunchKernelGGL((ssd_state_mfma_kernel<DISC>), dim3(persistent_grid(k1, 256, ntiles)),
-                     dim3(256), 0, s, a);
+  const uint32_t ngroups = (uint32_t)((rows + kWaveRows - 1) / kWaveRows);
+  const dim3 gw((unsigned)(8 * ((nchunks + 7) / 8) * ngroups));
+  hipLaunchKernelGGL((ssd_state_wave_kernel<DISC>), gw, dim3(256), 0, s, a, ngroups);
   const int64_t nblk = (PN + kPassEntries - 1) / kPassEntries;
   hipLaunchKernelGGL(ssd_pass_kernel, dim3((unsigned)(rows * nblk)), dim3(kPassEntries * kPassSegs),
                      0, s, a, PN);
-  const dim3 g3(persistent_grid(k3, 256, ntiles));
-  if (has_d) hipLaunchKernelGGL((ssd_out_mfma_kernel<DISC, true>), g3, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((ssd_out_mfma_kernel<DISC, false>), g3, dim3(256), 0, s, a);
+  if (has_d) hipLaunchKernelGGL((ssd_out_wave_kernel<DISC, true>), gw, dim3(256), 0, s, a, ngroups);
+  else hipLaunchKernelGGL((ssd_out_wave_kernel<DISC, false>), gw, dim3(256), 0, s, a, ngroups);
   return launch_status();
 }
 
@@ -888,8 +807,6 @@ int launch_ssd_mfma(bool has_d, int64_t rows, int64_t nchunks, int64_t PN, hipSt
 constexpr int kSqQ = 128;  // steps per block
 constexpr int kSqN = 64;   // state size
 constexpr int kSqP = 16;   // channels per product tile (a workgroup takes 1 or 2)
-
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 // LDS element offsets: 16-byte column blocks XORed with the row so that the
 // 16 rows read by one operand fetch spread over the banks.
@@ -1375,8 +1292,9 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
   a.tc = (uint32_t)tc;
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr;
-  // bf16 at P = 64, N = 16 with 256-step tiles: matrix-core passes
-  if (dtype == TSSM_BF16 && P == kMp && N == kMn && tc == kMq) {
+  // bf16 at P = 64, N = 16 with 256-step tiles: matrix-core passes (other
+  // row strides take the generic passes)
+  if (dtype == TSSM_BF16 && P == kMp && N == kMn && tc == kMq && ssd_wave_ok(a)) {
     TSSM_CHECK(aligned(x, 16) && aligned(B, 16) && aligned(C, 16) && aligned(y, 8), TSSM_ERR_ALIGN);
     TSSM_CHECK(sx_l % 8 == 0 && sx_h % 8 == 0 && sx_b % 8 == 0 && sB_l % 8 == 0 && sB_b % 8 == 0 &&
                    sB_h % 8 == 0 && sC_l % 8 == 0 && sC_b % 8 == 0 && sC_h % 8 == 0 &&
