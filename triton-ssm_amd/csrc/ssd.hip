@@ -156,12 +156,16 @@ __global__ __launch_bounds__(64) void ssd_state_kernel(SsdArgs a) {
 }
 
 // Pass 2: thread (entry e, segment sg) of a 1024-thread workgroup covering 32
-// consecutive state entries of one row and 32 segments of its chunks.  The
-// chunk loops load 8 chunks at a time (indices clamped into the segment, so
-// every load is in bounds and none waits behind a branch) before folding them.
-constexpr int kPassEntries = 32, kPassSegs = 32, kPassBatch = 8;
+// consecutive state entries of one row and 32 segments of its chunks.  A
+// segment's first kPassBatch chunks are loaded at once and stay in registers
+// for the second sweep, so with up to 32 x kPassBatch chunks per row each
+// sweep is one round trip to memory; longer segments continue kPassTail
+// chunks at a time (indices clamped into the segment, so every load is in
+// bounds and none waits behind a branch).
+constexpr int kPassEntries = 32, kPassSegs = 32, kPassBatch = 32, kPassTail = 8;
 __global__ __launch_bounds__(1024) void ssd_pass_kernel(SsdArgs a, int64_t PN) {
   __shared__ float s_a[kPassSegs][kPassEntries], s_x[kPassSegs][kPassEntries];
+  __shared__ __align__(16) float s_ca[kPassSegs][kPassBatch];
   const int el = threadIdx.x % kPassEntries;
   const int sg = threadIdx.x / kPassEntries;
   const int64_t nblk = (PN + kPassEntries - 1) / kPassEntries;
@@ -171,19 +175,45 @@ __global__ __launch_bounds__(1024) void ssd_pass_kernel(SsdArgs a, int64_t PN) {
   const int64_t nc = a.nchunks;
   const int64_t seg = (nc + kPassSegs - 1) / kPassSegs;
   const int64_t c0 = sg * seg < nc ? sg * seg : nc, c1 = c0 + seg < nc ? c0 + seg : nc;
-  const float* cA = a.chunkA + row * nc;
-  const float* cX = a.chunkX + row * nc * PN + (act ? e : 0);
-  float A = 1.0f, X = 0.0f;
-  for (int64_t c = c0; c < c1; c += kPassBatch) {
-    float xa[kPassBatch], aa[kPassBatch];
+  // row bases are uniform; a row's chunk states are indexed with 32 bits
+  // (the host keeps nchunks * P * N below 2^31)
+  const char* cA = reinterpret_cast<const char*>(a.chunkA + row * nc);
+  const char* cX = reinterpret_cast<const char*>(a.chunkX + row * nc * PN);
+  const uint32_t e0 = act ? (uint32_t)e : 0u, pn = (uint32_t)PN;
+  const uint32_t cmax = (uint32_t)(c1 > c0 ? c1 - 1 : 0);  // last chunk of the segment
+  // byte offsets as 32-bit lane registers on a uniform base
+  auto ldx = [&](uint32_t cc) {
+    return *reinterpret_cast<const float*>(cX + (uint32_t)((cc * pn + e0) * 4u));
+  };
+  auto lda = [&](uint32_t cc) { return *reinterpret_cast<const float*>(cA + (uint32_t)(cc * 4u)); };
+  // the segment's first batch: chunk states in registers, chunk decays (the
+  // same for every entry) loaded once per segment into LDS, thread el taking
+  // chunk c0 + el
+  static_assert(kPassBatch == kPassEntries, "one decay per thread of a segment");
+  s_ca[sg][el] = lda(min((uint32_t)c0 + (uint32_t)el, cmax));
+  float x0[kPassBatch];
 #pragma unroll
-    for (int k = 0; k < kPassBatch; ++k) {
-      const int64_t cc = c + k < c1 ? c + k : c;
-      xa[k] = cX[cc * PN];
-      aa[k] = cA[cc];
+  for (int k = 0; k < kPassBatch; ++k) x0[k] = ldx(min((uint32_t)c0 + (uint32_t)k, cmax));
+  __syncthreads();
+  const float* a0 = s_ca[sg];
+  float A = 1.0f, X = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kPassBatch; ++k) {
+    if (c0 + k < c1) {
+      X = __builtin_fmaf(a0[k], X, x0[k]);
+      A *= a0[k];
+    }
+  }
+  for (int64_t c = c0 + kPassBatch; c < c1; c += kPassTail) {
+    float xa[kPassTail], aa[kPassTail];
+#pragma unroll
+    for (int k = 0; k < kPassTail; ++k) {
+      const uint32_t cc = min((uint32_t)(c + k), cmax);
+      xa[k] = ldx(cc);
+      aa[k] = lda(cc);
     }
 #pragma unroll
-    for (int k = 0; k < kPassBatch; ++k) {
+    for (int k = 0; k < kPassTail; ++k) {
       if (c + k < c1) {
         X = __builtin_fmaf(aa[k], X, xa[k]);
         A *= aa[k];
@@ -195,19 +225,26 @@ __global__ __launch_bounds__(1024) void ssd_pass_kernel(SsdArgs a, int64_t PN) {
   __syncthreads();
   float S = (act && a.h0) ? a.h0[row * PN + e] : 0.0f;
   for (int k = 0; k < sg; ++k) S = __builtin_fmaf(s_a[k][el], S, s_x[k][el]);
-  float* en = a.entry + row * nc * PN + (act ? e : 0);
-  for (int64_t c = c0; c < c1; c += kPassBatch) {
-    float xa[kPassBatch], aa[kPassBatch];
+  float* en = a.entry + row * nc * PN;
 #pragma unroll
-    for (int k = 0; k < kPassBatch; ++k) {
-      const int64_t cc = c + k < c1 ? c + k : c;
-      xa[k] = cX[cc * PN];
-      aa[k] = cA[cc];
+  for (int k = 0; k < kPassBatch; ++k) {
+    if (c0 + k < c1) {
+      if (act) en[(uint32_t)(c0 + k) * pn + e0] = S;
+      S = __builtin_fmaf(a0[k], S, x0[k]);
+    }
+  }
+  for (int64_t c = c0 + kPassBatch; c < c1; c += kPassTail) {
+    float xa[kPassTail], aa[kPassTail];
+#pragma unroll
+    for (int k = 0; k < kPassTail; ++k) {
+      const uint32_t cc = min((uint32_t)(c + k), cmax);
+      xa[k] = ldx(cc);
+      aa[k] = lda(cc);
     }
 #pragma unroll
-    for (int k = 0; k < kPassBatch; ++k) {
+    for (int k = 0; k < kPassTail; ++k) {
       if (c + k < c1) {
-        if (act) en[(c + k) * PN] = S;
+        if (act) en[(uint32_t)(c + k) * pn + e0] = S;
         S = __builtin_fmaf(aa[k], S, xa[k]);
       }
     }
@@ -407,15 +444,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Wave-private LDS tiles, rows padded so that every access of a lane is one
 // base register plus a constant offset and the 16-row operand reads spread
-// over the banks (units of 8 bytes: bank pair 9 p + unit for x^T, 17 t + unit
+// over the banks (units of 8 bytes: bank pair 9 p + unit for x^T, 18 t + unit
 // for y, 10-dword rows for B):
 //   x^T [p][s]  64 rows x 32 steps bf16, 72-byte rows
-//   y   [t][p]  32 rows x 64 channels bf16, 136-byte rows (in the x^T space)
+//   y   [t][p]  32 rows x 64 channels bf16, 144-byte rows (in the x^T space)
 //   B   [s][n]  32 rows x 16 states bf16, 40-byte rows
 constexpr int kWxRow = 36;   // bf16 elements per x^T row
-constexpr int kWyRow = 68;   // per y row
+constexpr int kWyRow = 72;   // per y row (16-byte aligned rows)
 constexpr int kWbRow = 20;   // per B row
-constexpr int kWxElems = kMp * kWxRow;  // 2304 (>= 32 * kWyRow = 2176)
+constexpr int kWxElems = kMp * kWxRow;  // 2304 (= 32 * kWyRow)
 
 __device__ inline s16x4_t pk_s16x4(f32x4 v) {
   return __builtin_bit_cast(s16x4_t, make_uint2(pk_bf16(v[0], v[1]), pk_bf16(v[2], v[3])));
@@ -634,15 +671,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
   const __amdgpu_buffer_rsrc_t ry = wave_rsrc(yb, ((nrow - 1) * a.sy_l + kMp) * 2);
   const int32_t bC = (int32_t)(a.sC_l * 2), by = (int32_t)(a.sy_l * 2);
   const uint32_t oC = (uint32_t)(c16 * bC + 8 * q);
-  const uint32_t oy = (uint32_t)(q * by + 8 * c16);
+  const uint32_t oy = (uint32_t)((lane >> 3) * by + 16 * (lane & 7));
   u32x4 xr[4];
   u32x2 bq[2], cq[2];
   float dtv;
+  // C through the caches: the 4 waves of a workgroup share its 128-byte lines
+  // (a streaming hint let them be evicted between the waves' reads: 20% more
+  // bytes fetched)
   auto load_sub = [&](int r0) {  // r0: first row of the sub-chunk, from the tile start
     wt.load(r0, xr, bq, dtv);
 #pragma unroll
     for (int sg = 0; sg < 2; ++sg)
-      cq[sg] = __builtin_amdgcn_raw_buffer_load_b64(rC, (int)oC, (r0 + 16 * sg) * bC, kBufNt);
+      cq[sg] = __builtin_amdgcn_raw_buffer_load_b64(rC, (int)oC, (r0 + 16 * sg) * bC, 0);
   };
   load_sub(0);
 
@@ -747,23 +787,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
     }
     wave_state_update(st, xa, bs, sw, c16, q, exp2_fast(cumE));
 
-    // the staged 32 x 64 outputs leave as whole 128-byte rows (16 lanes a row)
+    // the staged 32 x 64 outputs leave as whole 128-byte rows (8 lanes a row)
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int tr = q + 4 * i;
-      const u32x2 v = *reinterpret_cast<const u32x2*>(xt + tr * kWyRow + 4 * c16);
-      __builtin_amdgcn_raw_buffer_store_b64(v, ry, (int)oy, (r0 + 4 * i) * by, kBufNt);
+    for (int i = 0; i < 4; ++i) {
+      const int tr = (lane >> 3) + 8 * i;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(xt + tr * kWyRow + 8 * (lane & 7));
+      __builtin_amdgcn_raw_buffer_store_b128(v, ry, (int)oy, (r0 + 8 * i) * by, kBufNt);
     }
   }
 }
 
 // The tile passes read rows past L as zero through the buffer range check:
 // every row stride must cover one row of the operand, and a tile's 256 rows
-// of every operand must span less than 2^31 bytes.
+// of every operand must span less than 2^31 bytes.  Outputs leave as 16-byte
+// pieces (y rows 16-byte aligned).
 inline bool ssd_wave_ok(const SsdArgs& a) {
   const int64_t lim = (int64_t)1 << 31;
-  return a.sx_l >= kMp && a.sB_l >= kMn && a.sC_l >= kMn && a.sy_l >= kMp && a.sdt_l >= 1 &&
+  return aligned(a.y, 16) && a.sy_l % 8 == 0 && a.sy_h % 8 == 0 && a.sy_b % 8 == 0 &&
+         a.sx_l >= kMp && a.sB_l >= kMn && a.sC_l >= kMn && a.sy_l >= kMp && a.sdt_l >= 1 &&
          (kMq * a.sx_l + kMp) * 2 < lim && (kMq * a.sB_l + kMn) * 2 < lim &&
          (kMq * a.sC_l + kMn) * 2 < lim && (kMq * a.sy_l + kMp) * 2 < lim &&
          (kMq * a.sdt_l + 1) * 4 < lim;
@@ -1275,7 +1317,8 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
   const int64_t nchunks = cdiv64(L, tc);
   const int64_t rows = nbatch * H;
   const int64_t PN = P * N;
-  TSSM_CHECK(nchunks * rows < (int64_t)INT32_MAX, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nchunks * rows < (int64_t)INT32_MAX && nchunks * PN < (int64_t)INT32_MAX,
+             TSSM_ERR_UNSUPPORTED);
   SsdArgs a;
   a.x = x; a.dt = dt; a.A_log = A_log; a.B = B; a.C = C; a.D = D; a.h0 = h0; a.y = y;
   a.h_last = h_last; a.L = L;
