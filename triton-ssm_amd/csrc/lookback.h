@@ -73,9 +73,14 @@ struct CarrySlot {
 // j-WIN+1 are loaded together, then folded newest first -- an inclusive word
 // ends the walk, an aggregate pair is folded in, a missing word stops the
 // batch and is re-polled (bounded).  ``h0`` is the state before chunk 0.
+// ``cha`` is the channel whose word holds the decay aggregate: ``ch`` itself,
+// or the first channel of the head when the channels of a head share one
+// decay (one word per head is then published and read).  A tile whose decay
+// product is exactly zero may publish its inclusive word only.
 template <int WIN>
-__device__ inline float lookback_channel(const CarrySlot& s, int64_t c, int ch, uint32_t tag,
-                                         float h0, uint32_t spin_limit, WsHeader* hdr) {
+__device__ inline float lookback_channel(const CarrySlot& s, int64_t c, int ch, int cha,
+                                         uint32_t tag, float h0, uint32_t spin_limit,
+                                         WsHeader* hdr) {
   float A_acc = 1.0f, X_acc = 0.0f;
   int64_t j = c - 1;
   uint32_t spins = 0;
@@ -85,7 +90,7 @@ __device__ inline float lookback_channel(const CarrySlot& s, int64_t c, int ch, 
     for (int k = 0; k < WIN; ++k) {
       if (j - k >= 0) {
         wi[k] = ld_word(s.inc(j - k, ch));
-        wa[k] = ld_word(s.agg_a(j - k, ch));
+        wa[k] = ld_word(s.agg_a(j - k, cha));
         wx[k] = ld_word(s.agg_x(j - k, ch));
       } else {
         wi[k] = wa[k] = wx[k] = 0;

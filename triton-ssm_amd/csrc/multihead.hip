@@ -520,20 +520,26 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
       const float TA = A * SA;
       const float TX = __builtin_fmaf(A, SX, X);
       CarrySlot slot{a.words + (int64_t)row * a.nchunks * 3 * P, 3 * P, P};
-      if (c > 0) {
-        st_word(slot.agg_a(c, ch), TA, tag);
-        st_word(slot.agg_x(c, ch), TX, tag);
-      }
+      // With one decay per head its channels' tile decays are bit-identical
+      // (the same products in the same order): the head's first channel
+      // carries it in one word, written once and read by every channel.
+      const int cha = APH ? ch - ch % (8 * NS) : ch;
       // A tile whose decay product underflowed to exactly zero forgets its
       // entry state: its inclusive state is TX whatever the carry, so it is
-      // published before the look-back and later tiles need not wait on it.
+      // published before the look-back, alone (no walker needs its aggregate),
+      // and later tiles need not wait on it.
       const bool forgets = TA == 0.0f;
-      if (forgets) st_word(slot.inc(c, ch), TX, tag);
+      if (forgets) {
+        st_word(slot.inc(c, ch), TX, tag);
+      } else if (c > 0) {
+        if (ch == cha) st_word(slot.agg_a(c, ch), TA, tag);
+        st_word(slot.agg_x(c, ch), TX, tag);
+      }
       const float hin = a.h0 ? a.h0[row * P + ch] : 0.0f;
       // per-channel walk: measured faster here than the status-word walk
       // (lookback_wave), which costs a second round trip per step
       const float carry =
-          (c > 0) ? lookback_channel<WIN>(slot, c, ch, tag, hin, a.spin_limit, a.hdr) : hin;
+          (c > 0) ? lookback_channel<WIN>(slot, c, ch, cha, tag, hin, a.spin_limit, a.hdr) : hin;
       const float incl = __builtin_fmaf(TA, carry, TX);
       if (!forgets) st_word(slot.inc(c, ch), incl, tag);
       if (a.h_last && c == a.nchunks - 1) a.h_last[row * P + ch] = incl;
