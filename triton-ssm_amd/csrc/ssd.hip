@@ -371,7 +371,7 @@ __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
 // bf16 inputs on the matrix cores: shared types, sizes and conversions.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kMq = 256;           // steps per tile (granularity of the state passing)
+constexpr int kMq = 256;           // steps per tile (the chunk the caller names)
 constexpr int kMp = 64, kMn = 16;  // head dim, state size of the tile passes
 
 __device__ inline bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -497,8 +497,8 @@ struct WaveTile {
     if (c >= a.nchunks || row >= a.rows) return false;
     b = row / a.H;
     h = row - b * a.H;
-    tbeg = (int64_t)c * kMq;
-    const int64_t nrow = (tbeg + kMq < a.L ? tbeg + kMq : a.L) - tbeg;
+    tbeg = (int64_t)c * a.tc;
+    const int64_t nrow = (tbeg + a.tc < a.L ? tbeg + a.tc : a.L) - tbeg;
     nsub = (int)((nrow + kWsub - 1) / kWsub);
     const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h;
     const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
   float* sw = s_sc[wv][2];
   uint16_t* xrow = s_xr[HAS_D ? wv : 0];
   const float a2 = -expf(a.A_log[wt.h]) * kLog2e;
-  const int64_t nrow = (wt.tbeg + kMq < a.L ? wt.tbeg + kMq : a.L) - wt.tbeg;
+  const int64_t nrow = (wt.tbeg + a.tc < a.L ? wt.tbeg + a.tc : a.L) - wt.tbeg;
   const uint16_t* Cb =
       reinterpret_cast<const uint16_t*>(a.C) + wt.b * a.sC_b + wt.h * a.sC_h + wt.tbeg * a.sC_l;
   uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + wt.b * a.sy_b + wt.h * a.sy_h + wt.tbeg * a.sy_l;
@@ -798,19 +798,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
   }
 }
 
-// The tile passes read rows past L as zero through the buffer range check:
-// every row stride must cover one row of the operand, and a tile's 256 rows
-// of every operand must span less than 2^31 bytes.  Outputs leave as 16-byte
-// pieces (y rows 16-byte aligned).
-inline bool ssd_wave_ok(const SsdArgs& a) {
-  const int64_t lim = (int64_t)1 << 31;
-  return aligned(a.y, 16) && a.sy_l % 8 == 0 && a.sy_h % 8 == 0 && a.sy_b % 8 == 0 &&
-         a.sx_l >= kMp && a.sB_l >= kMn && a.sC_l >= kMn && a.sy_l >= kMp && a.sdt_l >= 1 &&
-         (kMq * a.sx_l + kMp) * 2 < lim && (kMq * a.sB_l + kMn) * 2 < lim &&
-         (kMq * a.sC_l + kMn) * 2 < lim && (kMq * a.sy_l + kMp) * 2 < lim &&
-         (kMq * a.sdt_l + 1) * 4 < lim;
+// Tiles per wave of the tile passes: a wave walks ``seg`` consecutive
+// 256-step tiles with the state in registers, so the states are passed
+// between segments of seg tiles only.  Two tiles per wave when that still
+// gives kSegFill waves (4 per SIMD on 256 CUs, one resident generation):
+// half the state traffic of one tile per wave and half the passing.
+constexpr int64_t kSegFill = 4096;
+inline int64_t ssd_wave_seg(int64_t rows, int64_t nchunks) {
+  return rows * ((nchunks + 1) / 2) >= kSegFill ? 2 : 1;
 }
 
+// The tile passes read rows past L as zero through the buffer range check:
+// every row stride must cover one row of the operand, and a segment's rows
+// (seg_steps) of every operand must span less than 2^31 bytes.  Outputs leave
+// as 16-byte pieces (y rows 16-byte aligned).
+inline bool ssd_wave_ok(const SsdArgs& a, int64_t seg_steps) {
+  const int64_t lim = (int64_t)1 << 31, q = seg_steps;
+  return aligned(a.y, 16) && a.sy_l % 8 == 0 && a.sy_h % 8 == 0 && a.sy_b % 8 == 0 &&
+         a.sx_l >= kMp && a.sB_l >= kMn && a.sC_l >= kMn && a.sy_l >= kMp && a.sdt_l >= 1 &&
+         (q * a.sx_l + kMp) * 2 < lim && (q * a.sB_l + kMn) * 2 < lim &&
+         (q * a.sC_l + kMn) * 2 < lim && (q * a.sy_l + kMp) * 2 < lim &&
+         (q * a.sdt_l + 1) * 4 < lim;
+}
+
+// ``a.tc`` and ``a.nchunks`` are the segment length and count here; the
+// workspace laid out for 256-step chunks holds the fewer segments.
 template <int DISC>
 int launch_ssd_mfma(bool has_d, int64_t rows, int64_t nchunks, int64_t PN, hipStream_t s,
                     const SsdArgs& a) {
@@ -1337,14 +1349,18 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
   const bool has_d = D != nullptr;
   // bf16 at P = 64, N = 16 with 256-step tiles: matrix-core passes (other
   // row strides take the generic passes)
-  if (dtype == TSSM_BF16 && P == kMp && N == kMn && tc == kMq && ssd_wave_ok(a)) {
+  const int64_t wseg = ssd_wave_seg(rows, nchunks);
+  if (dtype == TSSM_BF16 && P == kMp && N == kMn && tc == kMq && ssd_wave_ok(a, wseg * kMq)) {
     TSSM_CHECK(aligned(x, 16) && aligned(B, 16) && aligned(C, 16) && aligned(y, 8), TSSM_ERR_ALIGN);
     TSSM_CHECK(sx_l % 8 == 0 && sx_h % 8 == 0 && sx_b % 8 == 0 && sB_l % 8 == 0 && sB_b % 8 == 0 &&
                    sB_h % 8 == 0 && sC_l % 8 == 0 && sC_b % 8 == 0 && sC_h % 8 == 0 &&
                    sy_l % 4 == 0 && sy_b % 4 == 0 && sy_h % 4 == 0,
                TSSM_ERR_ALIGN);
-    return disc == TSSM_DISC_ZOH ? launch_ssd_mfma<TSSM_DISC_ZOH>(has_d, rows, nchunks, PN, s, a)
-                                 : launch_ssd_mfma<TSSM_DISC_EULER>(has_d, rows, nchunks, PN, s, a);
+    const int64_t nseg = cdiv64(nchunks, wseg);
+    a.tc = (uint32_t)(wseg * kMq);
+    a.nchunks = (uint32_t)nseg;
+    return disc == TSSM_DISC_ZOH ? launch_ssd_mfma<TSSM_DISC_ZOH>(has_d, rows, nseg, PN, s, a)
+                                 : launch_ssd_mfma<TSSM_DISC_EULER>(has_d, rows, nseg, PN, s, a);
   }
   // bf16 at N = 64 with 16-channel blocks: one matrix-core pass per channel block
   if (dtype == TSSM_BF16 && N == kSqN && P % kSqP == 0 && aligned(x, 16) && aligned(B, 16) &&
