@@ -331,6 +331,7 @@ def wl_ssd_long(args, dev):
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
                 kernel="ssd_state_wave_kernel + ssd_pass_kernel + ssd_out_wave_kernel",
+                traffic="ssd_long_traffic.json",
                 dtype="bf16",
                 metric="SSD long-sequence scan elements/sec, B=1 L=262144 H=8 P=64 N=16 bf16",
                 unit="elements/s",
