@@ -181,6 +181,27 @@ def test_ssd_long_sequence_shape(dev):
     tssm.check(dev)
 
 
+@pytest.mark.parametrize("L", [65499, 204700])
+def test_ssd_scan_multi_tile_segments(dev, L):
+    """bf16 P=64 N=16 with 16 rows: the matrix-core passes walk one
+    (L=65499) or two (L=204700) consecutive 256-step tiles per wave and pass
+    the states between those segments; ragged last tile (an odd number of
+    32-step sub-chunks), skip term and h0.  Two heads of the second batch are
+    compared with the float64 oracle over every step."""
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, 2, L, 8, 64, 16, torch.bfloat16, seed=L % 1000, heavy=True)
+    h0 = torch.randn(2, 8, 64, 16, device=dev)
+    y, hl = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], disc="zoh",
+                             h0=h0, chunk=256, return_state=True)
+    torch.cuda.synchronize()
+    heads = [2, 7]
+    sl = (slice(1, 2), slice(None), heads)
+    y_ref, h_ref = O.ssd_scan(d["x"][sl], d["dt"][sl], d["A_log"][heads], d["B"][sl],
+                              d["C"][sl], d["D"][heads], h0=np64(h0[1:2, heads]), disc="zoh")
+    assert_close(y[sl], y_ref, 4e-3, f"segmented mfma ssd y L={L}")
+    assert_close(hl[1:2, heads], h_ref, 1e-3, "segmented mfma ssd h_last")
+
+
 def test_ssd_then_multihead_on_one_stream(dev):
     """The SSD passes write raw fp32 chunk data into their workspace; a
     look-back scan launched next on the same stream must not read any of it

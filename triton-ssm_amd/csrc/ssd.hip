@@ -1349,7 +1349,8 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
   const bool has_d = D != nullptr;
   // bf16 at P = 64, N = 16 with 256-step tiles: matrix-core passes (other
   // row strides take the generic passes)
-  const int64_t wseg = ssd_wave_seg(rows, nchunks);
+  int64_t wseg = ssd_wave_seg(rows, nchunks);
+  if (wseg > 1 && !ssd_wave_ok(a, wseg * kMq)) wseg = 1;  // row strides too long for a segment
   if (dtype == TSSM_BF16 && P == kMp && N == kMn && tc == kMq && ssd_wave_ok(a, wseg * kMq)) {
     TSSM_CHECK(aligned(x, 16) && aligned(B, 16) && aligned(C, 16) && aligned(y, 8), TSSM_ERR_ALIGN);
     TSSM_CHECK(sx_l % 8 == 0 && sx_h % 8 == 0 && sx_b % 8 == 0 && sB_l % 8 == 0 && sB_b % 8 == 0 &&
