@@ -27,20 +27,30 @@ __global__ __launch_bounds__(256) void stream_step_kernel(
   ld_lanes<T, V>(Abar + k, ab);
   ld_lanes<T, V>(Bbar + k, bb);
   ld_lanes<T, V>(D + k, dv);
+  // every row's loads first, so the thread makes one round trip to memory
+  // instead of one per row (a store's wait would otherwise hold up the next
+  // row's loads).  Rows past nb redo row nb - 1 from the same loaded values and
+  // store the same results there: no branch, so no load sinks back into one.
   const int64_t b0 = (int64_t)blockIdx.x * kStepRows;
-  for (int r = 0; r < kStepRows && b0 + r < nb; ++r) {
-    const int64_t b = b0 + r;
-    float v[V], hv[V], cv[V], yv[V];
-    ld_lanes<T, V>(vhat + b * svb + k, v);
-    ld_lanes<T, V>(h + b * shb + k, hv);
-    ld_lanes<T, V>(C + b * scb + k, cv);
+  float v[kStepRows][V], hv[kStepRows][V], cv[kStepRows][V];
+  int64_t rb[kStepRows];
+#pragma unroll
+  for (int r = 0; r < kStepRows; ++r) {
+    rb[r] = b0 + r < nb ? b0 + r : nb - 1;
+    ld_lanes<T, V>(vhat + rb[r] * svb + k, v[r]);
+    ld_lanes<T, V>(h + rb[r] * shb + k, hv[r]);
+    ld_lanes<T, V>(C + rb[r] * scb + k, cv[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < kStepRows; ++r) {
+    float yv[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      hv[j] = ab[j] * hv[j] + bb[j] * v[j];
-      yv[j] = cv[j] * hv[j] + dv[j] * v[j];
+      hv[r][j] = ab[j] * hv[r][j] + bb[j] * v[r][j];
+      yv[j] = cv[r][j] * hv[r][j] + dv[j] * v[r][j];
     }
-    st_lanes<T, V>(h + b * shb + k, hv);
-    st_lanes<T, V>(y + b * svb + k, yv);
+    st_lanes<T, V>(h + rb[r] * shb + k, hv[r]);
+    st_lanes<T, V>(y + rb[r] * svb + k, yv);
   }
 }
 
