@@ -70,58 +70,65 @@ __device__ inline void sel_update(float (&h)[NST], const float (&a2)[NST], const
 }
 
 // Lane parameters: a log2(e) and -1/a with a = -exp(A_log[d, k]).
+// Lane parameters from the raw A_log values: a log2(e) and -1/a with
+// a = -exp(A_log[d, k]).
 template <int NST>
-__device__ inline void sel_params(const float* __restrict__ A_log, int64_t d, float (&a2)[NST],
-                                  float (&nia)[NST]) {
+__device__ inline void sel_params(const float (&al)[NST], float (&a2)[NST], float (&nia)[NST]) {
+#pragma unroll
+  for (int k = 0; k < NST; ++k) {
+    const float x = al[k] * kLog2e;
+    a2[k] = -__builtin_amdgcn_exp2f(x) * kLog2e;
+    nia[k] = __builtin_amdgcn_exp2f(-x);
+  }
+}
+
+template <int NST>
+__device__ inline void load_alog(const float* __restrict__ A_log, int64_t d, float (&al)[NST]) {
   const float4* ap = reinterpret_cast<const float4*>(A_log + d * NST);
 #pragma unroll
   for (int q = 0; q < NST / 4; ++q) {
     const float4 v = ap[q];
-    const float l[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float x = l[i] * kLog2e;
-      a2[4 * q + i] = -__builtin_amdgcn_exp2f(x) * kLog2e;
-      nia[4 * q + i] = __builtin_amdgcn_exp2f(-x);
-    }
+    al[4 * q] = v.x; al[4 * q + 1] = v.y; al[4 * q + 2] = v.z; al[4 * q + 3] = v.w;
   }
 }
 
 // The chunk's rows [n4][NST] of B (or C) of this batch, staged once per
-// workgroup in LDS as fp32 (4 elements per thread and pass); rows n .. n4-1
-// (the padding to whole groups of kSelPf steps) repeat row n-1.  Every wave
-// then reads a step's row with broadcast LDS reads.
+// workgroup in LDS as fp32: thread i holds elements 4i .. 4i+3 (one pass:
+// kSelChunkSteps * NST <= 4 kSelThreads); rows n .. n4-1 (the padding to
+// whole groups of kSelPf steps) repeat row n-1.  Every wave then reads a
+// step's row with broadcast LDS reads.  Loaded in the prologue with every
+// other prologue load, stored to LDS after their one wait.
 template <typename T, int NST>
-__device__ inline void stage_rows(float* s, const T* __restrict__ base, int64_t sl, int n,
-                                  int n4) {
-  for (int i = (int)threadIdx.x * 4; i < n4 * NST; i += kSelThreads * 4) {
-    const int row = i / NST, col = i - row * NST;
-    const T* p = base + (int64_t)(row < n ? row : n - 1) * sl + col;
-    float4 v;
-    if constexpr (sizeof(T) == 4) {
-      v = *reinterpret_cast<const float4*>(p);
-    } else {
-      const uint2 w = *reinterpret_cast<const uint2*>(p);
-      v = make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
-                      __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
-    }
-    *reinterpret_cast<float4*>(s + i) = v;
+__device__ inline float4 stage_row_load(const T* __restrict__ base, int64_t sl, int n, int n4) {
+  static_assert(kSelChunkSteps * NST <= 4 * kSelThreads, "one staging pass");
+  const int i0 = (int)threadIdx.x * 4;
+  const int i = i0 < n4 * NST ? i0 : 0;  // threads past the rows load row 0 and store nothing
+  const int row = i / NST, col = i - row * NST;
+  const T* p = base + (int64_t)(row < n ? row : n - 1) * sl + col;
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const float4*>(p);
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
   }
 }
+template <int NST>
+__device__ inline void stage_row_store(float* s, float4 v, int n4) {
+  const int i = (int)threadIdx.x * 4;
+  if (i < n4 * NST) *reinterpret_cast<float4*>(s + i) = v;
+}
 
-// dt shared by the channels: the chunk's values [n4] in LDS, formed once per
-// workgroup (with timestamps the differences, dt_0 = tau_0); padded steps 0.
+// dt shared by the channels: the chunk's values [n4] (n4 <= kSelThreads), one
+// per thread (with timestamps the differences, dt_0 = tau_0); padded steps 0.
 template <bool TAU>
-__device__ inline void stage_dt(float* s, const float* __restrict__ row, int64_t sl, int64_t t0,
-                                int n, int n4) {
-  for (int i = (int)threadIdx.x; i < n4; i += kSelThreads) {
-    float v = 0.0f;
-    if (i < n) {
-      v = row[(t0 + i) * sl];
-      if constexpr (TAU) v -= (t0 + i > 0) ? row[(t0 + i - 1) * sl] : 0.0f;
-    }
-    s[i] = v;
-  }
+__device__ inline float stage_dt_load(const float* __restrict__ row, int64_t sl, int64_t t0,
+                                      int n) {
+  const int i = (int)threadIdx.x;
+  const int64_t tt = t0 + (i < n ? i : n - 1);
+  float v = row[tt * sl];
+  if constexpr (TAU) v -= (tt > 0) ? row[(tt - 1) * sl] : 0.0f;
+  return i < n ? v : 0.0f;
 }
 
 template <int NST>
@@ -134,28 +141,35 @@ __device__ inline void lds_row(const float* s, float (&v)[NST]) {
   }
 }
 
-// One chunk of the recurrence for a lane (channel dc of batch b), in groups
-// of kSelPf steps: x (and a per-channel dt) of step r + kSelPf is fetched
-// right after step r, into the register step r just freed, so no value is
-// copied and each fetch has kSelPf - 1 steps to arrive.
-// Only the prologue's fetches pass through opaque copies (one wait before the
-// loop); otherwise the compiler merges them with the loop's fetches into a
-// load at the top of the group, waited on at once.  Padded steps (r >= n)
-// have dt = 0 -- an identity step -- and repeat step n-1's x and B/C rows,
-// so they reproduce step n-1's output.  `step(r, u, dtv)` gets every step.
-template <typename T, bool DTS, typename F>
-__device__ inline void chunk_steps(const T* __restrict__ xp, int64_t sx_l,
-                                   const float* __restrict__ dtp, int64_t sdt_l,
-                                   const float* s_dt, int64_t t0, int n, int n4, F&& step) {
-  float u[kSelPf], dr[kSelPf];
+// x (and a per-channel dt) of the chunk's first kSelPf steps, issued in the
+// prologue with its other loads.
+template <typename T, bool DTS>
+__device__ inline void chunk_prefetch(const T* __restrict__ xp, int64_t sx_l,
+                                      const float* __restrict__ dtp, int64_t sdt_l, int64_t t0,
+                                      int n, float (&u)[kSelPf], float (&dr)[kSelPf]) {
 #pragma unroll
   for (int j = 0; j < kSelPf; ++j) {
     const int64_t tt = t0 + (j < n ? j : n - 1);
     u[j] = ldf(xp + tt * sx_l);
     dr[j] = DTS ? 0.0f : dtp[tt * sdt_l];
-    asm volatile("" : "+v"(u[j]), "+v"(dr[j]));
   }
-  __syncthreads();  // rows (and shared dt) staged by the caller
+}
+
+// One chunk of the recurrence for a lane (channel dc of batch b), in groups
+// of kSelPf steps: x (and a per-channel dt) of step r + kSelPf is fetched
+// right after step r, into the register step r just freed, so no value is
+// copied and each fetch has kSelPf - 1 steps to arrive.  u/dr hold the
+// prologue's fetches (chunk_prefetch), already waited on: they pass through
+// opaque copies once, with every other prologue load, so the compiler neither
+// merges them with the loop's fetches nor waits on them one by one.  Padded
+// steps (r >= n) have dt = 0 -- an identity step -- and repeat step n-1's x
+// and B/C rows, so they reproduce step n-1's output.  `step(r, u, dtv)` gets
+// every step.
+template <typename T, bool DTS, typename F>
+__device__ inline void chunk_steps(const T* __restrict__ xp, int64_t sx_l,
+                                   const float* __restrict__ dtp, int64_t sdt_l,
+                                   const float* s_dt, int64_t t0, int n, int n4,
+                                   float (&u)[kSelPf], float (&dr)[kSelPf], F&& step) {
   for (int r = 0; r < n4; r += kSelPf) {
 #pragma unroll
     for (int j = 0; j < kSelPf; ++j) {
@@ -187,13 +201,27 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
 
   __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
   __shared__ float sD[DTS ? kSelChunkSteps : 1];
-  stage_rows<T, NST>(sB, Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
-  stage_rows<T, NST>(sC, Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
-  if constexpr (DTS) stage_dt<TAU>(sD, dt + b * m.sdt_b, m.sdt_l, t0, n, n4);
-
-  float a2[NST], nia[NST], h[NST];
-  sel_params<NST>(A_log, dc, a2, nia);
+  // every prologue load first (rows to stage, lane parameters, the first x
+  // fetches), then one wait: each load would otherwise be a round trip of its own
+  const float* dtb = dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d);
+  const float4 vB = stage_row_load<T, NST>(Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
+  const float4 vC = stage_row_load<T, NST>(Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
+  float vdt = 0.0f;
+  if constexpr (DTS) vdt = stage_dt_load<TAU>(dt + b * m.sdt_b, m.sdt_l, t0, n);
+  float al[NST];
+  load_alog<NST>(A_log, dc, al);
   float Dd = HAS_D ? D[dc] : 0.0f;
+  float u[kSelPf], dr[kSelPf];
+  chunk_prefetch<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dtb, m.sdt_l, t0, n, u, dr);
+#pragma unroll
+  for (int j = 0; j < kSelPf; ++j) asm volatile("" : "+v"(u[j]), "+v"(dr[j]));
+  stage_row_store<NST>(sB, vB, n4);
+  stage_row_store<NST>(sC, vC, n4);
+  if constexpr (DTS) {
+    if ((int)threadIdx.x < n4) sD[threadIdx.x] = vdt;
+  }
+  float a2[NST], nia[NST], h[NST];
+  sel_params<NST>(al, a2, nia);
 #pragma unroll
   for (int k = 0; k < NST; ++k) {
     h[k] = 0.0f;
@@ -201,10 +229,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
   }
   asm volatile("" : "+v"(Dd));
   T* yp = y + b * m.sy_b + dc;
+  __syncthreads();  // rows (and shared dt) staged
 
   float sdt = 0.0f;
-  chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d),
-                      m.sdt_l, sD, t0, n, n4, [&](int rr, float u, float dtv) {
+  chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dtb, m.sdt_l, sD, t0, n, n4, u, dr,
+                      [&](int rr, float u, float dtv) {
                         float Bv[NST], Cv[NST];
                         lds_row<NST>(sB + rr * NST, Bv);
                         lds_row<NST>(sC + rr * NST, Cv);
@@ -248,12 +277,19 @@ __global__ __launch_bounds__(kSelCarryThreads) void sel_carry_kernel(
   const int64_t rem = (int64_t)blockIdx.x * kSelCarryThreads + threadIdx.x;
   if (rem >= per_b) return;  // no barrier in this kernel
   const int64_t d = rem / NST;
-  const float a2 = -__builtin_amdgcn_exp2f(A_log[rem] * kLog2e) * kLog2e;
   const int64_t idx = b * per_b + rem;
-  float st = h0 ? h0[idx] : 0.0f;
   float* sp = S + b * m.nch * per_b + rem;
   const float* tp = Tsum + b * m.nch * (DTS ? 1 : m.Dc) + (DTS ? 0 : d);
   const int64_t ts = DTS ? 1 : m.Dc;
+  // the lane's decay and initial state load behind the first batch of chunk
+  // states, so that batch and they share one round trip to memory
+  float a2 = 0.0f, st = 0.0f;
+  bool params = false;
+  auto load_params = [&]() {
+    a2 = -__builtin_amdgcn_exp2f(A_log[rem] * kLog2e) * kLog2e;
+    st = h0 ? h0[idx] : 0.0f;
+    params = true;
+  };
   // all loads of a batch of chunks are issued before the first use
   int64_t c0 = 0;
   for (; c0 + kSelCarryBatch <= m.nch; c0 += kSelCarryBatch) {
@@ -263,12 +299,14 @@ __global__ __launch_bounds__(kSelCarryThreads) void sel_carry_kernel(
       X[i] = sp[(c0 + i) * per_b];
       Tv[i] = tp[(c0 + i) * ts];
     }
+    if (!params) load_params();
 #pragma unroll
     for (int i = 0; i < kSelCarryBatch; ++i) {
       sp[(c0 + i) * per_b] = st;  // entry state of chunk c0 + i
       st = __builtin_fmaf(__builtin_amdgcn_exp2f(a2 * Tv[i]), st, X[i]);
     }
   }
+  if (!params) load_params();
   for (; c0 < m.nch; ++c0) {
     const float X = sp[c0 * per_b], Tv = tp[c0 * ts];
     sp[c0 * per_b] = st;
@@ -297,11 +335,14 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
 
   __shared__ float sC[kSelChunkSteps * NST];
   __shared__ float sD[DTS ? kSelChunkSteps : 1];
-  stage_rows<T, NST>(sC, Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
-  if constexpr (DTS) stage_dt<TAU>(sD, dt + b * m.sdt_b, m.sdt_l, t0, n, n4);
-
-  float a2[NST], nia[NST], h[NST];
-  sel_params<NST>(A_log, dc, a2, nia);
+  // every prologue load first, then one wait (as in pass 1)
+  const float* dtb = dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d);
+  T* yp = y + b * m.sy_b + dc;
+  const float4 vC = stage_row_load<T, NST>(Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
+  float vdt = 0.0f;
+  if constexpr (DTS) vdt = stage_dt_load<TAU>(dt + b * m.sdt_b, m.sdt_l, t0, n);
+  float al[NST], h[NST];
+  load_alog<NST>(A_log, dc, al);
   {
     const float4* sp = reinterpret_cast<const float4*>(S + ((b * m.nch + c) * m.Dc + dc) * NST);
 #pragma unroll
@@ -310,13 +351,23 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
       h[4 * q] = v.x; h[4 * q + 1] = v.y; h[4 * q + 2] = v.z; h[4 * q + 3] = v.w;
     }
   }
+  float u[kSelPf], dr[kSelPf];
+  chunk_prefetch<T, DTS>(yp, m.sy_l, dtb, m.sdt_l, t0, n, u, dr);
+#pragma unroll
+  for (int j = 0; j < kSelPf; ++j) asm volatile("" : "+v"(u[j]), "+v"(dr[j]));
+  stage_row_store<NST>(sC, vC, n4);
+  if constexpr (DTS) {
+    if ((int)threadIdx.x < n4) sD[threadIdx.x] = vdt;
+  }
+  float a2[NST], nia[NST];
+  sel_params<NST>(al, a2, nia);
 #pragma unroll
   for (int k = 0; k < NST; ++k) asm volatile("" : "+v"(h[k]), "+v"(a2[k]));  // before the loop
-  T* yp = y + b * m.sy_b + dc;
+  __syncthreads();  // rows (and shared dt) staged
 
   float cum = 0.0f;
-  chunk_steps<T, DTS>(yp, m.sy_l, dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d), m.sdt_l, sD, t0,
-                      n, n4, [&](int rr, float y1, float dtv) {
+  chunk_steps<T, DTS>(yp, m.sy_l, dtb, m.sdt_l, sD, t0, n, n4, u, dr,
+                      [&](int rr, float y1, float dtv) {
                         float Cv[NST];
                         lds_row<NST>(sC + rr * NST, Cv);
                         cum += dtv;
