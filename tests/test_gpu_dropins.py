@@ -58,7 +58,8 @@ def test_zoh_discretize_partial_grid(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(3, 50, 200, 64), (2, 70, 300, 128), (1, 3, 5, 4)])
+@pytest.mark.parametrize("shape", [(3, 50, 200, 64), (2, 70, 300, 128), (1, 3, 5, 4),
+                                   (5, 2, 40, 64), (7, 3, 64, 64)])   # rows wrap inside a batch of 4
 def test_zoh_discretize_bwd(dev, dtype, shape):
     """zoh_discretize_bwd_kernel[grid](...) against the float64 oracle (itself
     pinned by torch.autograd): dA accumulates into its input, ddt is the full
