@@ -272,10 +272,11 @@ def test_ssd_stream_step_config_size(dev):
 
 @pytest.mark.parametrize("N", [16, 128])
 @pytest.mark.parametrize("per_stream_dt", [True, False])
-def test_ssd_stream_step(dev, N, per_stream_dt):
+@pytest.mark.parametrize("P", [64, 40])   # 40: a batch of row passes runs past P
+def test_ssd_stream_step(dev, N, per_stream_dt, P):
     from tssm import ssd_stream_step
-    g = torch.Generator().manual_seed(N)
-    S, H, P = 37, 4, 64
+    g = torch.Generator().manual_seed(N + P)
+    S, H = 37, 4
     A_log = (torch.rand(H, generator=g) * np.log(16.0)).to(dev)
     D = torch.randn(H, P, generator=g).to(dev)
     state = torch.zeros(S, H, P, N, device=dev)

@@ -326,6 +326,8 @@ struct StreamArgs {
   int64_t sx_s, sx_h, sB_s, sB_h, sC_s, sC_h, sy_s, sy_h;
 };
 
+constexpr int kStreamPB = 8;  // passes whose loads are in flight together
+
 template <int DISC, bool HAS_D, int NG>
 __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
   // NG = threads per state row (N / 4); rows per pass = 256 / NG
@@ -342,27 +344,38 @@ __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
   const float4 bq = *reinterpret_cast<const float4*>(a.B + s * a.sB_s + h * a.sB_h + ng * 4);
   const float4 cq = *reinterpret_cast<const float4*>(a.C + s * a.sC_s + h * a.sC_h + ng * 4);
   float* st = a.state + ((s * a.H + h) * a.P) * a.N;
-  for (int64_t p0 = 0; p0 < a.P; p0 += RPP) {
-    const int64_t p = p0 + rp;
-    float acc = 0.0f;
-    float xv = 0.0f;
-    if (p < a.P) {
-      xv = a.x[s * a.sx_s + h * a.sx_h + p];
-      const float xs = cf * xv;
-      f32x4* sp = reinterpret_cast<f32x4*>(st + p * a.N + ng * 4);
-      f32x4 v = __builtin_nontemporal_load(sp);
-      v.x = __builtin_fmaf(ab, v.x, xs * bq.x);
-      v.y = __builtin_fmaf(ab, v.y, xs * bq.y);
-      v.z = __builtin_fmaf(ab, v.z, xs * bq.z);
-      v.w = __builtin_fmaf(ab, v.w, xs * bq.w);
-      __builtin_nontemporal_store(v, sp);
-      acc = cq.x * v.x + cq.y * v.y + cq.z * v.z + cq.w * v.w;
+  // kStreamPB passes of RPP rows per batch: every load of a batch (x and the
+  // state rows) is issued before the first update, so a workgroup makes one
+  // round trip per batch instead of one per pass.  Rows past P re-read row
+  // P-1 and store nothing.
+  const float* xr = a.x + s * a.sx_s + h * a.sx_h;
+  for (int64_t p0 = 0; p0 < a.P; p0 += RPP * kStreamPB) {
+    f32x4 v[kStreamPB];
+    float xv[kStreamPB];
+#pragma unroll
+    for (int u = 0; u < kStreamPB; ++u) {
+      const int64_t p = p0 + u * RPP + rp;
+      const int64_t pc = p < a.P ? p : a.P - 1;
+      xv[u] = xr[pc];
+      v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(st + pc * a.N + ng * 4));
     }
-    // sum over the NG threads of the row (aligned lane groups)
-    for (int o = NG / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-    if (ng == 0 && p < a.P) {
-      if (HAS_D) acc = __builtin_fmaf(a.D[h * a.P + p], xv, acc);
-      a.y[s * a.sy_s + h * a.sy_h + p] = acc;
+#pragma unroll
+    for (int u = 0; u < kStreamPB; ++u) {
+      const int64_t p = p0 + u * RPP + rp;
+      const float xs = cf * xv[u];
+      f32x4 w = v[u];
+      w.x = __builtin_fmaf(ab, w.x, xs * bq.x);
+      w.y = __builtin_fmaf(ab, w.y, xs * bq.y);
+      w.z = __builtin_fmaf(ab, w.z, xs * bq.z);
+      w.w = __builtin_fmaf(ab, w.w, xs * bq.w);
+      if (p < a.P) __builtin_nontemporal_store(w, reinterpret_cast<f32x4*>(st + p * a.N + ng * 4));
+      float acc = cq.x * w.x + cq.y * w.y + cq.z * w.z + cq.w * w.w;
+      // sum over the NG threads of the row (aligned lane groups)
+      for (int o = NG / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+      if (ng == 0 && p < a.P) {
+        if (HAS_D) acc = __builtin_fmaf(a.D[h * a.P + p], xv[u], acc);
+        a.y[s * a.sy_s + h * a.sy_h + p] = acc;
+      }
     }
   }
 }
