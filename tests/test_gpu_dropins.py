@@ -332,10 +332,14 @@ def test_interp_full_size(dev):
     (3, 60, 300, 10, 128, 0.02, torch.bfloat16, torch.bfloat16),   # config-2 tile, K
     (2, 90, 256, 64, 256, 0.01, torch.float32, torch.float16),     # K = 64: 129 rows x 256
     (2, 50, 600, 20, 512, 0.03, torch.float32, torch.float32)])    # tiles over 256 features
-def test_interp_ssm_step(dev, Bsz, T, F, K, FT, p_obs, dtype, mdtype):
+@pytest.mark.parametrize("tdtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_interp_ssm_step(dev, Bsz, T, F, K, FT, p_obs, dtype, mdtype, tdtype):
+    """fused_interp_ssm_step_kernel launched at every t against the oracle's
+    step; timestamps in every dtype (the oracle sees the same rounded values)."""
     import fused_ssm_interp as fs
     V, M, tau = _interp_inputs(Bsz, T, F, dtype, seed=4 + K, p_obs=p_obs, dev=dev)
     M = M.to(mdtype)
+    tau = tau.to(tdtype)
     g = torch.Generator().manual_seed(5)
     Ab = torch.rand(F, generator=g).to(dev)
     Bb = torch.randn(F, generator=g).to(dev)

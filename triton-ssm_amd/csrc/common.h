@@ -61,6 +61,21 @@ template <typename T> __device__ inline void stf(T* p, float v) { Elem<T>::st(p,
 
 // Runtime-typed scalar load, for small side inputs (masks, timestamps) whose
 // dtype the caller chooses freely.  The switch is wave-uniform.
+// ld_any without a branch around the load: two 16-bit loads (the second the
+// upper half of an fp32 element, or the same half again), then the value
+// selected by dtype.  A load inside a dtype branch must complete before the
+// branches join, a round trip of its own; this one waits only where its value
+// is used.  Every access stays inside the element.
+__device__ inline float ld_any_nb(const void* p, int64_t i, int dt) {
+  const int esz = dt == F32 ? 4 : 2;
+  const uint16_t* e = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p) + i * esz);
+  const uint32_t lo = e[0], hi = e[esz == 4 ? 1 : 0];
+  const float f32 = __uint_as_float(lo | (hi << 16));
+  const float b16 = __uint_as_float(lo << 16);
+  const float h16 = (float)__builtin_bit_cast(_Float16, (uint16_t)lo);
+  return dt == F32 ? f32 : (dt == BF16 ? b16 : h16);
+}
+
 __device__ inline float ld_any(const void* p, int64_t i, int dt) {
   switch (dt) {
     case BF16: return ldf(reinterpret_cast<const bf16_t*>(p) + i);

@@ -526,7 +526,10 @@ __device__ inline void step_mask_batch(const TM* M, int64_t row0, int64_t smt, i
   }
 }
 
-template <typename TV>
+// TM: the mask's element type, a template argument so that the mask loads
+// are straight-line code (behind a dtype switch each load would be waited on
+// before the switch's branches join: one round trip per load).
+template <typename TV, typename TM>
 __global__ __launch_bounds__(kInterpThreads) void interp_step_fast_kernel(StepArgs a) {
   extern __shared__ float s_tau[];  // [2K + 1], then the flags
   unsigned char* s_obs = reinterpret_cast<unsigned char*>(s_tau + 2 * a.K + 1);  // [2K + 1]
@@ -541,32 +544,29 @@ __global__ __launch_bounds__(kInterpThreads) void interp_step_fast_kernel(StepAr
 
   float mv[kStepBatch];
   int mi[kStepBatch];
-  switch (a.md) {  // uniform
-    case TSSM_BF16: step_mask_batch(reinterpret_cast<const bf16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, 0, tid, mv, mi); break;
-    case TSSM_F16: step_mask_batch(reinterpret_cast<const f16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, 0, tid, mv, mi); break;
-    default: step_mask_batch(reinterpret_cast<const float*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, 0, tid, mv, mi); break;
-  }
+  const TM* Mt = reinterpret_cast<const TM*>(a.M);
+  step_mask_batch(Mt, mrow, a.smt, f0, t_lo, a.T, nf, total, 0, tid, mv, mi);
   // feature side inputs
   const bool fact = tid < nf;
   const int64_t f = f0 + (fact ? tid : 0);
   const int64_t lin = b * a.s_hib + f;  // h_in reads 0 where b*stride_hib + f >= B*F (:97-98)
   const float hp = lin < a.nb * a.F ? a.h_in[lin] : 0.0f;
   const float abar = a.A_bar[f], bbar = a.B_bar[f];
+  // timestamps of the candidate rows (rows outside [0, T) read a clamped row
+  // and are never a neighbour); branch-free so that the loads stay in flight
+  // with the mask loads
   for (int i = tid; i < nrow; i += kInterpThreads) {
-    const int64_t t = t_lo + i;
+    int64_t t = t_lo + i;
+    t = t < 0 ? 0 : (t < a.T ? t : a.T - 1);
     s_obs[i] = 0;
-    s_tau[i] = (t >= 0 && t < a.T) ? ld_any(a.tau, b * a.stb + t * a.stt, a.td) : 0.0f;
+    s_tau[i] = ld_any_nb(a.tau, b * a.stb + t * a.stt, a.td);
   }
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < kStepBatch; ++j)
     if (mi[j] >= 0 && mv[j] > 0.5f) s_obs[mi[j]] = 1;
   for (int base = kStepBatch * kInterpThreads; base < total; base += kStepBatch * kInterpThreads) {
-    switch (a.md) {
-      case TSSM_BF16: step_mask_batch(reinterpret_cast<const bf16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, base, tid, mv, mi); break;
-      case TSSM_F16: step_mask_batch(reinterpret_cast<const f16_t*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, base, tid, mv, mi); break;
-      default: step_mask_batch(reinterpret_cast<const float*>(a.M), mrow, a.smt, f0, t_lo, a.T, nf, total, base, tid, mv, mi); break;
-    }
+    step_mask_batch(Mt, mrow, a.smt, f0, t_lo, a.T, nf, total, base, tid, mv, mi);
 #pragma unroll
     for (int j = 0; j < kStepBatch; ++j)
       if (mi[j] >= 0 && mv[j] > 0.5f) s_obs[mi[j]] = 1;
@@ -973,11 +973,21 @@ extern "C" int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, con
     const int64_t nb = grid_b - b0 < kMaxGridYZ ? grid_b - b0 : kMaxGridYZ;
     const dim3 grid((unsigned)gf, (unsigned)nb);
     if (fast) {
+#define TSSM_STEP_FAST(TT)                                                                   \
+  switch (m_dtype) {                                                                         \
+    case TSSM_F32: hipLaunchKernelGGL((interp_step_fast_kernel<TT, float>), grid,             \
+                                      dim3(kInterpThreads), lds, s, a); break;               \
+    case TSSM_BF16: hipLaunchKernelGGL((interp_step_fast_kernel<TT, bf16_t>), grid,           \
+                                       dim3(kInterpThreads), lds, s, a); break;              \
+    default: hipLaunchKernelGGL((interp_step_fast_kernel<TT, f16_t>), grid,                   \
+                                dim3(kInterpThreads), lds, s, a); break;                     \
+  }
       switch (v_dtype) {
-        case TSSM_F32: hipLaunchKernelGGL(interp_step_fast_kernel<float>, grid, dim3(kInterpThreads), lds, s, a); break;
-        case TSSM_BF16: hipLaunchKernelGGL(interp_step_fast_kernel<bf16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
-        default: hipLaunchKernelGGL(interp_step_fast_kernel<f16_t>, grid, dim3(kInterpThreads), lds, s, a); break;
+        case TSSM_F32: TSSM_STEP_FAST(float); break;
+        case TSSM_BF16: TSSM_STEP_FAST(bf16_t); break;
+        default: TSSM_STEP_FAST(f16_t); break;
       }
+#undef TSSM_STEP_FAST
     } else {
       switch (v_dtype) {
         case TSSM_F32: hipLaunchKernelGGL(interp_step_kernel<float>, grid, dim3(kInterpThreads), lds, s, a); break;
