@@ -497,7 +497,7 @@ def rows_sweep(args, dev):
                loc_a, loc_x, carry, Cm, Dm, u, y, B, T, nh * hd, nh, hd, *u.stride(),
                *Cm.stride(), BLK_L=BLK, NBLK=nblk, HEAD_DIM=hd))
     del u, Bm, Cm, dtm, loc_a, loc_x, carry, y, w
-    # a12 time-aware interpolation (config 2 shape)
+    # a12 time-aware interpolation at B=16 T=2048 F=256 (the interpolation + Mamba-1 workload shape)
     wi = workloads.interp_mamba1()
     V, M, tau = (wi[k].to(dev) for k in ("V", "M", "tau"))
     Bi, Ti, Fi = V.shape
