@@ -181,13 +181,14 @@ def test_ssd_long_sequence_shape(dev):
     tssm.check(dev)
 
 
-@pytest.mark.parametrize("L", [65499, 204700])
+@pytest.mark.parametrize("L", [65499, 205006])
 def test_ssd_scan_multi_tile_segments(dev, L):
     """bf16 P=64 N=16 with 16 rows: the matrix-core passes walk one
-    (L=65499) or two (L=204700) consecutive 256-step tiles per wave and pass
-    the states between those segments; ragged last tile (an odd number of
-    32-step sub-chunks), skip term and h0.  Two heads of the second batch are
-    compared with the float64 oracle over every step."""
+    (L=65499) or two (L=205006: 801 tiles, so the last segment holds one
+    tile) consecutive 256-step tiles per wave and pass the states between
+    those segments; ragged last tile (an odd number of 32-step sub-chunks),
+    skip term and h0.  Two heads of the second batch are compared with the
+    float64 oracle over every step."""
     from tssm import ssd_scan_forward
     d = _ssd_inputs(dev, 2, L, 8, 64, 16, torch.bfloat16, seed=L % 1000, heavy=True)
     h0 = torch.randn(2, 8, 64, 16, device=dev)
