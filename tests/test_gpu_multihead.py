@@ -249,3 +249,25 @@ def test_launcher_rejects_out_of_bounds(dev):
     small = torch.zeros(10, device=dev)
     with pytest.raises(ValueError):
         mk.multihead_ssm_carry_scan_kernel[(4,)](small, 4, 8)
+
+
+def test_fused_alternating_decays_on_one_workspace(dev):
+    """One stream, one workspace, six launches in a row that alternate between
+    decays that make most tiles forget their entry state (such a tile
+    publishes only its inclusive carry word) and slow decays (every tile
+    publishes its aggregate words and walks back), per head and per channel:
+    every launch must ignore the words the earlier launches left behind.
+    Each result is checked against the float64 oracle."""
+    from tssm import multihead_ssm_forward
+    for i in range(6):
+        per_head = i % 2 == 0
+        d = _inputs(dev, 2, 1500, 4, 64, torch.float32, seed=40 + i, per_head=per_head,
+                    with_d=False)
+        # fast (log a in [2, 2.8]) or slow (log a in [-6, -5]) decay
+        d["A_log"] = d["A_log"] * 0.05 + (2.0 if i % 4 < 2 else -6.0)
+        y, hl = multihead_ssm_forward(d["u"], d["A_log"], d["B"], d["C"], d["dt"], None,
+                                      disc="zoh", return_state=True)
+        torch.cuda.synchronize()
+        y_ref, h_ref = _oracle(d, "zoh")
+        assert_close(y, y_ref, 1e-5, f"launch {i} y")
+        assert_close(hl, h_ref, 1e-5, f"launch {i} h_last")
