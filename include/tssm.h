@@ -56,6 +56,18 @@ const char* tssm_strerror(int status);
  * the word of the current device's tssm_mh_scan_fused_noalloc scratch. */
 int tssm_workspace_error(const void* workspace, int clear, int* error_out);
 
+/* Attach a host-visible flag to a look-back workspace (workspace == NULL: the
+ * current device's no-allocation scratch), so that an expired wait is seen
+ * without synchronising: the kernel that sets the sticky word also stores 1
+ * to *host_flag (a system-scope store on that error path only; nothing is
+ * written there otherwise).  host_flag must be pinned host memory
+ * (hipHostMalloc, or a torch tensor made with pin_memory=True); the caller
+ * polls it (e.g. before its next launch on the workspace) and resets it.
+ * host_flag == NULL detaches.  A set-up call: one synchronous 8-byte copy into
+ * the workspace header.  No reference counterpart (the reference reports no
+ * errors at run time). */
+int tssm_workspace_attach_host_flag(void* workspace, int* host_flag);
+
 /* ------------------------------------------------------------------ ZOH
  * zoh_discretize_diag_kernel / zoh_discretize_diag_bf16_kernel
  * (discretize_kernel.py:16-57 / :61-94).  Grid (B, T, ceil(H/BLOCK_H)):
@@ -170,11 +182,16 @@ int tssm_mh_scan_fused(int dtype, int disc, const void* u, const float* A_log, c
  * arguments, kernel and results as tssm_mh_scan_fused, without the workspace:
  * the look-back words live in a fixed device array of
  * TSSM_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends), whose
- * address is resolved on the first call on each device.  Problems needing
- * more than that (tssm_mh_scan_workspace_bytes() > the maximum) return
- * TSSM_ERR_SCRATCH; `stream` must belong to the current device.  Calls that
- * overlap on one GPU race on the shared array.  Its sticky look-back error
- * word is read with tssm_workspace_error(NULL, ...). */
+ * address is resolved on the first call on each device -- make that first
+ * call outside graph capture.  Each call enqueues two kernels: a one-thread
+ * kernel that advances the scratch's epoch (the tag of the call's look-back
+ * words) on the device, then the scan, which reads it; so a call captured in
+ * a HIP graph takes a fresh tag on every replay, and nothing is cleared with
+ * a memset.  Problems needing more than the array
+ * (tssm_mh_scan_workspace_bytes() > the maximum) return TSSM_ERR_SCRATCH;
+ * `stream` must belong to the current device.  Every call on a GPU shares its
+ * array: calls (or graph replays) that overlap on one GPU race.  Its sticky
+ * look-back error word is read with tssm_workspace_error(NULL, ...). */
 #define TSSM_NOALLOC_SCRATCH_BYTES (16ll << 20)
 int tssm_mh_scan_fused_noalloc(int dtype, int disc, const void* u, const float* A_log,
                                const void* B, const void* C, const float* dt, const float* D,
@@ -190,8 +207,9 @@ int tssm_mh_scan_fused_noalloc(int dtype, int disc, const void* u, const float* 
  * fused_interp_fp16_kernel (fused_interp_kernel.py:10-100 / :104-181 /
  * :187-257).  V, Vhat in v_dtype; M and tau in any float dtype.  Grid
  * (B, T, ceil(F/FTILE)): computes b < grid_b, t < grid_t, tiles < grid_f.
- * K (search window, <= 64) and FTILE (tile of the "any observed" aggregate)
- * are semantic: they change results.  The per-(b, t, tile) "any observed"
+ * K (search window; bounded by the 64 KiB of LDS one workgroup stages the
+ * window's flags in: K <= 32352 here, TSSM_ERR_UNSUPPORTED beyond) and FTILE
+ * (tile of the "any observed" aggregate) are semantic: they change results.  The per-(b, t, tile) "any observed"
  * flags go through a caller workspace of
  * tssm_time_aware_interp_workspace_bytes() bytes (no clearing needed). */
 int64_t tssm_time_aware_interp_workspace_bytes(int64_t T, int64_t F, int64_t K, int64_t FTILE,

@@ -240,6 +240,32 @@ def test_check_reports_a_flag_set_by_the_host(dev):
     tssm.check(dev)
 
 
+def test_host_flag_reports_an_expired_wait_without_a_sync(dev):
+    """A lookback workspace carries the address of a pinned host int that a
+    kernel whose wait expired sets with the sticky word.  The next fused
+    launch on that workspace polls it on the host (no synchronisation) and
+    raises.  The int is set here by a host write, never by a real timeout."""
+    import tssm
+    from tssm import multihead_ssm_forward, workspace
+    d = _ssd_inputs(dev, 1, 256, 2, 64, 16, torch.float32, seed=2)
+    args = (d["x"].view(1, 256, 128), d["A_log"], d["B"].repeat(1, 1, 1, 4),
+            d["C"].repeat(1, 1, 1, 4), d["dt"], None)
+    multihead_ssm_forward(*args, disc="zoh")
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    flag = workspace.host_flag(dev, stream)
+    assert flag is not None and flag.is_pinned()
+    ws = workspace.get(dev, stream, 0)
+    assert ws[8:16].view(torch.int64).item() != 0   # header: flag address attached
+    torch.cuda.synchronize()
+    assert int(flag[0]) == 0                         # healthy launches leave it alone
+    flag[0] = 1                                      # what the error path stores
+    with pytest.raises(tssm.TssmError, match="host flag"):
+        multihead_ssm_forward(*args, disc="zoh")
+    assert int(flag[0]) == 0                         # reported once
+    multihead_ssm_forward(*args, disc="zoh")         # and the workspace goes on
+    tssm.check(dev)                                  # the device word was never set
+
+
 def test_ssd_stream_step_config_size(dev):
     """The streaming workload at its size: 4096 streams, H=32 P=64 N=128, the
     fp32 state [4096,32,64,128] (4 GiB, byte offsets past 2^32) resident and

@@ -181,6 +181,10 @@ def test_fused_full_headline_shape(dev, disc, a_layout, with_d):
     y_ref, _ = O.multihead_forward(d["u"], w["A_log"], d["B"], d["C"], d["dt"], D, disc=disc)
     e = assert_close(y, y_ref, 1e-2, f"headline {disc} {a_layout} D={with_d}")
     print(f"headline {disc} {a_layout} D={with_d} normwise relerr {e:.3e}")
+    # The contract is 1e-2 (bf16 inputs, fp32 state); the kernel's observed
+    # error is ~2e-3 (the bf16 rounding of y).  A regression bar at 5e-3 keeps
+    # an accuracy loss of 2.5x from passing under the contract.
+    assert e <= 5e-3, f"headline {disc} {a_layout} D={with_d}: relerr {e:.3e} above 5e-3"
 
 
 @pytest.mark.parametrize("hd,dtype,BLK,L", [(16, torch.float32, 16, 70),

@@ -198,6 +198,47 @@ def test_multihead_phases_match_fused_and_broadcast():
         assert np.all(yh == yh[..., :1])  # every slot of a head holds the same value
 
 
+def test_multihead_phase_layout_known_answer():
+    """Hand-computed phase intermediates at Bsz=1, nh=2, hd=2, BLK_L=2, L=4
+    (NBLK=2), Euler, dt=1, B=C=1, D=0.  Lane (h, p) has decay 1/k with
+    k = 2, 4, 8, 16 (A_log = log ln k) and input u[t, ch] = 1 + ch + 4t, so
+    every value is a dyadic rational (exp(-ln k) = 1/k up to rounding, hence
+    the 1e-13 bar).  The carry layout is
+    [2, rows, NBLK] with row_flat = b*nh*hd + h*hd + p
+    (multihead_ssm_kernel.py:98-100): a swapped (blk, row) order, a head/lane
+    transposition or an inclusive/exclusive mix-up moves these numbers."""
+    k = np.array([[2.0, 4.0], [8.0, 16.0]])
+    A_log = np.log(np.log(k))
+    u = (1.0 + np.arange(4)[None, :] + 4.0 * np.arange(4)[:, None])[None]    # [1,4,4]
+    B = np.ones((1, 4, 2, 2))
+    C = np.ones((1, 4, 2, 2))
+    dt = np.ones((1, 4, 2))
+    D = np.zeros(4)
+    la, lx, carry = O.multihead_fwd_local(u, A_log, B, C, dt, 2, 2, 2, 2)
+    A = np.array([0.5, 0.25, 0.125, 0.0625])                 # decay of rows 0..3
+    # loc_a: in-chunk cumulative products, chunk 0 = steps 0-1, chunk 1 = steps 2-3
+    np.testing.assert_allclose(la.reshape(4, 4), np.stack([A, A * A, A, A * A]), rtol=1e-13)
+    # loc_x: in-chunk states from zero
+    lx_ref = np.array([[1.0, 2.0, 3.0, 4.0],
+                       [5.5, 6.5, 7.375, 8.25],
+                       [9.0, 10.0, 11.0, 12.0],
+                       [13.5 + 4.0, 16.5, 16.375, 16.75]])
+    np.testing.assert_allclose(lx.reshape(4, 4), lx_ref, rtol=1e-13)
+    # carry[row*NBLK + blk] (a part), carry[rows*NBLK + row*NBLK + blk] (x part)
+    carry_ref = np.array([0.25, 0.25, 1 / 16, 1 / 16, 1 / 64, 1 / 64, 1 / 256, 1 / 256,
+                          5.5, 17.5, 6.5, 16.5, 7.375, 16.375, 8.25, 16.75])
+    np.testing.assert_allclose(carry, carry_ref, rtol=1e-13)
+    # inclusive carry scan over the chunks of each row: block 1 = block 0 o block 1
+    scanned = O.multihead_carry_scan(carry, 4, 2)
+    scanned_ref = np.array([0.25, 1 / 16, 1 / 16, 1 / 256, 1 / 64, 1 / 4096, 1 / 256, 1 / 65536,
+                            5.5, 18.875, 6.5, 16.90625, 7.375, 16.490234375, 8.25, 16.7822265625])
+    np.testing.assert_allclose(scanned, scanned_ref, rtol=1e-13)
+    # readout: y_head = sum_p h, stored to both slots of the head
+    y = O.multihead_output(la, lx, scanned, C, D, u, 2, 2, 2, 2)
+    yh = np.array([[3.0, 7.0], [12.0, 15.625], [23.375, 24.4375], [35.78125, 33.2724609375]])
+    np.testing.assert_allclose(y[0], np.repeat(yh, 2, axis=1), rtol=1e-13)
+
+
 def test_multihead_split_resume():
     d = _mh_inputs(L=20)
     cut = 7

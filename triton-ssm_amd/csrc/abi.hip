@@ -52,3 +52,20 @@ extern "C" int tssm_workspace_error(const void* workspace, int clear, int* error
   }
   return TSSM_OK;
 }
+
+extern "C" int tssm_workspace_attach_host_flag(void* workspace, int* host_flag) {
+  void* hdr = workspace;
+  if (hdr == nullptr) {
+    const int rc = tssm::noalloc_scratch_header(&hdr);
+    if (rc != TSSM_OK) return rc;
+  }
+  uint64_t addr = 0;
+  if (host_flag != nullptr) {
+    void* dev = nullptr;
+    const hipError_t st = hipHostGetDevicePointer(&dev, host_flag, 0);
+    if (st != hipSuccess) return (int)st;
+    addr = (uint64_t)(uintptr_t)dev;
+  }
+  auto* h = reinterpret_cast<tssm::WsHeader*>(hdr);
+  return (int)hipMemcpy(&h->host_flag, &addr, sizeof(addr), hipMemcpyHostToDevice);
+}

@@ -15,11 +15,16 @@
 // regardless (a timeout sets the sticky error word and the kernel finishes).
 //
 // Workspace layout (caller-owned, zero-filled ONCE when allocated):
-//   WsHeader (256 B: sticky error word) | uint64 carry words ...
-// The tag of a launch is an epoch that the library advances on every launch
-// that uses the workspace (``next_epoch``), so stale words never match and no
-// per-launch clearing is needed.  One workspace serves one stream at a time:
-// launches that overlap on the same workspace race.
+//   WsHeader (256 B: sticky error word, device epoch, host flag address)
+//   | uint64 carry words ...
+// The tag of a launch is an epoch that advances on every launch that uses
+// the workspace, so stale words never match and no per-launch clearing is
+// needed.  Workspace launches take it from a host counter (``next_epoch``)
+// as a kernel argument; the no-allocation scratch advances it on the device
+// (a one-thread kernel enqueued before the scan, which reads it from the
+// header), so a launch captured in a HIP graph gets a fresh tag on every
+// replay.  One workspace serves one stream at a time: launches that overlap
+// on the same workspace race.
 #pragma once
 
 #include "common.h"
@@ -27,8 +32,11 @@
 namespace tssm {
 
 struct WsHeader {
-  uint32_t error;   // sticky: set to 1 when a bounded look-back wait expired
-  uint32_t pad[63];
+  uint32_t error;      // sticky: set to 1 when a bounded look-back wait expired
+  uint32_t epoch;      // device-advanced tag (no-allocation scratch only)
+  uint64_t host_flag;  // 0, or the device address of a host-visible int that
+                       // is set to 1 together with `error`
+  uint32_t pad[60];
 };
 static_assert(sizeof(WsHeader) == 256, "header is 256 bytes");
 
@@ -42,6 +50,10 @@ uint32_t next_epoch(const void* workspace);
 // (0 when no no-allocation launch ran there yet); defined in multihead.hip.
 int noalloc_scratch_error(int clear, int* error_out);
 
+// Host: device address of the current device's no-allocation scratch (its
+// WsHeader), resolved on first use; defined in multihead.hip.
+int noalloc_scratch_header(void** ptr);
+
 __device__ inline uint64_t ld_word(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -52,8 +64,21 @@ __device__ inline void st_word(uint64_t* p, float v, uint32_t tag) {
 __device__ inline uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 32); }
 __device__ inline float word_val(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
+// Expired wait: the sticky word, and the host's flag when one is attached
+// (a system-scope store, visible to the host without a synchronisation once
+// it lands; only this error path writes host memory).
 __device__ inline void flag_error(WsHeader* hdr) {
   __hip_atomic_store(&hdr->error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hf =
+      __hip_atomic_load(&hdr->host_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (hf != 0)
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(hf), 1u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Tag of the current launch on a workspace whose epoch the device advances.
+__device__ inline uint32_t load_epoch(const WsHeader* hdr) {
+  return __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Carry words of one tile for one channel: aggregate (a, x) of the tile alone

@@ -59,6 +59,9 @@ struct MhArgs {
   uint64_t* words;
   uint32_t n_heads, nchunks, nrows;
   uint32_t tag;
+  // nonzero: the launch's tag is the header's device-advanced epoch
+  // (no-allocation scratch), not `tag`
+  uint32_t tag_in_ws = 0;
   uint32_t spin_limit;
   uint32_t dt_is_tau;    // dt holds timestamps: dt_t = tau_t - tau_{t-1}, dt_0 = tau_0
   // Every operand's per-lane offset within a tile (steps x row stride +
@@ -124,7 +127,7 @@ __global__ __launch_bounds__(512) void mh_scan_fused_kernel(MhArgs a) {
   // (row, c-1), a smaller index.  Numbering the chunks of all rows in groups
   // (chunk-major, or groups of 4-16 chunks) measured 7-25% slower: the
   // resident tiles then cover a scattered address range.
-  const uint32_t tag = a.tag;
+  const uint32_t tag = a.tag_in_ws ? load_epoch(a.hdr) : a.tag;
   const uint32_t row = blockIdx.x / a.nchunks;
   const uint32_t c = blockIdx.x - row * a.nchunks;
   const uint32_t b = row / a.n_heads;
@@ -954,11 +957,10 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch[kMaxDevices];
-uint32_t g_scratch_epoch[kMaxDevices];
 
-// Device address of the current device's scratch and the tag of its next
-// launch.  `device` is the current device.
-int scratch_for(int device, void** ptr, uint32_t* tag) {
+// Device address of the current device's scratch.  `device` is the current
+// device.
+int scratch_for(int device, void** ptr) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch[device] == nullptr) {
     void* p = nullptr;
@@ -967,14 +969,25 @@ int scratch_for(int device, void** ptr, uint32_t* tag) {
     g_scratch[device] = p;
   }
   *ptr = g_scratch[device];
-  uint32_t& e = g_scratch_epoch[device];
-  if (++e == 0) e = 1;
-  *tag = e;
   return TSSM_OK;
 }
 
+// The scratch's launch tag lives in its header and is advanced on the
+// device, by this one-thread kernel enqueued right before each scan on the
+// same stream: a launch captured in a HIP graph then takes a fresh tag on
+// every replay (a tag fixed at capture time would let a replay read the
+// previous replay's words as its own).  Vector stores only.
+__global__ void advance_epoch_kernel(WsHeader* hdr) {
+  if (threadIdx.x == 0) {
+    uint32_t e = load_epoch(hdr) + 1u;
+    if (e == 0) e = 1;  // 0 is the tag of a zero-filled word
+    __hip_atomic_store(&hdr->epoch, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // Argument checks and launch shared by tssm_mh_scan_fused and its
-// no-allocation variant; `tag` is the epoch of this launch on `workspace`.
+// no-allocation variant; `tag` is the epoch of this launch on `workspace`,
+// or 0 when the kernel takes the header's device-advanced epoch.
 int mh_scan_fused_launch(int dtype, int disc, const void* u, const float* A_log, const void* B,
                          const void* C, const float* dt, const float* D, const float* h0,
                          void* y, float* h_last, int64_t nbatch, int64_t L, int64_t n_heads,
@@ -1009,6 +1022,7 @@ int mh_scan_fused_launch(int dtype, int disc, const void* u, const float* A_log,
   a.nchunks = (uint32_t)nchunks;
   a.nrows = (uint32_t)nrows;
   a.tag = tag;
+  a.tag_in_ws = tag == 0 ? 1u : 0u;
   a.spin_limit = kDefaultSpinLimit;
   a.dt_is_tau = 0;
   a.off32 = tile_offsets_fit(cfg.TC, cfg.hpr, P, dtype == TSSM_F32 ? 4 : 2, su_l, sB_l, sC_l,
@@ -1020,6 +1034,11 @@ int mh_scan_fused_launch(int dtype, int disc, const void* u, const float* A_log,
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr;
   const bool aph = a_per_head != 0;
+  if (a.tag_in_ws) {
+    hipLaunchKernelGGL(advance_epoch_kernel, dim3(1), dim3(64), 0, s, a.hdr);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
   switch (dtype) {
     case TSSM_BF16: return launch_mh_fused_t<bf16_t>(disc, aph, has_d, cfg.G, cfg.NS, grid, block, lds, s, a);
     case TSSM_F16: return launch_mh_fused_t<f16_t>(disc, aph, has_d, cfg.G, cfg.NS, grid, block, lds, s, a);
@@ -1028,6 +1047,14 @@ int mh_scan_fused_launch(int dtype, int disc, const void* u, const float* A_log,
 }
 
 }  // namespace
+
+int noalloc_scratch_header(void** ptr) {
+  int device = 0;
+  const hipError_t st = hipGetDevice(&device);
+  if (st != hipSuccess) return (int)st;
+  TSSM_CHECK(device >= 0 && device < kMaxDevices, TSSM_ERR_UNSUPPORTED);
+  return scratch_for(device, ptr);
+}
 
 int noalloc_scratch_error(int clear, int* error_out) {
   int device = 0;
@@ -1107,12 +1134,12 @@ extern "C" int tssm_mh_scan_fused_noalloc(int dtype, int disc, const void* u, co
   TSSM_CHECK(device == stream_device && device >= 0 && device < kMaxDevices,
              TSSM_ERR_UNSUPPORTED);
   void* ws = nullptr;
-  uint32_t tag = 0;
-  const int rc = scratch_for(device, &ws, &tag);
+  const int rc = scratch_for(device, &ws);
   if (rc != TSSM_OK) return rc;
+  // tag 0: the scan takes the epoch that advance_epoch_kernel sets
   return mh_scan_fused_launch(dtype, disc, u, A_log, B, C, dt, D, h0, y, h_last, nbatch, L,
                               n_heads, head_dim, a_per_head, su_b, su_l, sB_b, sB_l, sB_h, sC_b,
-                              sC_l, sC_h, sdt_b, sdt_l, sdt_h, sy_b, sy_l, cfg, ws, tag, stream);
+                              sC_l, sC_h, sdt_b, sdt_l, sdt_h, sy_b, sy_l, cfg, ws, 0, stream);
 }
 
 extern "C" int tssm_mh_fwd_local(int dtype, const void* u, const float* A_log, const void* B,

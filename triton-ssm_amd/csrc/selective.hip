@@ -230,6 +230,9 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
   asm volatile("" : "+v"(Dd));
   T* yp = y + b * m.sy_b + dc;
   __syncthreads();  // rows (and shared dt) staged
+  // Waves whose lanes are all past Dc have staged their share and are done
+  // (no barrier follows).
+  if ((int64_t)blockIdx.y * kSelThreads + (threadIdx.x & ~63u) >= m.Dc) return;
 
   float sdt = 0.0f;
   chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dtb, m.sdt_l, sD, t0, n, n4, u, dr,
@@ -247,10 +250,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
                           acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
                           acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
                         }
-                        // Unconditional store: lanes past Dc computed channel
-                        // Dc-1 and padded steps step n-1, identical values to
-                        // what those write there, so no branch holds up the
-                        // waits for later fetches.
+                        // Unconditional store: lanes past Dc (in the wave of
+                        // channel Dc-1) computed channel Dc-1 and padded steps
+                        // step n-1, identical values to what those write
+                        // there, so no branch holds up the waits for later
+                        // fetches.
                         const int64_t tw = t0 + (rr < n ? rr : n - 1);
                         stf(yp + tw * m.sy_l, acc0 + acc1);
                       });
@@ -364,6 +368,13 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
 #pragma unroll
   for (int k = 0; k < NST; ++k) asm volatile("" : "+v"(h[k]), "+v"(a2[k]));  // before the loop
   __syncthreads();  // rows (and shared dt) staged
+  // y is updated in place (y += carried share), which is not idempotent: a
+  // wave whose lanes are all past Dc would read y[., Dc-1] at a time of its
+  // own and could add the carried share a second time.  Such waves have
+  // staged their share and leave here (no barrier follows).  Lanes past Dc
+  // in the wave of channel Dc-1 load and store in lockstep with that lane,
+  // so they write exactly its values.
+  if ((int64_t)blockIdx.y * kSelThreads + (threadIdx.x & ~63u) >= m.Dc) return;
 
   float cum = 0.0f;
   chunk_steps<T, DTS>(yp, m.sy_l, dtb, m.sdt_l, sD, t0, n, n4, u, dr,
@@ -379,7 +390,8 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
                           acc1 = __builtin_fmaf(Cv[k + 1] * h[k + 1],
                                                 __builtin_amdgcn_exp2f(a2[k + 1] * cum), acc1);
                         }
-                        // Unconditional (identical values as in pass 1).
+                        // Unconditional: the lanes past Dc that get here
+                        // share the wave of channel Dc-1 and store its value.
                         const int64_t tw = t0 + (rr < n ? rr : n - 1);
                         stf(yp + tw * m.sy_l, acc0 + acc1);
                       });

@@ -18,9 +18,16 @@ more; launches on different streams therefore never share one.
 
 A bounded look-back wait that expires (a predecessor tile that never
 published, ~1 s of polling) sets the sticky flag and the kernel finishes with
-that tile's carry incomplete.  ``check()`` synchronises, reads every lookback
-workspace's flag (and the no-allocation scratch's) and raises ``TssmError``
-if one is set.
+that tile's carry incomplete.  Two ways report it:
+
+* without a synchronisation: every lookback workspace gets a pinned host int
+  attached (``tssm_workspace_attach_host_flag``) that the failing kernel also
+  sets.  ``get()`` -- called by every fused launch before it launches -- reads
+  that int for the buffer it hands out and raises ``TssmError`` if a launch
+  on it has failed since (the int lands when that kernel finishes, so the
+  report comes with the first launch on the workspace after it);
+* ``check()`` synchronises, reads every lookback workspace's flag (and the
+  no-allocation scratch's) and raises ``TssmError`` if one is set.
 """
 from __future__ import annotations
 
@@ -37,10 +44,24 @@ KINDS = (LOOKBACK, SSD)
 
 _lock = threading.Lock()
 _cache: dict[tuple[int, int, str], torch.Tensor] = {}
+# pinned host int per lookback workspace (same key), set by a failing kernel
+_host_flags: dict[tuple[int, int, str], torch.Tensor] = {}
+
+_EXPIRED = ("a bounded look-back wait expired (a predecessor tile never published its "
+            "carry); outputs of fused scans since the last check are invalid: ")
 
 
 def _dev_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _raise_if_flagged(key) -> None:
+    """Host-side poll of a workspace's attached flag (no synchronisation)."""
+    flag = _host_flags.get(key)
+    if flag is not None and int(flag[0]) != 0:
+        flag[0] = 0
+        raise _lib.TssmError(_EXPIRED + f"device {key[0]} stream {key[1]:#x} (reported by the "
+                             "workspace's host flag; the device word stays set for check())")
 
 
 def get(device: torch.device, stream: int, nbytes: int, kind: str = LOOKBACK) -> torch.Tensor:
@@ -48,12 +69,26 @@ def get(device: torch.device, stream: int, nbytes: int, kind: str = LOOKBACK) ->
         raise ValueError(f"unknown workspace kind {kind!r}")
     key = (_dev_index(device), stream, kind)
     with _lock:
+        _raise_if_flagged(key)
         buf = _cache.get(key)
         if buf is None or buf.numel() < nbytes:
             # zero-filled on the current stream, so it is ordered before the scan
             buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
             _cache[key] = buf
+            if kind == LOOKBACK:
+                flag = _host_flags.get(key)
+                if flag is None:
+                    flag = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+                    _host_flags[key] = flag
+                # the header's flag address is written by a synchronous copy,
+                # after the zero fill above
+                _lib.call("tssm_workspace_attach_host_flag", buf.data_ptr(), flag.data_ptr())
         return buf
+
+
+def host_flag(device: torch.device, stream: int) -> torch.Tensor | None:
+    """The pinned int attached to the lookback workspace of (device, stream)."""
+    return _host_flags.get((_dev_index(device), stream, LOOKBACK))
 
 
 def error_flag(buf: torch.Tensor, clear: bool = True) -> int:
@@ -95,12 +130,16 @@ def check(device: torch.device | int | None = None, clear: bool = True) -> None:
             _lib.call("tssm_workspace_error", None, int(clear), ctypes.byref(out))
             if out.value:
                 bad.append(f"device {dev_idx} no-allocation scratch")
+    with _lock:
+        for k, _ in items:
+            flag = _host_flags.get(k)
+            if flag is not None:
+                flag[0] = 0   # reported here, with the device word
     if bad:
-        raise _lib.TssmError(
-            "a bounded look-back wait expired (a predecessor tile never published its carry); "
-            "outputs of fused scans since the last check are invalid: " + ", ".join(bad))
+        raise _lib.TssmError(_EXPIRED + ", ".join(bad))
 
 
 def clear() -> None:
     with _lock:
         _cache.clear()
+        _host_flags.clear()
