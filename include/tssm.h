@@ -337,14 +337,35 @@ int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt, int
                         int64_t sC_l, int64_t sy_b, int64_t sy_l, int64_t chunk, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
-/* tssm_selective_scan with the dt producer fused into the load stage: per
+/* tssm_selective_scan with the dt producer fused into the scan: per
  * (b, t, d), dt = clamp(softplus(sum_k dt_raw[b,t,k] W[k,d] + bias[d]),
  * dt_min, dt_max) -- dt_project_softplus_kernel (discretize_kernel.py:166-213,
  * the scalar block index at :203 taken as its evident intent) feeding the
- * scan, without the [B,L,Dc] dt tensor in between.  dt_raw f32 [B,L,rank]
- * (strides sr_b, sr_l, unit over k), W f32 [rank, Dc] (row stride sw_r, unit
- * over d), bias f32 [Dc]; rank <= 64.  Everything else as tssm_selective_scan
- * (same workspace size). */
+ * scan, without a caller-side [B,L,Dc] dt tensor or a projection launch.
+ * dt_raw f32 [B,L,rank] (strides sr_b, sr_l, unit over k), W f32 [rank, Dc]
+ * (row stride sw_r, unit over d), bias f32 [Dc]; rank <= 64.  Everything else
+ * as tssm_selective_scan.  Large problems (the three-pass scan) form dt on
+ * the matrix cores inside the passes, bit-identical to the projection
+ * kernel's values, when rank, Dc and the row strides are multiples of 4 and
+ * dt_raw, W, bias are 16-byte aligned.  The workspace may be
+ * tssm_selective_scan_workspace_bytes() bytes (pass 3 then produces dt again)
+ * or tssm_selective_scan_dtproj_workspace_bytes() (pass 1 also stores the dt
+ * it produced there and pass 3 reads it back, the faster form). */
+int64_t tssm_selective_scan_dtproj_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc,
+                                                   int64_t N, int64_t chunk);
+
+/* 1 if tssm_selective_scan (W == NULL: dt given, dt_raw its pointer, sdt_d
+ * its channel stride) or tssm_selective_scan_dtproj (W != NULL) takes the
+ * three-pass path for these operands, else 0 (the single-pass look-back
+ * kernel).  The three passes write raw fp32 chunk states (and the produced
+ * dt) into the workspace, not tagged look-back words: a workspace that served
+ * them must be zero-filled before any look-back launch uses it, so callers
+ * keep separate workspaces for the two paths (tssm/workspace.py does).  No
+ * reference counterpart. */
+int tssm_selective_scan_takes_passes(int dtype, int64_t nbatch, int64_t L, int64_t Dc, int64_t N,
+                                     int64_t sdt_d, int dt_is_tau, const float* dt_raw,
+                                     const float* W, const float* bias, int64_t rank,
+                                     int64_t sr_b, int64_t sr_l, int64_t sw_r);
 int tssm_selective_scan_dtproj(int dtype, int disc, const void* x, const float* dt_raw,
                                const float* W, const float* bias, float dt_min, float dt_max,
                                const float* A_log, const void* B, const void* C, const float* D,

@@ -123,3 +123,35 @@ def test_layer_launchers_validate_on_host():
         sk.masked_fill_zero_kernel[(1,)](x, torch.ones(2, 3), x, 2, 3, 8, BLOCK=64)
     with pytest.raises(TypeError):
         sk.mean_pool_logit_kernel[(2,)](x, w, w, w)   # missing arguments
+
+
+def test_selective_scan_path_query():
+    """tssm_selective_scan_takes_passes (host logic only): which problems the
+    three-pass path takes, so the caller can give it a raw-float workspace."""
+    L = _lib.lib()
+    F32, BF16, F16 = _lib.F32, _lib.BF16, _lib.F16
+    A = 1 << 20   # 16-byte aligned stand-in addresses (never dereferenced)
+    # interpolation workload's scan: dt shared (timestamps), 16 x 4 x 64 blocks
+    assert L.tssm_selective_scan_takes_passes(F32, 16, 2048, 256, 16, 0, 1, A, None, None, 0,
+                                              0, 0, 0) == 1
+    # too few blocks of 64 channels x 32 steps, N outside {8, 16}, fp16 I/O
+    assert L.tssm_selective_scan_takes_passes(F32, 2, 256, 16, 16, 0, 0, A, None, None, 0,
+                                              0, 0, 0) == 0
+    assert L.tssm_selective_scan_takes_passes(F32, 16, 2048, 256, 32, 0, 0, A, None, None, 0,
+                                              0, 0, 0) == 0
+    assert L.tssm_selective_scan_takes_passes(F16, 16, 2048, 256, 16, 0, 0, A, None, None, 0,
+                                              0, 0, 0) == 0
+    # per-channel timestamps are not supported by the passes
+    assert L.tssm_selective_scan_takes_passes(BF16, 16, 2048, 256, 16, 1, 1, A, None, None, 0,
+                                              0, 0, 0) == 0
+    # projected dt: 16-byte raw rows of rank 16 take the passes; rank 7 does not
+    assert L.tssm_selective_scan_takes_passes(F32, 16, 2048, 256, 16, 1, 0, A, A, A, 16,
+                                              2048 * 16, 16, 256) == 1
+    assert L.tssm_selective_scan_takes_passes(F32, 16, 2048, 256, 16, 1, 0, A, A, A, 7,
+                                              2048 * 7, 7, 256) == 0
+    assert L.tssm_selective_scan_takes_passes(F32, 16, 2048, 256, 16, 1, 0, A + 4, A, A, 16,
+                                              2048 * 16, 16, 256) == 0   # unaligned raw rows
+    # the dtproj workspace adds the produced-dt table to the passes' workspace
+    base = L.tssm_selective_scan_workspace_bytes(16, 2048, 256, 16, 256)
+    big = L.tssm_selective_scan_dtproj_workspace_bytes(16, 2048, 256, 16, 256)
+    assert big >= base + 16 * 2048 * 256 * 4

@@ -393,6 +393,104 @@ def test_selective_scan_dtproj(dev, dtype, N, Dc, rank, L):
     assert_close(h, h_ref, TOL[dtype], "dtproj h_last")
 
 
+@pytest.mark.parametrize("dtype,N,Dc,rank,L,Bsz", [
+    (torch.float32, 16, 100, 20, 2100, 8),    # rank block of 16 + a partial one; 28 lanes past Dc
+    (torch.bfloat16, 8, 260, 4, 1000, 16),    # second workgroup holds 4 channels; ragged L
+    (torch.float32, 16, 64, 64, 4096, 4),     # four rank blocks
+    (torch.float32, 16, 64, 7, 4096, 4),      # rank 7: raw rows not 16-byte vectors, single pass
+])
+def test_selective_scan_dtproj_three_pass(dev, dtype, N, Dc, rank, L, Bsz):
+    """dt produced on the matrix cores inside passes 1 and 3 of the three-pass
+    scan (problems large enough for it): against the oracle's projection and
+    scan, and against the two-launch path (projection kernel, then the scan
+    over the stored dt), with h0 and the skip term."""
+    import discretize_kernel as dk
+    from tssm import selective_scan_forward
+    g = torch.Generator().manual_seed(rank * 100 + Dc + N)
+    x = torch.randn(Bsz, L, Dc, generator=g).to(dtype)
+    raw = torch.randn(Bsz, L, rank, generator=g)
+    W = torch.randn(rank, Dc, generator=g) * (2.0 / rank ** 0.5)
+    bias = torch.empty(Dc).uniform_(-4.0, -1.0, generator=g)
+    A_log = torch.empty(Dc, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = (torch.randn(Bsz, L, N, generator=g) / N ** 0.5).to(dtype)
+    Cm = (torch.randn(Bsz, L, N, generator=g) / N ** 0.5).to(dtype)
+    D = torch.randn(Dc, generator=g)
+    h0 = torch.randn(Bsz, Dc, N, generator=g)
+    DT_MIN, DT_MAX = 2e-3, 0.25
+    dt_ref = O.dt_project_softplus(raw, W, bias, DT_MIN, DT_MAX)
+    assert (dt_ref == DT_MIN).any() and (dt_ref == DT_MAX).any()   # both clamps hit
+    d = {k: v.to(dev) for k, v in dict(x=x, raw=raw, W=W, bias=bias, A_log=A_log, B=Bm, C=Cm,
+                                        D=D, h0=h0).items()}
+    y, h = selective_scan_forward(d["x"], d["raw"], d["A_log"], d["B"], d["C"], d["D"],
+                                  h0=d["h0"], return_state=True,
+                                  dt_proj=(d["W"], d["bias"], DT_MIN, DT_MAX))
+    dt = torch.empty(Bsz, L, Dc, device=dev)
+    dk.dt_project_softplus_kernel[(Bsz, L, 1)](
+        d["raw"], d["W"], d["bias"], dt, Bsz, L, Dc, rank, *d["raw"].stride(),
+        d["W"].stride(0), d["W"].stride(1), *dt.stride(), DT_MIN=DT_MIN, DT_MAX=DT_MAX,
+        BLOCK_H=triton_pow2(Dc), BLOCK_R=16)
+    y2, h2 = selective_scan_forward(d["x"], dt, d["A_log"], d["B"], d["C"], d["D"], h0=d["h0"],
+                                    return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.selective_scan(x, dt_ref, A_log, Bm, Cm, D, h0=np64(h0))
+    e = assert_close(y, y_ref, TOL[dtype], f"dtproj three-pass y {dtype} N={N} Dc={Dc} R={rank}")
+    assert_close(h, h_ref, TOL[dtype], "dtproj three-pass h_last")
+    assert_close(y, y2, TOL[dtype], "fused vs two-launch y")
+    assert_close(h, h2, 1e-5, "fused vs two-launch h_last")
+    print(f"dtproj three-pass {dtype} N={N} Dc={Dc} R={rank}: relerr {e:.2e}, "
+          f"bitwise equal to the two-launch path: {torch.equal(y, y2)}")
+
+
+def test_selective_scan_dtproj_workspace_forms(dev):
+    """tssm_selective_scan_dtproj through the C ABI with the two workspace
+    sizes: tssm_selective_scan_dtproj_workspace_bytes (pass 1 stores the dt it
+    produced, pass 3 reads it back) and the smaller
+    tssm_selective_scan_workspace_bytes (pass 3 produces dt again).  Both
+    produce the same dt on the matrix cores, so y and h_last agree bit for
+    bit; both against the oracle."""
+    from tssm import _lib
+    Bsz, L, Dc, N, R = 8, 1030, 128, 16, 16
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(Bsz, L, Dc, generator=g)
+    raw = torch.randn(Bsz, L, R, generator=g)
+    W = torch.randn(R, Dc, generator=g) * 0.5
+    bias = torch.empty(Dc).uniform_(-3.0, -1.0, generator=g)
+    A_log = torch.empty(Dc, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = torch.randn(Bsz, L, N, generator=g) / N ** 0.5
+    Cm = torch.randn(Bsz, L, N, generator=g) / N ** 0.5
+    d = {k: v.to(dev) for k, v in dict(x=x, raw=raw, W=W, bias=bias, A_log=A_log, B=Bm,
+                                        C=Cm).items()}
+    lib = _lib.lib()
+    assert lib.tssm_selective_scan_takes_passes(
+        _lib.F32, Bsz, L, Dc, N, 1, 0, d["raw"].data_ptr(), d["W"].data_ptr(),
+        d["bias"].data_ptr(), R, L * R, R, Dc) == 1
+    small = lib.tssm_selective_scan_workspace_bytes(Bsz, L, Dc, N, 256)
+    big = lib.tssm_selective_scan_dtproj_workspace_bytes(Bsz, L, Dc, N, 256)
+    assert big > small > 0
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    outs = []
+    for nbytes in (big, small):
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        y = torch.empty_like(d["x"])
+        h = torch.empty(Bsz, Dc, N, device=dev)
+        _lib.call("tssm_selective_scan_dtproj", _lib.F32, _lib.DISC_ZOH, d["x"].data_ptr(),
+                  d["raw"].data_ptr(), d["W"].data_ptr(), d["bias"].data_ptr(), 1e-3, 0.5,
+                  d["A_log"].data_ptr(), d["B"].data_ptr(), d["C"].data_ptr(), None, None,
+                  y.data_ptr(), h.data_ptr(), Bsz, L, Dc, N, R, L * Dc, Dc, L * R, R, Dc,
+                  L * N, N, L * N, N, L * Dc, Dc, 256, ws.data_ptr(), nbytes, stream)
+        torch.cuda.synchronize()
+        outs.append((y, h))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    dt_ref = O.dt_project_softplus(raw, W, bias, 1e-3, 0.5)
+    y_ref, h_ref = O.selective_scan(x, dt_ref, A_log, Bm, Cm)
+    assert_close(outs[0][0], y_ref, 1e-5, "dtproj y (stored dt table)")
+    assert_close(outs[1][1], h_ref, 1e-5, "dtproj h_last (dt produced again)")
+
+
+def triton_pow2(n):
+    return 1 << (n - 1).bit_length()
+
+
 def test_selective_scan_dtproj_config_shape(dev):
     """B=16 L=2048 D=256 N=16 fp32, rank 16 (the interpolation workload's scan
     shape): the fused projection against the oracle, and against the two-launch

@@ -1284,6 +1284,15 @@ extern "C" int64_t tssm_selective_scan_workspace_bytes(int64_t nbatch, int64_t L
   return cb > 0 ? sel_chunked_offset(lb) + cb : lb;
 }
 
+extern "C" int64_t tssm_selective_scan_dtproj_workspace_bytes(int64_t nbatch, int64_t L,
+                                                              int64_t Dc, int64_t N,
+                                                              int64_t chunk) {
+  const int64_t base = tssm_selective_scan_workspace_bytes(nbatch, L, Dc, N, chunk);
+  if (base < 0) return -1;
+  if (sel_chunked_bytes(nbatch, L, Dc, N) == 0) return base;
+  return sel_chunked_offset(base) + sel_dt_table_bytes(nbatch, L, Dc);
+}
+
 namespace tssm {
 namespace {
 
@@ -1297,6 +1306,18 @@ struct DtProj {
   int64_t sw_r = 0, rank = 0;
   float dt_min = 0.0f, dt_max = 0.0f;
 };
+
+// Whether a selective scan takes the three-pass path: large problems with 8
+// or 16 states, fp32 or bf16 I/O; dt given (timestamps only when shared by
+// the channels) or projected from raw rows of 16-byte vectors.
+bool sel_takes_passes(int dtype, int64_t nbatch, int64_t L, int64_t Dc, int64_t N,
+                      bool dt_shared, bool dt_is_tau, bool proj, bool proj_ok) {
+  const int64_t rs = sel_chunk_steps(nbatch, L, Dc);
+  const int64_t cb = sel_chunked_bytes(nbatch, L, Dc, N);
+  return (!proj || proj_ok) && cb > 0 && (dtype == TSSM_F32 || dtype == TSSM_BF16) &&
+         (dt_shared || !dt_is_tau) && nbatch <= 65535 &&
+         nbatch * ((Dc + 63) / 64) * ((L + rs - 1) / rs) >= kSelMinWaves;
+}
 
 int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, int dt_is_tau,
                           const DtProj& proj, const float* A_log, const void* B, const void* C,
@@ -1324,22 +1345,38 @@ int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, i
   TSSM_CHECK(aligned(B, 16) && aligned(C, 16) && aligned(A_log, 16), TSSM_ERR_ALIGN);
   const int64_t strides[] = {sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b, sy_l};
   for (int64_t s : strides) TSSM_CHECK(s >= 0, TSSM_ERR_STRIDE);
+  if (proj.W) {
+    TSSM_CHECK(proj.bias, TSSM_ERR_NULL);
+    TSSM_CHECK(!dt_is_tau, TSSM_ERR_UNSUPPORTED);
+    TSSM_CHECK(proj.rank > 0 && proj.rank <= kMaxDtRank, TSSM_ERR_UNSUPPORTED);
+    TSSM_CHECK(proj.sw_r >= 0 && proj.dt_min <= proj.dt_max, TSSM_ERR_SHAPE);
+  }
   // Large problems with 8 or 16 states take the three-pass scan (lanes =
-  // channels, B/C through scalar loads): fp32 or bf16 I/O, dt given (not
-  // projected), timestamps only when shared by the channels.
+  // channels, B/C staged in LDS): fp32 or bf16 I/O; dt given (timestamps
+  // only when shared by the channels) or projected from raw rows of 16-byte
+  // vectors (produced on the matrix cores in passes 1 and 3).
   {
     const int64_t rs = sel_chunk_steps(nbatch, L, Dc);
     const int64_t cb = sel_chunked_bytes(nbatch, L, Dc, N);
-    const bool dt_shared = sdt_d == 0;
-    if (!proj.W && cb > 0 && (dtype == TSSM_F32 || dtype == TSSM_BF16) &&
-        (dt_shared || !dt_is_tau) && nbatch <= 65535 &&
-        nbatch * ((Dc + 63) / 64) * ((L + rs - 1) / rs) >= kSelMinWaves) {
+    const bool dt_shared = !proj.W && sdt_d == 0;
+    const bool proj_ok = proj.W && sel_proj_ok(dt, proj.W, proj.bias, Dc, proj.rank, sdt_b,
+                                               sdt_l, proj.sw_r);
+    if (sel_takes_passes(dtype, nbatch, L, Dc, N, dt_shared, dt_is_tau != 0, proj.W != nullptr,
+                         proj_ok)) {
       SelPtrs p;
       p.x = x; p.dt = dt; p.A_log = A_log; p.B = B; p.C = C; p.D = D; p.h0 = h0; p.y = y;
       p.h_last = h_last;
+      p.W = proj.W; p.bias = proj.bias; p.sw_r = proj.sw_r; p.rank = proj.rank;
+      p.dt_min = proj.dt_min; p.dt_max = proj.dt_max;
       const int64_t off = sel_chunked_offset(sel_lookback_bytes(nbatch, L, Dc, N, chunk));
       p.S = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
       p.T = p.S + nbatch * ((L + rs - 1) / rs) * Dc * N;
+      if (proj.W) {
+        // room for the produced-dt table: pass 1 stores it, pass 3 reads it
+        const int64_t toff = sel_chunked_offset(off + cb);
+        if (workspace_bytes >= toff + sel_dt_table_bytes(nbatch, L, Dc))
+          p.dtw = reinterpret_cast<float*>(static_cast<char*>(workspace) + toff);
+      }
       return sel_chunked_launch(dtype, disc, dt_shared, dt_is_tau != 0, p, nbatch, L, Dc, N,
                                 sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b,
                                 sy_l, as_stream(stream));
@@ -1351,10 +1388,6 @@ int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, i
   const int nrun = cfg.W * (64 / cfg.G);
   size_t lds = ((size_t)2 * nrun * P + 2 * (nrun / 8) * P + 3 * P) * sizeof(float);
   if (proj.W) {
-    TSSM_CHECK(proj.bias, TSSM_ERR_NULL);
-    TSSM_CHECK(!dt_is_tau, TSSM_ERR_UNSUPPORTED);
-    TSSM_CHECK(proj.rank > 0 && proj.rank <= kMaxDtRank, TSSM_ERR_UNSUPPORTED);
-    TSSM_CHECK(proj.sw_r >= 0 && proj.dt_min <= proj.dt_max, TSSM_ERR_SHAPE);
     const int64_t rp = (proj.rank + 3) & ~3ll;  // rank padded to whole float4s
     lds += (size_t)(cfg.TC * cpr + cfg.TC * (rp + 4) + rp * cpr) * sizeof(float);
     TSSM_CHECK(lds <= 64 * 1024, TSSM_ERR_UNSUPPORTED);
@@ -1393,6 +1426,17 @@ int selective_scan_launch(int dtype, int disc, const void* x, const float* dt, i
 
 }  // namespace
 }  // namespace tssm
+
+extern "C" int tssm_selective_scan_takes_passes(int dtype, int64_t nbatch, int64_t L, int64_t Dc,
+                                                int64_t N, int64_t sdt_d, int dt_is_tau,
+                                                const float* dt_raw, const float* W,
+                                                const float* bias, int64_t rank, int64_t sr_b,
+                                                int64_t sr_l, int64_t sw_r) {
+  const bool proj = W != nullptr;
+  const bool proj_ok = proj && sel_proj_ok(dt_raw, W, bias, Dc, rank, sr_b, sr_l, sw_r);
+  return sel_takes_passes(dtype, nbatch, L, Dc, N, !proj && sdt_d == 0, dt_is_tau != 0, proj,
+                          proj_ok) ? 1 : 0;
+}
 
 extern "C" int tssm_selective_scan(int dtype, int disc, const void* x, const float* dt,
                                    int dt_is_tau, const float* A_log, const void* B,

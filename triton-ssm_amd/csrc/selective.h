@@ -25,7 +25,25 @@ struct SelPtrs {
   float* h_last = nullptr;
   float* S = nullptr;  // [nbatch][nch][Dc][N] chunk end states -> entry states
   float* T = nullptr;  // [nbatch][nch][Dc] (or [nbatch][nch]) dt sums per chunk
+  // dt produced in the passes (W != NULL): `dt` then holds the raw rows
+  // [nbatch][L][rank] (strides sdt_b, sdt_l, 1) and
+  // dt[b,t,d] = clamp(softplus(sum_q raw[b,t,q] W[q,d] + bias[d]), dt_min, dt_max)
+  const float* W = nullptr;     // [rank][Dc], row stride sw_r
+  const float* bias = nullptr;  // [Dc]
+  int64_t sw_r = 0;
+  int64_t rank = 0;
+  float dt_min = 0.0f, dt_max = 0.0f;
+  // optional [nbatch][L][Dc] table: pass 1 stores the dt it produced there and
+  // pass 3 reads it back (NULL: pass 3 produces dt again)
+  float* dtw = nullptr;
 };
+
+// Whether the three-pass scan can produce dt itself for these operands: the
+// matrix-core form needs 16-byte rows (rank, Dc, row strides multiples of 4;
+// raw rows, W and bias 16-byte aligned) and rank <= kSelMaxRank.
+constexpr int64_t kSelMaxRank = 64;
+bool sel_proj_ok(const float* raw, const float* W, const float* bias, int64_t Dc, int64_t rank,
+                 int64_t sr_b, int64_t sr_l, int64_t sw_r);
 
 // Steps per chunk for these sizes (0: the three-pass scan does not apply).
 int64_t sel_chunk_steps(int64_t nbatch, int64_t L, int64_t Dc);
@@ -33,8 +51,12 @@ int64_t sel_chunk_steps(int64_t nbatch, int64_t L, int64_t Dc);
 // Workspace bytes of the three-pass scan (0 if it does not apply to the shape).
 int64_t sel_chunked_bytes(int64_t nbatch, int64_t L, int64_t Dc, int64_t N);
 
+// Bytes of the produced-dt table (SelPtrs::dtw).
+int64_t sel_dt_table_bytes(int64_t nbatch, int64_t L, int64_t Dc);
+
 // Launch the three passes on `s`.  dtype F32 or BF16, N 8 or 16; dt shared by
-// the channels (sdt_d unused) or per channel (then not timestamps).
+// the channels (sdt_d unused), per channel (then not timestamps), or produced
+// from raw rows (p.W set; sel_proj_ok must hold; dt_shared and tau false).
 int sel_chunked_launch(int dtype, int disc, bool dt_shared, bool tau, const SelPtrs& p,
                        int64_t nbatch, int64_t L, int64_t Dc, int64_t N, int64_t sx_b,
                        int64_t sx_l, int64_t sdt_b, int64_t sdt_l, int64_t sdt_d, int64_t sB_b,

@@ -42,7 +42,92 @@ struct SelDims {
   int64_t L, Dc, Rs, nch;
   int64_t sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b, sy_l;
   int64_t nbatch;
+  // dt produced from raw rows (DTP instances): W [rank][Dc] row stride sw_r
+  const float* W;
+  const float* bias;
+  int64_t sw_r;
+  int rank;
+  float dt_min, dt_max;
+  float* dtw;  // NULL, or [nbatch][L][Dc]: pass 1 stores the produced dt there
 };
+
+// Row stride of the produced-dt table s_dt[step][channel] in LDS: 260 = 4
+// mod 32 floats, so the 16-byte writes of the transpose (8 lanes per pass,
+// 8 consecutive steps) land on distinct banks; reads are one row of
+// consecutive channels.
+constexpr int kSelDtStride = kSelThreads + 4;
+
+// dt of the chunk's steps for the wave's 64 channels (first channel dw0),
+// into s_dt[r * kSelDtStride + column] (column = channel - the workgroup's
+// first channel).  The product raw[t0 + r, :] W[:, d] + bias[d] runs on the
+// matrix cores in the operand order of the standalone projection kernel
+// (dt_project_mfma_kernel: A = W columns, B = raw rows, 16x16x4 f32, the
+// rank in blocks of 16 with lane group lj holding ranks q0 + 4 lj + s), so
+// the values are those that kernel stores; then softplus and the clamp.
+// Lane (li, lj) holds D[h][t] for channels 16 ct + 4 lj + i and steps
+// 16 rt + li, written as one 16-byte row piece per (rt, ct).  Steps past the
+// chunk's n repeat step n-1 (the readers give padded steps dt = 0); columns
+// of channels past Dc hold values of no channel (clamped weights and bias)
+// and are never read: a lane past Dc computes channel Dc-1 and reads that
+// channel's column.  Every load is in bounds: Dc, rank and the row strides
+// are multiples of 4 (sel_proj_ok).
+__device__ inline void sel_proj_table(const float* __restrict__ raw_b, int64_t sr_l,
+                                      int64_t t0, int n, const SelDims& m, int64_t dw0,
+                                      int col0, float* s_dt) {
+  const int lane = threadIdx.x & 63, li = lane & 15, lj = lane >> 4;
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const int64_t h = dw0 + 16 * ct + 4 * lj;  // 4 channels, all in range or all out
+    const float4 bq = *reinterpret_cast<const float4*>(m.bias + (h < m.Dc ? h : 0));
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) acc[rt][ct] = f32x4{bq.x, bq.y, bq.z, bq.w};
+  }
+  for (int q0 = 0; q0 < m.rank; q0 += 16) {
+    const bool qok = q0 + 4 * lj < m.rank;  // rank % 4 == 0: a group is all in or all out
+    const int64_t qa = qok ? q0 + 4 * lj : 0;
+    float wa[4][4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int64_t h = dw0 + 16 * ct + li;
+      const float* wp = m.W + (h < m.Dc ? h : m.Dc - 1);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float v = wp[(qa + s) * m.sw_r];
+        wa[ct][s] = qok ? v : 0.0f;
+      }
+    }
+    f32x4 rv[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int r = 16 * rt + li;
+      const f32x4 v =
+          *reinterpret_cast<const f32x4*>(raw_b + (t0 + (r < n ? r : n - 1)) * sr_l + qa);
+      rv[rt] = qok ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[ct][s], rv[rt][s], acc[rt][ct],
+                                                              0, 0, 0);
+  }
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      float4 v;
+      v.x = clamp_med3(softplus_fast(acc[rt][ct][0]), m.dt_min, m.dt_max);
+      v.y = clamp_med3(softplus_fast(acc[rt][ct][1]), m.dt_min, m.dt_max);
+      v.z = clamp_med3(softplus_fast(acc[rt][ct][2]), m.dt_min, m.dt_max);
+      v.w = clamp_med3(softplus_fast(acc[rt][ct][3]), m.dt_min, m.dt_max);
+      *reinterpret_cast<float4*>(s_dt + (16 * rt + li) * kSelDtStride + col0 + 16 * ct +
+                                 4 * lj) = v;
+    }
+  }
+}
 
 // ab = exp2(dt a log2e) for each state; ZOH input term (ab - 1) B x / a
 // (h' = ab h + (ab - 1) B x / a); Euler B dt x.
@@ -165,7 +250,9 @@ __device__ inline void chunk_prefetch(const T* __restrict__ xp, int64_t sx_l,
 // steps (r >= n) have dt = 0 -- an identity step -- and repeat step n-1's x
 // and B/C rows, so they reproduce step n-1's output.  `step(r, u, dtv)` gets
 // every step.
-template <typename T, bool DTS, typename F>
+// DTP: dt produced in the pass, read from the lane's column of the LDS table
+// (s_dt then points at that column, row stride kSelDtStride).
+template <typename T, bool DTS, bool DTP = false, typename F>
 __device__ inline void chunk_steps(const T* __restrict__ xp, int64_t sx_l,
                                    const float* __restrict__ dtp, int64_t sdt_l,
                                    const float* s_dt, int64_t t0, int n, int n4,
@@ -174,23 +261,28 @@ __device__ inline void chunk_steps(const T* __restrict__ xp, int64_t sx_l,
 #pragma unroll
     for (int j = 0; j < kSelPf; ++j) {
       const int rr = r + j;
-      step(rr, u[j], DTS ? s_dt[rr] : (rr < n ? dr[j] : 0.0f));
+      float dtv;
+      if constexpr (DTS) dtv = s_dt[rr];
+      else if constexpr (DTP) dtv = rr < n ? s_dt[rr * kSelDtStride] : 0.0f;
+      else dtv = rr < n ? dr[j] : 0.0f;
+      step(rr, u[j], dtv);
       // refill the registers step rr just used (no copies across the loop)
       __builtin_amdgcn_sched_barrier(0);
       const int64_t tn = t0 + min(rr + kSelPf, n - 1);
       u[j] = ldf(xp + tn * sx_l);
-      if constexpr (!DTS) dr[j] = dtp[tn * sdt_l];
+      if constexpr (!DTS && !DTP) dr[j] = dtp[tn * sdt_l];
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
-template <typename T, int DISC, int NST, bool DTS, bool TAU, bool HAS_D>
+template <typename T, int DISC, int NST, bool DTS, bool TAU, bool HAS_D, bool DTP = false>
 __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
     const T* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
     const T* __restrict__ Bm, const T* __restrict__ Cm, const float* __restrict__ D,
     T* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum, SelDims m) {
   static_assert(!TAU || DTS, "timestamps only when shared by the channels");
+  static_assert(!DTP || (!DTS && !TAU), "produced dt is per channel");
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int64_t d = (int64_t)blockIdx.y * kSelThreads + threadIdx.x;
   const bool ok = d < m.Dc;
@@ -201,9 +293,10 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
 
   __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
   __shared__ float sD[DTS ? kSelChunkSteps : 1];
+  __shared__ float sP[DTP ? kSelChunkSteps * kSelDtStride : 1];  // produced dt [step][column]
   // every prologue load first (rows to stage, lane parameters, the first x
   // fetches), then one wait: each load would otherwise be a round trip of its own
-  const float* dtb = dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d);
+  const float* dtb = dt + b * m.sdt_b + (DTS || DTP ? 0 : dc * m.sdt_d);
   const float4 vB = stage_row_load<T, NST>(Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
   const float4 vC = stage_row_load<T, NST>(Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
   float vdt = 0.0f;
@@ -212,7 +305,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
   load_alog<NST>(A_log, dc, al);
   float Dd = HAS_D ? D[dc] : 0.0f;
   float u[kSelPf], dr[kSelPf];
-  chunk_prefetch<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dtb, m.sdt_l, t0, n, u, dr);
+  chunk_prefetch<T, DTS || DTP>(x + b * m.sx_b + dc, m.sx_l, dtb, m.sdt_l, t0, n, u, dr);
 #pragma unroll
   for (int j = 0; j < kSelPf; ++j) asm volatile("" : "+v"(u[j]), "+v"(dr[j]));
   stage_row_store<NST>(sB, vB, n4);
@@ -220,6 +313,10 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
   if constexpr (DTS) {
     if ((int)threadIdx.x < n4) sD[threadIdx.x] = vdt;
   }
+  if constexpr (DTP)
+    sel_proj_table(dtb, m.sdt_l, t0, n, m,
+                   (int64_t)blockIdx.y * kSelThreads + (threadIdx.x & ~63u),
+                   (int)(threadIdx.x & ~63u), sP);
   float a2[NST], nia[NST], h[NST];
   sel_params<NST>(al, a2, nia);
 #pragma unroll
@@ -235,7 +332,10 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
   if ((int64_t)blockIdx.y * kSelThreads + (threadIdx.x & ~63u) >= m.Dc) return;
 
   float sdt = 0.0f;
-  chunk_steps<T, DTS>(x + b * m.sx_b + dc, m.sx_l, dtb, m.sdt_l, sD, t0, n, n4, u, dr,
+  // lanes past Dc read channel Dc-1's column: they store its outputs
+  chunk_steps<T, DTS, DTP>(x + b * m.sx_b + dc, m.sx_l, dtb, m.sdt_l,
+                           DTP ? sP + (dc - (int64_t)blockIdx.y * kSelThreads) : sD, t0, n, n4,
+                           u, dr,
                       [&](int rr, float u, float dtv) {
                         float Bv[NST], Cv[NST];
                         lds_row<NST>(sB + rr * NST, Bv);
@@ -257,6 +357,13 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
                         // fetches.
                         const int64_t tw = t0 + (rr < n ? rr : n - 1);
                         stf(yp + tw * m.sy_l, acc0 + acc1);
+                        if constexpr (DTP) {
+                          // the table's row rr (a padded row repeats row n-1,
+                          // whose value it then stores again), for pass 3
+                          if (m.dtw)
+                            m.dtw[(b * m.L + tw) * m.Dc + dc] =
+                                sP[rr * kSelDtStride + (dc - (int64_t)blockIdx.y * kSelThreads)];
+                        }
                       });
   if (ok) {
     float4* sp = reinterpret_cast<float4*>(S + ((b * m.nch + c) * m.Dc + d) * NST);
@@ -325,11 +432,12 @@ __global__ __launch_bounds__(kSelCarryThreads) void sel_carry_kernel(
 // the product of the per-step factors of the recurrence written as one
 // exponential; it does not depend on the discretization.  y is read (four
 // steps ahead) and written in place, so it is not declared restrict.
-template <typename T, int NST, bool DTS, bool TAU>
+template <typename T, int NST, bool DTS, bool TAU, bool DTP = false>
 __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
     const float* __restrict__ dt, const float* __restrict__ A_log, const T* __restrict__ Cm,
     const float* __restrict__ S, T* y, SelDims m) {
   static_assert(!TAU || DTS, "timestamps only when shared by the channels");
+  static_assert(!DTP || (!DTS && !TAU), "produced dt is per channel");
   const int64_t c = blockIdx.x, b = blockIdx.z;
   const int64_t d = (int64_t)blockIdx.y * kSelThreads + threadIdx.x;
   const int64_t dc = d < m.Dc ? d : m.Dc - 1;
@@ -339,8 +447,9 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
 
   __shared__ float sC[kSelChunkSteps * NST];
   __shared__ float sD[DTS ? kSelChunkSteps : 1];
+  __shared__ float sP[DTP ? kSelChunkSteps * kSelDtStride : 1];  // produced dt [step][column]
   // every prologue load first, then one wait (as in pass 1)
-  const float* dtb = dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d);
+  const float* dtb = dt + b * m.sdt_b + (DTS || DTP ? 0 : dc * m.sdt_d);
   T* yp = y + b * m.sy_b + dc;
   const float4 vC = stage_row_load<T, NST>(Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
   float vdt = 0.0f;
@@ -356,13 +465,17 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
     }
   }
   float u[kSelPf], dr[kSelPf];
-  chunk_prefetch<T, DTS>(yp, m.sy_l, dtb, m.sdt_l, t0, n, u, dr);
+  chunk_prefetch<T, DTS || DTP>(yp, m.sy_l, dtb, m.sdt_l, t0, n, u, dr);
 #pragma unroll
   for (int j = 0; j < kSelPf; ++j) asm volatile("" : "+v"(u[j]), "+v"(dr[j]));
   stage_row_store<NST>(sC, vC, n4);
   if constexpr (DTS) {
     if ((int)threadIdx.x < n4) sD[threadIdx.x] = vdt;
   }
+  if constexpr (DTP)
+    sel_proj_table(dtb, m.sdt_l, t0, n, m,
+                   (int64_t)blockIdx.y * kSelThreads + (threadIdx.x & ~63u),
+                   (int)(threadIdx.x & ~63u), sP);
   float a2[NST], nia[NST];
   sel_params<NST>(al, a2, nia);
 #pragma unroll
@@ -377,7 +490,10 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
   if ((int64_t)blockIdx.y * kSelThreads + (threadIdx.x & ~63u) >= m.Dc) return;
 
   float cum = 0.0f;
-  chunk_steps<T, DTS>(yp, m.sy_l, dtb, m.sdt_l, sD, t0, n, n4, u, dr,
+  // lanes past Dc read channel Dc-1's column: they store its outputs
+  chunk_steps<T, DTS, DTP>(yp, m.sy_l, dtb, m.sdt_l,
+                           DTP ? sP + (dc - (int64_t)blockIdx.y * kSelThreads) : sD, t0, n, n4,
+                           u, dr,
                       [&](int rr, float y1, float dtv) {
                         float Cv[NST];
                         lds_row<NST>(sC + rr * NST, Cv);
@@ -400,7 +516,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
 // ---------------------------------------------------------------- host
 namespace {
 
-template <typename T, int DISC, int NST, bool DTS, bool TAU>
+template <typename T, int DISC, int NST, bool DTS, bool TAU, bool DTP = false>
 int sel_chunked_t(bool has_d, const SelPtrs& p, const SelDims& m, hipStream_t s) {
   const dim3 grid((unsigned)m.nch, (unsigned)((m.Dc + kSelThreads - 1) / kSelThreads),
                   (unsigned)m.nbatch);
@@ -409,10 +525,10 @@ int sel_chunked_t(bool has_d, const SelPtrs& p, const SelDims& m, hipStream_t s)
   const T* Cm = static_cast<const T*>(p.C);
   T* y = static_cast<T*>(p.y);
   if (has_d)
-    hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU, true>), grid,
+    hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU, true, DTP>), grid,
                        dim3(kSelThreads), 0, s, x, p.dt, p.A_log, Bm, Cm, p.D, y, p.S, p.T, m);
   else
-    hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU, false>), grid,
+    hipLaunchKernelGGL((sel_chunk_state_kernel<T, DISC, NST, DTS, TAU, false, DTP>), grid,
                        dim3(kSelThreads), 0, s, x, p.dt, p.A_log, Bm, Cm, p.D, y, p.S, p.T, m);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
@@ -423,14 +539,23 @@ int sel_chunked_t(bool has_d, const SelPtrs& p, const SelDims& m, hipStream_t s)
                      dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
   e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((sel_output_kernel<T, NST, DTS, TAU>), grid, dim3(kSelThreads), 0, s, p.dt,
-                     p.A_log, Cm, p.S, y, m);
+  if (DTP && p.dtw) {
+    // pass 3 reads the dt table pass 1 stored: the per-channel dt instance
+    SelDims m3 = m;
+    m3.sdt_b = m.L * m.Dc; m3.sdt_l = m.Dc; m3.sdt_d = 1;
+    hipLaunchKernelGGL((sel_output_kernel<T, NST, false, false, false>), grid, dim3(kSelThreads),
+                       0, s, p.dtw, p.A_log, Cm, p.S, y, m3);
+  } else {
+    hipLaunchKernelGGL((sel_output_kernel<T, NST, DTS, TAU, DTP>), grid, dim3(kSelThreads), 0, s,
+                       p.dt, p.A_log, Cm, p.S, y, m);
+  }
   return (int)hipGetLastError();
 }
 
 template <typename T, int DISC, int NST>
 int sel_chunked_dt(bool has_d, bool dts, bool tau, const SelPtrs& p, const SelDims& m,
                    hipStream_t s) {
+  if (p.W) return sel_chunked_t<T, DISC, NST, false, false, true>(has_d, p, m, s);
   if (dts) {
     return tau ? sel_chunked_t<T, DISC, NST, true, true>(has_d, p, m, s)
                : sel_chunked_t<T, DISC, NST, true, false>(has_d, p, m, s);
@@ -453,6 +578,17 @@ int64_t sel_chunk_steps(int64_t nbatch, int64_t L, int64_t Dc) {
   return L >= 64 ? kSelChunkSteps : 0;
 }
 
+bool sel_proj_ok(const float* raw, const float* W, const float* bias, int64_t Dc, int64_t rank,
+                 int64_t sr_b, int64_t sr_l, int64_t sw_r) {
+  return rank > 0 && rank <= kSelMaxRank && rank % 4 == 0 && Dc % 4 == 0 && sr_b % 4 == 0 &&
+         sr_l % 4 == 0 && sw_r % 4 == 0 && sr_b >= 0 && sr_l >= 0 && sw_r >= 0 &&
+         aligned(raw, 16) && aligned(W, 16) && aligned(bias, 16);
+}
+
+int64_t sel_dt_table_bytes(int64_t nbatch, int64_t L, int64_t Dc) {
+  return nbatch * L * Dc * (int64_t)sizeof(float);
+}
+
 int64_t sel_chunked_bytes(int64_t nbatch, int64_t L, int64_t Dc, int64_t N) {
   if (!(N == 8 || N == 16) || nbatch <= 0 || L <= 0 || Dc <= 0) return 0;
   const int64_t rs = sel_chunk_steps(nbatch, L, Dc);
@@ -472,6 +608,9 @@ int sel_chunked_launch(int dtype, int disc, bool dt_shared, bool tau, const SelP
   m.nch = (L + m.Rs - 1) / m.Rs;
   m.sx_b = sx_b; m.sx_l = sx_l; m.sdt_b = sdt_b; m.sdt_l = sdt_l; m.sdt_d = sdt_d;
   m.sB_b = sB_b; m.sB_l = sB_l; m.sC_b = sC_b; m.sC_l = sC_l; m.sy_b = sy_b; m.sy_l = sy_l;
+  m.W = p.W; m.bias = p.bias; m.sw_r = p.sw_r; m.rank = (int)p.rank;
+  m.dt_min = p.dt_min; m.dt_max = p.dt_max; m.dtw = p.W ? p.dtw : nullptr;
+  if (p.W && (dt_shared || tau)) return TSSM_ERR_UNSUPPORTED;
   const bool has_d = p.D != nullptr;
   if (dtype == TSSM_BF16) {
     return disc == TSSM_DISC_ZOH

@@ -291,10 +291,23 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
     _inner_unit(y, "out")
     h_last = torch.empty(Bsz, Dc, N, device=x.device, dtype=torch.float32) if return_state else None
     L_ = _lib.lib()
-    ws, stream = _ws(L_.tssm_selective_scan_workspace_bytes(Bsz, L, Dc, N, int(chunk)), x,
-                     "selective_scan")
+    # the three-pass path writes raw fp32 chunk states (and the produced dt)
+    # into its workspace, the single-pass kernel tagged look-back words: the
+    # two never share a buffer
     if proj is not None:
         W, bias, dt_min, dt_max, rank = proj
+        passes = L_.tssm_selective_scan_takes_passes(
+            code, Bsz, L, Dc, N, 1, 0, dt.data_ptr(), W.data_ptr(), bias.data_ptr(), rank,
+            dt.stride(0), dt.stride(1), W.stride(0))
+        nbytes = L_.tssm_selective_scan_dtproj_workspace_bytes(Bsz, L, Dc, N, int(chunk))
+    else:
+        passes = L_.tssm_selective_scan_takes_passes(
+            code, Bsz, L, Dc, N, sdt[2], int(bool(dt_is_tau)), dt.data_ptr(), None, None, 0,
+            0, 0, 0)
+        nbytes = L_.tssm_selective_scan_workspace_bytes(Bsz, L, Dc, N, int(chunk))
+    ws, stream = _ws(nbytes, x, "selective_scan",
+                     workspace.SSD if passes else workspace.LOOKBACK)
+    if proj is not None:
         _lib.call("tssm_selective_scan_dtproj", code, _disc_code(disc), x.data_ptr(),
                   dt.data_ptr(), W.data_ptr(), bias.data_ptr(), dt_min, dt_max,
                   A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), ptr(h0), y.data_ptr(),

@@ -9,9 +9,10 @@ launches.  Two kinds never share a buffer:
               launch, so stale words never match and no per-launch clearing
               is needed -- provided nothing but tagged words is ever written
               there.
-``ssd``       the SSD passes: raw fp32 chunk states and decays.  Kept apart
-              because an arbitrary fp32 pair read as a carry word could carry
-              a current epoch in its upper half.
+``ssd``       raw fp32 data: the SSD passes' chunk states and decays, and the
+              three-pass selective scan's chunk states, dt sums and produced
+              dt.  Kept apart because an arbitrary fp32 pair read as a carry
+              word could carry a current epoch in its upper half.
 
 One buffer is kept per (device, stream, kind) and grown when a launch needs
 more; launches on different streams therefore never share one.
