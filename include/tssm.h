@@ -244,6 +244,38 @@ int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, const void* V,
                          int64_t s_hob, int64_t t_cur, int64_t K, int64_t FTILE, int64_t grid_b,
                          int64_t grid_f, void* stream);
 
+/* Interpolation + Mamba-1 scan over a whole sequence (the sequence form of
+ * fused_interp_ssm_step_kernel, fused_ssm_interp.py:12-101, with the
+ * interpolation of fused_interp_kernel.py:29-100 and the scan of
+ * tssm_selective_scan with dt_t = tau_t - tau_{t-1}, dt_0 = tau_0): Vhat is
+ * formed inside the scan's first pass, written once and consumed there as x;
+ * three launches on `stream`.  V, Vhat, B, C, y in `dtype` (f32 or bf16), M
+ * and tau f32; V/M/Vhat [B,T,F], tau [B,T], B/C [B,T,N], y [B,T,F]; A_log
+ * f32 [F,N]; D f32 [F] or NULL; h0/h_last f32 [B,F,N] or NULL.  K and FTILE as
+ * in tssm_time_aware_interp (semantic).  Returns TSSM_ERR_UNSUPPORTED before
+ * any launch unless tssm_interp_selective_scan_supported() holds (f32 masks in
+ * 16-byte rows, FTILE a power of two in [16, 256], 1 <= K <= 64, F a multiple
+ * of 4, N 8 or 16, a problem of at least 512 blocks of 64 channels x 32
+ * steps); callers then run tssm_time_aware_interp and tssm_selective_scan.
+ * The workspace (raw fp32 chunk states, not look-back words) holds
+ * tssm_interp_selective_scan_workspace_bytes() bytes.  No reference
+ * counterpart as one entry point. */
+int64_t tssm_interp_selective_scan_workspace_bytes(int64_t nbatch, int64_t T, int64_t F,
+                                                   int64_t N);
+int tssm_interp_selective_scan_supported(int dtype, int m_dtype, int tau_dtype, int64_t nbatch,
+                                         int64_t T, int64_t F, int64_t N, int64_t K,
+                                         int64_t FTILE, const void* M, int64_t sm_b,
+                                         int64_t sm_t);
+int tssm_interp_selective_scan(int dtype, int disc, const void* V, const float* M,
+                               const float* tau, const float* A_log, const void* B,
+                               const void* C, const float* D, const float* h0, void* Vhat,
+                               void* y, float* h_last, int64_t nbatch, int64_t T, int64_t F,
+                               int64_t N, int64_t sv_b, int64_t sv_t, int64_t sm_b, int64_t sm_t,
+                               int64_t stau_b, int64_t stau_t, int64_t sB_b, int64_t sB_l,
+                               int64_t sC_b, int64_t sC_l, int64_t so_b, int64_t so_t,
+                               int64_t sy_b, int64_t sy_t, int64_t K, int64_t FTILE,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ streaming
  * streaming_ssm_inplace_kernel / streaming_ssm_inplace_bf16_kernel
  * (streaming_inference_kernel.py:7-37 / :41-71).  All tensors in `dtype`;

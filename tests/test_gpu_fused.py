@@ -541,6 +541,62 @@ def test_fused_interp_ssm_small(dev, FTILE):
     assert_close(h, h_ref, 1e-5, "h_last")
 
 
+@pytest.mark.parametrize("dtype,N,F,FTILE,K,T,Bsz,missing,extras", [
+    (torch.float32, 16, 256, 16, 5, 2000, 8, 0.97, True),      # 16 tiles per workgroup, gaps
+    (torch.bfloat16, 8, 260, 128, 64, 1100, 16, 0.999, False),  # ragged channels, K = 64, sparse
+    (torch.float32, 16, 128, 256, 1, 2048, 8, 0.5, False),      # tile wider than F, K = 1
+])
+def test_interp_scan_fused_forms(dev, dtype, N, F, FTILE, K, T, Bsz, missing, extras):
+    """Interpolation formed inside the scan's first pass
+    (tssm_interp_selective_scan, taken by fused_interp_ssm_forward for these
+    problems) against the oracle and against the two-kernel path (the
+    interpolation drop-in, then the selective scan over the stored Vhat):
+    Vhat bit for bit, y and h_last within the bars.  Sparse masks leave
+    whole tiles unobserved, so steps take every neighbour case (both, one
+    side, none within K)."""
+    import fused_interp_kernel as fik
+    from tssm import _lib, fused_interp_ssm_forward, selective_scan_forward
+    g = torch.Generator().manual_seed(F + K + FTILE)
+    tau = torch.sort(torch.rand(Bsz, T, generator=g) * (T / 20.0), dim=1).values
+    M = (torch.rand(Bsz, T, F, generator=g) >= missing).float()
+    V = (torch.randn(Bsz, T, F, generator=g) * M).to(dtype)
+    A_log = torch.empty(F, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = (torch.randn(Bsz, T, N, generator=g) / N ** 0.5).to(dtype)
+    Cm = (torch.randn(Bsz, T, N, generator=g) / N ** 0.5).to(dtype)
+    D = torch.randn(F, generator=g) if extras else None
+    h0 = torch.randn(Bsz, F, N, generator=g) if extras else None
+    d = {k: v.to(dev) for k, v in dict(V=V, M=M, tau=tau, A_log=A_log, B=Bm, C=Cm).items()}
+    Dd = D.to(dev) if extras else None
+    h0d = h0.to(dev) if extras else None
+    assert _lib.lib().tssm_interp_selective_scan_supported(
+        _lib.F32 if dtype == torch.float32 else _lib.BF16, _lib.F32, _lib.F32, Bsz, T, F, N, K,
+        FTILE, d["M"].data_ptr(),
+        d["M"].stride(0), d["M"].stride(1)) == 1
+    vhat, y, h = fused_interp_ssm_forward(d["V"], d["M"], d["tau"], d["A_log"], d["B"], d["C"],
+                                          Dd, K=K, FTILE=FTILE, h0=h0d, return_state=True)
+    # two-kernel path: the interpolation drop-in, then the scan over its Vhat
+    v2 = torch.empty_like(d["V"])
+    fik_kernel = fik.fused_time_aware_interp_kernel if dtype == torch.float32 else \
+        fik.fused_interp_bf16_kernel
+    fik_kernel[(Bsz, T, -(-F // FTILE))](d["V"], d["M"], d["tau"], v2, Bsz, T, F,
+                                         *d["V"].stride(), *d["M"].stride(), *d["tau"].stride(),
+                                         *v2.stride(), K=K, FTILE=FTILE)
+    y2, h2 = selective_scan_forward(v2, d["tau"], d["A_log"], d["B"], d["C"], Dd, h0=h0d,
+                                    return_state=True, dt_is_tau=True)
+    torch.cuda.synchronize()
+    assert torch.equal(vhat, v2), "Vhat differs from the interpolation kernel's"
+    v_ref, y_ref, h_ref = O.fused_interp_ssm(d["V"], d["M"], d["tau"], d["A_log"], d["B"],
+                                             d["C"], D, K=K, FTILE=FTILE,
+                                             h0=None if h0 is None else np64(h0))
+    tol = TOL[dtype]
+    assert_close(vhat, v_ref, 1e-6 if dtype == torch.float32 else 1e-2, "Vhat vs oracle")
+    e = assert_close(y, y_ref, tol, "y vs oracle")
+    assert_close(h, h_ref, tol, "h_last vs oracle")
+    assert_close(y, y2, 1e-5 if dtype == torch.float32 else 1e-2, "y vs two-kernel path")
+    print(f"interp-in-pass-1 {dtype} F={F} FTILE={FTILE} K={K}: relerr {e:.2e}, "
+          f"y bitwise equal to the two-kernel path: {torch.equal(y, y2)}")
+
+
 def test_fused_interp_ssm_full_shape(dev):
     """B=16 T=2048 F=D=256 N=16 fp32, 30% missing, K=10 FTILE=128."""
     from tssm import fused_interp_ssm_forward, workloads

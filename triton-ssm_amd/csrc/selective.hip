@@ -513,6 +513,210 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
                       });
 }
 
+// ---------------------------------------------------------------- interpolation in pass 1
+// Time-aware interpolation (fused_interp_kernel.py:29-100, reference
+// semantics as in interp.hip: "observed" is the FTILE-wide tile's mask sum
+// > 0.5, prev/next the nearest observed step within K on each side,
+// w = clip((tau_t - tau_prev)/(tau_next - tau_prev), 0, 1) or 0.5 when the
+// denominator <= 1e-9, vhat = interpolation / v_prev / v_next / v_cur)
+// formed inside pass 1 of the three-pass scan, which consumes it as x
+// (fused_ssm_interp.py:12-101 does the interpolation and the SSM update in
+// one kernel too, one step per launch).  Vhat is written once and never read
+// back; pass 3 reads y, C and tau only.
+//
+// A workgroup (256 channels of one batch, one chunk of n <= 32 steps):
+//  1. the tile flags of rows t0-K .. t0+n+K-1: wave w sums rows w, w+4, ...,
+//     lane l the 16-byte mask vector of channels 4l..4l+3, then an xor
+//     butterfly over the tile's FTILE/4 lanes -- the per-lane sums and the
+//     reduction order of interp_fused_kernel, so the same flags -- and the
+//     rows' timestamps, staged in LDS with the chunk's B/C rows and dt;
+//  2. per (step, tile): the neighbours and the weight, into LDS tables
+//     (padded steps repeat step n-1);
+//  3. the recurrence of pass 1, x_t of each lane interpolated in registers
+//     from V[prev] and V[next] (fetched four steps ahead), rounded to the
+//     I/O dtype as Vhat is, and stored to Vhat.
+constexpr int kSiMaxK = 64;       // search window the LDS tables hold
+constexpr int kSiMaxTiles = 16;   // FTILE >= 16: at most 16 tiles per 256 channels
+constexpr int kSiRows = kSelChunkSteps + 2 * kSiMaxK;
+
+struct SiDims {
+  int64_t svb, svt, smb, smt, sob, sot;  // V, M, Vhat strides (unit over features)
+  int K, lf, lvpt;                       // lf = log2 FTILE, lvpt = log2(FTILE / 4)
+};
+
+template <typename T>
+__device__ inline float round_io(float v) {
+  if constexpr (sizeof(T) == 4) return v;
+  else return bf16_bits_to_f32((uint16_t)f32_to_bf16_bits(v));
+}
+
+constexpr int kSiMaskU = 7;  // mask rows per wave in flight
+
+template <typename T, int DISC, int NST, bool HAS_D>
+__global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
+    const T* __restrict__ V, const float* __restrict__ M, const float* __restrict__ tau,
+    const float* __restrict__ A_log, const T* __restrict__ Bm, const T* __restrict__ Cm,
+    const float* __restrict__ D, T* __restrict__ Vhat, T* __restrict__ y,
+    float* __restrict__ S, float* __restrict__ Tsum, SelDims m, SiDims q) {
+  const int64_t c = blockIdx.x, b = blockIdx.z;
+  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t cb0 = (int64_t)blockIdx.y * kSelThreads;  // first channel of the workgroup
+  const int64_t d = cb0 + tid;
+  const bool ok = d < m.Dc;
+  const int64_t dc = ok ? d : m.Dc - 1;  // lanes past Dc compute channel Dc-1
+  const int64_t t0 = c * m.Rs;
+  const int n = (int)(m.L - t0 < m.Rs ? m.L - t0 : m.Rs);
+  const int n4 = (n + kSelPf - 1) / kSelPf * kSelPf;
+  const int K = q.K;
+  const int R = n + 2 * K;  // flag rows t0-K .. t0+n+K-1
+
+  __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
+  __shared__ float sD[kSelChunkSteps];
+  __shared__ float sTau[kSiRows];
+  __shared__ unsigned char sObs[kSiRows * kSiMaxTiles];
+  __shared__ int sPrev[kSelChunkSteps * kSiMaxTiles], sNext[kSelChunkSteps * kSiMaxTiles];
+  __shared__ float sW[kSelChunkSteps * kSiMaxTiles];
+
+  // ---- 1. prologue loads: rows to stage, timestamps, lane parameters, and
+  // the first batch of mask rows, before one wait
+  const float4 vB = stage_row_load<T, NST>(Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
+  const float4 vC = stage_row_load<T, NST>(Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
+  const float* taub = tau + b * m.sdt_b;
+  float vtau = 0.0f;
+  if (tid < R) {
+    const int64_t t = t0 - K + tid;
+    vtau = taub[(t < 0 ? 0 : (t >= m.L ? m.L - 1 : t)) * m.sdt_l];
+  }
+  float al[NST];
+  load_alog<NST>(A_log, dc, al);
+  float Dd = HAS_D ? D[dc] : 0.0f;
+  const float* Mb = M + b * q.smb + cb0 + 4 * lane;
+  const bool vec_ok = cb0 + 4 * lane < m.Dc;  // F = Dc, a multiple of 4
+  const int vpt = 1 << q.lvpt;
+  for (int i0 = wave; i0 < R; i0 += 4 * kSiMaskU) {
+    float sv[kSiMaskU];
+#pragma unroll
+    for (int u = 0; u < kSiMaskU; ++u) {
+      const int i = i0 + 4 * u;
+      const int64_t t = t0 - K + i;
+      const bool rok = i < R && t >= 0 && t < m.L && vec_ok;
+      const float4 v = *reinterpret_cast<const float4*>(rok ? Mb + t * q.smt : M);
+      float sum = 0.0f;
+      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
+      sv[u] = rok ? sum : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kSiMaskU; ++u) {
+      const int i = i0 + 4 * u;  // uniform per wave
+      float x = sv[u];
+      for (int o = 1; o < vpt; o <<= 1) x += __shfl_xor(x, o);
+      if (i < R && (lane & (vpt - 1)) == 0)
+        sObs[i * kSiMaxTiles + (lane >> q.lvpt)] = x > 0.5f ? 1 : 0;
+    }
+  }
+  stage_row_store<NST>(sB, vB, n4);
+  stage_row_store<NST>(sC, vC, n4);
+  if (tid < R) sTau[tid] = vtau;
+  float a2[NST], nia[NST], h[NST];
+  sel_params<NST>(al, a2, nia);
+#pragma unroll
+  for (int k = 0; k < NST; ++k) {
+    h[k] = 0.0f;
+    asm volatile("" : "+v"(a2[k]), "+v"(nia[k]));  // complete before the loop
+  }
+  asm volatile("" : "+v"(Dd));
+  __syncthreads();  // flags, timestamps, rows staged
+
+  // ---- 2. dt of the chunk's steps (timestamps differenced, padded steps 0)
+  // and the neighbour tables (padded steps repeat step n-1)
+  if (tid < n4) {
+    const int64_t t = t0 + tid;
+    sD[tid] = tid < n ? sTau[tid + K] - (t > 0 ? sTau[tid + K - 1] : 0.0f) : 0.0f;
+  }
+  const int ntl = kSelThreads >> q.lf;
+  for (int it = tid; it < n4 * ntl; it += kSelThreads) {
+    const int r = it / ntl, lt = it - r * ntl;
+    const int rr = r < n ? r : n - 1;
+    const int64_t t = t0 + rr;
+    int prev = -1, next = -1;
+    for (int k = 1; k <= K; ++k)
+      if (prev < 0 && sObs[(rr + K - k) * kSiMaxTiles + lt]) prev = (int)(t - k);
+    for (int k = 1; k <= K; ++k)
+      if (next < 0 && sObs[(rr + K + k) * kSiMaxTiles + lt]) next = (int)(t + k);
+    const float tau_t = sTau[rr + K];
+    const float tp = prev >= 0 ? sTau[rr + K - (int)(t - prev)] : 0.0f;
+    const float tn = next >= 0 ? sTau[rr + K + (int)(next - t)] : 0.0f;
+    const float den = tn - tp;
+    float w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
+    w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+    sPrev[r * kSiMaxTiles + lt] = prev;
+    sNext[r * kSiMaxTiles + lt] = next;
+    sW[r * kSiMaxTiles + lt] = w;
+  }
+  __syncthreads();
+  // Waves whose lanes are all past Dc are done (no barrier follows).
+  if (cb0 + (tid & ~63) >= m.Dc) return;
+
+  // ---- 3. the recurrence over interpolated inputs
+  const int lt = (int)((dc - cb0) >> q.lf);  // the lane's tile (of channel dc)
+  const T* vcol = V + b * q.svb + dc;
+  T* ocol = Vhat + b * q.sob + dc;
+  T* yp = y + b * m.sy_b + dc;
+  // rows read as "prev" and "next" for table row r (as interp_kernel: v_prev,
+  // else v_next, else v_cur; next falls back to the prev row)
+  auto fetch = [&](int r, float& vp, float& vn) {
+    const int pv = sPrev[r * kSiMaxTiles + lt], nx = sNext[r * kSiMaxTiles + lt];
+    const int64_t rp = pv >= 0 ? pv : (nx >= 0 ? nx : t0 + (r < n ? r : n - 1));
+    const int64_t rn = nx >= 0 ? nx : rp;
+    vp = ldf(vcol + rp * q.svt);
+    vn = ldf(vcol + rn * q.svt);
+  };
+  float vp[kSelPf], vn[kSelPf];
+#pragma unroll
+  for (int j = 0; j < kSelPf; ++j) fetch(j < n4 ? j : n4 - 1, vp[j], vn[j]);
+  float sdt = 0.0f;
+  for (int r = 0; r < n4; r += kSelPf) {
+#pragma unroll
+    for (int j = 0; j < kSelPf; ++j) {
+      const int rr = r + j;
+      const int ix = rr * kSiMaxTiles + lt;
+      const int mode = (sPrev[ix] >= 0 ? 1 : 0) | (sNext[ix] >= 0 ? 2 : 0);
+      const float w = sW[ix];
+      const float vh = mode == 3 ? (1.0f - w) * vp[j] + w * vn[j] : vp[j];
+      const float u = round_io<T>(vh);  // the scan consumes Vhat as stored
+      const float dtv = sD[rr];
+      const int64_t tw = t0 + (rr < n ? rr : n - 1);
+      float Bv[NST], Cv[NST];
+      lds_row<NST>(sB + rr * NST, Bv);
+      lds_row<NST>(sC + rr * NST, Cv);
+      sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
+      sdt += dtv;
+      float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NST; k += 2) {
+        acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
+        acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
+      }
+      // unconditional stores: padded steps and lanes past Dc (in the wave of
+      // channel Dc-1) store exactly the values of step n-1 / channel Dc-1
+      stf(ocol + tw * q.sot, vh);
+      stf(yp + tw * m.sy_l, acc0 + acc1);
+      // refill the registers this step used, for step rr + 4
+      __builtin_amdgcn_sched_barrier(0);
+      const int rn = rr + kSelPf < n4 ? rr + kSelPf : n4 - 1;
+      fetch(rn, vp[j], vn[j]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (ok) {
+    float4* sp = reinterpret_cast<float4*>(S + ((b * m.nch + c) * m.Dc + d) * NST);
+#pragma unroll
+    for (int qq = 0; qq < NST / 4; ++qq)
+      sp[qq] = make_float4(h[4 * qq], h[4 * qq + 1], h[4 * qq + 2], h[4 * qq + 3]);
+    if (d == 0) Tsum[b * m.nch + c] = sdt;
+  }
+}
+
 // ---------------------------------------------------------------- host
 namespace {
 
@@ -570,7 +774,89 @@ int sel_chunked_n(int64_t N, bool has_d, bool dts, bool tau, const SelPtrs& p, c
                  : sel_chunked_dt<T, DISC, 8>(has_d, dts, tau, p, m, s);
 }
 
+template <typename T, int DISC, int NST>
+int sel_interp_t(bool has_d, const void* V, const float* M, const float* tau, void* Vhat,
+                 const SelPtrs& p, const SelDims& m, const SiDims& q, hipStream_t s) {
+  const dim3 grid((unsigned)m.nch, (unsigned)((m.Dc + kSelThreads - 1) / kSelThreads),
+                  (unsigned)m.nbatch);
+  const T* Bm = static_cast<const T*>(p.B);
+  const T* Cm = static_cast<const T*>(p.C);
+  T* y = static_cast<T*>(p.y);
+  const T* Vt = static_cast<const T*>(V);
+  T* Ot = static_cast<T*>(Vhat);
+  if (has_d)
+    hipLaunchKernelGGL((sel_interp_state_kernel<T, DISC, NST, true>), grid, dim3(kSelThreads), 0,
+                       s, Vt, M, tau, p.A_log, Bm, Cm, p.D, Ot, y, p.S, p.T, m, q);
+  else
+    hipLaunchKernelGGL((sel_interp_state_kernel<T, DISC, NST, false>), grid, dim3(kSelThreads),
+                       0, s, Vt, M, tau, p.A_log, Bm, Cm, p.D, Ot, y, p.S, p.T, m, q);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const int64_t lanes = m.Dc * NST;  // per batch
+  hipLaunchKernelGGL((sel_carry_kernel<NST, true>),
+                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
+                          (unsigned)m.nbatch),
+                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((sel_output_kernel<T, NST, true, true>), grid, dim3(kSelThreads), 0, s, tau,
+                     p.A_log, Cm, p.S, y, m);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int DISC>
+int sel_interp_n(int64_t N, bool has_d, const void* V, const float* M, const float* tau,
+                 void* Vhat, const SelPtrs& p, const SelDims& m, const SiDims& q, hipStream_t s) {
+  return N == 16 ? sel_interp_t<T, DISC, 16>(has_d, V, M, tau, Vhat, p, m, q, s)
+                 : sel_interp_t<T, DISC, 8>(has_d, V, M, tau, Vhat, p, m, q, s);
+}
+
+int ilog2(int64_t v) {
+  int l = 0;
+  while ((int64_t)1 << (l + 1) <= v) ++l;
+  return l;
+}
+
 }  // namespace
+
+bool sel_interp_ok(int dtype, int64_t nbatch, int64_t T, int64_t F, int64_t N, int64_t K,
+                   int64_t FTILE, const void* M, int64_t sm_b, int64_t sm_t) {
+  const bool pow2 = FTILE > 0 && (FTILE & (FTILE - 1)) == 0;
+  const int64_t rs = sel_chunk_steps(nbatch, T, F);
+  return (dtype == TSSM_F32 || dtype == TSSM_BF16) && (N == 8 || N == 16) && rs > 0 &&
+         pow2 && FTILE >= 16 && FTILE <= kSelThreads && K >= 1 && K <= kSiMaxK && F > 0 &&
+         F % 4 == 0 && sm_b % 4 == 0 && sm_t % 4 == 0 && sm_b >= 0 && sm_t >= 0 &&
+         aligned(M, 16) && nbatch > 0 && nbatch <= 65535 &&
+         nbatch * ((F + 63) / 64) * ((T + rs - 1) / rs) >= kSelMinWaves;
+}
+
+int sel_interp_launch(int dtype, int disc, const void* V, const float* M, const float* tau,
+                      void* Vhat, const SelPtrs& p, int64_t nbatch, int64_t T, int64_t F,
+                      int64_t N, int64_t sv_b, int64_t sv_t, int64_t sm_b, int64_t sm_t,
+                      int64_t stau_b, int64_t stau_t, int64_t sB_b, int64_t sB_l, int64_t sC_b,
+                      int64_t sC_l, int64_t so_b, int64_t so_t, int64_t sy_b, int64_t sy_t,
+                      int64_t K, int64_t FTILE, hipStream_t s) {
+  SelDims m{};
+  m.L = T; m.Dc = F; m.nbatch = nbatch;
+  m.Rs = sel_chunk_steps(nbatch, T, F);
+  m.nch = (T + m.Rs - 1) / m.Rs;
+  m.sdt_b = stau_b; m.sdt_l = stau_t; m.sdt_d = 0;
+  m.sB_b = sB_b; m.sB_l = sB_l; m.sC_b = sC_b; m.sC_l = sC_l; m.sy_b = sy_b; m.sy_l = sy_t;
+  SiDims q;
+  q.svb = sv_b; q.svt = sv_t; q.smb = sm_b; q.smt = sm_t; q.sob = so_b; q.sot = so_t;
+  q.K = (int)K;
+  q.lf = ilog2(FTILE);
+  q.lvpt = q.lf - 2;
+  const bool has_d = p.D != nullptr;
+  if (dtype == TSSM_BF16) {
+    return disc == TSSM_DISC_ZOH
+               ? sel_interp_n<bf16_t, TSSM_DISC_ZOH>(N, has_d, V, M, tau, Vhat, p, m, q, s)
+               : sel_interp_n<bf16_t, TSSM_DISC_EULER>(N, has_d, V, M, tau, Vhat, p, m, q, s);
+  }
+  return disc == TSSM_DISC_ZOH
+             ? sel_interp_n<float, TSSM_DISC_ZOH>(N, has_d, V, M, tau, Vhat, p, m, q, s)
+             : sel_interp_n<float, TSSM_DISC_EULER>(N, has_d, V, M, tau, Vhat, p, m, q, s);
+}
 
 int64_t sel_chunk_steps(int64_t nbatch, int64_t L, int64_t Dc) {
   (void)nbatch;
@@ -623,3 +909,59 @@ int sel_chunked_launch(int dtype, int disc, bool dt_shared, bool tau, const SelP
 }
 
 }  // namespace tssm
+
+using namespace tssm;
+
+extern "C" int64_t tssm_interp_selective_scan_workspace_bytes(int64_t nbatch, int64_t T,
+                                                              int64_t F, int64_t N) {
+  const int64_t cb = sel_chunked_bytes(nbatch, T, F, N);
+  return cb > 0 ? cb : -1;
+}
+
+extern "C" int tssm_interp_selective_scan_supported(int dtype, int m_dtype, int tau_dtype,
+                                                    int64_t nbatch, int64_t T, int64_t F,
+                                                    int64_t N, int64_t K, int64_t FTILE,
+                                                    const void* M, int64_t sm_b,
+                                                    int64_t sm_t) {
+  return m_dtype == TSSM_F32 && tau_dtype == TSSM_F32 &&
+                 sel_interp_ok(dtype, nbatch, T, F, N, K, FTILE, M, sm_b, sm_t)
+             ? 1
+             : 0;
+}
+
+extern "C" int tssm_interp_selective_scan(int dtype, int disc, const void* V, const float* M,
+                                          const float* tau, const float* A_log, const void* B,
+                                          const void* C, const float* D, const float* h0,
+                                          void* Vhat, void* y, float* h_last, int64_t nbatch,
+                                          int64_t T, int64_t F, int64_t N, int64_t sv_b,
+                                          int64_t sv_t, int64_t sm_b, int64_t sm_t,
+                                          int64_t stau_b, int64_t stau_t, int64_t sB_b,
+                                          int64_t sB_l, int64_t sC_b, int64_t sC_l, int64_t so_b,
+                                          int64_t so_t, int64_t sy_b, int64_t sy_t, int64_t K,
+                                          int64_t FTILE, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(V && M && tau && A_log && B && C && Vhat && y, TSSM_ERR_NULL);
+  TSSM_CHECK(dtype == TSSM_F32 || dtype == TSSM_BF16, TSSM_ERR_DTYPE);
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nbatch > 0 && T > 0 && F > 0, TSSM_ERR_SHAPE);
+  const int64_t strides[] = {sv_b, sv_t, sm_b, sm_t, stau_b, stau_t, sB_b,
+                             sB_l, sC_b, sC_l, so_b, so_t, sy_b, sy_t};
+  for (int64_t st : strides) TSSM_CHECK(st >= 0, TSSM_ERR_STRIDE);
+  TSSM_CHECK(sel_interp_ok(dtype, nbatch, T, F, N, K, FTILE, M, sm_b, sm_t),
+             TSSM_ERR_UNSUPPORTED);
+  const int64_t vec = dtype == TSSM_F32 ? 4 : 8;
+  TSSM_CHECK(sB_b % vec == 0 && sB_l % vec == 0 && sC_b % vec == 0 && sC_l % vec == 0,
+             TSSM_ERR_ALIGN);
+  TSSM_CHECK(aligned(B, 16) && aligned(C, 16) && aligned(A_log, 16), TSSM_ERR_ALIGN);
+  const int64_t need = tssm_interp_selective_scan_workspace_bytes(nbatch, T, F, N);
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 16), TSSM_ERR_ALIGN);
+  SelPtrs p;
+  p.A_log = A_log; p.B = B; p.C = C; p.D = D; p.h0 = h0; p.y = y; p.h_last = h_last;
+  p.S = static_cast<float*>(workspace);
+  const int64_t nch = (T + sel_chunk_steps(nbatch, T, F) - 1) / sel_chunk_steps(nbatch, T, F);
+  p.T = p.S + nbatch * nch * F * N;
+  return sel_interp_launch(dtype, disc, V, M, tau, Vhat, p, nbatch, T, F, N, sv_b, sv_t, sm_b,
+                           sm_t, stau_b, stau_t, sB_b, sB_l, sC_b, sC_l, so_b, so_t, sy_b, sy_t,
+                           K, FTILE, as_stream(stream));
+}

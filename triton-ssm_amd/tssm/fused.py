@@ -324,6 +324,51 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
     return (y, h_last) if return_state else y
 
 
+def _interp_scan_fused(V, M, tau32, A_log, B, C, D, Vhat, K, FTILE, disc, h0, return_state):
+    """tssm_interp_selective_scan (the interpolation formed inside the scan's
+    first pass) when it supports the operands, else None."""
+    Bsz, T, F = V.shape
+    if B.dim() != 3 or B.shape[:2] != (Bsz, T) or C.shape != B.shape:
+        return None
+    N = B.shape[-1]
+    if (B.dtype != V.dtype or C.dtype != V.dtype or V.dtype not in (torch.float32, torch.bfloat16)
+            or M.dtype != torch.float32 or A_log.shape != (F, N)):
+        return None
+    L_ = _lib.lib()
+    code = dcode(V, "V")
+    if not L_.tssm_interp_selective_scan_supported(code, _lib.F32, _lib.F32, Bsz, T, F, N,
+                                                   int(K), int(FTILE), M.data_ptr(),
+                                                   M.stride(0), M.stride(1)):
+        return None
+    for t, w in ((A_log, "A_log"), (B, "B"), (C, "C")):
+        need_gpu(t, w)
+    _inner_unit(B, "B")
+    _inner_unit(C, "C")
+    A_log = as_f32(A_log, "A_log").contiguous()
+    if D is not None:
+        need_gpu(D, "D")
+        if D.numel() != F:
+            raise ValueError("D must have F elements")
+        D = as_f32(D, "D").contiguous()
+    if h0 is not None:
+        need_gpu(h0, "h0")
+        if tuple(h0.shape) != (Bsz, F, N):
+            raise ValueError("h0 must be [Bsz, F, N]")
+        h0 = as_f32(h0, "h0").contiguous()
+    y = torch.empty(Bsz, T, F, device=V.device, dtype=V.dtype)
+    h_last = torch.empty(Bsz, F, N, device=V.device, dtype=torch.float32) if return_state else None
+    ws, stream = _ws(L_.tssm_interp_selective_scan_workspace_bytes(Bsz, T, F, N), V,
+                     "interp_selective_scan", workspace.SSD)
+    _lib.call("tssm_interp_selective_scan", code, _disc_code(disc), V.data_ptr(), M.data_ptr(),
+              tau32.data_ptr(), A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), ptr(h0),
+              Vhat.data_ptr(), y.data_ptr(), ptr(h_last), Bsz, T, F, N, V.stride(0),
+              V.stride(1), M.stride(0), M.stride(1), tau32.stride(0), tau32.stride(1),
+              B.stride(0), B.stride(1), C.stride(0), C.stride(1), Vhat.stride(0),
+              Vhat.stride(1), y.stride(0), y.stride(1), int(K), int(FTILE), ws.data_ptr(),
+              ws.numel(), stream)
+    return (Vhat, y, h_last) if return_state else (Vhat, y)
+
+
 def fused_interp_ssm_forward(V, M, tau, A_log, B, C, D=None, *, K=10, FTILE=128, disc="zoh",
                              chunk=256, h0=None, return_state=False):
     """Interpolation of irregular observations followed by a Mamba-1 scan.
@@ -333,6 +378,10 @@ def fused_interp_ssm_forward(V, M, tau, A_log, B, C, D=None, *, K=10, FTILE=128,
     reference's time-aware interpolation (K, FTILE honoured); the scan then
     runs over channels F with dt_t = tau_t - tau_{t-1} (dt_0 = tau_0) computed
     in the scan's load stage.  Returns (Vhat, y[, h_last]).
+
+    Large problems with fp32 masks (tssm_interp_selective_scan_supported) form
+    Vhat inside the scan's first pass: written once, consumed there as x,
+    never read back.  Others run the interpolation kernel, then the scan.
     """
     for t, w in ((V, "V"), (M, "M"), (tau, "tau")):
         need_gpu(t, w)
@@ -343,6 +392,10 @@ def fused_interp_ssm_forward(V, M, tau, A_log, B, C, D=None, *, K=10, FTILE=128,
     _inner_unit(M, "M")
     Vhat = torch.empty(Bsz, T, F, device=V.device, dtype=V.dtype)
     tau32 = as_f32(tau, "tau").contiguous()
+    fused = _interp_scan_fused(V, M, tau32, A_log, B, C, D, Vhat, K, FTILE, disc, h0,
+                               return_state)
+    if fused is not None:
+        return fused
     nt = -(-F // int(FTILE))
     nbytes = _lib.lib().tssm_time_aware_interp_workspace_bytes(T, F, int(K), int(FTILE), Bsz, T, nt)
     ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=V.device)
