@@ -265,7 +265,7 @@ int64_t tssm_interp_selective_scan_workspace_bytes(int64_t nbatch, int64_t T, in
 int tssm_interp_selective_scan_supported(int dtype, int m_dtype, int tau_dtype, int64_t nbatch,
                                          int64_t T, int64_t F, int64_t N, int64_t K,
                                          int64_t FTILE, const void* M, int64_t sm_b,
-                                         int64_t sm_t);
+                                         int64_t sm_t, int64_t sv_t);
 int tssm_interp_selective_scan(int dtype, int disc, const void* V, const float* M,
                                const float* tau, const float* A_log, const void* B,
                                const void* C, const float* D, const float* h0, void* Vhat,

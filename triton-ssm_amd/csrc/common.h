@@ -212,6 +212,11 @@ template <int CTRL>
 __device__ inline float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
+// The value of lane i ^ 16 (within each 32-lane half), one ds_swizzle
+// (bitmask mode: and 0x1f, or 0, xor 0x10) without an address computation.
+__device__ inline float swizzle_xor16(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
 // Sum over aligned groups of G consecutive lanes (G a power of two <= 64; DPP
 // within rows of 16, lane shuffles beyond); every lane of the group receives
 // the sum.
@@ -240,6 +245,14 @@ __device__ inline float softplus_fast(float x) {
   const float r = __builtin_fmaf(e, e - 1.0f, 1.0f);
   const float lp = __builtin_fmaf(__builtin_amdgcn_logf(u), 0.6931471805599453f, -c * r);
   return fmaxf(x, 0.0f) + lp;
+}
+
+// Linear interpolation between a neighbour pair with weight w on the later
+// one, (1 - w) a + w b, in one fixed evaluation order (the product of the
+// earlier value rounded, then an fma): every interpolation kernel gives the
+// same bits whatever the compiler would contract.
+__device__ inline float lerp_pair(float a, float b, float w) {
+  return __builtin_fmaf(w, b, (1.0f - w) * a);
 }
 
 // clamp to [lo, hi] (lo <= hi) in one v_med3_f32

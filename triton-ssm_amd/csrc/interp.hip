@@ -303,7 +303,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_kernel(InterpArgs a) {
       Lanes<TV, E> o;
 #pragma unroll
       for (int j = 0; j < E; ++j)
-        o.v[j] = mode[u] == 3 ? (1.0f - wt[u]) * vp[u].v[j] + wt[u] * vn[u].v[j] : vp[u].v[j];
+        o.v[j] = mode[u] == 3 ? lerp_pair(vp[u].v[j], vn[u].v[j], wt[u]) : vp[u].v[j];
       o.store(O + ot[u] * a.sot + of[u]);
     }
   }
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_fused_kernel(InterpArgs
       Lanes<TV, E> o;
 #pragma unroll
       for (int j = 0; j < E; ++j)
-        o.v[j] = mode[u] == 3 ? (1.0f - wt[u]) * vp[u].v[j] + wt[u] * vn[u].v[j] : vp[u].v[j];
+        o.v[j] = mode[u] == 3 ? lerp_pair(vp[u].v[j], vn[u].v[j], wt[u]) : vp[u].v[j];
       o.store(O + ot[u] * a.sot + of[u]);
     }
   }
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_step_kernel(StepArgs a)
   for (int64_t f = f0 + tid; f < f1; f += kInterpThreads) {
     float v;
     if (prev >= 0 && next >= 0)
-      v = (1.0f - w) * ldf(V + prev * a.svt + f) + w * ldf(V + next * a.svt + f);
+      v = lerp_pair(ldf(V + prev * a.svt + f), ldf(V + next * a.svt + f), w);
     else if (prev >= 0)
       v = ldf(V + prev * a.svt + f);
     else if (next >= 0)
@@ -586,7 +586,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_step_fast_kernel(StepAr
     float w = den > 1e-9f ? (s_tau[K] - tp) / den : 0.5f;
     w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
     const float vp = ldf(V + (a.t_cur - kp) * a.svt), vn = ldf(V + (a.t_cur + kn) * a.svt);
-    v = (1.0f - w) * vp + w * vn;
+    v = lerp_pair(vp, vn, w);
   } else if (kp > 0) {
     v = ldf(V + (a.t_cur - kp) * a.svt);
   } else if (kn > 0) {
@@ -645,7 +645,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_corrected_kernel(Interp
         const float tp = s_tau[i - kp], tn = s_tau[i + kn], den = tn - tp;
         float w = den > 1e-9f ? (s_tau[i] - tp) / den : 0.5f;
         w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
-        v = (1.0f - w) * ldf(V + (t - kp) * a.svt) + w * ldf(V + (t + kn) * a.svt);
+        v = lerp_pair(ldf(V + (t - kp) * a.svt), ldf(V + (t + kn) * a.svt), w);
       } else if (kp > 0) {
         v = ldf(V + (t - kp) * a.svt);
       } else if (kn > 0) {
@@ -757,7 +757,7 @@ __global__ __launch_bounds__(kInterpThreads) void interp_corrected_staged_kernel
       const float tp = s_tau[i - kp], tn = s_tau[i + kn], den = tn - tp;
       float w = den > 1e-9f ? (s_tau[i] - tp) * __builtin_amdgcn_rcpf(den) : 0.5f;
       w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
-      return (1.0f - w) * s_v[i - kp][lane] + w * s_v[i + kn][lane];
+      return lerp_pair(s_v[i - kp][lane], s_v[i + kn][lane], w);
     }
     return kp > 0 ? s_v[i - kp][lane] : (kn > 0 ? s_v[i + kn][lane] : s_v[i][lane]);
   };

@@ -66,8 +66,8 @@ int sel_chunked_launch(int dtype, int disc, bool dt_shared, bool tau, const SelP
 // Whether the interpolation can be formed inside pass 1 (sel_interp_launch):
 // fp32/bf16 I/O, N 8 or 16, fp32 masks in 16-byte rows, FTILE a power of two
 // in [16, 256], 1 <= K <= 64, F a multiple of 4, a problem the three passes
-// take.
+// take, V's row stride small enough for 32-bit row offsets within a chunk.
 bool sel_interp_ok(int dtype, int64_t nbatch, int64_t T, int64_t F, int64_t N, int64_t K,
-                   int64_t FTILE, const void* M, int64_t sm_b, int64_t sm_t);
+                   int64_t FTILE, const void* M, int64_t sm_b, int64_t sm_t, int64_t sv_t);
 
 }  // namespace tssm

@@ -550,7 +550,7 @@ __device__ inline float round_io(float v) {
   else return bf16_bits_to_f32((uint16_t)f32_to_bf16_bits(v));
 }
 
-constexpr int kSiMaskU = 7;  // mask rows per wave in flight
+constexpr int kSiMaskU = 13;  // mask rows per wave in flight (one batch at K = 10)
 
 template <typename T, int DISC, int NST, bool HAS_D>
 __global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
@@ -573,12 +573,17 @@ __global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
   __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
   __shared__ float sD[kSelChunkSteps];
   __shared__ float sTau[kSiRows];
-  __shared__ unsigned char sObs[kSiRows * kSiMaxTiles];
-  __shared__ int sPrev[kSelChunkSteps * kSiMaxTiles], sNext[kSelChunkSteps * kSiMaxTiles];
-  __shared__ float sW[kSelChunkSteps * kSiMaxTiles];
+  // per flag row: the ballot of the row's tile sums > 0.5 over the lanes
+  // (lanes of one tile hold the same sum; bit lt << lvpt is tile lt's flag)
+  __shared__ uint64_t sRowB[kSiRows];
+  // per (step, tile): byte offsets of the rows read as "prev" and "next" from
+  // the row t0-K of the lane's column, and the weight (-1: no pair, vhat is
+  // the "prev" row's value)
+  __shared__ int4 sNb[kSelChunkSteps * kSiMaxTiles];
 
   // ---- 1. prologue loads: rows to stage, timestamps, lane parameters, and
   // the first batch of mask rows, before one wait
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float4 vB = stage_row_load<T, NST>(Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
   const float4 vC = stage_row_load<T, NST>(Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
   const float* taub = tau + b * m.sdt_b;
@@ -590,28 +595,53 @@ __global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
   float al[NST];
   load_alog<NST>(A_log, dc, al);
   float Dd = HAS_D ? D[dc] : 0.0f;
-  const float* Mb = M + b * q.smb + cb0 + 4 * lane;
+  // wave wv sums rows wv, wv+4, ...: a uniform row pointer, lane l the
+  // 16-byte vector of channels cb0+4l .. cb0+4l+3 (rows outside [0, L) and
+  // vectors past F read a valid vector and count 0)
   const bool vec_ok = cb0 + 4 * lane < m.Dc;  // F = Dc, a multiple of 4
   const int vpt = 1 << q.lvpt;
-  for (int i0 = wave; i0 < R; i0 += 4 * kSiMaskU) {
+  for (int i0 = wv; i0 < R; i0 += 4 * kSiMaskU) {
     float sv[kSiMaskU];
 #pragma unroll
     for (int u = 0; u < kSiMaskU; ++u) {
       const int i = i0 + 4 * u;
       const int64_t t = t0 - K + i;
-      const bool rok = i < R && t >= 0 && t < m.L && vec_ok;
-      const float4 v = *reinterpret_cast<const float4*>(rok ? Mb + t * q.smt : M);
+      const bool rok = i < R && t >= 0 && t < m.L;
+      const float* rowp = M + b * q.smb + (rok ? t : 0) * q.smt + cb0;
+      const float4 v = *reinterpret_cast<const float4*>(rowp + (vec_ok ? 4 * lane : 0));
       float sum = 0.0f;
       sum += v.x; sum += v.y; sum += v.z; sum += v.w;
-      sv[u] = rok ? sum : 0.0f;
+      sv[u] = rok && vec_ok ? sum : 0.0f;
+    }
+    // The tile sum over its vpt lanes, level by level across the rows (the
+    // rows' exchanges overlap).  Each level adds the partner group's sum, the
+    // value the xor butterfly of interp_fused_kernel adds (after a level all
+    // lanes of a group hold the same sum), so the flags are that kernel's.
+#pragma unroll
+    for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0xB1>(sv[u]);   // xor 1
+#pragma unroll
+    for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0x4E>(sv[u]);   // xor 2
+    if (vpt >= 8) {
+#pragma unroll
+      for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0x141>(sv[u]);  // the other quad
+    }
+    if (vpt >= 16) {
+#pragma unroll
+      for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0x140>(sv[u]);  // the other 8
+    }
+    if (vpt >= 32) {
+#pragma unroll
+      for (int u = 0; u < kSiMaskU; ++u) sv[u] += swizzle_xor16(sv[u]);
+    }
+    if (vpt >= 64) {
+#pragma unroll
+      for (int u = 0; u < kSiMaskU; ++u) sv[u] += __shfl_xor(sv[u], 32);
     }
 #pragma unroll
     for (int u = 0; u < kSiMaskU; ++u) {
       const int i = i0 + 4 * u;  // uniform per wave
-      float x = sv[u];
-      for (int o = 1; o < vpt; o <<= 1) x += __shfl_xor(x, o);
-      if (i < R && (lane & (vpt - 1)) == 0)
-        sObs[i * kSiMaxTiles + (lane >> q.lvpt)] = x > 0.5f ? 1 : 0;
+      const uint64_t bb = __ballot(sv[u] > 0.5f);
+      if (i < R && lane == 0) sRowB[i] = bb;
     }
   }
   stage_row_store<NST>(sB, vB, n4);
@@ -633,25 +663,52 @@ __global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
     const int64_t t = t0 + tid;
     sD[tid] = tid < n ? sTau[tid + K] - (t > 0 ? sTau[tid + K - 1] : 0.0f) : 0.0f;
   }
+  // Wave wv takes tiles wv, wv+4, ...: three ballots give the tile's flags of
+  // rows 0..191 (bit i: row t0-K+i) as uniform words, then lane r < n4 finds
+  // step r's neighbours with bit scans: the highest flagged row of
+  // [r, r+K-1] (prev) and the lowest of [r+K+1, r+2K] (next), row r+K being
+  // the step itself.
   const int ntl = kSelThreads >> q.lf;
-  for (int it = tid; it < n4 * ntl; it += kSelThreads) {
-    const int r = it / ntl, lt = it - r * ntl;
-    const int rr = r < n ? r : n - 1;
-    const int64_t t = t0 + rr;
-    int prev = -1, next = -1;
-    for (int k = 1; k <= K; ++k)
-      if (prev < 0 && sObs[(rr + K - k) * kSiMaxTiles + lt]) prev = (int)(t - k);
-    for (int k = 1; k <= K; ++k)
-      if (next < 0 && sObs[(rr + K + k) * kSiMaxTiles + lt]) next = (int)(t + k);
-    const float tau_t = sTau[rr + K];
-    const float tp = prev >= 0 ? sTau[rr + K - (int)(t - prev)] : 0.0f;
-    const float tn = next >= 0 ? sTau[rr + K + (int)(next - t)] : 0.0f;
-    const float den = tn - tp;
-    float w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
-    w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
-    sPrev[r * kSiMaxTiles + lt] = prev;
-    sNext[r * kSiMaxTiles + lt] = next;
-    sW[r * kSiMaxTiles + lt] = w;
+  const uint64_t kmask = K >= 64 ? ~0ull : ((1ull << K) - 1);
+  for (int lt = wv; lt < ntl; lt += 4) {
+    const int bit = lt << q.lvpt;
+    uint64_t mw[3];
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      const int i = g * 64 + lane;
+      mw[g] = __ballot(i < R && ((sRowB[i < R ? i : 0] >> bit) & 1ull));
+    }
+    if (lane < n4) {
+      const int rr = lane < n ? lane : n - 1;
+      const int64_t t = t0 + rr;
+      // 64 flag bits starting at row s (rows past 191 read 0)
+      auto bits64 = [&](int s) -> uint64_t {
+        const int g = s >> 6, sh = s & 63;
+        const uint64_t lo = g == 0 ? mw[0] : (g == 1 ? mw[1] : (g == 2 ? mw[2] : 0ull));
+        const uint64_t hi = g == 0 ? mw[1] : (g == 1 ? mw[2] : 0ull);
+        return sh == 0 ? lo : ((lo >> sh) | (hi << (64 - sh)));
+      };
+      const uint64_t wp = bits64(rr) & kmask;
+      const uint64_t wn = bits64(rr + K + 1) & kmask;
+      const int prev = wp ? (int)(t - K + (63 - __builtin_clzll(wp))) : -1;
+      const int next = wn ? (int)(t + 1 + __builtin_ctzll(wn)) : -1;
+      const float tau_t = sTau[rr + K];
+      const float tp = prev >= 0 ? sTau[rr + K - (int)(t - prev)] : 0.0f;
+      const float tn = next >= 0 ? sTau[rr + K + (int)(next - t)] : 0.0f;
+      const float den = tn - tp;
+      float w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
+      w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+      // rows read as "prev" and "next" (as interp_kernel: v_prev, else
+      // v_next, else v_cur; next falls back to the prev row), as byte offsets
+      // from row t0-K (both rows lie in [t0-K, t0+n+K): the host bounds
+      // (n+2K) row strides below 2^31 bytes)
+      const int64_t rp = prev >= 0 ? prev : (next >= 0 ? next : t);
+      const int64_t rn = next >= 0 ? next : rp;
+      const int64_t rs = q.svt * (int64_t)sizeof(T);
+      sNb[lane * kSiMaxTiles + lt] =
+          make_int4((int)((rp - (t0 - K)) * rs), (int)((rn - (t0 - K)) * rs),
+                    __float_as_int(prev >= 0 && next >= 0 ? w : -1.0f), 0);
+    }
   }
   __syncthreads();
   // Waves whose lanes are all past Dc are done (no barrier follows).
@@ -659,38 +716,46 @@ __global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
 
   // ---- 3. the recurrence over interpolated inputs
   const int lt = (int)((dc - cb0) >> q.lf);  // the lane's tile (of channel dc)
-  const T* vcol = V + b * q.svb + dc;
+  // row t0-K of the workgroup's first channel (uniform; for the first chunk
+  // it lies before V's row 0, and only rows >= 0 are read from it)
+  const char* vbase =
+      reinterpret_cast<const char*>(V + b * q.svb + (t0 - K) * q.svt + cb0);
+  const uint32_t lboff = (uint32_t)((dc - cb0) * (int64_t)sizeof(T));
   T* ocol = Vhat + b * q.sob + dc;
   T* yp = y + b * m.sy_b + dc;
-  // rows read as "prev" and "next" for table row r (as interp_kernel: v_prev,
-  // else v_next, else v_cur; next falls back to the prev row)
-  auto fetch = [&](int r, float& vp, float& vn) {
-    const int pv = sPrev[r * kSiMaxTiles + lt], nx = sNext[r * kSiMaxTiles + lt];
-    const int64_t rp = pv >= 0 ? pv : (nx >= 0 ? nx : t0 + (r < n ? r : n - 1));
-    const int64_t rn = nx >= 0 ? nx : rp;
-    vp = ldf(vcol + rp * q.svt);
-    vn = ldf(vcol + rn * q.svt);
+  // the pair of a table entry, and its weight
+  auto fetch = [&](const int4& e, float& vp, float& vn, float& w) {
+    vp = ldf(reinterpret_cast<const T*>(vbase + ((uint32_t)e.x + lboff)));
+    vn = ldf(reinterpret_cast<const T*>(vbase + ((uint32_t)e.y + lboff)));
+    w = __int_as_float(e.z);
   };
-  float vp[kSelPf], vn[kSelPf];
+  float vp[kSelPf], vn[kSelPf], wq[kSelPf];
 #pragma unroll
-  for (int j = 0; j < kSelPf; ++j) fetch(j < n4 ? j : n4 - 1, vp[j], vn[j]);
+  for (int j = 0; j < kSelPf; ++j) fetch(sNb[(j < n4 ? j : n4 - 1) * kSiMaxTiles + lt], vp[j], vn[j], wq[j]);
+  // dt one step ahead (the step's exp2s need only dt, so the B and C rows,
+  // read at the top of the step, arrive while they issue); the neighbour
+  // entry for step rr + 4 is read at the top too, used at the end
+  float dtc = sD[0];
   float sdt = 0.0f;
   for (int r = 0; r < n4; r += kSelPf) {
 #pragma unroll
     for (int j = 0; j < kSelPf; ++j) {
       const int rr = r + j;
-      const int ix = rr * kSiMaxTiles + lt;
-      const int mode = (sPrev[ix] >= 0 ? 1 : 0) | (sNext[ix] >= 0 ? 2 : 0);
-      const float w = sW[ix];
-      const float vh = mode == 3 ? (1.0f - w) * vp[j] + w * vn[j] : vp[j];
-      const float u = round_io<T>(vh);  // the scan consumes Vhat as stored
-      const float dtv = sD[rr];
-      const int64_t tw = t0 + (rr < n ? rr : n - 1);
+      const int r1 = rr + 1 < n4 ? rr + 1 : n4 - 1;
+      const int r4 = rr + kSelPf < n4 ? rr + kSelPf : n4 - 1;
       float Bv[NST], Cv[NST];
       lds_row<NST>(sB + rr * NST, Bv);
       lds_row<NST>(sC + rr * NST, Cv);
-      sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
-      sdt += dtv;
+      const float dtn = sD[r1];
+      const int4 e4 = sNb[r4 * kSiMaxTiles + lt];
+      __builtin_amdgcn_sched_barrier(0);  // the step's LDS reads issue first
+      // both forms computed, then a select (no branch around the loads' waits)
+      const float li = lerp_pair(vp[j], vn[j], wq[j]);
+      const float vh = wq[j] >= 0.0f ? li : vp[j];
+      const float u = round_io<T>(vh);  // the scan consumes Vhat as stored
+      const int64_t tw = t0 + (rr < n ? rr : n - 1);
+      sel_update<DISC, NST>(h, a2, nia, Bv, u, dtc);
+      sdt += dtc;
       float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
 #pragma unroll
       for (int k = 0; k < NST; k += 2) {
@@ -701,10 +766,10 @@ __global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
       // channel Dc-1) store exactly the values of step n-1 / channel Dc-1
       stf(ocol + tw * q.sot, vh);
       stf(yp + tw * m.sy_l, acc0 + acc1);
+      dtc = dtn;
       // refill the registers this step used, for step rr + 4
       __builtin_amdgcn_sched_barrier(0);
-      const int rn = rr + kSelPf < n4 ? rr + kSelPf : n4 - 1;
-      fetch(rn, vp[j], vn[j]);
+      fetch(e4, vp[j], vn[j], wq[j]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -820,11 +885,12 @@ int ilog2(int64_t v) {
 }  // namespace
 
 bool sel_interp_ok(int dtype, int64_t nbatch, int64_t T, int64_t F, int64_t N, int64_t K,
-                   int64_t FTILE, const void* M, int64_t sm_b, int64_t sm_t) {
+                   int64_t FTILE, const void* M, int64_t sm_b, int64_t sm_t, int64_t sv_t) {
   const bool pow2 = FTILE > 0 && (FTILE & (FTILE - 1)) == 0;
   const int64_t rs = sel_chunk_steps(nbatch, T, F);
   return (dtype == TSSM_F32 || dtype == TSSM_BF16) && (N == 8 || N == 16) && rs > 0 &&
          pow2 && FTILE >= 16 && FTILE <= kSelThreads && K >= 1 && K <= kSiMaxK && F > 0 &&
+         sv_t >= 0 && (kSelChunkSteps + 2 * K) * sv_t * (dtype == TSSM_F32 ? 4 : 2) < INT32_MAX &&
          F % 4 == 0 && sm_b % 4 == 0 && sm_t % 4 == 0 && sm_b >= 0 && sm_t >= 0 &&
          aligned(M, 16) && nbatch > 0 && nbatch <= 65535 &&
          nbatch * ((F + 63) / 64) * ((T + rs - 1) / rs) >= kSelMinWaves;
@@ -921,10 +987,10 @@ extern "C" int64_t tssm_interp_selective_scan_workspace_bytes(int64_t nbatch, in
 extern "C" int tssm_interp_selective_scan_supported(int dtype, int m_dtype, int tau_dtype,
                                                     int64_t nbatch, int64_t T, int64_t F,
                                                     int64_t N, int64_t K, int64_t FTILE,
-                                                    const void* M, int64_t sm_b,
-                                                    int64_t sm_t) {
+                                                    const void* M, int64_t sm_b, int64_t sm_t,
+                                                    int64_t sv_t) {
   return m_dtype == TSSM_F32 && tau_dtype == TSSM_F32 &&
-                 sel_interp_ok(dtype, nbatch, T, F, N, K, FTILE, M, sm_b, sm_t)
+                 sel_interp_ok(dtype, nbatch, T, F, N, K, FTILE, M, sm_b, sm_t, sv_t)
              ? 1
              : 0;
 }
@@ -947,7 +1013,7 @@ extern "C" int tssm_interp_selective_scan(int dtype, int disc, const void* V, co
   const int64_t strides[] = {sv_b, sv_t, sm_b, sm_t, stau_b, stau_t, sB_b,
                              sB_l, sC_b, sC_l, so_b, so_t, sy_b, sy_t};
   for (int64_t st : strides) TSSM_CHECK(st >= 0, TSSM_ERR_STRIDE);
-  TSSM_CHECK(sel_interp_ok(dtype, nbatch, T, F, N, K, FTILE, M, sm_b, sm_t),
+  TSSM_CHECK(sel_interp_ok(dtype, nbatch, T, F, N, K, FTILE, M, sm_b, sm_t, sv_t),
              TSSM_ERR_UNSUPPORTED);
   const int64_t vec = dtype == TSSM_F32 ? 4 : 8;
   TSSM_CHECK(sB_b % vec == 0 && sB_l % vec == 0 && sC_b % vec == 0 && sC_l % vec == 0,

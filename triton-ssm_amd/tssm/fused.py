@@ -338,7 +338,7 @@ def _interp_scan_fused(V, M, tau32, A_log, B, C, D, Vhat, K, FTILE, disc, h0, re
     code = dcode(V, "V")
     if not L_.tssm_interp_selective_scan_supported(code, _lib.F32, _lib.F32, Bsz, T, F, N,
                                                    int(K), int(FTILE), M.data_ptr(),
-                                                   M.stride(0), M.stride(1)):
+                                                   M.stride(0), M.stride(1), V.stride(1)):
         return None
     for t, w in ((A_log, "A_log"), (B, "B"), (C, "C")):
         need_gpu(t, w)
