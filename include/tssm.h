@@ -330,6 +330,39 @@ int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt, const flo
                   int64_t sC_l, int64_t sC_h, int64_t sy_b, int64_t sy_l, int64_t sy_h,
                   int64_t chunk, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* tssm_ssd_scan in one launch for bf16 x/B/C/y, P = 64, N = 16 and 256-step
+ * chunks (the matrix-core tile passes' case): a wave takes one segment of a
+ * (batch, head) row (one or two 256-step tiles), sweeps it last sub-chunk
+ * first for its end state (x, B, dt through the caches), publishes its carry
+ * as tagged look-back words, resolves its entry state by a decoupled
+ * look-back over the row's earlier segments (a decay product of exactly zero
+ * ends a walk), and sweeps the segment again forward for the outputs, so
+ * that what it reads a second time is still in the last-level cache.  Same
+ * arguments and results as tssm_ssd_scan (D f32 [H*P] or NULL; h0/h_last f32
+ * [B,H,P,N] contiguous or NULL); the workspace is a look-back workspace
+ * (zero-filled once, epoch-tagged words, tssm_workspace_error reads its
+ * sticky word) of tssm_ssd_scan_fused_workspace_bytes() bytes.
+ * tssm_ssd_scan_fused_supported() says whether these operands take it (else
+ * the call returns TSSM_ERR_UNSUPPORTED before any launch). */
+int64_t tssm_ssd_scan_fused_workspace_bytes(int64_t nbatch, int64_t L, int64_t H, int64_t P,
+                                            int64_t N, int64_t chunk);
+int tssm_ssd_scan_fused_supported(int dtype, const void* x, const float* dt, const float* A_log,
+                                  const void* B, const void* C, const float* D, const float* h0,
+                                  void* y, float* h_last, int64_t nbatch, int64_t L, int64_t H,
+                                  int64_t P, int64_t N, int64_t sx_b, int64_t sx_l, int64_t sx_h,
+                                  int64_t sdt_b, int64_t sdt_l, int64_t sdt_h, int64_t sB_b,
+                                  int64_t sB_l, int64_t sB_h, int64_t sC_b, int64_t sC_l,
+                                  int64_t sC_h, int64_t sy_b, int64_t sy_l, int64_t sy_h,
+                                  int64_t chunk);
+int tssm_ssd_scan_fused(int dtype, int disc, const void* x, const float* dt, const float* A_log,
+                        const void* B, const void* C, const float* D, const float* h0, void* y,
+                        float* h_last, int64_t nbatch, int64_t L, int64_t H, int64_t P,
+                        int64_t N, int64_t sx_b, int64_t sx_l, int64_t sx_h, int64_t sdt_b,
+                        int64_t sdt_l, int64_t sdt_h, int64_t sB_b, int64_t sB_l, int64_t sB_h,
+                        int64_t sC_b, int64_t sC_l, int64_t sC_h, int64_t sy_b, int64_t sy_l,
+                        int64_t sy_h, int64_t chunk, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
 /* One streaming SSD step for S independent streams with the state
  * [S,H,P,N] f32 resident in HBM and updated in place (the per-stream,
  * per-head generalisation of streaming_ssm_inplace_kernel,

@@ -181,6 +181,55 @@ def test_ssd_long_sequence_shape(dev):
     tssm.check(dev)
 
 
+@pytest.mark.parametrize("decay,L,Bsz,H,with_d", [
+    ("slow", 20000, 1, 2, False),    # no segment forgets: walks fold many aggregates
+    ("slow", 70001, 2, 3, True),     # more than 64 segments per row, ragged end, skip term
+    ("mixed", 205006, 2, 8, False),  # two-tile segments, forgetting and slow heads together
+])
+def test_ssd_scan_fused_lookback(dev, decay, L, Bsz, H, with_d):
+    """The one-launch SSD kernel (reverse first sweep, decoupled look-back,
+    forward second sweep) against the three tile passes on the same inputs,
+    and two heads against the float64 oracle over every step.  Slow decays
+    (decay product of a segment far from zero) make every segment publish an
+    aggregate and the walks fold long chains, beyond one 64-segment status
+    window; "mixed" gives half the heads decays that underflow to exactly
+    zero (inclusive state published at once) and half slow ones.  h0 and the
+    final state are checked too."""
+    import tssm
+    from tssm import ssd_scan_forward
+    g = torch.Generator().manual_seed(L + H)
+    x = torch.randn(Bsz, L, H, 64, generator=g).to(torch.bfloat16)
+    Bm = (torch.randn(Bsz, L, H, 16, generator=g) / 4).to(torch.bfloat16)
+    Cm = (torch.randn(Bsz, L, H, 16, generator=g) / 4).to(torch.bfloat16)
+    slow = torch.full((H,), np.log(0.02))
+    if decay == "slow":
+        A_log = slow
+        dt = torch.rand(Bsz, L, H, generator=g) * 0.02
+    else:
+        A_log = torch.where(torch.arange(H) % 2 == 0, torch.full((H,), np.log(8.0)), slow)
+        dt = torch.exp(torch.randn(Bsz, L, H, generator=g) * 1.5 - 3.0)
+    D = torch.randn(H * 64, generator=g) if with_d else None
+    h0 = torch.randn(Bsz, H, 64, 16, generator=g)
+    d = {k: v.to(dev) for k, v in dict(x=x, B=Bm, C=Cm, A_log=A_log, dt=dt, h0=h0).items()}
+    Dd = D.to(dev) if with_d else None
+    y, h = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], Dd, chunk=256,
+                            h0=d["h0"], return_state=True)
+    y3, h3 = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], Dd, chunk=256,
+                              h0=d["h0"], return_state=True, fused=False)
+    torch.cuda.synchronize()
+    tssm.check(dev)
+    assert_close(y, y3, 4e-3, f"fused vs three passes, y ({decay})")
+    assert_close(h, h3, 1e-4, f"fused vs three passes, final state ({decay})")
+    heads = [0, H - 1]
+    sl = (slice(Bsz - 1, Bsz), slice(None), heads)
+    y_ref, h_ref = O.ssd_scan(x[sl], dt[sl], A_log[heads], Bm[sl], Cm[sl],
+                              None if D is None else D.view(H, 64)[heads],
+                              h0=np64(h0[Bsz - 1:, heads]))
+    e = assert_close(y[sl], y_ref, 4e-3, f"fused y vs oracle ({decay})")
+    assert_close(h[Bsz - 1:, heads], h_ref, 1e-3, f"fused final state vs oracle ({decay})")
+    print(f"ssd fused look-back {decay} L={L}: relerr {e:.2e}")
+
+
 @pytest.mark.parametrize("L", [65499, 205006])
 def test_ssd_scan_multi_tile_segments(dev, L):
     """bf16 P=64 N=16 with 16 rows: the matrix-core passes walk one

@@ -23,6 +23,7 @@
 // ssd_stream_step_kernel: one streaming step with the state [S,H,P,N] fp32
 //   resident in HBM, updated in place; one workgroup per (stream, head).
 #include "common.h"
+#include "lookback.h"
 
 namespace tssm {
 
@@ -528,10 +529,14 @@ struct WaveTile {
     od = (uint32_t)((lane & 31) * bd);
     return true;
   }
+  // XPOL: cache policy of the x loads (non-temporal by default: a pass that
+  // reads x once; the fused kernel's first sweep reads it through the caches
+  // for its second sweep)
+  template <int XPOL = kBufNt>
   __device__ void load(int r0, u32x4* xr, u32x2* bq, float& dtv) const {
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      xr[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)ox, (r0 + k) * bx, kBufNt);
+      xr[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)ox, (r0 + k) * bx, XPOL);
 #pragma unroll
     for (int sg = 0; sg < 2; ++sg)
       bq[sg] = __builtin_amdgcn_raw_buffer_load_b64(rB, (int)oB, (r0 + 16 * sg) * bB, 0);
@@ -658,24 +663,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
   if (lane == 0) a.chunkA[(int64_t)wt.row * a.nchunks + wt.c] = exp2_fast(ltot);
 }
 
-// Pass 3: outputs of each tile from its entry state.
-template <int DISC, bool HAS_D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_out_wave_kernel(SsdArgs a, uint32_t ngroups) {
-  __shared__ __align__(16) uint16_t s_xt[kWaveRows][kWxElems];
-  __shared__ __align__(16) uint16_t s_b[kWaveRows][kWsub * kWbRow];
-  __shared__ __align__(16) float s_sc[kWaveRows][3][kWsub];  // cum, coef, w
-  __shared__ __align__(16) uint16_t s_xr[HAS_D ? kWaveRows : 1][HAS_D ? kWsub * kMp : 4];
-  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+// LDS of one wave in the output sweep.
+struct WaveOutLds {
+  uint16_t* xt;   // x^T, then the staged y rows
+  uint16_t* bs;   // B rows
+  float* scum;    // per-step scalars: inclusive log2 decay, coefficient, weight
+  float* scoef;
+  float* sw;
+  uint16_t* xrow; // row-major x (skip term)
+};
+
+// Outputs of one wave's segment from its entry state `st` (the state
+// advances through the segment; the lane holds H[16 pi + c16][4q..4q+3]).
+// XPOL: cache policy of the x loads.
+template <int DISC, bool HAS_D, int XPOL = kBufNt>
+__device__ inline void wave_out_sweep(const SsdArgs& a, const WaveTile& wt, f32x4* st,
+                                      const WaveOutLds& ld, float a2, int lane) {
   const int c16 = lane & 15, q = lane >> 4, g8 = lane & 7, sq = lane >> 3;
-  WaveTile wt;
-  if (!wt.init(a, ngroups, wv, lane)) return;  // whole waves; no barriers below
-  uint16_t* xt = s_xt[wv];
-  uint16_t* bs = s_b[wv];
-  float* scum = s_sc[wv][0];
-  float* scoef = s_sc[wv][1];
-  float* sw = s_sc[wv][2];
-  uint16_t* xrow = s_xr[HAS_D ? wv : 0];
-  const float a2 = -expf(a.A_log[wt.h]) * kLog2e;
+  uint16_t* xt = ld.xt;
+  uint16_t* bs = ld.bs;
+  float* scum = ld.scum;
+  float* scoef = ld.scoef;
+  float* sw = ld.sw;
+  uint16_t* xrow = ld.xrow;
   const int64_t nrow = (wt.tbeg + a.tc < a.L ? wt.tbeg + a.tc : a.L) - wt.tbeg;
   const uint16_t* Cb =
       reinterpret_cast<const uint16_t*>(a.C) + wt.b * a.sC_b + wt.h * a.sC_h + wt.tbeg * a.sC_l;
@@ -692,21 +702,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
   // (a streaming hint let them be evicted between the waves' reads: 20% more
   // bytes fetched)
   auto load_sub = [&](int r0) {  // r0: first row of the sub-chunk, from the tile start
-    wt.load(r0, xr, bq, dtv);
+    wt.template load<XPOL>(r0, xr, bq, dtv);
 #pragma unroll
     for (int sg = 0; sg < 2; ++sg)
       cq[sg] = __builtin_amdgcn_raw_buffer_load_b64(rC, (int)oC, (r0 + 16 * sg) * bC, 0);
   };
   load_sub(0);
-
-  // state entering the tile: lane holds H[16 pi + c16][4q..4q+3]
-  f32x4 st[4];
-  {
-    const float* en = a.entry + ((int64_t)wt.row * a.nchunks + wt.c) * (kMp * kMn);
-#pragma unroll
-    for (int pi = 0; pi < 4; ++pi)
-      st[pi] = *reinterpret_cast<const f32x4*>(en + (16 * pi + c16) * kMn + 4 * q);
-  }
   float dsk[4][4];
   if constexpr (HAS_D) {
 #pragma unroll
@@ -809,6 +810,269 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
       __builtin_amdgcn_raw_buffer_store_b128(v, ry, (int)oy, (r0 + 8 * i) * by, kBufNt);
     }
   }
+}
+
+
+// Pass 3: outputs of each tile from its entry state.
+template <int DISC, bool HAS_D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_out_wave_kernel(SsdArgs a, uint32_t ngroups) {
+  __shared__ __align__(16) uint16_t s_xt[kWaveRows][kWxElems];
+  __shared__ __align__(16) uint16_t s_b[kWaveRows][kWsub * kWbRow];
+  __shared__ __align__(16) float s_sc[kWaveRows][3][kWsub];  // cum, coef, w
+  __shared__ __align__(16) uint16_t s_xr[HAS_D ? kWaveRows : 1][HAS_D ? kWsub * kMp : 4];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, q = lane >> 4;
+  WaveTile wt;
+  if (!wt.init(a, ngroups, wv, lane)) return;  // whole waves; no barriers below
+  const WaveOutLds ld{s_xt[wv], s_b[wv], s_sc[wv][0], s_sc[wv][1], s_sc[wv][2],
+                      s_xr[HAS_D ? wv : 0]};
+  const float a2 = -expf(a.A_log[wt.h]) * kLog2e;
+  // state entering the tile: lane holds H[16 pi + c16][4q..4q+3]
+  f32x4 st[4];
+  {
+    const float* en = a.entry + ((int64_t)wt.row * a.nchunks + wt.c) * (kMp * kMn);
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi)
+      st[pi] = *reinterpret_cast<const f32x4*>(en + (16 * pi + c16) * kMn + 4 * q);
+  }
+  wave_out_sweep<DISC, HAS_D>(a, wt, st, ld, a2, lane);
+}
+
+// ---------------------------------------------------------------- fused tile kernel
+// One launch in place of the three tile passes (chunk states, state passing,
+// outputs): a wave takes one (row, segment) and
+//  1. sweeps the segment's 32-step sub-chunks LAST TO FIRST, accumulating the
+//     segment's end state from zero with each sub-chunk's weights taken to
+//     the segment end, H^T += sum_s 2^(lsum + cumE - cum_s) coef_s B_s x_s
+//     (lsum: the log2 decay of the later sub-chunks) -- the products of pass
+//     1, in reverse order -- and stops where the decay from the segment end
+//     has underflowed to exactly zero (the earlier steps add exact zeros);
+//  2. publishes the segment's carry as tagged look-back words (its end state
+//     from zero and decay product, or, when the decay product is exactly
+//     zero, its inclusive state -- the end state itself -- at once);
+//  3. resolves its entry state by a decoupled look-back over the segments of
+//     its row (ssd_lookback), publishes its inclusive state;
+//  4. sweeps the segment forward from the entry state, forming the outputs
+//     (wave_out_sweep, the products of pass 3).
+// Waves only wait on segments with a smaller index (lower blockIdx: see
+// WaveTile::init), every wait is bounded (an expired wait sets the sticky
+// error word).
+struct SsdLb {
+  uint64_t* status;  // [rows][nseg][2] tags: aggregate published, inclusive published
+  uint64_t* dec;     // [rows][nseg] decay product of the segment
+  uint64_t* agg;     // [rows][nseg][16][64] end state from zero (lane-major)
+  uint64_t* inc;     // [rows][nseg][16][64] state after the segment
+  WsHeader* hdr;
+  uint32_t tag, spin_limit;
+};
+constexpr int kSsdLbVals = 16;  // state values per lane (H[16 pi + c16][4q + r])
+
+// The 16 words of a lane at `base` (word v at base + 64 v + lane), waited on
+// until each carries the tag (bounded).
+__device__ inline void settle16(const uint64_t* base, int lane, uint32_t tag, float* v,
+                                uint32_t& spins, uint32_t spin_limit, WsHeader* hdr) {
+  uint64_t w[kSsdLbVals];
+#pragma unroll
+  for (int i = 0; i < kSsdLbVals; ++i) w[i] = ld_word(base + 64 * i + lane);
+#pragma unroll
+  for (int i = 0; i < kSsdLbVals; ++i) {
+    w[i] = settle_word(base + 64 * i + lane, w[i], tag, spins, spin_limit, hdr);
+    v[i] = word_val(w[i]);
+  }
+}
+
+// State entering segment c of the row whose segment 0 is `sbase`: fold the
+// predecessors' carries newest first -- an inclusive state ends the walk, an
+// aggregate (end state X, decay A) is folded in, S = A S_prev + X -- up to
+// the row's initial state h0v.  The status of 64 predecessors is read at
+// once (lane k: segment c-1-k).  A decay product of exactly zero ends the
+// walk too: nothing earlier can contribute.
+// h0p: the row's initial state ([P][N], NULL: zero); the lane's values are
+// H[16 pi + c16][4q..4q+3].
+__device__ inline void load_h0(const float* h0p, int lane, float* v) {
+  const int c16 = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int pi = 0; pi < 4; ++pi) {
+    const f32x4 w = h0p ? *reinterpret_cast<const f32x4*>(h0p + (16 * pi + c16) * kMn + 4 * q)
+                        : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[4 * pi + r] = w[r];
+  }
+}
+
+__device__ inline void ssd_lookback(const SsdLb& lb, int64_t sbase, int64_t c, int lane,
+                                    const float* h0p, float* S) {
+  float A = 1.0f, X[kSsdLbVals];
+#pragma unroll
+  for (int i = 0; i < kSsdLbVals; ++i) X[i] = 0.0f;
+  int64_t j = c - 1;  // newest predecessor not folded yet
+  uint32_t spins = 0;
+  while (true) {
+    bool inc_k = false, rdy_k = false;
+    if (j - lane < 0) {
+      inc_k = rdy_k = true;  // before segment 0 stands h0, an inclusive value
+    } else {
+      const uint64_t wi = ld_word(lb.status + 2 * (sbase + j - lane) + 1);
+      const uint64_t wa = ld_word(lb.status + 2 * (sbase + j - lane));
+      inc_k = word_tag(wi) == lb.tag;
+      rdy_k = inc_k || word_tag(wa) == lb.tag;
+    }
+    const uint64_t m_inc = __ballot(inc_k);
+    const uint64_t m_rdy = __ballot(rdy_k);
+    const int k_inc = m_inc ? __builtin_ctzll(m_inc) : 64;
+    const int k_gap = ~m_rdy ? __builtin_ctzll(~m_rdy) : 64;
+    const bool resolve = k_inc < k_gap;
+    const int n = resolve ? k_inc : k_gap;
+    for (int i = 0; i < n; ++i) {  // uniform
+      const int64_t sj = sbase + j - i;
+      const uint64_t wd = settle_word(lb.dec + sj, ld_word(lb.dec + sj), lb.tag, spins,
+                                      lb.spin_limit, lb.hdr);
+      float xv[kSsdLbVals];
+      settle16(lb.agg + sj * (64 * kSsdLbVals), lane, lb.tag, xv, spins, lb.spin_limit, lb.hdr);
+#pragma unroll
+      for (int v = 0; v < kSsdLbVals; ++v) X[v] = __builtin_fmaf(A, xv[v], X[v]);
+      A *= word_val(wd);
+      if (A == 0.0f) {  // uniform: earlier segments cannot contribute
+#pragma unroll
+        for (int v = 0; v < kSsdLbVals; ++v) S[v] = X[v];
+        return;
+      }
+    }
+    if (resolve) {
+      const int64_t ji = j - k_inc;
+      if (ji < 0) {
+        float hv[kSsdLbVals];
+        load_h0(h0p, lane, hv);
+#pragma unroll
+        for (int v = 0; v < kSsdLbVals; ++v) S[v] = __builtin_fmaf(A, hv[v], X[v]);
+      } else {
+        float iv[kSsdLbVals];
+        settle16(lb.inc + (sbase + ji) * (64 * kSsdLbVals), lane, lb.tag, iv, spins,
+                 lb.spin_limit, lb.hdr);
+#pragma unroll
+        for (int v = 0; v < kSsdLbVals; ++v) S[v] = __builtin_fmaf(A, iv[v], X[v]);
+      }
+      return;
+    }
+    j -= n;
+    if (n == 0) {
+      if (++spins > lb.spin_limit) {  // predecessor never published: give up loudly
+        flag_error(lb.hdr);
+#pragma unroll
+        for (int v = 0; v < kSsdLbVals; ++v) S[v] = X[v];
+        return;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (spins > lb.spin_limit) {
+#pragma unroll
+      for (int v = 0; v < kSsdLbVals; ++v) S[v] = X[v];
+      return;
+    }
+  }
+}
+
+template <int DISC, bool HAS_D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_fused_wave_kernel(SsdArgs a, SsdLb lb, uint32_t ngroups) {
+  __shared__ __align__(16) uint16_t s_xt[kWaveRows][kWxElems];
+  __shared__ __align__(16) uint16_t s_b[kWaveRows][kWsub * kWbRow];
+  __shared__ __align__(16) float s_sc[kWaveRows][3][kWsub];  // cum, coef, w
+  __shared__ __align__(16) uint16_t s_xr[HAS_D ? kWaveRows : 1][HAS_D ? kWsub * kMp : 4];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, q = lane >> 4, g8 = lane & 7, sq = lane >> 3;
+  WaveTile wt;
+  if (!wt.init(a, ngroups, wv, lane)) return;  // whole waves; no barriers in this kernel
+  const WaveOutLds ld{s_xt[wv], s_b[wv], s_sc[wv][0], s_sc[wv][1], s_sc[wv][2],
+                      s_xr[HAS_D ? wv : 0]};
+  const float a2 = -expf(a.A_log[wt.h]) * kLog2e;
+
+  // ---- 1. end state from zero, last sub-chunk first, x through the caches
+  f32x4 st[4];
+#pragma unroll
+  for (int pi = 0; pi < 4; ++pi) st[pi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float lsum = 0.0f;  // log2 decay from the end of the current sub-chunk to the segment end
+  {
+    u32x4 xr[4];
+    u32x2 bq[2];
+    float dtv;
+    wt.template load<0>((wt.nsub - 1) * kWsub, xr, bq, dtv);
+#pragma unroll 1
+    for (int k = wt.nsub - 1; k >= 0; --k) {
+      const int r0 = k * kWsub;
+      wave_put_xt(ld.xt, xr, g8, sq);
+#pragma unroll
+      for (int sg = 0; sg < 2; ++sg)
+        *reinterpret_cast<u32x2*>(ld.bs + (16 * sg + c16) * kWbRow + 4 * q) = bq[sg];
+      float pre, cf, cumE;
+      wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, lane, pre, cf, cumE);
+      if (lane < 32) ld.sw[lane] = exp2_fast(lsum + cumE - pre) * cf;
+      lsum += cumE;
+      // Once the decay from the segment end to this sub-chunk's start is
+      // exactly zero, every earlier step's weight 2^(lsum + cumE' - cum_s)
+      // (an exponent at most lsum) is exactly zero too: the earlier
+      // sub-chunks add exact zeros to the end state, and the segment's decay
+      // product is zero.  They are not read (uniform exit).
+      const bool done = k == 0 || exp2_fast(lsum) == 0.0f;
+      // the previous sub-chunk's loads overlap everything below
+      if (!done) wt.template load<0>(r0 - kWsub, xr, bq, dtv);
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+      s16x4_t xa[4][2];
+      wave_get_xa(ld.xt, c16, q, xa);
+      wave_state_update(st, xa, ld.bs, ld.sw, c16, q, 1.0f);
+      if (done) break;
+    }
+  }
+  // decay product of the segment (uniform; zero when the sweep stopped early)
+  const float dseg = exp2_fast(lsum);
+  // st now holds X, the end state from zero; X[4 pi + r] = st[pi][r]
+
+  // ---- 2./3. carry out, entry state in
+  const int64_t sbase = (int64_t)wt.row * a.nchunks;  // segment 0 of the row
+  const int64_t sidx = sbase + wt.c;
+  uint64_t* incw = lb.inc + sidx * (64 * kSsdLbVals);
+  const float* h0p = a.h0 ? a.h0 + (int64_t)wt.row * (kMp * kMn) : nullptr;
+  // Publish the carry before looking back: the inclusive state itself when
+  // the segment forgets everything before it (decay product exactly zero),
+  // else the aggregate (X, decay product).
+  if (wt.c != 0) {
+    const bool forget = dseg == 0.0f;  // uniform
+    uint64_t* dst = forget ? incw : lb.agg + sidx * (64 * kSsdLbVals);
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st_word(dst + 64 * (4 * pi + r) + lane, st[pi][r], lb.tag);
+    if (lane == 0) {
+      if (!forget) st_word(lb.dec + sidx, dseg, lb.tag);
+      st_word(lb.status + 2 * sidx + (forget ? 1 : 0), 0.0f, lb.tag);
+    }
+  }
+  float S[kSsdLbVals];  // state entering the segment
+  if (wt.c == 0) load_h0(h0p, lane, S);
+  else ssd_lookback(lb, sbase, wt.c, lane, h0p, S);
+  // state after the segment, O = dseg S + X: published (unless it already
+  // was) and, for the row's last segment, the final state
+  const bool last = a.h_last && wt.c + 1 == a.nchunks;
+  if (wt.c == 0 || dseg != 0.0f || last) {
+    float* hp = last ? a.h_last + (int64_t)wt.row * (kMp * kMn) : nullptr;
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+      f32x4 o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(dseg, S[4 * pi + r], st[pi][r]);
+      if (wt.c == 0 || dseg != 0.0f) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st_word(incw + 64 * (4 * pi + r) + lane, o[r], lb.tag);
+      }
+      if (last) *reinterpret_cast<f32x4*>(hp + (16 * pi + c16) * kMn + 4 * q) = o;
+    }
+    if ((wt.c == 0 || dseg != 0.0f) && lane == 0) st_word(lb.status + 2 * sidx + 1, 0.0f, lb.tag);
+  }
+
+  // ---- 4. outputs from the entry state
+#pragma unroll
+  for (int pi = 0; pi < 4; ++pi)
+    st[pi] = f32x4{S[4 * pi], S[4 * pi + 1], S[4 * pi + 2], S[4 * pi + 3]};
+  wave_out_sweep<DISC, HAS_D>(a, wt, st, ld, a2, lane);
 }
 
 // Tiles per wave of the tile passes: a wave walks ``seg`` consecutive
@@ -1389,6 +1653,143 @@ extern "C" int tssm_ssd_scan(int dtype, int disc, const void* x, const float* dt
     case TSSM_F16: return launch_ssd_t<f16_t>(disc, has_d, (int)N, rows, nchunks, PN, s, a);
     default: return launch_ssd_t<float>(disc, has_d, (int)N, rows, nchunks, PN, s, a);
   }
+}
+
+namespace tssm {
+namespace {
+
+// The fused tile kernel applies where the matrix-core tile passes do (bf16,
+// P = 64, N = 16, 256-step tiles, row strides that cover a row) and the
+// tagged words fit 32-bit segment indices.
+bool ssd_fused_ok(int dtype, int64_t P, int64_t N, int64_t tc, const SsdArgs& a, int64_t rows,
+                  int64_t nseg, int64_t seg_steps) {
+  return dtype == TSSM_BF16 && P == kMp && N == kMn && tc == kMq && ssd_wave_ok(a, seg_steps) &&
+         aligned(a.x, 16) && aligned(a.B, 16) && aligned(a.C, 16) && aligned(a.y, 8) &&
+         (!a.h0 || aligned(a.h0, 16)) && (!a.h_last || aligned(a.h_last, 16)) &&
+         a.sx_l % 8 == 0 && a.sx_h % 8 == 0 && a.sx_b % 8 == 0 && a.sB_l % 8 == 0 &&
+         a.sB_b % 8 == 0 && a.sB_h % 8 == 0 && a.sC_l % 8 == 0 && a.sC_b % 8 == 0 &&
+         a.sC_h % 8 == 0 && a.sy_l % 4 == 0 && a.sy_b % 4 == 0 && a.sy_h % 4 == 0 &&
+         rows * nseg < (int64_t)INT32_MAX;
+}
+
+// Look-back words of the fused kernel per (row, segment): 2 status, 1 decay,
+// 16 x 64 end-state and 16 x 64 inclusive-state words.
+constexpr int64_t kSsdSegWords = 3 + 2 * 64 * kSsdLbVals;
+
+int64_t ssd_fused_segs(int64_t rows, int64_t nchunks, int64_t* wseg) {
+  *wseg = ssd_wave_seg(rows, nchunks);
+  return cdiv64(nchunks, *wseg);
+}
+
+}  // namespace
+}  // namespace tssm
+
+extern "C" int64_t tssm_ssd_scan_fused_workspace_bytes(int64_t nbatch, int64_t L, int64_t H,
+                                                       int64_t P, int64_t N, int64_t chunk) {
+  if (nbatch <= 0 || L <= 0 || H <= 0 || P != kMp || N != kMn || ssd_tc(chunk) != kMq) return -1;
+  const int64_t rows = nbatch * H;
+  int64_t wseg = 1;
+  const int64_t nseg = ssd_fused_segs(rows, cdiv64(L, kMq), &wseg);
+  return (int64_t)sizeof(WsHeader) + rows * nseg * kSsdSegWords * 8;
+}
+
+namespace tssm {
+namespace {
+int ssd_fused_setup(int dtype, const void* x, const float* dt, const float* A_log, const void* B,
+                    const void* C, const float* D, const float* h0, void* y, float* h_last,
+                    int64_t nbatch, int64_t L, int64_t H, int64_t P, int64_t N, int64_t sx_b,
+                    int64_t sx_l, int64_t sx_h, int64_t sdt_b, int64_t sdt_l, int64_t sdt_h,
+                    int64_t sB_b, int64_t sB_l, int64_t sB_h, int64_t sC_b, int64_t sC_l,
+                    int64_t sC_h, int64_t sy_b, int64_t sy_l, int64_t sy_h, int64_t chunk,
+                    SsdArgs* a, int64_t* nseg_out) {
+  if (!(x && dt && A_log && B && C && y)) return TSSM_ERR_NULL;
+  if (nbatch <= 0 || L <= 0 || H <= 0) return TSSM_ERR_SHAPE;
+  const int64_t strides[] = {sx_b, sx_l, sx_h, sdt_b, sdt_l, sdt_h, sB_b, sB_l, sB_h,
+                             sC_b, sC_l, sC_h, sy_b, sy_l, sy_h};
+  for (int64_t st : strides)
+    if (st < 0) return TSSM_ERR_STRIDE;
+  const int64_t tc = ssd_tc(chunk);
+  const int64_t rows = nbatch * H;
+  int64_t wseg = 1;
+  const int64_t nseg = ssd_fused_segs(rows, cdiv64(L, kMq), &wseg);
+  SsdArgs& r = *a;
+  r.x = x; r.dt = dt; r.A_log = A_log; r.B = B; r.C = C; r.D = D; r.h0 = h0; r.y = y;
+  r.h_last = h_last; r.L = L;
+  r.sx_b = sx_b; r.sx_l = sx_l; r.sx_h = sx_h; r.sdt_b = sdt_b; r.sdt_l = sdt_l; r.sdt_h = sdt_h;
+  r.sB_b = sB_b; r.sB_l = sB_l; r.sB_h = sB_h; r.sC_b = sC_b; r.sC_l = sC_l; r.sC_h = sC_h;
+  r.sy_b = sy_b; r.sy_l = sy_l; r.sy_h = sy_h;
+  r.chunkA = r.chunkX = r.entry = nullptr;
+  r.H = (uint32_t)H; r.P = (uint32_t)P; r.rows = (uint32_t)rows;
+  r.nchunks = (uint32_t)nseg;
+  r.tc = (uint32_t)(wseg * kMq);
+  if (!ssd_fused_ok(dtype, P, N, tc, r, rows, nseg, wseg * kMq)) return TSSM_ERR_UNSUPPORTED;
+  *nseg_out = nseg;
+  return TSSM_OK;
+}
+}  // namespace
+}  // namespace tssm
+
+extern "C" int tssm_ssd_scan_fused_supported(int dtype, const void* x, const float* dt,
+                                             const float* A_log, const void* B, const void* C,
+                                             const float* D, const float* h0, void* y,
+                                             float* h_last, int64_t nbatch, int64_t L, int64_t H,
+                                             int64_t P, int64_t N, int64_t sx_b, int64_t sx_l,
+                                             int64_t sx_h, int64_t sdt_b, int64_t sdt_l,
+                                             int64_t sdt_h, int64_t sB_b, int64_t sB_l,
+                                             int64_t sB_h, int64_t sC_b, int64_t sC_l,
+                                             int64_t sC_h, int64_t sy_b, int64_t sy_l,
+                                             int64_t sy_h, int64_t chunk) {
+  SsdArgs a;
+  int64_t nseg = 0;
+  return ssd_fused_setup(dtype, x, dt, A_log, B, C, D, h0, y, h_last, nbatch, L, H, P, N, sx_b,
+                         sx_l, sx_h, sdt_b, sdt_l, sdt_h, sB_b, sB_l, sB_h, sC_b, sC_l, sC_h,
+                         sy_b, sy_l, sy_h, chunk, &a, &nseg) == TSSM_OK
+             ? 1
+             : 0;
+}
+
+extern "C" int tssm_ssd_scan_fused(int dtype, int disc, const void* x, const float* dt,
+                                   const float* A_log, const void* B, const void* C,
+                                   const float* D, const float* h0, void* y, float* h_last,
+                                   int64_t nbatch, int64_t L, int64_t H, int64_t P, int64_t N,
+                                   int64_t sx_b, int64_t sx_l, int64_t sx_h, int64_t sdt_b,
+                                   int64_t sdt_l, int64_t sdt_h, int64_t sB_b, int64_t sB_l,
+                                   int64_t sB_h, int64_t sC_b, int64_t sC_l, int64_t sC_h,
+                                   int64_t sy_b, int64_t sy_l, int64_t sy_h, int64_t chunk,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  SsdArgs a;
+  int64_t nseg = 0;
+  const int rc = ssd_fused_setup(dtype, x, dt, A_log, B, C, D, h0, y, h_last, nbatch, L, H, P, N,
+                                 sx_b, sx_l, sx_h, sdt_b, sdt_l, sdt_h, sB_b, sB_l, sB_h, sC_b,
+                                 sC_l, sC_h, sy_b, sy_l, sy_h, chunk, &a, &nseg);
+  if (rc != TSSM_OK) return rc;
+  const int64_t need = tssm_ssd_scan_fused_workspace_bytes(nbatch, L, H, P, N, chunk);
+  TSSM_CHECK(workspace && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 256), TSSM_ERR_ALIGN);
+  const int64_t rows = (int64_t)a.rows;
+  SsdLb lb;
+  lb.hdr = reinterpret_cast<WsHeader*>(workspace);
+  uint64_t* w = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + sizeof(WsHeader));
+  lb.status = w;
+  lb.dec = lb.status + 2 * rows * nseg;
+  lb.agg = lb.dec + rows * nseg;
+  lb.inc = lb.agg + rows * nseg * 64 * kSsdLbVals;
+  lb.tag = next_epoch(workspace);
+  lb.spin_limit = kDefaultSpinLimit;
+  const uint32_t ngroups = (uint32_t)((rows + kWaveRows - 1) / kWaveRows);
+  const dim3 gw((unsigned)(8 * ((nseg + 7) / 8) * ngroups));
+  const hipStream_t s = as_stream(stream);
+  const bool has_d = D != nullptr;
+#define TSSM_SF(DI, HD) \
+  hipLaunchKernelGGL((ssd_fused_wave_kernel<DI, HD>), gw, dim3(256), 0, s, a, lb, ngroups)
+  if (disc == TSSM_DISC_ZOH) {
+    if (has_d) TSSM_SF(TSSM_DISC_ZOH, true); else TSSM_SF(TSSM_DISC_ZOH, false);
+  } else {
+    if (has_d) TSSM_SF(TSSM_DISC_EULER, true); else TSSM_SF(TSSM_DISC_EULER, false);
+  }
+#undef TSSM_SF
+  return launch_status();
 }
 
 extern "C" int tssm_ssd_stream_step(int disc, const float* x, const float* dt, const float* A_log,

@@ -104,7 +104,7 @@ def _ws(nbytes, t, what, kind=workspace.LOOKBACK):
 
 
 def ssd_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=256, disc="zoh", h0=None,
-                     return_state=False, out=None):
+                     return_state=False, out=None, fused=True):
     """SSD selective scan: one decay per head, state [P, N] per (batch, head).
 
     x      [Bsz, L, H, P]  float32 / bfloat16 / float16 (P <= 64)
@@ -117,6 +117,10 @@ def ssd_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=256, disc="zoh", h0=No
     h_t[p,n] = exp(dt_t a) h_{t-1}[p,n] + Bbar_t x_t[p] B_t[n];
     y_t[p] = sum_n C_t[n] h_t[p,n] + D[p] x_t[p].  Returns y (dtype of x)
     and, with ``return_state``, the final state [Bsz, H, P, N] float32.
+
+    bf16 with P = 64, N = 16 and 256-step chunks runs in one launch
+    (tssm_ssd_scan_fused: two sweeps per segment around a decoupled
+    look-back) unless ``fused=False``, which keeps the three tile passes.
     """
     for t, w in ((x, "x"), (dt, "dt"), (A_log, "A_log"), (B, "B"), (C, "C")):
         need_gpu(t, w)
@@ -150,12 +154,20 @@ def ssd_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=256, disc="zoh", h0=No
     _inner_unit(y, "out")
     h_last = torch.empty(Bsz, H, P, N, device=x.device, dtype=torch.float32) if return_state else None
     L_ = _lib.lib()
-    ws, stream = _ws(L_.tssm_ssd_scan_workspace_bytes(Bsz, L, H, P, N, int(chunk)), x, "ssd_scan",
-                     workspace.SSD)
-    _lib.call("tssm_ssd_scan", code, _disc_code(disc), x.data_ptr(), dt.data_ptr(),
-              A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D), ptr(h0), y.data_ptr(),
-              ptr(h_last), Bsz, L, H, P, N, *x.stride()[:3], *dt.stride(), *B.stride()[:3],
-              *C.stride()[:3], *y.stride()[:3], int(chunk), ws.data_ptr(), ws.numel(), stream)
+    args = (x.data_ptr(), dt.data_ptr(), A_log.data_ptr(), B.data_ptr(), C.data_ptr(), ptr(D),
+            ptr(h0), y.data_ptr(), ptr(h_last), Bsz, L, H, P, N, *x.stride()[:3], *dt.stride(),
+            *B.stride()[:3], *C.stride()[:3], *y.stride()[:3], int(chunk))
+    if fused and L_.tssm_ssd_scan_fused_supported(code, *args):
+        # one launch with a decoupled look-back: a look-back workspace
+        ws, stream = _ws(L_.tssm_ssd_scan_fused_workspace_bytes(Bsz, L, H, P, N, int(chunk)), x,
+                         "ssd_scan")
+        _lib.call("tssm_ssd_scan_fused", code, _disc_code(disc), *args, ws.data_ptr(),
+                  ws.numel(), stream)
+    else:
+        ws, stream = _ws(L_.tssm_ssd_scan_workspace_bytes(Bsz, L, H, P, N, int(chunk)), x,
+                         "ssd_scan", workspace.SSD)
+        _lib.call("tssm_ssd_scan", code, _disc_code(disc), *args, ws.data_ptr(), ws.numel(),
+                  stream)
     return (y, h_last) if return_state else y
 
 
