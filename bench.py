@@ -12,7 +12,7 @@ x/B/C/y, fp32 dt and state, ZOH discretization fused into the load stage.
   ssd_config1    SSD scan on the headline shapes B=8 L=4096 H=16 P=N=64 bf16
   ssd_stream     streaming SSD step, 4096 streams H=32 P=64 N=128 fp32 state
   dtproj         Mamba-1 scan B=16 L=2048 D=256 N=16 fp32 with dt = clamp(softplus(
-                 dt_raw W + bias)) computed in the scan's load stage (rank 16)
+                 dt_raw W + bias)) formed inside the scan's passes (rank 16)
   dtproj_two_launch  the same as dt_project_softplus_kernel + the scan
   rows           every drop-in kernel at a config-sized shape (one JSON line, "rows" list)
 
@@ -39,6 +39,13 @@ sys.path.insert(0, str(ROOT / "triton-ssm_amd"))
 sys.path.insert(0, str(ROOT))
 
 PEAK_GBS = 8000.0
+# VALU roofline of the vector-bound workloads: MI355X's published fp32 rate
+# without packed math, 78.6 TFLOP/s = 39.3 T fused multiply-adds (lane
+# operations) per second; an exp2 occupies the issue of 2.31 of them (measured
+# on gfx950: independent v_exp_f32 at 3.51 ns and v_fma_f32 at 1.52 ns per
+# wave instruction per SIMD).
+PEAK_VALU_TLANE = 39.3
+EXP2_SLOTS = 2.31
 HEADLINE_METRIC = "scan elements/sec + achieved HBM GB/s (% of peak), B=8 L=4096 H=16 P=64 N=64"
 
 
@@ -69,6 +76,10 @@ def wl_multihead(args, dev):
     w = workloads.multihead(B=B, L=L, H=H, P=P)
     a_key = "A_log" if args.a_per_channel else "A_log_h"
     base = {k: w[k].to(dev) for k in ("u", "B", "C", "dt")}
+    if args.a_log_const is not None:
+        # a slowly decaying input of the same shape: every decay exp(-e^c dt)
+        w = dict(w)
+        w[a_key] = torch.full_like(w[a_key], args.a_log_const)
     A_log = w[a_key].to(dev)
     sets = []
     for i in range(args.sets):
@@ -97,6 +108,8 @@ def wl_multihead(args, dev):
            "B": B, "L": L, "H": H, "P": P, "N": P, "chunk": 128, "disc": args.disc,
            "io_dtype": "bf16", "state_dtype": "f32",
            "a_log": "per channel [H, P]" if args.a_per_channel else "per head [H]"}
+    if args.a_log_const is not None:
+        cfg["a_log_const"] = args.a_log_const
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, kernel="mh_scan_fused_kernel",
                 dtype="bf16", metric=HEADLINE_METRIC, unit="elements/s", config=cfg,
                 traffic="mh_scan_fused_traffic.json")
@@ -213,8 +226,12 @@ def wl_interp_mamba1(args, dev):
 
     n = B * T * F
     nbytes = 4 * (4 * n + B * T + F * N + 2 * B * T * N)   # V, M in; Vhat, y out
-    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
-                kernel="whole step: interp_fused_kernel, sel_chunk_state_kernel, "
+    # VALU floor per lane update (b, t, d, n) of the three-pass ZOH scan: the
+    # update (dt a, exp2, -1, B x, two fmas) and the readout fma in pass 1, the
+    # carried share (a cum, exp2, C S, fma) in pass 3: 9 ops and 2 exp2
+    valu = {"lane_updates": n * N, "ops_per_update": 9, "exp2_per_update": 2}
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, valu=valu,
+                kernel="whole step: sel_interp_state_kernel (interpolation in pass 1), "
                        "sel_carry_kernel, sel_output_kernel",
                 metric="interp + Mamba-1 scan elements/sec, B=16 T=2048 F=256 N=16 fp32",
                 unit="elements/s",
@@ -278,7 +295,11 @@ def _wl_dtproj(args, dev, fused):
     if not fused:
         nbytes += 2 * 4 * n      # dt written by the projection and read by the scan
     how = "fused into the scan's load stage" if fused else "two launches through dt [B,L,D]"
-    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, kernel="mh_scan_fused_kernel" if fused
+    # the same VALU floor per lane update as the interpolation workload's scan
+    valu = {"lane_updates": n * N, "ops_per_update": 9, "exp2_per_update": 2}
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, valu=valu,
+                kernel="sel_chunk_state_kernel (dt formed on the matrix cores) + "
+                       "sel_carry_kernel + sel_output_kernel" if fused
                 else "dt_project_mfma_kernel + sel_chunk_state_kernel + sel_carry_kernel + "
                      "sel_output_kernel",
                 metric=f"Mamba-1 scan with dt projection ({how}) elements/sec, B=16 L=2048 "
@@ -330,7 +351,7 @@ def wl_ssd_long(args, dev):
     n = B * L * H * P
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
-                kernel="ssd_state_wave_kernel + ssd_pass_kernel + ssd_out_wave_kernel",
+                kernel="ssd_fused_wave_kernel",
                 traffic="ssd_long_traffic.json",
                 dtype="bf16",
                 metric="SSD long-sequence scan elements/sec, B=1 L=262144 H=8 P=64 N=16 bf16",
@@ -618,6 +639,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["rows"], default="multihead")
     ap.add_argument("--disc", choices=["zoh", "euler"], default="zoh")
+    ap.add_argument("--a-log-const", type=float, default=None,
+                    help="multihead: every A_log entry set to this value (e.g. -4.6 = log 0.01, "
+                         "a slowly decaying input of the headline shape)")
     ap.add_argument("--a-per-channel", action="store_true",
                     help="multihead: pass A_log as [H, P] (the reference kernel's layout, the "
                          "per-head value repeated) instead of [H] (one decay per head)")
@@ -731,6 +755,31 @@ def main():
         "cpu_baseline": cpu,
         "p50_step_ms": statistics.median(per),
     }
+    v = wl.get("valu")
+    if v:
+        # vector-issue bound: the algorithm's floor of lane operations (exp2
+        # weighted by its issue cost) over the measured time, against the
+        # published lane-op rate; the HBM figures stay as secondary keys
+        slots = v["ops_per_update"] + EXP2_SLOTS * v["exp2_per_update"]
+        got = v["lane_updates"] * slots / (kern_ms * 1e-3) / 1e12
+        hbm = out["roofline"]
+        out["roofline"] = {
+            "bound": "valu",
+            "kernel": wl["kernel"],
+            "achieved": got,
+            "peak": PEAK_VALU_TLANE,
+            "unit": "T lane-ops/s",
+            "frac": got / PEAK_VALU_TLANE,
+            "traffic": hbm["traffic"],
+            "ops_per_lane_update": v["ops_per_update"],
+            "exp2_per_lane_update": v["exp2_per_update"],
+            "exp2_issue_slots": EXP2_SLOTS,
+            "lane_updates_per_launch": v["lane_updates"],
+            "hbm_achieved_GBs": hbm["achieved"],
+            "hbm_frac": hbm["frac"],
+            "algorithmic_bytes_per_launch": wl["bytes"],
+            "kernel_avg_us": kern_ms * 1e3,
+        }
     print(json.dumps(out), flush=True)
 
 
