@@ -14,6 +14,9 @@ x/B/C/y, fp32 dt and state, ZOH discretization fused into the load stage.
   dtproj         Mamba-1 scan B=16 L=2048 D=256 N=16 fp32 with dt = clamp(softplus(
                  dt_raw W + bias)) formed inside the scan's passes (rank 16)
   dtproj_two_launch  the same as dt_project_softplus_kernel + the scan
+  bcproj         Mamba-1 scan B=16 L=2048 D=256 N=16 fp32 with B, C = x W formed inside
+                 the scan's first pass
+  bcproj_two_launch  the same as matmuls producing B and C, then the scan
   rows           every drop-in kernel at a config-sized shape (one JSON line, "rows" list)
 
 A step is one pass of the path over one batch of seeded synthetic input that
@@ -319,6 +322,83 @@ def wl_dtproj_two_launch(args, dev):
     return _wl_dtproj(args, dev, False)
 
 
+def _wl_bcproj(args, dev, fused):
+    """Mamba-1 scan with B and C from x: B_t = x_t W_B, C_t = x_t W_C, at the
+    interpolation workload's scan shape (B=16 L=2048 D=256 N=16 fp32, dt from
+    sorted timestamps): formed inside the scan (bc_proj=), or as a matmul
+    producing B and C followed by the scan."""
+    import torch
+    from tssm import selective_scan_forward, workloads
+    w = workloads.interp_mamba1()
+    g = torch.Generator().manual_seed(1006)
+    B, L, Dc = w["V"].shape
+    N = w["A_log"].shape[1]
+    x0 = torch.randn(B, L, Dc, generator=g)
+    W_bc = (torch.randn(Dc, 2 * N, generator=g) / Dc ** 0.5).to(dev)
+    A_log = w["A_log"].to(dev)
+    sets = []
+    for i in range(max(args.sets, 3)):
+        st = {"x": torch.roll(x0, shifts=i, dims=0).contiguous().to(dev),
+              "tau": torch.roll(w["tau"], shifts=i, dims=0).contiguous().to(dev)}
+        st["y"] = torch.empty_like(st["x"])
+        st["Bm"] = torch.empty(B, L, N, device=dev)
+        st["Cm"] = torch.empty(B, L, N, device=dev)
+        sets.append(st)
+
+    def step(i):
+        d = sets[i % len(sets)]
+        if fused:
+            selective_scan_forward(d["x"], d["tau"], A_log, None, None, None, disc=args.disc,
+                                   dt_is_tau=True, out=d["y"], bc_proj=W_bc)
+        else:
+            torch.matmul(d["x"], W_bc[:, :N], out=d["Bm"])
+            torch.matmul(d["x"], W_bc[:, N:], out=d["Cm"])
+            selective_scan_forward(d["x"], d["tau"], A_log, d["Bm"], d["Cm"], None,
+                                   disc=args.disc, dt_is_tau=True, out=d["y"])
+
+    def cpu():
+        import numpy as np
+        from oracle import cport
+        x = _np32(x0)
+        Wn = _np32(W_bc.cpu())
+        tau = _np32(w["tau"])
+        Al = _np32(w["A_log"])
+
+        def run():
+            Bm = np.ascontiguousarray(x @ Wn[:, :N])
+            Cm = np.ascontiguousarray(x @ Wn[:, N:])
+            dt = np.diff(tau, axis=1, prepend=0.0).astype(np.float32)
+            cport.selective_scan(x, dt, Al, Bm, Cm, None, disc=args.disc)
+        med = _timed_cpu(run, args.cpu_reps)
+        return {"value": B * L * Dc / med, "unit": "elements/s", "cores": cport.threads(),
+                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                                          f"{med:.3f} s each"}
+
+    n = B * L * Dc
+    nbytes = 4 * (2 * n + B * L + Dc * N + Dc * 2 * N)   # x, y, tau, A_log, W
+    how = "formed in the scan" if fused else "matmul, then the scan"
+    valu = {"lane_updates": n * N, "ops_per_update": 9, "exp2_per_update": 2}
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, valu=valu,
+                kernel="sel_bcproj_state_kernel + sel_carry_kernel + sel_output_kernel" if fused
+                else "matmul (B), matmul (C), sel_chunk_state_kernel, sel_carry_kernel, "
+                     "sel_output_kernel",
+                metric=f"Mamba-1 scan with B, C = x W ({how}) elements/sec, B=16 L=2048 D=256 "
+                       "N=16 fp32",
+                unit="elements/s",
+                config={"workload": f"B_t = x_t W_B, C_t = x_t W_C ({how}) + Mamba-1 scan, "
+                                    f"B=16 L=2048 D=256 N=16 fp32, dt from timestamps, "
+                                    f"{args.disc.upper()}",
+                        "B": B, "L": L, "D": Dc, "N": N})
+
+
+def wl_bcproj(args, dev):
+    return _wl_bcproj(args, dev, True)
+
+
+def wl_bcproj_two_launch(args, dev):
+    return _wl_bcproj(args, dev, False)
+
+
 def wl_ssd_long(args, dev):
     import torch
     from tssm import ssd_scan_forward, workloads
@@ -612,7 +692,8 @@ def rows_sweep(args, dev):
                       "rows": rows}))
 
 
-WORKLOADS = {"multihead": wl_multihead, "mamba1_small": wl_mamba1_small,
+WORKLOADS = {"bcproj": wl_bcproj, "bcproj_two_launch": wl_bcproj_two_launch,
+             "multihead": wl_multihead, "mamba1_small": wl_mamba1_small,
              "interp_mamba1": wl_interp_mamba1, "ssd_long": wl_ssd_long,
              "ssd_config1": wl_ssd_config1,
              "ssd_stream": wl_ssd_stream, "dtproj": wl_dtproj,

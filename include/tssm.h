@@ -441,6 +441,29 @@ int tssm_selective_scan_dtproj(int dtype, int disc, const void* x, const float* 
                                int64_t sy_b, int64_t sy_l, int64_t chunk, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/* tssm_selective_scan with B and C produced from x in the scan: B_t = x_t W_B,
+ * C_t = x_t W_C (Mamba-1's input projection columns for B and C, the step
+ * before ssm_scan.py:239-264 in a selective model; the reference has no
+ * kernel for it), so no B/C tensors and no projection launch.  W_bc f32
+ * [Dc, 2N]: columns 0..N-1 W_B, N..2N-1 W_C, row stride sw_d (>= 2N), unit
+ * column stride (a column slice of a wider x_proj weight works).  fp32 x/y,
+ * Dc <= 256 and a multiple of 4, N 8 or 16, x rows 16-byte aligned; dt as in
+ * tssm_selective_scan (shared, with or without timestamps, or per channel).
+ * Three launches: pass 1 stages each 32-step chunk's x tile in LDS, forms
+ * the chunk's B/C rows on the fp32 matrix cores and runs the recurrence from
+ * that tile; pass 3 reads the C rows pass 1 stored in the workspace
+ * (tssm_selective_scan_bcproj_workspace_bytes() bytes: raw fp32, not
+ * look-back words).  No reference counterpart. */
+int64_t tssm_selective_scan_bcproj_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc,
+                                                   int64_t N);
+int tssm_selective_scan_bcproj(int disc, const float* x, const float* dt, int dt_is_tau,
+                               const float* A_log, const float* W_bc, int64_t sw_d,
+                               const float* D, const float* h0, float* y, float* h_last,
+                               int64_t nbatch, int64_t L, int64_t Dc, int64_t N, int64_t sx_b,
+                               int64_t sx_l, int64_t sdt_b, int64_t sdt_l, int64_t sdt_d,
+                               int64_t sy_b, int64_t sy_l, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ elementwise scan, single pass
  * The host functions ssm_forward / ssm_backward (ssm_scan.py:239-289) as one
  * launch each over contiguous [B, L, H] tensors of `dtype` (D [H]): every

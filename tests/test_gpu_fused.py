@@ -536,6 +536,57 @@ def test_selective_scan_dtproj_workspace_forms(dev):
     assert_close(outs[1][1], h_ref, 1e-5, "dtproj h_last (dt produced again)")
 
 
+@pytest.mark.parametrize("Dc,N,L,Bsz,dt_mode,extras,sliced", [
+    (256, 16, 2048, 4, "tau", False, False),      # the interpolation workload's scan shape
+    (100, 8, 333, 3, "per_channel", True, False),  # ragged channels and steps, D, h0
+    (64, 16, 700, 2, "shared", True, True),       # W as a column slice of a wider x_proj weight
+])
+def test_selective_scan_bcproj(dev, Dc, N, L, Bsz, dt_mode, extras, sliced):
+    """B_t = x_t W_B and C_t = x_t W_C formed inside the scan (bc_proj=):
+    against the float64 oracle fed the float64 products, and against the
+    unfused path (torch.matmul for B and C, then the scan)."""
+    from tssm import selective_scan_forward
+    g = torch.Generator().manual_seed(Dc + N + L)
+    x = torch.randn(Bsz, L, Dc, generator=g)
+    R = 16
+    Wx = torch.randn(Dc, R + 2 * N, generator=g) / Dc ** 0.5
+    W_bc = Wx[:, R:] if sliced else Wx[:, R:].contiguous()
+    if dt_mode == "tau":
+        dt = torch.sort(torch.rand(Bsz, L, generator=g) * (L / 20.0), dim=1).values
+    elif dt_mode == "shared":
+        dt = torch.rand(Bsz, L, generator=g) * 0.1
+    else:
+        dt = torch.rand(Bsz, L, Dc, generator=g) * 0.1
+    A_log = torch.empty(Dc, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    D = torch.randn(Dc, generator=g) if extras else None
+    h0 = torch.randn(Bsz, Dc, N, generator=g) if extras else None
+    d = {k: v.to(dev) for k, v in dict(x=x, dt=dt, A_log=A_log).items()}
+    Wd = Wx.to(dev)[:, R:] if sliced else W_bc.to(dev)
+    if sliced:
+        assert Wd.stride(0) == R + 2 * N
+    Dd = D.to(dev) if extras else None
+    h0d = h0.to(dev) if extras else None
+    tau = dt_mode == "tau"
+    y, h = selective_scan_forward(d["x"], d["dt"], d["A_log"], None, None, Dd, h0=h0d,
+                                  return_state=True, dt_is_tau=tau, bc_proj=Wd)
+    Bg = (d["x"] @ Wd[:, :N]).contiguous()
+    Cg = (d["x"] @ Wd[:, N:]).contiguous()
+    y2, h2 = selective_scan_forward(d["x"], d["dt"], d["A_log"], Bg, Cg, Dd, h0=h0d,
+                                    return_state=True, dt_is_tau=tau)
+    torch.cuda.synchronize()
+    x64, W64 = x.double(), W_bc.double()
+    Bref, Cref = x64 @ W64[:, :N], x64 @ W64[:, N:]
+    dtr = torch.diff(dt.double(), dim=1, prepend=torch.zeros(Bsz, 1, dtype=torch.float64)) \
+        if tau else dt
+    y_ref, h_ref = O.selective_scan(x, dtr, A_log, Bref, Cref, D,
+                                    h0=None if h0 is None else np64(h0))
+    e = assert_close(y, y_ref, 1e-5, f"bcproj y Dc={Dc} N={N} {dt_mode}")
+    assert_close(h, h_ref, 1e-5, "bcproj h_last")
+    assert_close(y, y2, 1e-5, "bcproj vs matmul + scan")
+    assert_close(h, h2, 1e-5, "bcproj h_last vs matmul + scan")
+    print(f"bcproj Dc={Dc} N={N} {dt_mode}: relerr {e:.2e}")
+
+
 def triton_pow2(n):
     return 1 << (n - 1).bit_length()
 

@@ -513,6 +513,176 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
                       });
 }
 
+// ---------------------------------------------------------------- x -> (B, C) in pass 1
+// The selective input projection producing B and C from x (B_t = x_t W_B,
+// C_t = x_t W_C: Mamba-1's x_proj columns for B and C) formed inside pass 1,
+// so B and C [B, L, N] are never read from a caller's tensor and no
+// projection launch runs.  fp32 I/O, Dc <= 256 (one workgroup holds every
+// channel of a step).  A workgroup stages its chunk's x tile [32][Dc] in LDS
+// (every step's row, padded steps repeating step n-1), wave w forms the
+// 16 x 16 output tile (steps 16 (w & 1).., columns 16 (w >> 1)..) of
+// [32][2N] = x W_BC on the fp32 matrix cores (16x16x4, the channels in steps
+// of 4), the rows are staged as pass 1's B/C rows, C's rows are also stored
+// for pass 3, and the recurrence reads x from the LDS tile instead of HBM.
+constexpr int kBcRow = kSelThreads + 4;  // x tile row stride (floats): 16-byte rows, banks spread
+constexpr int kBcKb = 16;                // W values per lane in flight in the B/C product
+
+template <int DISC, int NST, bool DTS, bool TAU, bool HAS_D>
+__global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
+    const float* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
+    const float* __restrict__ Wbc, int64_t sw_d, const float* __restrict__ D,
+    float* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum,
+    float* __restrict__ Cws, SelDims m) {
+  static_assert(!TAU || DTS, "timestamps only when shared by the channels");
+  static_assert(NST == 8 || NST == 16, "8 or 16 states");
+  const int64_t c = blockIdx.x, b = blockIdx.z;  // one channel block (blockIdx.y == 0)
+  const int tid = (int)threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t d = tid;
+  const bool ok = d < m.Dc;
+  const int64_t dc = ok ? d : m.Dc - 1;  // lanes past Dc compute channel Dc-1
+  const int64_t t0 = c * m.Rs;
+  const int n = (int)(m.L - t0 < m.Rs ? m.L - t0 : m.Rs);
+  const int n4 = (n + kSelPf - 1) / kSelPf * kSelPf;
+
+  __shared__ __align__(16) float sX[kSelChunkSteps * kBcRow];
+  __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
+  __shared__ float sD[DTS ? kSelChunkSteps : 1];
+  // ---- prologue loads: the x tile (thread: columns 4 (tid & 63).. of rows
+  // (tid >> 6) + 4 k; columns past Dc read as zero), shared dt, lane
+  // parameters, a per-channel dt's first fetches; then one wait
+  const float* xb = x + b * m.sx_b;
+  const int col = 4 * lane;
+  const bool cok = col < m.Dc;  // Dc a multiple of 4
+  float4 xv[kSelChunkSteps / 4];
+#pragma unroll
+  for (int k = 0; k < kSelChunkSteps / 4; ++k) {
+    const int r = wv + 4 * k;
+    const int rr = r < n ? r : n - 1;
+    const float4 v = *reinterpret_cast<const float4*>(xb + (t0 + rr) * m.sx_l + (cok ? col : 0));
+    xv[k] = cok ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float vdt = 0.0f;
+  if constexpr (DTS) vdt = stage_dt_load<TAU>(dt + b * m.sdt_b, m.sdt_l, t0, n);
+  const float* dtb = dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d);
+  float dr[kSelPf];
+#pragma unroll
+  for (int j = 0; j < kSelPf; ++j)
+    dr[j] = DTS ? 0.0f : dtb[(t0 + (j < n ? j : n - 1)) * m.sdt_l];
+  float al[NST];
+  load_alog<NST>(A_log, dc, al);
+  float Dd = HAS_D ? D[dc] : 0.0f;
+#pragma unroll
+  for (int k = 0; k < kSelChunkSteps / 4; ++k)
+    *reinterpret_cast<float4*>(sX + (wv + 4 * k) * kBcRow + col) = xv[k];
+  if constexpr (DTS) {
+    if (tid < n4) sD[tid] = vdt;
+  }
+  __syncthreads();  // x tile staged
+
+  // ---- B and C rows of the chunk on the matrix cores
+  if (wv < NST / 4) {  // 2N / 16 column tiles x 2 step tiles
+    const int rt = wv & 1, ct = wv >> 1;
+    const int li = lane & 15, lj = lane >> 4;
+    f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+    const float* xa = sX + (16 * rt + li) * kBcRow + lj;
+    const float* wb = Wbc + (int64_t)lj * sw_d + 16 * ct + li;
+    // W values (k-step j: W[4 j + lj][16 ct + li]) in blocks of kBcKb, the
+    // next block's loads in flight while the current block's products run
+    // (each product would otherwise wait on its own L2 round trip)
+    const int nk = (int)(m.Dc / 4);  // k-steps of 4 channels
+    float wcur[kBcKb], wnxt[kBcKb];
+    auto load_w = [&](int kb, float (&w)[kBcKb]) {
+#pragma unroll
+      for (int j = 0; j < kBcKb; ++j) {
+        const int kk = kb + j < nk ? kb + j : nk - 1;  // past the last k-step: any row, unused
+        w[j] = wb[(int64_t)(4 * kk) * sw_d];
+      }
+    };
+    load_w(0, wcur);
+    for (int kb = 0; kb < nk; kb += kBcKb) {
+      if (kb + kBcKb < nk) load_w(kb + kBcKb, wnxt);
+#pragma unroll
+      for (int j = 0; j < kBcKb; j += 2) {
+        if (kb + j < nk)
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[4 * (kb + j)], wcur[j], acc0, 0, 0, 0);
+        if (kb + j + 1 < nk)
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[4 * (kb + j + 1)], wcur[j + 1], acc1, 0,
+                                                      0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < kBcKb; ++j) wcur[j] = wnxt[j];
+    }
+    // lane (li, lj): steps 16 rt + 4 lj + i, column 16 ct + li of [B | C]
+    const int cc = 16 * ct + li;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * rt + 4 * lj + i;
+      const float v = acc0[i] + acc1[i];
+      if (cc < NST) {
+        sB[r * NST + cc] = v;
+      } else {
+        sC[r * NST + cc - NST] = v;
+        if (r < n) Cws[(b * m.L + t0 + r) * NST + cc - NST] = v;  // for pass 3
+      }
+    }
+  }
+  float a2[NST], nia[NST], h[NST];
+  sel_params<NST>(al, a2, nia);
+#pragma unroll
+  for (int k = 0; k < NST; ++k) {
+    h[k] = 0.0f;
+    asm volatile("" : "+v"(a2[k]), "+v"(nia[k]));  // complete before the loop
+  }
+  asm volatile("" : "+v"(Dd));
+  __syncthreads();  // B/C rows staged
+  // Waves whose lanes are all past Dc are done (no barrier follows).
+  if ((tid & ~63) >= m.Dc) return;
+
+  float* yp = y + b * m.sy_b + dc;
+  const float* xcol = sX + dc;
+  float sdt = 0.0f;
+  for (int r = 0; r < n4; r += kSelPf) {
+#pragma unroll
+    for (int j = 0; j < kSelPf; ++j) {
+      const int rr = r + j;
+      const float u = xcol[rr * kBcRow];
+      const float dtv = DTS ? sD[rr] : (rr < n ? dr[j] : 0.0f);
+      float Bv[NST], Cv[NST];
+      lds_row<NST>(sB + rr * NST, Bv);
+      lds_row<NST>(sC + rr * NST, Cv);
+      sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
+      sdt += dtv;
+      float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NST; k += 2) {
+        acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
+        acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
+      }
+      // unconditional store: lanes past Dc (in the wave of channel Dc-1) and
+      // padded steps store the values of channel Dc-1 / step n-1
+      const int64_t tw = t0 + (rr < n ? rr : n - 1);
+      yp[tw * m.sy_l] = acc0 + acc1;
+      if constexpr (!DTS) {
+        __builtin_amdgcn_sched_barrier(0);
+        dr[j] = dtb[(t0 + min(rr + kSelPf, n - 1)) * m.sdt_l];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  if (ok) {
+    float4* sp = reinterpret_cast<float4*>(S + ((b * m.nch + c) * m.Dc + d) * NST);
+#pragma unroll
+    for (int q = 0; q < NST / 4; ++q)
+      sp[q] = make_float4(h[4 * q], h[4 * q + 1], h[4 * q + 2], h[4 * q + 3]);
+    if constexpr (DTS) {
+      if (d == 0) Tsum[b * m.nch + c] = sdt;
+    } else {
+      Tsum[(b * m.nch + c) * m.Dc + d] = sdt;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- interpolation in pass 1
 // Time-aware interpolation (fused_interp_kernel.py:29-100, reference
 // semantics as in interp.hip: "observed" is the FTILE-wide tile's mask sum
@@ -884,6 +1054,47 @@ int ilog2(int64_t v) {
 
 }  // namespace
 
+template <int DISC, int NST, bool DTS, bool TAU>
+int sel_bcproj_t(bool has_d, const float* x, const float* dt, const float* Wbc, int64_t sw_d,
+                 float* Cws, const SelPtrs& p, const SelDims& m, hipStream_t s) {
+  const dim3 grid((unsigned)m.nch, 1u, (unsigned)m.nbatch);
+  float* y = static_cast<float*>(p.y);
+  if (has_d)
+    hipLaunchKernelGGL((sel_bcproj_state_kernel<DISC, NST, DTS, TAU, true>), grid,
+                       dim3(kSelThreads), 0, s, x, dt, p.A_log, Wbc, sw_d, p.D, y, p.S, p.T, Cws,
+                       m);
+  else
+    hipLaunchKernelGGL((sel_bcproj_state_kernel<DISC, NST, DTS, TAU, false>), grid,
+                       dim3(kSelThreads), 0, s, x, dt, p.A_log, Wbc, sw_d, p.D, y, p.S, p.T, Cws,
+                       m);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const int64_t lanes = m.Dc * NST;  // per batch
+  hipLaunchKernelGGL((sel_carry_kernel<NST, DTS>),
+                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
+                          (unsigned)m.nbatch),
+                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  // pass 3 reads the C rows pass 1 stored
+  SelDims m3 = m;
+  m3.sC_b = m.L * NST; m3.sC_l = NST;
+  hipLaunchKernelGGL((sel_output_kernel<float, NST, DTS, TAU>), grid, dim3(kSelThreads), 0, s,
+                     dt, p.A_log, Cws, p.S, y, m3);
+  return (int)hipGetLastError();
+}
+
+template <int DISC, int NST>
+int sel_bcproj_dt(bool has_d, bool dts, bool tau, const float* x, const float* dt,
+                  const float* Wbc, int64_t sw_d, float* Cws, const SelPtrs& p, const SelDims& m,
+                  hipStream_t s) {
+  if (dts) {
+    return tau ? sel_bcproj_t<DISC, NST, true, true>(has_d, x, dt, Wbc, sw_d, Cws, p, m, s)
+               : sel_bcproj_t<DISC, NST, true, false>(has_d, x, dt, Wbc, sw_d, Cws, p, m, s);
+  }
+  return sel_bcproj_t<DISC, NST, false, false>(has_d, x, dt, Wbc, sw_d, Cws, p, m, s);
+}
+
 bool sel_interp_ok(int dtype, int64_t nbatch, int64_t T, int64_t F, int64_t N, int64_t K,
                    int64_t FTILE, const void* M, int64_t sm_b, int64_t sm_t, int64_t sv_t) {
   const bool pow2 = FTILE > 0 && (FTILE & (FTILE - 1)) == 0;
@@ -1031,3 +1242,57 @@ extern "C" int tssm_interp_selective_scan(int dtype, int disc, const void* V, co
                            sm_t, stau_b, stau_t, sB_b, sB_l, sC_b, sC_l, so_b, so_t, sy_b, sy_t,
                            K, FTILE, as_stream(stream));
 }
+
+extern "C" int64_t tssm_selective_scan_bcproj_workspace_bytes(int64_t nbatch, int64_t L,
+                                                              int64_t Dc, int64_t N) {
+  if (nbatch <= 0 || L <= 0 || Dc <= 0 || !(N == 8 || N == 16)) return -1;
+  const int64_t nch = (L + kSelChunkSteps - 1) / kSelChunkSteps;
+  // chunk states + dt sums (per channel at most), then the C rows for pass 3
+  return (nbatch * nch * Dc * N + nbatch * nch * Dc) * 4 + nbatch * L * N * 4 + 256;
+}
+
+extern "C" int tssm_selective_scan_bcproj(int disc, const float* x, const float* dt,
+                                          int dt_is_tau, const float* A_log, const float* W_bc,
+                                          int64_t sw_d, const float* D, const float* h0,
+                                          float* y, float* h_last, int64_t nbatch, int64_t L,
+                                          int64_t Dc, int64_t N, int64_t sx_b, int64_t sx_l,
+                                          int64_t sdt_b, int64_t sdt_l, int64_t sdt_d,
+                                          int64_t sy_b, int64_t sy_l, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(x && dt && A_log && W_bc && y, TSSM_ERR_NULL);
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nbatch > 0 && L > 0 && Dc > 0, TSSM_ERR_SHAPE);
+  TSSM_CHECK((N == 8 || N == 16) && Dc <= kSelThreads && Dc % 4 == 0 && nbatch <= 65535,
+             TSSM_ERR_UNSUPPORTED);
+  const bool dt_shared = sdt_d == 0;
+  TSSM_CHECK(dt_shared || !dt_is_tau, TSSM_ERR_UNSUPPORTED);
+  const int64_t strides[] = {sx_b, sx_l, sdt_b, sdt_l, sdt_d, sy_b, sy_l};
+  for (int64_t st : strides) TSSM_CHECK(st >= 0, TSSM_ERR_STRIDE);
+  TSSM_CHECK(sw_d >= 2 * N, TSSM_ERR_STRIDE);
+  TSSM_CHECK(aligned(x, 16) && sx_b % 4 == 0 && sx_l % 4 == 0 && aligned(A_log, 16),
+             TSSM_ERR_ALIGN);
+  const int64_t need = tssm_selective_scan_bcproj_workspace_bytes(nbatch, L, Dc, N);
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 16), TSSM_ERR_ALIGN);
+  SelDims m{};
+  m.L = L; m.Dc = Dc; m.nbatch = nbatch;
+  m.Rs = kSelChunkSteps;
+  m.nch = (L + m.Rs - 1) / m.Rs;
+  m.sx_b = sx_b; m.sx_l = sx_l; m.sdt_b = sdt_b; m.sdt_l = sdt_l; m.sdt_d = sdt_d;
+  m.sy_b = sy_b; m.sy_l = sy_l;
+  SelPtrs p;
+  p.x = x; p.dt = dt; p.A_log = A_log; p.D = D; p.h0 = h0; p.y = y; p.h_last = h_last;
+  p.S = static_cast<float*>(workspace);
+  p.T = p.S + nbatch * m.nch * Dc * N;
+  float* Cws = p.T + nbatch * m.nch * Dc;
+  const hipStream_t s = as_stream(stream);
+  const bool has_d = D != nullptr, tau = dt_is_tau != 0;
+  if (N == 16)
+    return disc == TSSM_DISC_ZOH
+               ? sel_bcproj_dt<TSSM_DISC_ZOH, 16>(has_d, dt_shared, tau, x, dt, W_bc, sw_d, Cws, p, m, s)
+               : sel_bcproj_dt<TSSM_DISC_EULER, 16>(has_d, dt_shared, tau, x, dt, W_bc, sw_d, Cws, p, m, s);
+  return disc == TSSM_DISC_ZOH
+             ? sel_bcproj_dt<TSSM_DISC_ZOH, 8>(has_d, dt_shared, tau, x, dt, W_bc, sw_d, Cws, p, m, s)
+             : sel_bcproj_dt<TSSM_DISC_EULER, 8>(has_d, dt_shared, tau, x, dt, W_bc, sw_d, Cws, p, m, s);
+}
+

@@ -226,8 +226,60 @@ def ssd_stream_step(x, dt, A_log, B, C, D, state, *, disc="zoh", out=None):
     return y
 
 
-def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh", h0=None,
-                           return_state=False, dt_is_tau=False, out=None, dt_proj=None):
+def _selective_scan_bcproj(x, dt, A_log, W_bc, D, disc, h0, return_state, dt_is_tau, out):
+    """tssm_selective_scan_bcproj: B_t = x_t W_bc[:, :N], C_t = x_t W_bc[:, N:]
+    formed inside the scan's first pass (fp32, Dc <= 256)."""
+    for t, w in ((x, "x"), (dt, "dt"), (A_log, "A_log"), (W_bc, "bc_proj")):
+        need_gpu(t, w)
+    if x.dim() != 3 or x.dtype != torch.float32:
+        raise ValueError("bc_proj: x must be float32 [Bsz, L, Dc]")
+    Bsz, L, Dc = x.shape
+    if W_bc.dim() != 2 or W_bc.shape[0] != Dc or W_bc.shape[1] % 2:
+        raise ValueError("bc_proj: W_bc must be [Dc, 2N] (columns W_B then W_C)")
+    N = W_bc.shape[1] // 2
+    if A_log.shape != (Dc, N):
+        raise ValueError("shape mismatch between x, bc_proj and A_log")
+    if Dc > 256 or Dc % 4 or N not in (8, 16):
+        raise ValueError("bc_proj needs Dc <= 256 (a multiple of 4) and N = 8 or 16")
+    _inner_unit(x, "x")
+    W_bc = as_f32(W_bc, "bc_proj")
+    _inner_unit(W_bc, "bc_proj")
+    A_log = as_f32(A_log, "A_log").contiguous()
+    dt = as_f32(dt, "dt")
+    if dt.shape == (Bsz, L):
+        sdt = (dt.stride(0), dt.stride(1), 0)
+    elif dt.shape == (Bsz, L, Dc) and not dt_is_tau:
+        sdt = dt.stride()
+    else:
+        raise ValueError("dt must be [Bsz, L] (or [Bsz, L, Dc] without dt_is_tau)")
+    if D is not None:
+        need_gpu(D, "D")
+        if D.numel() != Dc:
+            raise ValueError("D must have Dc elements")
+        D = as_f32(D, "D").contiguous()
+    if h0 is not None:
+        need_gpu(h0, "h0")
+        if tuple(h0.shape) != (Bsz, Dc, N):
+            raise ValueError("h0 must be [Bsz, Dc, N]")
+        h0 = as_f32(h0, "h0").contiguous()
+    y = torch.empty(Bsz, L, Dc, device=x.device, dtype=x.dtype) if out is None else out
+    need_gpu(y, "out")
+    if y.shape != x.shape or y.dtype != x.dtype:
+        raise ValueError("out must match x in shape and dtype")
+    _inner_unit(y, "out")
+    h_last = torch.empty(Bsz, Dc, N, device=x.device, dtype=torch.float32) if return_state else None
+    ws, stream = _ws(_lib.lib().tssm_selective_scan_bcproj_workspace_bytes(Bsz, L, Dc, N), x,
+                     "selective_scan bc_proj", workspace.SSD)
+    _lib.call("tssm_selective_scan_bcproj", _disc_code(disc), x.data_ptr(), dt.data_ptr(),
+              int(bool(dt_is_tau)), A_log.data_ptr(), W_bc.data_ptr(), W_bc.stride(0), ptr(D),
+              ptr(h0), y.data_ptr(), ptr(h_last), Bsz, L, Dc, N, x.stride(0), x.stride(1),
+              *sdt, y.stride(0), y.stride(1), ws.data_ptr(), ws.numel(), stream)
+    return (y, h_last) if return_state else y
+
+
+def selective_scan_forward(x, dt, A_log, B=None, C=None, D=None, *, chunk=128, disc="zoh",
+                           h0=None, return_state=False, dt_is_tau=False, out=None, dt_proj=None,
+                           bc_proj=None):
     """Mamba-1 selective scan over lanes (channel d, state n).
 
     x      [Bsz, L, Dc]        float32 / bfloat16 / float16
@@ -241,10 +293,20 @@ def selective_scan_forward(x, dt, A_log, B, C, D=None, *, chunk=128, disc="zoh",
            in the scan's load stage as clamp(softplus(dt_raw @ W + bias),
            DT_MIN, DT_MAX) -- dt_project_softplus_kernel
            (discretize_kernel.py:166-213) fused into the scan; rank <= 64
+    bc_proj  W_bc [Dc, 2N] or None (then B and C are None): B_t = x_t W_bc[:, :N]
+           and C_t = x_t W_bc[:, N:] (the input projection's B and C columns)
+           are formed inside the scan (fp32, Dc <= 256, N = 8 or 16)
 
     h_t[d,n] = exp(dt_t a[d,n]) h_{t-1}[d,n] + Bbar_t[d,n] B_t[n] x_t[d];
     y_t[d] = sum_n C_t[n] h_t[d,n] + D[d] x_t[d].
     """
+    if bc_proj is not None:
+        if B is not None or C is not None or dt_proj is not None:
+            raise ValueError("bc_proj replaces B and C (and does not combine with dt_proj)")
+        return _selective_scan_bcproj(x, dt, A_log, bc_proj, D, disc, h0, return_state,
+                                      dt_is_tau, out)
+    if B is None or C is None:
+        raise ValueError("B and C are required unless bc_proj is given")
     for t, w in ((x, "x"), (dt, "dt"), (A_log, "A_log"), (B, "B"), (C, "C")):
         need_gpu(t, w)
     if x.dim() != 3 or B.dim() != 3 or C.shape != B.shape:
