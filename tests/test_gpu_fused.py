@@ -154,9 +154,12 @@ def test_ssd_scan_chunks_and_split(dev, chunk):
 def test_ssd_long_sequence_shape(dev):
     """B=1 L=262144 H=8 P=64 N=16 bf16, log-normal dt (the long-sequence
     workload, the instance the benchmark times).  Heads 0 and 7 are compared
-    with the float64 oracle over all 262144 steps (y and final state); every
-    head is finite; split/resume of the full run at L/2 reproduces the tail."""
+    with the float64 oracle over all 262144 steps (y and final state), and
+    every head, each on its own, with the oracle's fp32 C restatement (itself
+    checked against the float64 oracle on the CPU); split/resume of the full
+    run at L/2 reproduces the tail."""
     import tssm
+    from oracle import cport
     from tssm import ssd_scan_forward, workloads
     w = workloads.ssd_long()
     d = {k: w[k].to(dev) for k in ("x", "dt", "A_log", "B", "C")}
@@ -170,6 +173,16 @@ def test_ssd_long_sequence_shape(dev):
     e = assert_close(y[sl], y_ref, 1e-2, "full-length y, heads 0 and 7")
     assert_close(h[:, heads], h_ref, 1e-3, "final state, heads 0 and 7")
     print(f"ssd long full-length relerr {e:.3e}")
+    y32, h32 = cport.ssd_scan(w["x"].float(), w["dt"], w["A_log"], w["B"].float(),
+                              w["C"].float())
+    H = w["x"].shape[2]
+    yc, hc = y.float().cpu(), h.cpu()
+    errs = [assert_close(yc[:, :, k], y32[:, :, k], 1e-2, f"full-length y, head {k}")
+            for k in range(H)]
+    for k in range(H):
+        assert_close(hc[:, k], h32[:, k], 1e-3, f"final state, head {k}")
+    print("ssd long per-head relerr vs the fp32 restatement: "
+          + " ".join(f"{v:.2e}" for v in errs))
     cut = 131072
     _, h1 = ssd_scan_forward(d["x"][:, :cut], d["dt"][:, :cut], d["A_log"], d["B"][:, :cut],
                              d["C"][:, :cut], None, chunk=256, return_state=True)
@@ -315,14 +328,23 @@ def test_host_flag_reports_an_expired_wait_without_a_sync(dev):
     tssm.check(dev)                                  # the device word was never set
 
 
-def test_ssd_stream_step_config_size(dev):
+@pytest.fixture(scope="module")
+def stream_wl():
+    from tssm import workloads
+    return workloads.ssd_stream()
+
+
+def test_ssd_stream_step_config_size(dev, stream_wl):
     """The streaming workload at its size: 4096 streams, H=32 P=64 N=128, the
     fp32 state [4096,32,64,128] (4 GiB, byte offsets past 2^32) resident and
     updated in place over 50 steps of the benchmark's cycled input pool.  y of
     64 sampled streams (stream 0 and 4095 among them, all 32 heads) is checked
-    against the float64 oracle every step, and their state at the end."""
-    from tssm import ssd_stream_step, workloads
-    w = workloads.ssd_stream()
+    against the float64 oracle every step, and their state at the end; y of
+    every stream is checked against the oracle's fp32 C restatement in the
+    first two steps."""
+    from oracle import cport
+    from tssm import ssd_stream_step
+    w = stream_wl
     S, H, P, N = w["S"], w["H"], w["P"], w["N"]
     A_log = w["A_log"].to(dev)
     pool = [{k: v.to(dev) for k, v in st.items()} for st in w["steps"]]
@@ -331,6 +353,7 @@ def test_ssd_stream_step_config_size(dev):
     idx = torch.cat([torch.tensor([0, S - 1]), torch.randperm(S - 2, generator=g)[:62] + 1])
     idx = torch.sort(idx).values
     st_ref = np.zeros((len(idx), H, P, N))
+    st_all = np.zeros((S, H, P, N), np.float32)
     y = torch.empty(S, H, P, device=dev)
     worst = 0.0
     for step in range(50):
@@ -339,11 +362,55 @@ def test_ssd_stream_step_config_size(dev):
         cpu = w["steps"][step % len(pool)]
         y_ref = O.ssd_stream_step(cpu["x"][idx], cpu["dt"][idx], w["A_log"], cpu["B"][idx],
                                   cpu["C"][idx], None, st_ref)
+        if step < 2:
+            y_all = cport.ssd_stream_step(cpu["x"], cpu["dt"], w["A_log"], cpu["B"], cpu["C"],
+                                          None, st_all)
         torch.cuda.synchronize()
         worst = max(worst, assert_close(y[idx.to(dev)], y_ref, 1e-5, f"stream y step {step}"))
+        if step < 2:
+            yc = y.cpu()
+            for lo in range(0, S, 512):
+                assert_close(yc[lo:lo + 512], y_all[lo:lo + 512], 1e-5,
+                             f"stream y step {step}, streams {lo}..{lo + 511}")
+    del st_all
     assert_close(state[idx.to(dev)], st_ref, 1e-5, "stream state after 50 steps")
     assert torch.isfinite(state[-1, -1]).all()
     print(f"ssd stream config size: worst y relerr over 50 steps {worst:.3e}")
+
+
+def test_ssd_stream_step_full_run(dev, stream_wl):
+    """The streaming workload over its full run length of 10,000 steps (the
+    input pool cycled as the benchmark cycles it): 16 sampled streams (0 and
+    4095 among them) follow the oracle's fp32 C restatement step by step; y is
+    compared every 100 steps and the state after the last step."""
+    from oracle import cport
+    from tssm import ssd_stream_step
+    w = stream_wl
+    S, H, P, N = w["S"], w["H"], w["P"], w["N"]
+    A_log = w["A_log"].to(dev)
+    pool = [{k: v.to(dev) for k, v in st.items()} for st in w["steps"]]
+    g = torch.Generator().manual_seed(45)
+    idx = torch.cat([torch.tensor([0, S - 1]), torch.randperm(S - 2, generator=g)[:14] + 1])
+    idx = torch.sort(idx).values
+    idx_d = idx.to(dev)
+    sub = [{k: np.ascontiguousarray(v[idx].numpy(), dtype=np.float32) for k, v in st.items()}
+           for st in w["steps"]]
+    a32 = w["A_log"].numpy().astype(np.float32)
+    state = torch.zeros(S, H, P, N, device=dev)
+    st_ref = np.zeros((len(idx), H, P, N), np.float32)
+    y = torch.empty(S, H, P, device=dev)
+    worst = 0.0
+    for step in range(10000):
+        s = pool[step % len(pool)]
+        ssd_stream_step(s["x"], s["dt"], A_log, s["B"], s["C"], None, state, out=y)
+        c = sub[step % len(sub)]
+        y_ref = cport.ssd_stream_step(c["x"], c["dt"], a32, c["B"], c["C"], None, st_ref)
+        if step % 100 == 99:
+            worst = max(worst, assert_close(y[idx_d], y_ref, 1e-5, f"stream y step {step}"))
+        if step % 1000 == 999:
+            print(f"stream full run: step {step + 1}, worst y relerr {worst:.3e}", flush=True)
+    assert_close(state[idx_d], st_ref, 1e-5, "stream state after 10000 steps")
+    print(f"ssd stream full run: worst y relerr over 10000 steps {worst:.3e}")
 
 
 @pytest.mark.parametrize("N", [16, 128])
