@@ -427,6 +427,140 @@ __global__ __launch_bounds__(kInterpThreads) void interp_fused_kernel(InterpArgs
   }
 }
 
+// interp_fused_kernel with the workgroup's global loads issued in two rounds
+// instead of one per loop iteration and phase: first every mask vector of the
+// tile's rows t0-K .. t0+TB+K-1 (flags formed exactly as there) and the
+// timestamps of those rows (kept in LDS for the weights), then both
+// neighbours' V of every (step, vector) item of the thread.  No load sits
+// behind a branch (the compiler would sink it there and wait for it alone).
+// Same results as interp_fused_kernel.  LDS: tau [TB+2K] floats, flags
+// [TB+2K] bytes.
+constexpr int kBatMU = 12;  // mask vectors per thread in the first round
+
+template <typename TV, int E, typename TM, int EM>
+__global__ __launch_bounds__(kInterpThreads) void interp_batched_kernel(InterpArgs a, int lvpt) {
+  extern __shared__ __align__(16) unsigned char s_dyn[];
+  __shared__ int s_prev[kInterpTB], s_next[kInterpTB];
+  __shared__ float s_w[kInterpTB];
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.x * kInterpTB;
+  const int64_t tile = blockIdx.y;
+  const int64_t b = a.b0 + blockIdx.z;
+  const int64_t f0 = tile * a.FTILE;
+  const int64_t f1 = f0 + a.FTILE < a.F ? f0 + a.FTILE : a.F;
+  const int K = (int)a.K;
+  const int NR = kInterpTB + 2 * K;
+  float* s_tau = reinterpret_cast<float*>(s_dyn);
+  unsigned char* s_obs = s_dyn + (size_t)NR * 4;
+  const TM* M = reinterpret_cast<const TM*>(a.M) + b * a.smb + f0;
+  const int vpt = 1 << lvpt;
+  const int nitem = NR << lvpt;
+
+  // 1. mask vectors and timestamps.  Invalid items read the tile's first
+  // vector of row 0 (in bounds) and count zero.
+  auto m_item = [&](int q) {
+    const int i = q >> lvpt, j = q & (vpt - 1);
+    const int64_t t = t0 - K + i;
+    const bool ok = q < nitem && t >= 0 && t < a.rows && f0 + (int64_t)j * EM < f1;
+    Lanes<TM, EM> v;
+    v.load(M + (ok ? t * a.smt + (int64_t)j * EM : 0));
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < EM; ++k) s += v.v[k];
+    return ok ? s : 0.0f;
+  };
+  {
+    float sv[kBatMU];
+#pragma unroll
+    for (int u = 0; u < kBatMU; ++u) sv[u] = m_item(tid + u * kInterpThreads);
+    const int64_t rt = t0 - K + tid;
+    const bool tok = tid < NR && rt >= 0 && rt < a.rows;
+    const float tv = ld_any_nb(a.tau, b * a.stb + (tok ? rt : 0) * a.stt, a.td);
+    // tile sums: the xor butterfly of interp_fused_kernel, level by level
+    // over all items so that each level's exchanges issue together
+    for (int o = 1; o < vpt; o <<= 1)
+#pragma unroll
+      for (int u = 0; u < kBatMU; ++u) sv[u] += __shfl_xor(sv[u], o);
+#pragma unroll
+    for (int u = 0; u < kBatMU; ++u) {
+      const int q = tid + u * kInterpThreads;
+      if (q < nitem && (q & (vpt - 1)) == 0) s_obs[q >> lvpt] = sv[u] > 0.5f ? 1 : 0;
+    }
+    if (tid < NR) s_tau[tid] = tok ? tv : 0.0f;
+  }
+  // items beyond the first round (wide tiles or large K); q0 - tid is
+  // uniform, so every lane takes part in the exchanges
+  for (int q0 = tid + kBatMU * kInterpThreads; q0 - tid < nitem; q0 += kInterpThreads) {
+    float x = m_item(q0);
+    for (int o = 1; o < vpt; o <<= 1) x += __shfl_xor(x, o);
+    if (q0 < nitem && (q0 & (vpt - 1)) == 0) s_obs[q0 >> lvpt] = x > 0.5f ? 1 : 0;
+  }
+  for (int i = tid + kInterpThreads; i < NR; i += kInterpThreads) {
+    const int64_t r = t0 - K + i;
+    s_tau[i] = (r >= 0 && r < a.rows) ? ld_any(a.tau, b * a.stb + r * a.stt, a.td) : 0.0f;
+  }
+  __syncthreads();
+  // 2. neighbours and weight per step (as interp_fused_kernel, timestamps from LDS)
+  if (tid < kInterpTB) {
+    const int64_t t = t0 + tid;
+    int prev = -1, next = -1;
+    float w = 0.5f;
+    if (t < a.grid_t) {
+      // nearest first, without a branch per flag (the reads issue together)
+#pragma unroll 8
+      for (int k = 1; k <= K; ++k) {
+        const int fp = s_obs[tid + K - k], fn = s_obs[tid + K + k];
+        prev = (prev < 0 && fp) ? (int)(t - k) : prev;
+        next = (next < 0 && fn) ? (int)(t + k) : next;
+      }
+      const float tau_t = s_tau[tid + K];
+      const float tp = prev >= 0 ? s_tau[prev - (t0 - K)] : 0.0f;
+      const float tn = next >= 0 ? s_tau[next - (t0 - K)] : 0.0f;
+      const float den = tn - tp;
+      w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
+      w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
+    }
+    s_prev[tid] = prev;
+    s_next[tid] = next;
+    s_w[tid] = w;
+  }
+  __syncthreads();
+  // 3. interpolation, every item's two loads issued before the first use
+  const TV* V = reinterpret_cast<const TV*>(a.V) + b * a.svb + f0;
+  TV* O = reinterpret_cast<TV*>(a.Vhat) + b * a.sob + f0;
+  const int tmax = (int)((a.grid_t - t0) < kInterpTB ? (a.grid_t - t0) : kInterpTB);
+  const int ng = (int)((f1 - f0) / E);
+  const int total = tmax * ng;
+  constexpr int U = 32 / E;  // 32 values of each neighbour in flight per thread
+  for (int q0 = tid; q0 < total; q0 += U * kInterpThreads) {
+    Lanes<TV, E> vp[U], vn[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int q = q0 + u * kInterpThreads;
+      const int i = q < total ? q / ng : 0;  // items past the end load row t0's first vector
+      const int j = q < total ? q - i * ng : 0;
+      const int prev = s_prev[i], next = s_next[i];
+      const int64_t rp = prev >= 0 ? prev : (next >= 0 ? next : t0 + i);
+      const int64_t rn = next >= 0 ? next : rp;
+      vp[u].load(V + rp * a.svt + (int64_t)j * E);
+      vn[u].load(V + rn * a.svt + (int64_t)j * E);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int q = q0 + u * kInterpThreads;
+      if (q >= total) continue;
+      const int i = q / ng, j = q - (q / ng) * ng;
+      const bool both = s_prev[i] >= 0 && s_next[i] >= 0;
+      const float w = s_w[i];
+      Lanes<TV, E> o;
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        o.v[e] = both ? lerp_pair(vp[u].v[e], vn[u].v[e], w) : vp[u].v[e];
+      o.store(O + (t0 + i) * a.sot + (int64_t)j * E);
+    }
+  }
+}
+
 // fused_interp_ssm_step_kernel: one workgroup per (b, tile) at step t_cur.
 struct StepArgs {
   const void* V;
@@ -694,31 +828,37 @@ __global__ __launch_bounds__(kInterpThreads) void interp_corrected_staged_kernel
     const int64_t f0 = (int64_t)blockIdx.y * 64 + c4;
     const float* Vq = reinterpret_cast<const float*>(a.V) + b * a.svb + f0;
     const float* Mq = reinterpret_cast<const float*>(a.M) + b * a.smb + f0;
+    // No load sits behind a branch (the compiler would sink it into the
+    // branch and wait for it alone): positions past the window take the
+    // window's last row, loading and storing exactly what its own lanes do.
+    // the first timestamps load with the first batch of rows
+    const int64_t tt = t0 - K + tid;
+    const bool tok = tid < nrow && tt >= 0 && tt < a.T;
+    const float tv = ld_any_nb(a.tau, b * a.stb + (tok ? tt : 0) * a.stt, a.td);
     for (int q0 = 0; q0 * 4 * NW < nrow; q0 += kCorrBatch) {
-      float4 mv[kCorrBatch], vv[kCorrBatch];
+      f32x4 mv[kCorrBatch], vv[kCorrBatch];
 #pragma unroll
-      for (int q = 0; q < kCorrBatch; ++q) {  // rows out of range read row 0, discarded below
-        const int i = 4 * (wave + NW * (q0 + q)) + rl;
+      for (int q = 0; q < kCorrBatch; ++q) {  // rows outside [0, T) read row 0 (flags 0)
+        const int i = min(4 * (wave + NW * (q0 + q)) + rl, nrow - 1);
         const int64_t t = t0 - K + i;
         const int64_t tc = (t >= 0 && t < a.T) ? t : 0;
-        mv[q] = *reinterpret_cast<const float4*>(Mq + tc * a.smt);
-        vv[q] = *reinterpret_cast<const float4*>(Vq + tc * a.svt);
+        mv[q] = *reinterpret_cast<const f32x4*>(Mq + tc * a.smt);
+        vv[q] = *reinterpret_cast<const f32x4*>(Vq + tc * a.svt);
       }
 #pragma unroll
       for (int q = 0; q < kCorrBatch; ++q) {
-        const int i = 4 * (wave + NW * (q0 + q)) + rl;
-        if (i < nrow) {
-          const int64_t t = t0 - K + i;
-          const bool in = t >= 0 && t < a.T;
-          const uint32_t fl = in ? ((mv[q].x > 0.5f ? 1u : 0u) | (mv[q].y > 0.5f ? 0x100u : 0u) |
-                                    (mv[q].z > 0.5f ? 0x10000u : 0u) | (mv[q].w > 0.5f ? 0x1000000u : 0u))
-                                 : 0u;
-          *reinterpret_cast<uint32_t*>(&s_obs[i][c4]) = fl;
-          *reinterpret_cast<float4*>(&s_v[i][c4]) = vv[q];
-        }
+        const int i = min(4 * (wave + NW * (q0 + q)) + rl, nrow - 1);
+        const int64_t t = t0 - K + i;
+        const bool in = t >= 0 && t < a.T;
+        const uint32_t fl = in ? ((mv[q][0] > 0.5f ? 1u : 0u) | (mv[q][1] > 0.5f ? 0x100u : 0u) |
+                                  (mv[q][2] > 0.5f ? 0x10000u : 0u) | (mv[q][3] > 0.5f ? 0x1000000u : 0u))
+                               : 0u;
+        *reinterpret_cast<uint32_t*>(&s_obs[i][c4]) = fl;
+        *reinterpret_cast<f32x4*>(&s_v[i][c4]) = vv[q];
       }
     }
-    for (int i = tid; i < nrow; i += kInterpThreads) {
+    if (tid < nrow) s_tau[tid] = tok ? tv : 0.0f;
+    for (int i = tid + kInterpThreads; i < nrow; i += kInterpThreads) {
       const int64_t t = t0 - K + i;
       s_tau[i] = (t >= 0 && t < a.T) ? ld_any(a.tau, b * a.stb + t * a.stt, a.td) : 0.0f;
     }
@@ -840,6 +980,8 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
   const size_t lds_interp = (size_t)(kInterpTB + 2 * K);
   TSSM_CHECK(K <= kMaxLds && (int64_t)lds_interp + 3 * kInterpTB * 4 <= kMaxLds,
              TSSM_ERR_UNSUPPORTED);
+  // interp_batched_kernel adds the window's timestamps (while they fit)
+  const size_t lds_batched = lds_interp * 5;
   const int64_t ntile = (F + FTILE - 1) / FTILE;
   const int64_t gf = grid_f < ntile ? grid_f : ntile;
   if (grid_b == 0 || grid_t == 0 || gf == 0) return TSSM_OK;
@@ -870,9 +1012,13 @@ extern "C" int tssm_time_aware_interp(int v_dtype, int m_dtype, int tau_dtype, c
       const int64_t nb = grid_b - b0 < kMaxGridYZ ? grid_b - b0 : kMaxGridYZ;
       const dim3 grid((unsigned)((grid_t + kInterpTB - 1) / kInterpTB), (unsigned)gf,
                       (unsigned)nb);
-#define TSSM_FUSED(TT, EE, MT, ME)                                                         \
-  hipLaunchKernelGGL((interp_fused_kernel<TT, EE, MT, ME>), grid, dim3(kInterpThreads), \
-                     lds_interp, s, a, lvpt)
+#define TSSM_FUSED(TT, EE, MT, ME)                                                             \
+  if ((int64_t)lds_batched + 3 * kInterpTB * 4 <= kMaxLds)                                  \
+    hipLaunchKernelGGL((interp_batched_kernel<TT, EE, MT, ME>), grid, dim3(kInterpThreads), \
+                       lds_batched, s, a, lvpt);                                            \
+  else                                                                                      \
+    hipLaunchKernelGGL((interp_fused_kernel<TT, EE, MT, ME>), grid, dim3(kInterpThreads),   \
+                       lds_interp, s, a, lvpt)
 #define TSSM_FUSED_M(TT, EE)                                      \
   switch (m_dtype) {                                              \
     case TSSM_F32: TSSM_FUSED(TT, EE, float, 4); break;            \

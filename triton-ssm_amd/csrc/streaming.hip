@@ -173,28 +173,24 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_kernel(Ring
 }
 
 // 16-byte form (BLOCK_H = 4 LPT with LPT in 4 .. 64; H % 4 == 0; aligned
-// rows): a lane owns 4 adjacent features, LPT lanes one tile, so a wave
-// instruction covers 64 / LPT tiles.  Same steps as stream_interp_step_kernel:
-// insert, then per tile the new mask sum (an LPT-lane group sum), the ring
-// searched (all slots at once) only when some tile of the wave has no new
-// observation, and the in-place step.
+// rows, KRING - 1 <= kRingFast): a lane owns 4 adjacent features, LPT lanes
+// one tile, so a wave instruction covers 64 / LPT tiles.  Same steps as
+// stream_interp_step_kernel, with every load of a thread issued before the
+// first wait: per tile the new observation (inserted into the ring by the
+// lanes that own its features: a lane's tile loop covers exactly the features
+// the insert loop would give it), the new mask sum (an LPT-lane group sum),
+// the ring searched (all slots at once) only when some tile of the wave has no
+// new observation, and the in-place step.  Ring slots are uniform and formed
+// once, without 64-bit divisions.
 template <int LPT>
 __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_vec_kernel(RingArgs a) {
   constexpr int TPW = 64 / LPT;  // tiles per wave instruction
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   constexpr int nwaves = kStreamThreads / 64;
-  const int64_t KR = a.KRING;
-  const int64_t head = a.ring_head[b];
-  const int64_t nh = (head + 1) % KR;                                    // :107
+  const int KR = (int)a.KRING;
   float* rV = a.ring_V + b * a.srb;
   float* rM = a.ring_M + b * a.srb;
-  for (int64_t k = 4 * (int64_t)tid; k < a.H; k += 4 * kStreamThreads) {  // :110-114
-    *reinterpret_cast<float4*>(rV + nh * a.srk + k) =
-        *reinterpret_cast<const float4*>(a.v_new + b * a.svb + k);
-    *reinterpret_cast<float4*>(rM + nh * a.srk + k) =
-        *reinterpret_cast<const float4*>(a.m_new + b * a.svb + k);
-  }
   const int64_t ntile = (a.H + a.BLOCK_H - 1) / a.BLOCK_H;
   for (int64_t tg = (int64_t)wave * TPW; tg < ntile; tg += nwaves * TPW) {
     const int64_t tile = tg + lane / LPT;
@@ -209,17 +205,29 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_vec_kernel(
     ld_lanes<float, 4>(a.Abar + fs, ab);
     ld_lanes<float, 4>(a.Bbar + fs, bb);
     ld_lanes<float, 4>(a.D + fs, dv);
+    // the head is read here, after this tile's loads (volatile: read in the
+    // loop, so its wait is not hoisted ahead of them)
+    const int32_t head = *reinterpret_cast<const volatile int32_t*>(a.ring_head + b);
+    const int nh = (int)((((int64_t)head + 1) % KR + KR) % KR);            // :107
+    if (act) {  // insert the new observation (:110-114)
+      st_lanes<float, 4>(rV + nh * a.srk + f, vn);
+      st_lanes<float, 4>(rM + nh * a.srk + f, mn);
+    }
     const float sm = group_sum<LPT>(act ? (mn[0] + mn[1]) + (mn[2] + mn[3]) : 0.0f);
     const bool need = act && sm < 0.5f;  // same on every lane of the tile
     float v[4] = {vn[0], vn[1], vn[2], vn[3]};
     if (__ballot(need) != 0) {  // uniform
+      int slot[kRingFast];  // slot of the observation k steps back, nearest first
+#pragma unroll
+      for (int k = 1; k <= kRingFast; ++k) {
+        const int kk = k < KR ? k : KR - 1;  // clamped, ignored below
+        slot[k - 1] = nh - kk < 0 ? nh - kk + KR : nh - kk;
+      }
       float ms[kRingFast];
 #pragma unroll
       for (int k = 1; k <= kRingFast; ++k) {
-        const int64_t kk = k < KR ? k : KR - 1;  // clamped, zeroed below
-        const int64_t rk = (nh - kk + KR) % KR;
         float m[4];
-        ld_lanes<float, 4>(rM + rk * a.srk + fs, m);
+        ld_lanes<float, 4>(rM + slot[k - 1] * a.srk + fs, m);
         ms[k - 1] = (act && k < KR) ? (m[0] + m[1]) + (m[2] + m[3]) : 0.0f;
       }
 #pragma unroll
@@ -227,7 +235,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_vec_kernel(
       int prev_k = -1;  // nearest earlier slot whose tile has any observation (:124-130)
 #pragma unroll
       for (int k = kRingFast; k >= 1; --k)
-        if (k < KR && ms[k - 1] > 0.5f) prev_k = (int)((nh - k + KR) % KR);
+        if (k < KR && ms[k - 1] > 0.5f) prev_k = slot[k - 1];
       if (need && prev_k >= 0) ld_lanes<float, 4>(rV + prev_k * a.srk + fs, v);  // :133,143
     }
     if (act) {
@@ -243,6 +251,7 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_vec_kernel(
   }
   __syncthreads();  // every wave has read the head before it advances
   if (tid == 0) {
+    const int nh = (int)((((int64_t)a.ring_head[b] + 1) % KR + KR) % KR);
     a.ring_tau[b * KR + nh] = a.tau_new[b];                              // :116
     a.ring_head[b] = (int32_t)nh;                                        // :117
   }
@@ -303,54 +312,61 @@ __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_corrected_k
 // the search -- v_new, m_new, h, the parameters and the masks of all previous
 // slots -- at once; only V of the chosen slots follows.  Same results as the
 // kernel above.
-__device__ inline float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-__device__ inline void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
-__device__ inline float comp(const float4& v, int e) {
-  return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
-}
+__device__ inline f32x4 ld4v(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ inline void st4v(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
 __global__ __launch_bounds__(kStreamThreads) void stream_interp_step_corrected_vec_kernel(RingArgs a) {
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
-  const int64_t KR = a.KRING;
-  const int64_t nh = (a.ring_head[b] + 1) % KR;
+  const int KR = (int)a.KRING;  // KRING - 1 <= kRingFast (host)
+  const int nh = (int)((((int64_t)a.ring_head[b] + 1) % KR + KR) % KR);
+  // slots of the previous observations, nearest first (uniform; k past
+  // KRING - 1 repeats the last one and is ignored below)
+  int slot[kRingFast];
+#pragma unroll
+  for (int k = 1; k <= kRingFast; ++k) {
+    const int kk = k < KR ? k : KR - 1;
+    slot[k - 1] = nh - kk < 0 ? nh - kk + KR : nh - kk;
+  }
   float* rV = a.ring_V + b * a.srb;
   float* rM = a.ring_M + b * a.srb;
   for (int64_t f = 4 * tid; f < a.H; f += 4 * kStreamThreads) {
-    const float4 vn = ld4(a.v_new + b * a.svb + f);
-    const float4 mn = ld4(a.m_new + b * a.svb + f);
-    const float4 hp = ld4(a.h + b * a.shb + f);
-    const float4 ab = ld4(a.Abar + f), bb = ld4(a.Bbar + f), dd = ld4(a.D + f);
-    const float4 cc = ld4(a.C + b * a.scb + f);
-    float4 ms[kRingFast];
+    const f32x4 vn = ld4v(a.v_new + b * a.svb + f);
+    const f32x4 mn = ld4v(a.m_new + b * a.svb + f);
+    const f32x4 hp = ld4v(a.h + b * a.shb + f);
+    const f32x4 ab = ld4v(a.Abar + f), bb = ld4v(a.Bbar + f), dd = ld4v(a.D + f);
+    const f32x4 cc = ld4v(a.C + b * a.scb + f);
+    f32x4 ms[kRingFast];
 #pragma unroll
-    for (int k = 1; k <= kRingFast; ++k) {
-      const int64_t kk = k < KR ? k : KR - 1;  // clamped, ignored below
-      ms[k - 1] = ld4(rM + ((nh - kk + KR) % KR) * a.srk + f);
-    }
-    st4(rV + nh * a.srk + f, vn);  // the new slot: not among the slots searched
-    st4(rM + nh * a.srk + f, mn);
-    float v[4];
+    for (int k = 0; k < kRingFast; ++k) ms[k] = ld4v(rM + slot[k] * a.srk + f);
+    st4v(rV + nh * a.srk + f, vn);  // the new slot: not among the slots searched
+    st4v(rM + nh * a.srk + f, mn);
+    // per element the nearest observed slot; the four neighbour loads issue
+    // together (an unused one reads v_new, in bounds)
+    const float* src[4];
+    bool fill[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      int64_t hit = -1;
+      int hit = -1;
 #pragma unroll
-      for (int k = kRingFast; k >= 1; --k)  // nearest observed slot kept
-        if (k < KR && comp(ms[k - 1], e) > 0.5f) hit = (nh - k + KR) % KR;
-      v[e] = comp(vn, e);
-      if (!(comp(mn, e) > 0.5f) && hit >= 0) v[e] = rV[hit * a.srk + f + e];
+      for (int k = kRingFast; k >= 1; --k)
+        if (k < KR && ms[k - 1][e] > 0.5f) hit = slot[k - 1];
+      fill[e] = !(mn[e] > 0.5f) && hit >= 0;
+      src[e] = fill[e] ? rV + hit * a.srk + f + e : a.v_new + b * a.svb + f + e;
     }
-    float4 hn, yo;
-    hn.x = ab.x * hp.x + bb.x * v[0];
-    hn.y = ab.y * hp.y + bb.y * v[1];
-    hn.z = ab.z * hp.z + bb.z * v[2];
-    hn.w = ab.w * hp.w + bb.w * v[3];
-    yo.x = cc.x * hn.x + dd.x * v[0];
-    yo.y = cc.y * hn.y + dd.y * v[1];
-    yo.z = cc.z * hn.z + dd.z * v[2];
-    yo.w = cc.w * hn.w + dd.w * v[3];
-    st4(a.h + b * a.shb + f, hn);
-    st4(a.y + b * a.svb + f, yo);
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = *src[e];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = fill[e] ? v[e] : vn[e];
+    f32x4 hn, yo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hn[e] = ab[e] * hp[e] + bb[e] * v[e];
+      yo[e] = cc[e] * hn[e] + dd[e] * v[e];
+    }
+    st4v(a.h + b * a.shb + f, hn);
+    st4v(a.y + b * a.svb + f, yo);
   }
   __syncthreads();  // every thread has read the head before it advances
   if (tid == 0) {
