@@ -352,12 +352,13 @@ __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
   const float* xr = a.x + s * a.sx_s + h * a.sx_h;
   for (int64_t p0 = 0; p0 < a.P; p0 += RPP * kStreamPB) {
     f32x4 v[kStreamPB];
-    float xv[kStreamPB];
+    float xv[kStreamPB], dv[kStreamPB];
 #pragma unroll
     for (int u = 0; u < kStreamPB; ++u) {
       const int64_t p = p0 + u * RPP + rp;
       const int64_t pc = p < a.P ? p : a.P - 1;
       xv[u] = xr[pc];
+      dv[u] = HAS_D ? a.D[h * a.P + pc] : 0.0f;  // with the batch, not behind the store's branch
       v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(st + pc * a.N + ng * 4));
     }
 #pragma unroll
@@ -374,7 +375,7 @@ __global__ __launch_bounds__(256) void ssd_stream_step_kernel(StreamArgs a) {
       // sum over the NG threads of the row (aligned lane groups)
       for (int o = NG / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
       if (ng == 0 && p < a.P) {
-        if (HAS_D) acc = __builtin_fmaf(a.D[h * a.P + p], xv[u], acc);
+        if (HAS_D) acc = __builtin_fmaf(dv[u], xv[u], acc);
         a.y[s * a.sy_s + h * a.sy_h + p] = acc;
       }
     }
