@@ -605,9 +605,11 @@ __global__ void mh_fwd_local_kernel(const T* __restrict__ u, const float* __rest
   const int64_t ts = blk * blk_l;
   const int64_t te = ts + blk_l > L ? L : ts + blk_l;
   const int64_t rows_tot = nbatch * nh * hd;
-  // kB steps' loads are issued before any is used (clamped to the block's
-  // last step, whose duplicates are never stored): one load round trip per
-  // kB steps instead of one per step.  exp(d a) as hardware exp2 of d a log2e.
+  // The loads of a step are issued kB steps before it is computed: after each
+  // step its registers are refilled with step t + kB (clamped to the block's
+  // last step, whose duplicates are never used), so the wave streams instead
+  // of alternating a load round trip with kB steps of compute.  exp(d a) as
+  // hardware exp2 of d a log2e.
   constexpr int kB = 8;
   for (int64_t p = threadIdx.x; p < hd; p += blockDim.x) {
     const float a2 = -expf(A_log[hi * sal_h + p]) * kLog2e;
@@ -619,24 +621,32 @@ __global__ void mh_fwd_local_kernel(const T* __restrict__ u, const float* __rest
     float* lap = loc_a + bi * (L * nh * hd) + hi * hd + p;
     float* lxp = loc_x + bi * (L * nh * hd) + hi * hd + p;
     float ar = 1.0f, xr = 0.0f;
+    float dv[kB], bv[kB], uv[kB];
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int64_t t = ts + k < te ? ts + k : te - 1;
+      dv[k] = dtp[t * sdt_l];
+      bv[k] = ldf(bp + t * sB_l);
+      uv[k] = ldf(up + t * su_l);
+    }
     for (int64_t t0 = ts; t0 < te; t0 += kB) {
-      float dv[kB], bv[kB], uv[kB];
 #pragma unroll
       for (int k = 0; k < kB; ++k) {
-        const int64_t t = t0 + k < te ? t0 + k : te - 1;
-        dv[k] = dtp[t * sdt_l];
-        bv[k] = ldf(bp + t * sB_l);
-        uv[k] = ldf(up + t * su_l);
-      }
-#pragma unroll
-      for (int k = 0; k < kB; ++k) {
-        if (t0 + k >= te) break;  // uniform
-        const float ab = exp2_fast(dv[k] * a2);
-        xr = ab * xr + dv[k] * bv[k] * (u_ok ? uv[k] : 0.0f);
-        ar = ab * ar;
-        const int64_t off = (t0 + k) * (nh * hd);
-        lap[off] = ar;
-        lxp[off] = xr;
+        const int64_t t = t0 + k;
+        if (t < te) {  // uniform
+          const float ab = exp2_fast(dv[k] * a2);
+          xr = ab * xr + dv[k] * bv[k] * (u_ok ? uv[k] : 0.0f);
+          ar = ab * ar;
+          const int64_t off = t * (nh * hd);
+          lap[off] = ar;
+          lxp[off] = xr;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const int64_t tn = t + kB < te ? t + kB : te - 1;
+        dv[k] = dtp[tn * sdt_l];
+        bv[k] = ldf(bp + tn * sB_l);
+        uv[k] = ldf(up + tn * su_l);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     const int64_t rf = bi * (nh * hd) + hi * hd + p;
