@@ -825,6 +825,31 @@ def main():
         f"per-step events p50 {statistics.median(per) * 1e3:.1f} us, "
         f"min {min(per) * 1e3:.1f} us")
 
+    # A device copy (torch's copy_) moving the same bytes per step (half read,
+    # half written), over as many rotated buffer sets and timed the same way:
+    # what a plain streaming kernel of this size reaches on this box.
+    copy_ref = None
+    if not wl.get("valu") and wl["bytes"] <= (2 << 30):
+        half = max(1024, int(wl["bytes"]) // 8)
+        bufs = [(torch.empty(half, device=dev).uniform_(), torch.empty(half, device=dev))
+                for _ in range(max(1, args.sets))]
+        real_step = step
+
+        def step(i):  # noqa: F811 -- the copy stands in for the workload's step
+            src, dst = bufs[i % len(bufs)]
+            dst.copy_(src)
+
+        for i in range(args.warmup):
+            step(i)
+        copy_total, _ = timed(False)
+        step = real_step
+        del bufs
+        copy_ms = copy_total / args.steps
+        copy_gbs = wl["bytes"] / (copy_ms * 1e-3) / 1e9
+        copy_ref = {"ms_per_step": copy_ms, "achieved": copy_gbs, "unit": "GB/s",
+                    "frac": copy_gbs / PEAK_GBS, "kernel_vs_copy": copy_ms / ms_per_step}
+        log(f"device copy of the same bytes: {copy_ms * 1e3:.1f} us/step, {copy_gbs:.0f} GB/s")
+
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline ...")
@@ -855,6 +880,7 @@ def main():
             "traffic": traffic_from_profile(wl.get("traffic")),
             "algorithmic_bytes_per_launch": wl["bytes"],
             "kernel_avg_us": kern_ms * 1e3,
+            "copy_reference": copy_ref,
         },
         "cpu_baseline": cpu,
         "p50_step_ms": statistics.median(per),
