@@ -391,6 +391,94 @@ def _wl_bcproj(args, dev, fused):
                         "B": B, "L": L, "D": Dc, "N": N})
 
 
+def _wl_xproj(args, dev, fused):
+    """Mamba-1 scan with the whole input projection x -> (dt, B, C): x_dbl =
+    x W_x split into dt_raw (rank 16), B and C, dt = clamp(softplus(dt_raw W_dt
+    + bias)), at B=16 L=2048 D=256 N=16 fp32: formed inside the scan
+    (x_proj=), or as a matmul producing x_dbl, then the scan with the dt
+    projection (dt_proj=) reading the dt_raw columns and B/C copied out."""
+    import math
+    import torch
+    from tssm import selective_scan_forward, workloads
+    w = workloads.interp_mamba1()
+    g = torch.Generator().manual_seed(1007)
+    B, L, Dc = w["V"].shape
+    N = w["A_log"].shape[1]
+    R = 16
+    x0 = torch.randn(B, L, Dc, generator=g)
+    W_x = (torch.randn(Dc, R + 2 * N, generator=g) / Dc ** 0.5).to(dev)
+    W_dt = (torch.randn(R, Dc, generator=g) * (0.5 / R ** 0.5)).to(dev)
+    bias = (math.log(math.expm1(0.05)) + torch.empty(Dc).uniform_(-0.5, 0.5, generator=g)).to(dev)
+    dmin, dmax = 1e-3, 0.5
+    A_log = w["A_log"].to(dev)
+    sets = []
+    for i in range(max(args.sets, 3)):
+        st = {"x": torch.roll(x0, shifts=i, dims=0).contiguous().to(dev)}
+        st["y"] = torch.empty_like(st["x"])
+        st["xdbl"] = torch.empty(B, L, R + 2 * N, device=dev)
+        st["raw"] = torch.empty(B, L, R, device=dev)
+        st["Bm"] = torch.empty(B, L, N, device=dev)
+        st["Cm"] = torch.empty(B, L, N, device=dev)
+        sets.append(st)
+
+    def step(i):
+        d = sets[i % len(sets)]
+        if fused:
+            selective_scan_forward(d["x"], None, A_log, None, None, None, disc=args.disc,
+                                   out=d["y"], x_proj=(W_x, W_dt, bias, dmin, dmax))
+        else:
+            torch.matmul(d["x"], W_x, out=d["xdbl"])
+            d["raw"].copy_(d["xdbl"][..., :R])
+            d["Bm"].copy_(d["xdbl"][..., R:R + N])
+            d["Cm"].copy_(d["xdbl"][..., R + N:])
+            selective_scan_forward(d["x"], d["raw"], A_log, d["Bm"], d["Cm"], None,
+                                   disc=args.disc, out=d["y"],
+                                   dt_proj=(W_dt, bias, dmin, dmax))
+
+    def cpu():
+        import numpy as np
+        from oracle import cport
+        x = _np32(x0)
+        Wn, Wd, bn = _np32(W_x.cpu()), _np32(W_dt.cpu()), _np32(bias.cpu())
+        Al = _np32(w["A_log"])
+
+        def run():
+            xd = x @ Wn
+            acc = xd[..., :R] @ Wd + bn
+            dt = np.clip(np.logaddexp(0.0, acc), dmin, dmax).astype(np.float32)
+            cport.selective_scan(x, dt, Al, np.ascontiguousarray(xd[..., R:R + N]),
+                                 np.ascontiguousarray(xd[..., R + N:]), None, disc=args.disc)
+        med = _timed_cpu(run, args.cpu_reps)
+        return {"value": B * L * Dc / med, "unit": "elements/s", "cores": cport.threads(),
+                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                                          f"{med:.3f} s each"}
+
+    n = B * L * Dc
+    nbytes = 4 * (2 * n + Dc * N + Dc * (R + 2 * N) + R * Dc + Dc)  # x, y, A_log, W_x, W_dt, bias
+    how = "formed in the scan" if fused else "matmul, then the scan with the dt projection"
+    valu = {"lane_updates": n * N, "ops_per_update": 9, "exp2_per_update": 2}
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes, valu=valu,
+                kernel="sel_bcproj_state_kernel (x -> dt, B, C) + sel_carry_kernel + "
+                       "sel_output_kernel" if fused
+                else "matmul (x_dbl), copies, sel_chunk_state_kernel (dt projected), "
+                     "sel_carry_kernel, sel_output_kernel",
+                metric=f"Mamba-1 scan with dt, B, C from x ({how}) elements/sec, B=16 L=2048 "
+                       "D=256 N=16 R=16 fp32",
+                unit="elements/s",
+                config={"workload": f"x_dbl = x W_x -> dt_raw, B, C; dt = clamp(softplus(dt_raw "
+                                    f"W_dt + bias)) ({how}) + Mamba-1 scan, B=16 L=2048 D=256 "
+                                    f"N=16 R=16 fp32, {args.disc.upper()}",
+                        "B": B, "L": L, "D": Dc, "N": N, "R": R})
+
+
+def wl_xproj(args, dev):
+    return _wl_xproj(args, dev, True)
+
+
+def wl_xproj_unfused(args, dev):
+    return _wl_xproj(args, dev, False)
+
+
 def wl_bcproj(args, dev):
     return _wl_bcproj(args, dev, True)
 
@@ -716,6 +804,7 @@ def rows_sweep(args, dev):
 
 
 WORKLOADS = {"bcproj": wl_bcproj, "bcproj_two_launch": wl_bcproj_two_launch,
+             "xproj": wl_xproj, "xproj_unfused": wl_xproj_unfused,
              "multihead": wl_multihead, "mamba1_small": wl_mamba1_small,
              "interp_mamba1": wl_interp_mamba1, "ssd_long": wl_ssd_long,
              "ssd_config1": wl_ssd_config1,

@@ -464,6 +464,31 @@ int tssm_selective_scan_bcproj(int disc, const float* x, const float* dt, int dt
                                int64_t sy_b, int64_t sy_l, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/* tssm_selective_scan with the whole selective input projection in the
+ * scan, x -> (dt, B, C): x_dbl_t = x_t W_x (Mamba-1's x_proj; the reference
+ * has no kernel for it), dt_raw = x_dbl[:, :rank], B = x_dbl[:, rank:rank+N],
+ * C = x_dbl[:, rank+N:rank+2N], and dt = clamp(softplus(dt_raw W_dt + bias),
+ * dt_min, dt_max) as dt_project_softplus_kernel computes it
+ * (discretize_kernel.py:166-213).  W_x f32 [Dc, rank + 2N], row stride swx_d
+ * (>= rank + 2N), unit column stride; W_dt f32 [rank][Dc], row stride sw_r
+ * (>= Dc, a multiple of 4), bias [Dc]; rank 16, 32, 48 or 64.  fp32 x/y,
+ * Dc <= 256 and a multiple of 4, N 8 or 16, x rows and W_dt, bias, A_log
+ * 16-byte aligned.  Three launches: pass 1 stages each 32-step chunk's x tile
+ * in LDS, forms its dt_raw/B/C rows on the fp32 matrix cores, then every
+ * channel's dt (stored to a dt table in the workspace) and runs the
+ * recurrence; pass 3 reads the dt table and the C rows.  Workspace of
+ * tssm_selective_scan_xproj_workspace_bytes() bytes (raw fp32, not look-back
+ * words).  No reference counterpart. */
+int64_t tssm_selective_scan_xproj_workspace_bytes(int64_t nbatch, int64_t L, int64_t Dc,
+                                                  int64_t N);
+int tssm_selective_scan_xproj(int disc, const float* x, const float* A_log, const float* W_x,
+                              int64_t swx_d, int64_t rank, const float* W_dt, int64_t sw_r,
+                              const float* bias, float dt_min, float dt_max, const float* D,
+                              const float* h0, float* y, float* h_last, int64_t nbatch, int64_t L,
+                              int64_t Dc, int64_t N, int64_t sx_b, int64_t sx_l, int64_t sy_b,
+                              int64_t sy_l, void* workspace, int64_t workspace_bytes,
+                              void* stream);
+
 /* ------------------------------------------------------------------ elementwise scan, single pass
  * The host functions ssm_forward / ssm_backward (ssm_scan.py:239-289) as one
  * launch each over contiguous [B, L, H] tensors of `dtype` (D [H]): every

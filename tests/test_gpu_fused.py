@@ -654,6 +654,56 @@ def test_selective_scan_bcproj(dev, Dc, N, L, Bsz, dt_mode, extras, sliced):
     print(f"bcproj Dc={Dc} N={N} {dt_mode}: relerr {e:.2e}")
 
 
+@pytest.mark.parametrize("Dc,N,L,Bsz,R,extras,sliced", [
+    (256, 16, 2048, 4, 16, False, False),   # Mamba-1 at D = 256: dt rank D / 16
+    (100, 8, 333, 3, 32, True, False),      # ragged channels and steps, D, h0
+    (64, 16, 700, 2, 64, True, True),       # W_x as a column slice of a wider weight
+])
+def test_selective_scan_xproj(dev, Dc, N, L, Bsz, R, extras, sliced):
+    """The whole input projection inside the scan (x_proj=): x_dbl = x W_x split
+    into dt_raw, B and C, dt = clamp(softplus(dt_raw W_dt + bias)), against the
+    float64 oracle (its projection and dt_project_softplus fed float64
+    products) and against the unfused path (torch.matmul for x_dbl, then the
+    scan with dt_proj= over the dt_raw columns and the B/C columns)."""
+    from tssm import selective_scan_forward
+    g = torch.Generator().manual_seed(Dc + N + L + R)
+    x = torch.randn(Bsz, L, Dc, generator=g)
+    wide = torch.randn(Dc, R + 2 * N + (8 if sliced else 0), generator=g) / Dc ** 0.5
+    W_x = wide[:, :R + 2 * N]
+    W_dt = torch.randn(R, Dc, generator=g) * (0.5 / R ** 0.5)
+    bias = float(np.log(np.expm1(0.05))) + torch.empty(Dc).uniform_(-0.5, 0.5, generator=g)
+    dt_min, dt_max = 1e-3, 0.5
+    A_log = torch.empty(Dc, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    D = torch.randn(Dc, generator=g) if extras else None
+    h0 = torch.randn(Bsz, Dc, N, generator=g) if extras else None
+    xd, Ad = x.to(dev), A_log.to(dev)
+    Wxd = wide.to(dev)[:, :R + 2 * N] if sliced else W_x.contiguous().to(dev)
+    if sliced:
+        assert Wxd.stride(0) == R + 2 * N + 8
+    Wdt, bd = W_dt.to(dev), bias.to(dev)
+    Dd = D.to(dev) if extras else None
+    h0d = h0.to(dev) if extras else None
+    xp = (Wxd, Wdt, bd, dt_min, dt_max)
+    y, h = selective_scan_forward(xd, None, Ad, None, None, Dd, h0=h0d, return_state=True,
+                                  x_proj=xp)
+    xdbl = (xd @ Wxd).contiguous()
+    raw = xdbl[..., :R].contiguous()
+    Bg, Cg = xdbl[..., R:R + N].contiguous(), xdbl[..., R + N:].contiguous()
+    y2, h2 = selective_scan_forward(xd, raw, Ad, Bg, Cg, Dd, h0=h0d, return_state=True,
+                                    dt_proj=(Wdt, bd, dt_min, dt_max))
+    torch.cuda.synchronize()
+    x64 = x.double() @ W_x.double()
+    dt_ref = O.dt_project_softplus(x64[..., :R], W_dt, bias, dt_min, dt_max)
+    y_ref, h_ref = O.selective_scan(x, dt_ref, A_log, x64[..., R:R + N], x64[..., R + N:], D,
+                                    h0=None if h0 is None else np64(h0))
+    e = assert_close(y, y_ref, 1e-5, f"xproj y Dc={Dc} N={N} R={R}")
+    assert_close(h, h_ref, 1e-5, "xproj h_last")
+    assert_close(y, y2, 1e-5, "xproj vs matmul + dt_proj scan")
+    assert_close(h, h2, 1e-5, "xproj h_last vs matmul + dt_proj scan")
+    print(f"xproj Dc={Dc} N={N} R={R}: relerr {e:.2e}")
+
+
+
 def triton_pow2(n):
     return 1 << (n - 1).bit_length()
 

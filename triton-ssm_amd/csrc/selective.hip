@@ -524,17 +524,28 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
 // [32][2N] = x W_BC on the fp32 matrix cores (16x16x4, the channels in steps
 // of 4), the rows are staged as pass 1's B/C rows, C's rows are also stored
 // for pass 3, and the recurrence reads x from the LDS tile instead of HBM.
+//
+// XR > 0 (the whole input projection, x -> (dt, B, C), Mamba-1's x_proj and
+// dt_proj): W_bc's first XR columns give the rank-XR rows dt_raw_t = x_t W_x,
+// staged in LDS; each wave then forms dt = clamp(softplus(dt_raw W_dt +
+// bias)) for its 64 channels on the matrix cores, in the operand order of
+// dt_project_mfma_kernel (so the dt it stores is what that kernel stores for
+// the same dt_raw), into the dt table that pass 3 reads; after a workgroup
+// fence the recurrence reads it back per channel (L2-resident) as a
+// per-channel dt.
 constexpr int kBcRow = kSelThreads + 4;  // x tile row stride (floats): 16-byte rows, banks spread
 constexpr int kBcKb = 16;                // W values per lane in flight in the B/C product
 
-template <int DISC, int NST, bool DTS, bool TAU, bool HAS_D>
-__global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
+template <int DISC, int NST, bool DTS, bool TAU, bool HAS_D, int XR = 0>
+__global__ __launch_bounds__(kSelThreads) __attribute__((amdgpu_waves_per_eu(4))) void sel_bcproj_state_kernel(
     const float* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
     const float* __restrict__ Wbc, int64_t sw_d, const float* __restrict__ D,
     float* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum,
     float* __restrict__ Cws, SelDims m) {
   static_assert(!TAU || DTS, "timestamps only when shared by the channels");
   static_assert(NST == 8 || NST == 16, "8 or 16 states");
+  static_assert(XR == 0 || (!DTS && XR % 16 == 0 && XR <= kSelMaxRank), "dt produced per channel");
+  constexpr int kXrRow = XR + 4;  // dt_raw row stride in LDS (floats)
   const int64_t c = blockIdx.x, b = blockIdx.z;  // one channel block (blockIdx.y == 0)
   const int tid = (int)threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -548,6 +559,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
   __shared__ __align__(16) float sX[kSelChunkSteps * kBcRow];
   __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
   __shared__ float sD[DTS ? kSelChunkSteps : 1];
+  __shared__ __align__(16) float sR[XR ? kSelChunkSteps * kXrRow : 1];  // dt_raw rows
   // ---- prologue loads: the x tile (thread: columns 4 (tid & 63).. of rows
   // (tid >> 6) + 4 k; columns past Dc read as zero), shared dt, lane
   // parameters, a per-channel dt's first fetches; then one wait
@@ -564,14 +576,24 @@ __global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
   }
   float vdt = 0.0f;
   if constexpr (DTS) vdt = stage_dt_load<TAU>(dt + b * m.sdt_b, m.sdt_l, t0, n);
-  const float* dtb = dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d);
+  // XR: dt is the table this pass writes below (m.dtw, [nbatch][L][Dc])
+  const float* dtb = XR ? m.dtw + (b * m.L) * m.Dc + dc : dt + b * m.sdt_b + (DTS ? 0 : dc * m.sdt_d);
+  const int64_t sdt_l = XR ? m.Dc : m.sdt_l;
   float dr[kSelPf];
 #pragma unroll
   for (int j = 0; j < kSelPf; ++j)
-    dr[j] = DTS ? 0.0f : dtb[(t0 + (j < n ? j : n - 1)) * m.sdt_l];
+    dr[j] = (DTS || XR) ? 0.0f : dtb[(t0 + (j < n ? j : n - 1)) * sdt_l];
   float al[NST];
   load_alog<NST>(A_log, dc, al);
   float Dd = HAS_D ? D[dc] : 0.0f;
+  // XR: the recurrence reads x from memory (the tile's LDS becomes the dt
+  // table); its first steps load with the prologue
+  float u[kSelPf];
+  if constexpr (XR > 0) {
+    chunk_prefetch<float, true>(xb + dc, m.sx_l, nullptr, 0, t0, n, u, dr);
+#pragma unroll
+    for (int j = 0; j < kSelPf; ++j) asm volatile("" : "+v"(u[j]));
+  }
 #pragma unroll
   for (int k = 0; k < kSelChunkSteps / 4; ++k)
     *reinterpret_cast<float4*>(sX + (wv + 4 * k) * kBcRow + col) = xv[k];
@@ -580,9 +602,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
   }
   __syncthreads();  // x tile staged
 
-  // ---- B and C rows of the chunk on the matrix cores
-  if (wv < NST / 4) {  // 2N / 16 column tiles x 2 step tiles
-    const int rt = wv & 1, ct = wv >> 1;
+  // ---- (dt_raw,) B and C rows of the chunk on the matrix cores: (XR + 2N) / 16
+  // column tiles x 2 step tiles, tile tt = rt + 2 ct taken by wave tt mod 4
+  constexpr int kNt = 2 * ((XR + 2 * NST) / 16);
+  for (int tt = wv; tt < kNt; tt += kSelWaves) {
+    const int rt = tt & 1, ct = tt >> 1;
     const int li = lane & 15, lj = lane >> 4;
     f32x4 acc0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
     const float* xa = sX + (16 * rt + li) * kBcRow + lj;
@@ -613,17 +637,79 @@ __global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
 #pragma unroll
       for (int j = 0; j < kBcKb; ++j) wcur[j] = wnxt[j];
     }
-    // lane (li, lj): steps 16 rt + 4 lj + i, column 16 ct + li of [B | C]
-    const int cc = 16 * ct + li;
+    // lane (li, lj): steps 16 rt + 4 lj + i, column 16 ct + li of [dt_raw | B | C]
+    const int cc = 16 * ct + li - XR;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 16 * rt + 4 * lj + i;
       const float v = acc0[i] + acc1[i];
-      if (cc < NST) {
+      if (XR && cc < 0) {
+        sR[r * kXrRow + cc + XR] = v;
+      } else if (cc < NST) {
         sB[r * NST + cc] = v;
       } else {
         sC[r * NST + cc - NST] = v;
         if (r < n) Cws[(b * m.L + t0 + r) * NST + cc - NST] = v;  // for pass 3
+      }
+    }
+  }
+  if constexpr (XR > 0) {
+    __syncthreads();  // dt_raw rows staged; every wave is done with the x tile
+    // ---- dt of the wave's 64 channels for the chunk's steps: into the table
+    // (in the x tile's LDS, row stride kSelDtStride) for the recurrence, and
+    // into m.dtw for pass 3
+    float* sP = sX;
+    const int dw0 = 64 * wv;
+    if (dw0 < m.Dc) {
+      const int li = lane & 15, lj = lane >> 4;
+      f32x4 acc[2][4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int h = dw0 + 16 * ct + 4 * lj;  // 4 channels, all in range or all out
+        const float4 bq = *reinterpret_cast<const float4*>(m.bias + (h < m.Dc ? h : 0));
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) acc[rt][ct] = f32x4{bq.x, bq.y, bq.z, bq.w};
+      }
+#pragma unroll
+      for (int q0 = 0; q0 < XR; q0 += 16) {
+        const int qa = q0 + 4 * lj;
+        float wa[4][4];
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const int h = dw0 + 16 * ct + li;
+          const float* wp = m.W + (h < m.Dc ? h : m.Dc - 1);
+#pragma unroll
+          for (int s2 = 0; s2 < 4; ++s2) wa[ct][s2] = wp[(int64_t)(qa + s2) * m.sw_r];
+        }
+        f32x4 rv[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          rv[rt] = *reinterpret_cast<const f32x4*>(sR + (16 * rt + li) * kXrRow + qa);
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct)
+              acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[ct][s2], rv[rt][s2],
+                                                                  acc[rt][ct], 0, 0, 0);
+      }
+      // lane (li, lj): step 16 rt + li, channels 16 ct + 4 lj .. + 3
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int r = 16 * rt + li;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const int h = dw0 + 16 * ct + 4 * lj;
+          float4 v;
+          v.x = clamp_med3(softplus_fast(acc[rt][ct][0]), m.dt_min, m.dt_max);
+          v.y = clamp_med3(softplus_fast(acc[rt][ct][1]), m.dt_min, m.dt_max);
+          v.z = clamp_med3(softplus_fast(acc[rt][ct][2]), m.dt_min, m.dt_max);
+          v.w = clamp_med3(softplus_fast(acc[rt][ct][3]), m.dt_min, m.dt_max);
+          *reinterpret_cast<float4*>(sP + r * kSelDtStride + h) = v;
+          if (r < n && h < m.Dc)
+            *reinterpret_cast<float4*>(m.dtw + (b * m.L + t0 + r) * m.Dc + h) = v;
+        }
       }
     }
   }
@@ -635,38 +721,60 @@ __global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
     asm volatile("" : "+v"(a2[k]), "+v"(nia[k]));  // complete before the loop
   }
   asm volatile("" : "+v"(Dd));
-  __syncthreads();  // B/C rows staged
+  __syncthreads();  // B/C rows (and the dt table) staged
   // Waves whose lanes are all past Dc are done (no barrier follows).
   if ((tid & ~63) >= m.Dc) return;
 
   float* yp = y + b * m.sy_b + dc;
-  const float* xcol = sX + dc;
   float sdt = 0.0f;
-  for (int r = 0; r < n4; r += kSelPf) {
+  if constexpr (XR > 0) {
+    // x from memory (fetched kSelPf steps ahead), dt from the lane's column
+    // of the table, B/C rows from LDS
+    chunk_steps<float, false, true>(xb + dc, m.sx_l, nullptr, 0, sX + dc, t0, n, n4, u, dr,
+                                    [&](int rr, float uv, float dtv) {
+                                      float Bv[NST], Cv[NST];
+                                      lds_row<NST>(sB + rr * NST, Bv);
+                                      lds_row<NST>(sC + rr * NST, Cv);
+                                      sel_update<DISC, NST>(h, a2, nia, Bv, uv, dtv);
+                                      sdt += dtv;
+                                      float acc0 = HAS_D ? Dd * uv : 0.0f, acc1 = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kSelPf; ++j) {
-      const int rr = r + j;
-      const float u = xcol[rr * kBcRow];
-      const float dtv = DTS ? sD[rr] : (rr < n ? dr[j] : 0.0f);
-      float Bv[NST], Cv[NST];
-      lds_row<NST>(sB + rr * NST, Bv);
-      lds_row<NST>(sC + rr * NST, Cv);
-      sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
-      sdt += dtv;
-      float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
+                                      for (int kk = 0; kk < NST; kk += 2) {
+                                        acc0 = __builtin_fmaf(Cv[kk], h[kk], acc0);
+                                        acc1 = __builtin_fmaf(Cv[kk + 1], h[kk + 1], acc1);
+                                      }
+                                      // unconditional (as below)
+                                      const int64_t tw = t0 + (rr < n ? rr : n - 1);
+                                      yp[tw * m.sy_l] = acc0 + acc1;
+                                    });
+  } else {
+    const float* xcol = sX + dc;
+    for (int r = 0; r < n4; r += kSelPf) {
 #pragma unroll
-      for (int k = 0; k < NST; k += 2) {
-        acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
-        acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
-      }
-      // unconditional store: lanes past Dc (in the wave of channel Dc-1) and
-      // padded steps store the values of channel Dc-1 / step n-1
-      const int64_t tw = t0 + (rr < n ? rr : n - 1);
-      yp[tw * m.sy_l] = acc0 + acc1;
-      if constexpr (!DTS) {
-        __builtin_amdgcn_sched_barrier(0);
-        dr[j] = dtb[(t0 + min(rr + kSelPf, n - 1)) * m.sdt_l];
-        __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < kSelPf; ++j) {
+        const int rr = r + j;
+        const float u = xcol[rr * kBcRow];
+        const float dtv = DTS ? sD[rr] : (rr < n ? dr[j] : 0.0f);
+        float Bv[NST], Cv[NST];
+        lds_row<NST>(sB + rr * NST, Bv);
+        lds_row<NST>(sC + rr * NST, Cv);
+        sel_update<DISC, NST>(h, a2, nia, Bv, u, dtv);
+        sdt += dtv;
+        float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NST; k += 2) {
+          acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
+          acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
+        }
+        // unconditional store: lanes past Dc (in the wave of channel Dc-1) and
+        // padded steps store the values of channel Dc-1 / step n-1
+        const int64_t tw = t0 + (rr < n ? rr : n - 1);
+        yp[tw * m.sy_l] = acc0 + acc1;
+        if constexpr (!DTS) {
+          __builtin_amdgcn_sched_barrier(0);
+          dr[j] = dtb[(t0 + min(rr + kSelPf, n - 1)) * sdt_l];
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
   }
@@ -1084,6 +1192,50 @@ int sel_bcproj_t(bool has_d, const float* x, const float* dt, const float* Wbc, 
   return (int)hipGetLastError();
 }
 
+// The whole input projection in the pass: dt from the dt_raw columns of W_x
+// (into the dt table p.dtw), B and C from the next 2N columns.
+template <int DISC, int NST, int XR>
+int sel_xproj_t(bool has_d, const float* x, const float* Wx, int64_t swx_d, float* Cws,
+                const SelPtrs& p, const SelDims& m, hipStream_t s) {
+  const dim3 grid((unsigned)m.nch, 1u, (unsigned)m.nbatch);
+  float* y = static_cast<float*>(p.y);
+  if (has_d)
+    hipLaunchKernelGGL((sel_bcproj_state_kernel<DISC, NST, false, false, true, XR>), grid,
+                       dim3(kSelThreads), 0, s, x, nullptr, p.A_log, Wx, swx_d, p.D, y, p.S,
+                       p.T, Cws, m);
+  else
+    hipLaunchKernelGGL((sel_bcproj_state_kernel<DISC, NST, false, false, false, XR>), grid,
+                       dim3(kSelThreads), 0, s, x, nullptr, p.A_log, Wx, swx_d, p.D, y, p.S,
+                       p.T, Cws, m);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const int64_t lanes = m.Dc * NST;  // per batch
+  hipLaunchKernelGGL((sel_carry_kernel<NST, false>),
+                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
+                          (unsigned)m.nbatch),
+                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  // pass 3 reads the dt table and the C rows pass 1 stored
+  SelDims m3 = m;
+  m3.sdt_b = m.L * m.Dc; m3.sdt_l = m.Dc; m3.sdt_d = 1;
+  m3.sC_b = m.L * NST; m3.sC_l = NST;
+  hipLaunchKernelGGL((sel_output_kernel<float, NST, false, false>), grid, dim3(kSelThreads), 0,
+                     s, m.dtw, p.A_log, Cws, p.S, y, m3);
+  return (int)hipGetLastError();
+}
+
+template <int DISC, int NST>
+int sel_xproj_r(int64_t R, bool has_d, const float* x, const float* Wx, int64_t swx_d, float* Cws,
+                const SelPtrs& p, const SelDims& m, hipStream_t s) {
+  switch (R) {
+    case 16: return sel_xproj_t<DISC, NST, 16>(has_d, x, Wx, swx_d, Cws, p, m, s);
+    case 32: return sel_xproj_t<DISC, NST, 32>(has_d, x, Wx, swx_d, Cws, p, m, s);
+    case 48: return sel_xproj_t<DISC, NST, 48>(has_d, x, Wx, swx_d, Cws, p, m, s);
+    default: return sel_xproj_t<DISC, NST, 64>(has_d, x, Wx, swx_d, Cws, p, m, s);
+  }
+}
+
 template <int DISC, int NST>
 int sel_bcproj_dt(bool has_d, bool dts, bool tau, const float* x, const float* dt,
                   const float* Wbc, int64_t sw_d, float* Cws, const SelPtrs& p, const SelDims& m,
@@ -1241,6 +1393,66 @@ extern "C" int tssm_interp_selective_scan(int dtype, int disc, const void* V, co
   return sel_interp_launch(dtype, disc, V, M, tau, Vhat, p, nbatch, T, F, N, sv_b, sv_t, sm_b,
                            sm_t, stau_b, stau_t, sB_b, sB_l, sC_b, sC_l, so_b, so_t, sy_b, sy_t,
                            K, FTILE, as_stream(stream));
+}
+
+extern "C" int64_t tssm_selective_scan_xproj_workspace_bytes(int64_t nbatch, int64_t L,
+                                                             int64_t Dc, int64_t N) {
+  if (nbatch <= 0 || L <= 0 || Dc <= 0 || !(N == 8 || N == 16)) return -1;
+  const int64_t nch = (L + kSelChunkSteps - 1) / kSelChunkSteps;
+  // chunk states + per-channel dt sums, the C rows and the dt table for pass 3
+  return (nbatch * nch * Dc * N + nbatch * nch * Dc) * 4 + nbatch * L * N * 4 +
+         sel_dt_table_bytes(nbatch, L, Dc) + 512;
+}
+
+extern "C" int tssm_selective_scan_xproj(int disc, const float* x, const float* A_log,
+                                         const float* W_x, int64_t swx_d, int64_t rank,
+                                         const float* W_dt, int64_t sw_r, const float* bias,
+                                         float dt_min, float dt_max, const float* D,
+                                         const float* h0, float* y, float* h_last,
+                                         int64_t nbatch, int64_t L, int64_t Dc, int64_t N,
+                                         int64_t sx_b, int64_t sx_l, int64_t sy_b, int64_t sy_l,
+                                         void* workspace, int64_t workspace_bytes, void* stream) {
+  TSSM_CHECK(x && A_log && W_x && W_dt && bias && y, TSSM_ERR_NULL);
+  TSSM_CHECK(disc == TSSM_DISC_EULER || disc == TSSM_DISC_ZOH, TSSM_ERR_UNSUPPORTED);
+  TSSM_CHECK(nbatch > 0 && L > 0 && Dc > 0, TSSM_ERR_SHAPE);
+  TSSM_CHECK((N == 8 || N == 16) && Dc <= kSelThreads && Dc % 4 == 0 && nbatch <= 65535 &&
+                 (rank == 16 || rank == 32 || rank == 48 || rank == 64),
+             TSSM_ERR_UNSUPPORTED);
+  const int64_t strides[] = {sx_b, sx_l, sy_b, sy_l, sw_r};
+  for (int64_t st : strides) TSSM_CHECK(st >= 0, TSSM_ERR_STRIDE);
+  TSSM_CHECK(swx_d >= rank + 2 * N && sw_r >= Dc && sw_r % 4 == 0, TSSM_ERR_STRIDE);
+  TSSM_CHECK(aligned(x, 16) && sx_b % 4 == 0 && sx_l % 4 == 0 && aligned(A_log, 16) &&
+                 aligned(W_dt, 16) && aligned(bias, 16),
+             TSSM_ERR_ALIGN);
+  TSSM_CHECK(dt_min <= dt_max, TSSM_ERR_SHAPE);
+  const int64_t need = tssm_selective_scan_xproj_workspace_bytes(nbatch, L, Dc, N);
+  TSSM_CHECK(workspace != nullptr && workspace_bytes >= need, TSSM_ERR_WORKSPACE);
+  TSSM_CHECK(aligned(workspace, 16), TSSM_ERR_ALIGN);
+  SelDims m{};
+  m.L = L; m.Dc = Dc; m.nbatch = nbatch;
+  m.Rs = kSelChunkSteps;
+  m.nch = (L + m.Rs - 1) / m.Rs;
+  m.sx_b = sx_b; m.sx_l = sx_l;
+  m.sy_b = sy_b; m.sy_l = sy_l;
+  m.W = W_dt; m.bias = bias; m.sw_r = sw_r; m.rank = (int)rank;
+  m.dt_min = dt_min; m.dt_max = dt_max;
+  SelPtrs p;
+  p.x = x; p.A_log = A_log; p.D = D; p.h0 = h0; p.y = y; p.h_last = h_last;
+  p.S = static_cast<float*>(workspace);
+  p.T = p.S + nbatch * m.nch * Dc * N;
+  float* Cws = p.T + nbatch * m.nch * Dc;
+  // the dt table after the C rows, 16-byte aligned
+  const int64_t cws_end = (int64_t)(reinterpret_cast<uintptr_t>(Cws + nbatch * L * N));
+  m.dtw = reinterpret_cast<float*>((cws_end + 15) & ~int64_t(15));
+  const hipStream_t s = as_stream(stream);
+  const bool has_d = D != nullptr;
+  if (N == 16)
+    return disc == TSSM_DISC_ZOH
+               ? sel_xproj_r<TSSM_DISC_ZOH, 16>(rank, has_d, x, W_x, swx_d, Cws, p, m, s)
+               : sel_xproj_r<TSSM_DISC_EULER, 16>(rank, has_d, x, W_x, swx_d, Cws, p, m, s);
+  return disc == TSSM_DISC_ZOH
+             ? sel_xproj_r<TSSM_DISC_ZOH, 8>(rank, has_d, x, W_x, swx_d, Cws, p, m, s)
+             : sel_xproj_r<TSSM_DISC_EULER, 8>(rank, has_d, x, W_x, swx_d, Cws, p, m, s);
 }
 
 extern "C" int64_t tssm_selective_scan_bcproj_workspace_bytes(int64_t nbatch, int64_t L,

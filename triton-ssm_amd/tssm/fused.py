@@ -277,9 +277,69 @@ def _selective_scan_bcproj(x, dt, A_log, W_bc, D, disc, h0, return_state, dt_is_
     return (y, h_last) if return_state else y
 
 
+def _selective_scan_xproj(x, A_log, xp, D, disc, h0, return_state, out):
+    """tssm_selective_scan_xproj: dt, B and C formed from x inside the scan's
+    first pass (fp32, Dc <= 256).  xp = (W_x [Dc, R + 2N], W_dt [R, Dc], bias
+    [Dc], DT_MIN, DT_MAX)."""
+    try:
+        W_x, W_dt, bias, dt_min, dt_max = xp
+    except (TypeError, ValueError):
+        raise ValueError("x_proj must be (W_x, W_dt, bias, DT_MIN, DT_MAX)") from None
+    for t, w in ((x, "x"), (A_log, "A_log"), (W_x, "W_x"), (W_dt, "W_dt"), (bias, "bias")):
+        need_gpu(t, w)
+    if x.dim() != 3 or x.dtype != torch.float32:
+        raise ValueError("x_proj: x must be float32 [Bsz, L, Dc]")
+    Bsz, L, Dc = x.shape
+    if W_dt.dim() != 2 or W_dt.shape[1] != Dc:
+        raise ValueError("x_proj: W_dt must be [R, Dc]")
+    R = W_dt.shape[0]
+    if W_x.dim() != 2 or W_x.shape[0] != Dc or (W_x.shape[1] - R) % 2 or W_x.shape[1] <= R:
+        raise ValueError("x_proj: W_x must be [Dc, R + 2N] (columns dt_raw, B, C)")
+    N = (W_x.shape[1] - R) // 2
+    if A_log.shape != (Dc, N):
+        raise ValueError("shape mismatch between x, x_proj and A_log")
+    if Dc > 256 or Dc % 4 or N not in (8, 16) or R not in (16, 32, 48, 64):
+        raise ValueError("x_proj needs Dc <= 256 (a multiple of 4), N = 8 or 16, R in 16..64 "
+                         "(a multiple of 16)")
+    if bias.numel() != Dc:
+        raise ValueError("x_proj: bias must have Dc elements")
+    _inner_unit(x, "x")
+    W_x = as_f32(W_x, "W_x")
+    _inner_unit(W_x, "W_x")
+    W_dt = as_f32(W_dt, "W_dt")
+    if W_dt.stride(1) != 1 or W_dt.stride(0) % 4:
+        W_dt = W_dt.contiguous()
+    bias = as_f32(bias, "bias").contiguous()
+    A_log = as_f32(A_log, "A_log").contiguous()
+    if D is not None:
+        need_gpu(D, "D")
+        if D.numel() != Dc:
+            raise ValueError("D must have Dc elements")
+        D = as_f32(D, "D").contiguous()
+    if h0 is not None:
+        need_gpu(h0, "h0")
+        if tuple(h0.shape) != (Bsz, Dc, N):
+            raise ValueError("h0 must be [Bsz, Dc, N]")
+        h0 = as_f32(h0, "h0").contiguous()
+    y = torch.empty(Bsz, L, Dc, device=x.device, dtype=x.dtype) if out is None else out
+    need_gpu(y, "out")
+    if y.shape != x.shape or y.dtype != x.dtype:
+        raise ValueError("out must match x in shape and dtype")
+    _inner_unit(y, "out")
+    h_last = torch.empty(Bsz, Dc, N, device=x.device, dtype=torch.float32) if return_state else None
+    ws, stream = _ws(_lib.lib().tssm_selective_scan_xproj_workspace_bytes(Bsz, L, Dc, N), x,
+                     "selective_scan x_proj", workspace.SSD)
+    _lib.call("tssm_selective_scan_xproj", _disc_code(disc), x.data_ptr(), A_log.data_ptr(),
+              W_x.data_ptr(), W_x.stride(0), R, W_dt.data_ptr(), W_dt.stride(0),
+              bias.data_ptr(), float(dt_min), float(dt_max), ptr(D), ptr(h0), y.data_ptr(),
+              ptr(h_last), Bsz, L, Dc, N, x.stride(0), x.stride(1), y.stride(0), y.stride(1),
+              ws.data_ptr(), ws.numel(), stream)
+    return (y, h_last) if return_state else y
+
+
 def selective_scan_forward(x, dt, A_log, B=None, C=None, D=None, *, chunk=128, disc="zoh",
                            h0=None, return_state=False, dt_is_tau=False, out=None, dt_proj=None,
-                           bc_proj=None):
+                           bc_proj=None, x_proj=None):
     """Mamba-1 selective scan over lanes (channel d, state n).
 
     x      [Bsz, L, Dc]        float32 / bfloat16 / float16
@@ -296,10 +356,20 @@ def selective_scan_forward(x, dt, A_log, B=None, C=None, D=None, *, chunk=128, d
     bc_proj  W_bc [Dc, 2N] or None (then B and C are None): B_t = x_t W_bc[:, :N]
            and C_t = x_t W_bc[:, N:] (the input projection's B and C columns)
            are formed inside the scan (fp32, Dc <= 256, N = 8 or 16)
+    x_proj  (W_x [Dc, R + 2N], W_dt [R, Dc], bias [Dc], DT_MIN, DT_MAX) or None
+           (then dt, B and C are None): the whole input projection in the scan,
+           x_dbl = x @ W_x split into dt_raw, B, C and dt = clamp(softplus(
+           dt_raw @ W_dt + bias), DT_MIN, DT_MAX) (fp32, Dc <= 256, N = 8 or
+           16, R = 16, 32, 48 or 64)
 
     h_t[d,n] = exp(dt_t a[d,n]) h_{t-1}[d,n] + Bbar_t[d,n] B_t[n] x_t[d];
     y_t[d] = sum_n C_t[n] h_t[d,n] + D[d] x_t[d].
     """
+    if x_proj is not None:
+        if dt is not None or B is not None or C is not None or dt_proj is not None \
+                or bc_proj is not None:
+            raise ValueError("x_proj replaces dt, B and C (pass None for them)")
+        return _selective_scan_xproj(x, A_log, x_proj, D, disc, h0, return_state, out)
     if bc_proj is not None:
         if B is not None or C is not None or dt_proj is not None:
             raise ValueError("bc_proj replaces B and C (and does not combine with dt_proj)")
