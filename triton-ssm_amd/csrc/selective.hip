@@ -536,8 +536,8 @@ __global__ __launch_bounds__(kSelThreads) void sel_output_kernel(
 constexpr int kBcRow = kSelThreads + 4;  // x tile row stride (floats): 16-byte rows, banks spread
 constexpr int kBcKb = 16;                // W values per lane in flight in the B/C product
 
-template <int DISC, int NST, bool DTS, bool TAU, bool HAS_D, int XR = 0>
-__global__ __launch_bounds__(kSelThreads) __attribute__((amdgpu_waves_per_eu(4))) void sel_bcproj_state_kernel(
+template <int DISC, int NST, bool DTS, bool TAU, bool HAS_D, int XR>
+__device__ __forceinline__ void sel_bcproj_state_body(
     const float* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
     const float* __restrict__ Wbc, int64_t sw_d, const float* __restrict__ D,
     float* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum,
@@ -789,6 +789,28 @@ __global__ __launch_bounds__(kSelThreads) __attribute__((amdgpu_waves_per_eu(4))
       Tsum[(b * m.nch + c) * m.Dc + d] = sdt;
     }
   }
+}
+
+template <int DISC, int NST, bool DTS, bool TAU, bool HAS_D>
+__global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
+    const float* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ A_log,
+    const float* __restrict__ Wbc, int64_t sw_d, const float* __restrict__ D,
+    float* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum,
+    float* __restrict__ Cws, SelDims m) {
+  sel_bcproj_state_body<DISC, NST, DTS, TAU, HAS_D, 0>(x, dt, A_log, Wbc, sw_d, D, y, S, Tsum,
+                                                      Cws, m);
+}
+
+// The XR > 0 instances, held to 4 waves per SIMD (left alone the compiler
+// gives them 144 registers, 3 waves per SIMD, and the pass runs ~9% slower).
+template <int DISC, int NST, bool HAS_D, int XR>
+__global__ __launch_bounds__(kSelThreads) __attribute__((amdgpu_waves_per_eu(4))) void
+sel_xproj_state_kernel(const float* __restrict__ x, const float* __restrict__ A_log,
+                       const float* __restrict__ Wx, int64_t swx_d, const float* __restrict__ D,
+                       float* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum,
+                       float* __restrict__ Cws, SelDims m) {
+  sel_bcproj_state_body<DISC, NST, false, false, HAS_D, XR>(x, nullptr, A_log, Wx, swx_d, D, y,
+                                                            S, Tsum, Cws, m);
 }
 
 // ---------------------------------------------------------------- interpolation in pass 1
@@ -1200,13 +1222,11 @@ int sel_xproj_t(bool has_d, const float* x, const float* Wx, int64_t swx_d, floa
   const dim3 grid((unsigned)m.nch, 1u, (unsigned)m.nbatch);
   float* y = static_cast<float*>(p.y);
   if (has_d)
-    hipLaunchKernelGGL((sel_bcproj_state_kernel<DISC, NST, false, false, true, XR>), grid,
-                       dim3(kSelThreads), 0, s, x, nullptr, p.A_log, Wx, swx_d, p.D, y, p.S,
-                       p.T, Cws, m);
+    hipLaunchKernelGGL((sel_xproj_state_kernel<DISC, NST, true, XR>), grid, dim3(kSelThreads), 0,
+                       s, x, p.A_log, Wx, swx_d, p.D, y, p.S, p.T, Cws, m);
   else
-    hipLaunchKernelGGL((sel_bcproj_state_kernel<DISC, NST, false, false, false, XR>), grid,
-                       dim3(kSelThreads), 0, s, x, nullptr, p.A_log, Wx, swx_d, p.D, y, p.S,
-                       p.T, Cws, m);
+    hipLaunchKernelGGL((sel_xproj_state_kernel<DISC, NST, false, XR>), grid, dim3(kSelThreads),
+                       0, s, x, p.A_log, Wx, swx_d, p.D, y, p.S, p.T, Cws, m);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   const int64_t lanes = m.Dc * NST;  // per batch
