@@ -197,7 +197,8 @@ def test_ssd_long_sequence_shape(dev):
 @pytest.mark.parametrize("decay,L,Bsz,H,with_d", [
     ("slow", 20000, 1, 2, False),    # no segment forgets: walks fold many aggregates
     ("slow", 70001, 2, 3, True),     # more than 64 segments per row, ragged end, skip term
-    ("mixed", 205006, 2, 8, False),  # two-tile segments, forgetting and slow heads together
+    ("mixed", 205006, 2, 8, False),  # four-tile segments, forgetting and slow heads together
+    ("slow", 70001, 4, 8, False),    # four-tile segments, more than 64 per row, slow decays
 ])
 def test_ssd_scan_fused_lookback(dev, decay, L, Bsz, H, with_d):
     """The one-launch SSD kernel (reverse first sweep, decoupled look-back,

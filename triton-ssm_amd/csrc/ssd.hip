@@ -1677,8 +1677,14 @@ bool ssd_fused_ok(int dtype, int64_t P, int64_t N, int64_t tc, const SsdArgs& a,
 // 16 x 64 end-state and 16 x 64 inclusive-state words.
 constexpr int64_t kSsdSegWords = 3 + 2 * 64 * kSsdLbVals;
 
+// Segments of 4 tiles (1024 steps) while that still gives 2048 waves, else
+// as the wave passes (2 or 1).  At B=1 L=262144 H=8: 4 tiles (2048 waves)
+// 157.7 us, 2 tiles (4096 waves) 164.5 us, 8 tiles (1024 waves) 172.5 us --
+// longer segments halve the look-back words and the share of a segment the
+// first sweep re-reads, until too few waves remain to keep the memory busy.
+constexpr int64_t kFusedSeg4Waves = 2048;
 int64_t ssd_fused_segs(int64_t rows, int64_t nchunks, int64_t* wseg) {
-  *wseg = ssd_wave_seg(rows, nchunks);
+  *wseg = rows * cdiv64(nchunks, 4) >= kFusedSeg4Waves ? 4 : ssd_wave_seg(rows, nchunks);
   return cdiv64(nchunks, *wseg);
 }
 
