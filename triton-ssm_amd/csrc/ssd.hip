@@ -49,20 +49,6 @@ struct SsdArgs {
 constexpr float kRescaleFloor = 5.421010862427522e-20f;  // 2^-64
 constexpr int kSsdSub = 16;  // steps staged per sub-block
 
-// Per-step decay and input coefficient for steps [t0, t0+64) of one head,
-// computed by lane i for step t0+i and shared through LDS.  Steps at or past
-// L get dt = 0, i.e. decay 1 and coefficient 0, so they leave the state alone.
-template <int DISC>
-__device__ inline void step_scalars(const float* dtp, int64_t sdt_l, int64_t t0, int64_t L,
-                                    float a2, float* s_ab, float* s_cf, int lane) {
-  const int64_t t = t0 + lane;
-  const float d = t < L ? dtp[t * sdt_l] : 0.0f;
-  const float arg = d * a2;
-  const float ab = exp2_fast(arg);
-  s_ab[lane] = ab;
-  s_cf[lane] = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * d : d;
-}
-
 // One step of the rescaled recurrence h = Pt g:  h_t = ab h_{t-1} + xs B_t.
 // When Pt ab would fall below 2^-64 the factor is folded into g (the branch is
 // uniform: Pt and ab are the same on every lane of the wave).
@@ -84,28 +70,84 @@ __device__ inline void rescaled_step(float* g, float& Pt, float ab, float xs, co
   }
 }
 
-// Stage rows [t0, t0+kSsdSub) of an N-wide operand into LDS as fp32
-// (s[i*N + n]); rows at or past L read as zero.
-template <typename T, int N>
-__device__ inline void stage_rows(const T* __restrict__ base, int64_t sl, int64_t t0, int64_t L,
-                                  float* s, int lane) {
+// Registers of one sub-block of kSsdSub steps: x of the lane's channel and
+// the B (and, for the outputs, C) rows, spread over the wave.  Every load of
+// a sub-block is issued before the first is used: clamped addresses (steps
+// past L re-read step L-1) and selects at the LDS store, no branch around a
+// load (the compiler would wait for a load inside a branch on its own).
+//
+// With kSsdPipe<N> the loads of sub-block k+1 (and the dt of the next 64-step
+// group) are issued before sub-block k is computed from LDS, so they are in
+// flight during its steps.  That holds one more sub-block in registers:
+// fp32 at L=65536 H=8 P=64: N=16 195.98 -> 178.13 us (state 76 -> 109,
+// output 87 -> 127 VGPRs), N=32 267.1 -> 253.2 us; at N=64 the output pass
+// drops to one wave per SIMD and the passes slow 432.4 -> 585.7 us, so N=64
+// loads each sub-block just before it is used.
+template <int N>
+constexpr bool kSsdPipe = N <= 32;
+
+template <int N, bool WITH_C>
+struct SsdSub {
+  static constexpr int K = (kSsdSub * N + 63) / 64;
+  float x[kSsdSub], b[K], c[WITH_C ? K : 1];
+};
+
+template <typename T, int N, bool WITH_C>
+__device__ inline void sub_load(SsdSub<N, WITH_C>& r, const T* __restrict__ xp, int64_t sx_l,
+                                const T* __restrict__ Bp, int64_t sB_l, const T* __restrict__ Cp,
+                                int64_t sC_l, int64_t ts, int64_t L, int lane) {
 #pragma unroll
-  for (int k = lane; k < kSsdSub * N; k += 64) {
-    const int i = k / N, n = k - (k / N) * N;
-    const int64_t t = t0 + i;
-    s[k] = t < L ? ldf(base + t * sl + n) : 0.0f;
+  for (int i = 0; i < kSsdSub; ++i) {
+    const int64_t t = ts + i;
+    r.x[i] = ldf(xp + (t < L ? t : L - 1) * sx_l);
+  }
+#pragma unroll
+  for (int q = 0; q < SsdSub<N, WITH_C>::K; ++q) {
+    const int k = lane + 64 * q;
+    const int kc = k < kSsdSub * N ? k : 0;
+    const int i = kc / N, n = kc - (kc / N) * N;
+    const int64_t t = ts + i < L ? ts + i : L - 1;
+    r.b[q] = ldf(Bp + t * sB_l + n);
+    if constexpr (WITH_C) r.c[q] = ldf(Cp + t * sC_l + n);
   }
 }
 
-// Stage x_t[lane] for t in [t0, t0+kSsdSub) into s_x[i*64 + lane].
-template <typename T>
-__device__ inline void stage_x(const T* __restrict__ xp, int64_t sl, int64_t t0, int64_t L,
-                               bool act, float* s_x, int lane) {
+template <int N, bool WITH_C>
+__device__ inline void sub_store(const SsdSub<N, WITH_C>& r, int64_t ts, int64_t L, bool act,
+                                 float* s_x, float* s_B, float* s_C, int lane) {
 #pragma unroll
-  for (int i = 0; i < kSsdSub; ++i) {
-    const int64_t t = t0 + i;
-    s_x[i * 64 + lane] = (act && t < L) ? ldf(xp + t * sl) : 0.0f;
+  for (int i = 0; i < kSsdSub; ++i) s_x[i * 64 + lane] = (act && ts + i < L) ? r.x[i] : 0.0f;
+#pragma unroll
+  for (int q = 0; q < SsdSub<N, WITH_C>::K; ++q) {
+    const int k = lane + 64 * q;
+    if (k < kSsdSub * N) {
+      const bool in = ts + k / N < L;
+      s_B[k] = in ? r.b[q] : 0.0f;
+      if constexpr (WITH_C) s_C[k] = in ? r.c[q] : 0.0f;
+    }
   }
+}
+
+// dt of step t0 + lane (clamped address; steps at or past L are zeroed by
+// step_scalars_of).
+__device__ inline float dt_ahead(const float* dtp, int64_t sdt_l, int64_t t0, int64_t L,
+                                 int lane) {
+  const int64_t t = t0 + lane;
+  return dtp[(t < L ? t : L - 1) * sdt_l];
+}
+
+// Per-step decay and input coefficient for steps [t0, t0+64) of one head,
+// computed by lane i for step t0+i from its dt and shared through LDS.  Steps
+// at or past L get dt = 0, i.e. decay 1 and coefficient 0, so they leave the
+// state alone.
+template <int DISC>
+__device__ inline void step_scalars_of(float dl, int64_t t0, int64_t L, float a2, float* s_ab,
+                                       float* s_cf, int lane) {
+  const float d = t0 + lane < L ? dl : 0.0f;
+  const float arg = d * a2;
+  const float ab = exp2_fast(arg);
+  s_ab[lane] = ab;
+  s_cf[lane] = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * d : d;
 }
 
 template <typename T, int DISC, int N>
@@ -129,12 +171,27 @@ __global__ __launch_bounds__(64) void ssd_state_kernel(SsdArgs a) {
 #pragma unroll
   for (int n = 0; n < N; ++n) g[n] = 0.0f;
   float Pt = 1.0f, Achunk = 1.0f;
+  constexpr bool PIPE = kSsdPipe<N>;
+  SsdSub<N, false> nxt;
+  float dnext = 0.0f;
+  if constexpr (PIPE) {
+    sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, tbeg, a.L, lane);
+    dnext = dt_ahead(dtp, a.sdt_l, tbeg, a.L, lane);
+  }
   for (int64_t t0 = tbeg; t0 < tend; t0 += 64) {
-    step_scalars<DISC>(dtp, a.sdt_l, t0, a.L, a2, s_ab, s_cf, lane);
+    if constexpr (PIPE) {
+      step_scalars_of<DISC>(dnext, t0, a.L, a2, s_ab, s_cf, lane);
+      dnext = dt_ahead(dtp, a.sdt_l, t0 + 64, a.L, lane);
+    } else {
+      step_scalars_of<DISC>(dt_ahead(dtp, a.sdt_l, t0, a.L, lane), t0, a.L, a2, s_ab, s_cf, lane);
+    }
     for (int j = 0; j < 64 && t0 + j < tend; j += kSsdSub) {
-      stage_x<T>(xp, a.sx_l, t0 + j, a.L, act, s_x, lane);
-      stage_rows<T, N>(Bp, a.sB_l, t0 + j, a.L, s_B, lane);
+      const int64_t ts = t0 + j;
+      if constexpr (!PIPE) sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, ts, a.L, lane);
+      sub_store<N, false>(nxt, ts, a.L, act, s_x, s_B, s_B, lane);
       __syncthreads();
+      if constexpr (PIPE)
+        sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, ts + kSsdSub, a.L, lane);
 #pragma unroll 2
       for (int i = 0; i < kSsdSub; ++i) {
         const float ab = s_ab[j + i];
@@ -282,14 +339,28 @@ __global__ __launch_bounds__(64) void ssd_out_kernel(SsdArgs a) {
   }
   const float dv = (HAS_D && act) ? a.D[h * P + lane] : 0.0f;
   float Pt = 1.0f;
+  constexpr bool PIPE = kSsdPipe<N>;
+  SsdSub<N, true> nxt;
+  float dnext = 0.0f;
+  if constexpr (PIPE) {
+    sub_load<T, N, true>(nxt, xp, a.sx_l, Bp, a.sB_l, Cp, a.sC_l, tbeg, a.L, lane);
+    dnext = dt_ahead(dtp, a.sdt_l, tbeg, a.L, lane);
+  }
   for (int64_t t0 = tbeg; t0 < tend; t0 += 64) {
-    step_scalars<DISC>(dtp, a.sdt_l, t0, a.L, a2, s_ab, s_cf, lane);
+    if constexpr (PIPE) {
+      step_scalars_of<DISC>(dnext, t0, a.L, a2, s_ab, s_cf, lane);
+      dnext = dt_ahead(dtp, a.sdt_l, t0 + 64, a.L, lane);
+    } else {
+      step_scalars_of<DISC>(dt_ahead(dtp, a.sdt_l, t0, a.L, lane), t0, a.L, a2, s_ab, s_cf, lane);
+    }
     for (int j = 0; j < 64 && t0 + j < tend; j += kSsdSub) {
       const int64_t ts = t0 + j;
-      stage_x<T>(xp, a.sx_l, ts, a.L, act, s_x, lane);
-      stage_rows<T, N>(Bp, a.sB_l, ts, a.L, s_B, lane);
-      stage_rows<T, N>(Cp, a.sC_l, ts, a.L, s_C, lane);
+      if constexpr (!PIPE)
+        sub_load<T, N, true>(nxt, xp, a.sx_l, Bp, a.sB_l, Cp, a.sC_l, ts, a.L, lane);
+      sub_store<N, true>(nxt, ts, a.L, act, s_x, s_B, s_C, lane);
       __syncthreads();
+      if constexpr (PIPE)
+        sub_load<T, N, true>(nxt, xp, a.sx_l, Bp, a.sB_l, Cp, a.sC_l, ts + kSsdSub, a.L, lane);
       const int m = a.L - ts < kSsdSub ? (int)(a.L - ts) : kSsdSub;
 #pragma unroll 2
       for (int i = 0; i < kSsdSub; ++i) {
