@@ -110,6 +110,72 @@ def test_ssd_scan_n64_split_resume(dev, cut):
     assert_close(h2, h, 1e-3, f"n64 final state via h0, cut {cut}")
 
 
+@pytest.mark.parametrize("Bsz,L,H,P,decay", [
+    (1, 5000, 2, 64, "slow"),    # 2 rows x 2 channel blocks: 20 segments of 256 steps, ragged end
+    (1, 5000, 2, 64, "heavy"),
+    (1, 3001, 3, 48, "slow"),    # 3 rows (not a multiple of 8), 3 blocks of 16 channels
+    (2, 2000, 1, 16, "slow"),    # one 16-channel block: the step halves of pass 1 added
+    (1, 4000, 8, 32, "slow"),    # 8 rows (XCD mapping), one 32-channel block per row
+])
+@pytest.mark.parametrize("disc", ["zoh", "euler"])
+def test_ssd_scan_n64_segments(dev, Bsz, L, H, P, decay, disc):
+    """bf16 N = 64 with too few (row, channel block) units to fill the chip:
+    the one-pass kernel runs time segments (pass 1 segment end states, the
+    prefix pass over segments, pass 3 outputs from each entry state).  Slow
+    decays carry the state across every segment; h0, skip term and the final
+    state against the float64 oracle."""
+    from tssm import ssd_scan_forward
+    d = _ssd_inputs(dev, Bsz, L, H, P, 64, torch.bfloat16, seed=L + P + H, heavy=True)
+    if decay == "slow":
+        g = torch.Generator().manual_seed(L)
+        d["A_log"] = torch.full((H,), float(np.log(0.02)), device=dev)
+        d["dt"] = (torch.rand(Bsz, L, H, generator=g) * 0.02).to(dev)
+    h0 = torch.randn(Bsz, H, P, 64, device=dev)
+    y, hl = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], disc=disc,
+                             h0=h0, chunk=256, return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssd_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], h0=np64(h0),
+                              disc=disc)
+    assert_close(y, y_ref, 4e-3, f"segmented n64 ssd y L={L} P={P} {decay} {disc}")
+    assert_close(hl, h_ref, 1e-3, f"segmented n64 ssd h_last L={L} P={P} {decay} {disc}")
+
+
+def test_ssd_scan_n64_long_sequence(dev):
+    """B=1 L=65536 H=8 P=N=64 bf16, log-normal dt: 16 (row, channel block)
+    units, so the one-pass kernel runs 16 segments of 4096 steps.  Heads 0
+    and 7 against the float64 oracle over every step, every head against the
+    oracle's fp32 C restatement, and split/resume at L/2."""
+    import tssm
+    from oracle import cport
+    from tssm import ssd_scan_forward, workloads
+    w = workloads.ssd_long(L=65536, N=64)
+    d = {k: w[k].to(dev) for k in ("x", "dt", "A_log", "B", "C")}
+    y, h = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], None, chunk=256,
+                            return_state=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    heads = [0, 7]
+    sl = (slice(None), slice(None), heads)
+    y_ref, h_ref = O.ssd_scan(w["x"][sl], w["dt"][sl], w["A_log"][heads], w["B"][sl], w["C"][sl])
+    assert_close(y[sl], y_ref, 4e-3, "n64 long y, heads 0 and 7")
+    assert_close(h[:, heads], h_ref, 1e-3, "n64 long final state, heads 0 and 7")
+    y32, h32 = cport.ssd_scan(w["x"].float(), w["dt"], w["A_log"], w["B"].float(),
+                              w["C"].float())
+    yc, hc = y.float().cpu(), h.cpu()
+    for k in range(w["x"].shape[2]):
+        assert_close(yc[:, :, k], y32[:, :, k], 4e-3, f"n64 long y, head {k}")
+        assert_close(hc[:, k], h32[:, k], 1e-3, f"n64 long final state, head {k}")
+    cut = 32768
+    _, h1 = ssd_scan_forward(d["x"][:, :cut], d["dt"][:, :cut], d["A_log"], d["B"][:, :cut],
+                             d["C"][:, :cut], None, chunk=256, return_state=True)
+    y2, h2 = ssd_scan_forward(d["x"][:, cut:], d["dt"][:, cut:], d["A_log"], d["B"][:, cut:],
+                              d["C"][:, cut:], None, chunk=256, h0=h1, return_state=True)
+    torch.cuda.synchronize()
+    assert_close(y2, y[:, cut:], 4e-3, "n64 long tail via h0")
+    assert_close(h2, h, 1e-3, "n64 long final state via h0")
+    tssm.check(dev)
+
+
 def test_ssd_scan_n64_headline_shape(dev):
     """B=8 L=4096 H=16 P=N=64 bf16 (the headline shapes read as SSD), the
     seeded workload of the benchmark: batch 0 and 7, heads 0 and 15 against

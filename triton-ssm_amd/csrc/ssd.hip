@@ -1355,13 +1355,231 @@ __device__ inline void sq_put_state(float* Hf, uint16_t* Hh, uint16_t* Hl, int p
   Hl[sq_bix(p, n)] = (uint16_t)pk_bf16(v - bf16_lo(hi), 0.0f);
 }
 
+// Workgroup -> (row, channel block, time segment).  With rows a multiple of 8
+// the units of a row share blockIdx mod 8, so they run on one XCD (its L2
+// holds the row's B, C and dt) and are dispatched together.
+struct SqUnit {
+  uint32_t row, pb, seg;
+};
+__device__ inline SqUnit sq_unit(uint32_t bid, uint32_t rows, uint32_t npb, uint32_t nsg) {
+  const uint32_t g = npb * nsg;
+  uint32_t row, u;
+  if (rows % 8 == 0) {
+    const uint32_t j = bid >> 3;
+    u = j % g;
+    row = (j / g) * 8 + (bid & 7);
+  } else {
+    row = bid / g;
+    u = bid - row * g;
+  }
+  return {row, u % npb, u / npb};
+}
+
+// Time-segmented form, pass 1: the end state of every segment but the last,
+// from a zero state.
+// Workgroup (row, channel block, segment) walks the segment's 128-step blocks
+// with H' = 2^tot H + sum_s w_s x_s B_s^T (w_s = 2^(tot - cum_s) coef_s), the
+// same products as the state waves of ssd_seq_kernel but with the state tile
+// in registers: wave (k, w) of the 4 PB tiles holds channels 16k.. and state
+// columns 16w..; with one channel block the two halves of the waves take the
+// two halves of each block's steps and add their tiles at the end.  Writes
+// chunkX[row][seg][p][n] and the segment's decay chunkA[row][seg].
+constexpr int kSqAhead = 4;  // blocks whose loads are in flight in the segment state pass
+
+template <int DISC, int PB>
+__global__ __launch_bounds__(512) void ssd_seq_state_kernel(SsdArgs a, uint32_t npb, uint32_t nseg,
+                                                            uint32_t segb) {
+  constexpr int CP = kSqP * PB;
+  constexpr int KS = 2 / PB;              // step halves per tile
+  constexpr int kKs = kSqQ / 32 / KS;     // 32-step products per wave and block
+  __shared__ __align__(16) uint16_t xT[CP * kSqQ];    // x^T [p][s]
+  __shared__ __align__(16) uint16_t BT[kSqN * kSqQ];  // B^T [n][s]
+  __shared__ __align__(16) float s_w[kSqQ];
+  __shared__ __align__(16) float s_red[KS > 1 ? 4 * 64 * 4 : 4];
+  __shared__ float s_dec;
+  const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, c16 = lane & 15;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ti = wv % (4 * PB), kh = wv / (4 * PB);
+  const int w = ti & 3, k = ti >> 2;
+  const int n = 16 * w + c16;
+  const SqUnit un = sq_unit(blockIdx.x, a.rows, npb, nseg - 1);
+  const uint32_t row = un.row, b = row / a.H, h = row - b * a.H;
+  const int p0 = (int)un.pb * CP;
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h + p0;
+  const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
+  const float* dtb = a.dt + b * a.sdt_b + h * a.sdt_h;
+  const int64_t last = a.L - 1;
+  auto clampt = [&](int64_t t) { return t < last ? t : last; };
+  constexpr int kXq = CP / 4;
+  const bool x_item = tid < 64 * kXq;
+  const int x_sp = tid / kXq, x_pq = tid % kXq;
+  // kSqAhead blocks in flight: block i's registers are refilled with block
+  // i + kSqAhead as soon as they are staged (indices clamped into the row, so
+  // the loads past the segment's end stay in bounds and need no branch).
+  struct Blk {
+    uint2 xr[2];
+    u32x4 br[2];
+    float dl0, dl1;
+  };
+  // Every thread issues every load (threads past the x items and the waves
+  // other than wave 0 re-read addresses in bounds and drop the values): a
+  // load under a branch leaves the wait counts unknown where the paths join,
+  // and the compiler then waits for all loads in flight.
+  auto load = [&](Blk& r, int64_t blk) {
+    const int64_t t0 = blk * kSqQ;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      r.xr[j] = *reinterpret_cast<const uint2*>(xb + clampt(t0 + 2 * x_sp + j) * a.sx_l + 4 * x_pq);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      r.br[j] = *reinterpret_cast<const u32x4*>(Bb + clampt(t0 + 2 * (tid >> 3) + j) * a.sB_l +
+                                                8 * (tid & 7));
+    r.dl0 = dtb[clampt(t0 + 2 * lane) * a.sdt_l];
+    r.dl1 = dtb[clampt(t0 + 2 * lane + 1) * a.sdt_l];
+  };
+  // every segment before the last holds segb full blocks
+  const int64_t blk0 = (int64_t)un.seg * segb, blk1 = blk0 + segb;
+  f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+  float adec = 1.0f;
+  Blk rg[kSqAhead] = {};
+  // the sets issued one after another, as the loop refills them, so the wait
+  // before each block's staging can leave the later sets in flight
+#pragma unroll
+  for (int d = 0; d < kSqAhead; ++d) {
+    load(rg[d], blk0 + d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // segb is a multiple of kSqAhead
+  for (int64_t bb = blk0; bb < blk1; bb += kSqAhead)
+#pragma unroll
+  for (int d = 0; d < kSqAhead; ++d) {
+    const int64_t blk = bb + d;
+    const int64_t t0 = blk * kSqQ;
+    Blk& r = rg[d];
+    __syncthreads();  // the previous block's LDS reads are done
+    if (x_item) {
+      const int s = 2 * x_sp;
+#pragma unroll
+      for (int j = 0; j < 4; j += 2) {
+        const uint32_t w0 = j == 0 ? r.xr[0].x : r.xr[0].y, w1 = j == 0 ? r.xr[1].x : r.xr[1].y;
+        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * x_pq + j, s)) = perm_lo(w0, w1);
+        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * x_pq + j + 1, s)) = perm_hi(w0, w1);
+      }
+    }
+    {
+      const int s = 2 * (tid >> 3), ng = tid & 7;
+      const u32x4 b0 = r.br[0], b1 = r.br[1];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const int kk = e >> 1;
+        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e, s)) = perm_lo(b0[kk], b1[kk]);
+        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e + 1, s)) = perm_hi(b0[kk], b1[kk]);
+      }
+    }
+    if (wv == 0) {  // lane: steps 2 lane, 2 lane + 1
+      float l2a, ca, l2b, cb;
+      mfma_step_scalars<DISC>(a, h, t0, 2 * lane, r.dl0, &l2a, &ca);
+      mfma_step_scalars<DISC>(a, h, t0, 2 * lane + 1, r.dl1, &l2b, &cb);
+      float cum = l2a + l2b;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(cum, o);
+        cum += lane >= o ? u : 0.0f;
+      }
+      const float tot = __shfl(cum, 63);
+      const float cum_a = cum - l2b;
+      *reinterpret_cast<float2*>(s_w + 2 * lane) =
+          make_float2(exp2_fast(tot - cum_a) * ca, exp2_fast(tot - cum) * cb);
+      if (lane == 0) s_dec = exp2_fast(tot);
+    }
+    load(r, blk + kSqAhead);
+    __syncthreads();
+    const float dec = s_dec;
+    adec *= dec;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) st[v] *= dec;
+#pragma unroll
+    for (int kk = 0; kk < kKs; ++kk) {
+      const int s0 = 8 * q + 32 * (kh * kKs + kk);
+      const bf16x8_t bt = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + sq_tix(n, s0)));
+      const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
+      const float4 w1 = *reinterpret_cast<const float4*>(s_w + s0 + 4);
+      const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + sq_tix(16 * k + c16, s0));
+      const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
+                          bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
+                          bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
+      bf16x8_t fh, fl;
+      split_bf16(f, fh, fl);
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt, st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt, st, 0, 0, 0);
+    }
+  }
+  if constexpr (KS > 1) {
+    if (kh == 1) *reinterpret_cast<f32x4*>(s_red + (ti * 64 + lane) * 4) = st;
+    __syncthreads();
+    if (kh == 0) {
+      const f32x4 o = *reinterpret_cast<const f32x4*>(s_red + (ti * 64 + lane) * 4);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) st[v] += o[v];
+    }
+  }
+  const int64_t PN = (int64_t)a.P * kSqN;
+  const int64_t slot = (int64_t)row * nseg + un.seg;
+  if (kh == 0) {
+    float* out = a.chunkX + slot * PN + (int64_t)(p0 + 16 * k + 4 * q) * kSqN + n;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) out[v * kSqN] = st[v];
+  }
+  if (un.pb == 0 && tid == 0) a.chunkA[slot] = adec;
+}
+
+// Time-segmented form, pass 2: thread (row, state entry e) walks the segments
+// in order, entry[row][s] = the state entering segment s (h0, or zero, for
+// s = 0), next = decay(s) * entry + end(s).  The last segment's end state is
+// not needed (pass 3 forms the final state), so loads stop at segment
+// nseg - 2 (indices clamped there: every load of a batch is issued at once
+// and stays in bounds).
+constexpr int kSegBatch = 8;
+__global__ __launch_bounds__(256) void ssd_seg_prefix_kernel(SsdArgs a, uint32_t nseg, int64_t PN) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = i / PN, e = i - row * PN;
+  if (row >= (int64_t)a.rows) return;
+  float S = a.h0 ? a.h0[row * PN + e] : 0.0f;
+  const float* X = a.chunkX + row * nseg * PN + e;
+  const float* A = a.chunkA + row * nseg;
+  float* E = a.entry + row * nseg * PN + e;
+  const uint32_t smax = nseg >= 2 ? nseg - 2 : 0;
+  for (uint32_t s0 = 0; s0 < nseg; s0 += kSegBatch) {
+    float xs[kSegBatch], as[kSegBatch];
+#pragma unroll
+    for (int k = 0; k < kSegBatch; ++k) {
+      const uint32_t sc = min(s0 + k, smax);
+      xs[k] = X[(int64_t)sc * PN];
+      as[k] = A[sc];
+    }
+#pragma unroll
+    for (int k = 0; k < kSegBatch; ++k) {
+      if (s0 + k < nseg) {
+        E[(int64_t)(s0 + k) * PN] = S;
+        S = __builtin_fmaf(as[k], S, xs[k]);
+      }
+    }
+  }
+}
+
 // 8 waves: waves 0-3 form the weighted Gram blocks of their output groups
 // once and apply them to every channel block of the workgroup (PB blocks of
 // 16), then the carried-state term and the outputs; waves 4-7 update state
 // columns 16(w-4).. for every channel block.  Both read the state entering the
 // block; the updated state goes to the other buffer.
+//
+// Time-segmented form (nseg > 1), pass 3: workgroup (row, channel block,
+// segment) starts from the segment's entry state, entry[row][seg] (pass 2
+// puts h0, or zero, into segment 0's), and the last segment writes the final
+// state.
 template <int DISC, bool HAS_D, int PB>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void ssd_seq_kernel(SsdArgs a, uint32_t npb) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void ssd_seq_kernel(
+    SsdArgs a, uint32_t npb, uint32_t nseg, uint32_t segb) {
   constexpr int CP = kSqP * PB;  // channels per workgroup
   __shared__ __align__(16) uint16_t xT[CP * kSqQ];     // x^T [p][s]
   __shared__ __align__(16) uint16_t Bn[kSqQ * kSqN];   // B [s][n]
@@ -1374,15 +1592,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
   const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, c16 = lane & 15;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int w = wv & 3;
-  uint32_t row, pb;
-  if (a.rows % 8 == 0) {  // the channel blocks of a row on one XCD, dispatched together
-    const uint32_t j = blockIdx.x >> 3;
-    pb = j % npb;
-    row = (j / npb) * 8 + (blockIdx.x & 7);
-  } else {
-    row = blockIdx.x / npb;
-    pb = blockIdx.x - row * npb;
-  }
+  const SqUnit un = sq_unit(blockIdx.x, a.rows, npb, nseg);
+  const uint32_t row = un.row, pb = un.pb;
   const uint32_t b = row / a.H, h = row - b * a.H;
   const int p0 = (int)pb * CP;
   const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h + p0;
@@ -1391,10 +1602,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
   const float* dtb = a.dt + b * a.sdt_b + h * a.sdt_h;
   uint16_t* yb = reinterpret_cast<uint16_t*>(a.y) + b * a.sy_b + h * a.sy_h + p0;
   const int64_t PN = (int64_t)a.P * kSqN;
+  const float* hin = nseg > 1 ? a.entry + ((int64_t)row * nseg + un.seg) * PN
+                              : (a.h0 ? a.h0 + row * PN : nullptr);
   for (int k = tid; k < CP * kSqN; k += 512) {
     const int p = k >> 6, n = k & 63;
-    sq_put_state(sH[0], sHh[0], sHl[0], p, n,
-                 a.h0 ? a.h0[row * PN + (int64_t)(p0 + p) * kSqN + n] : 0.0f);
+    sq_put_state(sH[0], sHh[0], sHl[0], p, n, hin ? hin[(int64_t)(p0 + p) * kSqN + n] : 0.0f);
   }
   // output groups of an output wave and their steps
   const int tA = w, tB = 7 - w;
@@ -1431,9 +1643,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
     }
   };
   const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
-  load(0);
+  const int64_t blk0 = (int64_t)un.seg * segb;
+  const int64_t blk1 = blk0 + segb < nblk ? blk0 + segb : nblk;
+  load(blk0 * kSqQ);
   int cur = 0;
-  for (int64_t blk = 0; blk < nblk; ++blk) {
+  for (int64_t blk = blk0; blk < blk1; ++blk) {
     const int64_t t0 = blk * kSqQ;
     __syncthreads();  // the previous block's LDS reads are done
     if (x_item) {
@@ -1487,7 +1701,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
         s_fac = tot >= -240.0f;
       }
     }
-    if (blk + 1 < nblk) load(t0 + kSqQ);
+    if (blk + 1 < blk1) load(t0 + kSqQ);
     __syncthreads();
 
     if (wv < 4) {
@@ -1570,7 +1784,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
     }
     cur ^= 1;
   }
-  if (a.h_last) {
+  if (a.h_last && un.seg + 1 == nseg) {
     __syncthreads();
     for (int k = tid; k < CP * kSqN; k += 512) {
       const int p = k >> 6, n = k & 63;
@@ -1579,18 +1793,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
   }
 }
 
+// Time segments of the one-pass kernel: enough (row, channel block, segment)
+// workgroups for one per CU (the kernel holds one 512-thread workgroup per
+// CU), segments of a multiple of kSqAhead 128-step blocks and no more
+// segments than the workspace has chunk slots.  With one segment the kernel walks whole rows
+// from h0; with more, pass 1 forms each segment's end state from zero, pass 2
+// their entry states (h0 in the first), and pass 3 the outputs and the final
+// state.
+constexpr int64_t kSeqGroups = 256;
+
+template <int DISC, bool HAS_D, int PB>
+int launch_ssd_seq_pb(int64_t rows, int64_t npb, hipStream_t s, const SsdArgs& a) {
+  const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
+  int64_t nseg = (kSeqGroups + rows * npb - 1) / (rows * npb);
+  const int64_t by_len = (nblk + kSqAhead - 1) / kSqAhead;
+  if (nseg > by_len) nseg = by_len;
+  if (nseg > (int64_t)a.nchunks) nseg = a.nchunks;
+  if (nseg < 1) nseg = 1;
+  const int64_t segb = ((nblk + nseg - 1) / nseg + kSqAhead - 1) / kSqAhead * kSqAhead;
+  nseg = (nblk + segb - 1) / segb;
+  if (nseg > 1) {
+    hipLaunchKernelGGL((ssd_seq_state_kernel<DISC, PB>), dim3((unsigned)(rows * npb * (nseg - 1))),
+                       dim3(512), 0, s, a, (uint32_t)npb, (uint32_t)nseg, (uint32_t)segb);
+    const int64_t PN = (int64_t)a.P * kSqN;
+    hipLaunchKernelGGL(ssd_seg_prefix_kernel, dim3((unsigned)((rows * PN + 255) / 256)), dim3(256),
+                       0, s, a, (uint32_t)nseg, PN);
+  }
+  hipLaunchKernelGGL((ssd_seq_kernel<DISC, HAS_D, PB>), dim3((unsigned)(rows * npb * nseg)),
+                     dim3(512), 0, s, a, (uint32_t)npb, (uint32_t)nseg, (uint32_t)segb);
+  return launch_status();
+}
+
 template <int DISC, bool HAS_D>
 int launch_ssd_seq_d(int64_t rows, int64_t P, hipStream_t s, const SsdArgs& a) {
-  if (P % 32 == 0) {
-    const uint32_t npb = (uint32_t)(P / 32);
-    hipLaunchKernelGGL((ssd_seq_kernel<DISC, HAS_D, 2>), dim3((unsigned)(rows * npb)), dim3(512), 0,
-                       s, a, npb);
-  } else {
-    const uint32_t npb = (uint32_t)(P / 16);
-    hipLaunchKernelGGL((ssd_seq_kernel<DISC, HAS_D, 1>), dim3((unsigned)(rows * npb)), dim3(512), 0,
-                       s, a, npb);
-  }
-  return launch_status();
+  if (P % 32 == 0) return launch_ssd_seq_pb<DISC, HAS_D, 2>(rows, P / 32, s, a);
+  return launch_ssd_seq_pb<DISC, HAS_D, 1>(rows, P / 16, s, a);
 }
 
 template <int DISC>
