@@ -1375,193 +1375,185 @@ __device__ inline SqUnit sq_unit(uint32_t bid, uint32_t rows, uint32_t npb, uint
   return {row, u % npb, u / npb};
 }
 
-// Time-segmented form, pass 1: the end state of every segment but the last,
-// from a zero state.
-// Workgroup (row, channel block, segment) walks the segment's 128-step blocks
-// with H' = 2^tot H + sum_s w_s x_s B_s^T (w_s = 2^(tot - cum_s) coef_s), the
-// same products as the state waves of ssd_seq_kernel but with the state tile
-// in registers: wave (k, w) of the 4 PB tiles holds channels 16k.. and state
-// columns 16w..; with one channel block the two halves of the waves take the
-// two halves of each block's steps and add their tiles at the end.  Writes
-// chunkX[row][seg][p][n] and the segment's decay chunkA[row][seg].
-constexpr int kSqAhead = 4;  // blocks whose loads are in flight in the segment state pass
+// Time-segmented form, pass 1: the end state, from a zero state, of every
+// sub-segment before the last segment (a segment splits into m sub-segments
+// so that pass 1 has enough waves).  One wave per workgroup, no state shared
+// between waves: wave (row, sub-segment, tile) holds a 16CT-channel x
+// 32-column tile of the state in registers and walks the sub-segment in
+// 32-step sub-blocks, H' = 2^tot H + sum_s w_s x_s B_s^T (w_s = 2^(tot -
+// cum_s) coef_s) as bf16 hi/lo products on the matrix cores.  It stages its
+// own x and B slices through LDS (transposed to [column][step], the operand
+// layout of the products) and forms the sub-block's weights itself, so the
+// only barriers are its own.  kSgAhead sub-blocks of loads are in flight.
+// Writes chunkX[row][sub][p][n] and the sub-segment's decay chunkA[row][sub].
+constexpr int kSgAhead = 4;
+constexpr int kSgStride = 40;  // LDS row stride (bf16) of the staged slices
 
-template <int DISC, int PB>
-__global__ __launch_bounds__(512) void ssd_seq_state_kernel(SsdArgs a, uint32_t npb, uint32_t nseg,
-                                                            uint32_t segb) {
-  constexpr int CP = kSqP * PB;
-  constexpr int KS = 2 / PB;              // step halves per tile
-  constexpr int kKs = kSqQ / 32 / KS;     // 32-step products per wave and block
-  __shared__ __align__(16) uint16_t xT[CP * kSqQ];    // x^T [p][s]
-  __shared__ __align__(16) uint16_t BT[kSqN * kSqQ];  // B^T [n][s]
-  __shared__ __align__(16) float s_w[kSqQ];
-  __shared__ __align__(16) float s_red[KS > 1 ? 4 * 64 * 4 : 4];
-  __shared__ float s_dec;
-  const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, c16 = lane & 15;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ti = wv % (4 * PB), kh = wv / (4 * PB);
-  const int w = ti & 3, k = ti >> 2;
-  const int n = 16 * w + c16;
-  const SqUnit un = sq_unit(blockIdx.x, a.rows, npb, nseg - 1);
-  const uint32_t row = un.row, b = row / a.H, h = row - b * a.H;
-  const int p0 = (int)un.pb * CP;
-  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h + p0;
-  const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h;
+template <int DISC, int CT>
+__global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t tiles,
+                                                           uint32_t nsub, uint32_t subb) {
+  __shared__ __align__(16) uint16_t xT[16 * CT * kSgStride];
+  __shared__ __align__(16) uint16_t BT[32 * kSgStride];
+  __shared__ __align__(16) float s_w[32];
+  const int lane = threadIdx.x, q = lane >> 4, c16 = lane & 15;
+  const uint32_t ngrp = a.rows * nsub, bid = blockIdx.x;
+  uint32_t grp, tau;
+  if (ngrp % 8 == 0) {  // the tiles of a (row, sub-segment) on one XCD
+    const uint32_t j = bid >> 3;
+    tau = j % tiles;
+    grp = (j / tiles) * 8 + (bid & 7);
+  } else {
+    grp = bid / tiles;
+    tau = bid - grp * tiles;
+  }
+  const uint32_t row = grp / nsub, sub = grp - row * nsub;
+  const uint32_t b = row / a.H, h = row - b * a.H;
+  const int c0 = (int)(tau >> 1) * 16 * CT, n0 = (int)(tau & 1) * 32;
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(a.x) + b * a.sx_b + h * a.sx_h + c0;
+  const uint16_t* Bb = reinterpret_cast<const uint16_t*>(a.B) + b * a.sB_b + h * a.sB_h + n0;
   const float* dtb = a.dt + b * a.sdt_b + h * a.sdt_h;
+  const float a2 = -expf(a.A_log[h]) * kLog2e;
   const int64_t last = a.L - 1;
   auto clampt = [&](int64_t t) { return t < last ? t : last; };
-  constexpr int kXq = CP / 4;
-  const bool x_item = tid < 64 * kXq;
-  const int x_sp = tid / kXq, x_pq = tid % kXq;
-  // kSqAhead blocks in flight: block i's registers are refilled with block
-  // i + kSqAhead as soon as they are staged (indices clamped into the row, so
-  // the loads past the segment's end stay in bounds and need no branch).
-  struct Blk {
-    uint2 xr[2];
-    u32x4 br[2];
-    float dl0, dl1;
+  // lane: step pair sp, 8-column octet oc (x: octets past 2 CT re-read the
+  // first ones and are not staged)
+  const int sp = lane >> 2, oc = lane & 3;
+  const int xoc = oc < 2 * CT ? oc : oc - 2 * CT;
+  struct Sub {
+    u32x4 xr[2], br[2];
+    float dl;
   };
-  // Every thread issues every load (threads past the x items and the waves
-  // other than wave 0 re-read addresses in bounds and drop the values): a
-  // load under a branch leaves the wait counts unknown where the paths join,
-  // and the compiler then waits for all loads in flight.
-  auto load = [&](Blk& r, int64_t blk) {
-    const int64_t t0 = blk * kSqQ;
+  auto load = [&](Sub& r, int64_t t0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      r.xr[j] = *reinterpret_cast<const uint2*>(xb + clampt(t0 + 2 * x_sp + j) * a.sx_l + 4 * x_pq);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      r.br[j] = *reinterpret_cast<const u32x4*>(Bb + clampt(t0 + 2 * (tid >> 3) + j) * a.sB_l +
-                                                8 * (tid & 7));
-    r.dl0 = dtb[clampt(t0 + 2 * lane) * a.sdt_l];
-    r.dl1 = dtb[clampt(t0 + 2 * lane + 1) * a.sdt_l];
+    for (int j = 0; j < 2; ++j) {
+      const int64_t t = clampt(t0 + 2 * sp + j);
+      r.xr[j] = *reinterpret_cast<const u32x4*>(xb + t * a.sx_l + 8 * xoc);
+      r.br[j] = *reinterpret_cast<const u32x4*>(Bb + t * a.sB_l + 8 * oc);
+    }
+    r.dl = dtb[clampt(t0 + (lane & 31)) * a.sdt_l];
   };
-  // every segment before the last holds segb full blocks
-  const int64_t blk0 = (int64_t)un.seg * segb, blk1 = blk0 + segb;
-  f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+  // every sub-segment before the last segment is whole: subb sub-blocks of
+  // 32 steps, a multiple of kSgAhead (the refills of the last sets read
+  // steps past the sub-segment, clamped into the row, and are never staged)
+  const int64_t tbeg = (int64_t)sub * subb * 32;
+  f32x4 st[CT][2];
+#pragma unroll
+  for (int i = 0; i < CT; ++i) st[i][0] = st[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float adec = 1.0f;
-  Blk rg[kSqAhead] = {};
-  // the sets issued one after another, as the loop refills them, so the wait
-  // before each block's staging can leave the later sets in flight
+  Sub rg[kSgAhead];
 #pragma unroll
-  for (int d = 0; d < kSqAhead; ++d) {
-    load(rg[d], blk0 + d);
+  for (int d = 0; d < kSgAhead; ++d) {
+    load(rg[d], tbeg + 32 * d);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // segb is a multiple of kSqAhead
-  for (int64_t bb = blk0; bb < blk1; bb += kSqAhead)
+  for (int64_t kb = 0; kb < (int64_t)subb; kb += kSgAhead)
 #pragma unroll
-  for (int d = 0; d < kSqAhead; ++d) {
-    const int64_t blk = bb + d;
-    const int64_t t0 = blk * kSqQ;
-    Blk& r = rg[d];
-    __syncthreads();  // the previous block's LDS reads are done
-    if (x_item) {
-      const int s = 2 * x_sp;
-#pragma unroll
-      for (int j = 0; j < 4; j += 2) {
-        const uint32_t w0 = j == 0 ? r.xr[0].x : r.xr[0].y, w1 = j == 0 ? r.xr[1].x : r.xr[1].y;
-        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * x_pq + j, s)) = perm_lo(w0, w1);
-        *reinterpret_cast<uint32_t*>(xT + sq_tix(4 * x_pq + j + 1, s)) = perm_hi(w0, w1);
-      }
-    }
+  for (int d = 0; d < kSgAhead; ++d) {
     {
-      const int s = 2 * (tid >> 3), ng = tid & 7;
-      const u32x4 b0 = r.br[0], b1 = r.br[1];
+      const int64_t t0 = tbeg + 32 * (kb + d);
+      Sub& r = rg[d];
+      __syncthreads();  // the previous sub-block's LDS reads are done
+      if (oc < 2 * CT) {
 #pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const int kk = e >> 1;
-        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e, s)) = perm_lo(b0[kk], b1[kk]);
-        *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e + 1, s)) = perm_hi(b0[kk], b1[kk]);
+        for (int e = 0; e < 4; ++e) {
+          *reinterpret_cast<uint32_t*>(xT + (8 * oc + 2 * e) * kSgStride + 2 * sp) =
+              perm_lo(r.xr[0][e], r.xr[1][e]);
+          *reinterpret_cast<uint32_t*>(xT + (8 * oc + 2 * e + 1) * kSgStride + 2 * sp) =
+              perm_hi(r.xr[0][e], r.xr[1][e]);
+        }
       }
-    }
-    if (wv == 0) {  // lane: steps 2 lane, 2 lane + 1
-      float l2a, ca, l2b, cb;
-      mfma_step_scalars<DISC>(a, h, t0, 2 * lane, r.dl0, &l2a, &ca);
-      mfma_step_scalars<DISC>(a, h, t0, 2 * lane + 1, r.dl1, &l2b, &cb);
-      float cum = l2a + l2b;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
+      for (int e = 0; e < 4; ++e) {
+        *reinterpret_cast<uint32_t*>(BT + (8 * oc + 2 * e) * kSgStride + 2 * sp) =
+            perm_lo(r.br[0][e], r.br[1][e]);
+        *reinterpret_cast<uint32_t*>(BT + (8 * oc + 2 * e + 1) * kSgStride + 2 * sp) =
+            perm_hi(r.br[0][e], r.br[1][e]);
+      }
+      // weights of the sub-block's 32 steps (lanes 32-63 repeat lanes 0-31)
+      const int sl = lane & 31;
+      const float d = t0 + sl < a.L ? r.dl : 0.0f;
+      const float l2 = d * a2;
+      const float ab = exp2_fast(l2);
+      const float coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(l2 * 0.6931471805599453f, ab) * d : d;
+      float cum = l2;
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) {
         const float u = __shfl_up(cum, o);
-        cum += lane >= o ? u : 0.0f;
+        cum += sl >= o ? u : 0.0f;
       }
-      const float tot = __shfl(cum, 63);
-      const float cum_a = cum - l2b;
-      *reinterpret_cast<float2*>(s_w + 2 * lane) =
-          make_float2(exp2_fast(tot - cum_a) * ca, exp2_fast(tot - cum) * cb);
-      if (lane == 0) s_dec = exp2_fast(tot);
-    }
-    load(r, blk + kSqAhead);
-    __syncthreads();
-    const float dec = s_dec;
-    adec *= dec;
+      const float tot = __shfl(cum, 31);
+      s_w[sl] = exp2_fast(tot - cum) * coef;
+      const float dec = exp2_fast(tot);
+      load(r, t0 + 32 * kSgAhead);
+      __syncthreads();
+      adec *= dec;
+      const float4 w0 = *reinterpret_cast<const float4*>(s_w + 8 * q);
+      const float4 w1 = *reinterpret_cast<const float4*>(s_w + 8 * q + 4);
+      bf16x8_t bt[2];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) st[v] *= dec;
+      for (int j = 0; j < 2; ++j)
+        bt[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + (16 * j + c16) * kSgStride + 8 * q));
 #pragma unroll
-    for (int kk = 0; kk < kKs; ++kk) {
-      const int s0 = 8 * q + 32 * (kh * kKs + kk);
-      const bf16x8_t bt = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + sq_tix(n, s0)));
-      const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
-      const float4 w1 = *reinterpret_cast<const float4*>(s_w + s0 + 4);
-      const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + sq_tix(16 * k + c16, s0));
-      const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
-                          bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
-                          bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
-      bf16x8_t fh, fl;
-      split_bf16(f, fh, fl);
-      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt, st, 0, 0, 0);
-      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt, st, 0, 0, 0);
-    }
-  }
-  if constexpr (KS > 1) {
-    if (kh == 1) *reinterpret_cast<f32x4*>(s_red + (ti * 64 + lane) * 4) = st;
-    __syncthreads();
-    if (kh == 0) {
-      const f32x4 o = *reinterpret_cast<const f32x4*>(s_red + (ti * 64 + lane) * 4);
+      for (int i = 0; i < CT; ++i) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + (16 * i + c16) * kSgStride + 8 * q);
+        const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
+                            bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
+                            bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
+        bf16x8_t fh, fl;
+        split_bf16(f, fh, fl);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) st[v] += o[v];
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) st[i][j][v] *= dec;
+          st[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt[j], st[i][j], 0, 0, 0);
+          st[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt[j], st[i][j], 0, 0, 0);
+        }
+      }
     }
   }
   const int64_t PN = (int64_t)a.P * kSqN;
-  const int64_t slot = (int64_t)row * nseg + un.seg;
-  if (kh == 0) {
-    float* out = a.chunkX + slot * PN + (int64_t)(p0 + 16 * k + 4 * q) * kSqN + n;
+  const int64_t slot = (int64_t)row * nsub + sub;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) out[v * kSqN] = st[v];
-  }
-  if (un.pb == 0 && tid == 0) a.chunkA[slot] = adec;
+  for (int i = 0; i < CT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float* out = a.chunkX + slot * PN + (int64_t)(c0 + 16 * i + 4 * q) * kSqN + n0 + 16 * j + c16;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) out[v * kSqN] = st[i][j][v];
+    }
+  if (tau == 0 && lane == 0) a.chunkA[slot] = adec;
 }
 
-// Time-segmented form, pass 2: thread (row, state entry e) walks the segments
-// in order, entry[row][s] = the state entering segment s (h0, or zero, for
-// s = 0), next = decay(s) * entry + end(s).  The last segment's end state is
-// not needed (pass 3 forms the final state), so loads stop at segment
-// nseg - 2 (indices clamped there: every load of a batch is issued at once
-// and stays in bounds).
+// Time-segmented form, pass 2: thread (row, state entry e) walks the
+// sub-segments in order, S <- decay(k) S + end(k) from h0 (or zero), and
+// writes entry[row][s] = S at the start of segment s (every m-th
+// sub-segment).  Loads are clamped to the last sub-segment pass 1 formed, so
+// every load of a batch is issued at once and stays in bounds.
 constexpr int kSegBatch = 8;
-__global__ __launch_bounds__(256) void ssd_seg_prefix_kernel(SsdArgs a, uint32_t nseg, int64_t PN) {
+__global__ __launch_bounds__(256) void ssd_seg_prefix_kernel(SsdArgs a, uint32_t nsub, uint32_t m,
+                                                             int64_t PN) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = i / PN, e = i - row * PN;
   if (row >= (int64_t)a.rows) return;
+  const uint32_t nseg = nsub / m + 1;
   float S = a.h0 ? a.h0[row * PN + e] : 0.0f;
-  const float* X = a.chunkX + row * nseg * PN + e;
-  const float* A = a.chunkA + row * nseg;
+  const float* X = a.chunkX + row * nsub * PN + e;
+  const float* A = a.chunkA + row * nsub;
   float* E = a.entry + row * nseg * PN + e;
-  const uint32_t smax = nseg >= 2 ? nseg - 2 : 0;
-  for (uint32_t s0 = 0; s0 < nseg; s0 += kSegBatch) {
+  for (uint32_t s0 = 0; s0 <= nsub; s0 += kSegBatch) {
     float xs[kSegBatch], as[kSegBatch];
 #pragma unroll
     for (int k = 0; k < kSegBatch; ++k) {
-      const uint32_t sc = min(s0 + k, smax);
+      const uint32_t sc = min(s0 + k, nsub - 1);
       xs[k] = X[(int64_t)sc * PN];
       as[k] = A[sc];
     }
 #pragma unroll
     for (int k = 0; k < kSegBatch; ++k) {
-      if (s0 + k < nseg) {
-        E[(int64_t)(s0 + k) * PN] = S;
-        S = __builtin_fmaf(as[k], S, xs[k]);
+      const uint32_t sk = s0 + k;
+      if (sk <= nsub) {
+        if (sk % m == 0) E[(int64_t)(sk / m) * PN] = S;
+        if (sk < nsub) S = __builtin_fmaf(as[k], S, xs[k]);
       }
     }
   }
@@ -1795,29 +1787,38 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
 
 // Time segments of the one-pass kernel: enough (row, channel block, segment)
 // workgroups for one per CU (the kernel holds one 512-thread workgroup per
-// CU), segments of a multiple of kSqAhead 128-step blocks and no more
-// segments than the workspace has chunk slots.  With one segment the kernel walks whole rows
-// from h0; with more, pass 1 forms each segment's end state from zero, pass 2
-// their entry states (h0 in the first), and pass 3 the outputs and the final
-// state.
-constexpr int64_t kSeqGroups = 256;
+// CU), segments of at least two 128-step blocks and no more segments than
+// the workspace has chunk slots.  With one segment the kernel walks whole
+// rows from h0; with more, pass 1 forms the end states of the sub-segments
+// before the last segment (m per segment, m dividing the segment's blocks,
+// enough for about kSgWaves waves), pass 2 the segments' entry states (h0 in
+// the first), and pass 3 the outputs and the final state.
+constexpr int64_t kSeqGroups = 256, kSeqMinSegBlocks = 2, kSgWaves = 2048;
+static_assert((kSqQ / 32) % kSgAhead == 0, "pass-1 sub-segments hold whole sets of sub-blocks");
 
 template <int DISC, bool HAS_D, int PB>
 int launch_ssd_seq_pb(int64_t rows, int64_t npb, hipStream_t s, const SsdArgs& a) {
   const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
   int64_t nseg = (kSeqGroups + rows * npb - 1) / (rows * npb);
-  const int64_t by_len = (nblk + kSqAhead - 1) / kSqAhead;
+  const int64_t by_len = (nblk + kSeqMinSegBlocks - 1) / kSeqMinSegBlocks;
   if (nseg > by_len) nseg = by_len;
   if (nseg > (int64_t)a.nchunks) nseg = a.nchunks;
   if (nseg < 1) nseg = 1;
-  const int64_t segb = ((nblk + nseg - 1) / nseg + kSqAhead - 1) / kSqAhead * kSqAhead;
+  const int64_t segb = (nblk + nseg - 1) / nseg;
   nseg = (nblk + segb - 1) / segb;
   if (nseg > 1) {
-    hipLaunchKernelGGL((ssd_seq_state_kernel<DISC, PB>), dim3((unsigned)(rows * npb * (nseg - 1))),
-                       dim3(512), 0, s, a, (uint32_t)npb, (uint32_t)nseg, (uint32_t)segb);
+    constexpr int CT = PB;  // channel tiles of 16 per pass-1 wave
+    const int64_t tiles = (a.P / (16 * CT)) * 2;
+    const int64_t want = (kSgWaves + rows * (nseg - 1) * tiles - 1) / (rows * (nseg - 1) * tiles);
+    int64_t m = want < segb ? want : segb;
+    while (m > 1 && (segb % m != 0 || (nseg - 1) * m > (int64_t)a.nchunks)) --m;
+    const int64_t nsub = (nseg - 1) * m;
+    hipLaunchKernelGGL((ssd_seg_state_kernel<DISC, CT>), dim3((unsigned)(rows * nsub * tiles)),
+                       dim3(64), 0, s, a, (uint32_t)tiles, (uint32_t)nsub,
+                       (uint32_t)(segb / m * (kSqQ / 32)));
     const int64_t PN = (int64_t)a.P * kSqN;
     hipLaunchKernelGGL(ssd_seg_prefix_kernel, dim3((unsigned)((rows * PN + 255) / 256)), dim3(256),
-                       0, s, a, (uint32_t)nseg, PN);
+                       0, s, a, (uint32_t)nsub, (uint32_t)m, PN);
   }
   hipLaunchKernelGGL((ssd_seq_kernel<DISC, HAS_D, PB>), dim3((unsigned)(rows * npb * nseg)),
                      dim3(512), 0, s, a, (uint32_t)npb, (uint32_t)nseg, (uint32_t)segb);
