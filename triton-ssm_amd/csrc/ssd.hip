@@ -1563,7 +1563,9 @@ __global__ __launch_bounds__(256) void ssd_seg_prefix_kernel(SsdArgs a, uint32_t
 // once and apply them to every channel block of the workgroup (PB blocks of
 // 16), then the carried-state term and the outputs; waves 4-7 update state
 // columns 16(w-4).. for every channel block.  Both read the state entering the
-// block; the updated state goes to the other buffer.
+// block; the updated state goes to the other buffer.  The staged operands are
+// double-buffered, so every wave stages block i+1 (and wave 4 forms its step
+// scalars) before it works on block i, with one barrier per block.
 //
 // Time-segmented form (nseg > 1), pass 3: workgroup (row, channel block,
 // segment) starts from the segment's entry state, entry[row][seg] (pass 2
@@ -1573,14 +1575,17 @@ template <int DISC, bool HAS_D, int PB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void ssd_seq_kernel(
     SsdArgs a, uint32_t npb, uint32_t nseg, uint32_t segb) {
   constexpr int CP = kSqP * PB;  // channels per workgroup
-  __shared__ __align__(16) uint16_t xT[CP * kSqQ];     // x^T [p][s]
-  __shared__ __align__(16) uint16_t Bn[kSqQ * kSqN];   // B [s][n]
-  __shared__ __align__(16) uint16_t BT[kSqN * kSqQ];   // B^T [n][s]
+  // staged blocks, double-buffered: block i+1 is staged while block i is used
+  __shared__ __align__(16) uint16_t xTb[2][CP * kSqQ];    // x^T [p][s]
+  __shared__ __align__(16) uint16_t Bnb[2][kSqQ * kSqN];  // B [s][n]
+  __shared__ __align__(16) uint16_t BTb[2][kSqN * kSqQ];  // B^T [n][s]
   __shared__ __align__(16) float sH[2][CP * kSqN];     // state slice, ping-pong
   __shared__ __align__(16) uint16_t sHh[2][CP * kSqN], sHl[2][CP * kSqN];  // its bf16 parts
-  __shared__ __align__(16) float s_cum[kSqQ], s_coef[kSqQ], s_w[kSqQ], s_u[kSqQ], s_v[kSqQ];
-  __shared__ float s_dec, s_eref;
-  __shared__ int s_fac;
+  __shared__ __align__(16) float s_cumb[2][kSqQ], s_coefb[2][kSqQ], s_wb[2][kSqQ], s_ub[2][kSqQ],
+      s_vb[2][kSqQ];
+  __shared__ float s_decb[2], s_erefb[2];
+  __shared__ int s_facb[2];
+  __shared__ float s_D[HAS_D ? CP : 1];  // the skip term of the workgroup's channels
   const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, c16 = lane & 15;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int w = wv & 3;
@@ -1600,6 +1605,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
     const int p = k >> 6, n = k & 63;
     sq_put_state(sH[0], sHh[0], sHl[0], p, n, hin ? hin[(int64_t)(p0 + p) * kSqN + n] : 0.0f);
   }
+  if constexpr (HAS_D) {
+    if (tid < CP) s_D[tid] = a.D[h * a.P + p0 + tid];
+  }
   // output groups of an output wave and their steps
   const int tA = w, tB = 7 - w;
   const int sA = 16 * tA + c16, sB = 16 * tB + c16;
@@ -1613,7 +1621,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
   uint2 xr[2] = {};
   u32x4 br[2], cA0 = {}, cA1 = {}, cB0 = {}, cB1 = {};
   float dl0 = 0.0f, dl1 = 0.0f;
-  auto load = [&](int64_t t0) {
+  // x, B and dt are loaded two blocks ahead of their use (one ahead of their
+  // staging), C one block ahead (the output waves read it from registers)
+  auto load_xb = [&](int64_t t0) {
     if (x_item) {
 #pragma unroll
       for (int k = 0; k < 2; ++k)
@@ -1623,25 +1633,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
     for (int k = 0; k < 2; ++k)  // steps 2 (tid >> 3) + k, state columns 8 (tid & 7) ..
       br[k] = *reinterpret_cast<const u32x4*>(Bb + clampt(t0 + 2 * (tid >> 3) + k) * a.sB_l +
                                               8 * (tid & 7));
+    if (wv == 4) {
+      dl0 = dtb[clampt(t0 + 2 * lane) * a.sdt_l];
+      dl1 = dtb[clampt(t0 + 2 * lane + 1) * a.sdt_l];
+    }
+  };
+  auto load_c = [&](int64_t t0) {
     if (wv < 4) {
       const int64_t ta = clampt(t0 + sA), tb = clampt(t0 + sB);
       cA0 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q);
       cA1 = *reinterpret_cast<const u32x4*>(Cb + ta * a.sC_l + 8 * q + 32);
       cB0 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q);
       cB1 = *reinterpret_cast<const u32x4*>(Cb + tb * a.sC_l + 8 * q + 32);
-    } else if (wv == 4) {
-      dl0 = dtb[clampt(t0 + 2 * lane) * a.sdt_l];
-      dl1 = dtb[clampt(t0 + 2 * lane + 1) * a.sdt_l];
     }
   };
-  const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
-  const int64_t blk0 = (int64_t)un.seg * segb;
-  const int64_t blk1 = blk0 + segb < nblk ? blk0 + segb : nblk;
-  load(blk0 * kSqQ);
-  int cur = 0;
-  for (int64_t blk = blk0; blk < blk1; ++blk) {
-    const int64_t t0 = blk * kSqQ;
-    __syncthreads();  // the previous block's LDS reads are done
+  // Stage the block in xr / br / dl (its first step t0) into buffer sb: x^T,
+  // B, B^T, and (wave 4) the per-step scalars.
+  auto stage = [&](int sb, int64_t t0) {
+    uint16_t* xT = xTb[sb];
+    uint16_t* Bn = Bnb[sb];
+    uint16_t* BT = BTb[sb];
     if (x_item) {
       const int s = 2 * x_sp;
 #pragma unroll
@@ -1663,7 +1674,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
         *reinterpret_cast<uint32_t*>(BT + sq_tix(8 * ng + e + 1, s)) = perm_hi(b0[k], b1[k]);
       }
     }
-    const u32x4 a0 = cA0, a1 = cA1, b0 = cB0, b1 = cB1;
     if (wv == 4) {  // lane: steps 2 lane, 2 lane + 1
       float l2a, ca, l2b, cb;
       mfma_step_scalars<DISC>(a, h, t0, 2 * lane, dl0, &l2a, &ca);
@@ -1679,26 +1689,52 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
       // factored decay about the block's mid-value: every factor stays within
       // 2^+-120 while the block decays by at most 2^-240
       const float ref = 0.5f * tot;
-      *reinterpret_cast<float2*>(s_cum + 2 * lane) = make_float2(cum_a, cum);
-      *reinterpret_cast<float2*>(s_coef + 2 * lane) = make_float2(ca, cb);
-      *reinterpret_cast<float2*>(s_w + 2 * lane) =
+      *reinterpret_cast<float2*>(s_cumb[sb] + 2 * lane) = make_float2(cum_a, cum);
+      *reinterpret_cast<float2*>(s_coefb[sb] + 2 * lane) = make_float2(ca, cb);
+      *reinterpret_cast<float2*>(s_wb[sb] + 2 * lane) =
           make_float2(exp2_fast(tot - cum_a) * ca, exp2_fast(tot - cum) * cb);
-      *reinterpret_cast<float2*>(s_u + 2 * lane) =
+      *reinterpret_cast<float2*>(s_ub[sb] + 2 * lane) =
           make_float2(exp2_fast(cum_a - ref), exp2_fast(cum - ref));
-      *reinterpret_cast<float2*>(s_v + 2 * lane) =
+      *reinterpret_cast<float2*>(s_vb[sb] + 2 * lane) =
           make_float2(exp2_fast(ref - cum_a) * ca, exp2_fast(ref - cum) * cb);
       if (lane == 0) {
-        s_dec = exp2_fast(tot);
-        s_eref = exp2_fast(ref);
-        s_fac = tot >= -240.0f;
+        s_decb[sb] = exp2_fast(tot);
+        s_erefb[sb] = exp2_fast(ref);
+        s_facb[sb] = tot >= -240.0f;
       }
     }
-    if (blk + 1 < blk1) load(t0 + kSqQ);
-    __syncthreads();
+  };
+  const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
+  const int64_t blk0 = (int64_t)un.seg * segb;
+  const int64_t blk1 = blk0 + segb < nblk ? blk0 + segb : nblk;
+  load_xb(blk0 * kSqQ);
+  load_c(blk0 * kSqQ);
+  stage(0, blk0 * kSqQ);
+  load_xb((blk0 + 1) * kSqQ);
+  __syncthreads();
+  int cur = 0, sb = 0;
+  // Per block: stage the next block into the other buffer (its loads were
+  // issued a block earlier), issue the loads of the block after it, then use
+  // this block; one barrier ends the block.  Blocks past the segment stage
+  // clamped rows into the buffer that is not read again.
+  for (int64_t blk = blk0; blk < blk1; ++blk, sb ^= 1) {
+    const int64_t t0 = blk * kSqQ;
+    const u32x4 a0 = cA0, a1 = cA1, b0 = cB0, b1 = cB1;
+    stage(sb ^ 1, t0 + kSqQ);
+    load_xb(t0 + 2 * kSqQ);
+    load_c(t0 + kSqQ);
+    const uint16_t* xT = xTb[sb];
+    const uint16_t* Bn = Bnb[sb];
+    const uint16_t* BT = BTb[sb];
+    const float* s_cum = s_cumb[sb];
+    const float* s_coef = s_coefb[sb];
+    const float* s_w = s_wb[sb];
+    const float* s_u = s_ub[sb];
+    const float* s_v = s_vb[sb];
 
     if (wv < 4) {
       const float cum_a = s_cum[sA], cum_b = s_cum[sB];
-      const bool fac = __builtin_amdgcn_readfirstlane(s_fac) != 0;
+      const bool fac = __builtin_amdgcn_readfirstlane(s_facb[sb]) != 0;
       // decay-weighted Gram blocks and their products with x, both groups
       f32x4 accA[PB], accB[PB], zA[PB], zB[PB];
 #pragma unroll
@@ -1716,7 +1752,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
       }
       // outputs y[t0 + s][p0 + 16k + 4q .. +3]:
       //   factored: y = u_t (acc + 2^ref z);  exact: y = acc + 2^cum_t z
-      const float eref = s_eref;
+      const float eref = s_erefb[sb];
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         const int s = g == 0 ? sA : sB;
@@ -1732,7 +1768,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
             yv[v] = u_t * __builtin_fmaf(zs, z[v], acc[v]);
             if constexpr (HAS_D) {
               const float xv = bf16_bits_to_f32(xT[sq_tix(16 * k + 4 * q + v, s)]);
-              yv[v] = __builtin_fmaf(a.D[h * a.P + p0 + 16 * k + 4 * q + v], xv, yv[v]);
+              yv[v] = __builtin_fmaf(s_D[16 * k + 4 * q + v], xv, yv[v]);
             }
           }
           if (t < a.L)
@@ -1742,7 +1778,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
       }
     } else {
       // state columns 16w..16w+15 of every channel block: H' = 2^cum_e H + (x w)^T B
-      const float dec = s_dec;
+      const float dec = s_decb[sb];
       const int n = 16 * w + c16;
       const float* Hc = sH[cur];
       f32x4 st[PB];
@@ -1775,6 +1811,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
           sq_put_state(sH[cur ^ 1], sHh[cur ^ 1], sHl[cur ^ 1], 16 * k + 4 * q + v, n, st[k][v]);
     }
     cur ^= 1;
+    __syncthreads();  // this block's reads and the next block's staging are done
   }
   if (a.h_last && un.seg + 1 == nseg) {
     __syncthreads();
