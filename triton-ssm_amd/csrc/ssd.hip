@@ -1559,6 +1559,18 @@ __global__ __launch_bounds__(256) void ssd_seg_prefix_kernel(SsdArgs a, uint32_t
   }
 }
 
+// Store four state values H[p][n0..n0+3] (n0 a multiple of 4): fp32, bf16 hi
+// and bf16 lo, each as one contiguous write.
+__device__ inline void sq_put_state4(float* Hf, uint16_t* Hh, uint16_t* Hl, int p, int n0,
+                                     f32x4 v) {
+  *reinterpret_cast<f32x4*>(Hf + sq_hix(p, n0)) = v;
+  const uint32_t h01 = pk_bf16(v[0], v[1]), h23 = pk_bf16(v[2], v[3]);
+  const uint32_t l01 = pk_bf16(v[0] - bf16_lo(h01), v[1] - bf16_hi(h01));
+  const uint32_t l23 = pk_bf16(v[2] - bf16_lo(h23), v[3] - bf16_hi(h23));
+  *reinterpret_cast<uint2*>(Hh + sq_bix(p, n0)) = make_uint2(h01, h23);
+  *reinterpret_cast<uint2*>(Hl + sq_bix(p, n0)) = make_uint2(l01, l23);
+}
+
 // 8 waves: waves 0-3 form the weighted Gram blocks of their output groups
 // once and apply them to every channel block of the workgroup (PB blocks of
 // 16), then the carried-state term and the outputs; waves 4-7 update state
@@ -1777,38 +1789,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
         }
       }
     } else {
-      // state columns 16w..16w+15 of every channel block: H' = 2^cum_e H + (x w)^T B
+      // state columns 16w..16w+15 of every channel block: H'^T = 2^tot H^T + (w B)^T x,
+      // the weighted B^T rows (split into bf16 hi + lo) as the A operand,
+      // shared by the channel blocks, and the raw x^T rows as the B operand;
+      // lane: channel 16k + c16, state columns 16w + 4q .. +3
       const float dec = s_decb[sb];
-      const int n = 16 * w + c16;
+      const int p = c16, nq = 16 * w + 4 * q;
       const float* Hc = sH[cur];
       f32x4 st[PB];
 #pragma unroll
-      for (int k = 0; k < PB; ++k)
+      for (int k = 0; k < PB; ++k) {
+        const f32x4 hv = *reinterpret_cast<const f32x4*>(Hc + sq_hix(16 * k + p, nq));
 #pragma unroll
-        for (int v = 0; v < 4; ++v) st[k][v] = dec * Hc[sq_hix(16 * k + 4 * q + v, n)];
+        for (int v = 0; v < 4; ++v) st[k][v] = dec * hv[v];
+      }
 #pragma unroll
       for (int ks = 0; ks < kSqQ / 32; ++ks) {
         const int s0 = 8 * q + 32 * ks;
-        const bf16x8_t bt = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + sq_tix(n, s0)));
+        const u32x4 bv = *reinterpret_cast<const u32x4*>(BT + sq_tix(16 * w + c16, s0));
         const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
         const float4 w1 = *reinterpret_cast<const float4*>(s_w + s0 + 4);
+        const float f[8] = {bf16_lo(bv[0]) * w0.x, bf16_hi(bv[0]) * w0.y, bf16_lo(bv[1]) * w0.z,
+                            bf16_hi(bv[1]) * w0.w, bf16_lo(bv[2]) * w1.x, bf16_hi(bv[2]) * w1.y,
+                            bf16_lo(bv[3]) * w1.z, bf16_hi(bv[3]) * w1.w};
+        bf16x8_t fh, fl;
+        split_bf16(f, fh, fl);
 #pragma unroll
         for (int k = 0; k < PB; ++k) {
-          const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + sq_tix(16 * k + c16, s0));
-          const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
-                              bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
-                              bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
-          bf16x8_t fh, fl;
-          split_bf16(f, fh, fl);
-          st[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt, st[k], 0, 0, 0);
-          st[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt, st[k], 0, 0, 0);
+          const bf16x8_t xv = as_bf16x8(*reinterpret_cast<const u32x4*>(xT + sq_tix(16 * k + c16, s0)));
+          st[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, xv, st[k], 0, 0, 0);
+          st[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, xv, st[k], 0, 0, 0);
         }
       }
 #pragma unroll
       for (int k = 0; k < PB; ++k)
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          sq_put_state(sH[cur ^ 1], sHh[cur ^ 1], sHl[cur ^ 1], 16 * k + 4 * q + v, n, st[k][v]);
+        sq_put_state4(sH[cur ^ 1], sHh[cur ^ 1], sHl[cur ^ 1], 16 * k + p, nq, st[k]);
     }
     cur ^= 1;
     __syncthreads();  // this block's reads and the next block's staging are done
