@@ -10,6 +10,7 @@ x/B/C/y, fp32 dt and state, ZOH discretization fused into the load stage.
   interp_mamba1  interpolation + Mamba-1 scan B=16 T=2048 F=256 N=16 fp32
   ssd_long       SSD scan B=1 L=262144 H=8 P=64 N=16 bf16, chunk 256
   ssd_config1    SSD scan on the headline shapes B=8 L=4096 H=16 P=N=64 bf16
+  ssd_n64_long   SSD scan B=1 L=65536 H=8 P=N=64 bf16 (time-segmented one-pass kernel)
   ssd_stream     streaming SSD step, 4096 streams H=32 P=64 N=128 fp32 state
   dtproj         Mamba-1 scan B=16 L=2048 D=256 N=16 fp32 with dt = clamp(softplus(
                  dt_raw W + bias)) formed inside the scan's passes (rank 16)
@@ -530,6 +531,51 @@ def wl_ssd_long(args, dev):
                         "B": B, "L": L, "H": H, "P": P, "N": N, "chunk": args.ssd_chunk})
 
 
+def wl_ssd_n64_long(args, dev):
+    """bf16 N = 64 with one row per head and a long sequence (B=1 L=65536 H=8
+    P=N=64): 16 (row, channel block) units, so the one-pass kernel runs 16
+    time segments after the segment end-state and prefix passes."""
+    import torch
+    from tssm import ssd_scan_forward, workloads
+    w = workloads.ssd_long(L=65536, N=64)
+    base = {k: w[k].to(dev) for k in ("x", "dt", "B", "C")}
+    A_log = w["A_log"].to(dev)
+    B, L, H, P = base["x"].shape
+    N = base["B"].shape[-1]
+    sets = []
+    for i in range(min(args.sets, 2)):
+        s = {k: torch.roll(v, shifts=i * 997, dims=1).contiguous() for k, v in base.items()}
+        s["y"] = torch.empty_like(s["x"])
+        sets.append(s)
+
+    def step(i):
+        s = sets[i % len(sets)]
+        ssd_scan_forward(s["x"], s["dt"], A_log, s["B"], s["C"], None, chunk=args.ssd_chunk,
+                         disc=args.disc, out=s["y"])
+
+    def cpu():
+        from oracle import cport
+        Ls = 8192
+        arrs = [_np32(w[k][:, :Ls]) for k in ("x", "dt")] + [_np32(w["A_log"])] + \
+               [_np32(w[k][:, :Ls]) for k in ("B", "C")]
+        med = _timed_cpu(lambda: cport.ssd_scan(*arrs, None, None, disc=args.disc), args.cpu_reps)
+        return {"value": B * Ls * H * P / med, "unit": "elements/s", "cores": cport.threads(),
+                "kind": "port", "sample": f"first {Ls} of {L} steps (8 heads), median of "
+                                          f"{args.cpu_reps} runs, {med:.3f} s each"}
+
+    n = B * L * H * P
+    nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
+    return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
+                kernel="ssd_seg_state_kernel + ssd_seg_prefix_kernel + ssd_seq_kernel",
+                dtype="bf16",
+                metric="SSD long-sequence scan elements/sec, B=1 L=65536 H=8 P=N=64 bf16",
+                unit="elements/s",
+                config={"workload": "SSD scan (decay per head, P x N state), B=1 L=65536 H=8 "
+                                    f"P=N=64, chunk {args.ssd_chunk}, bf16 I/O, fp32 state, "
+                                    f"{args.disc.upper()}, time-segmented one-pass kernel",
+                        "B": B, "L": L, "H": H, "P": P, "N": N, "chunk": args.ssd_chunk})
+
+
 def wl_ssd_stream(args, dev):
     import torch
     from tssm import ssd_stream_step, workloads
@@ -807,7 +853,7 @@ WORKLOADS = {"bcproj": wl_bcproj, "bcproj_two_launch": wl_bcproj_two_launch,
              "xproj": wl_xproj, "xproj_unfused": wl_xproj_unfused,
              "multihead": wl_multihead, "mamba1_small": wl_mamba1_small,
              "interp_mamba1": wl_interp_mamba1, "ssd_long": wl_ssd_long,
-             "ssd_config1": wl_ssd_config1,
+             "ssd_config1": wl_ssd_config1, "ssd_n64_long": wl_ssd_n64_long,
              "ssd_stream": wl_ssd_stream, "dtproj": wl_dtproj,
              "dtproj_two_launch": wl_dtproj_two_launch}
 
