@@ -555,18 +555,18 @@ def wl_ssd_n64_long(args, dev):
 
     def cpu():
         from oracle import cport
-        Ls = 8192
-        arrs = [_np32(w[k][:, :Ls]) for k in ("x", "dt")] + [_np32(w["A_log"])] + \
-               [_np32(w[k][:, :Ls]) for k in ("B", "C")]
+        arrs = [_np32(w[k]) for k in ("x", "dt")] + [_np32(w["A_log"])] + \
+               [_np32(w[k]) for k in ("B", "C")]
         med = _timed_cpu(lambda: cport.ssd_scan(*arrs, None, None, disc=args.disc), args.cpu_reps)
-        return {"value": B * Ls * H * P / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"first {Ls} of {L} steps (8 heads), median of "
-                                          f"{args.cpu_reps} runs, {med:.3f} s each"}
+        return {"value": B * L * H * P / med, "unit": "elements/s", "cores": cport.threads(),
+                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                                          f"{med:.3f} s each"}
 
     n = B * L * H * P
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
     return dict(step=step, cpu=cpu, elements=n, bytes=nbytes,
                 kernel="ssd_seg_state_kernel + ssd_seg_prefix_kernel + ssd_seq_kernel",
+                traffic="ssd_n64_long_traffic.json",
                 dtype="bf16",
                 metric="SSD long-sequence scan elements/sec, B=1 L=65536 H=8 P=N=64 bf16",
                 unit="elements/s",
