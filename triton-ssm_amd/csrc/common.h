@@ -217,6 +217,28 @@ __device__ inline float dpp_mov(float v) {
 __device__ inline float swizzle_xor16(float v) {
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
 }
+// Lane i gets lane i - n of its 16-lane row (row_shr), 0 where that leaves
+// the row; or, with the row_bcast controls, lane 15 (0x142) / lane 31 (0x143)
+// of the preceding row(s) in the rows ROWS selects, 0 in the others.
+template <int CTRL, int ROWS>
+__device__ inline float dpp_in(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, true));
+}
+// Inclusive prefix sum over each 32-lane half of the wave (GROUP 32) or over
+// the whole wave (GROUP 64): Hillis-Steele within 16-lane rows by row shifts,
+// then the row totals carried by row broadcasts.  All VALU, no LDS round trip.
+template <int GROUP>
+__device__ inline float scan_incl(float v) {
+  static_assert(GROUP == 32 || GROUP == 64, "half-wave or wave scans");
+  v += dpp_in<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_in<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_in<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_in<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_in<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  if constexpr (GROUP == 64) v += dpp_in<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // Sum over aligned groups of G consecutive lanes (G a power of two <= 64; DPP
 // within rows of 16, lane shuffles beyond); every lane of the group receives
 // the sum.

@@ -635,16 +635,10 @@ __device__ inline void wave_put_xt(uint16_t* xt, const u32x4* w, int g8, int sq)
 template <int DISC>
 __device__ inline void wave_scalars(float dtv, bool live, float a2, int lane, float& pre,
                                     float& cf, float& cumE) {
-  const int s = lane & 31;
   const float d = live ? dtv : 0.0f;
   const float l2 = d * a2;
   cf = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(l2 * 0.6931471805599453f, exp2_fast(l2)) * d : d;
-  pre = l2;
-#pragma unroll
-  for (int o = 1; o < 32; o <<= 1) {
-    const float v = __shfl_up(pre, o);
-    pre += (s >= o) ? v : 0.0f;
-  }
+  pre = scan_incl<32>(l2);
   cumE = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pre), 31));
 }
 
@@ -1475,13 +1469,9 @@ __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t t
       const float l2 = d * a2;
       const float ab = exp2_fast(l2);
       const float coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(l2 * 0.6931471805599453f, ab) * d : d;
-      float cum = l2;
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) {
-        const float u = __shfl_up(cum, o);
-        cum += sl >= o ? u : 0.0f;
-      }
-      const float tot = __shfl(cum, 31);
+      const float cum = scan_incl<32>(l2);
+      const float tot = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cum), 31));
       s_w[sl] = exp2_fast(tot - cum) * coef;
       const float dec = exp2_fast(tot);
       load(r, t0 + 32 * kSgAhead);
@@ -1690,13 +1680,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
       float l2a, ca, l2b, cb;
       mfma_step_scalars<DISC>(a, h, t0, 2 * lane, dl0, &l2a, &ca);
       mfma_step_scalars<DISC>(a, h, t0, 2 * lane + 1, dl1, &l2b, &cb);
-      float cum = l2a + l2b;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float u = __shfl_up(cum, o);
-        cum += lane >= o ? u : 0.0f;
-      }
-      const float tot = __shfl(cum, 63);
+      const float cum = scan_incl<64>(l2a + l2b);
+      const float tot = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cum), 63));
       const float cum_a = cum - l2b;
       // factored decay about the block's mid-value: every factor stays within
       // 2^+-120 while the block decays by at most 2^-240
