@@ -140,6 +140,27 @@ def test_ssd_scan_n64_segments(dev, Bsz, L, H, P, decay, disc):
     assert_close(hl, h_ref, 1e-3, f"segmented n64 ssd h_last L={L} P={P} {decay} {disc}")
 
 
+@pytest.mark.parametrize("chunk", [64, 1024])
+def test_ssd_scan_n64_segments_chunk_slots(dev, chunk):
+    """The segment count is bounded by the workspace's chunk slots: with
+    1024-step chunks (L=5000: 5 slots) there are fewer segments and one
+    sub-segment per segment in pass 1; with 64-step chunks more sub-segments
+    fit.  Slow decays, h0, skip term, against the float64 oracle."""
+    from tssm import ssd_scan_forward
+    Bsz, L, H, P = 1, 5000, 2, 64
+    d = _ssd_inputs(dev, Bsz, L, H, P, 64, torch.bfloat16, seed=chunk, heavy=True)
+    g = torch.Generator().manual_seed(chunk + 1)
+    d["A_log"] = torch.full((H,), float(np.log(0.02)), device=dev)
+    d["dt"] = (torch.rand(Bsz, L, H, generator=g) * 0.02).to(dev)
+    h0 = torch.randn(Bsz, H, P, 64, device=dev)
+    y, hl = ssd_scan_forward(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], h0=h0,
+                             chunk=chunk, return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.ssd_scan(d["x"], d["dt"], d["A_log"], d["B"], d["C"], d["D"], h0=np64(h0))
+    assert_close(y, y_ref, 4e-3, f"segmented n64 ssd y, chunk {chunk}")
+    assert_close(hl, h_ref, 1e-3, f"segmented n64 ssd h_last, chunk {chunk}")
+
+
 def test_ssd_scan_n64_long_sequence(dev):
     """B=1 L=65536 H=8 P=N=64 bf16, log-normal dt: 16 (row, channel block)
     units, so the one-pass kernel runs 16 segments of 4096 steps.  Heads 0
