@@ -761,19 +761,24 @@ __device__ inline void wave_out_sweep(const SsdArgs& a, const WaveTile& wt, f32x
   const int32_t bC = (int32_t)(a.sC_l * 2), by = (int32_t)(a.sy_l * 2);
   const uint32_t oC = (uint32_t)(c16 * bC + 8 * q);
   const uint32_t oy = (uint32_t)((lane >> 3) * by + 16 * (lane & 7));
-  u32x4 xr[4];
-  u32x2 bq[2], cq[2];
-  float dtv;
   // C through the caches: the 4 waves of a workgroup share its 128-byte lines
   // (a streaming hint let them be evicted between the waves' reads: 20% more
-  // bytes fetched)
-  auto load_sub = [&](int r0) {  // r0: first row of the sub-chunk, from the tile start
+  // bytes fetched).  Two sub-chunks of loads are in flight: sub-chunk k + 2
+  // is loaded into k's registers once k is staged (rows clamped to the last
+  // sub-chunk, which is then re-read from the caches instead of branching).
+  auto load_sub = [&](int r0, u32x4* xr, u32x2* bq, u32x2* cq, float& dtv) {
     wt.template load<XPOL>(r0, xr, bq, dtv);
 #pragma unroll
     for (int sg = 0; sg < 2; ++sg)
       cq[sg] = __builtin_amdgcn_raw_buffer_load_b64(rC, (int)oC, (r0 + 16 * sg) * bC, 0);
   };
-  load_sub(0);
+  const int last_r0 = (wt.nsub - 1) * kWsub;
+  u32x4 xrA[4], xrB[4];
+  u32x2 bqA[2], cqA[2], bqB[2], cqB[2];
+  float dtA, dtB;
+  load_sub(0, xrA, bqA, cqA, dtA);
+  __builtin_amdgcn_sched_barrier(0);
+  load_sub(kWsub < last_r0 ? kWsub : last_r0, xrB, bqB, cqB, dtB);
   float dsk[4][4];
   if constexpr (HAS_D) {
 #pragma unroll
@@ -782,8 +787,7 @@ __device__ inline void wave_out_sweep(const SsdArgs& a, const WaveTile& wt, f32x
       for (int r = 0; r < 4; ++r) dsk[pi][r] = a.D[wt.h * kMp + 16 * pi + 4 * q + r];
   }
 
-#pragma unroll 1
-  for (int k = 0; k < wt.nsub; ++k) {
+  auto body = [&](int k, u32x4* xr, u32x2* bq, u32x2* cq, float& dtv) {
     const int r0 = k * kWsub;
     // x^T, B rows (and the row-major x for the skip term) into LDS
     const u32x2 bz[2] = {bq[0], bq[1]}, cz[2] = {cq[0], cq[1]};
@@ -803,8 +807,8 @@ __device__ inline void wave_out_sweep(const SsdArgs& a, const WaveTile& wt, f32x
       scoef[lane] = cf;
       sw[lane] = exp2_fast(cumE - pre) * cf;
     }
-    // the next sub-chunk's loads overlap everything below
-    if (k + 1 < wt.nsub) load_sub(r0 + kWsub);
+    // sub-chunk k + 2's loads overlap everything below and the next sub-chunk
+    load_sub(r0 + 2 * kWsub < last_r0 ? r0 + 2 * kWsub : last_r0, xr, bq, cq, dtv);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
 
     // decay-weighted Gram blocks (s-block sg <= t-block tb) as the B operands
@@ -875,13 +879,18 @@ __device__ inline void wave_out_sweep(const SsdArgs& a, const WaveTile& wt, f32x
       const u32x4 v = *reinterpret_cast<const u32x4*>(xt + tr * kWyRow + 8 * (lane & 7));
       __builtin_amdgcn_raw_buffer_store_b128(v, ry, (int)oy, (r0 + 8 * i) * by, kBufNt);
     }
+  };
+#pragma unroll 1
+  for (int k = 0; k < wt.nsub; k += 2) {
+    body(k, xrA, bqA, cqA, dtA);
+    if (k + 1 < wt.nsub) body(k + 1, xrB, bqB, cqB, dtB);
   }
 }
 
 
 // Pass 3: outputs of each tile from its entry state.
 template <int DISC, bool HAS_D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_out_wave_kernel(SsdArgs a, uint32_t ngroups) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HAS_D ? 2 : 3))) void ssd_out_wave_kernel(SsdArgs a, uint32_t ngroups) {
   __shared__ __align__(16) uint16_t s_xt[kWaveRows][kWxElems];
   __shared__ __align__(16) uint16_t s_b[kWaveRows][kWsub * kWbRow];
   __shared__ __align__(16) float s_sc[kWaveRows][3][kWsub];  // cum, coef, w
@@ -1039,7 +1048,7 @@ __device__ inline void ssd_lookback(const SsdLb& lb, int64_t sbase, int64_t c, i
 }
 
 template <int DISC, bool HAS_D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_fused_wave_kernel(SsdArgs a, SsdLb lb, uint32_t ngroups) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HAS_D ? 2 : 3))) void ssd_fused_wave_kernel(SsdArgs a, SsdLb lb, uint32_t ngroups) {
   __shared__ __align__(16) uint16_t s_xt[kWaveRows][kWxElems];
   __shared__ __align__(16) uint16_t s_b[kWaveRows][kWsub * kWbRow];
   __shared__ __align__(16) float s_sc[kWaveRows][3][kWsub];  // cum, coef, w
