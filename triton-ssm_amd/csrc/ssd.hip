@@ -1383,21 +1383,22 @@ __device__ inline SqUnit sq_unit(uint32_t bid, uint32_t rows, uint32_t npb, uint
 // so that pass 1 has enough waves).  One wave per workgroup, no state shared
 // between waves: wave (row, sub-segment, tile) holds a 16CT-channel x
 // 32-column tile of the state in registers and walks the sub-segment in
-// 32-step sub-blocks, H' = 2^tot H + sum_s w_s x_s B_s^T (w_s = 2^(tot -
+// 64-step sub-blocks, H' = 2^tot H + sum_s w_s x_s B_s^T (w_s = 2^(tot -
 // cum_s) coef_s) as bf16 hi/lo products on the matrix cores.  It stages its
 // own x and B slices through LDS (transposed to [column][step], the operand
 // layout of the products) and forms the sub-block's weights itself, so the
 // only barriers are its own.  kSgAhead sub-blocks of loads are in flight.
 // Writes chunkX[row][sub][p][n] and the sub-segment's decay chunkA[row][sub].
-constexpr int kSgAhead = 4;
-constexpr int kSgStride = 40;  // LDS row stride (bf16) of the staged slices
+constexpr int kSgSteps = 64;   // steps per sub-block
+constexpr int kSgAhead = 2;    // sub-blocks of loads in flight
+constexpr int kSgStride = kSgSteps + 8;  // LDS row stride (bf16) of the staged slices
 
 template <int DISC, int CT>
 __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t tiles,
                                                            uint32_t nsub, uint32_t subb) {
   __shared__ __align__(16) uint16_t xT[16 * CT * kSgStride];
   __shared__ __align__(16) uint16_t BT[32 * kSgStride];
-  __shared__ __align__(16) float s_w[32];
+  __shared__ __align__(16) float s_w[kSgSteps];
   const int lane = threadIdx.x, q = lane >> 4, c16 = lane & 15;
   const uint32_t ngrp = a.rows * nsub, bid = blockIdx.x;
   uint32_t grp, tau;
@@ -1418,27 +1419,27 @@ __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t t
   const float a2 = -expf(a.A_log[h]) * kLog2e;
   const int64_t last = a.L - 1;
   auto clampt = [&](int64_t t) { return t < last ? t : last; };
-  // lane: step pair sp, 8-column octet oc (x: octets past 2 CT re-read the
-  // first ones and are not staged)
+  // lane: step pairs sp and sp + 16, 8-column octet oc (x: octets past 2 CT
+  // re-read the first ones and are not staged)
   const int sp = lane >> 2, oc = lane & 3;
   const int xoc = oc < 2 * CT ? oc : oc - 2 * CT;
   struct Sub {
-    u32x4 xr[2], br[2];
+    u32x4 xr[4], br[4];  // [2 * half + step of the pair]
     float dl;
   };
   auto load = [&](Sub& r, int64_t t0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t t = clampt(t0 + 2 * sp + j);
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = clampt(t0 + 2 * sp + 32 * (j >> 1) + (j & 1));
       r.xr[j] = *reinterpret_cast<const u32x4*>(xb + t * a.sx_l + 8 * xoc);
       r.br[j] = *reinterpret_cast<const u32x4*>(Bb + t * a.sB_l + 8 * oc);
     }
-    r.dl = dtb[clampt(t0 + (lane & 31)) * a.sdt_l];
+    r.dl = dtb[clampt(t0 + lane) * a.sdt_l];
   };
   // every sub-segment before the last segment is whole: subb sub-blocks of
-  // 32 steps, a multiple of kSgAhead (the refills of the last sets read
+  // kSgSteps steps, a multiple of kSgAhead (the refills of the last sets read
   // steps past the sub-segment, clamped into the row, and are never staged)
-  const int64_t tbeg = (int64_t)sub * subb * 32;
+  const int64_t tbeg = (int64_t)sub * subb * kSgSteps;
   f32x4 st[CT][2];
 #pragma unroll
   for (int i = 0; i < CT; ++i) st[i][0] = st[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1446,66 +1447,77 @@ __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t t
   Sub rg[kSgAhead];
 #pragma unroll
   for (int d = 0; d < kSgAhead; ++d) {
-    load(rg[d], tbeg + 32 * d);
+    load(rg[d], tbeg + kSgSteps * d);
     __builtin_amdgcn_sched_barrier(0);
   }
   for (int64_t kb = 0; kb < (int64_t)subb; kb += kSgAhead)
 #pragma unroll
   for (int d = 0; d < kSgAhead; ++d) {
     {
-      const int64_t t0 = tbeg + 32 * (kb + d);
+      const int64_t t0 = tbeg + kSgSteps * (kb + d);
       Sub& r = rg[d];
       __syncthreads();  // the previous sub-block's LDS reads are done
-      if (oc < 2 * CT) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int col = 2 * sp + 32 * hh;
+        if (oc < 2 * CT) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            *reinterpret_cast<uint32_t*>(xT + (8 * oc + 2 * e) * kSgStride + col) =
+                perm_lo(r.xr[2 * hh][e], r.xr[2 * hh + 1][e]);
+            *reinterpret_cast<uint32_t*>(xT + (8 * oc + 2 * e + 1) * kSgStride + col) =
+                perm_hi(r.xr[2 * hh][e], r.xr[2 * hh + 1][e]);
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          *reinterpret_cast<uint32_t*>(xT + (8 * oc + 2 * e) * kSgStride + 2 * sp) =
-              perm_lo(r.xr[0][e], r.xr[1][e]);
-          *reinterpret_cast<uint32_t*>(xT + (8 * oc + 2 * e + 1) * kSgStride + 2 * sp) =
-              perm_hi(r.xr[0][e], r.xr[1][e]);
+          *reinterpret_cast<uint32_t*>(BT + (8 * oc + 2 * e) * kSgStride + col) =
+              perm_lo(r.br[2 * hh][e], r.br[2 * hh + 1][e]);
+          *reinterpret_cast<uint32_t*>(BT + (8 * oc + 2 * e + 1) * kSgStride + col) =
+              perm_hi(r.br[2 * hh][e], r.br[2 * hh + 1][e]);
         }
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        *reinterpret_cast<uint32_t*>(BT + (8 * oc + 2 * e) * kSgStride + 2 * sp) =
-            perm_lo(r.br[0][e], r.br[1][e]);
-        *reinterpret_cast<uint32_t*>(BT + (8 * oc + 2 * e + 1) * kSgStride + 2 * sp) =
-            perm_hi(r.br[0][e], r.br[1][e]);
-      }
-      // weights of the sub-block's 32 steps (lanes 32-63 repeat lanes 0-31)
-      const int sl = lane & 31;
-      const float d = t0 + sl < a.L ? r.dl : 0.0f;
+      // weights of the sub-block's steps, lane = step
+      const float d = t0 + lane < a.L ? r.dl : 0.0f;
       const float l2 = d * a2;
       const float ab = exp2_fast(l2);
       const float coef = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(l2 * 0.6931471805599453f, ab) * d : d;
-      const float cum = scan_incl<32>(l2);
+      const float cum = scan_incl<64>(l2);
       const float tot = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cum), 31));
-      s_w[sl] = exp2_fast(tot - cum) * coef;
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cum), 63));
+      s_w[lane] = exp2_fast(tot - cum) * coef;
       const float dec = exp2_fast(tot);
-      load(r, t0 + 32 * kSgAhead);
+      load(r, t0 + kSgSteps * kSgAhead);
       __syncthreads();
       adec *= dec;
-      const float4 w0 = *reinterpret_cast<const float4*>(s_w + 8 * q);
-      const float4 w1 = *reinterpret_cast<const float4*>(s_w + 8 * q + 4);
-      bf16x8_t bt[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bt[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + (16 * j + c16) * kSgStride + 8 * q));
+      for (int i = 0; i < CT; ++i)
 #pragma unroll
-      for (int i = 0; i < CT; ++i) {
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + (16 * i + c16) * kSgStride + 8 * q);
-        const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
-                            bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
-                            bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
-        bf16x8_t fh, fl;
-        split_bf16(f, fh, fl);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int v = 0; v < 4; ++v) st[i][j][v] *= dec;
-          st[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt[j], st[i][j], 0, 0, 0);
-          st[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt[j], st[i][j], 0, 0, 0);
+#pragma unroll
+      for (int kc = 0; kc < kSgSteps / 32; ++kc) {
+        const int s0 = 8 * q + 32 * kc;
+        const float4 w0 = *reinterpret_cast<const float4*>(s_w + s0);
+        const float4 w1 = *reinterpret_cast<const float4*>(s_w + s0 + 4);
+        bf16x8_t bt[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          bt[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(BT + (16 * j + c16) * kSgStride + s0));
+#pragma unroll
+        for (int i = 0; i < CT; ++i) {
+          const u32x4 xv = *reinterpret_cast<const u32x4*>(xT + (16 * i + c16) * kSgStride + s0);
+          const float f[8] = {bf16_lo(xv[0]) * w0.x, bf16_hi(xv[0]) * w0.y, bf16_lo(xv[1]) * w0.z,
+                              bf16_hi(xv[1]) * w0.w, bf16_lo(xv[2]) * w1.x, bf16_hi(xv[2]) * w1.y,
+                              bf16_lo(xv[3]) * w1.z, bf16_hi(xv[3]) * w1.w};
+          bf16x8_t fh, fl;
+          split_bf16(f, fh, fl);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            st[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh, bt[j], st[i][j], 0, 0, 0);
+            st[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl, bt[j], st[i][j], 0, 0, 0);
+          }
         }
       }
     }
@@ -1841,7 +1853,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
 // enough for about kSgWaves waves), pass 2 the segments' entry states (h0 in
 // the first), and pass 3 the outputs and the final state.
 constexpr int64_t kSeqGroups = 256, kSeqMinSegBlocks = 2, kSgWaves = 2048;
-static_assert((kSqQ / 32) % kSgAhead == 0, "pass-1 sub-segments hold whole sets of sub-blocks");
+static_assert((kSqQ / kSgSteps) % kSgAhead == 0, "pass-1 sub-segments hold whole sets of sub-blocks");
 
 template <int DISC, bool HAS_D, int PB>
 int launch_ssd_seq_pb(int64_t rows, int64_t npb, hipStream_t s, const SsdArgs& a) {
@@ -1862,7 +1874,7 @@ int launch_ssd_seq_pb(int64_t rows, int64_t npb, hipStream_t s, const SsdArgs& a
     const int64_t nsub = (nseg - 1) * m;
     hipLaunchKernelGGL((ssd_seg_state_kernel<DISC, CT>), dim3((unsigned)(rows * nsub * tiles)),
                        dim3(64), 0, s, a, (uint32_t)tiles, (uint32_t)nsub,
-                       (uint32_t)(segb / m * (kSqQ / 32)));
+                       (uint32_t)(segb / m * (kSqQ / kSgSteps)));
     const int64_t PN = (int64_t)a.P * kSqN;
     hipLaunchKernelGGL(ssd_seg_prefix_kernel, dim3((unsigned)((rows * PN + 255) / 256)), dim3(256),
                        0, s, a, (uint32_t)nsub, (uint32_t)m, PN);
