@@ -481,8 +481,8 @@ __global__ __launch_bounds__(kThreads) void pool_partial_kernel(
 template <typename T>
 __global__ __launch_bounds__(64) void pool_final_kernel(const float* __restrict__ part,
                                                         const T* __restrict__ bias,
-                                                        T* __restrict__ out, int64_t nb,
-                                                        int64_t nblk, float denom) {
+                                                        T* __restrict__ out, int64_t nblk,
+                                                        float denom) {
   const int64_t b = blockIdx.x;
   const int lane = threadIdx.x;
   float s = 0.0f;
@@ -788,7 +788,7 @@ extern "C" int tssm_mean_pool_logit(int dtype, const void* h, const void* W, con
                          dim3(kThreads), 0, s, (const T*)h, (const T*)W, part, nt, H, stride_b,
                          stride_t, nblk);
     hipLaunchKernelGGL((pool_final_kernel<T>), dim3((unsigned)grid_b), dim3(64), 0, s, part,
-                       (const T*)bias, (T*)out, grid_b, nblk, denom);
+                       (const T*)bias, (T*)out, nblk, denom);
   });
   return launch_status();
 }

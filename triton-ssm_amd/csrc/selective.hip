@@ -801,10 +801,11 @@ __global__ __launch_bounds__(kSelThreads) void sel_bcproj_state_kernel(
                                                       Cws, m);
 }
 
-// The XR > 0 instances, held to 4 waves per SIMD (left alone the compiler
-// gives them 144 registers, 3 waves per SIMD, and the pass runs ~9% slower).
+// The XR > 0 instances, held to 4 waves per SIMD up to rank 16 (left alone
+// the compiler gives them 144 registers, 3 waves per SIMD, and the pass runs
+// ~9% slower); rank 32 does not fit 4 and is held to 3.
 template <int DISC, int NST, bool HAS_D, int XR>
-__global__ __launch_bounds__(kSelThreads) __attribute__((amdgpu_waves_per_eu(4))) void
+__global__ __launch_bounds__(kSelThreads) __attribute__((amdgpu_waves_per_eu(XR <= 16 ? 4 : 3))) void
 sel_xproj_state_kernel(const float* __restrict__ x, const float* __restrict__ A_log,
                        const float* __restrict__ Wx, int64_t swx_d, const float* __restrict__ D,
                        float* __restrict__ y, float* __restrict__ S, float* __restrict__ Tsum,
@@ -859,7 +860,7 @@ __global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
     const float* __restrict__ D, T* __restrict__ Vhat, T* __restrict__ y,
     float* __restrict__ S, float* __restrict__ Tsum, SelDims m, SiDims q) {
   const int64_t c = blockIdx.x, b = blockIdx.z;
-  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = (int)threadIdx.x, lane = tid & 63;
   const int64_t cb0 = (int64_t)blockIdx.y * kSelThreads;  // first channel of the workgroup
   const int64_t d = cb0 + tid;
   const bool ok = d < m.Dc;

@@ -633,8 +633,8 @@ __device__ inline void wave_put_xt(uint16_t* xt, const u32x4* w, int g8, int sq)
 // prefix of the log2 decay, input coefficient and the sub-chunk total.
 // Steps at or past L get dt = 0 (decay 1, coefficient 0).
 template <int DISC>
-__device__ inline void wave_scalars(float dtv, bool live, float a2, int lane, float& pre,
-                                    float& cf, float& cumE) {
+__device__ inline void wave_scalars(float dtv, bool live, float a2, float& pre, float& cf,
+                                    float& cumE) {
   const float d = live ? dtv : 0.0f;
   const float l2 = d * a2;
   cf = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(l2 * 0.6931471805599453f, exp2_fast(l2)) * d : d;
@@ -712,7 +712,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
     for (int sg = 0; sg < 2; ++sg)
       *reinterpret_cast<u32x2*>(bs + (16 * sg + c16) * kWbRow + 4 * q) = bq[sg];
     float pre, cf, cumE;
-    wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, lane, pre, cf, cumE);
+    wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, pre, cf, cumE);
     if (lane < 32) sw[lane] = exp2_fast(cumE - pre) * cf;
     ltot += cumE;
     // the next sub-chunk's loads overlap everything below
@@ -801,7 +801,7 @@ __device__ inline void wave_out_sweep(const SsdArgs& a, const WaveTile& wt, f32x
     for (int sg = 0; sg < 2; ++sg)
       *reinterpret_cast<u32x2*>(bs + (16 * sg + c16) * kWbRow + 4 * q) = bz[sg];
     float pre, cf, cumE;
-    wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, lane, pre, cf, cumE);
+    wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, pre, cf, cumE);
     if (lane < 32) {
       scum[lane] = pre;
       scoef[lane] = cf;
@@ -1079,7 +1079,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HAS_D ? 2 :
       for (int sg = 0; sg < 2; ++sg)
         *reinterpret_cast<u32x2*>(ld.bs + (16 * sg + c16) * kWbRow + 4 * q) = bq[sg];
       float pre, cf, cumE;
-      wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, lane, pre, cf, cumE);
+      wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, pre, cf, cumE);
       if (lane < 32) ld.sw[lane] = exp2_fast(lsum + cumE - pre) * cf;
       lsum += cumE;
       // Once the decay from the segment end to this sub-chunk's start is
