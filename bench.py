@@ -62,14 +62,26 @@ def _np32(t):
     return np.ascontiguousarray(t.float().numpy())
 
 
+# The CPU baseline runs a workload at least ``--cpu-reps`` times and until
+# ``--cpu-seconds`` of CPU work have been timed (a bounded sample of about ten
+# seconds); the sample notes say how many runs that took.
+CPU_SECONDS = 10.0
+_cpu_runs = [0, 0.0]   # runs and total seconds of the last _timed_cpu
+
+
 def _timed_cpu(fn, reps):
     fn()   # warm
     times = []
-    for _ in range(reps):
+    while len(times) < reps or (sum(times) < CPU_SECONDS and len(times) < 100000):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
+    _cpu_runs[0], _cpu_runs[1] = len(times), sum(times)
     return statistics.median(times)
+
+
+def _runs_note():
+    return f"median of {_cpu_runs[0]} runs ({_cpu_runs[1]:.1f} s of CPU work)"
 
 
 # ------------------------------------------------------------------ workloads
@@ -102,7 +114,7 @@ def wl_multihead(args, dev):
         med = _timed_cpu(lambda: cport.multihead_scan(*arrs, None, disc=args.disc, prepared=True),
                          args.cpu_reps)
         return {"value": B * L * H * P / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                "kind": "port", "sample": f"whole workload, {_runs_note()}, "
                                           f"{med:.3f} s each"}
 
     n = B * L * H * P
@@ -148,7 +160,7 @@ def wl_ssd_config1(args, dev):
                 _np32(w["B"][:Bs]), _np32(w["C"][:Bs])]
         med = _timed_cpu(lambda: cport.ssd_scan(*arrs, None, None, disc=args.disc), args.cpu_reps)
         return {"value": Bs * L * H * P / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"batch 0 of {B}, median of {args.cpu_reps} runs, "
+                "kind": "port", "sample": f"batch 0 of {B}, {_runs_note()}, "
                                           f"{med:.3f} s each"}
 
     n = B * L * H * P
@@ -181,7 +193,7 @@ def wl_mamba1_small(args, dev):
                                   for _ in range(reps)], 3) / reps
         return {"value": B * L * Dc / med, "unit": "elements/s", "cores": cport.threads(),
                 "kind": "port",
-                "sample": f"whole workload x{reps}, median of 3, {med * 1e6:.1f} us each"}
+                "sample": f"whole workload x{reps}, {_runs_note()}, {med * 1e6:.1f} us each"}
 
     n = B * L * Dc
     nbytes = 4 * (2 * n + B * L + Dc * N + 2 * B * L * N)
@@ -225,7 +237,7 @@ def wl_interp_mamba1(args, dev):
             cport.selective_scan(vhat, dt, *rest, None, disc=args.disc)
         med = _timed_cpu(run, args.cpu_reps)
         return {"value": B * T * F / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                "kind": "port", "sample": f"whole workload, {_runs_note()}, "
                                           f"{med:.3f} s each"}
 
     n = B * T * F
@@ -291,7 +303,7 @@ def _wl_dtproj(args, dev, fused):
             cport.selective_scan(x, dt, *rest, None, disc=args.disc)
         med = _timed_cpu(run, args.cpu_reps)
         return {"value": B * L * Dc / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                "kind": "port", "sample": f"whole workload, {_runs_note()}, "
                                           f"{med:.3f} s each (projection in numpy)"}
 
     n = B * L * Dc
@@ -372,7 +384,7 @@ def _wl_bcproj(args, dev, fused):
             cport.selective_scan(x, dt, Al, Bm, Cm, None, disc=args.disc)
         med = _timed_cpu(run, args.cpu_reps)
         return {"value": B * L * Dc / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                "kind": "port", "sample": f"whole workload, {_runs_note()}, "
                                           f"{med:.3f} s each"}
 
     n = B * L * Dc
@@ -451,7 +463,7 @@ def _wl_xproj(args, dev, fused):
                                  np.ascontiguousarray(xd[..., R + N:]), None, disc=args.disc)
         med = _timed_cpu(run, args.cpu_reps)
         return {"value": B * L * Dc / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                "kind": "port", "sample": f"whole workload, {_runs_note()}, "
                                           f"{med:.3f} s each"}
 
     n = B * L * Dc
@@ -514,8 +526,8 @@ def wl_ssd_long(args, dev):
                [_np32(w[k][:, :Ls]) for k in ("B", "C")]
         med = _timed_cpu(lambda: cport.ssd_scan(*arrs, None, None, disc=args.disc), args.cpu_reps)
         return {"value": B * Ls * H * P / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"first {Ls} of {L} steps (8 heads), median of "
-                                          f"{args.cpu_reps} runs, {med:.3f} s each"}
+                "kind": "port", "sample": f"first {Ls} of {L} steps (8 heads), {_runs_note()}, "
+                                          f"{med:.3f} s each"}
 
     n = B * L * H * P
     nbytes = 2 * (2 * n + 2 * B * L * H * N) + 4 * B * L * H + 4 * H
@@ -559,7 +571,7 @@ def wl_ssd_n64_long(args, dev):
                [_np32(w[k]) for k in ("B", "C")]
         med = _timed_cpu(lambda: cport.ssd_scan(*arrs, None, None, disc=args.disc), args.cpu_reps)
         return {"value": B * L * H * P / med, "unit": "elements/s", "cores": cport.threads(),
-                "kind": "port", "sample": f"whole workload, median of {args.cpu_reps} runs, "
+                "kind": "port", "sample": f"whole workload, {_runs_note()}, "
                                           f"{med:.3f} s each"}
 
     n = B * L * H * P
@@ -894,7 +906,11 @@ def main():
                     help="steps per chunk of the SSD scan passes (multiple of 64, <= 1024)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="time the CPU baseline until this much CPU work has run")
     args = ap.parse_args()
+    global CPU_SECONDS
+    CPU_SECONDS = args.cpu_seconds
     if args.steps is None:
         args.steps = 10000 if args.workload == "ssd_stream" else 50
     world = int(os.environ.get("WORLD_SIZE", "1"))
