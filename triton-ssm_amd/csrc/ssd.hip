@@ -1540,7 +1540,7 @@ __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t t
 // writes entry[row][s] = S at the start of segment s (every m-th
 // sub-segment).  Loads are clamped to the last sub-segment pass 1 formed, so
 // every load of a batch is issued at once and stays in bounds.
-constexpr int kSegBatch = 8;
+constexpr int kSegBatch = 32;
 __global__ __launch_bounds__(256) void ssd_seg_prefix_kernel(SsdArgs a, uint32_t nsub, uint32_t m,
                                                              int64_t PN) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
