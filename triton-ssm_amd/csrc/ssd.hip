@@ -1844,8 +1844,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void s
   }
 }
 
-// Time segments of the one-pass kernel: enough (row, channel block, segment)
-// workgroups for one per CU (the kernel holds one 512-thread workgroup per
+// Time segments of the one-pass kernel: as many (row, channel block, segment)
+// workgroups as fit one per CU (the kernel holds one 512-thread workgroup per
 // CU), segments of at least two 128-step blocks and no more segments than
 // the workspace has chunk slots.  With one segment the kernel walks whole
 // rows from h0; with more, pass 1 forms the end states of the sub-segments
@@ -1858,7 +1858,9 @@ static_assert((kSqQ / kSgSteps) % kSgAhead == 0, "pass-1 sub-segments hold whole
 template <int DISC, bool HAS_D, int PB>
 int launch_ssd_seq_pb(int64_t rows, int64_t npb, hipStream_t s, const SsdArgs& a) {
   const int64_t nblk = (a.L + kSqQ - 1) / kSqQ;
-  int64_t nseg = (kSeqGroups + rows * npb - 1) / (rows * npb);
+  // at most kSeqGroups workgroups: a second, partial round of workgroups
+  // would cost a whole segment's time
+  int64_t nseg = kSeqGroups / (rows * npb);
   const int64_t by_len = (nblk + kSeqMinSegBlocks - 1) / kSeqMinSegBlocks;
   if (nseg > by_len) nseg = by_len;
   if (nseg > (int64_t)a.nchunks) nseg = a.nchunks;
