@@ -88,3 +88,63 @@ def test_three_pass_without_skip_or_state_and_reuse(dev):
     y_ref, _ = O.selective_scan(host["x"], host["dt"], host["A_log"], host["B"], host["C"])
     assert_close(y, y_ref, 1e-5, "three-pass y, no skip term")
     assert_close(y2, y_ref[:, : L - 40], 1e-5, "three-pass prefix")
+
+
+@pytest.mark.parametrize("dt_mode", ["shared", "channel"])
+def test_three_pass_few_chunks_ragged_lanes(dev, dt_mode):
+    """L = 70: three chunks, so of the carry pass's four waves per lane group
+    the last walks no chunk (its entry state is h_last); Dc = 100 with N = 8
+    gives 800 (d, n) entries per batch, a partial last group of 64 lanes."""
+    from tssm import selective_scan_forward
+    g = torch.Generator().manual_seed(23)
+    Bn, Lm, Dm, N = 100, 70, 100, 8
+    x = torch.randn(Bn, Lm, Dm, generator=g)
+    shape = (Bn, Lm, Dm) if dt_mode == "channel" else (Bn, Lm)
+    dt = torch.empty(shape).exponential_(20.0, generator=g).clamp_(1e-3, 1.0)
+    A_log = torch.empty(Dm, N).uniform_(np.log(0.5), np.log(5.0), generator=g)
+    Bm = torch.randn(Bn, Lm, N, generator=g) / N ** 0.5
+    Cm = torch.randn(Bn, Lm, N, generator=g) / N ** 0.5
+    h0 = torch.randn(Bn, Dm, N, generator=g)
+    y, h = selective_scan_forward(*(t.to(dev) for t in (x, dt, A_log, Bm, Cm)), None,
+                                  h0=h0.to(dev), return_state=True)
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.selective_scan(x, dt, A_log, Bm, Cm, h0=np64(h0))
+    assert_close(y, y_ref, 1e-5, f"three-pass y, 3 chunks, dt {dt_mode}")
+    assert_close(h, h_ref, 1e-5, f"three-pass h_last, 3 chunks, dt {dt_mode}")
+
+
+@pytest.mark.parametrize("Bn,Lm,Dm,N,dt_mode", [
+    (2, 9000, 36, 8, "channel"),    # 282 chunks: 9 segments, the last of 26 chunks
+    (1, 70000, 64, 16, "shared"),   # 2188 chunks: 69 segments, walked in two loads
+    (3, 12000, 20, 16, "tau"),      # per-batch timestamps; 320 (d, n) lanes
+])
+def test_three_pass_segmented_carry(dev, Bn, Lm, Dm, N, dt_mode):
+    """Few (batch, channel, state) lanes and many chunks: the carry pass folds
+    segments of 32 chunks, carries over the segments and walks each segment
+    again from its entry state."""
+    from tssm import selective_scan_forward
+    g = torch.Generator().manual_seed(Lm + Dm)
+    x = torch.randn(Bn, Lm, Dm, generator=g)
+    if dt_mode == "tau":
+        tau = torch.cumsum(torch.empty(Bn, Lm).exponential_(20.0, generator=g), 1)
+        dt_in, dt_ref = tau, torch.diff(tau, dim=1, prepend=torch.zeros(Bn, 1))
+    else:
+        shape = (Bn, Lm, Dm) if dt_mode == "channel" else (Bn, Lm)
+        dt_in = torch.empty(shape).exponential_(40.0, generator=g).clamp_(1e-3, 1.0)
+        dt_ref = dt_in
+    # decays down to a = -0.2 (dt ~ 0.025): a chunk's entry state still matters
+    # several chunks later, so a wrong segment entry shows in the outputs.
+    # (Slower decays over 70000 steps leave h_last ~1.2e-5 from the float64
+    # oracle on either form of the carry pass: the per-step exp2 rounding
+    # accumulated over the state's long memory, not the carry.)
+    A_log = torch.empty(Dm, N).uniform_(np.log(0.2), np.log(2.0), generator=g)
+    Bm = torch.randn(Bn, Lm, N, generator=g) / N ** 0.5
+    Cm = torch.randn(Bn, Lm, N, generator=g) / N ** 0.5
+    h0 = torch.randn(Bn, Dm, N, generator=g)
+    y, h = selective_scan_forward(x.to(dev), dt_in.to(dev), A_log.to(dev), Bm.to(dev),
+                                  Cm.to(dev), None, h0=h0.to(dev), return_state=True,
+                                  dt_is_tau=dt_mode == "tau")
+    torch.cuda.synchronize()
+    y_ref, h_ref = O.selective_scan(x, dt_ref, A_log, Bm, Cm, h0=np64(h0))
+    assert_close(y, y_ref, 1e-5, f"three-pass y, segmented carry, {Bn}x{Lm}x{Dm} N={N}")
+    assert_close(h, h_ref, 1e-5, f"three-pass h_last, segmented carry, {Bn}x{Lm}x{Dm} N={N}")

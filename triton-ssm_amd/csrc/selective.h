@@ -24,7 +24,8 @@ struct SelPtrs {
   void* y = nullptr;
   float* h_last = nullptr;
   float* S = nullptr;  // [nbatch][nch][Dc][N] chunk end states -> entry states
-  float* T = nullptr;  // [nbatch][nch][Dc] (or [nbatch][nch]) dt sums per chunk
+  float* T = nullptr;  // [nbatch][nch][Dc] (or [nbatch][nch]) dt sums per chunk,
+                       // followed by the carry pass's segment block (sel_state_floats)
   // dt produced in the passes (W != NULL): `dt` then holds the raw rows
   // [nbatch][L][rank] (strides sdt_b, sdt_l, 1) and
   // dt[b,t,d] = clamp(softplus(sum_q raw[b,t,q] W[q,d] + bias[d]), dt_min, dt_max)
@@ -47,6 +48,16 @@ bool sel_proj_ok(const float* raw, const float* W, const float* bias, int64_t Dc
 
 // Steps per chunk for these sizes (0: the three-pass scan does not apply).
 int64_t sel_chunk_steps(int64_t nbatch, int64_t L, int64_t Dc);
+
+// Chunks per segment when the carry pass splits a long sequence into segments
+// (few (batch, channel, state) lanes, many chunks).
+constexpr int64_t kSelSegChunks = 32;
+
+// Floats of the chunk-state block at SelPtrs::S: chunk end states
+// [nbatch][nch][Dc][N], dt sums [nbatch][nch][Dc], then the segment states
+// [nbatch][nseg][Dc][N] and segment dt sums [nbatch][nseg][Dc],
+// nseg = ceil(nch / kSelSegChunks).
+int64_t sel_state_floats(int64_t nbatch, int64_t nch, int64_t Dc, int64_t N);
 
 // Workspace bytes of the three-pass scan (0 if it does not apply to the shape).
 int64_t sel_chunked_bytes(int64_t nbatch, int64_t L, int64_t Dc, int64_t N);

@@ -10,9 +10,11 @@
 //     recurrence from a zero state, each lane keeping the N states of its
 //     channel in registers.  It stores y for that zero entry state, the
 //     chunk's end state X[b,c,d,:] and the chunk's dt sum.
-//   pass 2 (sel_carry_kernel): one thread per (b, d, n) walks the chunks:
-//     S_0 = h0, S_{c+1} = exp2(a log2e sum_c dt) S_c + X_c, overwriting X_c
-//     with the entry state S_c and writing h_last = S_nch.
+//   pass 2 (sel_carry_kernel): S_0 = h0, S_{c+1} = exp2(a log2e sum_c dt)
+//     S_c + X_c per (b, d, n), overwriting X_c with the entry state S_c and
+//     writing h_last = S_nch.  Four waves split a lane's chunks in quarters:
+//     each folds its quarter from zero, the quarters' (decay, state) pairs
+//     meet in LDS, and each wave walks its quarter again from its entry.
 //   pass 3 (sel_output_kernel): adds the entry state's share of the output,
 //     y[t] += sum_n C_t[n] exp2(a[n] log2e cum_t) S_c[n].
 //
@@ -34,8 +36,8 @@ namespace tssm {
 
 constexpr int kSelWaves = 4;                  // waves per workgroup
 constexpr int kSelThreads = 64 * kSelWaves;   // consecutive channels per workgroup
-constexpr int kSelCarryThreads = 256;
-constexpr int kSelCarryBatch = 32;            // chunks loaded ahead by pass 2
+constexpr int kSelCarryWaves = 4;             // pass 2: waves sharing a lane's chunks
+constexpr int kSelCarryBatch = 16;            // chunks a pass-2 wave loads at once
 constexpr int kSelPf = 4;                     // steps of x and dt fetched ahead
 
 struct SelDims {
@@ -378,52 +380,177 @@ __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
   }
 }
 
+// Pass 2.  Workgroup = 64 consecutive (d, n) entries of one batch (blockIdx.y)
+// x kSelCarryWaves waves; wave w takes chunks [w cpw, (w + 1) cpw) of the
+// entries, cpw = ceil(nch / kSelCarryWaves).  Walk 1 folds the wave's chunks
+// from zero into (decay product, state); after one barrier a wave's entry is
+// h0 folded through the pairs of the waves before it, and walk 2 stores each
+// chunk's entry state over its end state.  A quarter of up to kSelCarryBatch
+// chunks stays in registers between the walks; longer quarters are loaded
+// again (the chunks of one batch are all read before any is overwritten, and
+// the waves' chunk ranges are disjoint).  Lanes past the row read its last
+// entry and store nothing.  The last wave ends with h_last.
 template <int NST, bool DTS>
-__global__ __launch_bounds__(kSelCarryThreads) void sel_carry_kernel(
+__global__ __launch_bounds__(64 * kSelCarryWaves) void sel_carry_kernel(
     const float* __restrict__ A_log, const float* __restrict__ h0, float* __restrict__ S,
     const float* __restrict__ Tsum, float* __restrict__ h_last, SelDims m) {
-  // blockIdx.y = batch (uniform: the shared dt sums are scalar loads)
+  constexpr int kB = kSelCarryBatch;
+  __shared__ float s_dec[kSelCarryWaves][64], s_agg[kSelCarryWaves][64];
   const int64_t b = blockIdx.y;
   const int64_t per_b = m.Dc * NST;
-  const int64_t rem = (int64_t)blockIdx.x * kSelCarryThreads + threadIdx.x;
-  if (rem >= per_b) return;  // no barrier in this kernel
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t rem0 = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = rem0 < per_b;
+  const int64_t rem = live ? rem0 : per_b - 1;
   const int64_t d = rem / NST;
   const int64_t idx = b * per_b + rem;
   float* sp = S + b * m.nch * per_b + rem;
-  const float* tp = Tsum + b * m.nch * (DTS ? 1 : m.Dc) + (DTS ? 0 : d);
   const int64_t ts = DTS ? 1 : m.Dc;
-  // the lane's decay and initial state load behind the first batch of chunk
-  // states, so that batch and they share one round trip to memory
-  float a2 = 0.0f, st = 0.0f;
-  bool params = false;
-  auto load_params = [&]() {
-    a2 = -__builtin_amdgcn_exp2f(A_log[rem] * kLog2e) * kLog2e;
-    st = h0 ? h0[idx] : 0.0f;
-    params = true;
+  const float* tp = Tsum + b * m.nch * ts + (DTS ? 0 : d);
+  const float a2 = -__builtin_amdgcn_exp2f(A_log[rem] * kLog2e) * kLog2e;
+  const int64_t cpw = (m.nch + kSelCarryWaves - 1) / kSelCarryWaves;
+  const int64_t cb = wv * cpw < m.nch ? wv * cpw : m.nch;
+  const int64_t ce = cb + cpw < m.nch ? cb + cpw : m.nch;
+
+  // chunk end states and per-chunk decays of chunks c0 .. c0 + kB - 1; slots
+  // past the quarter get decay 1 and state 0 (they change nothing)
+  float X[kB], E[kB];
+#pragma unroll
+  for (int i = 0; i < kB; ++i) X[i] = 0.0f, E[i] = 1.0f;
+  auto load = [&](int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const int64_t c = c0 + i < ce ? c0 + i : ce - 1;
+      X[i] = sp[c * per_b];
+      E[i] = tp[c * ts];
+    }
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const bool ok = c0 + i < ce;
+      E[i] = ok ? __builtin_amdgcn_exp2f(a2 * E[i]) : 1.0f;
+      X[i] = ok ? X[i] : 0.0f;
+    }
   };
-  // all loads of a batch of chunks are issued before the first use
-  int64_t c0 = 0;
-  for (; c0 + kSelCarryBatch <= m.nch; c0 += kSelCarryBatch) {
-    float X[kSelCarryBatch], Tv[kSelCarryBatch];
+
+  // walk 1: the quarter from a zero state
+  float agg = 0.0f, dec = 1.0f;
+  for (int64_t c0 = cb; c0 < ce; c0 += kB) {
+    load(c0);
 #pragma unroll
-    for (int i = 0; i < kSelCarryBatch; ++i) {
-      X[i] = sp[(c0 + i) * per_b];
-      Tv[i] = tp[(c0 + i) * ts];
-    }
-    if (!params) load_params();
-#pragma unroll
-    for (int i = 0; i < kSelCarryBatch; ++i) {
-      sp[(c0 + i) * per_b] = st;  // entry state of chunk c0 + i
-      st = __builtin_fmaf(__builtin_amdgcn_exp2f(a2 * Tv[i]), st, X[i]);
+    for (int i = 0; i < kB; ++i) {
+      agg = __builtin_fmaf(E[i], agg, X[i]);
+      dec *= E[i];
     }
   }
-  if (!params) load_params();
-  for (; c0 < m.nch; ++c0) {
-    const float X = sp[c0 * per_b], Tv = tp[c0 * ts];
-    sp[c0 * per_b] = st;
-    st = __builtin_fmaf(__builtin_amdgcn_exp2f(a2 * Tv), st, X);
+  s_dec[wv][lane] = dec;
+  s_agg[wv][lane] = agg;
+  __syncthreads();
+  float st = h0 ? h0[idx] : 0.0f;
+  for (int v = 0; v < wv; ++v) st = __builtin_fmaf(s_dec[v][lane], st, s_agg[v][lane]);
+
+  // walk 2: entry states from the quarter's entry
+  auto walk = [&](int64_t c0) {
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      if (live && c0 + i < ce) sp[(c0 + i) * per_b] = st;
+      st = __builtin_fmaf(E[i], st, X[i]);
+    }
+  };
+  if (ce - cb <= kB) {
+    walk(cb);
+  } else {
+    for (int64_t c0 = cb; c0 < ce; c0 += kB) {
+      load(c0);
+      walk(c0);
+    }
   }
-  if (h_last) h_last[idx] = st;
+  if (wv == kSelCarryWaves - 1 && h_last && live) h_last[idx] = st;
+}
+
+// Pass 2 over segments, for long sequences with few lanes: one wave per
+// (64 lanes, segment of kSelSegChunks chunks, batch).  FOLD: the segment's
+// chunks from a zero state into Sg[b][seg][Dc N] and their dt sums into
+// Tg[b][seg] (Tg[b][seg][Dc] for per-channel dt).  Then sel_carry_kernel runs
+// over the segments (decay exp2(a log2e sum dt)) and leaves each segment's
+// entry state in Sg; !FOLD walks the segment's chunks again from that entry
+// and stores each chunk's entry state over its end state.
+template <int NST, bool DTS, bool FOLD>
+__global__ __launch_bounds__(256) void sel_carry_seg_kernel(
+    const float* __restrict__ A_log, float* __restrict__ S, const float* __restrict__ Tsum,
+    float* __restrict__ Sg, float* __restrict__ Tg, SelDims m, int64_t nseg) {
+  constexpr int kB = kSelCarryBatch;
+  const int64_t b = blockIdx.z;
+  const int64_t per_b = m.Dc * NST;
+  const int lane = threadIdx.x & 63;
+  const int64_t sg = (int64_t)blockIdx.y * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (sg >= nseg) return;  // whole waves; no barrier in this kernel
+  const int64_t rem0 = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = rem0 < per_b;
+  const int64_t rem = live ? rem0 : per_b - 1;
+  const int64_t d = rem / NST;
+  float* sp = S + b * m.nch * per_b + rem;
+  const int64_t ts = DTS ? 1 : m.Dc;
+  const float* tp = Tsum + b * m.nch * ts + (DTS ? 0 : d);
+  const float a2 = -__builtin_amdgcn_exp2f(A_log[rem] * kLog2e) * kLog2e;
+  const int64_t cb = sg * kSelSegChunks;
+  const int64_t ce = cb + kSelSegChunks < m.nch ? cb + kSelSegChunks : m.nch;
+  float* gp = Sg + (b * nseg + sg) * per_b + rem;
+  float st = FOLD ? 0.0f : *gp, tsum = 0.0f;
+  for (int64_t c0 = cb; c0 < ce; c0 += kB) {
+    float X[kB], Tv[kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const int64_t c = c0 + i < ce ? c0 + i : ce - 1;
+      X[i] = sp[c * per_b];
+      Tv[i] = tp[c * ts];
+    }
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const bool ok = c0 + i < ce;
+      if (!FOLD && live && ok) sp[(c0 + i) * per_b] = st;
+      const float e = ok ? __builtin_amdgcn_exp2f(a2 * Tv[i]) : 1.0f;
+      st = __builtin_fmaf(e, st, ok ? X[i] : 0.0f);
+      tsum += ok ? Tv[i] : 0.0f;
+    }
+  }
+  if (FOLD) {
+    if (live) *gp = st;
+    const bool writer = DTS ? (blockIdx.x == 0 && lane == 0) : (live && rem % NST == 0);
+    if (writer) Tg[(b * nseg + sg) * ts + (DTS ? 0 : d)] = tsum;
+  }
+}
+
+// Host side of pass 2.  Enough lanes: sel_carry_kernel on the chunks, grid
+// (ceil(Dc N / 64), batches) of kSelCarryWaves waves.  Few lanes and at least
+// four segments of chunks: fold the segments, carry over them, walk them
+// again (three launches, each with a wave per segment and 64 lanes).
+template <int NST, bool DTS>
+int launch_sel_carry(hipStream_t s, const SelPtrs& p, const SelDims& m) {
+  const int64_t lanes = m.Dc * NST;  // per batch
+  const int64_t groups = (lanes + 63) / 64;
+  const int64_t nseg = (m.nch + kSelSegChunks - 1) / kSelSegChunks;
+  if (m.nbatch * groups >= 512 || nseg < 4 || (nseg + 3) / 4 > 65535) {
+    hipLaunchKernelGGL((sel_carry_kernel<NST, DTS>), dim3((unsigned)groups, (unsigned)m.nbatch),
+                       dim3(64 * kSelCarryWaves), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
+    return (int)hipGetLastError();
+  }
+  float* Sg = p.T + m.nbatch * m.nch * m.Dc;
+  float* Tg = Sg + m.nbatch * nseg * lanes;
+  const dim3 grid((unsigned)groups, (unsigned)((nseg + 3) / 4), (unsigned)m.nbatch);
+  hipLaunchKernelGGL((sel_carry_seg_kernel<NST, DTS, true>), grid, dim3(256), 0, s, p.A_log, p.S,
+                     p.T, Sg, Tg, m, nseg);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  SelDims mg = m;
+  mg.nch = nseg;
+  hipLaunchKernelGGL((sel_carry_kernel<NST, DTS>), dim3((unsigned)groups, (unsigned)m.nbatch),
+                     dim3(64 * kSelCarryWaves), 0, s, p.A_log, p.h0, Sg, Tg, p.h_last, mg);
+  e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((sel_carry_seg_kernel<NST, DTS, false>), grid, dim3(256), 0, s, p.A_log,
+                     p.S, p.T, Sg, Tg, m, nseg);
+  return (int)hipGetLastError();
 }
 
 // Pass 3: y[t] += sum_n C_t[n] 2^(a[n] log2e cum_t) S_c[n], the part of the
@@ -1102,13 +1229,8 @@ int sel_chunked_t(bool has_d, const SelPtrs& p, const SelDims& m, hipStream_t s)
                        dim3(kSelThreads), 0, s, x, p.dt, p.A_log, Bm, Cm, p.D, y, p.S, p.T, m);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  const int64_t lanes = m.Dc * NST;  // per batch
-  hipLaunchKernelGGL((sel_carry_kernel<NST, DTS>),
-                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
-                          (unsigned)m.nbatch),
-                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
+  const int rc = launch_sel_carry<NST, DTS>(s, p, m);
+  if (rc != 0) return rc;
   if (DTP && p.dtw) {
     // pass 3 reads the dt table pass 1 stored: the per-channel dt instance
     SelDims m3 = m;
@@ -1158,13 +1280,8 @@ int sel_interp_t(bool has_d, const void* V, const float* M, const float* tau, vo
                        0, s, Vt, M, tau, p.A_log, Bm, Cm, p.D, Ot, y, p.S, p.T, m, q);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  const int64_t lanes = m.Dc * NST;  // per batch
-  hipLaunchKernelGGL((sel_carry_kernel<NST, true>),
-                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
-                          (unsigned)m.nbatch),
-                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
+  const int rc = launch_sel_carry<NST, true>(s, p, m);
+  if (rc != 0) return rc;
   hipLaunchKernelGGL((sel_output_kernel<T, NST, true, true>), grid, dim3(kSelThreads), 0, s, tau,
                      p.A_log, Cm, p.S, y, m);
   return (int)hipGetLastError();
@@ -1200,13 +1317,8 @@ int sel_bcproj_t(bool has_d, const float* x, const float* dt, const float* Wbc, 
                        m);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  const int64_t lanes = m.Dc * NST;  // per batch
-  hipLaunchKernelGGL((sel_carry_kernel<NST, DTS>),
-                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
-                          (unsigned)m.nbatch),
-                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
+  const int rc = launch_sel_carry<NST, DTS>(s, p, m);
+  if (rc != 0) return rc;
   // pass 3 reads the C rows pass 1 stored
   SelDims m3 = m;
   m3.sC_b = m.L * NST; m3.sC_l = NST;
@@ -1230,13 +1342,8 @@ int sel_xproj_t(bool has_d, const float* x, const float* Wx, int64_t swx_d, floa
                        0, s, x, p.A_log, Wx, swx_d, p.D, y, p.S, p.T, Cws, m);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  const int64_t lanes = m.Dc * NST;  // per batch
-  hipLaunchKernelGGL((sel_carry_kernel<NST, false>),
-                     dim3((unsigned)((lanes + kSelCarryThreads - 1) / kSelCarryThreads),
-                          (unsigned)m.nbatch),
-                     dim3(kSelCarryThreads), 0, s, p.A_log, p.h0, p.S, p.T, p.h_last, m);
-  e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
+  const int rc = launch_sel_carry<NST, false>(s, p, m);
+  if (rc != 0) return rc;
   // pass 3 reads the dt table and the C rows pass 1 stored
   SelDims m3 = m;
   m3.sdt_b = m.L * m.Dc; m3.sdt_l = m.Dc; m3.sdt_d = 1;
@@ -1325,12 +1432,17 @@ int64_t sel_dt_table_bytes(int64_t nbatch, int64_t L, int64_t Dc) {
   return nbatch * L * Dc * (int64_t)sizeof(float);
 }
 
+int64_t sel_state_floats(int64_t nbatch, int64_t nch, int64_t Dc, int64_t N) {
+  const int64_t nseg = (nch + kSelSegChunks - 1) / kSelSegChunks;
+  return nbatch * (nch + nseg) * Dc * (N + 1);
+}
+
 int64_t sel_chunked_bytes(int64_t nbatch, int64_t L, int64_t Dc, int64_t N) {
   if (!(N == 8 || N == 16) || nbatch <= 0 || L <= 0 || Dc <= 0) return 0;
   const int64_t rs = sel_chunk_steps(nbatch, L, Dc);
   if (rs == 0) return 0;
   const int64_t nch = (L + rs - 1) / rs;
-  return (nbatch * nch * Dc * N + nbatch * nch * Dc) * (int64_t)sizeof(float);
+  return sel_state_floats(nbatch, nch, Dc, N) * (int64_t)sizeof(float);
 }
 
 int sel_chunked_launch(int dtype, int disc, bool dt_shared, bool tau, const SelPtrs& p,
@@ -1420,8 +1532,8 @@ extern "C" int64_t tssm_selective_scan_xproj_workspace_bytes(int64_t nbatch, int
                                                              int64_t Dc, int64_t N) {
   if (nbatch <= 0 || L <= 0 || Dc <= 0 || !(N == 8 || N == 16)) return -1;
   const int64_t nch = (L + kSelChunkSteps - 1) / kSelChunkSteps;
-  // chunk states + per-channel dt sums, the C rows and the dt table for pass 3
-  return (nbatch * nch * Dc * N + nbatch * nch * Dc) * 4 + nbatch * L * N * 4 +
+  // chunk-state block, the C rows and the dt table for pass 3
+  return sel_state_floats(nbatch, nch, Dc, N) * 4 + nbatch * L * N * 4 +
          sel_dt_table_bytes(nbatch, L, Dc) + 512;
 }
 
@@ -1461,7 +1573,7 @@ extern "C" int tssm_selective_scan_xproj(int disc, const float* x, const float* 
   p.x = x; p.A_log = A_log; p.D = D; p.h0 = h0; p.y = y; p.h_last = h_last;
   p.S = static_cast<float*>(workspace);
   p.T = p.S + nbatch * m.nch * Dc * N;
-  float* Cws = p.T + nbatch * m.nch * Dc;
+  float* Cws = p.S + sel_state_floats(nbatch, m.nch, Dc, N);
   // the dt table after the C rows, 16-byte aligned
   const int64_t cws_end = (int64_t)(reinterpret_cast<uintptr_t>(Cws + nbatch * L * N));
   m.dtw = reinterpret_cast<float*>((cws_end + 15) & ~int64_t(15));
@@ -1480,8 +1592,8 @@ extern "C" int64_t tssm_selective_scan_bcproj_workspace_bytes(int64_t nbatch, in
                                                               int64_t Dc, int64_t N) {
   if (nbatch <= 0 || L <= 0 || Dc <= 0 || !(N == 8 || N == 16)) return -1;
   const int64_t nch = (L + kSelChunkSteps - 1) / kSelChunkSteps;
-  // chunk states + dt sums (per channel at most), then the C rows for pass 3
-  return (nbatch * nch * Dc * N + nbatch * nch * Dc) * 4 + nbatch * L * N * 4 + 256;
+  // chunk-state block, then the C rows for pass 3
+  return sel_state_floats(nbatch, nch, Dc, N) * 4 + nbatch * L * N * 4 + 256;
 }
 
 extern "C" int tssm_selective_scan_bcproj(int disc, const float* x, const float* dt,
@@ -1517,7 +1629,7 @@ extern "C" int tssm_selective_scan_bcproj(int disc, const float* x, const float*
   p.x = x; p.dt = dt; p.A_log = A_log; p.D = D; p.h0 = h0; p.y = y; p.h_last = h_last;
   p.S = static_cast<float*>(workspace);
   p.T = p.S + nbatch * m.nch * Dc * N;
-  float* Cws = p.T + nbatch * m.nch * Dc;
+  float* Cws = p.S + sel_state_floats(nbatch, m.nch, Dc, N);
   const hipStream_t s = as_stream(stream);
   const bool has_d = D != nullptr, tau = dt_is_tau != 0;
   if (N == 16)
