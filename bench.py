@@ -18,6 +18,9 @@ x/B/C/y, fp32 dt and state, ZOH discretization fused into the load stage.
   bcproj         Mamba-1 scan B=16 L=2048 D=256 N=16 fp32 with B, C = x W formed inside
                  the scan's first pass
   bcproj_two_launch  the same as matmuls producing B and C, then the scan
+  xproj          Mamba-1 scan B=16 L=2048 D=256 N=16 fp32 with the whole input
+                 projection x -> (dt, B, C) formed inside the scan (rank 16)
+  xproj_unfused  the same as the x_proj matmul, column copies and the dt-producing scan
   rows           every drop-in kernel at a config-sized shape (one JSON line, "rows" list)
 
 A step is one pass of the path over one batch of seeded synthetic input that
