@@ -2049,7 +2049,8 @@ constexpr int64_t kSsdSegWords = 3 + 2 * 64 * kSsdLbVals;
 
 // Segments of 4 tiles (1024 steps) while that still gives 2048 waves, else
 // as the wave passes (2 or 1).  At B=1 L=262144 H=8: 4 tiles (2048 waves)
-// 157.7 us, 2 tiles (4096 waves) 164.5 us, 8 tiles (1024 waves) 172.5 us --
+// 157.7 us, 2 tiles (4096 waves) 164.5 us, 8 tiles (1024 waves) 172.5 us
+// (later: 4 tiles 148-150 us against 167 us for 3 tiles, 2736 waves) --
 // longer segments halve the look-back words and the share of a segment the
 // first sweep re-reads, until too few waves remain to keep the memory busy.
 constexpr int64_t kFusedSeg4Waves = 2048;
