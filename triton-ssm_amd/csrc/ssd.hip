@@ -1383,12 +1383,17 @@ __device__ inline SqUnit sq_unit(uint32_t bid, uint32_t rows, uint32_t npb, uint
 // so that pass 1 has enough waves).  One wave per workgroup, no state shared
 // between waves: wave (row, sub-segment, tile) holds a 16CT-channel x
 // 32-column tile of the state in registers and walks the sub-segment in
-// 64-step sub-blocks, H' = 2^tot H + sum_s w_s x_s B_s^T (w_s = 2^(tot -
-// cum_s) coef_s) as bf16 hi/lo products on the matrix cores.  It stages its
-// own x and B slices through LDS (transposed to [column][step], the operand
-// layout of the products) and forms the sub-block's weights itself, so the
-// only barriers are its own.  kSgAhead sub-blocks of loads are in flight.
-// Writes chunkX[row][sub][p][n] and the sub-segment's decay chunkA[row][sub].
+// 64-step sub-blocks, last sub-block first: H += sum_s w_s x_s B_s^T with
+// w_s = 2^(lsum + tot - cum_s) coef_s (lsum: the log2 decay of the later
+// sub-blocks), as bf16 hi/lo products on the matrix cores.  Once the decay
+// from the sub-segment end has underflowed to exactly zero, every earlier
+// step's weight is exactly zero too: the walk stops there (checked every
+// kSgAhead sub-blocks) and the sub-segment's decay product is zero.  It
+// stages its own x and B slices through LDS (transposed to [column][step],
+// the operand layout of the products) and forms the sub-block's weights
+// itself, so the only barriers are its own.  kSgAhead sub-blocks of loads
+// are in flight.  Writes chunkX[row][sub][p][n] and the sub-segment's decay
+// chunkA[row][sub].
 constexpr int kSgSteps = 64;   // steps per sub-block
 constexpr int kSgAhead = 2;    // sub-blocks of loads in flight
 constexpr int kSgStride = kSgSteps + 8;  // LDS row stride (bf16) of the staged slices
@@ -1437,24 +1442,27 @@ __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t t
     r.dl = dtb[clampt(t0 + lane) * a.sdt_l];
   };
   // every sub-segment before the last segment is whole: subb sub-blocks of
-  // kSgSteps steps, a multiple of kSgAhead (the refills of the last sets read
-  // steps past the sub-segment, clamped into the row, and are never staged)
+  // kSgSteps steps, a multiple of kSgAhead (the refills of the last sets
+  // read sub-block 0 again and are never staged)
   const int64_t tbeg = (int64_t)sub * subb * kSgSteps;
+  auto t0_of = [&](int64_t kb) { return tbeg + kSgSteps * (kb > 0 ? kb : 0); };
   f32x4 st[CT][2];
 #pragma unroll
   for (int i = 0; i < CT; ++i) st[i][0] = st[i][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float adec = 1.0f;
+  float lsum = 0.0f;  // log2 decay from the end of the current sub-block to the sub-segment end
   Sub rg[kSgAhead];
 #pragma unroll
   for (int d = 0; d < kSgAhead; ++d) {
-    load(rg[d], tbeg + kSgSteps * d);
+    load(rg[d], t0_of((int64_t)subb - 1 - d));
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int64_t kb = 0; kb < (int64_t)subb; kb += kSgAhead)
+  bool done = false;
+  for (int64_t kb0 = (int64_t)subb - 1; kb0 >= 0 && !done; kb0 -= kSgAhead) {
 #pragma unroll
   for (int d = 0; d < kSgAhead; ++d) {
     {
-      const int64_t t0 = tbeg + kSgSteps * (kb + d);
+      const int64_t kb = kb0 - d;
+      const int64_t t0 = tbeg + kSgSteps * kb;
       Sub& r = rg[d];
       __syncthreads();  // the previous sub-block's LDS reads are done
 #pragma unroll
@@ -1485,17 +1493,10 @@ __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t t
       const float cum = scan_incl<64>(l2);
       const float tot = __builtin_bit_cast(
           float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cum), 63));
-      s_w[lane] = exp2_fast(tot - cum) * coef;
-      const float dec = exp2_fast(tot);
-      load(r, t0 + kSgSteps * kSgAhead);
+      s_w[lane] = exp2_fast(lsum + (tot - cum)) * coef;
+      lsum += tot;
+      load(r, t0_of(kb - kSgAhead));
       __syncthreads();
-      adec *= dec;
-#pragma unroll
-      for (int i = 0; i < CT; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) st[i][j][v] *= dec;
 #pragma unroll
       for (int kc = 0; kc < kSgSteps / 32; ++kc) {
         const int s0 = 8 * q + 32 * kc;
@@ -1522,6 +1523,10 @@ __global__ __launch_bounds__(64) void ssd_seg_state_kernel(SsdArgs a, uint32_t t
       }
     }
   }
+    // uniform: earlier sub-blocks would add exact zeros
+    done = exp2_fast(lsum) == 0.0f;
+  }
+  const float adec = exp2_fast(lsum);  // zero when the walk stopped early
   const int64_t PN = (int64_t)a.P * kSqN;
   const int64_t slot = (int64_t)row * nsub + sub;
 #pragma unroll
