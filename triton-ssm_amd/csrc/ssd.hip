@@ -150,6 +150,12 @@ __device__ inline void step_scalars_of(float dl, int64_t t0, int64_t L, float a2
   s_cf[lane] = (DISC == TSSM_DISC_ZOH) ? phi1_from_exp(arg * 0.6931471805599453f, ab) * d : d;
 }
 
+// Pass 1 of the generic passes: the chunk's end state from a zero state,
+// walked last step first, X += R_s coef_s x_s B_s with R_s the decay from
+// step s+1 to the chunk end (a running product of the per-step decays), and
+// the chunk's decay product R.  Once R has underflowed to exactly zero every
+// earlier step adds an exact zero: the walk stops there (uniform: R depends
+// only on the head's dt), and the decay product is zero.
 template <typename T, int DISC, int N>
 __global__ __launch_bounds__(64) void ssd_state_kernel(SsdArgs a) {
   __shared__ float s_ab[64], s_cf[64];
@@ -170,47 +176,55 @@ __global__ __launch_bounds__(64) void ssd_state_kernel(SsdArgs a) {
   float g[N];
 #pragma unroll
   for (int n = 0; n < N; ++n) g[n] = 0.0f;
-  float Pt = 1.0f, Achunk = 1.0f;
+  float R = 1.0f;
   constexpr bool PIPE = kSsdPipe<N>;
+  // sub-blocks of kSsdSub steps (a.tc is a multiple of 64), walked from the
+  // last; each 64-step group's step scalars are formed on entering it
+  const int64_t nsb = (tend - tbeg + kSsdSub - 1) / kSsdSub;
+  auto group_t0 = [&](int64_t k) { return tbeg + (k * kSsdSub) / 64 * 64; };
   SsdSub<N, false> nxt;
   float dnext = 0.0f;
   if constexpr (PIPE) {
-    sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, tbeg, a.L, lane);
-    dnext = dt_ahead(dtp, a.sdt_l, tbeg, a.L, lane);
+    sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, tbeg + (nsb - 1) * kSsdSub, a.L,
+                          lane);
+    dnext = dt_ahead(dtp, a.sdt_l, group_t0(nsb - 1), a.L, lane);
   }
-  for (int64_t t0 = tbeg; t0 < tend; t0 += 64) {
-    if constexpr (PIPE) {
-      step_scalars_of<DISC>(dnext, t0, a.L, a2, s_ab, s_cf, lane);
-      dnext = dt_ahead(dtp, a.sdt_l, t0 + 64, a.L, lane);
-    } else {
-      step_scalars_of<DISC>(dt_ahead(dtp, a.sdt_l, t0, a.L, lane), t0, a.L, a2, s_ab, s_cf, lane);
-    }
-    for (int j = 0; j < 64 && t0 + j < tend; j += kSsdSub) {
-      const int64_t ts = t0 + j;
-      if constexpr (!PIPE) sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, ts, a.L, lane);
-      sub_store<N, false>(nxt, ts, a.L, act, s_x, s_B, s_B, lane);
-      __syncthreads();
-      if constexpr (PIPE)
-        sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, ts + kSsdSub, a.L, lane);
-#pragma unroll 2
-      for (int i = 0; i < kSsdSub; ++i) {
-        const float ab = s_ab[j + i];
-        float bv[N];
-#pragma unroll
-        for (int n = 0; n < N; ++n) bv[n] = s_B[i * N + n];
-        rescaled_step<N>(g, Pt, ab, s_cf[j + i] * s_x[i * 64 + lane], bv);
-        Achunk *= ab;
+  for (int64_t k = nsb - 1; k >= 0; --k) {
+    const int64_t ts = tbeg + k * kSsdSub;
+    const int64_t t0 = group_t0(k);
+    const int j = (int)(ts - t0);
+    if (k == nsb - 1 || j + kSsdSub == 64) {  // entering a group from its end
+      if constexpr (PIPE) {
+        step_scalars_of<DISC>(dnext, t0, a.L, a2, s_ab, s_cf, lane);
+        dnext = dt_ahead(dtp, a.sdt_l, t0 > tbeg ? t0 - 64 : tbeg, a.L, lane);
+      } else {
+        step_scalars_of<DISC>(dt_ahead(dtp, a.sdt_l, t0, a.L, lane), t0, a.L, a2, s_ab, s_cf,
+                              lane);
       }
-      __syncthreads();
     }
+    if constexpr (!PIPE) sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, ts, a.L, lane);
+    sub_store<N, false>(nxt, ts, a.L, act, s_x, s_B, s_B, lane);
+    __syncthreads();
+    if constexpr (PIPE)
+      sub_load<T, N, false>(nxt, xp, a.sx_l, Bp, a.sB_l, Bp, 0, k > 0 ? ts - kSsdSub : ts, a.L,
+                            lane);
+#pragma unroll 2
+    for (int i = kSsdSub - 1; i >= 0; --i) {
+      const float w = R * (s_cf[j + i] * s_x[i * 64 + lane]);
+#pragma unroll
+      for (int n = 0; n < N; ++n) g[n] = __builtin_fmaf(w, s_B[i * N + n], g[n]);
+      R *= s_ab[j + i];
+    }
+    __syncthreads();
+    if (R == 0.0f) break;  // uniform: the earlier steps add exact zeros
   }
   const int64_t PN = (int64_t)P * N;
   if (act) {
     float* out = a.chunkX + ((int64_t)row * a.nchunks + c) * PN + (int64_t)lane * N;
 #pragma unroll
-    for (int n = 0; n < N; ++n) out[n] = Pt * g[n];
+    for (int n = 0; n < N; ++n) out[n] = g[n];
   }
-  if (lane == 0) a.chunkA[(int64_t)row * a.nchunks + c] = Achunk;
+  if (lane == 0) a.chunkA[(int64_t)row * a.nchunks + c] = R;
 }
 
 // Pass 2: thread (entry e, segment sg) of a 1024-thread workgroup covering 32
