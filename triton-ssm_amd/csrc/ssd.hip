@@ -696,7 +696,10 @@ __device__ inline void wave_state_update(f32x4* st, const s16x4_t (*xa)[2], cons
 }
 
 // Pass 1: end state of each tile from zero ([p][n] in chunkX) and its decay
-// product (chunkA).
+// product (chunkA).  The tile is walked last sub-chunk first, each weight
+// carrying the log2 decay of the later sub-chunks (lsum), and the walk stops
+// where the decay from the tile end has underflowed to exactly zero: every
+// earlier step's weight is then exactly zero, and so is the decay product.
 template <int DISC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ssd_state_wave_kernel(SsdArgs a, uint32_t ngroups) {
   __shared__ __align__(16) uint16_t s_xt[kWaveRows][kMp * kWxRow];
@@ -713,13 +716,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
   u32x4 xr[4];
   u32x2 bq[2];
   float dtv;
-  wt.load(0, xr, bq, dtv);
+  wt.load((wt.nsub - 1) * kWsub, xr, bq, dtv);
   f32x4 st[4];
 #pragma unroll
   for (int pi = 0; pi < 4; ++pi) st[pi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float ltot = 0.0f;
+  float lsum = 0.0f;  // log2 decay from the end of the current sub-chunk to the tile end
 #pragma unroll 1
-  for (int k = 0; k < wt.nsub; ++k) {
+  for (int k = wt.nsub - 1; k >= 0; --k) {
     const int r0 = k * kWsub;
     wave_put_xt(xt, xr, g8, sq);
 #pragma unroll
@@ -727,20 +730,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
       *reinterpret_cast<u32x2*>(bs + (16 * sg + c16) * kWbRow + 4 * q) = bq[sg];
     float pre, cf, cumE;
     wave_scalars<DISC>(dtv, wt.tbeg + r0 + (lane & 31) < a.L, a2, pre, cf, cumE);
-    if (lane < 32) sw[lane] = exp2_fast(cumE - pre) * cf;
-    ltot += cumE;
-    // the next sub-chunk's loads overlap everything below
-    if (k + 1 < wt.nsub) wt.load(r0 + kWsub, xr, bq, dtv);
+    if (lane < 32) sw[lane] = exp2_fast(lsum + cumE - pre) * cf;
+    lsum += cumE;
+    // uniform: the earlier sub-chunks would add exact zeros
+    const bool done = k == 0 || exp2_fast(lsum) == 0.0f;
+    // the previous sub-chunk's loads overlap everything below
+    if (!done) wt.load(r0 - kWsub, xr, bq, dtv);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
     s16x4_t xa[4][2];
     wave_get_xa(xt, c16, q, xa);
-    wave_state_update(st, xa, bs, sw, c16, q, exp2_fast(cumE));
+    wave_state_update(st, xa, bs, sw, c16, q, 1.0f);
+    if (done) break;
   }
   float* out = a.chunkX + ((int64_t)wt.row * a.nchunks + wt.c) * (kMp * kMn);
 #pragma unroll
   for (int pi = 0; pi < 4; ++pi)
     *reinterpret_cast<f32x4*>(out + (16 * pi + c16) * kMn + 4 * q) = st[pi];
-  if (lane == 0) a.chunkA[(int64_t)wt.row * a.nchunks + wt.c] = exp2_fast(ltot);
+  if (lane == 0) a.chunkA[(int64_t)wt.row * a.nchunks + wt.c] = exp2_fast(lsum);
 }
 
 // LDS of one wave in the output sweep.
