@@ -249,7 +249,9 @@ int tssm_interp_ssm_step(int v_dtype, int m_dtype, int tau_dtype, const void* V,
  * interpolation of fused_interp_kernel.py:29-100 and the scan of
  * tssm_selective_scan with dt_t = tau_t - tau_{t-1}, dt_0 = tau_0): Vhat is
  * formed inside the scan's first pass, written once and consumed there as x;
- * three launches on `stream`.  V, Vhat, B, C, y in `dtype` (f32 or bf16), M
+ * three launches on `stream` (five when few lanes carry many chunks: the
+ * carry scan then folds 32-chunk segments first).  V, Vhat, B, C, y in
+ * `dtype` (f32 or bf16), M
  * and tau f32; V/M/Vhat [B,T,F], tau [B,T], B/C [B,T,N], y [B,T,F]; A_log
  * f32 [F,N]; D f32 [F] or NULL; h0/h_last f32 [B,F,N] or NULL.  K and FTILE as
  * in tssm_time_aware_interp (semantic).  Returns TSSM_ERR_UNSUPPORTED before
@@ -385,8 +387,9 @@ int tssm_ssd_stream_step(int disc, const float* x, const float* dt, const float*
  * tssm_mh_scan_fused with the channel input broadcast over the states), or,
  * for N = 8 or 16 with f32/bf16 I/O and at least 512 blocks of 64 channels x
  * 32 steps, three launches on `stream` (chunk end states, a carry scan over
- * the chunks, the outputs) with lanes = channels; `chunk` then does not
- * apply.  The workspace size covers either.
+ * the chunks, the outputs; the carry scan takes three launches of its own
+ * when few lanes carry many chunks) with lanes = channels; `chunk` then does
+ * not apply.  The workspace size covers either.
  * x, B, C, y in `dtype` ([B,L,Dc] / [B,L,N]); A_log f32 [Dc,N]; dt f32 with
  * strides (b, l, d) -- sdt_d = 0 for one dt per (b,t); with dt_is_tau=1 dt
  * holds timestamps tau and dt_t = tau_t - tau_{t-1}, dt_0 = tau_0.
@@ -449,8 +452,8 @@ int tssm_selective_scan_dtproj(int dtype, int disc, const void* x, const float* 
  * column stride (a column slice of a wider x_proj weight works).  fp32 x/y,
  * Dc <= 256 and a multiple of 4, N 8 or 16, x rows 16-byte aligned; dt as in
  * tssm_selective_scan (shared, with or without timestamps, or per channel).
- * Three launches: pass 1 stages each 32-step chunk's x tile in LDS, forms
- * the chunk's B/C rows on the fp32 matrix cores and runs the recurrence from
+ * Three launches (five when few lanes carry many chunks): pass 1 stages
+ * each 32-step chunk's x tile in LDS, forms the chunk's B/C rows on the fp32 matrix cores and runs the recurrence from
  * that tile; pass 3 reads the C rows pass 1 stored in the workspace
  * (tssm_selective_scan_bcproj_workspace_bytes() bytes: raw fp32, not
  * look-back words).  No reference counterpart. */
@@ -473,8 +476,8 @@ int tssm_selective_scan_bcproj(int disc, const float* x, const float* dt, int dt
  * (>= rank + 2N), unit column stride; W_dt f32 [rank][Dc], row stride sw_r
  * (>= Dc, a multiple of 4), bias [Dc]; rank 16, 32, 48 or 64.  fp32 x/y,
  * Dc <= 256 and a multiple of 4, N 8 or 16, x rows and W_dt, bias, A_log
- * 16-byte aligned.  Three launches: pass 1 stages each 32-step chunk's x tile
- * in LDS, forms its dt_raw/B/C rows on the fp32 matrix cores, then every
+ * 16-byte aligned.  Three launches (five when few lanes carry many chunks):
+ * pass 1 stages each 32-step chunk's x tile in LDS, forms its dt_raw/B/C rows on the fp32 matrix cores, then every
  * channel's dt (stored to a dt table in the workspace) and runs the
  * recurrence; pass 3 reads the dt table and the C rows.  Workspace of
  * tssm_selective_scan_xproj_workspace_bytes() bytes (raw fp32, not look-back
