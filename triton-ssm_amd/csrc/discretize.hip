@@ -243,6 +243,7 @@ __global__ __launch_bounds__(kBwdLanes) void zoh_bwd_pass1_kernel(
 // added in wave order); ddt[r] = sum over lane blocks of part_ddt.  Both
 // orders are fixed, so results are deterministic.
 constexpr int kRedWaves = 16;
+constexpr int kRedBatch = 16;  // row-group partials a dA wave loads at once
 __global__ __launch_bounds__(64 * kRedWaves) void zoh_bwd_pass2_kernel(
     const float* __restrict__ part_dA, const float* __restrict__ part_ddt, float* __restrict__ dA,
     float* __restrict__ ddt, int64_t grid_t, int64_t nrows, int64_t hc, int64_t n_rg,
@@ -252,8 +253,22 @@ __global__ __launch_bounds__(64 * kRedWaves) void zoh_bwd_pass2_kernel(
   if ((int64_t)blockIdx.x < n_hblk) {  // uniform: a dA workgroup
     const int64_t h = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.0f;
-    if (h < hc)
-      for (int64_t g = wave; g < n_rg; g += kRedWaves) s += part_dA[g * hc + h];
+    if (h < hc) {
+      // kRedBatch row groups' partials loaded at once (indices past n_rg
+      // re-read the batch's first), then added in the same order as one at
+      // a time: g = wave, wave + kRedWaves, ...
+      for (int64_t g0 = wave; g0 < n_rg; g0 += (int64_t)kRedWaves * kRedBatch) {
+        float v[kRedBatch];
+#pragma unroll
+        for (int u = 0; u < kRedBatch; ++u) {
+          const int64_t g = g0 + (int64_t)u * kRedWaves;
+          v[u] = part_dA[(g < n_rg ? g : g0) * hc + h];
+        }
+#pragma unroll
+        for (int u = 0; u < kRedBatch; ++u)
+          s = g0 + (int64_t)u * kRedWaves < n_rg ? s + v[u] : s;
+      }
+    }
     red[wave][lane] = s;
     __syncthreads();
     if (wave == 0 && h < hc) {
