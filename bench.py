@@ -919,7 +919,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: every workload is data-parallel over rows or "
-              "streams and this build runs on a single MI355X; run with --gpus 1",
+              "streams, and the benchmark runs on a single MI355X; run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 
