@@ -32,6 +32,15 @@ CXXFLAGS = [
 ]
 
 
+# Per-source extra flags.  The interpolating pass 1 of the Mamba-1 scan is
+# built with the scheduler's max-ilp strategy (91.6 -> 87.6 us per step at
+# B=16 T=2048 F=256 N=16); for the other sources the default strategy
+# measured as fast or faster.
+SOURCE_FLAGS = {
+    "selective_interp": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -53,7 +62,7 @@ def _stale(obj: Path, src: Path) -> bool:
 def _compile(src: Path, force: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
     if force or _stale(obj, src):
-        cmd = [hipcc(), *CXXFLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc(), *CXXFLAGS, *SOURCE_FLAGS.get(src.stem, []), "-c", str(src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr}")

@@ -31,252 +31,9 @@
 
 #include "common.h"
 #include "selective.h"
+#include "selective_dev.h"
 
 namespace tssm {
-
-constexpr int kSelWaves = 4;                  // waves per workgroup
-constexpr int kSelThreads = 64 * kSelWaves;   // consecutive channels per workgroup
-constexpr int kSelCarryWaves = 4;             // pass 2: waves sharing a lane's chunks
-constexpr int kSelCarryBatch = 16;            // chunks a pass-2 wave loads at once
-constexpr int kSelPf = 4;                     // steps of x and dt fetched ahead
-
-struct SelDims {
-  int64_t L, Dc, Rs, nch;
-  int64_t sx_b, sx_l, sdt_b, sdt_l, sdt_d, sB_b, sB_l, sC_b, sC_l, sy_b, sy_l;
-  int64_t nbatch;
-  // dt produced from raw rows (DTP instances): W [rank][Dc] row stride sw_r
-  const float* W;
-  const float* bias;
-  int64_t sw_r;
-  int rank;
-  float dt_min, dt_max;
-  float* dtw;  // NULL, or [nbatch][L][Dc]: pass 1 stores the produced dt there
-};
-
-// Row stride of the produced-dt table s_dt[step][channel] in LDS: 260 = 4
-// mod 32 floats, so the 16-byte writes of the transpose (8 lanes per pass,
-// 8 consecutive steps) land on distinct banks; reads are one row of
-// consecutive channels.
-constexpr int kSelDtStride = kSelThreads + 4;
-
-// dt of the chunk's steps for the wave's 64 channels (first channel dw0),
-// into s_dt[r * kSelDtStride + column] (column = channel - the workgroup's
-// first channel).  The product raw[t0 + r, :] W[:, d] + bias[d] runs on the
-// matrix cores in the operand order of the standalone projection kernel
-// (dt_project_mfma_kernel: A = W columns, B = raw rows, 16x16x4 f32, the
-// rank in blocks of 16 with lane group lj holding ranks q0 + 4 lj + s), so
-// the values are those that kernel stores; then softplus and the clamp.
-// Lane (li, lj) holds D[h][t] for channels 16 ct + 4 lj + i and steps
-// 16 rt + li, written as one 16-byte row piece per (rt, ct).  Steps past the
-// chunk's n repeat step n-1 (the readers give padded steps dt = 0); columns
-// of channels past Dc hold values of no channel (clamped weights and bias)
-// and are never read: a lane past Dc computes channel Dc-1 and reads that
-// channel's column.  Every load is in bounds: Dc, rank and the row strides
-// are multiples of 4 (sel_proj_ok).
-__device__ inline void sel_proj_table(const float* __restrict__ raw_b, int64_t sr_l,
-                                      int64_t t0, int n, const SelDims& m, int64_t dw0,
-                                      int col0, float* s_dt) {
-  const int lane = threadIdx.x & 63, li = lane & 15, lj = lane >> 4;
-  f32x4 acc[2][4];
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const int64_t h = dw0 + 16 * ct + 4 * lj;  // 4 channels, all in range or all out
-    const float4 bq = *reinterpret_cast<const float4*>(m.bias + (h < m.Dc ? h : 0));
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) acc[rt][ct] = f32x4{bq.x, bq.y, bq.z, bq.w};
-  }
-  for (int q0 = 0; q0 < m.rank; q0 += 16) {
-    const bool qok = q0 + 4 * lj < m.rank;  // rank % 4 == 0: a group is all in or all out
-    const int64_t qa = qok ? q0 + 4 * lj : 0;
-    float wa[4][4];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const int64_t h = dw0 + 16 * ct + li;
-      const float* wp = m.W + (h < m.Dc ? h : m.Dc - 1);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float v = wp[(qa + s) * m.sw_r];
-        wa[ct][s] = qok ? v : 0.0f;
-      }
-    }
-    f32x4 rv[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int r = 16 * rt + li;
-      const f32x4 v =
-          *reinterpret_cast<const f32x4*>(raw_b + (t0 + (r < n ? r : n - 1)) * sr_l + qa);
-      rv[rt] = qok ? v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[ct][s], rv[rt][s], acc[rt][ct],
-                                                              0, 0, 0);
-  }
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      float4 v;
-      v.x = clamp_med3(softplus_fast(acc[rt][ct][0]), m.dt_min, m.dt_max);
-      v.y = clamp_med3(softplus_fast(acc[rt][ct][1]), m.dt_min, m.dt_max);
-      v.z = clamp_med3(softplus_fast(acc[rt][ct][2]), m.dt_min, m.dt_max);
-      v.w = clamp_med3(softplus_fast(acc[rt][ct][3]), m.dt_min, m.dt_max);
-      *reinterpret_cast<float4*>(s_dt + (16 * rt + li) * kSelDtStride + col0 + 16 * ct +
-                                 4 * lj) = v;
-    }
-  }
-}
-
-// ab = exp2(dt a log2e) for each state; ZOH input term (ab - 1) B x / a
-// (h' = ab h + (ab - 1) B x / a); Euler B dt x.
-template <int DISC, int NST>
-__device__ inline void sel_update(float (&h)[NST], const float (&a2)[NST], const float (&nia)[NST],
-                                  const float (&Bv)[NST], float u, float dtv) {
-  if constexpr (DISC == TSSM_DISC_ZOH) {
-#pragma unroll
-    for (int k = 0; k < NST; ++k) {
-      // h' = ab (h + B x / a) - B x / a = h + (ab - 1)(h + B x / a): the
-      // accumulating form adds onto h itself (no register copy per state),
-      // and ab - 1 is exact for ab in [0.5, 1] (Sterbenz)
-      const float abm1 = __builtin_amdgcn_exp2f(dtv * a2[k]) - 1.0f;
-      const float hb = __builtin_fmaf(-nia[k], Bv[k] * u, h[k]);
-      h[k] = __builtin_fmaf(abm1, hb, h[k]);
-    }
-  } else {
-    const float du = dtv * u;
-#pragma unroll
-    for (int k = 0; k < NST; ++k) {
-      const float ab = __builtin_amdgcn_exp2f(dtv * a2[k]);
-      h[k] = __builtin_fmaf(ab, h[k], Bv[k] * du);
-    }
-  }
-}
-
-// Lane parameters: a log2(e) and -1/a with a = -exp(A_log[d, k]).
-// Lane parameters from the raw A_log values: a log2(e) and -1/a with
-// a = -exp(A_log[d, k]).
-template <int NST>
-__device__ inline void sel_params(const float (&al)[NST], float (&a2)[NST], float (&nia)[NST]) {
-#pragma unroll
-  for (int k = 0; k < NST; ++k) {
-    const float x = al[k] * kLog2e;
-    a2[k] = -__builtin_amdgcn_exp2f(x) * kLog2e;
-    nia[k] = __builtin_amdgcn_exp2f(-x);
-  }
-}
-
-template <int NST>
-__device__ inline void load_alog(const float* __restrict__ A_log, int64_t d, float (&al)[NST]) {
-  const float4* ap = reinterpret_cast<const float4*>(A_log + d * NST);
-#pragma unroll
-  for (int q = 0; q < NST / 4; ++q) {
-    const float4 v = ap[q];
-    al[4 * q] = v.x; al[4 * q + 1] = v.y; al[4 * q + 2] = v.z; al[4 * q + 3] = v.w;
-  }
-}
-
-// The chunk's rows [n4][NST] of B (or C) of this batch, staged once per
-// workgroup in LDS as fp32: thread i holds elements 4i .. 4i+3 (one pass:
-// kSelChunkSteps * NST <= 4 kSelThreads); rows n .. n4-1 (the padding to
-// whole groups of kSelPf steps) repeat row n-1.  Every wave then reads a
-// step's row with broadcast LDS reads.  Loaded in the prologue with every
-// other prologue load, stored to LDS after their one wait.
-template <typename T, int NST>
-__device__ inline float4 stage_row_load(const T* __restrict__ base, int64_t sl, int n, int n4) {
-  static_assert(kSelChunkSteps * NST <= 4 * kSelThreads, "one staging pass");
-  const int i0 = (int)threadIdx.x * 4;
-  const int i = i0 < n4 * NST ? i0 : 0;  // threads past the rows load row 0 and store nothing
-  const int row = i / NST, col = i - row * NST;
-  const T* p = base + (int64_t)(row < n ? row : n - 1) * sl + col;
-  if constexpr (sizeof(T) == 4) {
-    return *reinterpret_cast<const float4*>(p);
-  } else {
-    const uint2 w = *reinterpret_cast<const uint2*>(p);
-    return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
-                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
-  }
-}
-template <int NST>
-__device__ inline void stage_row_store(float* s, float4 v, int n4) {
-  const int i = (int)threadIdx.x * 4;
-  if (i < n4 * NST) *reinterpret_cast<float4*>(s + i) = v;
-}
-
-// dt shared by the channels: the chunk's values [n4] (n4 <= kSelThreads), one
-// per thread (with timestamps the differences, dt_0 = tau_0); padded steps 0.
-template <bool TAU>
-__device__ inline float stage_dt_load(const float* __restrict__ row, int64_t sl, int64_t t0,
-                                      int n) {
-  const int i = (int)threadIdx.x;
-  const int64_t tt = t0 + (i < n ? i : n - 1);
-  float v = row[tt * sl];
-  if constexpr (TAU) v -= (tt > 0) ? row[(tt - 1) * sl] : 0.0f;
-  return i < n ? v : 0.0f;
-}
-
-template <int NST>
-__device__ inline void lds_row(const float* s, float (&v)[NST]) {
-  const float4* q = reinterpret_cast<const float4*>(s);
-#pragma unroll
-  for (int i = 0; i < NST / 4; ++i) {
-    const float4 w = q[i];
-    v[4 * i] = w.x; v[4 * i + 1] = w.y; v[4 * i + 2] = w.z; v[4 * i + 3] = w.w;
-  }
-}
-
-// x (and a per-channel dt) of the chunk's first kSelPf steps, issued in the
-// prologue with its other loads.
-template <typename T, bool DTS>
-__device__ inline void chunk_prefetch(const T* __restrict__ xp, int64_t sx_l,
-                                      const float* __restrict__ dtp, int64_t sdt_l, int64_t t0,
-                                      int n, float (&u)[kSelPf], float (&dr)[kSelPf]) {
-#pragma unroll
-  for (int j = 0; j < kSelPf; ++j) {
-    const int64_t tt = t0 + (j < n ? j : n - 1);
-    u[j] = ldf(xp + tt * sx_l);
-    dr[j] = DTS ? 0.0f : dtp[tt * sdt_l];
-  }
-}
-
-// One chunk of the recurrence for a lane (channel dc of batch b), in groups
-// of kSelPf steps: x (and a per-channel dt) of step r + kSelPf is fetched
-// right after step r, into the register step r just freed, so no value is
-// copied and each fetch has kSelPf - 1 steps to arrive.  u/dr hold the
-// prologue's fetches (chunk_prefetch), already waited on: they pass through
-// opaque copies once, with every other prologue load, so the compiler neither
-// merges them with the loop's fetches nor waits on them one by one.  Padded
-// steps (r >= n) have dt = 0 -- an identity step -- and repeat step n-1's x
-// and B/C rows, so they reproduce step n-1's output.  `step(r, u, dtv)` gets
-// every step.
-// DTP: dt produced in the pass, read from the lane's column of the LDS table
-// (s_dt then points at that column, row stride kSelDtStride).
-template <typename T, bool DTS, bool DTP = false, typename F>
-__device__ inline void chunk_steps(const T* __restrict__ xp, int64_t sx_l,
-                                   const float* __restrict__ dtp, int64_t sdt_l,
-                                   const float* s_dt, int64_t t0, int n, int n4,
-                                   float (&u)[kSelPf], float (&dr)[kSelPf], F&& step) {
-  for (int r = 0; r < n4; r += kSelPf) {
-#pragma unroll
-    for (int j = 0; j < kSelPf; ++j) {
-      const int rr = r + j;
-      float dtv;
-      if constexpr (DTS) dtv = s_dt[rr];
-      else if constexpr (DTP) dtv = rr < n ? s_dt[rr * kSelDtStride] : 0.0f;
-      else dtv = rr < n ? dr[j] : 0.0f;
-      step(rr, u[j], dtv);
-      // refill the registers step rr just used (no copies across the loop)
-      __builtin_amdgcn_sched_barrier(0);
-      const int64_t tn = t0 + min(rr + kSelPf, n - 1);
-      u[j] = ldf(xp + tn * sx_l);
-      if constexpr (!DTS && !DTP) dr[j] = dtp[tn * sdt_l];
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-}
 
 template <typename T, int DISC, int NST, bool DTS, bool TAU, bool HAS_D, bool DTP = false>
 __global__ __launch_bounds__(kSelThreads) void sel_chunk_state_kernel(
@@ -941,275 +698,6 @@ sel_xproj_state_kernel(const float* __restrict__ x, const float* __restrict__ A_
                                                             S, Tsum, Cws, m);
 }
 
-// ---------------------------------------------------------------- interpolation in pass 1
-// Time-aware interpolation (fused_interp_kernel.py:29-100, reference
-// semantics as in interp.hip: "observed" is the FTILE-wide tile's mask sum
-// > 0.5, prev/next the nearest observed step within K on each side,
-// w = clip((tau_t - tau_prev)/(tau_next - tau_prev), 0, 1) or 0.5 when the
-// denominator <= 1e-9, vhat = interpolation / v_prev / v_next / v_cur)
-// formed inside pass 1 of the three-pass scan, which consumes it as x
-// (fused_ssm_interp.py:12-101 does the interpolation and the SSM update in
-// one kernel too, one step per launch).  Vhat is written once and never read
-// back; pass 3 reads y, C and tau only.
-//
-// A workgroup (256 channels of one batch, one chunk of n <= 32 steps):
-//  1. the tile flags of rows t0-K .. t0+n+K-1: wave w sums rows w, w+4, ...,
-//     lane l the 16-byte mask vector of channels 4l..4l+3, then an xor
-//     butterfly over the tile's FTILE/4 lanes -- the per-lane sums and the
-//     reduction order of interp_fused_kernel, so the same flags -- and the
-//     rows' timestamps, staged in LDS with the chunk's B/C rows and dt;
-//  2. per (step, tile): the neighbours and the weight, into LDS tables
-//     (padded steps repeat step n-1);
-//  3. the recurrence of pass 1, x_t of each lane interpolated in registers
-//     from V[prev] and V[next] (fetched four steps ahead), rounded to the
-//     I/O dtype as Vhat is, and stored to Vhat.
-constexpr int kSiMaxK = 64;       // search window the LDS tables hold
-constexpr int kSiMaxTiles = 16;   // FTILE >= 16: at most 16 tiles per 256 channels
-constexpr int kSiRows = kSelChunkSteps + 2 * kSiMaxK;
-
-struct SiDims {
-  int64_t svb, svt, smb, smt, sob, sot;  // V, M, Vhat strides (unit over features)
-  int K, lf, lvpt;                       // lf = log2 FTILE, lvpt = log2(FTILE / 4)
-};
-
-template <typename T>
-__device__ inline float round_io(float v) {
-  if constexpr (sizeof(T) == 4) return v;
-  else return bf16_bits_to_f32((uint16_t)f32_to_bf16_bits(v));
-}
-
-constexpr int kSiMaskU = 13;  // mask rows per wave in flight (one batch at K = 10)
-
-template <typename T, int DISC, int NST, bool HAS_D>
-__global__ __launch_bounds__(kSelThreads) void sel_interp_state_kernel(
-    const T* __restrict__ V, const float* __restrict__ M, const float* __restrict__ tau,
-    const float* __restrict__ A_log, const T* __restrict__ Bm, const T* __restrict__ Cm,
-    const float* __restrict__ D, T* __restrict__ Vhat, T* __restrict__ y,
-    float* __restrict__ S, float* __restrict__ Tsum, SelDims m, SiDims q) {
-  const int64_t c = blockIdx.x, b = blockIdx.z;
-  const int tid = (int)threadIdx.x, lane = tid & 63;
-  const int64_t cb0 = (int64_t)blockIdx.y * kSelThreads;  // first channel of the workgroup
-  const int64_t d = cb0 + tid;
-  const bool ok = d < m.Dc;
-  const int64_t dc = ok ? d : m.Dc - 1;  // lanes past Dc compute channel Dc-1
-  const int64_t t0 = c * m.Rs;
-  const int n = (int)(m.L - t0 < m.Rs ? m.L - t0 : m.Rs);
-  const int n4 = (n + kSelPf - 1) / kSelPf * kSelPf;
-  const int K = q.K;
-  const int R = n + 2 * K;  // flag rows t0-K .. t0+n+K-1
-
-  __shared__ float sB[kSelChunkSteps * NST], sC[kSelChunkSteps * NST];
-  __shared__ float sD[kSelChunkSteps];
-  __shared__ float sTau[kSiRows];
-  // per flag row: the ballot of the row's tile sums > 0.5 over the lanes
-  // (lanes of one tile hold the same sum; bit lt << lvpt is tile lt's flag)
-  __shared__ uint64_t sRowB[kSiRows];
-  // per (step, tile): byte offsets of the rows read as "prev" and "next" from
-  // the row t0-K of the lane's column, and the weight (-1: no pair, vhat is
-  // the "prev" row's value)
-  __shared__ int4 sNb[kSelChunkSteps * kSiMaxTiles];
-
-  // ---- 1. prologue loads: rows to stage, timestamps, lane parameters, and
-  // the first batch of mask rows, before one wait
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const float4 vB = stage_row_load<T, NST>(Bm + b * m.sB_b + t0 * m.sB_l, m.sB_l, n, n4);
-  const float4 vC = stage_row_load<T, NST>(Cm + b * m.sC_b + t0 * m.sC_l, m.sC_l, n, n4);
-  const float* taub = tau + b * m.sdt_b;
-  float vtau = 0.0f;
-  if (tid < R) {
-    const int64_t t = t0 - K + tid;
-    vtau = taub[(t < 0 ? 0 : (t >= m.L ? m.L - 1 : t)) * m.sdt_l];
-  }
-  float al[NST];
-  load_alog<NST>(A_log, dc, al);
-  float Dd = HAS_D ? D[dc] : 0.0f;
-  // wave wv sums rows wv, wv+4, ...: a uniform row pointer, lane l the
-  // 16-byte vector of channels cb0+4l .. cb0+4l+3 (rows outside [0, L) and
-  // vectors past F read a valid vector and count 0)
-  const bool vec_ok = cb0 + 4 * lane < m.Dc;  // F = Dc, a multiple of 4
-  const int vpt = 1 << q.lvpt;
-  for (int i0 = wv; i0 < R; i0 += 4 * kSiMaskU) {
-    float sv[kSiMaskU];
-#pragma unroll
-    for (int u = 0; u < kSiMaskU; ++u) {
-      const int i = i0 + 4 * u;
-      const int64_t t = t0 - K + i;
-      const bool rok = i < R && t >= 0 && t < m.L;
-      const float* rowp = M + b * q.smb + (rok ? t : 0) * q.smt + cb0;
-      const float4 v = *reinterpret_cast<const float4*>(rowp + (vec_ok ? 4 * lane : 0));
-      float sum = 0.0f;
-      sum += v.x; sum += v.y; sum += v.z; sum += v.w;
-      sv[u] = rok && vec_ok ? sum : 0.0f;
-    }
-    // The tile sum over its vpt lanes, level by level across the rows (the
-    // rows' exchanges overlap).  Each level adds the partner group's sum, the
-    // value the xor butterfly of interp_fused_kernel adds (after a level all
-    // lanes of a group hold the same sum), so the flags are that kernel's.
-#pragma unroll
-    for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0xB1>(sv[u]);   // xor 1
-#pragma unroll
-    for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0x4E>(sv[u]);   // xor 2
-    if (vpt >= 8) {
-#pragma unroll
-      for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0x141>(sv[u]);  // the other quad
-    }
-    if (vpt >= 16) {
-#pragma unroll
-      for (int u = 0; u < kSiMaskU; ++u) sv[u] += dpp_mov<0x140>(sv[u]);  // the other 8
-    }
-    if (vpt >= 32) {
-#pragma unroll
-      for (int u = 0; u < kSiMaskU; ++u) sv[u] += swizzle_xor16(sv[u]);
-    }
-    if (vpt >= 64) {
-#pragma unroll
-      for (int u = 0; u < kSiMaskU; ++u) sv[u] += __shfl_xor(sv[u], 32);
-    }
-#pragma unroll
-    for (int u = 0; u < kSiMaskU; ++u) {
-      const int i = i0 + 4 * u;  // uniform per wave
-      const uint64_t bb = __ballot(sv[u] > 0.5f);
-      if (i < R && lane == 0) sRowB[i] = bb;
-    }
-  }
-  stage_row_store<NST>(sB, vB, n4);
-  stage_row_store<NST>(sC, vC, n4);
-  if (tid < R) sTau[tid] = vtau;
-  float a2[NST], nia[NST], h[NST];
-  sel_params<NST>(al, a2, nia);
-#pragma unroll
-  for (int k = 0; k < NST; ++k) {
-    h[k] = 0.0f;
-    asm volatile("" : "+v"(a2[k]), "+v"(nia[k]));  // complete before the loop
-  }
-  asm volatile("" : "+v"(Dd));
-  __syncthreads();  // flags, timestamps, rows staged
-
-  // ---- 2. dt of the chunk's steps (timestamps differenced, padded steps 0)
-  // and the neighbour tables (padded steps repeat step n-1)
-  if (tid < n4) {
-    const int64_t t = t0 + tid;
-    sD[tid] = tid < n ? sTau[tid + K] - (t > 0 ? sTau[tid + K - 1] : 0.0f) : 0.0f;
-  }
-  // Wave wv takes tiles wv, wv+4, ...: three ballots give the tile's flags of
-  // rows 0..191 (bit i: row t0-K+i) as uniform words, then lane r < n4 finds
-  // step r's neighbours with bit scans: the highest flagged row of
-  // [r, r+K-1] (prev) and the lowest of [r+K+1, r+2K] (next), row r+K being
-  // the step itself.
-  const int ntl = kSelThreads >> q.lf;
-  const uint64_t kmask = K >= 64 ? ~0ull : ((1ull << K) - 1);
-  for (int lt = wv; lt < ntl; lt += 4) {
-    const int bit = lt << q.lvpt;
-    uint64_t mw[3];
-#pragma unroll
-    for (int g = 0; g < 3; ++g) {
-      const int i = g * 64 + lane;
-      mw[g] = __ballot(i < R && ((sRowB[i < R ? i : 0] >> bit) & 1ull));
-    }
-    if (lane < n4) {
-      const int rr = lane < n ? lane : n - 1;
-      const int64_t t = t0 + rr;
-      // 64 flag bits starting at row s (rows past 191 read 0)
-      auto bits64 = [&](int s) -> uint64_t {
-        const int g = s >> 6, sh = s & 63;
-        const uint64_t lo = g == 0 ? mw[0] : (g == 1 ? mw[1] : (g == 2 ? mw[2] : 0ull));
-        const uint64_t hi = g == 0 ? mw[1] : (g == 1 ? mw[2] : 0ull);
-        return sh == 0 ? lo : ((lo >> sh) | (hi << (64 - sh)));
-      };
-      const uint64_t wp = bits64(rr) & kmask;
-      const uint64_t wn = bits64(rr + K + 1) & kmask;
-      const int prev = wp ? (int)(t - K + (63 - __builtin_clzll(wp))) : -1;
-      const int next = wn ? (int)(t + 1 + __builtin_ctzll(wn)) : -1;
-      const float tau_t = sTau[rr + K];
-      const float tp = prev >= 0 ? sTau[rr + K - (int)(t - prev)] : 0.0f;
-      const float tn = next >= 0 ? sTau[rr + K + (int)(next - t)] : 0.0f;
-      const float den = tn - tp;
-      float w = den > 1e-9f ? (tau_t - tp) / den : 0.5f;
-      w = w < 0.0f ? 0.0f : (w > 1.0f ? 1.0f : w);
-      // rows read as "prev" and "next" (as interp_kernel: v_prev, else
-      // v_next, else v_cur; next falls back to the prev row), as byte offsets
-      // from row t0-K (both rows lie in [t0-K, t0+n+K): the host bounds
-      // (n+2K) row strides below 2^31 bytes)
-      const int64_t rp = prev >= 0 ? prev : (next >= 0 ? next : t);
-      const int64_t rn = next >= 0 ? next : rp;
-      const int64_t rs = q.svt * (int64_t)sizeof(T);
-      sNb[lane * kSiMaxTiles + lt] =
-          make_int4((int)((rp - (t0 - K)) * rs), (int)((rn - (t0 - K)) * rs),
-                    __float_as_int(prev >= 0 && next >= 0 ? w : -1.0f), 0);
-    }
-  }
-  __syncthreads();
-  // Waves whose lanes are all past Dc are done (no barrier follows).
-  if (cb0 + (tid & ~63) >= m.Dc) return;
-
-  // ---- 3. the recurrence over interpolated inputs
-  const int lt = (int)((dc - cb0) >> q.lf);  // the lane's tile (of channel dc)
-  // row t0-K of the workgroup's first channel (uniform; for the first chunk
-  // it lies before V's row 0, and only rows >= 0 are read from it)
-  const char* vbase =
-      reinterpret_cast<const char*>(V + b * q.svb + (t0 - K) * q.svt + cb0);
-  const uint32_t lboff = (uint32_t)((dc - cb0) * (int64_t)sizeof(T));
-  T* ocol = Vhat + b * q.sob + dc;
-  T* yp = y + b * m.sy_b + dc;
-  // the pair of a table entry, and its weight
-  auto fetch = [&](const int4& e, float& vp, float& vn, float& w) {
-    vp = ldf(reinterpret_cast<const T*>(vbase + ((uint32_t)e.x + lboff)));
-    vn = ldf(reinterpret_cast<const T*>(vbase + ((uint32_t)e.y + lboff)));
-    w = __int_as_float(e.z);
-  };
-  float vp[kSelPf], vn[kSelPf], wq[kSelPf];
-#pragma unroll
-  for (int j = 0; j < kSelPf; ++j) fetch(sNb[(j < n4 ? j : n4 - 1) * kSiMaxTiles + lt], vp[j], vn[j], wq[j]);
-  // dt one step ahead (the step's exp2s need only dt, so the B and C rows,
-  // read at the top of the step, arrive while they issue); the neighbour
-  // entry for step rr + 4 is read at the top too, used at the end
-  float dtc = sD[0];
-  float sdt = 0.0f;
-  for (int r = 0; r < n4; r += kSelPf) {
-#pragma unroll
-    for (int j = 0; j < kSelPf; ++j) {
-      const int rr = r + j;
-      const int r1 = rr + 1 < n4 ? rr + 1 : n4 - 1;
-      const int r4 = rr + kSelPf < n4 ? rr + kSelPf : n4 - 1;
-      float Bv[NST], Cv[NST];
-      lds_row<NST>(sB + rr * NST, Bv);
-      lds_row<NST>(sC + rr * NST, Cv);
-      const float dtn = sD[r1];
-      const int4 e4 = sNb[r4 * kSiMaxTiles + lt];
-      __builtin_amdgcn_sched_barrier(0);  // the step's LDS reads issue first
-      // both forms computed, then a select (no branch around the loads' waits)
-      const float li = lerp_pair(vp[j], vn[j], wq[j]);
-      const float vh = wq[j] >= 0.0f ? li : vp[j];
-      const float u = round_io<T>(vh);  // the scan consumes Vhat as stored
-      const int64_t tw = t0 + (rr < n ? rr : n - 1);
-      sel_update<DISC, NST>(h, a2, nia, Bv, u, dtc);
-      sdt += dtc;
-      float acc0 = HAS_D ? Dd * u : 0.0f, acc1 = 0.0f;
-#pragma unroll
-      for (int k = 0; k < NST; k += 2) {
-        acc0 = __builtin_fmaf(Cv[k], h[k], acc0);
-        acc1 = __builtin_fmaf(Cv[k + 1], h[k + 1], acc1);
-      }
-      // unconditional stores: padded steps and lanes past Dc (in the wave of
-      // channel Dc-1) store exactly the values of step n-1 / channel Dc-1
-      stf(ocol + tw * q.sot, vh);
-      stf(yp + tw * m.sy_l, acc0 + acc1);
-      dtc = dtn;
-      // refill the registers this step used, for step rr + 4
-      __builtin_amdgcn_sched_barrier(0);
-      fetch(e4, vp[j], vn[j], wq[j]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-  if (ok) {
-    float4* sp = reinterpret_cast<float4*>(S + ((b * m.nch + c) * m.Dc + d) * NST);
-#pragma unroll
-    for (int qq = 0; qq < NST / 4; ++qq)
-      sp[qq] = make_float4(h[4 * qq], h[4 * qq + 1], h[4 * qq + 2], h[4 * qq + 3]);
-    if (d == 0) Tsum[b * m.nch + c] = sdt;
-  }
-}
-
 // ---------------------------------------------------------------- host
 namespace {
 
@@ -1267,19 +755,10 @@ int sel_interp_t(bool has_d, const void* V, const float* M, const float* tau, vo
                  const SelPtrs& p, const SelDims& m, const SiDims& q, hipStream_t s) {
   const dim3 grid((unsigned)m.nch, (unsigned)((m.Dc + kSelThreads - 1) / kSelThreads),
                   (unsigned)m.nbatch);
-  const T* Bm = static_cast<const T*>(p.B);
   const T* Cm = static_cast<const T*>(p.C);
   T* y = static_cast<T*>(p.y);
-  const T* Vt = static_cast<const T*>(V);
-  T* Ot = static_cast<T*>(Vhat);
-  if (has_d)
-    hipLaunchKernelGGL((sel_interp_state_kernel<T, DISC, NST, true>), grid, dim3(kSelThreads), 0,
-                       s, Vt, M, tau, p.A_log, Bm, Cm, p.D, Ot, y, p.S, p.T, m, q);
-  else
-    hipLaunchKernelGGL((sel_interp_state_kernel<T, DISC, NST, false>), grid, dim3(kSelThreads),
-                       0, s, Vt, M, tau, p.A_log, Bm, Cm, p.D, Ot, y, p.S, p.T, m, q);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
+  const int e = sel_interp_pass1(sizeof(T) == 2, DISC, NST, has_d, V, M, tau, Vhat, p, m, q, s);
+  if (e != hipSuccess) return e;
   const int rc = launch_sel_carry<NST, true>(s, p, m);
   if (rc != 0) return rc;
   hipLaunchKernelGGL((sel_output_kernel<T, NST, true, true>), grid, dim3(kSelThreads), 0, s, tau,
