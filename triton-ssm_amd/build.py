@@ -6,7 +6,8 @@
 Each ``csrc/*.hip`` is compiled to ``_build/<name>.o`` in parallel with
 ``hipcc --offload-arch=gfx950 -O3``, then linked into ``tssm/libtssm.so``.
 Packed-FP32 instructions are disabled for all device code
-(``-Xclang -target-feature -Xclang -packed-fp32-ops``).
+(``-Xclang -target-feature -Xclang -packed-fp32-ops``); ``SOURCE_FLAGS`` adds
+per-source options (the scheduling strategy of one translation unit).
 """
 from __future__ import annotations
 
