@@ -35,10 +35,12 @@ CXXFLAGS = [
 
 # Per-source extra flags.  The interpolating pass 1 of the Mamba-1 scan is
 # built with the scheduler's max-ilp strategy (91.6 -> 87.6 us per step at
-# B=16 T=2048 F=256 N=16); for the other sources the default strategy
+# B=16 T=2048 F=256 N=16), and so is the bf16 N = 64 SSD path (~1.5% on the
+# B=8 L=4096 H=16 shapes); for the other sources the default strategy
 # measured as fast or faster.
 SOURCE_FLAGS = {
     "selective_interp": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "ssd_n64": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
 }
 
 
